@@ -1,0 +1,324 @@
+#!/usr/bin/env python
+"""Benchmark of the MI355X deformable-attention core (one GPU).
+
+Metric (the benchmark definition's headline): fwd+bwd microseconds per call and achieved HBM GB/s
+at the RF-DETR Nano group-DETR shape (config 2: batch 8, one 24x24 level, 16 heads x 16, 3900
+queries, 2 points, f32). A "step" is one forward + one backward call over that batch, with
+inputs already resident in HBM.
+
+Timing: W warm-up steps, then K steps enqueued through a HIP graph (so host launch overhead is
+not what is measured) between two events on the launch stream, synchronised on both sides. The
+same K steps launched eagerly from Python are reported beside it. The dominant kernel's
+average duration is measured with events around graph replays of that kernel alone.
+
+CPU baseline: the repository's C restatement of the reference gather path (oracle/msda_ref.c,
+OpenMP over slices) on the same inputs, on this host's cores (at most 16), rank 0 only.
+
+``--gpus N`` with N > 1 exits: this build runs on one GPU (the op needs no collective; each GPU of
+a data-parallel job runs it on its own batch shard).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "rf-detr-jax_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "deform-attn fwd+bwd μs/call + achieved HBM GB/s (% peak), Nano group-DETR shape"
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+LDS_PEAK_GBPS = 256 * 128 * 2.4  # 256 CUs x 128 B/clk x 2.4 GHz (conservative)
+
+
+def log(msg):
+    sys.stderr.write(f"[bench] {msg}\n")
+    sys.stderr.flush()
+
+
+class Calls:
+    """Pre-built C-ABI argument lists and output buffers for one workload (minimal host overhead)."""
+
+    def __init__(self, w, dev):
+        import torch
+
+        from rfdetr_jax_amd import _native
+        from rfdetr_jax_amd.workloads import workload_inputs
+
+        self.w = w
+        value, loc, attn, grad = workload_inputs(w, with_grad=True)
+        bf16 = w.value_dtype == "bf16"
+        self.v = torch.from_numpy(value).to(dev)
+        if bf16:
+            self.v = self.v.to(torch.bfloat16)
+        self.loc = torch.from_numpy(loc).to(dev)
+        self.attn = torch.from_numpy(attn).to(dev)
+        self.grad = torch.from_numpy(grad).to(dev)
+        self.out = torch.empty(w.batch, w.queries, w.heads * w.head_dim, device=dev)
+        self.dv = torch.empty_like(self.v)
+        self.dloc = torch.empty_like(self.loc)
+        self.dattn = torch.empty_like(self.attn)
+        self.host = (value, loc, attn, grad)
+        flat = [x for hw in w.shapes for x in hw]
+        self._shapes = (ctypes.c_int32 * len(flat))(*flat)
+        starts, acc = [], 0
+        for h, wd in w.shapes:
+            starts.append(acc)
+            acc += h * wd
+        self._starts = (ctypes.c_int32 * len(starts))(*starts)
+        vdt = _native.DTYPE_BF16 if bf16 else _native.DTYPE_F32
+        shape_args = (w.batch, w.heads, w.head_dim, w.queries, w.levels, w.points, self._shapes, self._starts,
+                      w.len_value)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        self.fargs = (p(self.v), vdt, p(self.loc), p(self.attn), p(self.out), _native.DTYPE_F32) + shape_args
+        self.bargs = (p(self.v), vdt, p(self.loc), p(self.attn), p(self.grad), _native.DTYPE_F32, p(self.dv),
+                      p(self.dloc), p(self.dattn)) + shape_args
+        self.lib = _native.lib()
+        self.check = _native.check
+
+    def fwd(self, stream):
+        rc = self.lib.msda_fwd(*self.fargs, stream)
+        if rc:
+            self.check(rc)
+
+    def bwd(self, stream):
+        rc = self.lib.msda_bwd(*self.bargs, stream)
+        if rc:
+            self.check(rc)
+
+
+def _stream_handle():
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def time_graph(fn, reps, iters_per_graph=20):
+    """Average device time (us) of ``fn`` (which enqueues work on the current stream) by replaying
+    a HIP graph holding ``iters_per_graph`` copies of it ``ceil(reps / iters_per_graph)`` times."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(_stream_handle())  # warm inside the capture stream's context
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        h = _stream_handle()
+        for _ in range(iters_per_graph):
+            fn(h)
+    replays = max(1, -(-reps // iters_per_graph))
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / (replays * iters_per_graph), replays * iters_per_graph
+
+
+def time_eager(fn, reps):
+    import torch
+
+    h = _stream_handle()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn(h)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / reps
+
+
+def measure(w, dev, steps, warmup):
+    calls = Calls(w, dev)
+    h = _stream_handle()
+    for _ in range(warmup):
+        calls.fwd(h)
+        if w.backward:
+            calls.bwd(h)
+
+    def step(hs):
+        calls.fwd(hs)
+        if w.backward:
+            calls.bwd(hs)
+
+    res = {}
+    res["step_us_graph"], res["graph_steps"] = time_graph(step, steps)
+    res["step_us_eager"] = time_eager(step, steps)
+    res["fwd_us"] = time_graph(calls.fwd, steps)[0]
+    if w.backward:
+        res["bwd_us"] = time_graph(calls.bwd, steps)[0]
+    b = w.hbm_bytes()
+    res["hbm_bytes"] = b
+    res["fwd_gbps"] = b["fwd"] / res["fwd_us"] / 1e3
+    if w.backward:
+        res["bwd_gbps"] = b["bwd"] / res["bwd_us"] / 1e3
+    res["step_gbps"] = b["total"] / res["step_us_graph"] / 1e3
+    return res, calls
+
+
+def cpu_baseline(calls, budget_s=3.0, max_reps=20):
+    """fwd+bwd of the C oracle on the same inputs; median us/call."""
+    from oracle import cref
+
+    value, loc, attn, grad = calls.host
+    w = calls.w
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = max(1, min(16, cores))
+    times = []
+    t_end = time.perf_counter() + budget_s
+    cref.forward(value, w.shapes, loc, attn, threads)  # warm-up
+    while len(times) < max_reps and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        cref.forward(value, w.shapes, loc, attn, threads)
+        if w.backward:
+            cref.backward(value, w.shapes, loc, attn, grad, threads)
+        times.append(time.perf_counter() - t0)
+    return {
+        "value": statistics.median(times) * 1e6,
+        "unit": "us/call",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"full {w.name} workload (B={w.batch}, Q={w.queries}, levels={list(w.shapes)}, "
+                   f"{w.heads}x{w.head_dim}, P={w.points}) {'fwd+bwd' if w.backward else 'fwd'}, "
+                   f"median of {len(times)} runs of oracle/msda_ref.c (f32, OpenMP, {threads} threads)"),
+    }
+
+
+def profile_run(w, dev, steps, warmup, copy_mb):
+    """Eager launches only (every dispatch visible to a counter profiler), plus a copy kernel."""
+    import torch
+
+    calls = Calls(w, dev)
+    h = _stream_handle()
+    for _ in range(warmup):
+        calls.fwd(h)
+        if w.backward:
+            calls.bwd(h)
+    torch.cuda.synchronize()
+    fwd_us = time_eager(calls.fwd, steps)
+    bwd_us = time_eager(calls.bwd, steps) if w.backward else None
+    n = copy_mb * (1 << 20) // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    copy_us = time_eager(lambda _h: dst.copy_(src), steps)
+    print(json.dumps({"workload": w.name, "steps": steps, "fwd_us_eager": fwd_us, "bwd_us_eager": bwd_us,
+                      "copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "copy_us": copy_us,
+                      "hbm_bytes": w.hbm_bytes()}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=2, help="workload id (default 2: the headline shape)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-per-config", action="store_true", help="skip timing the other four workloads")
+    ap.add_argument("--profile", action="store_true",
+                    help="for rocprofv3 runs: W + K eager steps of the workload, then K plain copies of a "
+                         "--copy-mb buffer (counter calibration); prints one JSON line of timings")
+    ap.add_argument("--copy-mb", type=int, default=256)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}): the deformable-attention op needs no "
+              "collective, so each GPU of a data-parallel job runs it on its own batch shard.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from rfdetr_jax_amd.workloads import CONFIGS
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    w = CONFIGS[args.config]
+    if args.profile:
+        profile_run(w, dev, args.steps, args.warmup, args.copy_mb)
+        return
+    log(f"workload {w.name}: warmup {args.warmup}, steps {args.steps}")
+    res, calls = measure(w, dev, args.steps, args.warmup)
+    log(f"step {res['step_us_graph']:.2f} us (graph), {res['step_us_eager']:.2f} us (eager); fwd {res['fwd_us']:.2f} us"
+        + (f", bwd {res['bwd_us']:.2f} us" if w.backward else ""))
+
+    kernels = {"fwd": (res["fwd_us"], res["hbm_bytes"]["fwd"])}
+    if w.backward:
+        kernels["bwd"] = (res["bwd_us"], res["hbm_bytes"]["bwd"])
+    dom = max(kernels, key=lambda k: kernels[k][0])
+    dom_us, dom_bytes = kernels[dom]
+    achieved = dom_bytes / dom_us / 1e3
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{w.name}_{dom}.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+
+    per_config = {}
+    if not args.no_per_config:
+        for cid, cw in sorted(CONFIGS.items()):
+            if cid == args.config:
+                r = res
+            else:
+                log(f"workload {cw.name}")
+                r, _ = measure(cw, dev, max(50, args.steps // 4), 10)
+            entry = {"step_us": round(r["step_us_graph"], 3), "fwd_us": round(r["fwd_us"], 3),
+                     "fwd_hbm_gbps": round(r["fwd_gbps"], 1), "hbm_bytes": r["hbm_bytes"]["total"],
+                     "step_hbm_frac": round(r["step_gbps"] / HBM_PEAK_GBPS, 4)}
+            if cw.backward:
+                entry.update({"bwd_us": round(r["bwd_us"], 3), "bwd_hbm_gbps": round(r["bwd_gbps"], 1)})
+            per_config[cw.name] = entry
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(calls)
+        log(f"cpu {cpu['value']:.0f} us/call on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(res["step_us_graph"], 3),
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": res["graph_steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(res["step_us_graph"] / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.value_dtype == "bf16" else "f32",
+        "data": "synthetic (seeded N(0,1) value, U[0,1]^2 + N(0,0.05) locations, softmax weights, N(0,1) grad)",
+        "config": {"workload": w.name, "batch": w.batch, "heads": w.heads, "head_dim": w.head_dim,
+                   "queries": w.queries, "levels": [list(s) for s in w.shapes], "points": w.points,
+                   "value_dtype": w.value_dtype, "mode": "fwd+bwd" if w.backward else "fwd"},
+        "achieved_hbm_gbps": round(res["step_gbps"], 1),
+        "hbm_peak_frac": round(res["step_gbps"] / HBM_PEAK_GBPS, 4),
+        "eager_us_per_call": round(res["step_us_eager"], 3),
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "algorithmic_bytes": dom_bytes, "avg_launch_us": round(dom_us, 3)},
+        "cpu_baseline": cpu,
+        "per_config": per_config,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

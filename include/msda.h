@@ -1,0 +1,110 @@
+/*
+ * msda.h — C ABI of the MI355X (gfx950) multi-scale deformable-attention library.
+ *
+ * The library computes RF-DETR-JAX's deformable-attention core: bilinear, zero-padded sampling of
+ * a multi-level value map at per-query sample positions, weighted by per-sample attention weights
+ * and summed over levels x points; and the three gradients of that map (value, sampling
+ * locations, attention weights).
+ *
+ * Reference interface replaced (paths are into the RF-DETR-JAX source tree):
+ *   msda_fwd  <- ms_deform_attn_core_rows(value, spatial_shapes, sampling_locations,
+ *                attention_weights, sampler)            src/rfdetr_jax/models/ops.py:208-292
+ *                (the per-level sampler _sample_rows,   ops.py:64-134, and the point-weighted
+ *                einsum,                                ops.py:289)
+ *   msda_bwd  <- the VJP of the same function, which the reference obtains by JAX autodiff of
+ *                ops.py:64-134 + ops.py:289, and which its fused TPU sampler implements by hand
+ *                in _sample_bwd / _backward_kernel      src/rfdetr_jax/models/deform_pallas.py:97-120,157-175
+ *
+ * Layouts (all row-major, contiguous):
+ *   value                 [batch * n_heads, len_value, head_dim]    value_dtype   (ops.py:218)
+ *   sampling_locations    [batch, len_query, n_heads, n_levels, n_points, 2]  f32, (x, y) in [0,1]
+ *   attention_weights     [batch, len_query, n_heads, n_levels * n_points]    f32, level-major
+ *   output                [batch, len_query, n_heads * head_dim]    output_dtype  (ops.py:229)
+ *   spatial_shapes        host int32 [n_levels][2] = (H_l, W_l)
+ *   level_start_index     host int32 [n_levels] = prefix sums of H_l * W_l (may be NULL)
+ *   len_value             sum over levels of H_l * W_l
+ *
+ * Semantics: torch grid_sample(mode="bilinear", padding_mode="zeros", align_corners=False) on the
+ * normalised grid 2*loc-1, exactly as ops.py:83-134 and ops.py:270 state it. Sample coordinates
+ * are computed in f32 without fused multiply-adds so floor() decisions match the reference.
+ *
+ * Calls are enqueue-only on `stream` (a hipStream_t, passed as void*; NULL = default stream):
+ * no allocation, no host synchronisation, no global mutable state beyond one-time per-device
+ * initialisation. All buffers are owned by the caller. Inputs are read-only; every output element
+ * is written by the call (grad_value needs no zero-initialisation).
+ *
+ * Return values: MSDA_OK (0) or a negative MSDA_ERR_* code; msda_last_error() then returns a
+ * message for the calling thread. Argument validation happens before any HIP call.
+ */
+#ifndef MSDA_H_
+#define MSDA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum msda_dtype {
+  MSDA_DTYPE_F32 = 0,
+  MSDA_DTYPE_BF16 = 1
+};
+
+enum msda_status {
+  MSDA_OK = 0,
+  MSDA_ERR_INVALID_ARGUMENT = -1, /* shapes, pointers or level table inconsistent */
+  MSDA_ERR_UNSUPPORTED = -2,      /* valid but outside what the kernels handle (dtype, head_dim) */
+  MSDA_ERR_LAUNCH = -3,           /* a kernel launch failed */
+  MSDA_ERR_DEVICE = -4            /* a HIP runtime query failed */
+};
+
+/* Maximum number of feature levels per call. */
+#define MSDA_MAX_LEVELS 16
+
+/* Library version string, e.g. "msda-gfx950 0.1.0". */
+const char* msda_version(void);
+
+/* Message describing the last failed call on the calling thread ("" if none). */
+const char* msda_last_error(void);
+
+/*
+ * Forward: output = sum_{l,p} A[b,q,h,l*P+p] * bilinear(value[b*H+h], level l, loc[b,q,h,l,p]).
+ * Replaces ms_deform_attn_core_rows (src/rfdetr_jax/models/ops.py:208-292) and its "pallas"
+ * branch (ops.py:243-263 -> deform_pallas.py:193-228 sample_weighted).
+ * output_dtype is the dtype of result_type(value, attention_weights) in the reference (ops.py:260),
+ * i.e. MSDA_DTYPE_F32 whenever the weights are f32; MSDA_DTYPE_BF16 is accepted for callers that
+ * keep bf16 weights.
+ */
+int msda_fwd(const void* value, int value_dtype,
+             const float* sampling_locations, const float* attention_weights,
+             void* output, int output_dtype,
+             int batch, int n_heads, int head_dim, int len_query,
+             int n_levels, int n_points,
+             const int32_t* spatial_shapes, const int32_t* level_start_index,
+             int64_t len_value, void* stream);
+
+/*
+ * Backward (vector-Jacobian product of msda_fwd with cotangent grad_output):
+ *   grad_value              [batch*n_heads, len_value, head_dim]  value_dtype (accumulated in f32,
+ *                           rounded once; deform_pallas.py:175 casts the same way)
+ *   grad_sampling_locations [batch, len_query, n_heads, n_levels, n_points, 2] f32
+ *   grad_attention_weights  [batch, len_query, n_heads, n_levels*n_points]     f32
+ * Replaces the JAX autodiff VJP of ops.py:64-134/289 and deform_pallas.py:157-175 (_sample_bwd).
+ * Any of the three gradient pointers may be NULL to skip that gradient. grad_output has
+ * grad_output_dtype (the forward's output dtype).
+ */
+int msda_bwd(const void* value, int value_dtype,
+             const float* sampling_locations, const float* attention_weights,
+             const void* grad_output, int grad_output_dtype,
+             void* grad_value, float* grad_sampling_locations, float* grad_attention_weights,
+             int batch, int n_heads, int head_dim, int len_query,
+             int n_levels, int n_points,
+             const int32_t* spatial_shapes, const int32_t* level_start_index,
+             int64_t len_value, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSDA_H_ */

@@ -1,0 +1,397 @@
+// msda_abi.hip — C ABI (include/msda.h): argument validation, launch planning, kernel dispatch.
+//
+// Validation runs before any HIP call, so malformed calls fail with MSDA_ERR_INVALID_ARGUMENT /
+// MSDA_ERR_UNSUPPORTED on any host (no GPU needed). Launch planning reads two device attributes
+// (LDS per workgroup, CU count) once per device.
+#include "msda.h"
+#include "msda_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+// ------------------------------------------------------------------------------------------
+// shape validation shared by forward and backward
+
+struct Shape {
+  int batch, heads, dim, queries, levels, points;
+  int64_t len_value;
+  int h[msda::kMaxLevels], w[msda::kMaxLevels];
+  int64_t start[msda::kMaxLevels];
+};
+
+int validate(Shape* s, int batch, int heads, int dim, int queries, int levels, int points,
+             const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value) {
+  if (batch < 0 || queries < 0) return fail(MSDA_ERR_INVALID_ARGUMENT, "batch (%d) and len_query (%d) must be >= 0", batch, queries);
+  if (heads < 1 || dim < 1 || points < 1) return fail(MSDA_ERR_INVALID_ARGUMENT, "n_heads (%d), head_dim (%d) and n_points (%d) must be >= 1", heads, dim, points);
+  if (levels < 1 || levels > MSDA_MAX_LEVELS) return fail(MSDA_ERR_INVALID_ARGUMENT, "n_levels must be in [1, %d], got %d", MSDA_MAX_LEVELS, levels);
+  if (spatial_shapes == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "spatial_shapes is NULL");
+  int64_t acc = 0;
+  for (int l = 0; l < levels; ++l) {
+    const int hl = spatial_shapes[2 * l], wl = spatial_shapes[2 * l + 1];
+    if (hl < 1 || wl < 1) return fail(MSDA_ERR_INVALID_ARGUMENT, "spatial_shapes[%d] = (%d, %d) must be positive", l, hl, wl);
+    if (level_start_index != nullptr && level_start_index[l] != acc)
+      return fail(MSDA_ERR_INVALID_ARGUMENT, "level_start_index[%d] = %d, expected %lld (prefix sum of H*W)", l,
+                  level_start_index[l], static_cast<long long>(acc));
+    s->h[l] = hl;
+    s->w[l] = wl;
+    s->start[l] = acc;
+    acc += static_cast<int64_t>(hl) * wl;
+  }
+  if (acc != len_value) return fail(MSDA_ERR_INVALID_ARGUMENT, "len_value = %lld but sum(H*W) = %lld", static_cast<long long>(len_value), static_cast<long long>(acc));
+  // Index arithmetic inside a slice is 32-bit.
+  if (len_value * dim > (int64_t{1} << 30)) return fail(MSDA_ERR_UNSUPPORTED, "len_value * head_dim = %lld exceeds 2^30", static_cast<long long>(len_value * dim));
+  if (static_cast<int64_t>(batch) * heads * 4096 > (int64_t{1} << 31)) return fail(MSDA_ERR_UNSUPPORTED, "batch * n_heads too large");
+  if (static_cast<int64_t>(levels) * points > 4096) return fail(MSDA_ERR_UNSUPPORTED, "n_levels * n_points = %d exceeds 4096", levels * points);
+  s->batch = batch;
+  s->heads = heads;
+  s->dim = dim;
+  s->queries = queries;
+  s->levels = levels;
+  s->points = points;
+  s->len_value = len_value;
+  return MSDA_OK;
+}
+
+int check_dtype(int dt, const char* what) {
+  if (dt != MSDA_DTYPE_F32 && dt != MSDA_DTYPE_BF16) return fail(MSDA_ERR_UNSUPPORTED, "%s: unsupported dtype code %d", what, dt);
+  return MSDA_OK;
+}
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Channels per lane: the widest of 16 bytes that divides head_dim and keeps every listed
+// pointer aligned.
+int pick_vec(int dim, int value_bytes, std::initializer_list<std::pair<const void*, int>> ptrs) {
+  int vec = 16 / value_bytes;
+  while (vec > 1) {
+    bool ok = dim % vec == 0;
+    for (auto& pr : ptrs)
+      if (pr.first != nullptr && !aligned(pr.first, static_cast<size_t>(vec) * pr.second)) ok = false;
+    if (ok) break;
+    vec >>= 1;
+  }
+  return vec;
+}
+
+int lpq_shift_for(int dim, int vec) {
+  const int lanes = (dim + vec - 1) / vec;
+  int shift = 0;
+  while ((1 << shift) < lanes) ++shift;
+  return shift;
+}
+
+// ------------------------------------------------------------------------------------------
+// per-device attributes (one-time, idempotent initialisation)
+
+struct DevInfo {
+  int lds_bytes;
+  int cus;
+};
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_dev_lds[kMaxDevices];
+std::atomic<int> g_dev_cus[kMaxDevices];
+
+int device_info(DevInfo* info) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MSDA_ERR_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MSDA_ERR_DEVICE, "device index %d out of range", dev);
+  int lds = g_dev_lds[dev].load(std::memory_order_relaxed);
+  int cus = g_dev_cus[dev].load(std::memory_order_relaxed);
+  if (lds <= 0 || cus <= 0) {
+    e = hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (e != hipSuccess) return fail(MSDA_ERR_DEVICE, "hipDeviceGetAttribute(LDS): %s", hipGetErrorString(e));
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return fail(MSDA_ERR_DEVICE, "hipDeviceGetAttribute(CUs): %s", hipGetErrorString(e));
+    g_dev_lds[dev].store(lds, std::memory_order_relaxed);
+    g_dev_cus[dev].store(cus, std::memory_order_relaxed);
+  }
+  info->lds_bytes = lds;
+  info->cus = cus;
+  return MSDA_OK;
+}
+
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  if (v == nullptr || *v == 0) return dflt;
+  return std::atoi(v);
+}
+
+inline int align16(int64_t x) { return static_cast<int>((x + 15) & ~int64_t{15}); }
+
+// Allow a kernel instantiation to use more than 64 KB of dynamic LDS. The attribute is raised
+// once per (instantiation, device) to the largest size requested so far, so steady-state launches
+// (including ones under stream capture) make no extra runtime call.
+template <typename K>
+int allow_lds(K kernel, int bytes, std::atomic<int> (&granted)[kMaxDevices]) {
+  if (bytes <= 65536) return MSDA_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return fail(MSDA_ERR_DEVICE, "hipGetDevice failed");
+  if (granted[dev].load(std::memory_order_relaxed) >= bytes) return MSDA_OK;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MSDA_ERR_LAUNCH, "hipFuncSetAttribute(%d bytes LDS): %s", bytes, hipGetErrorString(e));
+  }
+  int cur = granted[dev].load(std::memory_order_relaxed);
+  while (cur < bytes && !granted[dev].compare_exchange_weak(cur, bytes)) {
+  }
+  return MSDA_OK;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MSDA_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return MSDA_OK;
+}
+
+// ------------------------------------------------------------------------------------------
+// forward dispatch
+
+template <typename VT, int VEC>
+int launch_fwd(const msda::FwdParams& p, int grid, int lds, hipStream_t stream) {
+  static std::atomic<int> granted[kMaxDevices];  // per instantiation
+  auto k = msda::fwd_kernel<VT, VEC>;
+  int rc = allow_lds(k, lds, granted);
+  if (rc != MSDA_OK) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(msda::kFwdThreads), lds, stream, p);
+  return check_launch("msda forward");
+}
+
+template <typename VT>
+int dispatch_fwd(int vec, const msda::FwdParams& p, int grid, int lds, hipStream_t stream) {
+  switch (vec) {
+    case 1: return launch_fwd<VT, 1>(p, grid, lds, stream);
+    case 2: return launch_fwd<VT, 2>(p, grid, lds, stream);
+    case 4: return launch_fwd<VT, 4>(p, grid, lds, stream);
+    case 8:
+      if constexpr (sizeof(VT) == 2) return launch_fwd<VT, 8>(p, grid, lds, stream);
+      break;
+  }
+  return fail(MSDA_ERR_UNSUPPORTED, "no forward kernel for %d channels per lane", vec);
+}
+
+template <typename VT, int VEC>
+int launch_bwd(const msda::BwdParams& p, int grid, int lds, hipStream_t stream) {
+  static std::atomic<int> granted[kMaxDevices];  // per instantiation
+  auto k = msda::bwd_kernel<VT, VEC>;
+  int rc = allow_lds(k, lds, granted);
+  if (rc != MSDA_OK) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(msda::kBwdThreads), lds, stream, p);
+  return check_launch("msda backward");
+}
+
+template <typename VT>
+int dispatch_bwd(int vec, const msda::BwdParams& p, int grid, int lds, hipStream_t stream) {
+  switch (vec) {
+    case 1: return launch_bwd<VT, 1>(p, grid, lds, stream);
+    case 2: return launch_bwd<VT, 2>(p, grid, lds, stream);
+    case 4: return launch_bwd<VT, 4>(p, grid, lds, stream);
+    case 8:
+      if constexpr (sizeof(VT) == 2) return launch_bwd<VT, 8>(p, grid, lds, stream);
+      break;
+  }
+  return fail(MSDA_ERR_UNSUPPORTED, "no backward kernel for %d channels per lane", vec);
+}
+
+// 16-byte staging / flushing is allowed when every level's rows start and end on 16 bytes.
+bool rows_16b(const Shape& s, int vbytes, const void* a, const void* b) {
+  if (!aligned(a, 16) || (b != nullptr && !aligned(b, 16))) return false;
+  if ((s.len_value * s.dim * vbytes) % 16 != 0) return false;
+  for (int l = 0; l < s.levels; ++l) {
+    if ((s.start[l] * s.dim * vbytes) % 16 != 0) return false;
+    if ((static_cast<int64_t>(s.w[l]) * s.dim * vbytes) % 16 != 0) return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* msda_version(void) { return "msda-gfx950 0.1.0"; }
+
+const char* msda_last_error(void) { return g_last_error.c_str(); }
+
+int msda_fwd(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
+             void* output, int output_dtype, int batch, int n_heads, int head_dim, int len_query, int n_levels,
+             int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value,
+             void* stream) {
+  g_last_error.clear();
+  Shape s;
+  int rc = validate(&s, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value);
+  if (rc != MSDA_OK) return rc;
+  if ((rc = check_dtype(value_dtype, "value")) != MSDA_OK) return rc;
+  if ((rc = check_dtype(output_dtype, "output")) != MSDA_OK) return rc;
+  if (batch == 0 || len_query == 0) return MSDA_OK;
+  if (value == nullptr || sampling_locations == nullptr || attention_weights == nullptr || output == nullptr)
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_fwd: NULL tensor pointer");
+  if (!aligned(sampling_locations, 8) || !aligned(attention_weights, 4))
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "sampling_locations must be 8-byte aligned and attention_weights 4-byte aligned");
+  const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
+  const int obytes = output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
+  if (!aligned(value, vbytes) || !aligned(output, obytes)) return fail(MSDA_ERR_INVALID_ARGUMENT, "value/output not aligned to their element size");
+  const int vec = pick_vec(head_dim, vbytes, {{value, vbytes}, {output, obytes}});
+  const int shift = lpq_shift_for(head_dim, vec);
+  if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
+
+  DevInfo dev;
+  if ((rc = device_info(&dev)) != MSDA_OK) return rc;
+
+  msda::FwdParams p{};
+  p.value = value;
+  p.loc = sampling_locations;
+  p.attn = attention_weights;
+  p.out = output;
+  p.out_bf16 = output_dtype == MSDA_DTYPE_BF16;
+  p.heads = n_heads;
+  p.dim = head_dim;
+  p.queries = len_query;
+  p.levels = n_levels;
+  p.points = n_points;
+  p.len_value = len_value;
+  p.lpq_shift = shift;
+  p.vec16 = rows_16b(s, vbytes, value, nullptr);
+
+  // Stage every level that fits the per-workgroup LDS budget; the rest is read through L2.
+  const int budget = std::min(dev.lds_bytes, env_int("MSDA_FWD_LDS_BUDGET", 80 * 1024));
+  int lds = 0;
+  for (int l = 0; l < n_levels; ++l) {
+    const int64_t bytes = static_cast<int64_t>(s.h[l]) * s.w[l] * head_dim * vbytes;
+    p.lv[l] = msda::LevelDesc{s.h[l], s.w[l], static_cast<int>(s.start[l]), -1, 0, 0};
+    if (lds + align16(bytes) <= budget) {
+      p.lv[l].lds = lds / vbytes;
+      lds += align16(bytes);
+    }
+  }
+  const int slots = msda::kFwdThreads >> shift;
+  const int64_t N = static_cast<int64_t>(batch) * n_heads;
+  const int target = env_int("MSDA_FWD_TARGET_WGS", 4 * dev.cus);
+  const int max_chunks = (len_query + slots - 1) / slots;
+  int nqc = static_cast<int>(std::min<int64_t>(max_chunks, std::max<int64_t>(1, (target + N - 1) / N)));
+  int per = (len_query + nqc - 1) / nqc;
+  p.qchunk = ((per + slots - 1) / slots) * slots;
+  p.nqc = (len_query + p.qchunk - 1) / p.qchunk;
+  const int64_t grid = N * p.nqc;
+  if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "forward grid too large");
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (value_dtype == MSDA_DTYPE_BF16) return dispatch_fwd<msda::bf16_t>(vec, p, static_cast<int>(grid), lds, st);
+  return dispatch_fwd<float>(vec, p, static_cast<int>(grid), lds, st);
+}
+
+int msda_bwd(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
+             const void* grad_output, int grad_output_dtype, void* grad_value, float* grad_sampling_locations,
+             float* grad_attention_weights, int batch, int n_heads, int head_dim, int len_query, int n_levels,
+             int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value,
+             void* stream) {
+  g_last_error.clear();
+  Shape s;
+  int rc = validate(&s, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value);
+  if (rc != MSDA_OK) return rc;
+  if ((rc = check_dtype(value_dtype, "value")) != MSDA_OK) return rc;
+  if ((rc = check_dtype(grad_output_dtype, "grad_output")) != MSDA_OK) return rc;
+  if (batch == 0) return MSDA_OK;
+  if (grad_value == nullptr && grad_sampling_locations == nullptr && grad_attention_weights == nullptr) return MSDA_OK;
+  if (value == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_bwd: value is NULL");
+  if (len_query > 0 && (sampling_locations == nullptr || attention_weights == nullptr || grad_output == nullptr))
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_bwd: NULL tensor pointer");
+  if (!aligned(sampling_locations, 8) || !aligned(attention_weights, 4) || !aligned(grad_sampling_locations, 8) ||
+      !aligned(grad_attention_weights, 4))
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "location tensors must be 8-byte aligned and weight tensors 4-byte aligned");
+  const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
+  const int gbytes = grad_output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
+  if (!aligned(value, vbytes) || !aligned(grad_value, vbytes) || !aligned(grad_output, gbytes))
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "value/grad_value/grad_output not aligned to their element size");
+  const int vec = pick_vec(head_dim, vbytes, {{value, vbytes}, {grad_value, vbytes}, {grad_output, gbytes}});
+  const int shift = lpq_shift_for(head_dim, vec);
+  if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
+
+  DevInfo dev;
+  if ((rc = device_info(&dev)) != MSDA_OK) return rc;
+
+  msda::BwdParams p{};
+  p.value = value;
+  p.loc = sampling_locations;
+  p.attn = attention_weights;
+  p.gout = grad_output;
+  p.dvalue = grad_value;
+  p.dloc = grad_sampling_locations;
+  p.dattn = grad_attention_weights;
+  p.gout_bf16 = grad_output_dtype == MSDA_DTYPE_BF16;
+  p.heads = n_heads;
+  p.dim = head_dim;
+  p.queries = len_query;
+  p.levels = n_levels;
+  p.points = n_points;
+  p.len_value = len_value;
+  p.lpq_shift = shift;
+  p.vec16 = rows_16b(s, vbytes, value, grad_value);
+
+  // Bands: enough rows per band to keep the workgroup count near the target, few enough that the
+  // staged rows (+1 halo row) and the f32 accumulator fit the LDS budget.
+  const int64_t N = static_cast<int64_t>(batch) * n_heads;
+  const int target = env_int("MSDA_BWD_TARGET_WGS", 2 * dev.cus);
+  const int soft_budget = std::min(dev.lds_bytes, env_int("MSDA_BWD_LDS_BUDGET", 80 * 1024));
+  const int hard_budget = dev.lds_bytes;
+  int64_t total_area = 0;
+  for (int l = 0; l < n_levels; ++l) total_area += static_cast<int64_t>(s.h[l]) * s.w[l];
+  const int64_t want_items = std::max<int64_t>(1, (target + N - 1) / N);
+  int nwork = 0;
+  int lds_max = 0;
+  for (int l = 0; l < n_levels; ++l) {
+    const int64_t row_v = static_cast<int64_t>(s.w[l]) * head_dim * vbytes;
+    const int64_t row_a = static_cast<int64_t>(s.w[l]) * head_dim * 4;
+    auto bytes_for = [&](int rb) -> int64_t {
+      const int staged = std::min(rb + 1, s.h[l]);
+      return align16(staged * row_v) + rb * row_a;
+    };
+    int budget = soft_budget;
+    if (bytes_for(1) > budget) budget = hard_budget;
+    if (bytes_for(1) > budget)
+      return fail(MSDA_ERR_UNSUPPORTED, "level %d row (width %d, head_dim %d) does not fit in LDS", l, s.w[l], head_dim);
+    int rb_max = 1;
+    while (rb_max < s.h[l] && bytes_for(rb_max + 1) <= budget) ++rb_max;
+    const int nb_min = (s.h[l] + rb_max - 1) / rb_max;
+    const int64_t area = static_cast<int64_t>(s.h[l]) * s.w[l];
+    int nb_want = static_cast<int>((want_items * area + total_area / 2) / total_area);
+    const int forced = env_int("MSDA_BWD_BANDS", 0);
+    if (forced > 0) nb_want = forced;
+    int nb = std::min(s.h[l], std::max(nb_min, std::max(1, nb_want)));
+    const int rb = (s.h[l] + nb - 1) / nb;
+    nb = (s.h[l] + rb - 1) / rb;
+    p.lv[l] = msda::LevelDesc{s.h[l], s.w[l], static_cast<int>(s.start[l]), -1, rb, nwork};
+    nwork += nb;
+    lds_max = std::max<int>(lds_max, static_cast<int>(bytes_for(rb)));
+  }
+  p.nwork = nwork;
+  const int64_t grid = N * nwork;
+  if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (value_dtype == MSDA_DTYPE_BF16) return dispatch_bwd<msda::bf16_t>(vec, p, static_cast<int>(grid), lds_max, st);
+  return dispatch_bwd<float>(vec, p, static_cast<int>(grid), lds_max, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,24 @@
+"""MI355X (gfx950) multi-scale deformable attention for RF-DETR-JAX's decoder.
+
+Host-side mirror of the reference interface ``rfdetr_jax.models.ops``
+(src/rfdetr_jax/models/ops.py:208-314): the same function names, argument meanings and errors,
+backed by hand-written HIP kernels through the C ABI in include/msda.h.
+"""
+
+from .ops import (
+    SAMPLERS,
+    ms_deform_attn,
+    ms_deform_attn_backward,
+    ms_deform_attn_core,
+    ms_deform_attn_core_rows,
+    ms_deform_attn_forward,
+)
+
+__all__ = [
+    "SAMPLERS",
+    "ms_deform_attn",
+    "ms_deform_attn_backward",
+    "ms_deform_attn_core",
+    "ms_deform_attn_core_rows",
+    "ms_deform_attn_forward",
+]

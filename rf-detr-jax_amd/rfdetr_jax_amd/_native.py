@@ -1,0 +1,75 @@
+"""ctypes binding of the HIP library's C ABI (include/msda.h).
+
+There is no CPU fallback: if the library is missing, :func:`lib` raises, and every op that
+needs it fails loudly.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from .build import LIB_PATH
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+OK = 0
+ERR_INVALID_ARGUMENT = -1
+ERR_UNSUPPORTED = -2
+ERR_LAUNCH = -3
+ERR_DEVICE = -4
+
+#: Every function include/msda.h declares, with its ctypes signature.
+_I = ctypes.c_int
+_P = ctypes.c_void_p
+_I32P = ctypes.POINTER(ctypes.c_int32)
+_SHAPE_ARGS = [_I] * 6 + [_I32P, _I32P, ctypes.c_int64, _P]
+SIGNATURES = {
+    "msda_version": ([], ctypes.c_char_p),
+    "msda_last_error": ([], ctypes.c_char_p),
+    "msda_fwd": ([_P, _I, _P, _P, _P, _I] + _SHAPE_ARGS, _I),
+    "msda_bwd": ([_P, _I, _P, _P, _P, _I, _P, _P, _P] + _SHAPE_ARGS, _I),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class MsdaError(RuntimeError):
+    """A failed library call; ``code`` is the MSDA_ERR_* status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"msda error {code}: {message}")
+        self.code = code
+
+
+def lib(path: str | None = None) -> ctypes.CDLL:
+    """Load (once) and return the HIP library."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        target = path or os.environ.get("MSDA_LIBRARY", LIB_PATH)
+        if not os.path.exists(target):
+            raise RuntimeError(
+                f"HIP library not found at {target}; build it with __graft_entry__.build() "
+                "(hipcc --offload-arch=gfx950). There is no CPU fallback."
+            )
+        handle = ctypes.CDLL(target)
+        for name, (argtypes, restype) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        if path is None:
+            _lib = handle
+        return handle
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        msg = lib().msda_last_error().decode("utf-8", "replace")
+        raise MsdaError(rc, msg)

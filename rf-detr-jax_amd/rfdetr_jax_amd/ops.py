@@ -1,0 +1,243 @@
+"""Multi-scale deformable attention on MI355X: the reference's entry points, backed by HIP.
+
+Mirrors ``rfdetr_jax.models.ops`` (src/rfdetr_jax/models/ops.py):
+
+* :func:`ms_deform_attn_core_rows` — ops.py:208-292, same arguments (``value [B*H, S, D]``,
+  ``spatial_shapes`` as Python ints, ``sampling_locations [B, Q, H, L, P, 2]``,
+  ``attention_weights [B, Q, H, L*P]``, ``sampler``), same result ``[B, Q, H*D]`` with dtype
+  ``result_type(value, attention_weights)`` (ops.py:260), same ``ValueError`` for an unknown
+  sampler (ops.py:235-238). Every sampler name the reference accepts selects the HIP kernels:
+  they compute the same function (the reference's tests hold them to 1e-5 of each other,
+  tests/test_ops.py:112-248), so configurations that name one keep working unchanged.
+* :func:`ms_deform_attn_core` — ops.py:295-314, ``value [B, H, D, S]``.
+* :func:`ms_deform_attn` — the ``(value, spatial_shapes, level_start_index, sampling_locations,
+  attention_weights)`` signature of the upstream Deformable-DETR op; ``level_start_index`` is
+  checked against the prefix sums of ``spatial_shapes`` (ops.py:265-267 derives them).
+
+Differentiation is a ``torch.autograd.Function`` whose forward and backward each enqueue one
+kernel through the C ABI — the counterpart of the reference's ``jax.custom_vjp`` around its fused
+sampler (deform_pallas.py:132-178). Tensors must be on a GPU: there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native
+
+#: Sampler names accepted by ms_deform_attn_core_rows (the reference's five, ops.py:235, + "hip").
+SAMPLERS = ("hip", "gather", "gather-f32", "matmul", "auto", "pallas")
+
+_VALUE_DTYPES = {torch.float32: _native.DTYPE_F32, torch.bfloat16: _native.DTYPE_BF16}
+
+
+def _as_shapes(spatial_shapes) -> tuple[tuple[int, int], ...]:
+    """Normalise ``spatial_shapes`` to a tuple of ``(H, W)`` Python ints."""
+    if isinstance(spatial_shapes, torch.Tensor):
+        spatial_shapes = spatial_shapes.detach().cpu().tolist()
+    shapes = tuple((int(h), int(w)) for h, w in spatial_shapes)
+    if not shapes:
+        raise ValueError("spatial_shapes must name at least one level")
+    return shapes
+
+
+def _prefix_sums(shapes) -> list[int]:
+    offsets = [0]
+    for h, w in shapes:
+        offsets.append(offsets[-1] + h * w)
+    return offsets
+
+
+def _check_level_start_index(level_start_index, shapes) -> None:
+    if level_start_index is None:
+        return
+    if isinstance(level_start_index, torch.Tensor):
+        level_start_index = level_start_index.detach().cpu().tolist()
+    got = [int(v) for v in level_start_index]
+    want = _prefix_sums(shapes)[:-1]
+    if got != want:
+        raise ValueError(f"level_start_index {got} does not match the prefix sums of spatial_shapes {want}")
+
+
+def _shape_arrays(shapes):
+    flat = [v for hw in shapes for v in hw]
+    arr = (ctypes.c_int32 * len(flat))(*flat)
+    starts = (ctypes.c_int32 * len(shapes))(*_prefix_sums(shapes)[:-1])
+    return arr, starts
+
+
+def _check_inputs(value, shapes, sampling_locations, attention_weights):
+    if value.dim() != 3:
+        raise ValueError(f"value must be [B*n_heads, sum(H*W), head_dim], got shape {tuple(value.shape)}")
+    if sampling_locations.dim() != 6 or sampling_locations.shape[-1] != 2:
+        raise ValueError(
+            f"sampling_locations must be [B, Lq, n_heads, n_levels, n_points, 2], got {tuple(sampling_locations.shape)}"
+        )
+    batch, len_query, n_heads, n_levels, n_points, _ = sampling_locations.shape
+    if n_levels != len(shapes):
+        raise ValueError(f"sampling_locations has {n_levels} levels but spatial_shapes has {len(shapes)}")
+    if tuple(attention_weights.shape) != (batch, len_query, n_heads, n_levels * n_points):
+        raise ValueError(
+            f"attention_weights must be {(batch, len_query, n_heads, n_levels * n_points)}, got {tuple(attention_weights.shape)}"
+        )
+    if value.shape[0] != batch * n_heads:
+        raise ValueError(f"value has {value.shape[0]} rows of slices, expected batch*n_heads = {batch * n_heads}")
+    if value.shape[1] != _prefix_sums(shapes)[-1]:
+        raise ValueError(f"value length {value.shape[1]} != sum(H*W) = {_prefix_sums(shapes)[-1]}")
+    if value.dtype not in _VALUE_DTYPES:
+        raise TypeError(f"value dtype {value.dtype} is not supported (float32 or bfloat16)")
+    for name, t in (("value", value), ("sampling_locations", sampling_locations), ("attention_weights", attention_weights)):
+        if t.device.type != "cuda":
+            raise RuntimeError(f"{name} is on {t.device}; the HIP kernels need GPU tensors (there is no CPU path)")
+    if sampling_locations.device != value.device or attention_weights.device != value.device:
+        raise RuntimeError("value, sampling_locations and attention_weights must be on the same device")
+    return batch, len_query, n_heads, n_levels, n_points, value.shape[2]
+
+
+def _out_dtype(value, attention_weights):
+    dt = torch.result_type(value, attention_weights)
+    if dt not in (torch.float32, torch.bfloat16):
+        dt = torch.float32
+    return dt
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def ms_deform_attn_forward(value, spatial_shapes, sampling_locations, attention_weights, level_start_index=None,
+                           out_dtype=None):
+    """One forward launch (no autograd): returns ``[B, Q, H*D]``.
+
+    ``sampling_locations`` / ``attention_weights`` of another float dtype are converted to f32
+    first (the reference computes positions in at least f32, ops.py:80, :270).
+    """
+    shapes = _as_shapes(spatial_shapes)
+    _check_level_start_index(level_start_index, shapes)
+    batch, len_query, n_heads, n_levels, n_points, head_dim = _check_inputs(
+        value, shapes, sampling_locations, attention_weights
+    )
+    out_dtype = out_dtype or _out_dtype(value, attention_weights)
+    value = value.contiguous()
+    loc = sampling_locations.to(torch.float32).contiguous()
+    attn = attention_weights.to(torch.float32).contiguous()
+    out = torch.empty((batch, len_query, n_heads * head_dim), dtype=out_dtype, device=value.device)
+    arr, starts = _shape_arrays(shapes)
+    lib = _native.lib()
+    with torch.cuda.device(value.device):
+        rc = lib.msda_fwd(
+            _ptr(value), _VALUE_DTYPES[value.dtype], _ptr(loc), _ptr(attn), _ptr(out), _VALUE_DTYPES[out_dtype],
+            batch, n_heads, head_dim, len_query, n_levels, n_points, arr, starts, value.shape[1], _stream(value.device),
+        )
+    _native.check(rc)
+    return out
+
+
+def ms_deform_attn_backward(value, spatial_shapes, sampling_locations, attention_weights, grad_output,
+                            level_start_index=None, needs=(True, True, True)):
+    """One backward launch: returns ``(grad_value, grad_sampling_locations, grad_attention_weights)``.
+
+    ``grad_value`` has the value dtype (f32 accumulation, one rounding); the other two are f32.
+    Entries of ``needs`` that are false come back as ``None`` and are not computed.
+    """
+    shapes = _as_shapes(spatial_shapes)
+    _check_level_start_index(level_start_index, shapes)
+    batch, len_query, n_heads, n_levels, n_points, head_dim = _check_inputs(
+        value, shapes, sampling_locations, attention_weights
+    )
+    if tuple(grad_output.shape) != (batch, len_query, n_heads * head_dim):
+        raise ValueError(f"grad_output must be {(batch, len_query, n_heads * head_dim)}, got {tuple(grad_output.shape)}")
+    value = value.contiguous()
+    loc = sampling_locations.to(torch.float32).contiguous()
+    attn = attention_weights.to(torch.float32).contiguous()
+    if grad_output.dtype not in _VALUE_DTYPES:
+        grad_output = grad_output.to(torch.float32)
+    grad_output = grad_output.contiguous()
+    dev = value.device
+    grad_value = torch.empty_like(value) if needs[0] else None
+    grad_loc = torch.empty(loc.shape, dtype=torch.float32, device=dev) if needs[1] else None
+    grad_attn = torch.empty(attn.shape, dtype=torch.float32, device=dev) if needs[2] else None
+    arr, starts = _shape_arrays(shapes)
+    lib = _native.lib()
+    with torch.cuda.device(dev):
+        rc = lib.msda_bwd(
+            _ptr(value), _VALUE_DTYPES[value.dtype], _ptr(loc), _ptr(attn), _ptr(grad_output),
+            _VALUE_DTYPES[grad_output.dtype], _ptr(grad_value), _ptr(grad_loc), _ptr(grad_attn),
+            batch, n_heads, head_dim, len_query, n_levels, n_points, arr, starts, value.shape[1], _stream(dev),
+        )
+    _native.check(rc)
+    return grad_value, grad_loc, grad_attn
+
+
+class _MSDeformAttnFunction(torch.autograd.Function):
+    """custom-VJP pair: forward = msda_fwd, backward = msda_bwd (deform_pallas.py:132-178 contract)."""
+
+    @staticmethod
+    def forward(ctx, value, sampling_locations, attention_weights, shapes):
+        out = ms_deform_attn_forward(value, shapes, sampling_locations, attention_weights)
+        ctx.save_for_backward(value, sampling_locations, attention_weights)
+        ctx.shapes = shapes
+        ctx.out_dtype = out.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        value, loc, attn = ctx.saved_tensors
+        needs = ctx.needs_input_grad[:3]
+        grad_output = grad_output.to(ctx.out_dtype)
+        gv, gl, ga = ms_deform_attn_backward(value, ctx.shapes, loc, attn, grad_output, needs=needs)
+        # Gradients come back in the input dtypes (deform_pallas.py:175).
+        if gl is not None and gl.dtype != loc.dtype:
+            gl = gl.to(loc.dtype)
+        if ga is not None and ga.dtype != attn.dtype:
+            ga = ga.to(attn.dtype)
+        return gv, gl, ga, None
+
+
+def ms_deform_attn_core_rows(value, spatial_shapes, sampling_locations, attention_weights, sampler: str = "hip"):
+    """Sample and weight multi-scale features, channels last (ops.py:208-292).
+
+    Args:
+        value: ``[B * n_heads, sum(H*W), head_dim]``, float32 or bfloat16, on the GPU.
+        spatial_shapes: per-level ``(H, W)`` pairs.
+        sampling_locations: ``[B, Lq, n_heads, n_levels, n_points, 2]`` in ``[0, 1]`` (outside is
+            zero-padded).
+        attention_weights: ``[B, Lq, n_heads, n_levels * n_points]``.
+        sampler: one of :data:`SAMPLERS`; all select the HIP kernels.
+
+    Returns:
+        ``[B, Lq, n_heads * head_dim]`` with dtype ``result_type(value, attention_weights)``.
+
+    Raises:
+        ValueError: unknown ``sampler`` or inconsistent shapes.
+    """
+    if sampler not in SAMPLERS:
+        raise ValueError(
+            f"unknown sampler {sampler!r}; expected 'gather', 'gather-f32', 'matmul', 'auto', 'pallas' or 'hip'"
+        )
+    shapes = _as_shapes(spatial_shapes)
+    return _MSDeformAttnFunction.apply(value, sampling_locations, attention_weights, shapes)
+
+
+def ms_deform_attn(value, spatial_shapes, level_start_index, sampling_locations, attention_weights):
+    """``ms_deform_attn(value, spatial_shapes, level_start_index, sampling_locations, attention_weights)``.
+
+    ``value`` is in the rows layout ``[B * n_heads, sum(H*W), head_dim]`` the Flax module hands over
+    (ops.py:405-410). ``level_start_index`` must equal the prefix sums of ``spatial_shapes``.
+    """
+    shapes = _as_shapes(spatial_shapes)
+    _check_level_start_index(level_start_index, shapes)
+    return _MSDeformAttnFunction.apply(value, sampling_locations, attention_weights, shapes)
+
+
+def ms_deform_attn_core(value, spatial_shapes, sampling_locations, attention_weights):
+    """ops.py:295-314: ``value [B, n_heads, head_dim, sum(H*W)]``, transposed to rows first."""
+    batch, n_heads, head_dim, length = value.shape
+    rows = value.transpose(2, 3).reshape(batch * n_heads, length, head_dim)
+    return ms_deform_attn_core_rows(rows, spatial_shapes, sampling_locations, attention_weights)

@@ -1,0 +1,192 @@
+"""The C ABI and the host-side mirror, without a GPU.
+
+* The HIP library loads and exports every function include/msda.h declares.
+* Malformed calls return the documented error codes and messages; validation runs before any HIP
+  call, so these run on any host (no kernel is launched).
+* The Python mirror of ``ms_deform_attn_core_rows`` rejects unknown samplers and inconsistent
+  shapes as the reference does (ops.py:235-238), and refuses CPU tensors (there is no CPU path).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from rfdetr_jax_amd import _native
+from rfdetr_jax_amd import ops as hip_ops
+from rfdetr_jax_amd.build import LIB_PATH
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "msda.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(msda_\w+)\s*\(", text)))
+
+
+def test_library_is_built():
+    assert os.path.exists(LIB_PATH), f"run __graft_entry__.build() first: {LIB_PATH} missing"
+
+
+def test_library_exports_every_declared_function():
+    declared = _declared_functions()
+    assert {"msda_fwd", "msda_bwd", "msda_version", "msda_last_error"} <= set(declared)
+    lib = ctypes.CDLL(LIB_PATH)
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/msda.h but not exported"
+    assert set(declared) == set(_native.SIGNATURES), "ctypes signatures out of sync with include/msda.h"
+
+
+def test_version():
+    assert _native.lib().msda_version().decode().startswith("msda-gfx950")
+
+
+# --------------------------------------------------------------------------------------------
+# argument validation through the raw C ABI (no GPU work happens on these paths)
+
+
+def _shapes(pairs):
+    flat = [v for hw in pairs for v in hw]
+    return (ctypes.c_int32 * len(flat))(*flat)
+
+
+def _starts(vals):
+    return (ctypes.c_int32 * len(vals))(*vals)
+
+
+def _fwd(**kw):
+    args = dict(value=1 << 20, vdt=0, loc=1 << 20, attn=1 << 20, out=1 << 20, odt=0, batch=1, heads=2, dim=16,
+                queries=4, levels=1, points=2, shapes=_shapes([(4, 4)]), starts=_starts([0]), len_value=16)
+    args.update(kw)
+    lib = _native.lib()
+    rc = lib.msda_fwd(
+        ctypes.c_void_p(args["value"]), args["vdt"], ctypes.c_void_p(args["loc"]), ctypes.c_void_p(args["attn"]),
+        ctypes.c_void_p(args["out"]), args["odt"], args["batch"], args["heads"], args["dim"], args["queries"],
+        args["levels"], args["points"], args["shapes"], args["starts"], args["len_value"], None,
+    )
+    return rc, lib.msda_last_error().decode()
+
+
+def _bwd(**kw):
+    args = dict(value=1 << 20, vdt=0, loc=1 << 20, attn=1 << 20, gout=1 << 20, gdt=0, dv=1 << 20, dl=1 << 20,
+                da=1 << 20, batch=1, heads=2, dim=16, queries=4, levels=1, points=2, shapes=_shapes([(4, 4)]),
+                starts=_starts([0]), len_value=16)
+    args.update(kw)
+    lib = _native.lib()
+    rc = lib.msda_bwd(
+        ctypes.c_void_p(args["value"]), args["vdt"], ctypes.c_void_p(args["loc"]), ctypes.c_void_p(args["attn"]),
+        ctypes.c_void_p(args["gout"]), args["gdt"], ctypes.c_void_p(args["dv"]), ctypes.c_void_p(args["dl"]),
+        ctypes.c_void_p(args["da"]), args["batch"], args["heads"], args["dim"], args["queries"], args["levels"],
+        args["points"], args["shapes"], args["starts"], args["len_value"], None,
+    )
+    return rc, lib.msda_last_error().decode()
+
+
+@pytest.mark.parametrize("call", [_fwd, _bwd])
+@pytest.mark.parametrize(
+    "kw, code, message",
+    [
+        (dict(starts=_starts([3])), _native.ERR_INVALID_ARGUMENT, "level_start_index"),
+        (dict(len_value=17), _native.ERR_INVALID_ARGUMENT, "len_value"),
+        (dict(levels=0), _native.ERR_INVALID_ARGUMENT, "n_levels"),
+        (dict(levels=17), _native.ERR_INVALID_ARGUMENT, "n_levels"),
+        (dict(shapes=_shapes([(0, 16)]), len_value=0), _native.ERR_INVALID_ARGUMENT, "positive"),
+        (dict(heads=0), _native.ERR_INVALID_ARGUMENT, "n_heads"),
+        (dict(points=0), _native.ERR_INVALID_ARGUMENT, "n_points"),
+        (dict(batch=-1), _native.ERR_INVALID_ARGUMENT, "batch"),
+        (dict(vdt=7), _native.ERR_UNSUPPORTED, "dtype"),
+        (dict(dim=1024, shapes=_shapes([(4, 4)])), _native.ERR_UNSUPPORTED, "head_dim"),
+        (dict(shapes=None), _native.ERR_INVALID_ARGUMENT, "spatial_shapes"),
+    ],
+)
+def test_invalid_arguments_are_reported(call, kw, code, message):
+    rc, msg = call(**kw)
+    assert rc == code, msg
+    assert message in msg
+
+
+def test_two_levels_level_start_index_checked():
+    pairs = [(4, 4), (2, 2)]
+    rc, msg = _fwd(levels=2, shapes=_shapes(pairs), starts=_starts([0, 16]), len_value=20, value=0)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "NULL" in msg  # shapes fine, then the NULL value
+    rc, msg = _fwd(levels=2, shapes=_shapes(pairs), starts=_starts([0, 15]), len_value=20)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "level_start_index[1]" in msg
+
+
+def test_misaligned_locations_rejected():
+    rc, msg = _fwd(loc=(1 << 20) + 4)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "aligned" in msg
+
+
+def test_empty_calls_are_no_ops():
+    """batch = 0 (both) and len_query = 0 (forward) succeed without touching the device."""
+    assert _fwd(batch=0)[0] == _native.OK
+    assert _fwd(queries=0)[0] == _native.OK
+    assert _bwd(batch=0)[0] == _native.OK
+    assert _bwd(dv=0, dl=0, da=0)[0] == _native.OK  # nothing requested
+
+
+def test_error_message_is_per_call():
+    _fwd(levels=0)
+    assert _fwd(batch=0)[1] == ""
+
+
+# --------------------------------------------------------------------------------------------
+# host-side mirror of the reference interface
+
+
+def _cpu_inputs(b=1, q=3, h=2, l=1, p=2, d=4, shapes=((4, 4),)):
+    s = sum(x * y for x, y in shapes)
+    return (torch.zeros(b * h, s, d), torch.zeros(b, q, h, l, p, 2), torch.zeros(b, q, h, l * p))
+
+
+def test_unknown_sampler_is_rejected():
+    value, loc, attn = _cpu_inputs()
+    with pytest.raises(ValueError, match="unknown sampler"):
+        hip_ops.ms_deform_attn_core_rows(value, ((4, 4),), loc, attn, "nearest")
+
+
+def test_reference_sampler_names_are_accepted():
+    assert set(hip_ops.SAMPLERS) >= {"gather", "gather-f32", "matmul", "auto", "pallas", "hip"}
+
+
+def test_cpu_tensors_fail_loudly():
+    value, loc, attn = _cpu_inputs()
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        hip_ops.ms_deform_attn_core_rows(value, ((4, 4),), loc, attn, "gather")
+
+
+def test_level_start_index_must_match():
+    value, loc, attn = _cpu_inputs(l=2, shapes=((4, 4), (2, 2)))
+    with pytest.raises(ValueError, match="level_start_index"):
+        hip_ops.ms_deform_attn(value, ((4, 4), (2, 2)), torch.tensor([0, 15]), loc, attn)
+
+
+@pytest.mark.parametrize(
+    "bad",
+    ["value_rows", "value_len", "levels", "weights"],
+)
+def test_inconsistent_shapes_are_rejected(bad):
+    value, loc, attn = _cpu_inputs()
+    shapes = ((4, 4),)
+    if bad == "value_rows":
+        value = torch.zeros(3, 16, 4)
+    elif bad == "value_len":
+        value = torch.zeros(2, 15, 4)
+    elif bad == "levels":
+        shapes = ((4, 4), (2, 2))
+    else:
+        attn = torch.zeros(1, 3, 2, 3)
+    with pytest.raises(ValueError):
+        hip_ops.ms_deform_attn_forward(value, shapes, loc, attn)
+
+
+def test_unsupported_value_dtype():
+    value, loc, attn = _cpu_inputs()
+    with pytest.raises(TypeError, match="not supported"):
+        hip_ops.ms_deform_attn_forward(value.double(), ((4, 4),), loc, attn)

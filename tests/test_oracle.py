@@ -1,0 +1,248 @@
+"""Pin the CPU oracles (oracle/msda_ref.py, oracle/msda_ref.c) before trusting them.
+
+Checks, none of which retypes the oracle's formulas:
+* the reference's closed-form known answers (tests/test_ops.py:22-54);
+* torch ``F.grid_sample`` (bilinear, zeros, align_corners=False) — the routine ops.py:14-16 says
+  the reference sampler reproduces — and torch autograd through it, in float64;
+* central finite differences of the float64 forward;
+* exact identities: the output is linear in value and in the weights, so
+  ``<G, out> = <grad_value, value> = <grad_weights, weights>``;
+* a pure-Python brute-force loop on tiny inputs;
+* the C restatement against the NumPy one (forward and all gradients);
+* the committed golden fixtures are reproduced.
+Planted mistakes (a dropped corner, a transposed x/y, a wrong chain factor) are shown to fail.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import cref
+from oracle import msda_ref as R
+from rfdetr_jax_amd.workloads import make_inputs
+from tests._util import assert_close, golden_names, load_golden
+
+
+def _torch_reference(value, shapes, loc, attn, grad):
+    from tests.golden.make_golden import torch_reference
+
+    return torch_reference(value, shapes, loc, attn, grad)
+
+
+# --------------------------------------------------------------------------------------------
+# known answers of the reference's own tests
+
+
+def test_kat_pixel_centres():
+    """tests/test_ops.py:22-29: grid (-0.5,-0.5) -> 1, (0.5,0.5) -> 4 on [[1,2],[3,4]]."""
+    value = np.array([1, 2, 3, 4], np.float32).reshape(1, 4, 1)
+    loc = np.array([[0.25, 0.25], [0.75, 0.75]], np.float32).reshape(1, 2, 1, 1, 1, 2)
+    out = R.ms_deform_attn_core_rows(value, ((2, 2),), loc, np.ones((1, 2, 1, 1), np.float32))
+    assert out[0, 0, 0] == pytest.approx(1.0) and out[0, 1, 0] == pytest.approx(4.0)
+    assert cref.forward(value, ((2, 2),), loc, np.ones((1, 2, 1, 1), np.float32))[0, :, 0] == pytest.approx([1.0, 4.0])
+
+
+def test_kat_zero_pad():
+    """tests/test_ops.py:32-36: a sample far outside contributes exactly 0."""
+    out = R.ms_deform_attn_core_rows(np.ones((1, 4, 1), np.float32), ((2, 2),),
+                                     np.full((1, 1, 1, 1, 1, 2), 3.0, np.float32), np.ones((1, 1, 1, 1), np.float32))
+    assert out[0, 0, 0] == 0.0
+
+
+def test_kat_midpoint():
+    """tests/test_ops.py:39-43: midway between pixel values 0 and 4 gives 2."""
+    out = R.ms_deform_attn_core_rows(np.array([0, 4], np.float32).reshape(1, 2, 1), ((1, 2),),
+                                     np.full((1, 1, 1, 1, 1, 2), 0.5, np.float32), np.ones((1, 1, 1, 1), np.float32))
+    assert out[0, 0, 0] == pytest.approx(2.0)
+
+
+def test_kat_mean_of_points():
+    """tests/test_ops.py:46-54: uniform weights over two points of arange(4) give 1.5."""
+    out = R.ms_deform_attn_core_rows(np.arange(4, dtype=np.float32).reshape(1, 4, 1), ((2, 2),),
+                                     np.array([[0.25, 0.25], [0.75, 0.75]], np.float32).reshape(1, 1, 1, 1, 2, 2),
+                                     np.full((1, 1, 1, 2), 0.5, np.float32))
+    assert out.shape == (1, 1, 1)
+    assert out[0, 0, 0] == pytest.approx(1.5)
+
+
+# --------------------------------------------------------------------------------------------
+# independent references
+
+
+def _random_case(seed, shapes=((8, 16), (4, 8)), b=2, q=23, h=2, p=3, d=8, lo=-0.2, hi=1.2, dtype=np.float32):
+    rng = np.random.default_rng(seed)
+    s = sum(x * y for x, y in shapes)
+    value = rng.standard_normal((b * h, s, d)).astype(dtype)
+    loc = rng.uniform(lo, hi, (b, q, h, len(shapes), p, 2)).astype(dtype)
+    attn = rng.uniform(0, 1, (b, q, h, len(shapes) * p)).astype(dtype)
+    grad = rng.standard_normal((b, q, h * d)).astype(dtype)
+    return value, loc, attn, grad
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_forward_matches_torch_grid_sample(seed):
+    value, loc, attn, grad = _random_case(seed)
+    shapes = ((8, 16), (4, 8))
+    want = _torch_reference(value, shapes, loc, attn, grad)[0]
+    assert_close(R.ms_deform_attn_core_rows(value, shapes, loc, attn), want, 1e-6, "forward vs grid_sample")
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_vjp_matches_torch_autograd_float64(seed):
+    """float64 inputs: coordinates are float64 too (ops.py:269-270), as in torch."""
+    shapes = ((8, 16), (4, 8))
+    value, loc, attn, grad = _random_case(seed, dtype=np.float64)
+    _, t_gv, t_gl, t_ga = _torch_reference(value, shapes, loc, attn, grad)
+    gv, gl, ga = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
+    assert_close(gv, t_gv, 1e-12, "grad_value")
+    assert_close(gl, t_gl, 1e-12, "grad_loc")
+    assert_close(ga, t_ga, 1e-12, "grad_attn")
+
+
+def test_vjp_matches_finite_differences():
+    shapes = ((6, 7), (3, 4))
+    value, loc, attn, grad = _random_case(5, shapes=shapes, b=1, q=5, h=2, p=2, d=3, lo=0.05, hi=0.95, dtype=np.float64)
+    # Keep every sample away from pixel-cell boundaries, where floor() makes the map kinked.
+    for lvl, (hl, wl) in enumerate(shapes):
+        for axis, size in ((0, wl), (1, hl)):
+            pix = loc[:, :, :, lvl, :, axis] * size - 0.5
+            frac = pix - np.floor(pix)
+            pix = np.where(frac < 0.05, pix + 0.1, np.where(frac > 0.95, pix - 0.1, pix))
+            loc[:, :, :, lvl, :, axis] = (pix + 0.5) / size
+    gv, gl, ga = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
+
+    def f(v, lc, a):
+        return float(np.sum(R.ms_deform_attn_core_rows(v, shapes, lc, a) * grad))
+
+    eps = 1e-6
+    rng = np.random.default_rng(0)
+    for name, arr, analytic in (("value", value, gv), ("loc", loc, gl), ("attn", attn, ga)):
+        flat_idx = rng.choice(arr.size, size=min(25, arr.size), replace=False)
+        for i in flat_idx:
+            plus, minus = arr.copy(), arr.copy()
+            plus.reshape(-1)[i] += eps
+            minus.reshape(-1)[i] -= eps
+            args_p = {"value": (plus, loc, attn), "loc": (value, plus, attn), "attn": (value, loc, plus)}[name]
+            args_m = {"value": (minus, loc, attn), "loc": (value, minus, attn), "attn": (value, loc, minus)}[name]
+            numeric = (f(*args_p) - f(*args_m)) / (2 * eps)
+            assert abs(numeric - analytic.reshape(-1)[i]) <= 1e-6 * max(1.0, abs(numeric)), (name, i)
+
+
+def test_linearity_identities():
+    """out is linear in value and in weights: <G,out> = <dV,V> = <dA,A> exactly (up to rounding)."""
+    shapes = ((8, 16), (4, 8))
+    value, loc, attn, grad = _random_case(9)
+    out = R.ms_deform_attn_core_rows(value, shapes, loc, attn)
+    gv, _, ga = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
+    inner = float(np.sum(out * grad))
+    assert np.sum(gv * value) == pytest.approx(inner, rel=1e-10, abs=1e-10)
+    assert np.sum(ga * attn) == pytest.approx(inner, rel=1e-10, abs=1e-10)
+
+
+def test_brute_force_loop_agrees():
+    shapes = ((5, 4), (2, 3))
+    value, loc, attn, _ = _random_case(4, shapes=shapes, b=2, q=3, h=2, p=2, d=3)
+    assert_close(R.ms_deform_attn_core_rows(value, shapes, loc, attn),
+                 R.brute_force_forward(value, shapes, loc, attn), 1e-12, "brute force")
+
+
+def test_integer_translation():
+    """Shifting every sample by exactly one pixel to the right equals sampling a map shifted left."""
+    shapes = ((8, 16),)
+    rng = np.random.default_rng(12)
+    value = rng.standard_normal((2, 128, 4)).astype(np.float32)
+    # dyadic locations keep every coordinate exact in f32
+    loc = (rng.integers(8, 120, (1, 9, 2, 1, 2, 2)) / 128.0).astype(np.float32)
+    attn = rng.uniform(0, 1, (1, 9, 2, 2)).astype(np.float32)
+    moved = loc.copy()
+    moved[..., 0] += np.float32(1.0 / 16)
+    shifted = np.zeros_like(value).reshape(2, 8, 16, 4)
+    shifted[:, :, :-1] = value.reshape(2, 8, 16, 4)[:, :, 1:]
+    a = R.ms_deform_attn_core_rows(value, shapes, moved, attn)
+    b = R.ms_deform_attn_core_rows(shifted.reshape(2, 128, 4), shapes, loc, attn)
+    assert_close(a, b, 1e-12, "translation")
+
+
+# --------------------------------------------------------------------------------------------
+# planted mistakes must be caught by the references above
+
+
+def test_planted_mistakes_are_caught(monkeypatch):
+    shapes = ((8, 16), (4, 8))
+    value, loc, attn, grad = _random_case(1)
+    want = _torch_reference(value, shapes, loc, attn, grad)
+    orig = R._corners
+
+    def dropped_corner(*a):
+        idx, w, m, fx, fy = orig(*a)
+        w = w.copy()
+        w[..., 3] = 0.0
+        return idx, w, m, fx, fy
+
+    def swapped_xy(loc_x, loc_y, height, width):
+        return orig(loc_y, loc_x, height, width)
+
+    for bad in (dropped_corner, swapped_xy):
+        monkeypatch.setattr(R, "_corners", bad)
+        with pytest.raises(AssertionError):
+            assert_close(R.ms_deform_attn_core_rows(value, shapes, loc, attn), want[0], 1e-6, bad.__name__)
+        monkeypatch.setattr(R, "_corners", orig)
+    # a wrong chain factor (d ix/d loc = W/2 instead of W) shows up in grad_loc only
+    gv, gl, ga = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
+    with pytest.raises(AssertionError):
+        assert_close(gl / 2, want[2], 1e-6, "half chain factor")
+
+
+# --------------------------------------------------------------------------------------------
+# the C restatement (used as full-size oracle and CPU baseline)
+
+
+@pytest.mark.parametrize("seed", [0, 3])
+def test_c_oracle_matches_numpy(seed):
+    shapes = ((8, 16), (4, 8))
+    value, loc, attn, grad = _random_case(seed, q=31)
+    assert_close(cref.forward(value, shapes, loc, attn), R.ms_deform_attn_core_rows(value, shapes, loc, attn), 1e-6, "fwd")
+    cv, cl, ca = cref.backward(value, shapes, loc, attn, grad)
+    gv, gl, ga = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
+    assert_close(cv, gv, 1e-6, "grad_value")
+    assert_close(cl, gl, 1e-5, "grad_loc")
+    assert_close(ca, ga, 1e-6, "grad_attn")
+
+
+def test_c_oracle_config1_size():
+    """Benchmark config 1 at full size (B=16, 24x24, Q=300, P=2): C vs NumPy oracle."""
+    value, loc, attn, grad = make_inputs(1, 16, 16, 16, 300, ((24, 24),), 2)
+    shapes = ((24, 24),)
+    assert_close(cref.forward(value, shapes, loc, attn), R.ms_deform_attn_core_rows(value, shapes, loc, attn), 1e-5, "fwd")
+    cv, cl, ca = cref.backward(value, shapes, loc, attn, grad)
+    gv, gl, ga = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
+    assert_close(cv, gv, 1e-5, "grad_value")
+    assert_close(cl, gl, 1e-4, "grad_loc")
+    assert_close(ca, ga, 1e-5, "grad_attn")
+
+
+# --------------------------------------------------------------------------------------------
+# golden fixtures
+
+
+@pytest.mark.parametrize("name", golden_names())
+def test_golden_fixture_reproduced(name):
+    g = load_golden(name)
+    out = R.ms_deform_attn_core_rows(g["value"], g["shapes"], g["loc"], g["attn"])
+    gv, gl, ga = R.ms_deform_attn_core_rows_vjp(g["value"], g["shapes"], g["loc"], g["attn"], g["grad"])
+    assert_close(out, g["out"], 1e-6, "out")
+    assert_close(gv, g["grad_value"], 1e-6, "grad_value")
+    assert_close(gl, g["grad_loc"], 1e-6, "grad_loc")
+    assert_close(ga, g["grad_attn"], 1e-6, "grad_attn")
+    if "expect" in g["meta"]:
+        assert np.allclose(out.reshape(-1), g["meta"]["expect"])
+
+
+def test_bf16_round():
+    x = np.array([1.0, 1.00390625, 1.005859375, -2.5, 3.0e38, np.inf], np.float32)
+    r = R.bf16_round(x)
+    assert r[0] == 1.0 and r[1] == 1.0  # tie -> even
+    assert r[2] == np.float32(1.0078125)
+    assert r[3] == -2.5 and np.isinf(r[5])
+    assert np.isnan(R.bf16_round(np.array([np.nan], np.float32))[0])
