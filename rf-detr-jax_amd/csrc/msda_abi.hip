@@ -79,17 +79,20 @@ int check_dtype(int dt, const char* what) {
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// Channels per lane: the widest of 16 bytes that divides head_dim and keeps every listed
-// pointer aligned.
-int pick_vec(int dim, int value_bytes, std::initializer_list<std::pair<const void*, int>> ptrs) {
-  int vec = 16 / value_bytes;
-  while (vec > 1) {
-    bool ok = dim % vec == 0;
-    for (auto& pr : ptrs)
-      if (pr.first != nullptr && !aligned(pr.first, static_cast<size_t>(vec) * pr.second)) ok = false;
-    if (ok) break;
-    vec >>= 1;
-  }
+// Channels per lane (VEC): the largest power of two <= max_vec that divides head_dim and keeps
+// every listed pointer aligned to min(VEC * element size, 16) bytes. max_vec = 16 gives one lane
+// per query for head_dim 16 (the RF-DETR shape).
+int pick_vec(int dim, int max_vec, std::initializer_list<std::pair<const void*, int>> ptrs) {
+  auto fits = [&](int vec) {
+    if (dim % vec != 0) return false;
+    for (auto& pr : ptrs) {
+      const size_t a = std::min<size_t>(static_cast<size_t>(vec) * pr.second, 16);
+      if (pr.first != nullptr && !aligned(pr.first, a)) return false;
+    }
+    return true;
+  };
+  int vec = 16;
+  while (vec > 1 && (vec > max_vec || !fits(vec))) vec >>= 1;
   return vec;
 }
 
@@ -185,9 +188,8 @@ int dispatch_fwd(int vec, const msda::FwdParams& p, int grid, int lds, hipStream
     case 1: return launch_fwd<VT, 1>(p, grid, lds, stream);
     case 2: return launch_fwd<VT, 2>(p, grid, lds, stream);
     case 4: return launch_fwd<VT, 4>(p, grid, lds, stream);
-    case 8:
-      if constexpr (sizeof(VT) == 2) return launch_fwd<VT, 8>(p, grid, lds, stream);
-      break;
+    case 8: return launch_fwd<VT, 8>(p, grid, lds, stream);
+    case 16: return launch_fwd<VT, 16>(p, grid, lds, stream);
   }
   return fail(MSDA_ERR_UNSUPPORTED, "no forward kernel for %d channels per lane", vec);
 }
@@ -208,9 +210,8 @@ int dispatch_bwd(int vec, const msda::BwdParams& p, int grid, int lds, hipStream
     case 1: return launch_bwd<VT, 1>(p, grid, lds, stream);
     case 2: return launch_bwd<VT, 2>(p, grid, lds, stream);
     case 4: return launch_bwd<VT, 4>(p, grid, lds, stream);
-    case 8:
-      if constexpr (sizeof(VT) == 2) return launch_bwd<VT, 8>(p, grid, lds, stream);
-      break;
+    case 8: return launch_bwd<VT, 8>(p, grid, lds, stream);
+    case 16: return launch_bwd<VT, 16>(p, grid, lds, stream);
   }
   return fail(MSDA_ERR_UNSUPPORTED, "no backward kernel for %d channels per lane", vec);
 }
@@ -252,7 +253,7 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
   const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   const int obytes = output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   if (!aligned(value, vbytes) || !aligned(output, obytes)) return fail(MSDA_ERR_INVALID_ARGUMENT, "value/output not aligned to their element size");
-  const int vec = pick_vec(head_dim, vbytes, {{value, vbytes}, {output, obytes}});
+  const int vec = pick_vec(head_dim, env_int("MSDA_FWD_MAX_VEC", 16), {{value, vbytes}, {output, obytes}});
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
 
@@ -293,6 +294,13 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
   int per = (len_query + nqc - 1) / nqc;
   p.qchunk = ((per + slots - 1) / slots) * slots;
   p.nqc = (len_query + p.qchunk - 1) / p.qchunk;
+  // Stage the chunk's locations (8 B) and weights (4 B) per sample when they fit the budget too.
+  const int64_t loc_bytes = static_cast<int64_t>(p.qchunk) * n_levels * n_points * 12;
+  p.loc_lds = -1;
+  if (env_int("MSDA_FWD_STAGE_LOC", 1) != 0 && lds + loc_bytes <= budget) {
+    p.loc_lds = lds;
+    lds += align16(loc_bytes);
+  }
   const int64_t grid = N * p.nqc;
   if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "forward grid too large");
 
@@ -324,7 +332,8 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   const int gbytes = grad_output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   if (!aligned(value, vbytes) || !aligned(grad_value, vbytes) || !aligned(grad_output, gbytes))
     return fail(MSDA_ERR_INVALID_ARGUMENT, "value/grad_value/grad_output not aligned to their element size");
-  const int vec = pick_vec(head_dim, vbytes, {{value, vbytes}, {grad_value, vbytes}, {grad_output, gbytes}});
+  const int vec = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 16),
+                           {{value, vbytes}, {grad_value, vbytes}, {grad_output, gbytes}});
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
 
@@ -363,9 +372,14 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   for (int l = 0; l < n_levels; ++l) {
     const int64_t row_v = static_cast<int64_t>(s.w[l]) * head_dim * vbytes;
     const int64_t row_a = static_cast<int64_t>(s.w[l]) * head_dim * 4;
+    // staged rows (+1 halo) | one f32 accumulator per wave | one int tag per pixel per wave |
+    // one record ring per wave
+    const int nwaves = msda::kBwdThreads / 64;
     auto bytes_for = [&](int rb) -> int64_t {
       const int staged = std::min(rb + 1, s.h[l]);
-      return align16(staged * row_v) + rb * row_a;
+      const int64_t acc = ((rb * row_a / 4 + 3) & ~int64_t{3}) * 4;
+      const int64_t tags = ((nwaves * static_cast<int64_t>(rb) * s.w[l] + 3) & ~int64_t{3}) * 4;
+      return align16(staged * row_v) + nwaves * acc + tags + nwaves * msda::kRing * 4;
     };
     int budget = soft_budget;
     if (bytes_for(1) > budget) budget = hard_budget;
@@ -386,6 +400,12 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     lds_max = std::max<int>(lds_max, static_cast<int>(bytes_for(rb)));
   }
   p.nwork = nwork;
+  // Locations / weights of `chunk_q` queries of one level are staged in LDS at a time.
+  p.chunk_q = std::max(1, std::min(len_query, env_int("MSDA_BWD_CHUNK", 1024)));
+  p.loc_lds = align16(lds_max);
+  lds_max = p.loc_lds + align16(static_cast<int64_t>(p.chunk_q) * n_points * 12);
+  if (lds_max > hard_budget)
+    return fail(MSDA_ERR_UNSUPPORTED, "backward LDS plan (%d bytes) exceeds the device's %d bytes", lds_max, hard_budget);
   const int64_t grid = N * nwork;
   if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
 

@@ -100,7 +100,7 @@ def _bwd(**kw):
         (dict(points=0), _native.ERR_INVALID_ARGUMENT, "n_points"),
         (dict(batch=-1), _native.ERR_INVALID_ARGUMENT, "batch"),
         (dict(vdt=7), _native.ERR_UNSUPPORTED, "dtype"),
-        (dict(dim=1024, shapes=_shapes([(4, 4)])), _native.ERR_UNSUPPORTED, "head_dim"),
+        (dict(dim=2048, shapes=_shapes([(4, 4)])), _native.ERR_UNSUPPORTED, "head_dim"),
         (dict(shapes=None), _native.ERR_INVALID_ARGUMENT, "spatial_shapes"),
     ],
 )
