@@ -253,7 +253,7 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
   const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   const int obytes = output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   if (!aligned(value, vbytes) || !aligned(output, obytes)) return fail(MSDA_ERR_INVALID_ARGUMENT, "value/output not aligned to their element size");
-  const int vec = pick_vec(head_dim, env_int("MSDA_FWD_MAX_VEC", 16), {{value, vbytes}, {output, obytes}});
+  const int vec = pick_vec(head_dim, env_int("MSDA_FWD_MAX_VEC", 8), {{value, vbytes}, {output, obytes}});
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
 
@@ -358,54 +358,45 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   p.lpq_shift = shift;
   p.vec16 = rows_16b(s, vbytes, value, grad_value);
 
-  // Bands: enough rows per band to keep the workgroup count near the target, few enough that the
-  // staged rows (+1 halo row) and the f32 accumulator fit the LDS budget.
+  // Bands of image rows: each (slice, level, band) workgroup owns the band's grad_value rows.
+  // Rows per band are chosen so the workgroup count reaches the target and the LDS layout
+  // (staged rows, accumulator, cell tables, chunk buffers) fits the budget.
   const int64_t N = static_cast<int64_t>(batch) * n_heads;
   const int target = env_int("MSDA_BWD_TARGET_WGS", 2 * dev.cus);
-  const int soft_budget = std::min(dev.lds_bytes, env_int("MSDA_BWD_LDS_BUDGET", 80 * 1024));
-  const int hard_budget = dev.lds_bytes;
+  const int budget = std::min(dev.lds_bytes, env_int("MSDA_BWD_LDS_BUDGET", 80 * 1024));
+  const int scan_seg = std::max(64, std::min({std::max(len_query, 1), env_int("MSDA_BWD_SCAN_SEG", 4096), 65536}));
+  const int64_t want_items = std::max<int64_t>(1, (target + N - 1) / N);
   int64_t total_area = 0;
   for (int l = 0; l < n_levels; ++l) total_area += static_cast<int64_t>(s.h[l]) * s.w[l];
-  const int64_t want_items = std::max<int64_t>(1, (target + N - 1) / N);
+  int chunk_m = std::max(16, env_int("MSDA_BWD_CHUNK", 256));
   int nwork = 0;
   int lds_max = 0;
   for (int l = 0; l < n_levels; ++l) {
-    const int64_t row_v = static_cast<int64_t>(s.w[l]) * head_dim * vbytes;
-    const int64_t row_a = static_cast<int64_t>(s.w[l]) * head_dim * 4;
-    // staged rows (+1 halo) | one f32 accumulator per wave | one int tag per pixel per wave |
-    // one record ring per wave
-    const int nwaves = msda::kBwdThreads / 64;
-    auto bytes_for = [&](int rb) -> int64_t {
-      const int staged = std::min(rb + 1, s.h[l]);
-      const int64_t acc = ((rb * row_a / 4 + 3) & ~int64_t{3}) * 4;
-      const int64_t tags = ((nwaves * static_cast<int64_t>(rb) * s.w[l] + 3) & ~int64_t{3}) * 4;
-      return align16(staged * row_v) + nwaves * acc + tags + nwaves * msda::kRing * 4;
+    auto bytes_for = [&](int rb, int m) {
+      return msda::bwd_layout(std::min(rb + 1, s.h[l]), rb, s.w[l], head_dim, vbytes, n_points, m, scan_seg).total;
     };
-    int budget = soft_budget;
-    if (bytes_for(1) > budget) budget = hard_budget;
-    if (bytes_for(1) > budget)
-      return fail(MSDA_ERR_UNSUPPORTED, "level %d row (width %d, head_dim %d) does not fit in LDS", l, s.w[l], head_dim);
+    // shrink the chunk until a one-row band fits the device
+    while (bytes_for(1, chunk_m) > dev.lds_bytes && chunk_m > 16) chunk_m >>= 1;
+    if (bytes_for(1, chunk_m) > dev.lds_bytes)
+      return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], head_dim);
+    const int cap = bytes_for(1, chunk_m) <= budget ? budget : dev.lds_bytes;
     int rb_max = 1;
-    while (rb_max < s.h[l] && bytes_for(rb_max + 1) <= budget) ++rb_max;
-    const int nb_min = (s.h[l] + rb_max - 1) / rb_max;
+    while (rb_max < s.h[l] && bytes_for(rb_max + 1, chunk_m) <= cap) ++rb_max;
     const int64_t area = static_cast<int64_t>(s.h[l]) * s.w[l];
-    int nb_want = static_cast<int>((want_items * area + total_area / 2) / total_area);
+    int nb = static_cast<int>((want_items * area + total_area / 2) / total_area);
     const int forced = env_int("MSDA_BWD_BANDS", 0);
-    if (forced > 0) nb_want = forced;
-    int nb = std::min(s.h[l], std::max(nb_min, std::max(1, nb_want)));
+    if (forced > 0) nb = forced;
+    nb = std::min(s.h[l], std::max({1, nb, (s.h[l] + rb_max - 1) / rb_max}));
     const int rb = (s.h[l] + nb - 1) / nb;
     nb = (s.h[l] + rb - 1) / rb;
     p.lv[l] = msda::LevelDesc{s.h[l], s.w[l], static_cast<int>(s.start[l]), -1, rb, nwork};
     nwork += nb;
-    lds_max = std::max<int>(lds_max, static_cast<int>(bytes_for(rb)));
+    lds_max = std::max(lds_max, bytes_for(rb, chunk_m));
   }
   p.nwork = nwork;
-  // Locations / weights of `chunk_q` queries of one level are staged in LDS at a time.
-  p.chunk_q = std::max(1, std::min(len_query, env_int("MSDA_BWD_CHUNK", 1024)));
-  p.loc_lds = align16(lds_max);
-  lds_max = p.loc_lds + align16(static_cast<int64_t>(p.chunk_q) * n_points * 12);
-  if (lds_max > hard_budget)
-    return fail(MSDA_ERR_UNSUPPORTED, "backward LDS plan (%d bytes) exceeds the device's %d bytes", lds_max, hard_budget);
+  p.chunk_m = chunk_m;
+  p.scan_seg = scan_seg;
+  p.g_vec4 = (head_dim % 4 == 0) && aligned(grad_output, grad_output_dtype == MSDA_DTYPE_BF16 ? 8 : 16);
   const int64_t grid = N * nwork;
   if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
 

@@ -46,20 +46,8 @@ constexpr int kMaxLevels = 16;
 constexpr int kXcds = 8;  // MI355X: 8 accelerator complex dies, workgroups dispatched round-robin
 constexpr int kFwdThreads = 256;
 constexpr int kBwdThreads = 256;
-constexpr int kRing = 128;  // records per wave in the backward ring (two waves' worth)
 
 using bf16_t = uint16_t;
-typedef __attribute__((address_space(3))) volatile int lds_vint;
-typedef __attribute__((address_space(3))) int lds_int;
-
-// An integer the compiler cannot see through. Reading a tag back through an opaque copy of its
-// address keeps the compiler from forwarding the value this lane just stored (the read must see
-// what *any* lane stored), without the per-access waits a volatile pointer costs.
-__device__ __forceinline__ int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
 struct LevelDesc {
   int h, w;        // level height and width
   int start;       // first position of the level in the value slice
@@ -95,13 +83,46 @@ struct BwdParams {
   int gout_bf16;
   int heads, dim, queries, levels, points;
   int64_t len_value;
-  int lpq_shift;
-  int nwork;    // (level, band) items per slice
+  int lpq_shift;  // log2(lanes per sample) in the owner pass
+  int nwork;      // (level, band) items per slice
   int vec16;
-  int chunk_q;  // queries whose locations / weights are staged in LDS at a time
-  int loc_lds;  // byte offset of that staging area in LDS
+  int chunk_m;    // relevant queries whose inputs are staged in LDS at a time
+  int scan_seg;   // queries scanned per segment (capacity of the relevant-query list)
+  int g_vec4;     // grad_output rows may be read 4 channels at a time
   LevelDesc lv[kMaxLevels];
 };
+
+// LDS carve-up of one backward workgroup; shared by the host planner and the kernel so both
+// agree on the size. Every region starts on a 16-byte boundary.
+struct BwdLayout {
+  int sv, acc, cnt, off, misc, rel, cg, cl, ca, skey, srank, swt, rslot, rw, total;
+};
+
+__host__ __device__ inline int bwd_align16(int x) { return (x + 15) & ~15; }
+
+__host__ __device__ inline BwdLayout bwd_layout(int staged_rows, int band_rows, int w, int dim, int vbytes, int points,
+                                                int chunk_m, int scan_seg) {
+  BwdLayout L;
+  const int ncell = (band_rows + 1) * (w + 1);
+  const int ns = chunk_m * points;  // samples per chunk
+  int o = 0;
+  L.sv = o;    o += bwd_align16(staged_rows * w * dim * vbytes);
+  L.acc = o;   o += bwd_align16(band_rows * w * dim * 4);
+  L.cnt = o;   o += bwd_align16(ncell * 4);
+  L.off = o;   o += bwd_align16((ncell + 1) * 4);
+  L.misc = o;  o += 64;
+  L.rel = o;   o += bwd_align16(scan_seg * 2);
+  L.cg = o;    o += bwd_align16(chunk_m * dim * 4);
+  L.cl = o;    o += bwd_align16(ns * 8);
+  L.ca = o;    o += bwd_align16(ns * 4);
+  L.skey = o;  o += bwd_align16(ns * 4);
+  L.srank = o; o += bwd_align16(ns * 4);
+  L.swt = o;   o += bwd_align16(ns * 16);
+  L.rslot = o; o += bwd_align16(ns * 4);
+  L.rw = o;    o += bwd_align16(ns * 16);
+  L.total = o;
+  return L;
+}
 
 // ---------------------------------------------------------------------------------------------
 // scalar helpers
@@ -395,48 +416,50 @@ __global__ void __launch_bounds__(kFwdThreads) fwd_kernel(const FwdParams p) {
 
 // ---------------------------------------------------------------------------------------------
 // backward
+//
+// One workgroup per (slice, level, band of rows [r0, r1)). Phases:
+//  0. stage the band's value rows (+1 halo row); zero the f32 accumulator of the band's pixels.
+//  1. scan: the row coordinate of every sample of the slice on this level is loaded (all loads of
+//     a round in flight) and tested against the band; queries with a relevant sample are
+//     compacted into a list (ballot per wave, one LDS atomic per wave to reserve space).
+//  2. per chunk of `chunk_m` listed queries:
+//     a. stage grad_output rows, locations and weights of the chunk into LDS;
+//     b. one lane group per sample: owned samples (floor row in the band) get their grad_weight
+//        and grad_location from the staged value rows; samples with a corner pixel in the band
+//        are bucketed by bilinear cell (x0, y0): ds_add_rtn_u32 on the cell's count gives the
+//        sample's rank inside the cell;
+//     c. exclusive scan of the cell counts (cells are ordered row-major);
+//     d. samples are written into cell order;
+//     e. pixel-major gather: one lane per (band pixel, 4 channels) sums, in registers, a * w_k * g
+//        over the samples of the four cells that have this pixel as corner k, and adds the sum to
+//        its own accumulator slot. Every accumulator element has exactly one writer per chunk.
+//  3. the accumulator is written to grad_value in the value dtype.
+// Integer LDS atomics are cheap on gfx950 (~10 lanes/clk); float ones are not, and none are used.
 
-// acc[pix[k]] += aw[k] * g for the corners k with `pending[k]`, for every lane group of the wave.
-// Same-pixel collisions between lane groups are resolved with write-tag / read-back rounds (see
-// the header comment); all four corners of a sample share each round. Corners of one sample with
-// nonzero weight are distinct pixels; a repeated pixel (possible only for NaN weights, whose
-// clipped corners coincide) is deferred to a later round so no read-modify-write is lost.
-template <int VEC>
-__device__ __forceinline__ void accumulate_corners(float* acc, int dim, int c0, bool lane_on, const int (&pix)[4],
-                                                   bool (&pending)[4], const float (&aw)[4], const float (&g)[VEC],
-                                                   lds_int* tags, int gid) {
-  while (__any(pending[0] || pending[1] || pending[2] || pending[3])) {
-    bool att[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      att[k] = pending[k];
-#pragma unroll
-      for (int m = 0; m < k; ++m) att[k] = att[k] && !(att[m] && pix[m] == pix[k]);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (att[k]) tags[pix[k]] = gid;
-    // Reads are issued for every lane (from pixel 0 when not needed) so they share one wait.
-    bool win[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int t = tags[opaque(att[k] ? pix[k] : 0)];
-      win[k] = att[k] && t == gid;
-    }
-    float cur[4][VEC];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) load_vec<float, VEC>(acc + (win[k] ? pix[k] : 0) * dim + c0, cur[k]);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      if (win[k] && lane_on) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) cur[k][e] += aw[k] * g[e];
-        store_vec<float, VEC>(acc + pix[k] * dim + c0, cur[k]);
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) pending[k] = pending[k] && !win[k];
+// Exclusive prefix sum of cnt[0, n) into off[0, n] (off[n] = total); block-wide, ends in a barrier.
+// cnt is cleared for reuse. `tmp` holds one int per wave.
+__device__ __forceinline__ void block_scan_counts(int* cnt, int* off, int n, int* tmp) {
+  const int nt = blockDim.x, t = threadIdx.x, lane = t & 63;
+  const int per = (n + nt - 1) / nt;
+  const int b0 = min(n, t * per), b1 = min(n, b0 + per);
+  int sum = 0;
+  for (int i = b0; i < b1; ++i) sum += cnt[i];
+  int incl = sum;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
   }
+  if (lane == 63) tmp[t >> 6] = incl;
+  __syncthreads();
+  int run = incl - sum;
+  for (int w = 0; w < (t >> 6); ++w) run += tmp[w];
+  for (int i = b0; i < b1; ++i) {
+    off[i] = run;
+    run += cnt[i];
+    cnt[i] = 0;
+  }
+  if (t == nt - 1) off[n] = run;
+  __syncthreads();
 }
 
 template <typename VT, int VEC>
@@ -451,188 +474,291 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_kernel(const BwdParams p) {
   int l = 0;
   while (l + 1 < p.levels && wk >= p.lv[l + 1].band_first) ++l;
   const LevelDesc L = p.lv[l];
+  const int W = L.w;
   const int r0 = (wk - L.band_first) * L.band_rows;  // band rows [r0, r1); staged rows [r0, rs1)
   const int r1 = min(L.h, r0 + L.band_rows);
   const int rs1 = min(L.h, r1 + 1);
-  const int rowlen = L.w * p.dim;
+  const int rb = r1 - r0;
+  const int D = p.dim;
+  const int P = p.points;
+  const int LP = p.levels * P;
+  const int Q = p.queries;
+  const int ncell = (rb + 1) * (W + 1);
   const int64_t n = static_cast<int64_t>(b) * p.heads + h;
-  const int64_t band_off = (n * p.len_value + L.start + static_cast<int64_t>(r0) * L.w) * p.dim;
+  const int64_t band_off = (n * p.len_value + L.start + static_cast<int64_t>(r0) * W) * D;
+  const int nt = blockDim.x, t = threadIdx.x, lane = t & 63;
 
-  // LDS: staged rows | per-wave f32 accumulators | per-wave pixel tags | per-wave record rings |
-  //      staged locations (float2) and weights of `chunk_q` queries x `points` samples
-  const int nwaves = blockDim.x >> 6;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int band_px = (r1 - r0) * L.w;
-  const int nacc = band_px * p.dim;
-  const int nacc_pad = (nacc + 3) & ~3;
-  VT* sv = reinterpret_cast<VT*>(lds_raw);
-  const int nstage = (rs1 - r0) * rowlen;
-  const int stage_bytes = ((nstage * static_cast<int>(sizeof(VT))) + 15) & ~15;
-  float* acc_all = reinterpret_cast<float*>(lds_raw + stage_bytes);
-  int* tags_all = reinterpret_cast<int*>(acc_all + nwaves * nacc_pad);
-  lds_vint* ring_all = (lds_vint*)(tags_all + ((nwaves * band_px + 3) & ~3));
-  float* acc = acc_all + wave * nacc_pad;
-  lds_int* tags = (lds_int*)(tags_all + wave * band_px);
-  lds_vint* ring = ring_all + wave * kRing;
-  float2* cl = reinterpret_cast<float2*>(lds_raw + p.loc_lds);  // [chunk_q][points]
-  float* ca = reinterpret_cast<float*>(cl + p.chunk_q * p.points);
+  const BwdLayout lay = bwd_layout(rs1 - r0, rb, W, D, static_cast<int>(sizeof(VT)), P, p.chunk_m, p.scan_seg);
+  VT* sv = reinterpret_cast<VT*>(lds_raw + lay.sv);
+  float* acc = reinterpret_cast<float*>(lds_raw + lay.acc);
+  int* cnt = reinterpret_cast<int*>(lds_raw + lay.cnt);
+  int* off = reinterpret_cast<int*>(lds_raw + lay.off);
+  int* misc = reinterpret_cast<int*>(lds_raw + lay.misc);  // [0] list size, [4..] scan scratch
+  uint16_t* rel = reinterpret_cast<uint16_t*>(lds_raw + lay.rel);
+  float* cg = reinterpret_cast<float*>(lds_raw + lay.cg);
+  float2* cl = reinterpret_cast<float2*>(lds_raw + lay.cl);
+  float* ca = reinterpret_cast<float*>(lds_raw + lay.ca);
+  int* skey = reinterpret_cast<int*>(lds_raw + lay.skey);
+  int* srank = reinterpret_cast<int*>(lds_raw + lay.srank);
+  float4* swt = reinterpret_cast<float4*>(lds_raw + lay.swt);
+  int* rslot = reinterpret_cast<int*>(lds_raw + lay.rslot);
+  float4* rw = reinterpret_cast<float4*>(lds_raw + lay.rw);
+
   const bool want_dv = p.dvalue != nullptr;
   const bool want_dl = p.dloc != nullptr || p.dattn != nullptr;
+  const float fw = static_cast<float>(W), fh = static_cast<float>(L.h);
+  const int64_t qstride = static_cast<int64_t>(p.heads) * LP;                    // samples between queries
+  const int64_t srow0 = (static_cast<int64_t>(b) * Q * p.heads + h) * LP + l * P;  // sample (q=0, pt=0)
+  const float2* loc2 = reinterpret_cast<const float2*>(p.loc);
+  const bool gbf = p.gout_bf16 != 0;
 
-  stage_copy(sv, static_cast<const VT*>(p.value) + band_off, nstage, p.vec16);
-  if (want_dv) {
-    float4* a4 = reinterpret_cast<float4*>(acc_all);
-    const int n4 = (nwaves * nacc_pad) >> 2;
-    for (int i = threadIdx.x; i < n4; i += blockDim.x) a4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  // ---- phase 0
+  stage_copy(sv, static_cast<const VT*>(p.value) + band_off, (rs1 - r0) * W * D, p.vec16);
+  {
+    const int na = rb * W * D;
+    float4* a4 = reinterpret_cast<float4*>(acc);
+    for (int i = t; i < (na >> 2); i += nt) a4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int i = (na & ~3) + t; i < na; i += nt) acc[i] = 0.0f;
+    for (int i = t; i < ncell; i += nt) cnt[i] = 0;
   }
-  __syncthreads();
 
   const int lpq = 1 << p.lpq_shift;
-  const int j = lane & (lpq - 1);
-  const int gid = lane >> p.lpq_shift;  // record slot inside the wave (also the tag value)
-  const int per_pass = 64 >> p.lpq_shift;
-  const bool lane_on = j * VEC < p.dim;
+  const int j = t & (lpq - 1);
+  const bool lane_on = j * VEC < D;
   const int c0 = lane_on ? j * VEC : 0;
-  const int LP = p.levels * p.points;
-  const int P = p.points;
-  const int band_base = r0 * L.w;  // flat index of the band's first pixel inside the level
-  const float fw = static_cast<float>(L.w), fh = static_cast<float>(L.h);
-  const bool gbf = p.gout_bf16 != 0;
-  const int64_t qstride = static_cast<int64_t>(p.heads) * LP;  // samples between consecutive queries
-  const int64_t srow0 = (static_cast<int64_t>(b) * p.queries * p.heads + h) * LP + l * P;  // sample (q=0, pt=0)
-  const float2* lsrc = reinterpret_cast<const float2*>(p.loc);
+  const int ngroups = nt >> p.lpq_shift;
+  const int M = p.chunk_m;
+  constexpr int kSQ = 8;  // queries per thread per scan round
+  constexpr int kSP = 4;  // points per load batch in the scan
 
-  // Process `cnt` (<= per_pass) queued queries starting at ring position `head`, one per lane
-  // group; `c_lo` is the first query of the staged chunk.
-  auto process = [&](int head, int cnt, int c_lo) {
-    const bool has = gid < cnt;
-    const int q = has ? ring[(head + gid) & (kRing - 1)] : c_lo;
-    const int64_t bqh = (static_cast<int64_t>(b) * p.queries + q) * p.heads + h;
-    const int64_t s0 = srow0 + static_cast<int64_t>(q) * qstride;
-    float g[VEC];
-    if (has) load_any<VEC>(p.gout, bqh * p.dim + c0, gbf, g);
-    if (!has || !lane_on) {
+  for (int qs = 0; qs < Q; qs += p.scan_seg) {
+    const int qe = min(Q, qs + p.scan_seg);
+    if (t == 0) misc[0] = 0;
+    __syncthreads();
+    // ---- phase 1: scan [qs, qe)
+    for (int qb = qs; qb < qe; qb += kSQ * nt) {
+      bool relq[kSQ];
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) g[k] = 0.0f;
+      for (int k = 0; k < kSQ; ++k) relq[k] = false;
+      for (int pg = 0; pg < P; pg += kSP) {
+        float ys[kSQ][kSP];
+#pragma unroll
+        for (int k = 0; k < kSQ; ++k) {
+          const int q = qb + t + k * nt;
+#pragma unroll
+          for (int e = 0; e < kSP; ++e) {
+            const int pt = pg + e;
+            ys[k][e] = (q < qe && pt < P) ? p.loc[2 * (srow0 + static_cast<int64_t>(q) * qstride + pt) + 1] : -1.0e30f;
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < kSQ; ++k) {
+#pragma unroll
+          for (int e = 0; e < kSP; ++e) {
+            // rows [y0, y0+1] clipped into the level (NaN -> row 0) against the band
+            const float y0f = floorf(pixel_coord(ys[k][e], fh));
+            const float lo = fminf(fmaxf(y0f, 0.0f), fh - 1.0f);
+            const float hi = fminf(fmaxf(y0f + 1.0f, 0.0f), fh - 1.0f);
+            const bool valid = (qb + t + k * nt < qe) && (pg + e < P);
+            relq[k] = relq[k] || (valid && hi >= static_cast<float>(r0) && lo < static_cast<float>(r1));
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kSQ; ++k) {
+        const uint64_t mask = __ballot(relq[k]);
+        int base = 0;
+        if (lane == 0 && mask) base = atomicAdd(&misc[0], __popcll(mask));
+        base = __shfl(base, 0, 64);
+        if (relq[k]) rel[base + __popcll(mask & ((uint64_t{1} << lane) - 1))] = static_cast<uint16_t>(qb + t + k * nt - qs);
+      }
     }
-    for (int pt = 0; pt < P; ++pt) {
-      const float2 xy = cl[(q - c_lo) * P + pt];
-      const float a = ca[(q - c_lo) * P + pt];
-      const Bilinear c = bilinear(xy.x, xy.y, L.h, L.w);
-      // Owner band: the one holding the floor row clamped into the level (NaN -> row 0); both
-      // clipped corner rows of an owned sample are among the staged rows.
-      const int yo = static_cast<int>(fminf(fmaxf(c.y0f, 0.0f), fh - 1.0f));
-      const bool own = has && want_dl && yo >= r0 && yo < r1;
-      const bool in0 = has && c.y0c >= r0 && c.y0c < r1;
-      const bool in1 = has && c.y1c >= r0 && c.y1c < r1;
-      if (own) {
-        // D_c = <g, v_c> per corner; every gradient term is a combination of these.
-        float v[VEC];
-        float d00 = 0.0f, d10 = 0.0f, d01 = 0.0f, d11 = 0.0f;
-        const VT* base = sv + c0;
-        load_vec<VT, VEC>(base + (c.i00 - band_base) * p.dim, v);
+    __syncthreads();
+    const int nrel = misc[0];
+
+    // ---- phase 2: chunks of listed queries
+    for (int m0 = 0; m0 < nrel; m0 += M) {
+      const int m = min(M, nrel - m0);
+      const int ns = m * P;
+      // a. stage grad_output rows (4 channels per item), locations and weights
+      {
+        const int gq = D >> 2;  // 4-channel items per row
+        if (p.g_vec4) {
+          for (int e = t; e < m * gq; e += nt) {
+            const int i = e / gq, part = e - i * gq;
+            const int q = qs + rel[m0 + i];
+            const int64_t go = ((static_cast<int64_t>(b) * Q + q) * p.heads + h) * D + part * 4;
+            float v[4];
+            load_any<4>(p.gout, go, gbf, v);
+            *reinterpret_cast<float4*>(cg + i * D + part * 4) = make_float4(v[0], v[1], v[2], v[3]);
+          }
+        } else {
+          for (int e = t; e < m * D; e += nt) {
+            const int i = e / D, ch = e - i * D;
+            const int q = qs + rel[m0 + i];
+            float v[1];
+            load_any<1>(p.gout, ((static_cast<int64_t>(b) * Q + q) * p.heads + h) * D + ch, gbf, v);
+            cg[e] = v[0];
+          }
+        }
+        for (int e = t; e < ns; e += nt) {
+          const int i = e / P, pt = e - i * P;
+          const int64_t si = srow0 + static_cast<int64_t>(qs + rel[m0 + i]) * qstride + pt;
+          cl[e] = loc2[si];
+          ca[e] = p.attn[si];
+        }
+      }
+      __syncthreads();
+      // b. owner gradients and cell buckets, one lane group per sample
+      for (int e = t >> p.lpq_shift; e < ns; e += ngroups) {
+        const int i = e / P, pt = e - i * P;
+        const float2 xy = cl[e];
+        const float a = ca[e];
+        const Bilinear c = bilinear(xy.x, xy.y, L.h, W);
+        const int yo = static_cast<int>(fminf(fmaxf(c.y0f, 0.0f), fh - 1.0f));
+        if (want_dl && yo >= r0 && yo < r1) {
+          // D_c = <g, v_c>; dA = sum_c w_c D_c; d out/d ix = gy (m10 D10 - m00 D00) + fy (m11 D11 - m01 D01), ...
+          float g[VEC], v[VEC];
+          load_vec<float, VEC>(cg + i * D + c0, g);
+          if (!lane_on) {
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) d00 += g[k] * v[k];
-        load_vec<VT, VEC>(base + (c.i10 - band_base) * p.dim, v);
+            for (int k = 0; k < VEC; ++k) g[k] = 0.0f;
+          }
+          const VT* base = sv + c0;
+          const int bb = r0 * W;
+          float d00 = 0.0f, d10 = 0.0f, d01 = 0.0f, d11 = 0.0f;
+          load_vec<VT, VEC>(base + (c.i00 - bb) * D, v);
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) d10 += g[k] * v[k];
-        load_vec<VT, VEC>(base + (c.i01 - band_base) * p.dim, v);
+          for (int k = 0; k < VEC; ++k) d00 += g[k] * v[k];
+          load_vec<VT, VEC>(base + (c.i10 - bb) * D, v);
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) d01 += g[k] * v[k];
-        load_vec<VT, VEC>(base + (c.i11 - band_base) * p.dim, v);
+          for (int k = 0; k < VEC; ++k) d10 += g[k] * v[k];
+          load_vec<VT, VEC>(base + (c.i01 - bb) * D, v);
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) d11 += g[k] * v[k];
-        d00 = group_sum(d00, lpq);
-        d10 = group_sum(d10, lpq);
-        d01 = group_sum(d01, lpq);
-        d11 = group_sum(d11, lpq);
-        if (j == 0) {
-          // dA = sum_c w_c D_c; d out/d ix = gy (m10 D10 - m00 D00) + fy (m11 D11 - m01 D01), etc.
-          const float da = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
-          const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
-          const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
-          const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
-          const int64_t si = s0 + pt;
-          if (p.dattn) p.dattn[si] = da;
-          if (p.dloc) *reinterpret_cast<float2*>(p.dloc + 2 * si) = make_float2(a * fw * dx, a * fh * dy);
+          for (int k = 0; k < VEC; ++k) d01 += g[k] * v[k];
+          load_vec<VT, VEC>(base + (c.i11 - bb) * D, v);
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) d11 += g[k] * v[k];
+          d00 = group_sum(d00, lpq);
+          d10 = group_sum(d10, lpq);
+          d01 = group_sum(d01, lpq);
+          d11 = group_sum(d11, lpq);
+          if (j == 0) {
+            const float da = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
+            const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
+            const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
+            const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
+            const int64_t si = srow0 + static_cast<int64_t>(qs + rel[m0 + i]) * qstride + pt;
+            if (p.dattn) p.dattn[si] = da;
+            if (p.dloc) *reinterpret_cast<float2*>(p.dloc + 2 * si) = make_float2(a * fw * dx, a * fh * dy);
+          }
+        }
+        if (j == 0 && want_dv) {
+          // The sample's cell: its floor corner (x0, y0), or for non-finite weights its clipped
+          // first corner (the reference adds those weights at the clipped corner indices).
+          int cx, cy;
+          const bool finite = isfinite(c.w00) && isfinite(c.w10) && isfinite(c.w01) && isfinite(c.w11);
+          if (finite) {
+            cx = static_cast<int>(fminf(fmaxf(floorf(pixel_coord(xy.x, fw)), -2.0f), fw));
+            cy = static_cast<int>(fminf(fmaxf(c.y0f, -2.0f), fh));
+          } else {
+            cx = c.i00 % W;
+            cy = c.i00 / W;
+          }
+          const int kx = cx + 1, ky = cy - r0 + 1;  // cell coordinates inside the band's cell grid
+          const bool in = kx >= 0 && kx <= W && ky >= 0 && ky <= rb &&
+                          (c.w00 != 0.0f || c.w10 != 0.0f || c.w01 != 0.0f || c.w11 != 0.0f);
+          int key = -1;
+          if (in) {
+            key = ky * (W + 1) + kx;
+            srank[e] = atomicAdd(&cnt[key], 1);
+            swt[e] = make_float4(a * c.w00, a * c.w10, a * c.w01, a * c.w11);
+          }
+          skey[e] = key;
         }
       }
       if (want_dv) {
-        const int pix[4] = {c.i00 - band_base, c.i10 - band_base, c.i01 - band_base, c.i11 - band_base};
-        bool pend[4] = {in0 && c.w00 != 0.0f, in0 && c.w10 != 0.0f, in1 && c.w01 != 0.0f, in1 && c.w11 != 0.0f};
-        const float aw[4] = {a * c.w00, a * c.w10, a * c.w01, a * c.w11};
-        accumulate_corners<VEC>(acc, p.dim, c0, lane_on, pix, pend, aw, g, tags, gid);
-      }
-    }
-  };
-
-  int head = 0, tail = 0;  // wave-uniform ring positions
-  constexpr int UL = 4;
-  const int nt = blockDim.x;
-  for (int c_lo = 0; c_lo < p.queries; c_lo += p.chunk_q) {
-    const int nq = min(p.chunk_q, p.queries - c_lo);
-    const int E = nq * P;
-    // Stage this chunk's locations / weights (all loads of a batch in flight before the stores).
-    for (int base = threadIdx.x; base < E; base += UL * nt) {
-      float2 rl[UL];
-      float ra[UL];
+        __syncthreads();
+        // c. cell offsets (clears the counts for the next chunk)
+        block_scan_counts(cnt, off, ncell, misc + 4);
+        // d. samples into cell order (query slot and a * corner weights)
+        for (int e = t; e < ns; e += nt) {
+          const int key = skey[e];
+          if (key >= 0) {
+            const int pos = off[key] + srank[e];
+            rslot[pos] = e / P;
+            rw[pos] = swt[e];
+          }
+        }
+        __syncthreads();
+        // e. cell-major accumulation in four colour phases: one lane per (cell, 4 channels) sums
+        //    a * w_k * g over the cell's samples for its four corners in registers, then adds them
+        //    to the corner pixels. Cells of one colour (cell x and y parities) are at least two
+        //    cells apart, so their 2x2 pixel footprints are disjoint and no two lanes write the
+        //    same accumulator element.
+        const int gpp = (D + 3) >> 2;  // channel groups per cell
+        for (int color = 0; color < 4; ++color) {
+          const int ox = color & 1, oy = color >> 1;
+          const int nu = (W + 1 - ox + 1) >> 1;   // cells per row of this colour
+          const int nv = (rb + 1 - oy + 1) >> 1;  // cell rows of this colour
+          for (int task = t; task < nu * nv * gpp; task += nt) {
+            const int cidx = task / gpp, grp = task - cidx * gpp;
+            const int v = cidx / nu, u = cidx - v * nu;
+            const int kx = 2 * u + ox, ky = 2 * v + oy;
+            const int key = ky * (W + 1) + kx;
+            const int ch0 = grp * 4;
+            const int nch = min(4, D - ch0);
+            float s[4][4];
 #pragma unroll
-      for (int u = 0; u < UL; ++u) {
-        const int i = base + u * nt;
-        if (i < E) {
-          const int qq = i / P, pt = i - qq * P;
-          const int64_t si = srow0 + static_cast<int64_t>(c_lo + qq) * qstride + pt;
-          rl[u] = lsrc[si];
-          ra[u] = p.attn[si];
-        }
-      }
+            for (int k = 0; k < 4; ++k)
 #pragma unroll
-      for (int u = 0; u < UL; ++u) {
-        const int i = base + u * nt;
-        if (i < E) {
-          cl[i] = rl[u];
-          ca[i] = ra[u];
+              for (int e = 0; e < 4; ++e) s[k][e] = 0.0f;
+            const int rbeg = off[key], rend = off[key + 1];
+            for (int r = rbeg; r < rend; ++r) {
+              const float4 w4 = rw[r];
+              const float* gr = cg + rslot[r] * D + ch0;
+              float g4[4];
+              if (nch == 4) {
+                const float4 gv = *reinterpret_cast<const float4*>(gr);
+                g4[0] = gv.x; g4[1] = gv.y; g4[2] = gv.z; g4[3] = gv.w;
+              } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) g4[e] = e < nch ? gr[e] : 0.0f;
+              }
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                s[0][e] += w4.x * g4[e];
+                s[1][e] += w4.y * g4[e];
+                s[2][e] += w4.z * g4[e];
+                s[3][e] += w4.w * g4[e];
+              }
+            }
+            if (rend > rbeg) {
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                // corner k of cell (kx, ky) is pixel (kx - 1 + (k & 1), ky - 1 + (k >> 1)) of the band
+                const int px = kx - 1 + (k & 1), py = ky - 1 + (k >> 1);
+                if (px >= 0 && px < W && py >= 0 && py < rb) {
+                  float* ap = acc + (py * W + px) * D + ch0;
+                  for (int e = 0; e < nch; ++e) ap[e] += s[k][e];
+                }
+              }
+            }
+          }
+          __syncthreads();
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
-    // Scan, one lane per query: the query is relevant if one of its samples on this level has its
-    // floor row (clamped into the level) in the band, or a clipped corner row in the band. Rows
-    // [y0, y0+1] clipped to [0, H-1]: y0 <= -1 gives row 0 only, y0 >= H-1 gives row H-1 only.
-    for (int qb = wave * 64; qb < nq; qb += nwaves * 64) {
-      const int qq = qb + lane;
-      bool rel = false;
-      if (qq < nq) {
-        for (int pt = 0; pt < P; ++pt) {
-          const float y0f = floorf(pixel_coord(cl[qq * P + pt].y, fh));
-          const float lo = fminf(fmaxf(y0f, 0.0f), fh - 1.0f);        // clipped first row (NaN -> 0)
-          const float hi = fminf(fmaxf(y0f + 1.0f, 0.0f), fh - 1.0f);  // clipped second row
-          rel = rel || (hi >= static_cast<float>(r0) && lo < static_cast<float>(r1));
-        }
-      }
-      const uint64_t mask = __ballot(rel);
-      if (rel) ring[(tail + __popcll(mask & ((uint64_t{1} << lane) - 1))) & (kRing - 1)] = c_lo + qq;
-      tail += __popcll(mask);
-      while (tail - head >= per_pass) {
-        process(head, per_pass, c_lo);
-        head += per_pass;
-      }
-    }
-    while (head < tail) {  // drain before the staged chunk is replaced
-      process(head, min(per_pass, tail - head), c_lo);
-      head += min(per_pass, tail - head);
-    }
-    __syncthreads();
   }
 
+  // ---- phase 3
+  __syncthreads();
   if (want_dv) {
     VT* dst = static_cast<VT*>(p.dvalue) + band_off;
-    for (int i = threadIdx.x; i < nacc; i += blockDim.x) {
-      float s = 0.0f;
-      for (int w = 0; w < nwaves; ++w) s += acc_all[w * nacc_pad + i];
-      if constexpr (std::is_same<VT, float>::value) dst[i] = s;
-      else dst[i] = f32_to_bf16(s);
+    for (int i = t; i < rb * W * D; i += nt) {
+      if constexpr (std::is_same<VT, float>::value) dst[i] = acc[i];
+      else dst[i] = f32_to_bf16(acc[i]);
     }
   }
 }
