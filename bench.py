@@ -267,9 +267,10 @@ def main():
     dom_us, dom_bytes = kernels[dom]
     achieved = dom_bytes / dom_us / 1e3
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"traffic_{w.name}_{dom}.json")
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{w.name}.json")
     if os.path.exists(tfile):
-        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+        # calibrated FETCH_SIZE + WRITE_SIZE of the kernel, from the rocprofv3 counter passes that file records
+        traffic = json.load(open(tfile)).get("kernels", {}).get(dom, {}).get("hbm_bytes_per_launch")
 
     per_config = {}
     if not args.no_per_config:
