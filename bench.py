@@ -77,10 +77,14 @@ class Calls:
         shape_args = (w.batch, w.heads, w.head_dim, w.queries, w.levels, w.points, self._shapes, self._starts,
                       w.len_value)
         p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        self.lib = _native.lib()
+        ws_bytes = self.lib.msda_bwd_workspace_size(*shape_args)
+        if ws_bytes < 0:
+            _native.check(int(ws_bytes))
+        self.ws = torch.empty((max(1, ws_bytes // 16), 4), dtype=torch.int32, device=dev)  # per-sample records
         self.fargs = (p(self.v), vdt, p(self.loc), p(self.attn), p(self.out), _native.DTYPE_F32) + shape_args
         self.bargs = (p(self.v), vdt, p(self.loc), p(self.attn), p(self.grad), _native.DTYPE_F32, p(self.dv),
-                      p(self.dloc), p(self.dattn)) + shape_args
-        self.lib = _native.lib()
+                      p(self.dloc), p(self.dattn)) + shape_args + (p(self.ws), ctypes.c_int64(ws_bytes))
         self.check = _native.check
 
     def fwd(self, stream):

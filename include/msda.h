@@ -30,8 +30,9 @@
  *
  * Calls are enqueue-only on `stream` (a hipStream_t, passed as void*; NULL = default stream):
  * no allocation, no host synchronisation, no global mutable state beyond one-time per-device
- * initialisation. All buffers are owned by the caller. Inputs are read-only; every output element
- * is written by the call (grad_value needs no zero-initialisation).
+ * initialisation. All buffers, including the backward's scratch workspace, are owned by the
+ * caller. Inputs are read-only; every output element is written by the call (grad_value needs no
+ * zero-initialisation).
  *
  * Return values: MSDA_OK (0) or a negative MSDA_ERR_* code; msda_last_error() then returns a
  * message for the calling thread. Argument validation happens before any HIP call.
@@ -85,6 +86,19 @@ int msda_fwd(const void* value, int value_dtype,
              int64_t len_value, void* stream);
 
 /*
+ * Device workspace msda_bwd needs for this shape, in bytes (>= 0), or a negative MSDA_ERR_* code.
+ * It holds one 16-byte record per sample (batch * n_heads * n_levels * len_query * n_points),
+ * written by the per-sample pass and read by the grad_value pass, and is only needed when
+ * grad_value is requested. It plays the role of the scratch an XLA FFI handler obtains from
+ * ffi::ScratchAllocator (the reference has no counterpart: JAX autodiff materialises its own
+ * intermediates, ops.py:120-134).
+ */
+int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_query,
+                                int n_levels, int n_points,
+                                const int32_t* spatial_shapes, const int32_t* level_start_index,
+                                int64_t len_value);
+
+/*
  * Backward (vector-Jacobian product of msda_fwd with cotangent grad_output):
  *   grad_value              [batch*n_heads, len_value, head_dim]  value_dtype (accumulated in f32,
  *                           rounded once; deform_pallas.py:175 casts the same way)
@@ -92,7 +106,9 @@ int msda_fwd(const void* value, int value_dtype,
  *   grad_attention_weights  [batch, len_query, n_heads, n_levels*n_points]     f32
  * Replaces the JAX autodiff VJP of ops.py:64-134/289 and deform_pallas.py:157-175 (_sample_bwd).
  * Any of the three gradient pointers may be NULL to skip that gradient. grad_output has
- * grad_output_dtype (the forward's output dtype).
+ * grad_output_dtype (the forward's output dtype). workspace: 16-byte aligned device memory of at
+ * least msda_bwd_workspace_size() bytes (workspace_bytes says how many), or NULL when grad_value
+ * is NULL; its contents on entry do not matter. Calls that share a workspace must not overlap.
  */
 int msda_bwd(const void* value, int value_dtype,
              const float* sampling_locations, const float* attention_weights,
@@ -101,7 +117,7 @@ int msda_bwd(const void* value, int value_dtype,
              int batch, int n_heads, int head_dim, int len_query,
              int n_levels, int n_points,
              const int32_t* spatial_shapes, const int32_t* level_start_index,
-             int64_t len_value, void* stream);
+             int64_t len_value, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

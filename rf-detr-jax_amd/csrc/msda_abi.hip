@@ -170,50 +170,118 @@ int check_launch(const char* what) {
 }
 
 // ------------------------------------------------------------------------------------------
-// forward dispatch
+// dispatch
 
 template <typename VT, int VEC>
-int launch_fwd(const msda::FwdParams& p, int grid, int lds, hipStream_t stream) {
+int launch_fwd(const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
   static std::atomic<int> granted[kMaxDevices];  // per instantiation
   auto k = msda::fwd_kernel<VT, VEC>;
   int rc = allow_lds(k, lds, granted);
   if (rc != MSDA_OK) return rc;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(msda::kFwdThreads), lds, stream, p);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
   return check_launch("msda forward");
 }
 
-template <typename VT>
-int dispatch_fwd(int vec, const msda::FwdParams& p, int grid, int lds, hipStream_t stream) {
-  switch (vec) {
-    case 1: return launch_fwd<VT, 1>(p, grid, lds, stream);
-    case 2: return launch_fwd<VT, 2>(p, grid, lds, stream);
-    case 4: return launch_fwd<VT, 4>(p, grid, lds, stream);
-    case 8: return launch_fwd<VT, 8>(p, grid, lds, stream);
-    case 16: return launch_fwd<VT, 16>(p, grid, lds, stream);
-  }
-  return fail(MSDA_ERR_UNSUPPORTED, "no forward kernel for %d channels per lane", vec);
-}
-
 template <typename VT, int VEC>
-int launch_bwd(const msda::BwdParams& p, int grid, int lds, hipStream_t stream) {
-  static std::atomic<int> granted[kMaxDevices];  // per instantiation
-  auto k = msda::bwd_kernel<VT, VEC>;
+int launch_bwd_sample(const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
+  static std::atomic<int> granted[kMaxDevices];
+  auto k = msda::bwd_sample_kernel<VT, VEC>;
   int rc = allow_lds(k, lds, granted);
   if (rc != MSDA_OK) return rc;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(msda::kBwdThreads), lds, stream, p);
-  return check_launch("msda backward");
+  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
+  return check_launch("msda backward (per-sample pass)");
 }
 
 template <typename VT>
-int dispatch_bwd(int vec, const msda::BwdParams& p, int grid, int lds, hipStream_t stream) {
+int launch_bwd_value(const msda::ValueParams& p, int grid, int threads, int lds, hipStream_t stream) {
+  static std::atomic<int> granted[kMaxDevices];
+  auto k = msda::bwd_value_kernel<VT>;
+  int rc = allow_lds(k, lds, granted);
+  if (rc != MSDA_OK) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
+  return check_launch("msda backward (grad_value pass)");
+}
+
+template <typename VT>
+int dispatch_sample(bool backward, int vec, const msda::SampleParams& p, int grid, int threads, int lds,
+                    hipStream_t stream) {
   switch (vec) {
-    case 1: return launch_bwd<VT, 1>(p, grid, lds, stream);
-    case 2: return launch_bwd<VT, 2>(p, grid, lds, stream);
-    case 4: return launch_bwd<VT, 4>(p, grid, lds, stream);
-    case 8: return launch_bwd<VT, 8>(p, grid, lds, stream);
-    case 16: return launch_bwd<VT, 16>(p, grid, lds, stream);
+    case 1: return backward ? launch_bwd_sample<VT, 1>(p, grid, threads, lds, stream) : launch_fwd<VT, 1>(p, grid, threads, lds, stream);
+    case 2: return backward ? launch_bwd_sample<VT, 2>(p, grid, threads, lds, stream) : launch_fwd<VT, 2>(p, grid, threads, lds, stream);
+    case 4: return backward ? launch_bwd_sample<VT, 4>(p, grid, threads, lds, stream) : launch_fwd<VT, 4>(p, grid, threads, lds, stream);
+    case 8: return backward ? launch_bwd_sample<VT, 8>(p, grid, threads, lds, stream) : launch_fwd<VT, 8>(p, grid, threads, lds, stream);
+    case 16: return backward ? launch_bwd_sample<VT, 16>(p, grid, threads, lds, stream) : launch_fwd<VT, 16>(p, grid, threads, lds, stream);
   }
-  return fail(MSDA_ERR_UNSUPPORTED, "no backward kernel for %d channels per lane", vec);
+  return fail(MSDA_ERR_UNSUPPORTED, "no kernel for %d channels per lane", vec);
+}
+
+// ------------------------------------------------------------------------------------------
+// planning of the per-sample kernels (forward and the backward's per-sample pass)
+
+struct SamplePlan {
+  int grid, threads, lds;
+};
+
+// Each level whose slice still fits one head's LDS budget is staged (packed in level order); the
+// rest are gathered through L2. Head groups: a workgroup serves `hg` heads of one batch entry, so
+// the lanes of one query touch contiguous runs of its [H, ...] rows; hg is the largest power of
+// two <= the cap that divides n_heads and keeps the group's slices within half the LDS, so that
+// two workgroups still share a CU (measured: two heads of a 24x24x16 f32 level per workgroup beat
+// one and four). Then one resident wave of workgroups: fewer, longer workgroups amortise the
+// value staging.
+int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* prefix, int shift, msda::SampleParams* p,
+                SamplePlan* out) {
+  auto knob = [&](const char* name, int dflt) {
+    std::string key = std::string(prefix) + name;
+    return env_int(key.c_str(), dflt);
+  };
+  const int budget = std::min(dev.lds_bytes, knob("_LDS_BUDGET", dev.lds_bytes));
+  int head_lds = 0;  // elements
+  bool all_staged = true;
+  for (int l = 0; l < s.levels; ++l) {
+    const int64_t bytes = static_cast<int64_t>(s.h[l]) * s.w[l] * s.dim * vbytes;
+    p->lv[l] = msda::LevelDesc{s.h[l], s.w[l], static_cast<int>(s.start[l]), -1, 0, 0};
+    if (static_cast<int64_t>(head_lds) * vbytes + bytes <= budget) {
+      p->lv[l].lds = head_lds;
+      head_lds += static_cast<int>(bytes / vbytes);
+    } else {
+      all_staged = false;
+    }
+  }
+  const int64_t head_bytes = align16(static_cast<int64_t>(head_lds) * vbytes);
+  int hg = 1;
+  const int hg_cap = std::max(1, knob("_HEADS", 2));
+  const int group_budget = std::min(budget, knob("_GROUP_LDS", dev.lds_bytes / 2));
+  while (hg * 2 <= hg_cap && s.heads % (hg * 2) == 0 && (hg * 2) * head_bytes <= group_budget) hg *= 2;
+  // With every level staged a head's region is its whole value slice; regions stay 16-byte aligned.
+  const int head_stride = all_staged ? static_cast<int>(s.len_value * s.dim) : static_cast<int>(head_bytes / vbytes);
+  p->head_lds = head_stride;
+  p->all_staged = all_staged ? 1 : 0;
+  p->hg = hg;
+  p->lpq_shift = shift;
+  const int lds = align16(static_cast<int64_t>(hg) * head_stride * vbytes);
+  if (all_staged && (static_cast<int64_t>(s.len_value) * s.dim * vbytes) % 16 != 0) p->vec16 = 0;
+
+  const int per_cu = lds > 0 ? std::max(1, dev.lds_bytes / lds) : 8;
+  int threads = knob("_THREADS", per_cu >= 4 ? 256 : 512);
+  threads = std::max(64, std::min(msda::kSampleMaxThreads, (threads / 64) * 64));
+  const int tpq = hg << shift;  // threads per query
+  if (tpq > threads) threads = std::min(msda::kSampleMaxThreads, ((tpq + 63) / 64) * 64);
+  if (tpq > threads) return fail(MSDA_ERR_UNSUPPORTED, "head group of %d heads x %d lanes exceeds a workgroup", hg, 1 << shift);
+  const int qpp = threads / tpq;
+  const int64_t units = static_cast<int64_t>(s.batch) * (s.heads / hg);
+  const int target = knob("_TARGET_WGS", dev.cus * std::min(per_cu, 8));
+  const int max_blocks = std::max(1, (s.queries + qpp - 1) / qpp);
+  const int nqb = static_cast<int>(std::min<int64_t>(max_blocks, std::max<int64_t>(1, (target + units - 1) / units)));
+  const int per = (s.queries + nqb - 1) / nqb;
+  p->qblock = std::max(qpp, ((per + qpp - 1) / qpp) * qpp);
+  p->nqb = std::max(1, (s.queries + p->qblock - 1) / p->qblock);
+  const int64_t grid = units * p->nqb;
+  if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "grid too large");
+  out->grid = static_cast<int>(grid);
+  out->threads = threads;
+  out->lds = lds;
+  return MSDA_OK;
 }
 
 // 16-byte staging / flushing is allowed when every level's rows start and end on 16 bytes.
@@ -227,11 +295,16 @@ bool rows_16b(const Shape& s, int vbytes, const void* a, const void* b) {
   return true;
 }
 
+
+int64_t workspace_bytes_for(const Shape& s) {
+  return static_cast<int64_t>(s.batch) * s.heads * s.levels * s.queries * s.points * static_cast<int64_t>(sizeof(msda::SampleRec));
+}
+
 }  // namespace
 
 extern "C" {
 
-const char* msda_version(void) { return "msda-gfx950 0.1.0"; }
+const char* msda_version(void) { return "msda-gfx950 0.2.0"; }
 
 const char* msda_last_error(void) { return g_last_error.c_str(); }
 
@@ -260,7 +333,7 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
   DevInfo dev;
   if ((rc = device_info(&dev)) != MSDA_OK) return rc;
 
-  msda::FwdParams p{};
+  msda::SampleParams p{};
   p.value = value;
   p.loc = sampling_locations;
   p.attn = attention_weights;
@@ -272,48 +345,28 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
   p.levels = n_levels;
   p.points = n_points;
   p.len_value = len_value;
-  p.lpq_shift = shift;
   p.vec16 = rows_16b(s, vbytes, value, nullptr);
-
-  // Stage every level that fits the per-workgroup LDS budget; the rest is read through L2.
-  const int budget = std::min(dev.lds_bytes, env_int("MSDA_FWD_LDS_BUDGET", 80 * 1024));
-  int lds = 0;
-  for (int l = 0; l < n_levels; ++l) {
-    const int64_t bytes = static_cast<int64_t>(s.h[l]) * s.w[l] * head_dim * vbytes;
-    p.lv[l] = msda::LevelDesc{s.h[l], s.w[l], static_cast<int>(s.start[l]), -1, 0, 0};
-    if (lds + align16(bytes) <= budget) {
-      p.lv[l].lds = lds / vbytes;
-      lds += align16(bytes);
-    }
-  }
-  const int slots = msda::kFwdThreads >> shift;
-  const int64_t N = static_cast<int64_t>(batch) * n_heads;
-  const int target = env_int("MSDA_FWD_TARGET_WGS", 4 * dev.cus);
-  const int max_chunks = (len_query + slots - 1) / slots;
-  int nqc = static_cast<int>(std::min<int64_t>(max_chunks, std::max<int64_t>(1, (target + N - 1) / N)));
-  int per = (len_query + nqc - 1) / nqc;
-  p.qchunk = ((per + slots - 1) / slots) * slots;
-  p.nqc = (len_query + p.qchunk - 1) / p.qchunk;
-  // Stage the chunk's locations (8 B) and weights (4 B) per sample when they fit the budget too.
-  const int64_t loc_bytes = static_cast<int64_t>(p.qchunk) * n_levels * n_points * 12;
-  p.loc_lds = -1;
-  if (env_int("MSDA_FWD_STAGE_LOC", 1) != 0 && lds + loc_bytes <= budget) {
-    p.loc_lds = lds;
-    lds += align16(loc_bytes);
-  }
-  const int64_t grid = N * p.nqc;
-  if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "forward grid too large");
-
+  SamplePlan plan;
+  if ((rc = plan_sample(s, vbytes, dev, "MSDA_FWD", shift, &p, &plan)) != MSDA_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (value_dtype == MSDA_DTYPE_BF16) return dispatch_fwd<msda::bf16_t>(vec, p, static_cast<int>(grid), lds, st);
-  return dispatch_fwd<float>(vec, p, static_cast<int>(grid), lds, st);
+  if (value_dtype == MSDA_DTYPE_BF16) return dispatch_sample<msda::bf16_t>(false, vec, p, plan.grid, plan.threads, plan.lds, st);
+  return dispatch_sample<float>(false, vec, p, plan.grid, plan.threads, plan.lds, st);
+}
+
+int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_query, int n_levels, int n_points,
+                                const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value) {
+  g_last_error.clear();
+  Shape s;
+  int rc = validate(&s, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value);
+  if (rc != MSDA_OK) return rc;
+  return workspace_bytes_for(s);
 }
 
 int msda_bwd(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
              const void* grad_output, int grad_output_dtype, void* grad_value, float* grad_sampling_locations,
              float* grad_attention_weights, int batch, int n_heads, int head_dim, int len_query, int n_levels,
              int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value,
-             void* stream) {
+             void* workspace, int64_t workspace_bytes, void* stream) {
   g_last_error.clear();
   Shape s;
   int rc = validate(&s, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value);
@@ -332,77 +385,117 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   const int gbytes = grad_output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   if (!aligned(value, vbytes) || !aligned(grad_value, vbytes) || !aligned(grad_output, gbytes))
     return fail(MSDA_ERR_INVALID_ARGUMENT, "value/grad_value/grad_output not aligned to their element size");
-  const int vec = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 16),
-                           {{value, vbytes}, {grad_value, vbytes}, {grad_output, gbytes}});
+  const int64_t need = workspace_bytes_for(s);
+  const bool want_dv = grad_value != nullptr;
+  if (want_dv && len_query > 0) {
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace of %lld bytes needed, got %lld", static_cast<long long>(need),
+                  static_cast<long long>(workspace == nullptr ? 0 : workspace_bytes));
+    if (!aligned(workspace, 16)) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  }
+  for (int l = 0; l < n_levels; ++l)
+    if (s.h[l] > 32000 || s.w[l] > 32000)
+      return fail(MSDA_ERR_UNSUPPORTED, "level %d (%d x %d) exceeds 32000 rows or columns", l, s.h[l], s.w[l]);
+  if (static_cast<int64_t>(len_query) * n_points > 0x7fffffff / 16)
+    return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_points too large");
+  const int vec = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 8), {{value, vbytes}, {grad_output, gbytes}});
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
 
   DevInfo dev;
   if ((rc = device_info(&dev)) != MSDA_OK) return rc;
-
-  msda::BwdParams p{};
-  p.value = value;
-  p.loc = sampling_locations;
-  p.attn = attention_weights;
-  p.gout = grad_output;
-  p.dvalue = grad_value;
-  p.dloc = grad_sampling_locations;
-  p.dattn = grad_attention_weights;
-  p.gout_bf16 = grad_output_dtype == MSDA_DTYPE_BF16;
-  p.heads = n_heads;
-  p.dim = head_dim;
-  p.queries = len_query;
-  p.levels = n_levels;
-  p.points = n_points;
-  p.len_value = len_value;
-  p.lpq_shift = shift;
-  p.vec16 = rows_16b(s, vbytes, value, grad_value);
-
-  // Bands of image rows: each (slice, level, band) workgroup owns the band's grad_value rows.
-  // Rows per band are chosen so the workgroup count reaches the target and the LDS layout
-  // (staged rows, accumulator, cell tables, chunk buffers) fits the budget.
-  const int64_t N = static_cast<int64_t>(batch) * n_heads;
-  const int target = env_int("MSDA_BWD_TARGET_WGS", 2 * dev.cus);
-  const int budget = std::min(dev.lds_bytes, env_int("MSDA_BWD_LDS_BUDGET", 80 * 1024));
-  const int scan_seg = std::max(64, std::min({std::max(len_query, 1), env_int("MSDA_BWD_SCAN_SEG", 4096), 65536}));
-  const int64_t want_items = std::max<int64_t>(1, (target + N - 1) / N);
-  int64_t total_area = 0;
-  for (int l = 0; l < n_levels; ++l) total_area += static_cast<int64_t>(s.h[l]) * s.w[l];
-  int chunk_m = std::max(16, env_int("MSDA_BWD_CHUNK", 256));
-  int nwork = 0;
-  int lds_max = 0;
-  for (int l = 0; l < n_levels; ++l) {
-    auto bytes_for = [&](int rb, int m) {
-      return msda::bwd_layout(std::min(rb + 1, s.h[l]), rb, s.w[l], head_dim, vbytes, n_points, m, scan_seg).total;
-    };
-    // shrink the chunk until a one-row band fits the device
-    while (bytes_for(1, chunk_m) > dev.lds_bytes && chunk_m > 16) chunk_m >>= 1;
-    if (bytes_for(1, chunk_m) > dev.lds_bytes)
-      return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], head_dim);
-    const int cap = bytes_for(1, chunk_m) <= budget ? budget : dev.lds_bytes;
-    int rb_max = 1;
-    while (rb_max < s.h[l] && bytes_for(rb_max + 1, chunk_m) <= cap) ++rb_max;
-    const int64_t area = static_cast<int64_t>(s.h[l]) * s.w[l];
-    int nb = static_cast<int>((want_items * area + total_area / 2) / total_area);
-    const int forced = env_int("MSDA_BWD_BANDS", 0);
-    if (forced > 0) nb = forced;
-    nb = std::min(s.h[l], std::max({1, nb, (s.h[l] + rb_max - 1) / rb_max}));
-    const int rb = (s.h[l] + nb - 1) / nb;
-    nb = (s.h[l] + rb - 1) / rb;
-    p.lv[l] = msda::LevelDesc{s.h[l], s.w[l], static_cast<int>(s.start[l]), -1, rb, nwork};
-    nwork += nb;
-    lds_max = std::max(lds_max, bytes_for(rb, chunk_m));
-  }
-  p.nwork = nwork;
-  p.chunk_m = chunk_m;
-  p.scan_seg = scan_seg;
-  p.g_vec4 = (head_dim % 4 == 0) && aligned(grad_output, grad_output_dtype == MSDA_DTYPE_BF16 ? 8 : 16);
-  const int64_t grid = N * nwork;
-  if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
-
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (value_dtype == MSDA_DTYPE_BF16) return dispatch_bwd<msda::bf16_t>(vec, p, static_cast<int>(grid), lds_max, st);
-  return dispatch_bwd<float>(vec, p, static_cast<int>(grid), lds_max, st);
+
+  // ---- grad_value plan (checked before anything is launched)
+  msda::ValueParams vp{};
+  int vgrid = 0, vthreads = 0, vlds = 0;
+  if (want_dv) {
+    vp.rec = static_cast<const msda::SampleRec*>(workspace);
+    vp.gout = grad_output;
+    vp.gout_bf16 = grad_output_dtype == MSDA_DTYPE_BF16;
+    vp.dvalue = grad_value;
+    vp.heads = n_heads;
+    vp.dim = head_dim;
+    vp.queries = len_query;
+    vp.levels = n_levels;
+    vp.points = n_points;
+    vp.len_value = len_value;
+    vp.g_vec4 = (head_dim % 4 == 0) && aligned(grad_output, grad_output_dtype == MSDA_DTYPE_BF16 ? 8 : 16);
+    vp.vec16 = rows_16b(s, vbytes, grad_value, nullptr);
+    // Bands of image rows: each (slice, level, band) workgroup owns the band's grad_value rows.
+    // Rows per band are chosen so the grid reaches the target and the LDS layout (accumulator,
+    // cell tables, record list) fits the budget; the list holds as many records as fit.
+    const int64_t N = static_cast<int64_t>(batch) * n_heads;
+    const int target = env_int("MSDA_BWD_TARGET_WGS", 2 * dev.cus);
+    const int budget = std::min(dev.lds_bytes, env_int("MSDA_BWD_LDS_BUDGET", dev.lds_bytes / 2));
+    const int64_t want_items = std::max<int64_t>(1, (target + N - 1) / N);
+    int64_t total_area = 0;
+    for (int l = 0; l < n_levels; ++l) total_area += static_cast<int64_t>(s.h[l]) * s.w[l];
+    const int records = std::max(1, len_query * n_points);
+    const int cap_want = std::min({65535, records, std::max(256, env_int("MSDA_BWD_LIST", 65535))});
+    int nwork = 0, cap = cap_want, lds_max = 0;
+    int rbs[msda::kMaxLevels];
+    for (int l = 0; l < n_levels; ++l) {
+      const int64_t area = static_cast<int64_t>(s.h[l]) * s.w[l];
+      int nb = static_cast<int>((want_items * area + total_area / 2) / total_area);
+      const int forced = env_int("MSDA_BWD_BANDS", 0);
+      if (forced > 0) nb = forced;
+      nb = std::min(s.h[l], std::max(1, nb));
+      int rb = (s.h[l] + nb - 1) / nb;
+      // shrink the band until the accumulator and cell tables leave room for a list of >= 256
+      // 22 bytes of LDS per listed record (16 list + 4 key/rank + 2 order), 32 of alignment slack
+      auto fixed = [&](int r) { return msda::value_layout(r, s.w[l], head_dim, 0).total + 32; };
+      while (rb > 1 && (budget - fixed(rb)) / 22 < std::min(256, cap_want)) --rb;
+      if ((rb + 1) * (s.w[l] + 1) > 65535 || (dev.lds_bytes - fixed(rb)) / 22 < std::min(256, cap_want))
+        return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], head_dim);
+      rbs[l] = rb;
+      const int room = (std::max(budget, fixed(rb) + 22 * std::min(256, cap_want)) - fixed(rb)) / 22;
+      cap = std::min(cap, room);
+    }
+    cap = std::max(1, cap);
+    for (int l = 0; l < n_levels; ++l) {
+      const int rb = rbs[l];
+      const int nb = (s.h[l] + rb - 1) / rb;
+      vp.lv[l] = msda::LevelDesc{s.h[l], s.w[l], static_cast<int>(s.start[l]), -1, rb, nwork};
+      nwork += nb;
+      lds_max = std::max(lds_max, msda::value_layout(rb, s.w[l], head_dim, cap).total);
+    }
+    vp.nwork = nwork;
+    vp.cap = cap;
+    const int64_t grid = N * nwork;
+    if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
+    vgrid = static_cast<int>(grid);
+    vlds = lds_max;
+    vthreads = std::max(64, std::min(msda::kValueMaxThreads, (env_int("MSDA_BWD_VALUE_THREADS", 256) / 64) * 64));
+  }
+
+  // ---- per-sample pass: grad_attention_weights, grad_sampling_locations, grad_value records
+  if (len_query > 0) {
+    msda::SampleParams p{};
+    p.value = value;
+    p.loc = sampling_locations;
+    p.attn = attention_weights;
+    p.gout = grad_output;
+    p.gout_bf16 = grad_output_dtype == MSDA_DTYPE_BF16;
+    p.dloc = grad_sampling_locations;
+    p.dattn = grad_attention_weights;
+    p.rec = want_dv ? static_cast<uint4*>(workspace) : nullptr;
+    p.heads = n_heads;
+    p.dim = head_dim;
+    p.queries = len_query;
+    p.levels = n_levels;
+    p.points = n_points;
+    p.len_value = len_value;
+    p.vec16 = rows_16b(s, vbytes, value, nullptr);
+    SamplePlan plan;
+    if ((rc = plan_sample(s, vbytes, dev, "MSDA_BWDS", shift, &p, &plan)) != MSDA_OK) return rc;
+    rc = value_dtype == MSDA_DTYPE_BF16 ? dispatch_sample<msda::bf16_t>(true, vec, p, plan.grid, plan.threads, plan.lds, st)
+                                        : dispatch_sample<float>(true, vec, p, plan.grid, plan.threads, plan.lds, st);
+    if (rc != MSDA_OK) return rc;
+  }
+  if (!want_dv) return MSDA_OK;
+  if (value_dtype == MSDA_DTYPE_BF16) return launch_bwd_value<msda::bf16_t>(vp, vgrid, vthreads, vlds, st);
+  return launch_bwd_value<float>(vp, vgrid, vthreads, vlds, st);
 }
 
 }  // extern "C"

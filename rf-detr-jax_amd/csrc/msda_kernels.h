@@ -5,121 +5,123 @@
 // slice at 2*loc-1, corner order (x0,y0),(x1,y0),(x0,y1),(x1,y1), masked weights multiplied onto
 // values read at clipped indices, level-major point sum. Gradients are the VJP of those lines.
 //
-// Measured on MI355X (per CU): random 64-byte-row ds_read_b128 gathers run at ~220 B/clk (close to
-// the ~260 B/clk of contiguous reads), random ds_write_b128 at ~66 B/clk, ds_add_f32 at one lane
-// per ~3 cycles, and device-wide f32 atomics to L2 at ~1.3 TB/s. The design therefore gathers from
-// LDS freely, never uses atomics, and keeps every lane busy with useful work:
+// Kernels:
+//  * fwd_kernel — one workgroup per (batch b, group of hg heads, block of queries). The group's
+//    value slices (the levels that fit) are staged into LDS with one batched copy; levels that do
+//    not fit are gathered through L2. Lanes are laid out channel group, then head, then query, so
+//    the lanes of one query read locations / weights and write output rows as contiguous runs of
+//    the [B, Q, H, ...] tensors. Each lane group computes a sample's coordinates once; the next
+//    query's inputs are loaded while the current one is computed.
+//  * bwd_sample_kernel — the same decomposition for the backward pass: per sample, the dot
+//    products D_c = <g, v_c> with the four corners give grad_attention_weights and
+//    grad_sampling_locations, and a 16-byte record (floor cell, a*(1-fx), a*fx, fy) is written to
+//    a workspace in slice-major order [b*H+h][l][q][p], which grad_value reads contiguously.
+//  * bwd_value_kernel — one workgroup per (slice, level, band of rows). It reads its slice's
+//    records, lists those whose cell touches the band, counting-sorts them by cell in LDS (integer
+//    LDS atomics give each record its rank), and has one lane per (cell, 4 channels) sum
+//    a * w_k * g over the cell's records in registers, grad_output rows being gathered from global
+//    memory. The sums are added to an f32 band accumulator in four colour classes of cells (x and
+//    y parity) whose 2x2 pixel footprints are disjoint, so no two lanes write one element and no
+//    atomics on floats are needed; each grad_value element is written once, in the value dtype.
 //
-//  * Forward: one workgroup per (slice n = b*H+h, chunk of queries). The levels that fit the LDS
-//    budget and the chunk's sampling locations / weights are staged into LDS with all global loads
-//    in flight at once; levels that do not fit are gathered through L2. Each group of `lpq` lanes
-//    (normally one lane) owns a query and VEC channels of it, and computes each sample position
-//    once.
-//  * Backward: one workgroup per (slice, level, band of image rows). It stages the band's value
-//    rows (+1 halo row) and keeps one f32 grad_value accumulator per wave for the band. Each wave
-//    scans queries with one lane per query, computing only the row of each sample to decide
-//    whether the query matters to this band; the relevant queries are compacted (ballot + mbcnt)
-//    into a per-wave ring of records, which is processed one record per lane group once a full
-//    wave of records is available. A sample whose floor row lies in the band is "owned": its
-//    grad_location / grad_weight are computed here from the staged rows. Every sample with a
-//    corner row in the band adds a * w_c * g to its wave's accumulator. At the end the wave
-//    accumulators are summed and written once, in the value dtype: each grad element has one
-//    writer, with no atomics, no zero-fill pass and no cross-workgroup reduction.
-//  * Inside a wave, lane groups that target the same accumulator pixel in the same step are
-//    serialised by a write-tag / read-back round (write own id to the pixel's tag, read it back,
-//    the surviving id does a plain read-modify-write, the others retry). LDS instructions of one
-//    wave execute in order, so every round sees the previous round's writes.
-//  * Workgroups are re-numbered so each XCD receives a contiguous range of logical work items;
-//    the heads of one (batch, query range) are adjacent in that order, so the workgroups that
-//    share cache lines of sampling_locations / attention_weights / output / grad_output (all laid
-//    out [B, Q, H, ...]) run on the same XCD and share its L2.
+// Measured on MI355X (per CU): LDS float atomics (ds_add_f32) cost ~195 cycles per wave
+// instruction against ~6 for integer ones, and device-wide f32 atomics reach ~1.3 TB/s at best;
+// hence no float atomics anywhere. Generic (flat) pointers to LDS cost vector-memory issue slots,
+// so LDS reads go through address_space(3) pointers.
 #pragma once
 
 #include <hip/hip_runtime.h>
-#include <stdint.h>
 
+#include <cstdint>
 #include <type_traits>
 
 namespace msda {
 
 constexpr int kMaxLevels = 16;
-constexpr int kXcds = 8;  // MI355X: 8 accelerator complex dies, workgroups dispatched round-robin
-constexpr int kFwdThreads = 256;
-constexpr int kBwdThreads = 256;
+constexpr int kXcds = 8;               // MI355X: 8 accelerator complex dies, workgroups dispatched round-robin
+constexpr int kSampleMaxThreads = 512;  // forward and per-sample backward workgroups
+constexpr int kValueMaxThreads = 512;   // grad_value workgroups
+constexpr int kPassBatch = 4;           // samples whose loads are issued together (software-pipelined)
 
 using bf16_t = uint16_t;
+
 struct LevelDesc {
   int h, w;        // level height and width
   int start;       // first position of the level in the value slice
-  int lds;         // forward: element offset of the staged level in LDS, -1 = read from global memory
-  int band_rows;   // backward: image rows per band
-  int band_first;  // backward: index of the level's first band among a slice's (level, band) items
+  int lds;         // per-sample kernels: element offset of the staged level inside a head's LDS region, -1 = L2
+  int band_rows;   // grad_value kernel: image rows per band
+  int band_first;  // grad_value kernel: index of the level's first band among a slice's (level, band) items
 };
 
-struct FwdParams {
+// Forward and per-sample backward kernels.
+struct SampleParams {
   const void* value;
   const float* loc;
   const float* attn;
-  void* out;
+  void* out;         // forward: output [B, Q, H*D]
   int out_bf16;
-  int heads, dim, queries, levels, points;
-  int64_t len_value;
-  int lpq_shift;  // log2(lanes per query)
-  int qchunk;     // queries per workgroup
-  int nqc;        // query chunks per slice
-  int vec16;      // value staging may use 16-byte vectors
-  int loc_lds;    // byte offset of the staged locations/weights in LDS, -1 = read them from global memory
-  LevelDesc lv[kMaxLevels];
-};
-
-struct BwdParams {
-  const void* value;
-  const float* loc;
-  const float* attn;
-  const void* gout;
-  void* dvalue;
-  float* dloc;
-  float* dattn;
+  const void* gout;  // backward: grad_output [B, Q, H*D]
   int gout_bf16;
+  float* dloc;       // backward: grad_sampling_locations, or null
+  float* dattn;      // backward: grad_attention_weights, or null
+  uint4* rec;        // backward: per-sample records for grad_value, or null
   int heads, dim, queries, levels, points;
   int64_t len_value;
-  int lpq_shift;  // log2(lanes per sample) in the owner pass
-  int nwork;      // (level, band) items per slice
-  int vec16;
-  int chunk_m;    // relevant queries whose inputs are staged in LDS at a time
-  int scan_seg;   // queries scanned per segment (capacity of the relevant-query list)
-  int g_vec4;     // grad_output rows may be read 4 channels at a time
+  int lpq_shift;   // log2(lanes per (query, head)); each lane owns VEC channels
+  int hg;          // heads per workgroup (divides heads)
+  int qblock;      // queries per workgroup
+  int nqb;         // query blocks per (batch, head group)
+  int head_lds;    // LDS elements of one head's staged levels
+  int all_staged;  // every level is staged, so a head group's value rows are one contiguous copy
+  int vec16;       // value staging may use 16-byte vectors
   LevelDesc lv[kMaxLevels];
 };
 
-// LDS carve-up of one backward workgroup; shared by the host planner and the kernel so both
-// agree on the size. Every region starts on a 16-byte boundary.
-struct BwdLayout {
-  int sv, acc, cnt, off, misc, rel, cg, cl, ca, skey, srank, swt, rslot, rw, total;
+// A sample's record for grad_value: the floor cell (x0, y0) packed as two int16 (for non-finite
+// weights, the clipped first corner), u = a * (1 - fx), v = a * fx, and fy, so that the corner
+// weights are u*(1-fy), v*(1-fy), u*fy, v*fy.
+struct __align__(16) SampleRec {
+  uint32_t cell;
+  float u, v, fy;
 };
 
-__host__ __device__ inline int bwd_align16(int x) { return (x + 15) & ~15; }
+__host__ __device__ inline uint32_t pack_cell(int x0, int y0) {
+  return (static_cast<uint32_t>(x0) & 0xffffu) | (static_cast<uint32_t>(y0) << 16);
+}
 
-__host__ __device__ inline BwdLayout bwd_layout(int staged_rows, int band_rows, int w, int dim, int vbytes, int points,
-                                                int chunk_m, int scan_seg) {
-  BwdLayout L;
+struct ValueParams {
+  const SampleRec* rec;
+  const void* gout;
+  int gout_bf16;
+  void* dvalue;
+  int heads, dim, queries, levels, points;
+  int64_t len_value;
+  int nwork;   // (level, band) items per slice
+  int cap;     // records listed per segment (LDS list capacity)
+  int g_vec4;  // grad_output rows may be read 4 channels at a time
+  int vec16;   // grad_value rows may be written 16 bytes at a time
+  LevelDesc lv[kMaxLevels];
+};
+
+// LDS carve-up of one grad_value workgroup; shared by the host planner and the kernel. Every
+// region starts on a 16-byte boundary.
+struct ValueLayout {
+  int acc, cnt, off, misc, list, keyrank, sorted, total;
+};
+
+__host__ __device__ inline int align16i(int x) { return (x + 15) & ~15; }
+
+__host__ __device__ inline ValueLayout value_layout(int band_rows, int w, int dim, int cap) {
+  ValueLayout L;
   const int ncell = (band_rows + 1) * (w + 1);
-  const int ns = chunk_m * points;  // samples per chunk
   int o = 0;
-  L.sv = o;    o += bwd_align16(staged_rows * w * dim * vbytes);
-  L.acc = o;   o += bwd_align16(band_rows * w * dim * 4);
-  L.cnt = o;   o += bwd_align16(ncell * 4);
-  L.off = o;   o += bwd_align16((ncell + 1) * 4);
-  L.misc = o;  o += 64;
-  L.rel = o;   o += bwd_align16(scan_seg * 2);
-  L.cg = o;    o += bwd_align16(chunk_m * dim * 4);
-  L.cl = o;    o += bwd_align16(ns * 8);
-  L.ca = o;    o += bwd_align16(ns * 4);
-  L.skey = o;  o += bwd_align16(ns * 4);
-  L.srank = o; o += bwd_align16(ns * 4);
-  L.swt = o;   o += bwd_align16(ns * 16);
-  L.rslot = o; o += bwd_align16(ns * 4);
-  L.rw = o;    o += bwd_align16(ns * 16);
+  L.acc = o;     o += align16i(band_rows * w * dim * 4);
+  L.cnt = o;     o += align16i((ncell + 1) * 4);
+  L.off = o;     o += align16i((ncell + 1) * 4);
+  L.misc = o;    o += 64;
+  L.list = o;    o += cap * 16;
+  L.keyrank = o; o += align16i(cap * 4);
+  L.sorted = o;  o += align16i(cap * 2);
   L.total = o;
   return L;
 }
@@ -158,8 +160,7 @@ struct Bilinear {
   float w00, w10, w01, w11;    // masked corner weights
   float m00, m10, m01, m11;    // in-bounds masks
   float fx, fy;                // fractional parts
-  int y0c, y1c;                // clipped rows of the two corner rows
-  float y0f;                   // floor of the row coordinate
+  int x0, y0;                  // floor corner, clamped to [-2, size] (outside means all-masked)
 };
 
 // ops.py:85-128 for one sample position.
@@ -195,9 +196,8 @@ __device__ __forceinline__ Bilinear bilinear(float lx, float ly, int h, int w) {
   c.w10 = (c.fx * gy) * c.m10;
   c.w01 = (gx * c.fy) * c.m01;
   c.w11 = (c.fx * c.fy) * c.m11;
-  c.y0c = cy0;
-  c.y1c = cy1;
-  c.y0f = y0f;
+  c.x0 = x0;
+  c.y0 = y0;
   return c;
 }
 
@@ -222,6 +222,28 @@ __device__ __forceinline__ void load_vec(const VT* __restrict__ p, float (&o)[VE
     for (int k = 0; k < VEC; ++k) o[k] = v[k];
   } else {
     const typename VecT<bf16_t, VEC>::type v = *reinterpret_cast<const typename VecT<bf16_t, VEC>::type*>(p);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = bf16_to_f32(v[k]);
+  }
+}
+
+// LDS-qualified loads: a generic pointer that may point at LDS or global memory compiles to
+// flat loads, and the optimizer merges identical LDS / global branches back into one, so LDS
+// reads go through an address_space(3) pointer.
+#define MSDA_LDS __attribute__((address_space(3)))
+
+template <typename VT, int VEC>
+__device__ __forceinline__ void load_vec_lds(const VT* p_generic, float (&o)[VEC]) {
+  const MSDA_LDS VT* p = (const MSDA_LDS VT*)(p_generic);
+  if constexpr (VEC == 1) {
+    if constexpr (std::is_same<VT, float>::value) o[0] = *p;
+    else o[0] = bf16_to_f32(*p);
+  } else if constexpr (std::is_same<VT, float>::value) {
+    const typename VecT<float, VEC>::type v = *(const MSDA_LDS typename VecT<float, VEC>::type*)(p);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = v[k];
+  } else {
+    const typename VecT<bf16_t, VEC>::type v = *(const MSDA_LDS typename VecT<bf16_t, VEC>::type*)(p);
 #pragma unroll
     for (int k = 0; k < VEC; ++k) o[k] = bf16_to_f32(v[k]);
   }
@@ -295,146 +317,339 @@ __device__ __forceinline__ float group_sum(float v, int lpq) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// forward
+// per-sample kernels: shared work-item decomposition and staging
 
-template <typename VT, int VEC>
-__global__ void __launch_bounds__(kFwdThreads) fwd_kernel(const FwdParams p) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  VT* lds = reinterpret_cast<VT*>(lds_raw);
+struct SampleItem {
+  int b, h0, qb;
+};
 
+// Work item = (batch b, head group, query block); the blocks of one (b, group) are adjacent in
+// logical order, so they run on one XCD and share its L2 copy of the group's value rows.
+__device__ __forceinline__ SampleItem sample_item(const SampleParams& p) {
+  const int ngroups = p.heads / p.hg;
   const int lid = xcd_logical(blockIdx.x, gridDim.x);
-  const int h = lid % p.heads;
-  const int rest = lid / p.heads;
-  const int qc = rest % p.nqc;
-  const int b = rest / p.nqc;
-  const int64_t n = static_cast<int64_t>(b) * p.heads + h;
-  const VT* __restrict__ vs = static_cast<const VT*>(p.value) + n * p.len_value * p.dim;
-  const int LP = p.levels * p.points;
-  const int q_lo = qc * p.qchunk;
-  const int q_hi = min(p.queries, q_lo + p.qchunk);
+  SampleItem it;
+  it.qb = lid % p.nqb;
+  const int rest = lid / p.nqb;
+  it.h0 = (rest % ngroups) * p.hg;
+  it.b = rest / ngroups;
+  return it;
+}
 
-  // The chunk's sampling locations [q][LP] (float2) and weights [q][LP], contiguous per query in
-  // LDS. Their loads are issued first, in batches held in registers, so they overlap the value
-  // staging below; the LDS stores happen after it.
-  const bool loc_in_lds = p.loc_lds >= 0;
-  float2* sl = reinterpret_cast<float2*>(lds_raw + (loc_in_lds ? p.loc_lds : 0));
-  float* sa = reinterpret_cast<float*>(sl + p.qchunk * LP);
-  constexpr int UL = 4;
-  const int nt = blockDim.x;
-  const int E = loc_in_lds ? (q_hi - q_lo) * LP : 0;
-  const int64_t row0 = (static_cast<int64_t>(b) * p.queries + q_lo) * p.heads + h;
-  const float2* lsrc = reinterpret_cast<const float2*>(p.loc) + row0 * LP;
-  const float* asrc = p.attn + row0 * LP;
-  const int64_t qstride = static_cast<int64_t>(p.heads) * LP;  // samples between consecutive queries
-  float2 rl[UL];
-  float ra[UL];
-#pragma unroll
-  for (int u = 0; u < UL; ++u) {
-    const int i = threadIdx.x + u * nt;
-    if (i < E) {
-      const int qq = i / LP, k = i - qq * LP;
-      rl[u] = lsrc[qq * qstride + k];
-      ra[u] = asrc[qq * qstride + k];
-    }
+// The group's slices are consecutive rows of value [B*H, S, D]: when every level is staged they
+// are one contiguous copy.
+template <typename VT>
+__device__ __forceinline__ void stage_group(const SampleParams& p, VT* lds, const VT* __restrict__ vg) {
+  const int64_t slice_elems = p.len_value * p.dim;
+  if (p.all_staged) {
+    stage_copy(lds, vg, static_cast<int>(p.hg * slice_elems), p.vec16);
+    return;
   }
-  for (int l = 0; l < p.levels; ++l) {
-    const LevelDesc L = p.lv[l];
-    if (L.lds >= 0) stage_copy(lds + L.lds, vs + static_cast<int64_t>(L.start) * p.dim, L.h * L.w * p.dim, p.vec16);
-  }
-#pragma unroll
-  for (int u = 0; u < UL; ++u) {
-    const int i = threadIdx.x + u * nt;
-    if (i < E) {
-      sl[i] = rl[u];
-      sa[i] = ra[u];
-    }
-  }
-  for (int base = threadIdx.x + UL * nt; base < E; base += UL * nt) {  // chunks larger than UL * nt
-#pragma unroll
-    for (int u = 0; u < UL; ++u) {
-      const int i = base + u * nt;
-      if (i < E) {
-        const int qq = i / LP, k = i - qq * LP;
-        rl[u] = lsrc[qq * qstride + k];
-        ra[u] = asrc[qq * qstride + k];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < UL; ++u) {
-      const int i = base + u * nt;
-      if (i < E) {
-        sl[i] = rl[u];
-        sa[i] = ra[u];
-      }
-    }
-  }
-  __syncthreads();
-
-  const int lpq = 1 << p.lpq_shift;
-  const int j = threadIdx.x & (lpq - 1);
-  const int slot = threadIdx.x >> p.lpq_shift;
-  const int nslots = blockDim.x >> p.lpq_shift;
-  const bool lane_on = j * VEC < p.dim;
-  const int c0 = lane_on ? j * VEC : 0;
-
-  for (int q = q_lo + slot; q < q_hi; q += nslots) {
-    const int64_t bqh = (static_cast<int64_t>(b) * p.queries + q) * p.heads + h;
-    const float2* lq = loc_in_lds ? sl + (q - q_lo) * LP : reinterpret_cast<const float2*>(p.loc) + bqh * LP;
-    const float* aq = loc_in_lds ? sa + (q - q_lo) * LP : p.attn + bqh * LP;
-    float acc[VEC];
-#pragma unroll
-    for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
+  for (int hh = 0; hh < p.hg; ++hh)
     for (int l = 0; l < p.levels; ++l) {
       const LevelDesc L = p.lv[l];
-      for (int pt = 0; pt < p.points; ++pt) {
-        const int s = l * p.points + pt;
-        const float2 xy = lq[s];
-        const float a = aq[s];
-        const Bilinear c = bilinear(xy.x, xy.y, L.h, L.w);
-        float v00[VEC], v10[VEC], v01[VEC], v11[VEC];
-        if (L.lds >= 0) {
-          const VT* base = lds + L.lds + c0;
-          load_vec<VT, VEC>(base + c.i00 * p.dim, v00);
-          load_vec<VT, VEC>(base + c.i10 * p.dim, v10);
-          load_vec<VT, VEC>(base + c.i01 * p.dim, v01);
-          load_vec<VT, VEC>(base + c.i11 * p.dim, v11);
-        } else {
-          const VT* base = vs + static_cast<int64_t>(L.start) * p.dim + c0;
-          load_vec<VT, VEC>(base + static_cast<int64_t>(c.i00) * p.dim, v00);
-          load_vec<VT, VEC>(base + static_cast<int64_t>(c.i10) * p.dim, v10);
-          load_vec<VT, VEC>(base + static_cast<int64_t>(c.i01) * p.dim, v01);
-          load_vec<VT, VEC>(base + static_cast<int64_t>(c.i11) * p.dim, v11);
-        }
-        const float a00 = a * c.w00, a10 = a * c.w10, a01 = a * c.w01, a11 = a * c.w11;
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) acc[k] += v00[k] * a00 + v10[k] * a10 + v01[k] * a01 + v11[k] * a11;
-      }
+      if (L.lds >= 0)
+        stage_copy(lds + hh * p.head_lds + L.lds, vg + hh * slice_elems + static_cast<int64_t>(L.start) * p.dim,
+                   L.h * L.w * p.dim, p.vec16);
     }
-    if (lane_on) store_any<VEC>(p.out, bqh * p.dim + c0, p.out_bf16 != 0, acc);
+}
+
+// Lane layout: channel groups of one (query, head) are adjacent, then the group's heads, then
+// queries; so the lanes of one query touch contiguous runs of its [H, ...] rows.
+struct SampleLane {
+  int j, hl, qs, qpp, c0;
+  bool active, lane_on;
+};
+
+template <int VEC>
+__device__ __forceinline__ SampleLane sample_lane(const SampleParams& p) {
+  SampleLane s;
+  const int lpq = 1 << p.lpq_shift;
+  const int t = threadIdx.x;
+  s.j = t & (lpq - 1);
+  const int hq = t >> p.lpq_shift;
+  s.hl = hq % p.hg;
+  s.qs = hq / p.hg;
+  s.qpp = (static_cast<int>(blockDim.x) >> p.lpq_shift) / p.hg;  // queries per pass
+  s.active = s.qs < s.qpp;
+  s.lane_on = s.j * VEC < p.dim;
+  s.c0 = s.lane_on ? s.j * VEC : 0;
+  return s;
+}
+
+// A lane's inputs for up to kPassBatch samples of one (query, head).
+struct PassIn {
+  float2 xy[kPassBatch];
+  float a[kPassBatch];
+};
+
+__device__ __forceinline__ void load_pass(PassIn& f, const float2* __restrict__ lq, const float* __restrict__ aq, int s0,
+                                          int LP) {
+#pragma unroll
+  for (int u = 0; u < kPassBatch; ++u) {
+    if (s0 + u < LP) {
+      f.xy[u] = lq[s0 + u];
+      f.a[u] = aq[s0 + u];
+    }
   }
 }
 
 // ---------------------------------------------------------------------------------------------
-// backward
-//
-// One workgroup per (slice, level, band of rows [r0, r1)). Phases:
-//  0. stage the band's value rows (+1 halo row); zero the f32 accumulator of the band's pixels.
-//  1. scan: the row coordinate of every sample of the slice on this level is loaded (all loads of
-//     a round in flight) and tested against the band; queries with a relevant sample are
-//     compacted into a list (ballot per wave, one LDS atomic per wave to reserve space).
-//  2. per chunk of `chunk_m` listed queries:
-//     a. stage grad_output rows, locations and weights of the chunk into LDS;
-//     b. one lane group per sample: owned samples (floor row in the band) get their grad_weight
-//        and grad_location from the staged value rows; samples with a corner pixel in the band
-//        are bucketed by bilinear cell (x0, y0): ds_add_rtn_u32 on the cell's count gives the
-//        sample's rank inside the cell;
-//     c. exclusive scan of the cell counts (cells are ordered row-major);
-//     d. samples are written into cell order;
-//     e. pixel-major gather: one lane per (band pixel, 4 channels) sums, in registers, a * w_k * g
-//        over the samples of the four cells that have this pixel as corner k, and adds the sum to
-//        its own accumulator slot. Every accumulator element has exactly one writer per chunk.
-//  3. the accumulator is written to grad_value in the value dtype.
-// Integer LDS atomics are cheap on gfx950 (~10 lanes/clk); float ones are not, and none are used.
+// forward
+
+template <typename VT, int VEC, bool kLds>
+__device__ __forceinline__ void fwd_corners(float (&acc)[VEC], const VT* base, const Bilinear& c, int D, float a) {
+  const float a00 = a * c.w00, a10 = a * c.w10, a01 = a * c.w01, a11 = a * c.w11;
+  // Two corners in flight at a time keeps 16-channel lanes within the register budget.
+  float u0[VEC], u1[VEC];
+  if constexpr (kLds) {
+    load_vec_lds<VT, VEC>(base + c.i00 * D, u0);
+    load_vec_lds<VT, VEC>(base + c.i10 * D, u1);
+  } else {
+    load_vec<VT, VEC>(base + c.i00 * D, u0);
+    load_vec<VT, VEC>(base + c.i10 * D, u1);
+  }
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) acc[k] += u0[k] * a00 + u1[k] * a10;
+  if constexpr (kLds) {
+    load_vec_lds<VT, VEC>(base + c.i01 * D, u0);
+    load_vec_lds<VT, VEC>(base + c.i11 * D, u1);
+  } else {
+    load_vec<VT, VEC>(base + c.i01 * D, u0);
+    load_vec<VT, VEC>(base + c.i11 * D, u1);
+  }
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) acc[k] += u0[k] * a01 + u1[k] * a11;
+}
+
+template <typename VT, int VEC>
+__device__ __forceinline__ void fwd_pass(float (&acc)[VEC], const PassIn& f, int s0, int LP, int& l, int& pt,
+                                         const SampleParams& p, const VT* hlds, const VT* __restrict__ vs) {
+  const int D = p.dim;
+#pragma unroll
+  for (int u = 0; u < kPassBatch; ++u) {
+    if (s0 + u < LP) {
+      const LevelDesc L = p.lv[l];
+      const Bilinear c = bilinear(f.xy[u].x, f.xy[u].y, L.h, L.w);
+      // Separate LDS and global paths: a pointer that may be either compiles to flat loads.
+      if (L.lds >= 0) fwd_corners<VT, VEC, true>(acc, hlds + L.lds, c, D, f.a[u]);
+      else fwd_corners<VT, VEC, false>(acc, vs + static_cast<int64_t>(L.start) * D, c, D, f.a[u]);
+      if (++pt == p.points) {
+        pt = 0;
+        ++l;
+      }
+    }
+  }
+}
+
+template <typename VT, int VEC>
+__global__ void __launch_bounds__(kSampleMaxThreads) fwd_kernel(const SampleParams p) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  VT* lds = reinterpret_cast<VT*>(lds_raw);
+  const SampleItem it = sample_item(p);
+  const SampleLane ln = sample_lane<VEC>(p);
+  const int D = p.dim;
+  const int64_t slice_elems = p.len_value * D;
+  const VT* __restrict__ vg = static_cast<const VT*>(p.value) + (static_cast<int64_t>(it.b) * p.heads + it.h0) * slice_elems;
+  const int h = it.h0 + ln.hl;
+  const int LP = p.levels * p.points;
+  const bool pipelined = LP <= kPassBatch;
+  const int q_lo = it.qb * p.qblock;
+  const int q_hi = min(p.queries, q_lo + p.qblock);
+  const float2* __restrict__ loc2 = reinterpret_cast<const float2*>(p.loc);
+  auto row_of = [&](int q) { return (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h; };  // (b, q, h)
+
+  // The first pass's inputs are requested before the value rows, so both latencies overlap.
+  int q = q_lo + ln.qs;
+  PassIn cur;
+  if (ln.active && pipelined && q < q_hi) load_pass(cur, loc2 + row_of(q) * LP, p.attn + row_of(q) * LP, 0, LP);
+  stage_group(p, lds, vg);
+  __syncthreads();
+  if (!ln.active) return;  // no barrier follows
+
+  const VT* __restrict__ vs = vg + ln.hl * slice_elems + ln.c0;  // this head's slice in global memory
+  const VT* hlds = lds + ln.hl * p.head_lds + ln.c0;
+  for (; q < q_hi; q += ln.qpp) {
+    const int64_t row = row_of(q);
+    float acc[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
+    int l = 0, pt = 0;  // level and point of the next sample (level-major order, ops.py:285)
+    if (pipelined) {
+      PassIn nxt;
+      const int qn = q + ln.qpp;
+      if (qn < q_hi) load_pass(nxt, loc2 + row_of(qn) * LP, p.attn + row_of(qn) * LP, 0, LP);
+      fwd_pass<VT, VEC>(acc, cur, 0, LP, l, pt, p, hlds, vs);
+      cur = nxt;
+    } else {
+      for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
+        PassIn f;
+        load_pass(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
+        fwd_pass<VT, VEC>(acc, f, s0, LP, l, pt, p, hlds, vs);
+      }
+    }
+    if (ln.lane_on) store_any<VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// backward, per sample: grad_attention_weights, grad_sampling_locations, grad_value records
+
+template <typename VT, int VEC, bool kLds>
+__device__ __forceinline__ void corner_dots(const VT* base, const Bilinear& c, int D, const float (&g)[VEC], float& d00,
+                                            float& d10, float& d01, float& d11) {
+  float u0[VEC], u1[VEC];
+  if constexpr (kLds) {
+    load_vec_lds<VT, VEC>(base + c.i00 * D, u0);
+    load_vec_lds<VT, VEC>(base + c.i10 * D, u1);
+  } else {
+    load_vec<VT, VEC>(base + c.i00 * D, u0);
+    load_vec<VT, VEC>(base + c.i10 * D, u1);
+  }
+  d00 = 0.0f;
+  d10 = 0.0f;
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    d00 += g[k] * u0[k];
+    d10 += g[k] * u1[k];
+  }
+  if constexpr (kLds) {
+    load_vec_lds<VT, VEC>(base + c.i01 * D, u0);
+    load_vec_lds<VT, VEC>(base + c.i11 * D, u1);
+  } else {
+    load_vec<VT, VEC>(base + c.i01 * D, u0);
+    load_vec<VT, VEC>(base + c.i11 * D, u1);
+  }
+  d01 = 0.0f;
+  d11 = 0.0f;
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    d01 += g[k] * u0[k];
+    d11 += g[k] * u1[k];
+  }
+}
+
+template <typename VT, int VEC>
+__device__ __forceinline__ void bwd_pass(const PassIn& f, const float (&g)[VEC], int s0, int LP, int& l, int& pt,
+                                         const SampleParams& p, const SampleLane& ln, const VT* hlds,
+                                         const VT* __restrict__ vs, int64_t row, int64_t rec_row, int64_t rec_lstride) {
+  const int D = p.dim;
+  const int lpq = 1 << p.lpq_shift;
+#pragma unroll
+  for (int u = 0; u < kPassBatch; ++u) {
+    if (s0 + u < LP) {
+      const LevelDesc L = p.lv[l];
+      const Bilinear c = bilinear(f.xy[u].x, f.xy[u].y, L.h, L.w);
+      const float a = f.a[u];
+      float d00, d10, d01, d11;
+      if (L.lds >= 0) corner_dots<VT, VEC, true>(hlds + L.lds, c, D, g, d00, d10, d01, d11);
+      else corner_dots<VT, VEC, false>(vs + static_cast<int64_t>(L.start) * D, c, D, g, d00, d10, d01, d11);
+      d00 = group_sum(d00, lpq);
+      d10 = group_sum(d10, lpq);
+      d01 = group_sum(d01, lpq);
+      d11 = group_sum(d11, lpq);
+      if (ln.j == 0) {
+        const int64_t si = row * LP + s0 + u;  // sample index in [B, Q, H, L, P]
+        // dA = sum_c w_c D_c (the sample itself); d out / d ix = gy (m10 D10 - m00 D00) + fy (m11 D11 - m01 D01)
+        if (p.dattn) p.dattn[si] = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
+        if (p.dloc) {
+          const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
+          const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
+          const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
+          // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
+          *reinterpret_cast<float2*>(p.dloc + 2 * si) =
+              make_float2(a * static_cast<float>(L.w) * dx, a * static_cast<float>(L.h) * dy);
+        }
+        if (p.rec) {
+          // Non-finite weights (NaN or infinite coordinates) go to the clipped first corner's cell,
+          // where the reference's scatter-add puts them.
+          const bool finite = isfinite(c.w00) && isfinite(c.w10) && isfinite(c.w01) && isfinite(c.w11);
+          const uint32_t cell = finite ? pack_cell(c.x0, c.y0) : pack_cell(c.i00 % L.w, c.i00 / L.w);
+          p.rec[rec_row + l * rec_lstride + pt] =
+              make_uint4(cell, __float_as_uint(a * (1.0f - c.fx)), __float_as_uint(a * c.fx), __float_as_uint(c.fy));
+        }
+      }
+      if (++pt == p.points) {
+        pt = 0;
+        ++l;
+      }
+    }
+  }
+}
+
+template <typename VT, int VEC>
+__global__ void __launch_bounds__(kSampleMaxThreads) bwd_sample_kernel(const SampleParams p) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  VT* lds = reinterpret_cast<VT*>(lds_raw);
+  const SampleItem it = sample_item(p);
+  const SampleLane ln = sample_lane<VEC>(p);
+  const int D = p.dim;
+  const int64_t slice_elems = p.len_value * D;
+  const VT* __restrict__ vg = static_cast<const VT*>(p.value) + (static_cast<int64_t>(it.b) * p.heads + it.h0) * slice_elems;
+  const int h = it.h0 + ln.hl;
+  const int P = p.points;
+  const int LP = p.levels * P;
+  const bool pipelined = LP <= kPassBatch;
+  const int q_lo = it.qb * p.qblock;
+  const int q_hi = min(p.queries, q_lo + p.qblock);
+  const float2* __restrict__ loc2 = reinterpret_cast<const float2*>(p.loc);
+  const bool gbf = p.gout_bf16 != 0;
+  auto row_of = [&](int q) { return (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h; };  // (b, q, h)
+  // records of slice n = b*H + h: [n][l][q][p]
+  const int64_t rec_lstride = static_cast<int64_t>(p.queries) * P;
+  const int64_t rec_slice = (static_cast<int64_t>(it.b) * p.heads + h) * p.levels * rec_lstride;
+
+  int q = q_lo + ln.qs;
+  PassIn cur;
+  float gcur[VEC];
+  if (ln.active && pipelined && q < q_hi) {
+    load_pass(cur, loc2 + row_of(q) * LP, p.attn + row_of(q) * LP, 0, LP);
+    load_any<VEC>(p.gout, row_of(q) * D + ln.c0, gbf, gcur);
+  }
+  stage_group(p, lds, vg);
+  __syncthreads();
+  if (!ln.active) return;  // no barrier follows
+
+  const VT* __restrict__ vs = vg + ln.hl * slice_elems + ln.c0;
+  const VT* hlds = lds + ln.hl * p.head_lds + ln.c0;
+  for (; q < q_hi; q += ln.qpp) {
+    const int64_t row = row_of(q);
+    const int64_t rec_row = rec_slice + static_cast<int64_t>(q) * P;
+    int l = 0, pt = 0;
+    if (pipelined) {
+      PassIn nxt;
+      float gnxt[VEC];
+      const int qn = q + ln.qpp;
+      if (qn < q_hi) {
+        load_pass(nxt, loc2 + row_of(qn) * LP, p.attn + row_of(qn) * LP, 0, LP);
+        load_any<VEC>(p.gout, row_of(qn) * D + ln.c0, gbf, gnxt);
+      }
+      if (!ln.lane_on) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) gcur[k] = 0.0f;
+      }
+      bwd_pass<VT, VEC>(cur, gcur, 0, LP, l, pt, p, ln, hlds, vs, row, rec_row, rec_lstride);
+      cur = nxt;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) gcur[k] = gnxt[k];
+    } else {
+      float g[VEC];
+      load_any<VEC>(p.gout, row * D + ln.c0, gbf, g);
+      if (!ln.lane_on) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) g[k] = 0.0f;
+      }
+      for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
+        PassIn f;
+        load_pass(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
+        bwd_pass<VT, VEC>(f, g, s0, LP, l, pt, p, ln, hlds, vs, row, rec_row, rec_lstride);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// backward, grad_value: one workgroup per (slice, level, band of rows [r0, r1))
 
 // Exclusive prefix sum of cnt[0, n) into off[0, n] (off[n] = total); block-wide, ends in a barrier.
 // cnt is cleared for reuse. `tmp` holds one int per wave.
@@ -462,8 +677,28 @@ __device__ __forceinline__ void block_scan_counts(int* cnt, int* off, int n, int
   __syncthreads();
 }
 
-template <typename VT, int VEC>
-__global__ void __launch_bounds__(kBwdThreads) bwd_kernel(const BwdParams p) {
+// 4 channels of grad_output row `row` starting at channel ch0 (nch of them valid).
+__device__ __forceinline__ float4 load_g4(const ValueParams& p, int64_t off, int nch) {
+  if (nch == 4 && p.g_vec4) {
+    if (p.gout_bf16) {
+      const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const bf16_t*>(p.gout) + off);
+      return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
+                         __uint_as_float(r.y & 0xffff0000u));
+    }
+    return *reinterpret_cast<const float4*>(static_cast<const float*>(p.gout) + off);
+  }
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float x[1] = {0.0f};
+    if (e < nch) load_any<1>(p.gout, off + e, p.gout_bf16 != 0, x);
+    v[e] = x[0];
+  }
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+template <typename VT>
+__global__ void __launch_bounds__(kValueMaxThreads) bwd_value_kernel(const ValueParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
 
   const int lid = xcd_logical(blockIdx.x, gridDim.x);
@@ -475,291 +710,188 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_kernel(const BwdParams p) {
   while (l + 1 < p.levels && wk >= p.lv[l + 1].band_first) ++l;
   const LevelDesc L = p.lv[l];
   const int W = L.w;
-  const int r0 = (wk - L.band_first) * L.band_rows;  // band rows [r0, r1); staged rows [r0, rs1)
+  const int r0 = (wk - L.band_first) * L.band_rows;
   const int r1 = min(L.h, r0 + L.band_rows);
-  const int rs1 = min(L.h, r1 + 1);
   const int rb = r1 - r0;
   const int D = p.dim;
   const int P = p.points;
-  const int LP = p.levels * P;
   const int Q = p.queries;
   const int ncell = (rb + 1) * (W + 1);
   const int64_t n = static_cast<int64_t>(b) * p.heads + h;
-  const int64_t band_off = (n * p.len_value + L.start + static_cast<int64_t>(r0) * W) * D;
   const int nt = blockDim.x, t = threadIdx.x, lane = t & 63;
 
-  const BwdLayout lay = bwd_layout(rs1 - r0, rb, W, D, static_cast<int>(sizeof(VT)), P, p.chunk_m, p.scan_seg);
-  VT* sv = reinterpret_cast<VT*>(lds_raw + lay.sv);
+  const ValueLayout lay = value_layout(L.band_rows, W, D, p.cap);
   float* acc = reinterpret_cast<float*>(lds_raw + lay.acc);
   int* cnt = reinterpret_cast<int*>(lds_raw + lay.cnt);
   int* off = reinterpret_cast<int*>(lds_raw + lay.off);
-  int* misc = reinterpret_cast<int*>(lds_raw + lay.misc);  // [0] list size, [4..] scan scratch
-  uint16_t* rel = reinterpret_cast<uint16_t*>(lds_raw + lay.rel);
-  float* cg = reinterpret_cast<float*>(lds_raw + lay.cg);
-  float2* cl = reinterpret_cast<float2*>(lds_raw + lay.cl);
-  float* ca = reinterpret_cast<float*>(lds_raw + lay.ca);
-  int* skey = reinterpret_cast<int*>(lds_raw + lay.skey);
-  int* srank = reinterpret_cast<int*>(lds_raw + lay.srank);
-  float4* swt = reinterpret_cast<float4*>(lds_raw + lay.swt);
-  int* rslot = reinterpret_cast<int*>(lds_raw + lay.rslot);
-  float4* rw = reinterpret_cast<float4*>(lds_raw + lay.rw);
+  int* misc = reinterpret_cast<int*>(lds_raw + lay.misc);  // [0] list size, [1] band records, [4..] scan scratch
+  float4* list = reinterpret_cast<float4*>(lds_raw + lay.list);
+  uint32_t* keyrank = reinterpret_cast<uint32_t*>(lds_raw + lay.keyrank);
+  uint16_t* sorted = reinterpret_cast<uint16_t*>(lds_raw + lay.sorted);
 
-  const bool want_dv = p.dvalue != nullptr;
-  const bool want_dl = p.dloc != nullptr || p.dattn != nullptr;
-  const float fw = static_cast<float>(W), fh = static_cast<float>(L.h);
-  const int64_t qstride = static_cast<int64_t>(p.heads) * LP;                    // samples between queries
-  const int64_t srow0 = (static_cast<int64_t>(b) * Q * p.heads + h) * LP + l * P;  // sample (q=0, pt=0)
-  const float2* loc2 = reinterpret_cast<const float2*>(p.loc);
-  const bool gbf = p.gout_bf16 != 0;
-
-  // ---- phase 0
-  stage_copy(sv, static_cast<const VT*>(p.value) + band_off, (rs1 - r0) * W * D, p.vec16);
   {
     const int na = rb * W * D;
     float4* a4 = reinterpret_cast<float4*>(acc);
     for (int i = t; i < (na >> 2); i += nt) a4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int i = (na & ~3) + t; i < na; i += nt) acc[i] = 0.0f;
     for (int i = t; i < ncell; i += nt) cnt[i] = 0;
+    if (t < 2) misc[t] = 0;
   }
 
-  const int lpq = 1 << p.lpq_shift;
-  const int j = t & (lpq - 1);
-  const bool lane_on = j * VEC < D;
-  const int c0 = lane_on ? j * VEC : 0;
-  const int ngroups = nt >> p.lpq_shift;
-  const int M = p.chunk_m;
-  constexpr int kSQ = 8;  // queries per thread per scan round
-  constexpr int kSP = 4;  // points per load batch in the scan
+  const int NR = Q * P;
+  const SampleRec* __restrict__ R = p.rec + (n * p.levels + l) * static_cast<int64_t>(NR);
+  // A record's cell (x0, y0) covers pixels x0..x0+1, y0..y0+1; in band cell coordinates
+  // (kx, ky) = (x0 + 1, y0 - r0 + 1) it touches the band iff 0 <= kx <= W and 0 <= ky <= rb.
+  auto band_key = [&](uint32_t cell, int& key) {
+    const int kx = static_cast<int16_t>(cell & 0xffffu) + 1;
+    const int ky = static_cast<int16_t>(cell >> 16) - r0 + 1;
+    key = ky * (W + 1) + kx;
+    return kx >= 0 && kx <= W && ky >= 0 && ky <= rb;
+  };
+  constexpr int U = 8;  // records loaded per thread before use
 
-  for (int qs = 0; qs < Q; qs += p.scan_seg) {
-    const int qe = min(Q, qs + p.scan_seg);
-    if (t == 0) misc[0] = 0;
-    __syncthreads();
-    // ---- phase 1: scan [qs, qe)
-    for (int qb = qs; qb < qe; qb += kSQ * nt) {
-      bool relq[kSQ];
+  // How many records touch the band: one segment if they fit the list, else segments of `cap`
+  // records (each record is listed at most once, so a segment never overflows).
+  __syncthreads();
+  {
+    int mine = 0;
+    for (int r = t; r < NR; r += U * nt) {
+      uint32_t cells[U];
 #pragma unroll
-      for (int k = 0; k < kSQ; ++k) relq[k] = false;
-      for (int pg = 0; pg < P; pg += kSP) {
-        float ys[kSQ][kSP];
+      for (int u = 0; u < U; ++u) cells[u] = (r + u * nt < NR) ? R[r + u * nt].cell : 0x80008000u;
 #pragma unroll
-        for (int k = 0; k < kSQ; ++k) {
-          const int q = qb + t + k * nt;
-#pragma unroll
-          for (int e = 0; e < kSP; ++e) {
-            const int pt = pg + e;
-            ys[k][e] = (q < qe && pt < P) ? p.loc[2 * (srow0 + static_cast<int64_t>(q) * qstride + pt) + 1] : -1.0e30f;
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < kSQ; ++k) {
-#pragma unroll
-          for (int e = 0; e < kSP; ++e) {
-            // rows [y0, y0+1] clipped into the level (NaN -> row 0) against the band
-            const float y0f = floorf(pixel_coord(ys[k][e], fh));
-            const float lo = fminf(fmaxf(y0f, 0.0f), fh - 1.0f);
-            const float hi = fminf(fmaxf(y0f + 1.0f, 0.0f), fh - 1.0f);
-            const bool valid = (qb + t + k * nt < qe) && (pg + e < P);
-            relq[k] = relq[k] || (valid && hi >= static_cast<float>(r0) && lo < static_cast<float>(r1));
-          }
-        }
+      for (int u = 0; u < U; ++u) {
+        int key;
+        mine += band_key(cells[u], key) ? 1 : 0;
       }
+    }
+    for (int o = 32; o > 0; o >>= 1) mine += __shfl_xor(mine, o, 64);
+    if (lane == 0 && mine) atomicAdd(&misc[1], mine);
+  }
+  __syncthreads();
+  const int seg = misc[1] <= p.cap ? NR : p.cap;
+  const int64_t grow0 = (static_cast<int64_t>(b) * Q * p.heads + h) * D;  // grad_output (b, q=0, h)
+  const int64_t gqstride = static_cast<int64_t>(p.heads) * D;
+  const int gpp = (D + 3) >> 2;  // channel groups of 4
+
+  for (int s_lo = 0; s_lo < NR; s_lo += seg) {
+    const int s_hi = min(NR, s_lo + seg);
+    // ---- list the segment's records that touch the band; rank within their cell
+    for (int r = s_lo + t; r < s_hi; r += U * nt) {
+      uint4 rr[U];
 #pragma unroll
-      for (int k = 0; k < kSQ; ++k) {
-        const uint64_t mask = __ballot(relq[k]);
+      for (int u = 0; u < U; ++u)
+        rr[u] = (r + u * nt < s_hi) ? *reinterpret_cast<const uint4*>(R + r + u * nt) : make_uint4(0x80008000u, 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        int key;
+        const bool rel = band_key(rr[u].x, key);
+        int rank = 0;
+        if (rel) rank = atomicAdd(&cnt[key], 1);
+        const uint64_t mask = __ballot(rel);
         int base = 0;
         if (lane == 0 && mask) base = atomicAdd(&misc[0], __popcll(mask));
         base = __shfl(base, 0, 64);
-        if (relq[k]) rel[base + __popcll(mask & ((uint64_t{1} << lane) - 1))] = static_cast<uint16_t>(qb + t + k * nt - qs);
+        if (rel) {
+          const int pos = base + __popcll(mask & ((uint64_t{1} << lane) - 1));
+          const int q = (r + u * nt) / P;
+          list[pos] = make_float4(__uint_as_float(rr[u].y), __uint_as_float(rr[u].z), __uint_as_float(rr[u].w), __int_as_float(q));
+          keyrank[pos] = static_cast<uint32_t>(key) | (static_cast<uint32_t>(rank) << 16);
+        }
       }
     }
     __syncthreads();
-    const int nrel = misc[0];
-
-    // ---- phase 2: chunks of listed queries
-    for (int m0 = 0; m0 < nrel; m0 += M) {
-      const int m = min(M, nrel - m0);
-      const int ns = m * P;
-      // a. stage grad_output rows (4 channels per item), locations and weights
-      {
-        const int gq = D >> 2;  // 4-channel items per row
-        if (p.g_vec4) {
-          for (int e = t; e < m * gq; e += nt) {
-            const int i = e / gq, part = e - i * gq;
-            const int q = qs + rel[m0 + i];
-            const int64_t go = ((static_cast<int64_t>(b) * Q + q) * p.heads + h) * D + part * 4;
-            float v[4];
-            load_any<4>(p.gout, go, gbf, v);
-            *reinterpret_cast<float4*>(cg + i * D + part * 4) = make_float4(v[0], v[1], v[2], v[3]);
+    const int nlist = misc[0];
+    // ---- cell offsets, then list indices in cell order
+    block_scan_counts(cnt, off, ncell, misc + 4);
+    for (int e = t; e < nlist; e += nt) {
+      const uint32_t kr = keyrank[e];
+      sorted[off[kr & 0xffffu] + (kr >> 16)] = static_cast<uint16_t>(e);
+    }
+    __syncthreads();
+    // ---- one lane per (cell, 4 channels): sum a * w_k * g over the cell's records, then add the
+    //      sums to the cell's 2x2 pixels; cells of one colour (x, y parity) never share a pixel.
+    for (int color = 0; color < 4; ++color) {
+      const int ox = color & 1, oy = color >> 1;
+      const int nu = (W + 2 - ox) >> 1;   // cells per row of this colour
+      const int nv = (rb + 2 - oy) >> 1;  // cell rows of this colour
+      for (int task = t; task < nu * nv * gpp; task += nt) {
+        const int cidx = task / gpp, grp = task - cidx * gpp;
+        const int v = cidx / nu, uu = cidx - v * nu;
+        const int kx = 2 * uu + ox, ky = 2 * v + oy;
+        const int key = ky * (W + 1) + kx;
+        const int ch0 = grp * 4;
+        const int nch = min(4, D - ch0);
+        float s[4][4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[k][e] = 0.0f;
+        const int ebeg = off[key], eend = off[key + 1];
+        for (int e0 = ebeg; e0 < eend; e0 += 4) {
+          float4 w[4], g[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (e0 + i < eend) {
+              w[i] = list[sorted[e0 + i]];
+              g[i] = load_g4(p, grow0 + static_cast<int64_t>(__float_as_int(w[i].w)) * gqstride + ch0, nch);
+            }
           }
-        } else {
-          for (int e = t; e < m * D; e += nt) {
-            const int i = e / D, ch = e - i * D;
-            const int q = qs + rel[m0 + i];
-            float v[1];
-            load_any<1>(p.gout, ((static_cast<int64_t>(b) * Q + q) * p.heads + h) * D + ch, gbf, v);
-            cg[e] = v[0];
-          }
-        }
-        for (int e = t; e < ns; e += nt) {
-          const int i = e / P, pt = e - i * P;
-          const int64_t si = srow0 + static_cast<int64_t>(qs + rel[m0 + i]) * qstride + pt;
-          cl[e] = loc2[si];
-          ca[e] = p.attn[si];
-        }
-      }
-      __syncthreads();
-      // b. owner gradients and cell buckets, one lane group per sample
-      for (int e = t >> p.lpq_shift; e < ns; e += ngroups) {
-        const int i = e / P, pt = e - i * P;
-        const float2 xy = cl[e];
-        const float a = ca[e];
-        const Bilinear c = bilinear(xy.x, xy.y, L.h, W);
-        const int yo = static_cast<int>(fminf(fmaxf(c.y0f, 0.0f), fh - 1.0f));
-        if (want_dl && yo >= r0 && yo < r1) {
-          // D_c = <g, v_c>; dA = sum_c w_c D_c; d out/d ix = gy (m10 D10 - m00 D00) + fy (m11 D11 - m01 D01), ...
-          float g[VEC], v[VEC];
-          load_vec<float, VEC>(cg + i * D + c0, g);
-          if (!lane_on) {
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) g[k] = 0.0f;
-          }
-          const VT* base = sv + c0;
-          const int bb = r0 * W;
-          float d00 = 0.0f, d10 = 0.0f, d01 = 0.0f, d11 = 0.0f;
-          load_vec<VT, VEC>(base + (c.i00 - bb) * D, v);
-#pragma unroll
-          for (int k = 0; k < VEC; ++k) d00 += g[k] * v[k];
-          load_vec<VT, VEC>(base + (c.i10 - bb) * D, v);
-#pragma unroll
-          for (int k = 0; k < VEC; ++k) d10 += g[k] * v[k];
-          load_vec<VT, VEC>(base + (c.i01 - bb) * D, v);
-#pragma unroll
-          for (int k = 0; k < VEC; ++k) d01 += g[k] * v[k];
-          load_vec<VT, VEC>(base + (c.i11 - bb) * D, v);
-#pragma unroll
-          for (int k = 0; k < VEC; ++k) d11 += g[k] * v[k];
-          d00 = group_sum(d00, lpq);
-          d10 = group_sum(d10, lpq);
-          d01 = group_sum(d01, lpq);
-          d11 = group_sum(d11, lpq);
-          if (j == 0) {
-            const float da = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
-            const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
-            const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
-            const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
-            const int64_t si = srow0 + static_cast<int64_t>(qs + rel[m0 + i]) * qstride + pt;
-            if (p.dattn) p.dattn[si] = da;
-            if (p.dloc) *reinterpret_cast<float2*>(p.dloc + 2 * si) = make_float2(a * fw * dx, a * fh * dy);
-          }
-        }
-        if (j == 0 && want_dv) {
-          // The sample's cell: its floor corner (x0, y0), or for non-finite weights its clipped
-          // first corner (the reference adds those weights at the clipped corner indices).
-          int cx, cy;
-          const bool finite = isfinite(c.w00) && isfinite(c.w10) && isfinite(c.w01) && isfinite(c.w11);
-          if (finite) {
-            cx = static_cast<int>(fminf(fmaxf(floorf(pixel_coord(xy.x, fw)), -2.0f), fw));
-            cy = static_cast<int>(fminf(fmaxf(c.y0f, -2.0f), fh));
-          } else {
-            cx = c.i00 % W;
-            cy = c.i00 / W;
-          }
-          const int kx = cx + 1, ky = cy - r0 + 1;  // cell coordinates inside the band's cell grid
-          const bool in = kx >= 0 && kx <= W && ky >= 0 && ky <= rb &&
-                          (c.w00 != 0.0f || c.w10 != 0.0f || c.w01 != 0.0f || c.w11 != 0.0f);
-          int key = -1;
-          if (in) {
-            key = ky * (W + 1) + kx;
-            srank[e] = atomicAdd(&cnt[key], 1);
-            swt[e] = make_float4(a * c.w00, a * c.w10, a * c.w01, a * c.w11);
-          }
-          skey[e] = key;
-        }
-      }
-      if (want_dv) {
-        __syncthreads();
-        // c. cell offsets (clears the counts for the next chunk)
-        block_scan_counts(cnt, off, ncell, misc + 4);
-        // d. samples into cell order (query slot and a * corner weights)
-        for (int e = t; e < ns; e += nt) {
-          const int key = skey[e];
-          if (key >= 0) {
-            const int pos = off[key] + srank[e];
-            rslot[pos] = e / P;
-            rw[pos] = swt[e];
-          }
-        }
-        __syncthreads();
-        // e. cell-major accumulation in four colour phases: one lane per (cell, 4 channels) sums
-        //    a * w_k * g over the cell's samples for its four corners in registers, then adds them
-        //    to the corner pixels. Cells of one colour (cell x and y parities) are at least two
-        //    cells apart, so their 2x2 pixel footprints are disjoint and no two lanes write the
-        //    same accumulator element.
-        const int gpp = (D + 3) >> 2;  // channel groups per cell
-        for (int color = 0; color < 4; ++color) {
-          const int ox = color & 1, oy = color >> 1;
-          const int nu = (W + 1 - ox + 1) >> 1;   // cells per row of this colour
-          const int nv = (rb + 1 - oy + 1) >> 1;  // cell rows of this colour
-          for (int task = t; task < nu * nv * gpp; task += nt) {
-            const int cidx = task / gpp, grp = task - cidx * gpp;
-            const int v = cidx / nu, u = cidx - v * nu;
-            const int kx = 2 * u + ox, ky = 2 * v + oy;
-            const int key = ky * (W + 1) + kx;
-            const int ch0 = grp * 4;
-            const int nch = min(4, D - ch0);
-            float s[4][4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) s[k][e] = 0.0f;
-            const int rbeg = off[key], rend = off[key + 1];
-            for (int r = rbeg; r < rend; ++r) {
-              const float4 w4 = rw[r];
-              const float* gr = cg + rslot[r] * D + ch0;
-              float g4[4];
-              if (nch == 4) {
-                const float4 gv = *reinterpret_cast<const float4*>(gr);
-                g4[0] = gv.x; g4[1] = gv.y; g4[2] = gv.z; g4[3] = gv.w;
-              } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) g4[e] = e < nch ? gr[e] : 0.0f;
-              }
+          for (int i = 0; i < 4; ++i) {
+            if (e0 + i < eend) {
+              const float w00 = w[i].x * (1.0f - w[i].z), w10 = w[i].y * (1.0f - w[i].z);
+              const float w01 = w[i].x * w[i].z, w11 = w[i].y * w[i].z;
+              const float ge[4] = {g[i].x, g[i].y, g[i].z, g[i].w};
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
-                s[0][e] += w4.x * g4[e];
-                s[1][e] += w4.y * g4[e];
-                s[2][e] += w4.z * g4[e];
-                s[3][e] += w4.w * g4[e];
-              }
-            }
-            if (rend > rbeg) {
-#pragma unroll
-              for (int k = 0; k < 4; ++k) {
-                // corner k of cell (kx, ky) is pixel (kx - 1 + (k & 1), ky - 1 + (k >> 1)) of the band
-                const int px = kx - 1 + (k & 1), py = ky - 1 + (k >> 1);
-                if (px >= 0 && px < W && py >= 0 && py < rb) {
-                  float* ap = acc + (py * W + px) * D + ch0;
-                  for (int e = 0; e < nch; ++e) ap[e] += s[k][e];
-                }
+                s[0][e] += w00 * ge[e];
+                s[1][e] += w10 * ge[e];
+                s[2][e] += w01 * ge[e];
+                s[3][e] += w11 * ge[e];
               }
             }
           }
-          __syncthreads();
+        }
+        if (eend > ebeg) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            // corner k of cell (kx, ky) is pixel (kx - 1 + (k & 1), ky - 1 + (k >> 1)) of the band
+            const int px = kx - 1 + (k & 1), py = ky - 1 + (k >> 1);
+            if (px >= 0 && px < W && py >= 0 && py < rb) {
+              float* ap = acc + (py * W + px) * D + ch0;
+              if (nch == 4 && (D & 3) == 0) {
+                float4 o = *reinterpret_cast<float4*>(ap);
+                o.x += s[k][0];
+                o.y += s[k][1];
+                o.z += s[k][2];
+                o.w += s[k][3];
+                *reinterpret_cast<float4*>(ap) = o;
+              } else {
+                for (int e = 0; e < nch; ++e) ap[e] += s[k][e];
+              }
+            }
+          }
         }
       }
       __syncthreads();
     }
+    if (t == 0) misc[0] = 0;
+    __syncthreads();
   }
 
-  // ---- phase 3
-  __syncthreads();
-  if (want_dv) {
-    VT* dst = static_cast<VT*>(p.dvalue) + band_off;
-    for (int i = t; i < rb * W * D; i += nt) {
-      if constexpr (std::is_same<VT, float>::value) dst[i] = acc[i];
-      else dst[i] = f32_to_bf16(acc[i]);
+  // ---- the band's grad_value rows, once, in the value dtype
+  VT* dst = static_cast<VT*>(p.dvalue) + (n * p.len_value + L.start + static_cast<int64_t>(r0) * W) * D;
+  const int na = rb * W * D;
+  if constexpr (std::is_same<VT, float>::value) {
+    if (p.vec16) {
+      for (int i = t; i < (na >> 2); i += nt) reinterpret_cast<float4*>(dst)[i] = reinterpret_cast<const float4*>(acc)[i];
+      for (int i = (na & ~3) + t; i < na; i += nt) dst[i] = acc[i];
+    } else {
+      for (int i = t; i < na; i += nt) dst[i] = acc[i];
     }
+  } else {
+    for (int i = t; i < na; i += nt) dst[i] = f32_to_bf16(acc[i]);
   }
 }
 

@@ -25,12 +25,14 @@ ERR_DEVICE = -4
 _I = ctypes.c_int
 _P = ctypes.c_void_p
 _I32P = ctypes.POINTER(ctypes.c_int32)
-_SHAPE_ARGS = [_I] * 6 + [_I32P, _I32P, ctypes.c_int64, _P]
+_I64 = ctypes.c_int64
+_DIMS = [_I] * 6 + [_I32P, _I32P, _I64]  # batch .. n_points, spatial_shapes, level_start_index, len_value
 SIGNATURES = {
     "msda_version": ([], ctypes.c_char_p),
     "msda_last_error": ([], ctypes.c_char_p),
-    "msda_fwd": ([_P, _I, _P, _P, _P, _I] + _SHAPE_ARGS, _I),
-    "msda_bwd": ([_P, _I, _P, _P, _P, _I, _P, _P, _P] + _SHAPE_ARGS, _I),
+    "msda_fwd": ([_P, _I, _P, _P, _P, _I] + _DIMS + [_P], _I),
+    "msda_bwd_workspace_size": (list(_DIMS), _I64),
+    "msda_bwd": ([_P, _I, _P, _P, _P, _I, _P, _P, _P] + _DIMS + [_P, _I64, _P], _I),
 }
 
 _lock = threading.Lock()

@@ -165,11 +165,19 @@ def ms_deform_attn_backward(value, spatial_shapes, sampling_locations, attention
     grad_attn = torch.empty(attn.shape, dtype=torch.float32, device=dev) if needs[2] else None
     arr, starts = _shape_arrays(shapes)
     lib = _native.lib()
+    dims = (batch, n_heads, head_dim, len_query, n_levels, n_points, arr, starts, value.shape[1])
+    workspace, ws_bytes = None, 0
+    if grad_value is not None:
+        ws_bytes = lib.msda_bwd_workspace_size(*dims)
+        if ws_bytes < 0:
+            _native.check(int(ws_bytes))
+        # scratch for the per-sample records (16 bytes each); torch's caching allocator serves it
+        workspace = torch.empty((max(1, ws_bytes // 16), 4), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         rc = lib.msda_bwd(
             _ptr(value), _VALUE_DTYPES[value.dtype], _ptr(loc), _ptr(attn), _ptr(grad_output),
             _VALUE_DTYPES[grad_output.dtype], _ptr(grad_value), _ptr(grad_loc), _ptr(grad_attn),
-            batch, n_heads, head_dim, len_query, n_levels, n_points, arr, starts, value.shape[1], _stream(dev),
+            *dims, _ptr(workspace), ws_bytes, _stream(dev),
         )
     _native.check(rc)
     return grad_value, grad_loc, grad_attn

@@ -35,7 +35,7 @@ def test_library_is_built():
 
 def test_library_exports_every_declared_function():
     declared = _declared_functions()
-    assert {"msda_fwd", "msda_bwd", "msda_version", "msda_last_error"} <= set(declared)
+    assert {"msda_fwd", "msda_bwd", "msda_bwd_workspace_size", "msda_version", "msda_last_error"} <= set(declared)
     lib = ctypes.CDLL(LIB_PATH)
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in include/msda.h but not exported"
@@ -75,14 +75,15 @@ def _fwd(**kw):
 def _bwd(**kw):
     args = dict(value=1 << 20, vdt=0, loc=1 << 20, attn=1 << 20, gout=1 << 20, gdt=0, dv=1 << 20, dl=1 << 20,
                 da=1 << 20, batch=1, heads=2, dim=16, queries=4, levels=1, points=2, shapes=_shapes([(4, 4)]),
-                starts=_starts([0]), len_value=16)
+                starts=_starts([0]), len_value=16, ws=1 << 20, ws_bytes=1 << 20)
     args.update(kw)
     lib = _native.lib()
     rc = lib.msda_bwd(
         ctypes.c_void_p(args["value"]), args["vdt"], ctypes.c_void_p(args["loc"]), ctypes.c_void_p(args["attn"]),
         ctypes.c_void_p(args["gout"]), args["gdt"], ctypes.c_void_p(args["dv"]), ctypes.c_void_p(args["dl"]),
         ctypes.c_void_p(args["da"]), args["batch"], args["heads"], args["dim"], args["queries"], args["levels"],
-        args["points"], args["shapes"], args["starts"], args["len_value"], None,
+        args["points"], args["shapes"], args["starts"], args["len_value"], ctypes.c_void_p(args["ws"]),
+        args["ws_bytes"], None,
     )
     return rc, lib.msda_last_error().decode()
 
@@ -116,6 +117,24 @@ def test_two_levels_level_start_index_checked():
     assert rc == _native.ERR_INVALID_ARGUMENT and "NULL" in msg  # shapes fine, then the NULL value
     rc, msg = _fwd(levels=2, shapes=_shapes(pairs), starts=_starts([0, 15]), len_value=20)
     assert rc == _native.ERR_INVALID_ARGUMENT and "level_start_index[1]" in msg
+
+
+def test_workspace_size():
+    """One 16-byte record per sample (batch * heads * levels * queries * points)."""
+    lib = _native.lib()
+    size = lib.msda_bwd_workspace_size(3, 2, 16, 5, 2, 4, _shapes([(4, 4), (2, 2)]), _starts([0, 16]), 20)
+    assert size == 3 * 2 * 2 * 5 * 4 * 16
+    assert lib.msda_bwd_workspace_size(1, 2, 16, 4, 1, 2, _shapes([(4, 4)]), _starts([3]), 16) == _native.ERR_INVALID_ARGUMENT
+
+
+def test_workspace_checked_when_grad_value_requested():
+    need = 1 * 2 * 1 * 4 * 2 * 16
+    rc, msg = _bwd(ws=0)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "workspace" in msg
+    rc, msg = _bwd(ws_bytes=need - 16)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "workspace" in msg
+    rc, msg = _bwd(ws=(1 << 20) + 8, ws_bytes=need)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "aligned" in msg
 
 
 def test_misaligned_locations_rejected():
