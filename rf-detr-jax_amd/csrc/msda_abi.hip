@@ -192,10 +192,10 @@ int launch_bwd_sample(const msda::SampleParams& p, int grid, int threads, int ld
   return check_launch("msda backward (per-sample pass)");
 }
 
-template <typename VT>
+template <typename VT, int CG>
 int launch_bwd_value(const msda::ValueParams& p, int grid, int threads, int lds, hipStream_t stream) {
   static std::atomic<int> granted[kMaxDevices];
-  auto k = msda::bwd_value_kernel<VT>;
+  auto k = msda::bwd_value_kernel<VT, CG>;
   int rc = allow_lds(k, lds, granted);
   if (rc != MSDA_OK) return rc;
   hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
@@ -396,8 +396,8 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   for (int l = 0; l < n_levels; ++l)
     if (s.h[l] > 32000 || s.w[l] > 32000)
       return fail(MSDA_ERR_UNSUPPORTED, "level %d (%d x %d) exceeds 32000 rows or columns", l, s.h[l], s.w[l]);
-  if (static_cast<int64_t>(len_query) * n_points > 0x7fffffff / 16)
-    return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_points too large");
+  if (static_cast<int64_t>(len_query) * n_points > 0x7fffffff / 16 || static_cast<int64_t>(len_query) * n_heads * head_dim > 0x7fffffff)
+    return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_points or len_query * n_heads * head_dim too large");
   const int vec = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 8), {{value, vbytes}, {grad_output, gbytes}});
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
@@ -427,7 +427,8 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     // cell tables, record list) fits the budget; the list holds as many records as fit.
     const int64_t N = static_cast<int64_t>(batch) * n_heads;
     const int target = env_int("MSDA_BWD_TARGET_WGS", 2 * dev.cus);
-    const int budget = std::min(dev.lds_bytes, env_int("MSDA_BWD_LDS_BUDGET", dev.lds_bytes / 2));
+    // half a CU's LDS (less allocation-granularity slack) keeps two workgroups per CU
+    const int budget = std::min(dev.lds_bytes, env_int("MSDA_BWD_LDS_BUDGET", dev.lds_bytes / 2 - 1024));
     const int64_t want_items = std::max<int64_t>(1, (target + N - 1) / N);
     int64_t total_area = 0;
     for (int l = 0; l < n_levels; ++l) total_area += static_cast<int64_t>(s.h[l]) * s.w[l];
@@ -443,13 +444,13 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
       nb = std::min(s.h[l], std::max(1, nb));
       int rb = (s.h[l] + nb - 1) / nb;
       // shrink the band until the accumulator and cell tables leave room for a list of >= 256
-      // 22 bytes of LDS per listed record (16 list + 4 key/rank + 2 order), 32 of alignment slack
+      // 16 bytes of LDS per listed record, 32 of alignment slack
       auto fixed = [&](int r) { return msda::value_layout(r, s.w[l], head_dim, 0).total + 32; };
-      while (rb > 1 && (budget - fixed(rb)) / 22 < std::min(256, cap_want)) --rb;
-      if ((rb + 1) * (s.w[l] + 1) > 65535 || (dev.lds_bytes - fixed(rb)) / 22 < std::min(256, cap_want))
+      while (rb > 1 && (budget - fixed(rb)) / 16 < std::min(256, cap_want)) --rb;
+      if ((rb + 1) * (s.w[l] + 1) > 65535 || (dev.lds_bytes - fixed(rb)) / 16 < std::min(256, cap_want))
         return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], head_dim);
       rbs[l] = rb;
-      const int room = (std::max(budget, fixed(rb) + 22 * std::min(256, cap_want)) - fixed(rb)) / 22;
+      const int room = (std::max(budget, fixed(rb) + 16 * std::min(256, cap_want)) - fixed(rb)) / 16;
       cap = std::min(cap, room);
     }
     cap = std::max(1, cap);
@@ -466,7 +467,7 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
     vgrid = static_cast<int>(grid);
     vlds = lds_max;
-    vthreads = std::max(64, std::min(msda::kValueMaxThreads, (env_int("MSDA_BWD_VALUE_THREADS", 256) / 64) * 64));
+    vthreads = std::max(64, std::min(msda::kValueMaxThreads, (env_int("MSDA_BWD_VALUE_THREADS", 512) / 64) * 64));
   }
 
   // ---- per-sample pass: grad_attention_weights, grad_sampling_locations, grad_value records
@@ -494,8 +495,8 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     if (rc != MSDA_OK) return rc;
   }
   if (!want_dv) return MSDA_OK;
-  if (value_dtype == MSDA_DTYPE_BF16) return launch_bwd_value<msda::bf16_t>(vp, vgrid, vthreads, vlds, st);
-  return launch_bwd_value<float>(vp, vgrid, vthreads, vlds, st);
+  if (value_dtype == MSDA_DTYPE_BF16) return launch_bwd_value<msda::bf16_t, 4>(vp, vgrid, vthreads, vlds, st);
+  return launch_bwd_value<float, 4>(vp, vgrid, vthreads, vlds, st);
 }
 
 }  // extern "C"

@@ -17,8 +17,8 @@
 //    grad_sampling_locations, and a 16-byte record (floor cell, a*(1-fx), a*fx, fy) is written to
 //    a workspace in slice-major order [b*H+h][l][q][p], which grad_value reads contiguously.
 //  * bwd_value_kernel — one workgroup per (slice, level, band of rows). It reads its slice's
-//    records, lists those whose cell touches the band, counting-sorts them by cell in LDS (integer
-//    LDS atomics give each record its rank), and has one lane per (cell, 4 channels) sum
+//    records, counting-sorts those whose cell touches the band by cell into LDS (integer LDS
+//    atomics count and rank them), and has one lane per (cell, 4 channels) sum
 //    a * w_k * g over the cell's records in registers, grad_output rows being gathered from global
 //    memory. The sums are added to an f32 band accumulator in four colour classes of cells (x and
 //    y parity) whose 2x2 pixel footprints are disjoint, so no two lanes write one element and no
@@ -40,7 +40,9 @@ namespace msda {
 constexpr int kMaxLevels = 16;
 constexpr int kXcds = 8;               // MI355X: 8 accelerator complex dies, workgroups dispatched round-robin
 constexpr int kSampleMaxThreads = 512;  // forward and per-sample backward workgroups
-constexpr int kValueMaxThreads = 512;   // grad_value workgroups
+constexpr int kValueMaxThreads = 1024;  // grad_value workgroups
+constexpr int kGatherBatch = 8;         // grad_output rows fetched together per lane in the grad_value gather
+constexpr int kGatherSlots = 1;         // (cell, channel group) tasks a lane carries through one round (1 or 2)
 constexpr int kPassBatch = 4;           // samples whose loads are issued together (software-pipelined)
 
 using bf16_t = uint16_t;
@@ -106,7 +108,7 @@ struct ValueParams {
 // LDS carve-up of one grad_value workgroup; shared by the host planner and the kernel. Every
 // region starts on a 16-byte boundary.
 struct ValueLayout {
-  int acc, cnt, off, misc, list, keyrank, sorted, total;
+  int acc, cnt, off, misc, nonempty, list, total;
 };
 
 __host__ __device__ inline int align16i(int x) { return (x + 15) & ~15; }
@@ -115,13 +117,12 @@ __host__ __device__ inline ValueLayout value_layout(int band_rows, int w, int di
   ValueLayout L;
   const int ncell = (band_rows + 1) * (w + 1);
   int o = 0;
-  L.acc = o;     o += align16i(band_rows * w * dim * 4);
-  L.cnt = o;     o += align16i((ncell + 1) * 4);
-  L.off = o;     o += align16i((ncell + 1) * 4);
-  L.misc = o;    o += 64;
-  L.list = o;    o += cap * 16;
-  L.keyrank = o; o += align16i(cap * 4);
-  L.sorted = o;  o += align16i(cap * 2);
+  L.acc = o;      o += align16i(band_rows * w * dim * 4);
+  L.cnt = o;      o += align16i((ncell + 1) * 4);
+  L.off = o;      o += align16i((ncell + 1) * 4);
+  L.misc = o;     o += 128;  // 4 counters + one scan slot per wave (<= 16 waves) + spare
+  L.nonempty = o; o += align16i(ncell * 2);
+  L.list = o;     o += cap * 16;
   L.total = o;
   return L;
 }
@@ -677,28 +678,42 @@ __device__ __forceinline__ void block_scan_counts(int* cnt, int* off, int n, int
   __syncthreads();
 }
 
-// 4 channels of grad_output row `row` starting at channel ch0 (nch of them valid).
-__device__ __forceinline__ float4 load_g4(const ValueParams& p, int64_t off, int nch) {
-  if (nch == 4 && p.g_vec4) {
-    if (p.gout_bf16) {
-      const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const bf16_t*>(p.gout) + off);
-      return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
-                         __uint_as_float(r.y & 0xffff0000u));
-    }
-    return *reinterpret_cast<const float4*>(static_cast<const float*>(p.gout) + off);
-  }
-  float v[4];
+// CG channels of a grad_output row: `base` is the (b, q=0, h) row of this workgroup's slice and
+// `off` a 32-bit element offset from it (nch channels valid; the rest read as 0).
+template <int CG>
+__device__ __forceinline__ void load_gc(const void* __restrict__ base, bool bf16, bool vec4, int off, int nch, float (&o)[CG]) {
+  if (nch == CG && vec4) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float x[1] = {0.0f};
-    if (e < nch) load_any<1>(p.gout, off + e, p.gout_bf16 != 0, x);
-    v[e] = x[0];
+    for (int k = 0; k < CG; k += 4) {
+      if (bf16) {
+        const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const bf16_t*>(base) + off + k);
+        o[k] = __uint_as_float(r.x << 16);
+        o[k + 1] = __uint_as_float(r.x & 0xffff0000u);
+        o[k + 2] = __uint_as_float(r.y << 16);
+        o[k + 3] = __uint_as_float(r.y & 0xffff0000u);
+      } else {
+        const float4 r = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + off + k);
+        o[k] = r.x;
+        o[k + 1] = r.y;
+        o[k + 2] = r.z;
+        o[k + 3] = r.w;
+      }
+    }
+    return;
   }
-  return make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+  for (int e = 0; e < CG; ++e) {
+    float x[1] = {0.0f};
+    if (e < nch) load_any<1>(base, off + e, bf16, x);
+    o[e] = x[0];
+  }
 }
 
-template <typename VT>
-__global__ void __launch_bounds__(kValueMaxThreads) bwd_value_kernel(const ValueParams p) {
+// CG: channels per gather lane (4). Four waves per SIMD (<= 128 VGPRs) let two 512-thread
+// workgroups share a CU.
+template <typename VT, int CG>
+__global__ void __launch_bounds__(kValueMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
+bwd_value_kernel(const ValueParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
 
   const int lid = xcd_logical(blockIdx.x, gridDim.x);
@@ -724,10 +739,9 @@ __global__ void __launch_bounds__(kValueMaxThreads) bwd_value_kernel(const Value
   float* acc = reinterpret_cast<float*>(lds_raw + lay.acc);
   int* cnt = reinterpret_cast<int*>(lds_raw + lay.cnt);
   int* off = reinterpret_cast<int*>(lds_raw + lay.off);
-  int* misc = reinterpret_cast<int*>(lds_raw + lay.misc);  // [0] list size, [1] band records, [4..] scan scratch
-  float4* list = reinterpret_cast<float4*>(lds_raw + lay.list);
-  uint32_t* keyrank = reinterpret_cast<uint32_t*>(lds_raw + lay.keyrank);
-  uint16_t* sorted = reinterpret_cast<uint16_t*>(lds_raw + lay.sorted);
+  int* misc = reinterpret_cast<int*>(lds_raw + lay.misc);  // [0] segment's band records, [2] non-empty cells, [3] all band records, [4..] scan scratch
+  uint16_t* nonempty = reinterpret_cast<uint16_t*>(lds_raw + lay.nonempty);
+  float4* list = reinterpret_cast<float4*>(lds_raw + lay.list);  // segment's records, in cell order
 
   {
     const int na = rb * W * D;
@@ -735,7 +749,7 @@ __global__ void __launch_bounds__(kValueMaxThreads) bwd_value_kernel(const Value
     for (int i = t; i < (na >> 2); i += nt) a4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int i = (na & ~3) + t; i < na; i += nt) acc[i] = 0.0f;
     for (int i = t; i < ncell; i += nt) cnt[i] = 0;
-    if (t < 2) misc[t] = 0;
+    if (t < 4) misc[t] = 0;
   }
 
   const int NR = Q * P;
@@ -749,11 +763,20 @@ __global__ void __launch_bounds__(kValueMaxThreads) bwd_value_kernel(const Value
     return kx >= 0 && kx <= W && ky >= 0 && ky <= rb;
   };
   constexpr int U = 8;  // records loaded per thread before use
-
-  // How many records touch the band: one segment if they fit the list, else segments of `cap`
-  // records (each record is listed at most once, so a segment never overflows).
-  __syncthreads();
-  {
+  // grad_output row (b, q=0, h); row q is q * H * D elements further (fits 32 bits: checked on the host)
+  const int64_t grow0 = (static_cast<int64_t>(b) * Q * p.heads + h) * D;
+  const void* gbase = p.gout_bf16 ? static_cast<const void*>(static_cast<const bf16_t*>(p.gout) + grow0)
+                                  : static_cast<const void*>(static_cast<const float*>(p.gout) + grow0);
+  const bool gbf = p.gout_bf16 != 0, gv4 = p.g_vec4 != 0;
+  const int gqstride = p.heads * D;
+  const int gpp = (D + CG - 1) / CG;  // channel groups per cell
+  // All records form one segment when their band records fit the list (counted first when the
+  // record count alone does not settle it). Otherwise a segment is the longest run of record
+  // blocks that fits, counted block by block (a record counts at most once) and cut at the first
+  // block that might not fit.
+  __syncthreads();  // counters cleared
+  bool one_seg = NR <= p.cap;
+  if (!one_seg) {
     int mine = 0;
     for (int r = t; r < NR; r += U * nt) {
       uint32_t cells[U];
@@ -766,118 +789,180 @@ __global__ void __launch_bounds__(kValueMaxThreads) bwd_value_kernel(const Value
       }
     }
     for (int o = 32; o > 0; o >>= 1) mine += __shfl_xor(mine, o, 64);
-    if (lane == 0 && mine) atomicAdd(&misc[1], mine);
+    if (lane == 0 && mine) atomicAdd(&misc[3], mine);
+    __syncthreads();
+    one_seg = misc[3] <= p.cap;
   }
-  __syncthreads();
-  const int seg = misc[1] <= p.cap ? NR : p.cap;
-  const int64_t grow0 = (static_cast<int64_t>(b) * Q * p.heads + h) * D;  // grad_output (b, q=0, h)
-  const int64_t gqstride = static_cast<int64_t>(p.heads) * D;
-  const int gpp = (D + 3) >> 2;  // channel groups of 4
+  const int blk = one_seg ? NR : min(U * nt, p.cap);
 
-  for (int s_lo = 0; s_lo < NR; s_lo += seg) {
-    const int s_hi = min(NR, s_lo + seg);
-    // ---- list the segment's records that touch the band; rank within their cell
+  for (int s_lo = 0; s_lo < NR;) {
+    int s_hi = s_lo;
+    // ---- pass A: per-cell counts of the segment's records that touch the band
+    while (s_hi < NR) {
+      __syncthreads();
+      const int counted = misc[0];
+      __syncthreads();  // every thread has read the total before any adds to it
+      if (!one_seg && counted + min(blk, NR - s_hi) > p.cap) break;
+      const int b_hi = min(NR, s_hi + blk);
+      int mine = 0;
+      for (int r = s_hi + t; r < b_hi; r += U * nt) {
+        uint32_t cells[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) cells[u] = (r + u * nt < b_hi) ? R[r + u * nt].cell : 0x80008000u;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          int key;
+          if (band_key(cells[u], key)) {
+            atomicAdd(&cnt[key], 1);
+            ++mine;
+          }
+        }
+      }
+      for (int o = 32; o > 0; o >>= 1) mine += __shfl_xor(mine, o, 64);
+      if (lane == 0 && mine) atomicAdd(&misc[0], mine);
+      s_hi = b_hi;
+    }
+    __syncthreads();
+    // ---- cell offsets (counts cleared: they become the placement cursors) and non-empty cells
+    block_scan_counts(cnt, off, ncell, misc + 4);
+    for (int k0 = 0; k0 < ncell; k0 += nt) {
+      const int key = k0 + t;
+      const bool busy = key < ncell && off[key + 1] > off[key];
+      const uint64_t mask = __ballot(busy);
+      int base = 0;
+      if (lane == 0 && mask) base = atomicAdd(&misc[2], __popcll(mask));
+      base = __shfl(base, 0, 64);
+      if (busy) nonempty[base + __popcll(mask & ((uint64_t{1} << lane) - 1))] = static_cast<uint16_t>(key);
+    }
+    // ---- pass B: each band record goes to its place in cell order
     for (int r = s_lo + t; r < s_hi; r += U * nt) {
       uint4 rr[U];
 #pragma unroll
       for (int u = 0; u < U; ++u)
         rr[u] = (r + u * nt < s_hi) ? *reinterpret_cast<const uint4*>(R + r + u * nt) : make_uint4(0x80008000u, 0, 0, 0);
+      int pos[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         int key;
-        const bool rel = band_key(rr[u].x, key);
-        int rank = 0;
-        if (rel) rank = atomicAdd(&cnt[key], 1);
-        const uint64_t mask = __ballot(rel);
-        int base = 0;
-        if (lane == 0 && mask) base = atomicAdd(&misc[0], __popcll(mask));
-        base = __shfl(base, 0, 64);
-        if (rel) {
-          const int pos = base + __popcll(mask & ((uint64_t{1} << lane) - 1));
-          const int q = (r + u * nt) / P;
-          list[pos] = make_float4(__uint_as_float(rr[u].y), __uint_as_float(rr[u].z), __uint_as_float(rr[u].w), __int_as_float(q));
-          keyrank[pos] = static_cast<uint32_t>(key) | (static_cast<uint32_t>(rank) << 16);
-        }
+        pos[u] = band_key(rr[u].x, key) ? off[key] + atomicAdd(&cnt[key], 1) : -1;
       }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (pos[u] >= 0 && pos[u] < p.cap)
+          list[pos[u]] = make_float4(__uint_as_float(rr[u].y), __uint_as_float(rr[u].z), __uint_as_float(rr[u].w),
+                                     __int_as_float((r + u * nt) / P));
     }
     __syncthreads();
-    const int nlist = misc[0];
-    // ---- cell offsets, then list indices in cell order
-    block_scan_counts(cnt, off, ncell, misc + 4);
-    for (int e = t; e < nlist; e += nt) {
-      const uint32_t kr = keyrank[e];
-      sorted[off[kr & 0xffffu] + (kr >> 16)] = static_cast<uint16_t>(e);
-    }
-    __syncthreads();
-    // ---- one lane per (cell, 4 channels): sum a * w_k * g over the cell's records, then add the
-    //      sums to the cell's 2x2 pixels; cells of one colour (x, y parity) never share a pixel.
-    for (int color = 0; color < 4; ++color) {
-      const int ox = color & 1, oy = color >> 1;
-      const int nu = (W + 2 - ox) >> 1;   // cells per row of this colour
-      const int nv = (rb + 2 - oy) >> 1;  // cell rows of this colour
-      for (int task = t; task < nu * nv * gpp; task += nt) {
-        const int cidx = task / gpp, grp = task - cidx * gpp;
-        const int v = cidx / nu, uu = cidx - v * nu;
-        const int kx = 2 * uu + ox, ky = 2 * v + oy;
-        const int key = ky * (W + 1) + kx;
-        const int ch0 = grp * 4;
-        const int nch = min(4, D - ch0);
-        float s[4][4];
+    const int ntask = misc[2] * gpp;
+    // ---- one lane per (non-empty cell, CG channels) task, kGatherSlots tasks per round: sum
+    //      a * w_k * g over the cell's records in registers, kGatherBatch grad_output rows in flight;
+    //      then add the sums to the cells' 2x2 pixels in four colour passes (cells of one x/y parity
+    //      never share a pixel).
+    for (int t0 = 0; t0 < ntask; t0 += kGatherSlots * nt) {
+      int kx[kGatherSlots], ky[kGatherSlots], ch0[kGatherSlots], nch[kGatherSlots], ebeg[kGatherSlots], elen[kGatherSlots];
+      float s[kGatherSlots][4][CG];
+#pragma unroll
+      for (int slot = 0; slot < kGatherSlots; ++slot) {
+        const int task = t0 + slot * nt + t;
+        kx[slot] = ky[slot] = ch0[slot] = nch[slot] = ebeg[slot] = elen[slot] = 0;
+        if (task < ntask) {
+          const int ci = task / gpp, grp = task - ci * gpp;
+          const int key = nonempty[ci];
+          ky[slot] = key / (W + 1);
+          kx[slot] = key - ky[slot] * (W + 1);
+          ch0[slot] = grp * CG;
+          nch[slot] = min(CG, D - ch0[slot]);
+          ebeg[slot] = off[key];
+          elen[slot] = off[key + 1] - ebeg[slot];
+        }
 #pragma unroll
         for (int k = 0; k < 4; ++k)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s[k][e] = 0.0f;
-        const int ebeg = off[key], eend = off[key + 1];
-        for (int e0 = ebeg; e0 < eend; e0 += 4) {
-          float4 w[4], g[4];
+          for (int e = 0; e < CG; ++e) s[slot][k][e] = 0.0f;
+      }
+      // The slots' records form one sequence, walked kGatherBatch at a time so that many
+      // grad_output rows are in flight per lane.
+      const int total = elen[0] + (kGatherSlots > 1 ? elen[kGatherSlots - 1] : 0);
+      for (int f0 = 0; f0 < total; f0 += kGatherBatch) {
+        float4 w[kGatherBatch];
+        float g[kGatherBatch][CG];
+        bool second[kGatherBatch];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (e0 + i < eend) {
-              w[i] = list[sorted[e0 + i]];
-              g[i] = load_g4(p, grow0 + static_cast<int64_t>(__float_as_int(w[i].w)) * gqstride + ch0, nch);
-            }
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (e0 + i < eend) {
-              const float w00 = w[i].x * (1.0f - w[i].z), w10 = w[i].y * (1.0f - w[i].z);
-              const float w01 = w[i].x * w[i].z, w11 = w[i].y * w[i].z;
-              const float ge[4] = {g[i].x, g[i].y, g[i].z, g[i].w};
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                s[0][e] += w00 * ge[e];
-                s[1][e] += w10 * ge[e];
-                s[2][e] += w01 * ge[e];
-                s[3][e] += w11 * ge[e];
-              }
-            }
+        for (int i = 0; i < kGatherBatch; ++i) {
+          const int f = f0 + i;
+          second[i] = f >= elen[0];
+          if (f < total) {
+            const int e = second[i] ? ebeg[kGatherSlots - 1] + (f - elen[0]) : ebeg[0] + f;
+            const int c0 = second[i] ? ch0[kGatherSlots - 1] : ch0[0];
+            const int nc = second[i] ? nch[kGatherSlots - 1] : nch[0];
+            w[i] = list[e];
+            // the query index is < Q by construction; the clamp only keeps a broken invariant in bounds
+            const int q = static_cast<int>(min(static_cast<unsigned>(__float_as_int(w[i].w)), static_cast<unsigned>(Q - 1)));
+            load_gc<CG>(gbase, gbf, gv4, q * gqstride + c0, nc, g[i]);
           }
         }
-        if (eend > ebeg) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            // corner k of cell (kx, ky) is pixel (kx - 1 + (k & 1), ky - 1 + (k >> 1)) of the band
-            const int px = kx - 1 + (k & 1), py = ky - 1 + (k >> 1);
-            if (px >= 0 && px < W && py >= 0 && py < rb) {
-              float* ap = acc + (py * W + px) * D + ch0;
-              if (nch == 4 && (D & 3) == 0) {
-                float4 o = *reinterpret_cast<float4*>(ap);
-                o.x += s[k][0];
-                o.y += s[k][1];
-                o.z += s[k][2];
-                o.w += s[k][3];
-                *reinterpret_cast<float4*>(ap) = o;
-              } else {
-                for (int e = 0; e < nch; ++e) ap[e] += s[k][e];
+        for (int i = 0; i < kGatherBatch; ++i) {
+          if (f0 + i < total) {
+            const float w00 = w[i].x * (1.0f - w[i].z), w10 = w[i].y * (1.0f - w[i].z);
+            const float w01 = w[i].x * w[i].z, w11 = w[i].y * w[i].z;
+            if (!second[i]) {
+#pragma unroll
+              for (int e = 0; e < CG; ++e) {
+                s[0][0][e] += w00 * g[i][e];
+                s[0][1][e] += w10 * g[i][e];
+                s[0][2][e] += w01 * g[i][e];
+                s[0][3][e] += w11 * g[i][e];
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < CG; ++e) {
+                s[kGatherSlots - 1][0][e] += w00 * g[i][e];
+                s[kGatherSlots - 1][1][e] += w10 * g[i][e];
+                s[kGatherSlots - 1][2][e] += w01 * g[i][e];
+                s[kGatherSlots - 1][3][e] += w11 * g[i][e];
               }
             }
           }
         }
       }
-      __syncthreads();
+      for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int slot = 0; slot < kGatherSlots; ++slot) {
+          if (t0 + slot * nt + t < ntask && ((kx[slot] & 1) | ((ky[slot] & 1) << 1)) == c) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              // corner k of cell (kx, ky) is pixel (kx - 1 + (k & 1), ky - 1 + (k >> 1)) of the band
+              const int px = kx[slot] - 1 + (k & 1), py = ky[slot] - 1 + (k >> 1);
+              if (px >= 0 && px < W && py >= 0 && py < rb) {
+                float* ap = acc + (py * W + px) * D + ch0[slot];
+                if (nch[slot] == CG && (D & 3) == 0) {
+#pragma unroll
+                  for (int e = 0; e < CG; e += 4) {
+                    float4 o = *reinterpret_cast<float4*>(ap + e);
+                    o.x += s[slot][k][e];
+                    o.y += s[slot][k][e + 1];
+                    o.z += s[slot][k][e + 2];
+                    o.w += s[slot][k][e + 3];
+                    *reinterpret_cast<float4*>(ap + e) = o;
+                  }
+                } else {
+                  for (int e = 0; e < nch[slot]; ++e) ap[e] += s[slot][k][e];
+                }
+              }
+            }
+          }
+        }
+        __syncthreads();
+      }
     }
-    if (t == 0) misc[0] = 0;
-    __syncthreads();
+    // the placement cursors start the next segment at zero
+    for (int i = t; i < ncell; i += nt) cnt[i] = 0;
+    if (t == 0) {
+      misc[0] = 0;
+      misc[2] = 0;
+    }
+    s_lo = s_hi;
   }
 
   // ---- the band's grad_value rows, once, in the value dtype
