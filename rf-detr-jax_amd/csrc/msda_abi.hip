@@ -215,6 +215,20 @@ int dispatch_sample(bool backward, int vec, const msda::SampleParams& p, int gri
   return fail(MSDA_ERR_UNSUPPORTED, "no kernel for %d channels per lane", vec);
 }
 
+msda::LevelDesc level_desc(const Shape& s, int l, int lds, int band_rows, int band_first) {
+  msda::LevelDesc d{};
+  d.h = s.h[l];
+  d.w = s.w[l];
+  d.fh = static_cast<float>(s.h[l]);
+  d.fw = static_cast<float>(s.w[l]);
+  d.small = static_cast<int64_t>(s.h[l]) * s.w[l] * s.dim < (int64_t{1} << 24) ? 1 : 0;
+  d.start = static_cast<int>(s.start[l]);
+  d.lds = lds;
+  d.band_rows = band_rows;
+  d.band_first = band_first;
+  return d;
+}
+
 // ------------------------------------------------------------------------------------------
 // planning of the per-sample kernels (forward and the backward's per-sample pass)
 
@@ -230,7 +244,7 @@ struct SamplePlan {
 // one and four). Then one resident wave of workgroups: fewer, longer workgroups amortise the
 // value staging.
 int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* prefix, int shift, msda::SampleParams* p,
-                SamplePlan* out) {
+                SamplePlan* out, int forced_qblock = 0, int extra_lds = 0) {
   auto knob = [&](const char* name, int dflt) {
     std::string key = std::string(prefix) + name;
     return env_int(key.c_str(), dflt);
@@ -240,7 +254,7 @@ int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* pref
   bool all_staged = true;
   for (int l = 0; l < s.levels; ++l) {
     const int64_t bytes = static_cast<int64_t>(s.h[l]) * s.w[l] * s.dim * vbytes;
-    p->lv[l] = msda::LevelDesc{s.h[l], s.w[l], static_cast<int>(s.start[l]), -1, 0, 0};
+    p->lv[l] = level_desc(s, l, -1, 0, 0);
     if (static_cast<int64_t>(head_lds) * vbytes + bytes <= budget) {
       p->lv[l].lds = head_lds;
       head_lds += static_cast<int>(bytes / vbytes);
@@ -272,15 +286,20 @@ int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* pref
   const int64_t units = static_cast<int64_t>(s.batch) * (s.heads / hg);
   const int target = knob("_TARGET_WGS", dev.cus * std::min(per_cu, 8));
   const int max_blocks = std::max(1, (s.queries + qpp - 1) / qpp);
-  const int nqb = static_cast<int>(std::min<int64_t>(max_blocks, std::max<int64_t>(1, (target + units - 1) / units)));
-  const int per = (s.queries + nqb - 1) / nqb;
-  p->qblock = std::max(qpp, ((per + qpp - 1) / qpp) * qpp);
+  if (forced_qblock > 0) {
+    p->qblock = forced_qblock;  // the grad_value bins fix the query blocks
+  } else {
+    const int nqb = static_cast<int>(std::min<int64_t>(max_blocks, std::max<int64_t>(1, (target + units - 1) / units)));
+    const int per = (s.queries + nqb - 1) / nqb;
+    p->qblock = std::max(qpp, ((per + qpp - 1) / qpp) * qpp);
+  }
   p->nqb = std::max(1, (s.queries + p->qblock - 1) / p->qblock);
   const int64_t grid = units * p->nqb;
   if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "grid too large");
   out->grid = static_cast<int>(grid);
   out->threads = threads;
-  out->lds = lds;
+  out->lds = align16(lds) + extra_lds;
+  if (out->lds > dev.lds_bytes) return fail(MSDA_ERR_UNSUPPORTED, "per-sample pass needs %d bytes of LDS", out->lds);
   return MSDA_OK;
 }
 
@@ -296,8 +315,68 @@ bool rows_16b(const Shape& s, int vbytes, const void* a, const void* b) {
 }
 
 
-int64_t workspace_bytes_for(const Shape& s) {
-  return static_cast<int64_t>(s.batch) * s.heads * s.levels * s.queries * s.points * static_cast<int64_t>(sizeof(msda::SampleRec));
+// Geometry of the grad_value pass and of the records that feed it; depends on the shape and the
+// device only, so the workspace size can be queried before the tensors exist.
+struct BinPlan {
+  int qblock, nqb;  // query blocks of the per-sample pass (records are binned per block)
+  int nwork;        // (level, band) items per slice
+  int rb[msda::kMaxLevels];
+  int cap;          // records listed per grad_value segment
+  int lds;          // grad_value workgroup LDS
+  int64_t bins_bytes, counts_bytes, total_bytes;
+};
+
+int plan_bins(const Shape& s, const DevInfo& dev, BinPlan* bp) {
+  const int64_t N = static_cast<int64_t>(s.batch) * s.heads;
+  // query blocks: about two workgroups of the per-sample pass per CU with two-head groups, and
+  // offsets inside a block fit 16 bits
+  const int64_t units = std::max<int64_t>(1, N / 2);
+  int nqb = static_cast<int>(std::max<int64_t>(1, (env_int("MSDA_BWDS_TARGET_WGS", 2 * dev.cus) + units - 1) / units));
+  nqb = std::max(nqb, (s.queries + 65534) / 65535);
+  nqb = std::max(1, std::min(nqb, std::max(1, s.queries)));
+  bp->qblock = std::max(1, (s.queries + nqb - 1) / nqb);
+  bp->nqb = std::max(1, (s.queries + bp->qblock - 1) / bp->qblock);
+  // Bands of image rows: each (slice, level, band) workgroup owns the band's grad_value rows.
+  // Rows per band are chosen so the grid reaches the target and the LDS layout (accumulator,
+  // cell tables, record list) fits the budget; the list holds as many records as fit.
+  const int target = env_int("MSDA_BWD_TARGET_WGS", 2 * dev.cus);
+  // half a CU's LDS (less allocation-granularity slack) keeps two workgroups per CU
+  const int budget = std::min(dev.lds_bytes, env_int("MSDA_BWD_LDS_BUDGET", dev.lds_bytes / 2 - 1024));
+  const int64_t want_items = std::max<int64_t>(1, (target + N - 1) / std::max<int64_t>(1, N));
+  int64_t total_area = 0;
+  for (int l = 0; l < s.levels; ++l) total_area += static_cast<int64_t>(s.h[l]) * s.w[l];
+  const int records = std::max(1, s.queries * s.points);
+  const int cap_want = std::min({65535, records, std::max(256, env_int("MSDA_BWD_LIST", 65535))});
+  const int cap_min = std::min(256, cap_want);
+  int cap = cap_want;
+  for (int l = 0; l < s.levels; ++l) {
+    const int64_t area = static_cast<int64_t>(s.h[l]) * s.w[l];
+    int nb = static_cast<int>((want_items * area + total_area / 2) / total_area);
+    const int forced = env_int("MSDA_BWD_BANDS", 0);
+    if (forced > 0) nb = forced;
+    nb = std::min(s.h[l], std::max(1, nb));
+    int rb = (s.h[l] + nb - 1) / nb;
+    // 16 bytes of LDS per listed record, 32 of alignment slack; shrink the band until a list of
+    // cap_min records fits
+    auto fixed = [&](int r) { return msda::value_layout(r, s.w[l], s.dim, 0, bp->nqb).total + 32; };
+    while (rb > 1 && (budget - fixed(rb)) / 16 < cap_min) --rb;
+    if ((rb + 1) * (s.w[l] + 1) > 65535 || (dev.lds_bytes - fixed(rb)) / 16 < cap_min)
+      return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], s.dim);
+    bp->rb[l] = rb;
+    cap = std::min(cap, (std::max(budget, fixed(rb) + 16 * cap_min) - fixed(rb)) / 16);
+  }
+  bp->cap = std::max(1, cap);
+  bp->nwork = 0;
+  bp->lds = 0;
+  for (int l = 0; l < s.levels; ++l) {
+    bp->nwork += (s.h[l] + bp->rb[l] - 1) / bp->rb[l];
+    bp->lds = std::max(bp->lds, msda::value_layout(bp->rb[l], s.w[l], s.dim, bp->cap, bp->nqb).total);
+  }
+  const int64_t sub = static_cast<int64_t>(bp->qblock) * s.points;  // records per (slice, item, block) at most
+  bp->bins_bytes = N * bp->nwork * bp->nqb * sub * static_cast<int64_t>(sizeof(msda::SampleRec));
+  bp->counts_bytes = align16(N * bp->nwork * bp->nqb * 4);
+  bp->total_bytes = bp->bins_bytes + bp->counts_bytes;
+  return MSDA_OK;
 }
 
 }  // namespace
@@ -359,7 +438,12 @@ int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_qu
   Shape s;
   int rc = validate(&s, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value);
   if (rc != MSDA_OK) return rc;
-  return workspace_bytes_for(s);
+  if (batch == 0 || len_query == 0) return 0;
+  DevInfo dev;
+  if ((rc = device_info(&dev)) != MSDA_OK) return rc;
+  BinPlan bp;
+  if ((rc = plan_bins(s, dev, &bp)) != MSDA_OK) return rc;
+  return bp.total_bytes;
 }
 
 int msda_bwd(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
@@ -385,19 +469,16 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   const int gbytes = grad_output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   if (!aligned(value, vbytes) || !aligned(grad_value, vbytes) || !aligned(grad_output, gbytes))
     return fail(MSDA_ERR_INVALID_ARGUMENT, "value/grad_value/grad_output not aligned to their element size");
-  const int64_t need = workspace_bytes_for(s);
   const bool want_dv = grad_value != nullptr;
   if (want_dv && len_query > 0) {
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace of %lld bytes needed, got %lld", static_cast<long long>(need),
-                  static_cast<long long>(workspace == nullptr ? 0 : workspace_bytes));
+    if (workspace == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace is NULL (see msda_bwd_workspace_size)");
     if (!aligned(workspace, 16)) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   }
   for (int l = 0; l < n_levels; ++l)
     if (s.h[l] > 32000 || s.w[l] > 32000)
       return fail(MSDA_ERR_UNSUPPORTED, "level %d (%d x %d) exceeds 32000 rows or columns", l, s.h[l], s.w[l]);
-  if (static_cast<int64_t>(len_query) * n_points > 0x7fffffff / 16 || static_cast<int64_t>(len_query) * n_heads * head_dim > 0x7fffffff)
-    return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_points or len_query * n_heads * head_dim too large");
+  if (static_cast<int64_t>(len_query) * n_heads * head_dim > 0x7fffffff)
+    return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * head_dim exceeds 2^31");
   const int vec = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 8), {{value, vbytes}, {grad_output, gbytes}});
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
@@ -406,11 +487,48 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   if ((rc = device_info(&dev)) != MSDA_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  // ---- grad_value plan (checked before anything is launched)
+  // ---- grad_value plan (checked, with the workspace, before anything is launched)
+  BinPlan bp{};
   msda::ValueParams vp{};
-  int vgrid = 0, vthreads = 0, vlds = 0;
+  if (want_dv && len_query > 0) {
+    if ((rc = plan_bins(s, dev, &bp)) != MSDA_OK) return rc;
+    if (workspace_bytes < bp.total_bytes)
+      return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace of %lld bytes needed, got %lld", static_cast<long long>(bp.total_bytes),
+                  static_cast<long long>(workspace_bytes));
+    vp.bins = static_cast<const msda::SampleRec*>(workspace);
+    vp.bin_counts = reinterpret_cast<const int*>(static_cast<const char*>(workspace) + bp.bins_bytes);
+    vp.nqb = bp.nqb;
+    vp.qblock = bp.qblock;
+    vp.cap = bp.cap;
+    vp.nwork = bp.nwork;
+  } else if (want_dv) {
+    // no queries: grad_value is zero; one band per level and an empty record list
+    bp.nqb = 1;
+    bp.qblock = 1;
+    bp.cap = 1;
+    bp.nwork = 0;
+    bp.lds = 0;
+    for (int l = 0; l < n_levels; ++l) {
+      bp.rb[l] = 1;
+      while (bp.rb[l] < s.h[l] && msda::value_layout(bp.rb[l] + 1, s.w[l], head_dim, 1, 1).total <= dev.lds_bytes / 2) ++bp.rb[l];
+      if (msda::value_layout(bp.rb[l], s.w[l], head_dim, 1, 1).total > dev.lds_bytes)
+        return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], head_dim);
+      bp.nwork += (s.h[l] + bp.rb[l] - 1) / bp.rb[l];
+      bp.lds = std::max(bp.lds, msda::value_layout(bp.rb[l], s.w[l], head_dim, 1, 1).total);
+    }
+    vp.bins = nullptr;
+    vp.bin_counts = nullptr;
+    vp.nqb = 1;
+    vp.qblock = 1;
+    vp.cap = 1;
+    vp.nwork = bp.nwork;
+  }
+  int nwork_acc = 0;
   if (want_dv) {
-    vp.rec = static_cast<const msda::SampleRec*>(workspace);
+    for (int l = 0; l < n_levels; ++l) {
+      vp.lv[l] = level_desc(s, l, -1, bp.rb[l], nwork_acc);
+      nwork_acc += (s.h[l] + bp.rb[l] - 1) / bp.rb[l];
+    }
     vp.gout = grad_output;
     vp.gout_bf16 = grad_output_dtype == MSDA_DTYPE_BF16;
     vp.dvalue = grad_value;
@@ -422,52 +540,6 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     vp.len_value = len_value;
     vp.g_vec4 = (head_dim % 4 == 0) && aligned(grad_output, grad_output_dtype == MSDA_DTYPE_BF16 ? 8 : 16);
     vp.vec16 = rows_16b(s, vbytes, grad_value, nullptr);
-    // Bands of image rows: each (slice, level, band) workgroup owns the band's grad_value rows.
-    // Rows per band are chosen so the grid reaches the target and the LDS layout (accumulator,
-    // cell tables, record list) fits the budget; the list holds as many records as fit.
-    const int64_t N = static_cast<int64_t>(batch) * n_heads;
-    const int target = env_int("MSDA_BWD_TARGET_WGS", 2 * dev.cus);
-    // half a CU's LDS (less allocation-granularity slack) keeps two workgroups per CU
-    const int budget = std::min(dev.lds_bytes, env_int("MSDA_BWD_LDS_BUDGET", dev.lds_bytes / 2 - 1024));
-    const int64_t want_items = std::max<int64_t>(1, (target + N - 1) / N);
-    int64_t total_area = 0;
-    for (int l = 0; l < n_levels; ++l) total_area += static_cast<int64_t>(s.h[l]) * s.w[l];
-    const int records = std::max(1, len_query * n_points);
-    const int cap_want = std::min({65535, records, std::max(256, env_int("MSDA_BWD_LIST", 65535))});
-    int nwork = 0, cap = cap_want, lds_max = 0;
-    int rbs[msda::kMaxLevels];
-    for (int l = 0; l < n_levels; ++l) {
-      const int64_t area = static_cast<int64_t>(s.h[l]) * s.w[l];
-      int nb = static_cast<int>((want_items * area + total_area / 2) / total_area);
-      const int forced = env_int("MSDA_BWD_BANDS", 0);
-      if (forced > 0) nb = forced;
-      nb = std::min(s.h[l], std::max(1, nb));
-      int rb = (s.h[l] + nb - 1) / nb;
-      // shrink the band until the accumulator and cell tables leave room for a list of >= 256
-      // 16 bytes of LDS per listed record, 32 of alignment slack
-      auto fixed = [&](int r) { return msda::value_layout(r, s.w[l], head_dim, 0).total + 32; };
-      while (rb > 1 && (budget - fixed(rb)) / 16 < std::min(256, cap_want)) --rb;
-      if ((rb + 1) * (s.w[l] + 1) > 65535 || (dev.lds_bytes - fixed(rb)) / 16 < std::min(256, cap_want))
-        return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], head_dim);
-      rbs[l] = rb;
-      const int room = (std::max(budget, fixed(rb) + 16 * std::min(256, cap_want)) - fixed(rb)) / 16;
-      cap = std::min(cap, room);
-    }
-    cap = std::max(1, cap);
-    for (int l = 0; l < n_levels; ++l) {
-      const int rb = rbs[l];
-      const int nb = (s.h[l] + rb - 1) / rb;
-      vp.lv[l] = msda::LevelDesc{s.h[l], s.w[l], static_cast<int>(s.start[l]), -1, rb, nwork};
-      nwork += nb;
-      lds_max = std::max(lds_max, msda::value_layout(rb, s.w[l], head_dim, cap).total);
-    }
-    vp.nwork = nwork;
-    vp.cap = cap;
-    const int64_t grid = N * nwork;
-    if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
-    vgrid = static_cast<int>(grid);
-    vlds = lds_max;
-    vthreads = std::max(64, std::min(msda::kValueMaxThreads, (env_int("MSDA_BWD_VALUE_THREADS", 512) / 64) * 64));
   }
 
   // ---- per-sample pass: grad_attention_weights, grad_sampling_locations, grad_value records
@@ -480,7 +552,6 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     p.gout_bf16 = grad_output_dtype == MSDA_DTYPE_BF16;
     p.dloc = grad_sampling_locations;
     p.dattn = grad_attention_weights;
-    p.rec = want_dv ? static_cast<uint4*>(workspace) : nullptr;
     p.heads = n_heads;
     p.dim = head_dim;
     p.queries = len_query;
@@ -489,14 +560,29 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     p.len_value = len_value;
     p.vec16 = rows_16b(s, vbytes, value, nullptr);
     SamplePlan plan;
-    if ((rc = plan_sample(s, vbytes, dev, "MSDA_BWDS", shift, &p, &plan)) != MSDA_OK) return rc;
+    if ((rc = plan_sample(s, vbytes, dev, "MSDA_BWDS", shift, &p, &plan, want_dv ? bp.qblock : 0, 0)) != MSDA_OK) return rc;
+    if (want_dv) {
+      p.bins = static_cast<uint4*>(workspace);
+      p.bin_counts = reinterpret_cast<int*>(static_cast<char*>(workspace) + bp.bins_bytes);
+      p.nwork = bp.nwork;
+      for (int l = 0; l < n_levels; ++l) {
+        p.lv[l].band_rows = vp.lv[l].band_rows;
+        p.lv[l].band_first = vp.lv[l].band_first;
+      }
+      // per (head, item) record counters after the staged value rows
+      plan.lds = align16(plan.lds) + align16(static_cast<int64_t>(p.hg) * bp.nwork * 4);
+      if (plan.lds > dev.lds_bytes) return fail(MSDA_ERR_UNSUPPORTED, "per-sample pass needs %d bytes of LDS", plan.lds);
+    }
     rc = value_dtype == MSDA_DTYPE_BF16 ? dispatch_sample<msda::bf16_t>(true, vec, p, plan.grid, plan.threads, plan.lds, st)
                                         : dispatch_sample<float>(true, vec, p, plan.grid, plan.threads, plan.lds, st);
     if (rc != MSDA_OK) return rc;
   }
   if (!want_dv) return MSDA_OK;
-  if (value_dtype == MSDA_DTYPE_BF16) return launch_bwd_value<msda::bf16_t, 4>(vp, vgrid, vthreads, vlds, st);
-  return launch_bwd_value<float, 4>(vp, vgrid, vthreads, vlds, st);
+  const int64_t vgrid = static_cast<int64_t>(batch) * n_heads * vp.nwork;
+  if (vgrid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
+  const int vthreads = std::max(64, std::min(msda::kValueMaxThreads, (env_int("MSDA_BWD_VALUE_THREADS", 512) / 64) * 64));
+  if (value_dtype == MSDA_DTYPE_BF16) return launch_bwd_value<msda::bf16_t, 4>(vp, static_cast<int>(vgrid), vthreads, bp.lds, st);
+  return launch_bwd_value<float, 4>(vp, static_cast<int>(vgrid), vthreads, bp.lds, st);
 }
 
 }  // extern "C"

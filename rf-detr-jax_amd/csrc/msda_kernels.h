@@ -49,6 +49,8 @@ using bf16_t = uint16_t;
 
 struct LevelDesc {
   int h, w;        // level height and width
+  float fh, fw;    // the same, as floats
+  int small;       // h * w * dim < 2^24: corner offsets fit 24-bit multiplies
   int start;       // first position of the level in the value slice
   int lds;         // per-sample kernels: element offset of the staged level inside a head's LDS region, -1 = L2
   int band_rows;   // grad_value kernel: image rows per band
@@ -66,7 +68,9 @@ struct SampleParams {
   int gout_bf16;
   float* dloc;       // backward: grad_sampling_locations, or null
   float* dattn;      // backward: grad_attention_weights, or null
-  uint4* rec;        // backward: per-sample records for grad_value, or null
+  uint4* bins;       // backward: grad_value records, binned by (slice, level band), or null
+  int* bin_counts;   // backward: records per (slice, level band, query block)
+  int nwork;         // backward: (level, band) items per slice
   int heads, dim, queries, levels, points;
   int64_t len_value;
   int lpq_shift;   // log2(lanes per (query, head)); each lane owns VEC channels
@@ -79,20 +83,20 @@ struct SampleParams {
   LevelDesc lv[kMaxLevels];
 };
 
-// A sample's record for grad_value: the floor cell (x0, y0) packed as two int16 (for non-finite
-// weights, the clipped first corner), u = a * (1 - fx), v = a * fx, and fy, so that the corner
-// weights are u*(1-fy), v*(1-fy), u*fy, v*fy.
+// A sample's record for grad_value, one per (sample, band its bilinear cell touches), in the bin of
+// (slice, level band) and query block that produced it: `key` is the cell's index in the band's
+// cell grid ((ky * (W + 1) + kx) with kx = x0 + 1, ky = y0 - r0 + 1; for non-finite weights the
+// clipped first corner's cell), packed with the query's offset inside its query block; then
+// u = a * (1 - fx), v = a * fx and fy, so that the corner weights are u*(1-fy), v*(1-fy), u*fy, v*fy.
 struct __align__(16) SampleRec {
-  uint32_t cell;
+  uint32_t key_q;  // key | (query offset in block) << 16
   float u, v, fy;
 };
 
-__host__ __device__ inline uint32_t pack_cell(int x0, int y0) {
-  return (static_cast<uint32_t>(x0) & 0xffffu) | (static_cast<uint32_t>(y0) << 16);
-}
-
 struct ValueParams {
-  const SampleRec* rec;
+  const SampleRec* bins;   // [slice][item][query block][qblock * points]
+  const int* bin_counts;   // [slice][item][query block]
+  int nqb, qblock;         // query blocks of the per-sample pass, and their size
   const void* gout;
   int gout_bf16;
   void* dvalue;
@@ -108,12 +112,12 @@ struct ValueParams {
 // LDS carve-up of one grad_value workgroup; shared by the host planner and the kernel. Every
 // region starts on a 16-byte boundary.
 struct ValueLayout {
-  int acc, cnt, off, misc, nonempty, list, total;
+  int acc, cnt, off, misc, nonempty, binpre, list, total;
 };
 
 __host__ __device__ inline int align16i(int x) { return (x + 15) & ~15; }
 
-__host__ __device__ inline ValueLayout value_layout(int band_rows, int w, int dim, int cap) {
+__host__ __device__ inline ValueLayout value_layout(int band_rows, int w, int dim, int cap, int nqb) {
   ValueLayout L;
   const int ncell = (band_rows + 1) * (w + 1);
   int o = 0;
@@ -122,6 +126,7 @@ __host__ __device__ inline ValueLayout value_layout(int band_rows, int w, int di
   L.off = o;      o += align16i((ncell + 1) * 4);
   L.misc = o;     o += 128;  // 4 counters + one scan slot per wave (<= 16 waves) + spare
   L.nonempty = o; o += align16i(ncell * 2);
+  L.binpre = o;   o += align16i((nqb + 1) * 4);
   L.list = o;     o += cap * 16;
   L.total = o;
   return L;
@@ -157,26 +162,29 @@ __device__ __forceinline__ float pixel_coord(float loc, float size) {
 }
 
 struct Bilinear {
-  int i00, i10, i01, i11;      // clipped flat indices inside the level
+  int o00, o10, o01, o11;      // element offsets (clipped pixel index * dim) of the corners in the level
   float w00, w10, w01, w11;    // masked corner weights
   float m00, m10, m01, m11;    // in-bounds masks
   float fx, fy;                // fractional parts
   int x0, y0;                  // floor corner, clamped to [-2, size] (outside means all-masked)
+  int cx0, cy0;                // clipped floor corner
 };
 
-// ops.py:85-128 for one sample position.
-__device__ __forceinline__ Bilinear bilinear(float lx, float ly, int h, int w) {
+// ops.py:85-128 for one sample position. Offsets use 24-bit multiplies (full rate), valid while
+// a level's H*W*dim < 2^24 elements; larger levels take the 32-bit path.
+__device__ __forceinline__ Bilinear bilinear(float lx, float ly, const LevelDesc& L, int dim) {
   Bilinear c;
-  const float ix = pixel_coord(lx, static_cast<float>(w));
-  const float iy = pixel_coord(ly, static_cast<float>(h));
+  const int h = L.h, w = L.w;
+  const float ix = pixel_coord(lx, L.fw);
+  const float iy = pixel_coord(ly, L.fh);
   const float x0f = floorf(ix), y0f = floorf(iy);
   c.fx = ix - x0f;  // rounded in f32 like ops.py:88-89 (inexact only for ix in (-1, 0))
   c.fy = iy - y0f;
   const float gx = 1.0f - c.fx, gy = 1.0f - c.fy;
   // Clamp before the integer conversion so huge or NaN coordinates stay defined; the clamp does
   // not change any in-bounds decision (values below -1 or above size-1 are out of bounds anyway).
-  const int x0 = static_cast<int>(fminf(fmaxf(x0f, -2.0f), static_cast<float>(w)));
-  const int y0 = static_cast<int>(fminf(fmaxf(y0f, -2.0f), static_cast<float>(h)));
+  const int x0 = static_cast<int>(fminf(fmaxf(x0f, -2.0f), L.fw));
+  const int y0 = static_cast<int>(fminf(fmaxf(y0f, -2.0f), L.fh));
   const int x1 = x0 + 1, y1 = y0 + 1;
   const bool mx0 = static_cast<unsigned>(x0) < static_cast<unsigned>(w);
   const bool mx1 = static_cast<unsigned>(x1) < static_cast<unsigned>(w);
@@ -184,10 +192,18 @@ __device__ __forceinline__ Bilinear bilinear(float lx, float ly, int h, int w) {
   const bool my1 = static_cast<unsigned>(y1) < static_cast<unsigned>(h);
   const int cx0 = min(max(x0, 0), w - 1), cx1 = min(max(x1, 0), w - 1);
   const int cy0 = min(max(y0, 0), h - 1), cy1 = min(max(y1, 0), h - 1);
-  c.i00 = cy0 * w + cx0;
-  c.i10 = cy0 * w + cx1;
-  c.i01 = cy1 * w + cx0;
-  c.i11 = cy1 * w + cx1;
+  if (L.small) {
+    const int r0 = __umul24(cy0, w), r1 = __umul24(cy1, w);
+    c.o00 = __umul24(r0 + cx0, dim);
+    c.o10 = __umul24(r0 + cx1, dim);
+    c.o01 = __umul24(r1 + cx0, dim);
+    c.o11 = __umul24(r1 + cx1, dim);
+  } else {
+    c.o00 = (cy0 * w + cx0) * dim;
+    c.o10 = (cy0 * w + cx1) * dim;
+    c.o01 = (cy1 * w + cx0) * dim;
+    c.o11 = (cy1 * w + cx1) * dim;
+  }
   c.m00 = (mx0 && my0) ? 1.0f : 0.0f;
   c.m10 = (mx1 && my0) ? 1.0f : 0.0f;
   c.m01 = (mx0 && my1) ? 1.0f : 0.0f;
@@ -199,6 +215,8 @@ __device__ __forceinline__ Bilinear bilinear(float lx, float ly, int h, int w) {
   c.w11 = (c.fx * c.fy) * c.m11;
   c.x0 = x0;
   c.y0 = y0;
+  c.cx0 = cx0;
+  c.cy0 = cy0;
   return c;
 }
 
@@ -399,28 +417,29 @@ __device__ __forceinline__ void load_pass(PassIn& f, const float2* __restrict__ 
 // forward
 
 template <typename VT, int VEC, bool kLds>
-__device__ __forceinline__ void fwd_corners(float (&acc)[VEC], const VT* base, const Bilinear& c, int D, float a) {
+__device__ __forceinline__ void fwd_corners(float (&acc)[VEC], const VT* base, const Bilinear& c, float a) {
   const float a00 = a * c.w00, a10 = a * c.w10, a01 = a * c.w01, a11 = a * c.w11;
-  // Two corners in flight at a time keeps 16-channel lanes within the register budget.
+  // Two corners in flight at a time keeps 16-channel lanes within the register budget; one fused
+  // multiply-add per channel and corner.
   float u0[VEC], u1[VEC];
   if constexpr (kLds) {
-    load_vec_lds<VT, VEC>(base + c.i00 * D, u0);
-    load_vec_lds<VT, VEC>(base + c.i10 * D, u1);
+    load_vec_lds<VT, VEC>(base + c.o00, u0);
+    load_vec_lds<VT, VEC>(base + c.o10, u1);
   } else {
-    load_vec<VT, VEC>(base + c.i00 * D, u0);
-    load_vec<VT, VEC>(base + c.i10 * D, u1);
+    load_vec<VT, VEC>(base + c.o00, u0);
+    load_vec<VT, VEC>(base + c.o10, u1);
   }
 #pragma unroll
-  for (int k = 0; k < VEC; ++k) acc[k] += u0[k] * a00 + u1[k] * a10;
+  for (int k = 0; k < VEC; ++k) acc[k] = fmaf(u1[k], a10, fmaf(u0[k], a00, acc[k]));
   if constexpr (kLds) {
-    load_vec_lds<VT, VEC>(base + c.i01 * D, u0);
-    load_vec_lds<VT, VEC>(base + c.i11 * D, u1);
+    load_vec_lds<VT, VEC>(base + c.o01, u0);
+    load_vec_lds<VT, VEC>(base + c.o11, u1);
   } else {
-    load_vec<VT, VEC>(base + c.i01 * D, u0);
-    load_vec<VT, VEC>(base + c.i11 * D, u1);
+    load_vec<VT, VEC>(base + c.o01, u0);
+    load_vec<VT, VEC>(base + c.o11, u1);
   }
 #pragma unroll
-  for (int k = 0; k < VEC; ++k) acc[k] += u0[k] * a01 + u1[k] * a11;
+  for (int k = 0; k < VEC; ++k) acc[k] = fmaf(u1[k], a11, fmaf(u0[k], a01, acc[k]));
 }
 
 template <typename VT, int VEC>
@@ -431,10 +450,10 @@ __device__ __forceinline__ void fwd_pass(float (&acc)[VEC], const PassIn& f, int
   for (int u = 0; u < kPassBatch; ++u) {
     if (s0 + u < LP) {
       const LevelDesc L = p.lv[l];
-      const Bilinear c = bilinear(f.xy[u].x, f.xy[u].y, L.h, L.w);
+      const Bilinear c = bilinear(f.xy[u].x, f.xy[u].y, L, D);
       // Separate LDS and global paths: a pointer that may be either compiles to flat loads.
-      if (L.lds >= 0) fwd_corners<VT, VEC, true>(acc, hlds + L.lds, c, D, f.a[u]);
-      else fwd_corners<VT, VEC, false>(acc, vs + static_cast<int64_t>(L.start) * D, c, D, f.a[u]);
+      if (L.lds >= 0) fwd_corners<VT, VEC, true>(acc, hlds + L.lds, c, f.a[u]);
+      else fwd_corners<VT, VEC, false>(acc, vs + static_cast<int64_t>(L.start) * D, c, f.a[u]);
       if (++pt == p.points) {
         pt = 0;
         ++l;
@@ -497,54 +516,63 @@ __global__ void __launch_bounds__(kSampleMaxThreads) fwd_kernel(const SamplePara
 // backward, per sample: grad_attention_weights, grad_sampling_locations, grad_value records
 
 template <typename VT, int VEC, bool kLds>
-__device__ __forceinline__ void corner_dots(const VT* base, const Bilinear& c, int D, const float (&g)[VEC], float& d00,
+__device__ __forceinline__ void corner_dots(const VT* base, const Bilinear& c, const float (&g)[VEC], float& d00,
                                             float& d10, float& d01, float& d11) {
   float u0[VEC], u1[VEC];
   if constexpr (kLds) {
-    load_vec_lds<VT, VEC>(base + c.i00 * D, u0);
-    load_vec_lds<VT, VEC>(base + c.i10 * D, u1);
+    load_vec_lds<VT, VEC>(base + c.o00, u0);
+    load_vec_lds<VT, VEC>(base + c.o10, u1);
   } else {
-    load_vec<VT, VEC>(base + c.i00 * D, u0);
-    load_vec<VT, VEC>(base + c.i10 * D, u1);
+    load_vec<VT, VEC>(base + c.o00, u0);
+    load_vec<VT, VEC>(base + c.o10, u1);
   }
   d00 = 0.0f;
   d10 = 0.0f;
 #pragma unroll
   for (int k = 0; k < VEC; ++k) {
-    d00 += g[k] * u0[k];
-    d10 += g[k] * u1[k];
+    d00 = fmaf(g[k], u0[k], d00);
+    d10 = fmaf(g[k], u1[k], d10);
   }
   if constexpr (kLds) {
-    load_vec_lds<VT, VEC>(base + c.i01 * D, u0);
-    load_vec_lds<VT, VEC>(base + c.i11 * D, u1);
+    load_vec_lds<VT, VEC>(base + c.o01, u0);
+    load_vec_lds<VT, VEC>(base + c.o11, u1);
   } else {
-    load_vec<VT, VEC>(base + c.i01 * D, u0);
-    load_vec<VT, VEC>(base + c.i11 * D, u1);
+    load_vec<VT, VEC>(base + c.o01, u0);
+    load_vec<VT, VEC>(base + c.o11, u1);
   }
   d01 = 0.0f;
   d11 = 0.0f;
 #pragma unroll
   for (int k = 0; k < VEC; ++k) {
-    d01 += g[k] * u0[k];
-    d11 += g[k] * u1[k];
+    d01 = fmaf(g[k], u0[k], d01);
+    d11 = fmaf(g[k], u1[k], d11);
   }
+}
+
+// Appends a record to the bin of (slice n, item) for this workgroup's query block; the rank comes
+// from the workgroup's LDS counter of that (head, item).
+__device__ __forceinline__ void emit_record(const SampleParams& p, int* lcnt, int hl, int item, int key, int qoff, int64_t n,
+                                            int qb, uint4 payload) {
+  const int pos = atomicAdd(&lcnt[hl * p.nwork + item], 1);
+  payload.x = static_cast<uint32_t>(key) | (static_cast<uint32_t>(qoff) << 16);
+  p.bins[((n * p.nwork + item) * p.nqb + qb) * static_cast<int64_t>(p.qblock) * p.points + pos] = payload;
 }
 
 template <typename VT, int VEC>
 __device__ __forceinline__ void bwd_pass(const PassIn& f, const float (&g)[VEC], int s0, int LP, int& l, int& pt,
                                          const SampleParams& p, const SampleLane& ln, const VT* hlds,
-                                         const VT* __restrict__ vs, int64_t row, int64_t rec_row, int64_t rec_lstride) {
+                                         const VT* __restrict__ vs, int64_t row, int* lcnt, int qoff, int64_t n, int qb) {
   const int D = p.dim;
   const int lpq = 1 << p.lpq_shift;
 #pragma unroll
   for (int u = 0; u < kPassBatch; ++u) {
     if (s0 + u < LP) {
       const LevelDesc L = p.lv[l];
-      const Bilinear c = bilinear(f.xy[u].x, f.xy[u].y, L.h, L.w);
+      const Bilinear c = bilinear(f.xy[u].x, f.xy[u].y, L, D);
       const float a = f.a[u];
       float d00, d10, d01, d11;
-      if (L.lds >= 0) corner_dots<VT, VEC, true>(hlds + L.lds, c, D, g, d00, d10, d01, d11);
-      else corner_dots<VT, VEC, false>(vs + static_cast<int64_t>(L.start) * D, c, D, g, d00, d10, d01, d11);
+      if (L.lds >= 0) corner_dots<VT, VEC, true>(hlds + L.lds, c, g, d00, d10, d01, d11);
+      else corner_dots<VT, VEC, false>(vs + static_cast<int64_t>(L.start) * D, c, g, d00, d10, d01, d11);
       d00 = group_sum(d00, lpq);
       d10 = group_sum(d10, lpq);
       d01 = group_sum(d01, lpq);
@@ -559,15 +587,23 @@ __device__ __forceinline__ void bwd_pass(const PassIn& f, const float (&g)[VEC],
           const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
           // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
           *reinterpret_cast<float2*>(p.dloc + 2 * si) =
-              make_float2(a * static_cast<float>(L.w) * dx, a * static_cast<float>(L.h) * dy);
+              make_float2(a * L.fw * dx, a * L.fh * dy);
         }
-        if (p.rec) {
+        if (p.bins) {
           // Non-finite weights (NaN or infinite coordinates) go to the clipped first corner's cell,
           // where the reference's scatter-add puts them.
           const bool finite = isfinite(c.w00) && isfinite(c.w10) && isfinite(c.w01) && isfinite(c.w11);
-          const uint32_t cell = finite ? pack_cell(c.x0, c.y0) : pack_cell(c.i00 % L.w, c.i00 / L.w);
-          p.rec[rec_row + l * rec_lstride + pt] =
-              make_uint4(cell, __float_as_uint(a * (1.0f - c.fx)), __float_as_uint(a * c.fx), __float_as_uint(c.fy));
+          const int x0 = finite ? c.x0 : c.cx0, y0 = finite ? c.y0 : c.cy0;
+          const uint4 payload = make_uint4(0u, __float_as_uint(a * (1.0f - c.fx)), __float_as_uint(a * c.fx), __float_as_uint(c.fy));
+          // the cell's rows y0, y0 + 1 that lie in the level, and the band of each
+          if (x0 >= -1 && x0 <= L.w - 1) {
+            const int ya = y0 >= 0 && y0 < L.h ? y0 : -1;
+            const int yb = y0 + 1 >= 0 && y0 + 1 < L.h ? y0 + 1 : -1;
+            const int ba = ya >= 0 ? ya / L.band_rows : -1;
+            const int bb = yb >= 0 ? yb / L.band_rows : -1;
+            if (ba >= 0) emit_record(p, lcnt, ln.hl, L.band_first + ba, (y0 - ba * L.band_rows + 1) * (L.w + 1) + x0 + 1, qoff, n, qb, payload);
+            if (bb >= 0 && bb != ba) emit_record(p, lcnt, ln.hl, L.band_first + bb, (y0 - bb * L.band_rows + 1) * (L.w + 1) + x0 + 1, qoff, n, qb, payload);
+          }
         }
       }
       if (++pt == p.points) {
@@ -596,9 +632,11 @@ __global__ void __launch_bounds__(kSampleMaxThreads) bwd_sample_kernel(const Sam
   const float2* __restrict__ loc2 = reinterpret_cast<const float2*>(p.loc);
   const bool gbf = p.gout_bf16 != 0;
   auto row_of = [&](int q) { return (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h; };  // (b, q, h)
-  // records of slice n = b*H + h: [n][l][q][p]
-  const int64_t rec_lstride = static_cast<int64_t>(p.queries) * P;
-  const int64_t rec_slice = (static_cast<int64_t>(it.b) * p.heads + h) * p.levels * rec_lstride;
+  const int64_t n = static_cast<int64_t>(it.b) * p.heads + h;
+  // per (head, item) record counters of this workgroup, after the staged value rows
+  int* lcnt = reinterpret_cast<int*>(lds_raw + align16i(p.hg * p.head_lds * static_cast<int>(sizeof(VT))));
+  const int ncnt = p.bins ? p.hg * p.nwork : 0;
+  for (int i = threadIdx.x; i < ncnt; i += blockDim.x) lcnt[i] = 0;
 
   int q = q_lo + ln.qs;
   PassIn cur;
@@ -609,13 +647,11 @@ __global__ void __launch_bounds__(kSampleMaxThreads) bwd_sample_kernel(const Sam
   }
   stage_group(p, lds, vg);
   __syncthreads();
-  if (!ln.active) return;  // no barrier follows
 
   const VT* __restrict__ vs = vg + ln.hl * slice_elems + ln.c0;
   const VT* hlds = lds + ln.hl * p.head_lds + ln.c0;
-  for (; q < q_hi; q += ln.qpp) {
+  for (; ln.active && q < q_hi; q += ln.qpp) {
     const int64_t row = row_of(q);
-    const int64_t rec_row = rec_slice + static_cast<int64_t>(q) * P;
     int l = 0, pt = 0;
     if (pipelined) {
       PassIn nxt;
@@ -629,7 +665,7 @@ __global__ void __launch_bounds__(kSampleMaxThreads) bwd_sample_kernel(const Sam
 #pragma unroll
         for (int k = 0; k < VEC; ++k) gcur[k] = 0.0f;
       }
-      bwd_pass<VT, VEC>(cur, gcur, 0, LP, l, pt, p, ln, hlds, vs, row, rec_row, rec_lstride);
+      bwd_pass<VT, VEC>(cur, gcur, 0, LP, l, pt, p, ln, hlds, vs, row, lcnt, q - q_lo, n, it.qb);
       cur = nxt;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) gcur[k] = gnxt[k];
@@ -643,9 +679,17 @@ __global__ void __launch_bounds__(kSampleMaxThreads) bwd_sample_kernel(const Sam
       for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
         PassIn f;
         load_pass(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
-        bwd_pass<VT, VEC>(f, g, s0, LP, l, pt, p, ln, hlds, vs, row, rec_row, rec_lstride);
+        bwd_pass<VT, VEC>(f, g, s0, LP, l, pt, p, ln, hlds, vs, row, lcnt, q - q_lo, n, it.qb);
       }
     }
+  }
+  if (!p.bins) return;
+  // records per (slice, item) of this query block, for the grad_value pass
+  __syncthreads();
+  for (int i = threadIdx.x; i < ncnt; i += blockDim.x) {
+    const int hh = i / p.nwork, item = i - hh * p.nwork;
+    const int64_t nn = static_cast<int64_t>(it.b) * p.heads + it.h0 + hh;
+    p.bin_counts[(nn * p.nwork + item) * p.nqb + it.qb] = lcnt[i];
   }
 }
 
@@ -735,12 +779,13 @@ bwd_value_kernel(const ValueParams p) {
   const int64_t n = static_cast<int64_t>(b) * p.heads + h;
   const int nt = blockDim.x, t = threadIdx.x, lane = t & 63;
 
-  const ValueLayout lay = value_layout(L.band_rows, W, D, p.cap);
+  const ValueLayout lay = value_layout(L.band_rows, W, D, p.cap, p.nqb);
   float* acc = reinterpret_cast<float*>(lds_raw + lay.acc);
   int* cnt = reinterpret_cast<int*>(lds_raw + lay.cnt);
   int* off = reinterpret_cast<int*>(lds_raw + lay.off);
-  int* misc = reinterpret_cast<int*>(lds_raw + lay.misc);  // [0] segment's band records, [2] non-empty cells, [3] all band records, [4..] scan scratch
+  int* misc = reinterpret_cast<int*>(lds_raw + lay.misc);  // [2] non-empty cells, [4..] scan scratch
   uint16_t* nonempty = reinterpret_cast<uint16_t*>(lds_raw + lay.nonempty);
+  int* binpre = reinterpret_cast<int*>(lds_raw + lay.binpre);
   float4* list = reinterpret_cast<float4*>(lds_raw + lay.list);  // segment's records, in cell order
 
   {
@@ -752,16 +797,19 @@ bwd_value_kernel(const ValueParams p) {
     if (t < 4) misc[t] = 0;
   }
 
-  const int NR = Q * P;
-  const SampleRec* __restrict__ R = p.rec + (n * p.levels + l) * static_cast<int64_t>(NR);
-  // A record's cell (x0, y0) covers pixels x0..x0+1, y0..y0+1; in band cell coordinates
-  // (kx, ky) = (x0 + 1, y0 - r0 + 1) it touches the band iff 0 <= kx <= W and 0 <= ky <= rb.
-  auto band_key = [&](uint32_t cell, int& key) {
-    const int kx = static_cast<int16_t>(cell & 0xffffu) + 1;
-    const int ky = static_cast<int16_t>(cell >> 16) - r0 + 1;
-    key = ky * (W + 1) + kx;
-    return kx >= 0 && kx <= W && ky >= 0 && ky <= rb;
-  };
+  // This workgroup's records: the bins of (slice n, item wk), one per query block of the
+  // per-sample pass, with their counts; prefix sums of the counts in LDS.
+  const int64_t subcap = static_cast<int64_t>(p.qblock) * P;
+  const SampleRec* __restrict__ R = p.bins ? p.bins + (n * p.nwork + wk) * p.nqb * subcap : nullptr;
+  const int* __restrict__ C = p.bin_counts ? p.bin_counts + (n * p.nwork + wk) * p.nqb : nullptr;
+  if (t == 0) {
+    int run = 0;
+    for (int i = 0; i < p.nqb; ++i) {
+      binpre[i] = run;
+      run += p.bin_counts ? C[i] : 0;  // no bins without queries
+    }
+    binpre[p.nqb] = run;
+  }
   constexpr int U = 8;  // records loaded per thread before use
   // grad_output row (b, q=0, h); row q is q * H * D elements further (fits 32 bits: checked on the host)
   const int64_t grow0 = (static_cast<int64_t>(b) * Q * p.heads + h) * D;
@@ -770,57 +818,30 @@ bwd_value_kernel(const ValueParams p) {
   const bool gbf = p.gout_bf16 != 0, gv4 = p.g_vec4 != 0;
   const int gqstride = p.heads * D;
   const int gpp = (D + CG - 1) / CG;  // channel groups per cell
-  // All records form one segment when their band records fit the list (counted first when the
-  // record count alone does not settle it). Otherwise a segment is the longest run of record
-  // blocks that fits, counted block by block (a record counts at most once) and cut at the first
-  // block that might not fit.
-  __syncthreads();  // counters cleared
-  bool one_seg = NR <= p.cap;
-  if (!one_seg) {
-    int mine = 0;
-    for (int r = t; r < NR; r += U * nt) {
-      uint32_t cells[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) cells[u] = (r + u * nt < NR) ? R[r + u * nt].cell : 0x80008000u;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        int key;
-        mine += band_key(cells[u], key) ? 1 : 0;
-      }
-    }
-    for (int o = 32; o > 0; o >>= 1) mine += __shfl_xor(mine, o, 64);
-    if (lane == 0 && mine) atomicAdd(&misc[3], mine);
-    __syncthreads();
-    one_seg = misc[3] <= p.cap;
-  }
-  const int blk = one_seg ? NR : min(U * nt, p.cap);
+  __syncthreads();  // counters cleared, prefix ready
+  const int NR = binpre[p.nqb];
+  // Record f of the workgroup lives in bin `qb` with binpre[qb] <= f < binpre[qb + 1]; a thread's f
+  // only grows, so its bin index only moves forward.
+  auto record = [&](int f, int& qb) {
+    while (binpre[qb + 1] <= f) ++qb;
+    return *reinterpret_cast<const uint4*>(R + qb * subcap + (f - binpre[qb]));
+  };
+  const int ncell_max = ncell;
 
+  // Segments of at most `cap` records (a segment's records all fit the list).
   for (int s_lo = 0; s_lo < NR;) {
-    int s_hi = s_lo;
-    // ---- pass A: per-cell counts of the segment's records that touch the band
-    while (s_hi < NR) {
-      __syncthreads();
-      const int counted = misc[0];
-      __syncthreads();  // every thread has read the total before any adds to it
-      if (!one_seg && counted + min(blk, NR - s_hi) > p.cap) break;
-      const int b_hi = min(NR, s_hi + blk);
-      int mine = 0;
-      for (int r = s_hi + t; r < b_hi; r += U * nt) {
-        uint32_t cells[U];
+    const int s_hi = min(NR, s_lo + p.cap);
+    // ---- pass A: per-cell counts
+    {
+      int qb = 0;
+      for (int f = s_lo + t; f < s_hi; f += U * nt) {
+        uint32_t keys[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) cells[u] = (r + u * nt < b_hi) ? R[r + u * nt].cell : 0x80008000u;
+        for (int u = 0; u < U; ++u) keys[u] = (f + u * nt < s_hi) ? record(f + u * nt, qb).x & 0xffffu : 0xffffu;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          int key;
-          if (band_key(cells[u], key)) {
-            atomicAdd(&cnt[key], 1);
-            ++mine;
-          }
-        }
+        for (int u = 0; u < U; ++u)
+          if (static_cast<int>(keys[u]) < ncell_max) atomicAdd(&cnt[keys[u]], 1);
       }
-      for (int o = 32; o > 0; o >>= 1) mine += __shfl_xor(mine, o, 64);
-      if (lane == 0 && mine) atomicAdd(&misc[0], mine);
-      s_hi = b_hi;
     }
     __syncthreads();
     // ---- cell offsets (counts cleared: they become the placement cursors) and non-empty cells
@@ -834,23 +855,29 @@ bwd_value_kernel(const ValueParams p) {
       base = __shfl(base, 0, 64);
       if (busy) nonempty[base + __popcll(mask & ((uint64_t{1} << lane) - 1))] = static_cast<uint16_t>(key);
     }
-    // ---- pass B: each band record goes to its place in cell order
-    for (int r = s_lo + t; r < s_hi; r += U * nt) {
-      uint4 rr[U];
+    // ---- pass B: each record goes to its place in cell order
+    {
+      int qb = 0;
+      for (int f = s_lo + t; f < s_hi; f += U * nt) {
+        uint4 rr[U];
+        int qbs[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        rr[u] = (r + u * nt < s_hi) ? *reinterpret_cast<const uint4*>(R + r + u * nt) : make_uint4(0x80008000u, 0, 0, 0);
-      int pos[U];
+        for (int u = 0; u < U; ++u) {
+          rr[u] = (f + u * nt < s_hi) ? record(f + u * nt, qb) : make_uint4(0xffffu, 0, 0, 0);
+          qbs[u] = qb;
+        }
+        int pos[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        int key;
-        pos[u] = band_key(rr[u].x, key) ? off[key] + atomicAdd(&cnt[key], 1) : -1;
+        for (int u = 0; u < U; ++u) {
+          const int key = static_cast<int>(rr[u].x & 0xffffu);
+          pos[u] = key < ncell_max ? off[key] + atomicAdd(&cnt[key], 1) : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (pos[u] >= 0 && pos[u] < p.cap)
+            list[pos[u]] = make_float4(__uint_as_float(rr[u].y), __uint_as_float(rr[u].z), __uint_as_float(rr[u].w),
+                                       __int_as_float(qbs[u] * p.qblock + static_cast<int>(rr[u].x >> 16)));
       }
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (pos[u] >= 0 && pos[u] < p.cap)
-          list[pos[u]] = make_float4(__uint_as_float(rr[u].y), __uint_as_float(rr[u].z), __uint_as_float(rr[u].w),
-                                     __int_as_float((r + u * nt) / P));
     }
     __syncthreads();
     const int ntask = misc[2] * gpp;
@@ -958,10 +985,8 @@ bwd_value_kernel(const ValueParams p) {
     }
     // the placement cursors start the next segment at zero
     for (int i = t; i < ncell; i += nt) cnt[i] = 0;
-    if (t == 0) {
-      misc[0] = 0;
-      misc[2] = 0;
-    }
+    if (t == 0) misc[2] = 0;
+    __syncthreads();
     s_lo = s_hi;
   }
 
