@@ -192,10 +192,10 @@ int launch_bwd_sample(const msda::SampleParams& p, int grid, int threads, int ld
   return check_launch("msda backward (per-sample pass)");
 }
 
-template <typename VT, int CG>
+template <typename VT, int CG, int NACC>
 int launch_bwd_value(const msda::ValueParams& p, int grid, int threads, int lds, hipStream_t stream) {
   static std::atomic<int> granted[kMaxDevices];
-  auto k = msda::bwd_value_kernel<VT, CG>;
+  auto k = msda::bwd_value_kernel<VT, CG, NACC>;
   int rc = allow_lds(k, lds, granted);
   if (rc != MSDA_OK) return rc;
   hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
@@ -322,6 +322,7 @@ struct BinPlan {
   int nwork;        // (level, band) items per slice
   int rb[msda::kMaxLevels];
   int cap;          // records listed per grad_value segment
+  int nacc;         // grad_value accumulators: 4 (one per corner) or 1 (colour passes)
   int lds;          // grad_value workgroup LDS
   int64_t bins_bytes, counts_bytes, total_bytes;
 };
@@ -349,16 +350,26 @@ int plan_bins(const Shape& s, const DevInfo& dev, BinPlan* bp) {
   const int cap_want = std::min({65535, records, std::max(256, env_int("MSDA_BWD_LIST", 65535))});
   const int cap_min = std::min(256, cap_want);
   int cap = cap_want;
-  for (int l = 0; l < s.levels; ++l) {
+  auto target_rows = [&](int l) {
     const int64_t area = static_cast<int64_t>(s.h[l]) * s.w[l];
     int nb = static_cast<int>((want_items * area + total_area / 2) / total_area);
     const int forced = env_int("MSDA_BWD_BANDS", 0);
     if (forced > 0) nb = forced;
     nb = std::min(s.h[l], std::max(1, nb));
-    int rb = (s.h[l] + nb - 1) / nb;
+    return (s.h[l] + nb - 1) / nb;
+  };
+  // Four accumulators (no colour passes) when every level's target band fits with them and room
+  // for a sizeable list; otherwise one accumulator, so bands need not shrink.
+  bp->nacc = 4;
+  for (int l = 0; l < s.levels; ++l)
+    if (msda::value_layout(target_rows(l), s.w[l], s.dim, std::min(cap_want, 1024), bp->nqb, 4).total + 32 > budget) bp->nacc = 1;
+  const int forced_acc = env_int("MSDA_BWD_ACCUMULATORS", 0);
+  if (forced_acc == 1 || forced_acc == 4) bp->nacc = forced_acc;
+  for (int l = 0; l < s.levels; ++l) {
+    int rb = target_rows(l);
     // 16 bytes of LDS per listed record, 32 of alignment slack; shrink the band until a list of
     // cap_min records fits
-    auto fixed = [&](int r) { return msda::value_layout(r, s.w[l], s.dim, 0, bp->nqb).total + 32; };
+    auto fixed = [&](int r) { return msda::value_layout(r, s.w[l], s.dim, 0, bp->nqb, bp->nacc).total + 32; };
     while (rb > 1 && (budget - fixed(rb)) / 16 < cap_min) --rb;
     if ((rb + 1) * (s.w[l] + 1) > 65535 || (dev.lds_bytes - fixed(rb)) / 16 < cap_min)
       return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], s.dim);
@@ -370,7 +381,7 @@ int plan_bins(const Shape& s, const DevInfo& dev, BinPlan* bp) {
   bp->lds = 0;
   for (int l = 0; l < s.levels; ++l) {
     bp->nwork += (s.h[l] + bp->rb[l] - 1) / bp->rb[l];
-    bp->lds = std::max(bp->lds, msda::value_layout(bp->rb[l], s.w[l], s.dim, bp->cap, bp->nqb).total);
+    bp->lds = std::max(bp->lds, msda::value_layout(bp->rb[l], s.w[l], s.dim, bp->cap, bp->nqb, bp->nacc).total);
   }
   const int64_t sub = static_cast<int64_t>(bp->qblock) * s.points;  // records per (slice, item, block) at most
   bp->bins_bytes = N * bp->nwork * bp->nqb * sub * static_cast<int64_t>(sizeof(msda::SampleRec));
@@ -479,7 +490,7 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
       return fail(MSDA_ERR_UNSUPPORTED, "level %d (%d x %d) exceeds 32000 rows or columns", l, s.h[l], s.w[l]);
   if (static_cast<int64_t>(len_query) * n_heads * head_dim > 0x7fffffff)
     return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * head_dim exceeds 2^31");
-  const int vec = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 8), {{value, vbytes}, {grad_output, gbytes}});
+  const int vec = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 16), {{value, vbytes}, {grad_output, gbytes}});
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
 
@@ -506,15 +517,16 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     bp.nqb = 1;
     bp.qblock = 1;
     bp.cap = 1;
+    bp.nacc = 1;
     bp.nwork = 0;
     bp.lds = 0;
     for (int l = 0; l < n_levels; ++l) {
       bp.rb[l] = 1;
-      while (bp.rb[l] < s.h[l] && msda::value_layout(bp.rb[l] + 1, s.w[l], head_dim, 1, 1).total <= dev.lds_bytes / 2) ++bp.rb[l];
-      if (msda::value_layout(bp.rb[l], s.w[l], head_dim, 1, 1).total > dev.lds_bytes)
+      while (bp.rb[l] < s.h[l] && msda::value_layout(bp.rb[l] + 1, s.w[l], head_dim, 1, 1, 1).total <= dev.lds_bytes / 2) ++bp.rb[l];
+      if (msda::value_layout(bp.rb[l], s.w[l], head_dim, 1, 1, 1).total > dev.lds_bytes)
         return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], head_dim);
       bp.nwork += (s.h[l] + bp.rb[l] - 1) / bp.rb[l];
-      bp.lds = std::max(bp.lds, msda::value_layout(bp.rb[l], s.w[l], head_dim, 1, 1).total);
+      bp.lds = std::max(bp.lds, msda::value_layout(bp.rb[l], s.w[l], head_dim, 1, 1, 1).total);
     }
     vp.bins = nullptr;
     vp.bin_counts = nullptr;
@@ -581,8 +593,10 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   const int64_t vgrid = static_cast<int64_t>(batch) * n_heads * vp.nwork;
   if (vgrid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
   const int vthreads = std::max(64, std::min(msda::kValueMaxThreads, (env_int("MSDA_BWD_VALUE_THREADS", 512) / 64) * 64));
-  if (value_dtype == MSDA_DTYPE_BF16) return launch_bwd_value<msda::bf16_t, 4>(vp, static_cast<int>(vgrid), vthreads, bp.lds, st);
-  return launch_bwd_value<float, 4>(vp, static_cast<int>(vgrid), vthreads, bp.lds, st);
+  const int g = static_cast<int>(vgrid);
+  if (value_dtype == MSDA_DTYPE_BF16)
+    return bp.nacc == 4 ? launch_bwd_value<msda::bf16_t, 4, 4>(vp, g, vthreads, bp.lds, st) : launch_bwd_value<msda::bf16_t, 4, 1>(vp, g, vthreads, bp.lds, st);
+  return bp.nacc == 4 ? launch_bwd_value<float, 4, 4>(vp, g, vthreads, bp.lds, st) : launch_bwd_value<float, 4, 1>(vp, g, vthreads, bp.lds, st);
 }
 
 }  // extern "C"

@@ -10,8 +10,7 @@
 //    value slices (the levels that fit) are staged into LDS with one batched copy; levels that do
 //    not fit are gathered through L2. Lanes are laid out channel group, then head, then query, so
 //    the lanes of one query read locations / weights and write output rows as contiguous runs of
-//    the [B, Q, H, ...] tensors. Each lane group computes a sample's coordinates once; the next
-//    query's inputs are loaded while the current one is computed.
+//    the [B, Q, H, ...] tensors. Each lane group computes a sample's coordinates once.
 //  * bwd_sample_kernel — the same decomposition for the backward pass: per sample, the dot
 //    products D_c = <g, v_c> with the four corners give grad_attention_weights and
 //    grad_sampling_locations, and a 16-byte record (floor cell, a*(1-fx), a*fx, fy) is written to
@@ -20,9 +19,10 @@
 //    records, counting-sorts those whose cell touches the band by cell into LDS (integer LDS
 //    atomics count and rank them), and has one lane per (cell, 4 channels) sum
 //    a * w_k * g over the cell's records in registers, grad_output rows being gathered from global
-//    memory. The sums are added to an f32 band accumulator in four colour classes of cells (x and
-//    y parity) whose 2x2 pixel footprints are disjoint, so no two lanes write one element and no
-//    atomics on floats are needed; each grad_value element is written once, in the value dtype.
+//    memory. Corner k's sum goes to the k-th of four f32 band accumulators: for a fixed corner,
+//    distinct cells hit distinct pixels, so no two lanes ever update one element and no atomics on
+//    floats are needed; each grad_value element is written once, as the sum of the four, in the
+//    value dtype.
 //
 // Measured on MI355X (per CU): LDS float atomics (ds_add_f32) cost ~195 cycles per wave
 // instruction against ~6 for integer ones, and device-wide f32 atomics reach ~1.3 TB/s at best;
@@ -42,8 +42,7 @@ constexpr int kXcds = 8;               // MI355X: 8 accelerator complex dies, wo
 constexpr int kSampleMaxThreads = 512;  // forward and per-sample backward workgroups
 constexpr int kValueMaxThreads = 1024;  // grad_value workgroups
 constexpr int kGatherBatch = 8;         // grad_output rows fetched together per lane in the grad_value gather
-constexpr int kGatherSlots = 1;         // (cell, channel group) tasks a lane carries through one round (1 or 2)
-constexpr int kPassBatch = 4;           // samples whose loads are issued together (software-pipelined)
+constexpr int kPassBatch = 4;           // samples whose location / weight loads are issued together
 
 using bf16_t = uint16_t;
 
@@ -117,11 +116,11 @@ struct ValueLayout {
 
 __host__ __device__ inline int align16i(int x) { return (x + 15) & ~15; }
 
-__host__ __device__ inline ValueLayout value_layout(int band_rows, int w, int dim, int cap, int nqb) {
+__host__ __device__ inline ValueLayout value_layout(int band_rows, int w, int dim, int cap, int nqb, int nacc) {
   ValueLayout L;
   const int ncell = (band_rows + 1) * (w + 1);
   int o = 0;
-  L.acc = o;      o += align16i(band_rows * w * dim * 4);
+  L.acc = o;      o += nacc * align16i(band_rows * w * dim * 4);  // one per bilinear corner, or one in all
   L.cnt = o;      o += align16i((ncell + 1) * 4);
   L.off = o;      o += align16i((ncell + 1) * 4);
   L.misc = o;     o += 128;  // 4 counters + one scan slot per wave (<= 16 waves) + spare
@@ -396,7 +395,7 @@ __device__ __forceinline__ SampleLane sample_lane(const SampleParams& p) {
   return s;
 }
 
-// A lane's inputs for up to kPassBatch samples of one (query, head).
+// A lane's inputs for up to kPassBatch samples of one (query, head), loaded together.
 struct PassIn {
   float2 xy[kPassBatch];
   float a[kPassBatch];
@@ -462,8 +461,11 @@ __device__ __forceinline__ void fwd_pass(float (&acc)[VEC], const PassIn& f, int
   }
 }
 
+// Four waves per SIMD (<= 128 VGPRs): latency is hidden by other waves rather than by
+// registers holding the next query's inputs (measured faster on MI355X).
 template <typename VT, int VEC>
-__global__ void __launch_bounds__(kSampleMaxThreads) fwd_kernel(const SampleParams p) {
+__global__ void __launch_bounds__(kSampleMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
+fwd_kernel(const SampleParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   VT* lds = reinterpret_cast<VT*>(lds_raw);
   const SampleItem it = sample_item(p);
@@ -473,40 +475,25 @@ __global__ void __launch_bounds__(kSampleMaxThreads) fwd_kernel(const SamplePara
   const VT* __restrict__ vg = static_cast<const VT*>(p.value) + (static_cast<int64_t>(it.b) * p.heads + it.h0) * slice_elems;
   const int h = it.h0 + ln.hl;
   const int LP = p.levels * p.points;
-  const bool pipelined = LP <= kPassBatch;
   const int q_lo = it.qb * p.qblock;
   const int q_hi = min(p.queries, q_lo + p.qblock);
   const float2* __restrict__ loc2 = reinterpret_cast<const float2*>(p.loc);
-  auto row_of = [&](int q) { return (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h; };  // (b, q, h)
-
-  // The first pass's inputs are requested before the value rows, so both latencies overlap.
-  int q = q_lo + ln.qs;
-  PassIn cur;
-  if (ln.active && pipelined && q < q_hi) load_pass(cur, loc2 + row_of(q) * LP, p.attn + row_of(q) * LP, 0, LP);
   stage_group(p, lds, vg);
   __syncthreads();
   if (!ln.active) return;  // no barrier follows
 
   const VT* __restrict__ vs = vg + ln.hl * slice_elems + ln.c0;  // this head's slice in global memory
   const VT* hlds = lds + ln.hl * p.head_lds + ln.c0;
-  for (; q < q_hi; q += ln.qpp) {
-    const int64_t row = row_of(q);
+  for (int q = q_lo + ln.qs; q < q_hi; q += ln.qpp) {
+    const int64_t row = (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h;  // (b, q, h)
     float acc[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
     int l = 0, pt = 0;  // level and point of the next sample (level-major order, ops.py:285)
-    if (pipelined) {
-      PassIn nxt;
-      const int qn = q + ln.qpp;
-      if (qn < q_hi) load_pass(nxt, loc2 + row_of(qn) * LP, p.attn + row_of(qn) * LP, 0, LP);
-      fwd_pass<VT, VEC>(acc, cur, 0, LP, l, pt, p, hlds, vs);
-      cur = nxt;
-    } else {
-      for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
-        PassIn f;
-        load_pass(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
-        fwd_pass<VT, VEC>(acc, f, s0, LP, l, pt, p, hlds, vs);
-      }
+    for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
+      PassIn f;
+      load_pass(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
+      fwd_pass<VT, VEC>(acc, f, s0, LP, l, pt, p, hlds, vs);
     }
     if (ln.lane_on) store_any<VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, acc);
   }
@@ -615,7 +602,8 @@ __device__ __forceinline__ void bwd_pass(const PassIn& f, const float (&g)[VEC],
 }
 
 template <typename VT, int VEC>
-__global__ void __launch_bounds__(kSampleMaxThreads) bwd_sample_kernel(const SampleParams p) {
+__global__ void __launch_bounds__(kSampleMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
+bwd_sample_kernel(const SampleParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   VT* lds = reinterpret_cast<VT*>(lds_raw);
   const SampleItem it = sample_item(p);
@@ -624,63 +612,34 @@ __global__ void __launch_bounds__(kSampleMaxThreads) bwd_sample_kernel(const Sam
   const int64_t slice_elems = p.len_value * D;
   const VT* __restrict__ vg = static_cast<const VT*>(p.value) + (static_cast<int64_t>(it.b) * p.heads + it.h0) * slice_elems;
   const int h = it.h0 + ln.hl;
-  const int P = p.points;
-  const int LP = p.levels * P;
-  const bool pipelined = LP <= kPassBatch;
+  const int LP = p.levels * p.points;
   const int q_lo = it.qb * p.qblock;
   const int q_hi = min(p.queries, q_lo + p.qblock);
   const float2* __restrict__ loc2 = reinterpret_cast<const float2*>(p.loc);
   const bool gbf = p.gout_bf16 != 0;
-  auto row_of = [&](int q) { return (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h; };  // (b, q, h)
   const int64_t n = static_cast<int64_t>(it.b) * p.heads + h;
   // per (head, item) record counters of this workgroup, after the staged value rows
   int* lcnt = reinterpret_cast<int*>(lds_raw + align16i(p.hg * p.head_lds * static_cast<int>(sizeof(VT))));
   const int ncnt = p.bins ? p.hg * p.nwork : 0;
   for (int i = threadIdx.x; i < ncnt; i += blockDim.x) lcnt[i] = 0;
-
-  int q = q_lo + ln.qs;
-  PassIn cur;
-  float gcur[VEC];
-  if (ln.active && pipelined && q < q_hi) {
-    load_pass(cur, loc2 + row_of(q) * LP, p.attn + row_of(q) * LP, 0, LP);
-    load_any<VEC>(p.gout, row_of(q) * D + ln.c0, gbf, gcur);
-  }
   stage_group(p, lds, vg);
   __syncthreads();
 
   const VT* __restrict__ vs = vg + ln.hl * slice_elems + ln.c0;
   const VT* hlds = lds + ln.hl * p.head_lds + ln.c0;
-  for (; ln.active && q < q_hi; q += ln.qpp) {
-    const int64_t row = row_of(q);
+  for (int q = q_lo + ln.qs; ln.active && q < q_hi; q += ln.qpp) {
+    const int64_t row = (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h;  // (b, q, h)
+    float g[VEC];
+    load_any<VEC>(p.gout, row * D + ln.c0, gbf, g);
+    if (!ln.lane_on) {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) g[k] = 0.0f;
+    }
     int l = 0, pt = 0;
-    if (pipelined) {
-      PassIn nxt;
-      float gnxt[VEC];
-      const int qn = q + ln.qpp;
-      if (qn < q_hi) {
-        load_pass(nxt, loc2 + row_of(qn) * LP, p.attn + row_of(qn) * LP, 0, LP);
-        load_any<VEC>(p.gout, row_of(qn) * D + ln.c0, gbf, gnxt);
-      }
-      if (!ln.lane_on) {
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) gcur[k] = 0.0f;
-      }
-      bwd_pass<VT, VEC>(cur, gcur, 0, LP, l, pt, p, ln, hlds, vs, row, lcnt, q - q_lo, n, it.qb);
-      cur = nxt;
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) gcur[k] = gnxt[k];
-    } else {
-      float g[VEC];
-      load_any<VEC>(p.gout, row * D + ln.c0, gbf, g);
-      if (!ln.lane_on) {
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) g[k] = 0.0f;
-      }
-      for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
-        PassIn f;
-        load_pass(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
-        bwd_pass<VT, VEC>(f, g, s0, LP, l, pt, p, ln, hlds, vs, row, lcnt, q - q_lo, n, it.qb);
-      }
+    for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
+      PassIn f;
+      load_pass(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
+      bwd_pass<VT, VEC>(f, g, s0, LP, l, pt, p, ln, hlds, vs, row, lcnt, q - q_lo, n, it.qb);
     }
   }
   if (!p.bins) return;
@@ -753,9 +712,11 @@ __device__ __forceinline__ void load_gc(const void* __restrict__ base, bool bf16
   }
 }
 
-// CG: channels per gather lane (4). Four waves per SIMD (<= 128 VGPRs) let two 512-thread
-// workgroups share a CU.
-template <typename VT, int CG>
+// CG: channels per gather lane (4). NACC: 4 = one accumulator per bilinear corner (conflict-free,
+// no colour passes); 1 = a single accumulator updated in four colour passes per round of tasks
+// (cells of one x/y parity never share a pixel), for bands where four accumulators do not fit.
+// Four waves per SIMD (<= 128 VGPRs) let two 512-thread workgroups share a CU.
+template <typename VT, int CG, int NACC>
 __global__ void __launch_bounds__(kValueMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
 bwd_value_kernel(const ValueParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -779,7 +740,7 @@ bwd_value_kernel(const ValueParams p) {
   const int64_t n = static_cast<int64_t>(b) * p.heads + h;
   const int nt = blockDim.x, t = threadIdx.x, lane = t & 63;
 
-  const ValueLayout lay = value_layout(L.band_rows, W, D, p.cap, p.nqb);
+  const ValueLayout lay = value_layout(L.band_rows, W, D, p.cap, p.nqb, NACC);
   float* acc = reinterpret_cast<float*>(lds_raw + lay.acc);
   int* cnt = reinterpret_cast<int*>(lds_raw + lay.cnt);
   int* off = reinterpret_cast<int*>(lds_raw + lay.off);
@@ -788,8 +749,11 @@ bwd_value_kernel(const ValueParams p) {
   int* binpre = reinterpret_cast<int*>(lds_raw + lay.binpre);
   float4* list = reinterpret_cast<float4*>(lds_raw + lay.list);  // segment's records, in cell order
 
+  // With four accumulators, one per bilinear corner k, a cell adds its corner-k sum to accumulator
+  // k, and distinct cells hit distinct pixels for a fixed k, so no two lanes ever update one element.
+  const int acc_stride = align16i(L.band_rows * W * D * 4) / 4;  // floats between accumulators
   {
-    const int na = rb * W * D;
+    const int na = (NACC - 1) * acc_stride + rb * W * D;
     float4* a4 = reinterpret_cast<float4*>(acc);
     for (int i = t; i < (na >> 2); i += nt) a4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int i = (na & ~3) + t; i < na; i += nt) acc[i] = 0.0f;
@@ -802,13 +766,22 @@ bwd_value_kernel(const ValueParams p) {
   const int64_t subcap = static_cast<int64_t>(p.qblock) * P;
   const SampleRec* __restrict__ R = p.bins ? p.bins + (n * p.nwork + wk) * p.nqb * subcap : nullptr;
   const int* __restrict__ C = p.bin_counts ? p.bin_counts + (n * p.nwork + wk) * p.nqb : nullptr;
-  if (t == 0) {
-    int run = 0;
-    for (int i = 0; i < p.nqb; ++i) {
-      binpre[i] = run;
-      run += p.bin_counts ? C[i] : 0;  // no bins without queries
+  // counts loaded in parallel, then an exclusive scan by the first wave (no bins without queries)
+  for (int i = t; i < p.nqb; i += nt) binpre[i + 1] = C ? C[i] : 0;
+  if (t == 0) binpre[0] = 0;
+  __syncthreads();
+  if (t < 64) {
+    int carry = 0;
+    for (int i0 = 0; i0 < p.nqb; i0 += 64) {
+      const int i = i0 + lane;
+      int v = i < p.nqb ? binpre[i + 1] : 0;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int x = __shfl_up(v, o, 64);
+        if (lane >= o) v += x;
+      }
+      if (i < p.nqb) binpre[i + 1] = carry + v;
+      carry += __shfl(v, 63, 64);
     }
-    binpre[p.nqb] = run;
   }
   constexpr int U = 8;  // records loaded per thread before use
   // grad_output row (b, q=0, h); row q is q * H * D elements further (fits 32 bits: checked on the host)
@@ -881,108 +854,87 @@ bwd_value_kernel(const ValueParams p) {
     }
     __syncthreads();
     const int ntask = misc[2] * gpp;
-    // ---- one lane per (non-empty cell, CG channels) task, kGatherSlots tasks per round: sum
-    //      a * w_k * g over the cell's records in registers, kGatherBatch grad_output rows in flight;
-    //      then add the sums to the cells' 2x2 pixels in four colour passes (cells of one x/y parity
-    //      never share a pixel).
-    for (int t0 = 0; t0 < ntask; t0 += kGatherSlots * nt) {
-      int kx[kGatherSlots], ky[kGatherSlots], ch0[kGatherSlots], nch[kGatherSlots], ebeg[kGatherSlots], elen[kGatherSlots];
-      float s[kGatherSlots][4][CG];
-#pragma unroll
-      for (int slot = 0; slot < kGatherSlots; ++slot) {
-        const int task = t0 + slot * nt + t;
-        kx[slot] = ky[slot] = ch0[slot] = nch[slot] = ebeg[slot] = elen[slot] = 0;
-        if (task < ntask) {
-          const int ci = task / gpp, grp = task - ci * gpp;
-          const int key = nonempty[ci];
-          ky[slot] = key / (W + 1);
-          kx[slot] = key - ky[slot] * (W + 1);
-          ch0[slot] = grp * CG;
-          nch[slot] = min(CG, D - ch0[slot]);
-          ebeg[slot] = off[key];
-          elen[slot] = off[key + 1] - ebeg[slot];
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-#pragma unroll
-          for (int e = 0; e < CG; ++e) s[slot][k][e] = 0.0f;
+    // ---- one lane per (non-empty cell, CG channels) task: sum a * w_k * g over the cell's records
+    //      in registers, kGatherBatch grad_output rows in flight, then add corner k's sum to
+    //      accumulator k (conflict-free, so tasks need no barriers between them).
+    for (int t0 = 0; t0 < ntask; t0 += nt) {
+      const int task = t0 + t;
+      int kx = 0, ky = 0, ch0 = 0, nch = 0, ebeg = 0, eend = 0;
+      if (task < ntask) {
+        const int ci = task / gpp, grp = task - ci * gpp;
+        const int key = nonempty[ci];
+        ky = key / (W + 1);
+        kx = key - ky * (W + 1);
+        ch0 = grp * CG;
+        nch = min(CG, D - ch0);
+        ebeg = off[key];
+        eend = off[key + 1];
       }
-      // The slots' records form one sequence, walked kGatherBatch at a time so that many
-      // grad_output rows are in flight per lane.
-      const int total = elen[0] + (kGatherSlots > 1 ? elen[kGatherSlots - 1] : 0);
-      for (int f0 = 0; f0 < total; f0 += kGatherBatch) {
-        float4 w[kGatherBatch];
+      float s[4][CG];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int e = 0; e < CG; ++e) s[k][e] = 0.0f;
+      for (int e0 = ebeg; e0 < eend; e0 += kGatherBatch) {
+        float u[kGatherBatch], v[kGatherBatch], fy[kGatherBatch];
         float g[kGatherBatch][CG];
-        bool second[kGatherBatch];
 #pragma unroll
         for (int i = 0; i < kGatherBatch; ++i) {
-          const int f = f0 + i;
-          second[i] = f >= elen[0];
-          if (f < total) {
-            const int e = second[i] ? ebeg[kGatherSlots - 1] + (f - elen[0]) : ebeg[0] + f;
-            const int c0 = second[i] ? ch0[kGatherSlots - 1] : ch0[0];
-            const int nc = second[i] ? nch[kGatherSlots - 1] : nch[0];
-            w[i] = list[e];
+          if (e0 + i < eend) {
+            const float4 w = list[e0 + i];
+            u[i] = w.x;
+            v[i] = w.y;
+            fy[i] = w.z;
             // the query index is < Q by construction; the clamp only keeps a broken invariant in bounds
-            const int q = static_cast<int>(min(static_cast<unsigned>(__float_as_int(w[i].w)), static_cast<unsigned>(Q - 1)));
-            load_gc<CG>(gbase, gbf, gv4, q * gqstride + c0, nc, g[i]);
+            const int q = static_cast<int>(min(static_cast<unsigned>(__float_as_int(w.w)), static_cast<unsigned>(Q - 1)));
+            load_gc<CG>(gbase, gbf, gv4, q * gqstride + ch0, nch, g[i]);
           }
         }
 #pragma unroll
         for (int i = 0; i < kGatherBatch; ++i) {
-          if (f0 + i < total) {
-            const float w00 = w[i].x * (1.0f - w[i].z), w10 = w[i].y * (1.0f - w[i].z);
-            const float w01 = w[i].x * w[i].z, w11 = w[i].y * w[i].z;
-            if (!second[i]) {
+          if (e0 + i < eend) {
+            const float w00 = u[i] * (1.0f - fy[i]), w10 = v[i] * (1.0f - fy[i]);
+            const float w01 = u[i] * fy[i], w11 = v[i] * fy[i];
 #pragma unroll
-              for (int e = 0; e < CG; ++e) {
-                s[0][0][e] += w00 * g[i][e];
-                s[0][1][e] += w10 * g[i][e];
-                s[0][2][e] += w01 * g[i][e];
-                s[0][3][e] += w11 * g[i][e];
-              }
-            } else {
-#pragma unroll
-              for (int e = 0; e < CG; ++e) {
-                s[kGatherSlots - 1][0][e] += w00 * g[i][e];
-                s[kGatherSlots - 1][1][e] += w10 * g[i][e];
-                s[kGatherSlots - 1][2][e] += w01 * g[i][e];
-                s[kGatherSlots - 1][3][e] += w11 * g[i][e];
-              }
+            for (int e = 0; e < CG; ++e) {
+              s[0][e] = fmaf(w00, g[i][e], s[0][e]);
+              s[1][e] = fmaf(w10, g[i][e], s[1][e]);
+              s[2][e] = fmaf(w01, g[i][e], s[2][e]);
+              s[3][e] = fmaf(w11, g[i][e], s[3][e]);
             }
           }
         }
       }
-      for (int c = 0; c < 4; ++c) {
+      // With one accumulator, cells of one colour (x and y parity) are updated per pass.
+      const int color = (kx & 1) | ((ky & 1) << 1);
+      for (int c = 0; c < (NACC == 4 ? 1 : 4); ++c) {
+        if (task < ntask && (NACC == 4 || color == c)) {
 #pragma unroll
-        for (int slot = 0; slot < kGatherSlots; ++slot) {
-          if (t0 + slot * nt + t < ntask && ((kx[slot] & 1) | ((ky[slot] & 1) << 1)) == c) {
+          for (int k = 0; k < 4; ++k) {
+            // corner k of cell (kx, ky) is pixel (kx - 1 + (k & 1), ky - 1 + (k >> 1)) of the band
+            const int px = kx - 1 + (k & 1), py = ky - 1 + (k >> 1);
+            if (px >= 0 && px < W && py >= 0 && py < rb) {
+              float* ap = acc + (NACC == 4 ? k * acc_stride : 0) + (py * W + px) * D + ch0;
+              if (nch == CG && (D & 3) == 0) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              // corner k of cell (kx, ky) is pixel (kx - 1 + (k & 1), ky - 1 + (k >> 1)) of the band
-              const int px = kx[slot] - 1 + (k & 1), py = ky[slot] - 1 + (k >> 1);
-              if (px >= 0 && px < W && py >= 0 && py < rb) {
-                float* ap = acc + (py * W + px) * D + ch0[slot];
-                if (nch[slot] == CG && (D & 3) == 0) {
-#pragma unroll
-                  for (int e = 0; e < CG; e += 4) {
-                    float4 o = *reinterpret_cast<float4*>(ap + e);
-                    o.x += s[slot][k][e];
-                    o.y += s[slot][k][e + 1];
-                    o.z += s[slot][k][e + 2];
-                    o.w += s[slot][k][e + 3];
-                    *reinterpret_cast<float4*>(ap + e) = o;
-                  }
-                } else {
-                  for (int e = 0; e < nch[slot]; ++e) ap[e] += s[slot][k][e];
+                for (int e = 0; e < CG; e += 4) {
+                  float4 o = *reinterpret_cast<float4*>(ap + e);
+                  o.x += s[k][e];
+                  o.y += s[k][e + 1];
+                  o.z += s[k][e + 2];
+                  o.w += s[k][e + 3];
+                  *reinterpret_cast<float4*>(ap + e) = o;
                 }
+              } else {
+                for (int e = 0; e < nch; ++e) ap[e] += s[k][e];
               }
             }
           }
         }
-        __syncthreads();
+        if (NACC == 1) __syncthreads();
       }
     }
+    __syncthreads();  // every task done before the cell tables are reused
     // the placement cursors start the next segment at zero
     for (int i = t; i < ncell; i += nt) cnt[i] = 0;
     if (t == 0) misc[2] = 0;
@@ -990,18 +942,30 @@ bwd_value_kernel(const ValueParams p) {
     s_lo = s_hi;
   }
 
-  // ---- the band's grad_value rows, once, in the value dtype
+  // ---- the band's grad_value rows, once, in the value dtype (the sum of the accumulators)
   VT* dst = static_cast<VT*>(p.dvalue) + (n * p.len_value + L.start + static_cast<int64_t>(r0) * W) * D;
   const int na = rb * W * D;
-  if constexpr (std::is_same<VT, float>::value) {
-    if (p.vec16) {
-      for (int i = t; i < (na >> 2); i += nt) reinterpret_cast<float4*>(dst)[i] = reinterpret_cast<const float4*>(acc)[i];
-      for (int i = (na & ~3) + t; i < na; i += nt) dst[i] = acc[i];
-    } else {
-      for (int i = t; i < na; i += nt) dst[i] = acc[i];
+  if (p.vec16 && (na & 3) == 0) {
+    for (int i = t; i < (na >> 2); i += nt) {
+      float4 a = reinterpret_cast<const float4*>(acc)[i];
+#pragma unroll
+      for (int k = 1; k < NACC; ++k) {
+        const float4 b = reinterpret_cast<const float4*>(acc + k * acc_stride)[i];
+        a.x += b.x;
+        a.y += b.y;
+        a.z += b.z;
+        a.w += b.w;
+      }
+      const float o[4] = {a.x, a.y, a.z, a.w};
+      store_vec<VT, 4>(dst + 4 * i, o);
     }
   } else {
-    for (int i = t; i < na; i += nt) dst[i] = f32_to_bf16(acc[i]);
+    for (int i = t; i < na; i += nt) {
+      float o[1] = {acc[i]};
+#pragma unroll
+      for (int k = 1; k < NACC; ++k) o[0] += acc[i + k * acc_stride];
+      store_vec<VT, 1>(dst + i, o);
+    }
   }
 }
 

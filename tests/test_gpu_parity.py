@@ -186,6 +186,24 @@ def test_global_gather_path_and_many_bands(monkeypatch):
     assert_close(ga, g["grad_attn"], 1e-4, "grad_attn")
 
 
+@pytest.mark.parametrize("accumulators", [1, 4])
+@pytest.mark.parametrize("list_cap", [None, 256])
+def test_grad_value_accumulator_modes_and_segments(monkeypatch, accumulators, list_cap):
+    """grad_value with one band accumulator (colour passes) and with one per bilinear corner, with a
+    record list large enough for one segment per band and small enough to force several."""
+    monkeypatch.setenv("MSDA_BWD_ACCUMULATORS", str(accumulators))
+    if list_cap:
+        monkeypatch.setenv("MSDA_BWD_LIST", str(list_cap))
+    shapes = ((24, 24), (12, 12))
+    value, loc, attn, grad = make_inputs(77, 2, 4, 16, 700, shapes, 2)
+    _note(f"accumulators={accumulators} list_cap={list_cap}")
+    out, (gv, gl, ga) = _run(value, shapes, loc, attn, grad)
+    rv, rl, ra = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
+    assert_close(gv, rv, 1e-4, "grad_value")
+    assert_close(gl, rl, 1e-4, "grad_loc")
+    assert_close(ga, ra, 1e-4, "grad_attn")
+
+
 def test_level_larger_than_lds():
     """A 200x120 f32 level (1.5 MB per slice) plus a small one: global-gather forward, banded backward."""
     shapes = ((200, 120), (10, 12))
