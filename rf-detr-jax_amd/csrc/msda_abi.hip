@@ -172,20 +172,20 @@ int check_launch(const char* what) {
 // ------------------------------------------------------------------------------------------
 // dispatch
 
-template <typename VT, int VEC>
+template <typename VT, int VEC, int NS, bool STAGED>
 int launch_fwd(const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
   static std::atomic<int> granted[kMaxDevices];  // per instantiation
-  auto k = msda::fwd_kernel<VT, VEC>;
+  auto k = msda::fwd_kernel<VT, VEC, NS, STAGED>;
   int rc = allow_lds(k, lds, granted);
   if (rc != MSDA_OK) return rc;
   hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
   return check_launch("msda forward");
 }
 
-template <typename VT, int VEC>
+template <typename VT, int VEC, int NS, bool STAGED>
 int launch_bwd_sample(const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
   static std::atomic<int> granted[kMaxDevices];
-  auto k = msda::bwd_sample_kernel<VT, VEC>;
+  auto k = msda::bwd_sample_kernel<VT, VEC, NS, STAGED>;
   int rc = allow_lds(k, lds, granted);
   if (rc != MSDA_OK) return rc;
   hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
@@ -202,15 +202,49 @@ int launch_bwd_value(const msda::ValueParams& p, int grid, int threads, int lds,
   return check_launch("msda backward (grad_value pass)");
 }
 
+template <typename VT, int VEC, int NS, bool STAGED>
+int launch_sample(bool backward, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
+  return backward ? launch_bwd_sample<VT, VEC, NS, STAGED>(p, grid, threads, lds, stream)
+                  : launch_fwd<VT, VEC, NS, STAGED>(p, grid, threads, lds, stream);
+}
+
+// Grouped-query kernels come in two forms: every level staged in LDS (no L2 gather path) or not.
+template <typename VT, int VEC>
+int dispatch_ns(bool backward, int ns, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
+  const bool staged = p.all_staged != 0;
+  switch (ns) {
+    case 2: return staged ? launch_sample<VT, VEC, 2, true>(backward, p, grid, threads, lds, stream)
+                          : launch_sample<VT, VEC, 2, false>(backward, p, grid, threads, lds, stream);
+    case 4: return staged ? launch_sample<VT, VEC, 4, true>(backward, p, grid, threads, lds, stream)
+                          : launch_sample<VT, VEC, 4, false>(backward, p, grid, threads, lds, stream);
+    default: return launch_sample<VT, VEC, 0, false>(backward, p, grid, threads, lds, stream);
+  }
+}
+
+// Samples per (query, head) = levels * points. Up to four, the count is a compile-time bound of
+// the kernel, which then loads several queries' inputs at once; beyond that a query's samples are
+// processed in chunks.
+inline int samples_bound(int levels, int points) {
+  const int lp = levels * points;
+  return lp <= 2 ? 2 : lp <= 4 ? 4 : 0;
+}
+
 template <typename VT>
-int dispatch_sample(bool backward, int vec, const msda::SampleParams& p, int grid, int threads, int lds,
+int dispatch_value(int cg, int nacc, const msda::ValueParams& vp, int grid, int threads, int lds, hipStream_t st) {
+  if (cg == 8)
+    return nacc == 4 ? launch_bwd_value<VT, 8, 4>(vp, grid, threads, lds, st) : launch_bwd_value<VT, 8, 1>(vp, grid, threads, lds, st);
+  return nacc == 4 ? launch_bwd_value<VT, 4, 4>(vp, grid, threads, lds, st) : launch_bwd_value<VT, 4, 1>(vp, grid, threads, lds, st);
+}
+
+template <typename VT>
+int dispatch_sample(bool backward, int vec, int ns, const msda::SampleParams& p, int grid, int threads, int lds,
                     hipStream_t stream) {
   switch (vec) {
-    case 1: return backward ? launch_bwd_sample<VT, 1>(p, grid, threads, lds, stream) : launch_fwd<VT, 1>(p, grid, threads, lds, stream);
-    case 2: return backward ? launch_bwd_sample<VT, 2>(p, grid, threads, lds, stream) : launch_fwd<VT, 2>(p, grid, threads, lds, stream);
-    case 4: return backward ? launch_bwd_sample<VT, 4>(p, grid, threads, lds, stream) : launch_fwd<VT, 4>(p, grid, threads, lds, stream);
-    case 8: return backward ? launch_bwd_sample<VT, 8>(p, grid, threads, lds, stream) : launch_fwd<VT, 8>(p, grid, threads, lds, stream);
-    case 16: return backward ? launch_bwd_sample<VT, 16>(p, grid, threads, lds, stream) : launch_fwd<VT, 16>(p, grid, threads, lds, stream);
+    case 1: return dispatch_ns<VT, 1>(backward, ns, p, grid, threads, lds, stream);
+    case 2: return dispatch_ns<VT, 2>(backward, ns, p, grid, threads, lds, stream);
+    case 4: return dispatch_ns<VT, 4>(backward, ns, p, grid, threads, lds, stream);
+    case 8: return dispatch_ns<VT, 8>(backward, ns, p, grid, threads, lds, stream);
+    case 16: return dispatch_ns<VT, 16>(backward, ns, p, grid, threads, lds, stream);
   }
   return fail(MSDA_ERR_UNSUPPORTED, "no kernel for %d channels per lane", vec);
 }
@@ -239,10 +273,11 @@ struct SamplePlan {
 // Each level whose slice still fits one head's LDS budget is staged (packed in level order); the
 // rest are gathered through L2. Head groups: a workgroup serves `hg` heads of one batch entry, so
 // the lanes of one query touch contiguous runs of its [H, ...] rows; hg is the largest power of
-// two <= the cap that divides n_heads and keeps the group's slices within half the LDS, so that
-// two workgroups still share a CU (measured: two heads of a 24x24x16 f32 level per workgroup beat
-// one and four). Then one resident wave of workgroups: fewer, longer workgroups amortise the
-// value staging.
+// two <= the cap (4) that divides n_heads and keeps the group's slices within the LDS. A workgroup
+// that fills a CU's LDS gets 1024 threads (measured on MI355X for a 24x24x16 f32 level: four heads
+// in one 1024-thread workgroup per CU match or beat two heads in two 512-thread workgroups, and
+// halve the location / weight rows fetched per query). Then one resident wave of workgroups:
+// fewer, longer workgroups amortise the value staging.
 int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* prefix, int shift, msda::SampleParams* p,
                 SamplePlan* out, int forced_qblock = 0, int extra_lds = 0) {
   auto knob = [&](const char* name, int dflt) {
@@ -264,8 +299,8 @@ int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* pref
   }
   const int64_t head_bytes = align16(static_cast<int64_t>(head_lds) * vbytes);
   int hg = 1;
-  const int hg_cap = std::max(1, knob("_HEADS", 2));
-  const int group_budget = std::min(budget, knob("_GROUP_LDS", dev.lds_bytes / 2));
+  const int hg_cap = std::max(1, knob("_HEADS", 4));
+  const int group_budget = std::min(budget, knob("_GROUP_LDS", dev.lds_bytes));
   while (hg * 2 <= hg_cap && s.heads % (hg * 2) == 0 && (hg * 2) * head_bytes <= group_budget) hg *= 2;
   // With every level staged a head's region is its whole value slice; regions stay 16-byte aligned.
   const int head_stride = all_staged ? static_cast<int>(s.len_value * s.dim) : static_cast<int>(head_bytes / vbytes);
@@ -277,7 +312,7 @@ int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* pref
   if (all_staged && (static_cast<int64_t>(s.len_value) * s.dim * vbytes) % 16 != 0) p->vec16 = 0;
 
   const int per_cu = lds > 0 ? std::max(1, dev.lds_bytes / lds) : 8;
-  int threads = knob("_THREADS", per_cu >= 4 ? 256 : 512);
+  int threads = knob("_THREADS", per_cu >= 4 ? 256 : per_cu >= 2 ? 512 : 1024);
   threads = std::max(64, std::min(msda::kSampleMaxThreads, (threads / 64) * 64));
   const int tpq = hg << shift;  // threads per query
   if (tpq > threads) threads = std::min(msda::kSampleMaxThreads, ((tpq + 63) / 64) * 64);
@@ -323,6 +358,8 @@ struct BinPlan {
   int rb[msda::kMaxLevels];
   int cap;          // records listed per grad_value segment
   int nacc;         // grad_value accumulators: 4 (one per corner) or 1 (colour passes)
+  int threads;      // grad_value workgroup size
+  int cg;           // channels per grad_value gather lane (8 when head_dim allows, else 4)
   int lds;          // grad_value workgroup LDS
   int64_t bins_bytes, counts_bytes, total_bytes;
 };
@@ -348,6 +385,9 @@ int plan_bins(const Shape& s, const DevInfo& dev, BinPlan* bp) {
   for (int l = 0; l < s.levels; ++l) total_area += static_cast<int64_t>(s.h[l]) * s.w[l];
   const int records = std::max(1, s.queries * s.points);
   const int cap_want = std::min({65535, records, std::max(256, env_int("MSDA_BWD_LIST", 65535))});
+  bp->threads = std::max(64, std::min(msda::kValueMaxThreads, (env_int("MSDA_BWD_VALUE_THREADS", 512) / 64) * 64));
+  const int cg_env = env_int("MSDA_BWD_VALUE_CG", 4);
+  bp->cg = (cg_env == 8 && s.dim % 8 == 0) ? 8 : 4;
   const int cap_min = std::min(256, cap_want);
   int cap = cap_want;
   auto target_rows = [&](int l) {
@@ -417,6 +457,7 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
   const int obytes = output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   if (!aligned(value, vbytes) || !aligned(output, obytes)) return fail(MSDA_ERR_INVALID_ARGUMENT, "value/output not aligned to their element size");
   const int vec = pick_vec(head_dim, env_int("MSDA_FWD_MAX_VEC", 8), {{value, vbytes}, {output, obytes}});
+  const int ns = env_int("MSDA_FWD_GROUPED", 1) ? samples_bound(n_levels, n_points) : 0;
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
 
@@ -439,8 +480,8 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
   SamplePlan plan;
   if ((rc = plan_sample(s, vbytes, dev, "MSDA_FWD", shift, &p, &plan)) != MSDA_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (value_dtype == MSDA_DTYPE_BF16) return dispatch_sample<msda::bf16_t>(false, vec, p, plan.grid, plan.threads, plan.lds, st);
-  return dispatch_sample<float>(false, vec, p, plan.grid, plan.threads, plan.lds, st);
+  if (value_dtype == MSDA_DTYPE_BF16) return dispatch_sample<msda::bf16_t>(false, vec, ns, p, plan.grid, plan.threads, plan.lds, st);
+  return dispatch_sample<float>(false, vec, ns, p, plan.grid, plan.threads, plan.lds, st);
 }
 
 int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_query, int n_levels, int n_points,
@@ -491,6 +532,7 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   if (static_cast<int64_t>(len_query) * n_heads * head_dim > 0x7fffffff)
     return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * head_dim exceeds 2^31");
   const int vec = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 16), {{value, vbytes}, {grad_output, gbytes}});
+  const int ns = env_int("MSDA_BWD_GROUPED", 0) ? samples_bound(n_levels, n_points) : 0;
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
 
@@ -518,6 +560,8 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     bp.qblock = 1;
     bp.cap = 1;
     bp.nacc = 1;
+    bp.threads = 256;
+    bp.cg = 4;
     bp.nwork = 0;
     bp.lds = 0;
     for (int l = 0; l < n_levels; ++l) {
@@ -585,18 +629,17 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
       plan.lds = align16(plan.lds) + align16(static_cast<int64_t>(p.hg) * bp.nwork * 4);
       if (plan.lds > dev.lds_bytes) return fail(MSDA_ERR_UNSUPPORTED, "per-sample pass needs %d bytes of LDS", plan.lds);
     }
-    rc = value_dtype == MSDA_DTYPE_BF16 ? dispatch_sample<msda::bf16_t>(true, vec, p, plan.grid, plan.threads, plan.lds, st)
-                                        : dispatch_sample<float>(true, vec, p, plan.grid, plan.threads, plan.lds, st);
+    rc = value_dtype == MSDA_DTYPE_BF16 ? dispatch_sample<msda::bf16_t>(true, vec, ns, p, plan.grid, plan.threads, plan.lds, st)
+                                        : dispatch_sample<float>(true, vec, ns, p, plan.grid, plan.threads, plan.lds, st);
     if (rc != MSDA_OK) return rc;
   }
   if (!want_dv) return MSDA_OK;
   const int64_t vgrid = static_cast<int64_t>(batch) * n_heads * vp.nwork;
   if (vgrid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
-  const int vthreads = std::max(64, std::min(msda::kValueMaxThreads, (env_int("MSDA_BWD_VALUE_THREADS", 512) / 64) * 64));
+  const int vthreads = bp.threads;
   const int g = static_cast<int>(vgrid);
-  if (value_dtype == MSDA_DTYPE_BF16)
-    return bp.nacc == 4 ? launch_bwd_value<msda::bf16_t, 4, 4>(vp, g, vthreads, bp.lds, st) : launch_bwd_value<msda::bf16_t, 4, 1>(vp, g, vthreads, bp.lds, st);
-  return bp.nacc == 4 ? launch_bwd_value<float, 4, 4>(vp, g, vthreads, bp.lds, st) : launch_bwd_value<float, 4, 1>(vp, g, vthreads, bp.lds, st);
+  return value_dtype == MSDA_DTYPE_BF16 ? dispatch_value<msda::bf16_t>(bp.cg, bp.nacc, vp, g, vthreads, bp.lds, st)
+                                        : dispatch_value<float>(bp.cg, bp.nacc, vp, g, vthreads, bp.lds, st);
 }
 
 }  // extern "C"

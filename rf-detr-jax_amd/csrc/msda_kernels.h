@@ -39,9 +39,8 @@ namespace msda {
 
 constexpr int kMaxLevels = 16;
 constexpr int kXcds = 8;               // MI355X: 8 accelerator complex dies, workgroups dispatched round-robin
-constexpr int kSampleMaxThreads = 512;  // forward and per-sample backward workgroups
+constexpr int kSampleMaxThreads = 1024;  // forward and per-sample backward workgroups
 constexpr int kValueMaxThreads = 1024;  // grad_value workgroups
-constexpr int kGatherBatch = 8;         // grad_output rows fetched together per lane in the grad_value gather
 constexpr int kPassBatch = 4;           // samples whose location / weight loads are issued together
 
 using bf16_t = uint16_t;
@@ -297,6 +296,75 @@ __device__ __forceinline__ void store_any(void* base, int64_t off, bool is_bf16,
   else store_vec<float, VEC>(static_cast<float*>(base) + off, a);
 }
 
+// Rotated chunk order. A lane's VEC channels span N = VEC * sizeof(VT) / 16 chunks of 16 bytes
+// (N = 1 when the run is a single chunk, shorter, or not a multiple of 16 bytes). Register slot k
+// of a lane holds channel chunk (k + rot) mod N, where rot steps with the lane's (query, head)
+// index. An LDS row of 64 bytes spans four of the 16 four-bank groups a 16-lane access cycle
+// uses, so lanes reading the same chunk of random rows pile into four groups; rotating the chunk
+// by lane spreads them over all 16 (measured: same-chunk reads of random rows spend about two
+// thirds of LDS cycles in bank conflicts).
+template <typename VT, int VEC>
+constexpr int rot_chunks() {
+  return (VEC * static_cast<int>(sizeof(VT))) % 16 == 0 && VEC * static_cast<int>(sizeof(VT)) >= 32
+             ? VEC * static_cast<int>(sizeof(VT)) / 16
+             : 1;
+}
+
+template <typename VT, int VEC, bool kLds>
+__device__ __forceinline__ void load_rot(const VT* p, int rot, float (&o)[VEC]) {
+  constexpr int N = rot_chunks<VT, VEC>();
+  if constexpr (N == 1) {
+    if constexpr (kLds) load_vec_lds<VT, VEC>(p, o);
+    else load_vec<VT, VEC>(p, o);
+  } else {
+    constexpr int E = VEC / N;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      const int c = (k + rot) & (N - 1);
+      float t[E];
+      if constexpr (kLds) load_vec_lds<VT, E>(p + c * E, t);
+      else load_vec<VT, E>(p + c * E, t);
+#pragma unroll
+      for (int i = 0; i < E; ++i) o[k * E + i] = t[i];
+    }
+  }
+}
+
+// The same order for a tensor in either dtype (grad_output), chunks counted in VT elements.
+template <typename VT, int VEC>
+__device__ __forceinline__ void load_any_rot(const void* base, int64_t off, bool is_bf16, int rot, float (&o)[VEC]) {
+  constexpr int N = rot_chunks<VT, VEC>();
+  if constexpr (N == 1) {
+    load_any<VEC>(base, off, is_bf16, o);
+  } else {
+    constexpr int E = VEC / N;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      float t[E];
+      load_any<E>(base, off + ((k + rot) & (N - 1)) * E, is_bf16, t);
+#pragma unroll
+      for (int i = 0; i < E; ++i) o[k * E + i] = t[i];
+    }
+  }
+}
+
+template <typename VT, int VEC>
+__device__ __forceinline__ void store_any_rot(void* base, int64_t off, bool is_bf16, int rot, const float (&a)[VEC]) {
+  constexpr int N = rot_chunks<VT, VEC>();
+  if constexpr (N == 1) {
+    store_any<VEC>(base, off, is_bf16, a);
+  } else {
+    constexpr int E = VEC / N;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      float t[E];
+#pragma unroll
+      for (int i = 0; i < E; ++i) t[i] = a[k * E + i];
+      store_any<E>(base, off + ((k + rot) & (N - 1)) * E, is_bf16, t);
+    }
+  }
+}
+
 // Cooperative copy global -> LDS of `count` elements. Each thread issues a batch of loads before
 // any store, so the copy is bounded by bandwidth rather than by one load latency per step.
 template <typename VT>
@@ -328,6 +396,13 @@ __device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, 
     for (; i < count; i += nt) dst[i] = src[i];
   }
 }
+
+// Waits until every vector-memory operation this wave issued has completed (gfx9 s_waitcnt
+// encoding: vmcnt 0, expcnt and lgkmcnt left at their maxima). Placed where a group of loads is
+// about to be consumed and before the group's stores: vmcnt counts loads and stores in issue order,
+// so once the wait is explicit the compiler needs no later vmcnt waits, which would otherwise also
+// wait for the acknowledgement of every store issued before them.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 __device__ __forceinline__ float group_sum(float v, int lpq) {
   for (int o = 1; o < lpq; o <<= 1) v += __shfl_xor(v, o, 64);
@@ -376,10 +451,11 @@ __device__ __forceinline__ void stage_group(const SampleParams& p, VT* lds, cons
 // queries; so the lanes of one query touch contiguous runs of its [H, ...] rows.
 struct SampleLane {
   int j, hl, qs, qpp, c0;
+  int rot;  // chunk rotation of this lane's channel run (rot_chunks)
   bool active, lane_on;
 };
 
-template <int VEC>
+template <typename VT, int VEC>
 __device__ __forceinline__ SampleLane sample_lane(const SampleParams& p) {
   SampleLane s;
   const int lpq = 1 << p.lpq_shift;
@@ -392,22 +468,50 @@ __device__ __forceinline__ SampleLane sample_lane(const SampleParams& p) {
   s.active = s.qs < s.qpp;
   s.lane_on = s.j * VEC < p.dim;
   s.c0 = s.lane_on ? s.j * VEC : 0;
+  s.rot = hq & (rot_chunks<VT, VEC>() - 1);  // consecutive (query, head) lanes rotate by one chunk
   return s;
 }
 
-// A lane's inputs for up to kPassBatch samples of one (query, head), loaded together.
-struct PassIn {
-  float2 xy[kPassBatch];
-  float a[kPassBatch];
+// A lane's inputs for up to N samples of one (query, head), loaded together.
+template <int N>
+struct SampleIn {
+  float2 xy[N];
+  float a[N];
 };
 
-__device__ __forceinline__ void load_pass(PassIn& f, const float2* __restrict__ lq, const float* __restrict__ aq, int s0,
-                                          int LP) {
+template <int N>
+__device__ __forceinline__ void load_in(SampleIn<N>& f, const float2* __restrict__ lq, const float* __restrict__ aq, int s0,
+                                        int LP) {
 #pragma unroll
-  for (int u = 0; u < kPassBatch; ++u) {
+  for (int u = 0; u < N; ++u) {
     if (s0 + u < LP) {
       f.xy[u] = lq[s0 + u];
       f.a[u] = aq[s0 + u];
+    }
+  }
+}
+
+// Queries per lane whose inputs are loaded together when a query's samples fit NS (NS = 0: one
+// query at a time, its samples in chunks of kPassBatch). The loads of a group are all in flight
+// before the first is used, so a lane waits one memory latency per group rather than per query;
+// the backward also holds each query's grad_output row (VEC floats), so it groups fewer (sized so
+// that no instantiation spills registers at four waves per SIMD).
+constexpr int query_group(int ns, int vec, bool backward) {
+  if (ns == 0) return 1;
+  if (!backward) return ns <= 2 ? 4 : 2;
+  if (vec >= 16) return ns <= 2 ? 2 : 1;
+  if (vec == 8) return 2;
+  return ns <= 2 ? 4 : 2;
+}
+
+template <int NS, int QU>
+__device__ __forceinline__ void load_group(SampleIn<NS> (&in)[QU], const float2* __restrict__ loc2, const float* __restrict__ attn,
+                                           int64_t row0, int64_t row_step, int q0, int q_step, int q_hi, int LP) {
+#pragma unroll
+  for (int i = 0; i < QU; ++i) {
+    if (q0 + i * q_step < q_hi) {
+      const int64_t row = row0 + i * row_step;
+      load_in<NS>(in[i], loc2 + row * LP, attn + row * LP, 0, LP);
     }
   }
 }
@@ -416,43 +520,34 @@ __device__ __forceinline__ void load_pass(PassIn& f, const float2* __restrict__ 
 // forward
 
 template <typename VT, int VEC, bool kLds>
-__device__ __forceinline__ void fwd_corners(float (&acc)[VEC], const VT* base, const Bilinear& c, float a) {
+__device__ __forceinline__ void fwd_corners(float (&acc)[VEC], const VT* base, const Bilinear& c, float a, int rot) {
   const float a00 = a * c.w00, a10 = a * c.w10, a01 = a * c.w01, a11 = a * c.w11;
   // Two corners in flight at a time keeps 16-channel lanes within the register budget; one fused
   // multiply-add per channel and corner.
   float u0[VEC], u1[VEC];
-  if constexpr (kLds) {
-    load_vec_lds<VT, VEC>(base + c.o00, u0);
-    load_vec_lds<VT, VEC>(base + c.o10, u1);
-  } else {
-    load_vec<VT, VEC>(base + c.o00, u0);
-    load_vec<VT, VEC>(base + c.o10, u1);
-  }
+  load_rot<VT, VEC, kLds>(base + c.o00, rot, u0);
+  load_rot<VT, VEC, kLds>(base + c.o10, rot, u1);
 #pragma unroll
   for (int k = 0; k < VEC; ++k) acc[k] = fmaf(u1[k], a10, fmaf(u0[k], a00, acc[k]));
-  if constexpr (kLds) {
-    load_vec_lds<VT, VEC>(base + c.o01, u0);
-    load_vec_lds<VT, VEC>(base + c.o11, u1);
-  } else {
-    load_vec<VT, VEC>(base + c.o01, u0);
-    load_vec<VT, VEC>(base + c.o11, u1);
-  }
+  load_rot<VT, VEC, kLds>(base + c.o01, rot, u0);
+  load_rot<VT, VEC, kLds>(base + c.o11, rot, u1);
 #pragma unroll
   for (int k = 0; k < VEC; ++k) acc[k] = fmaf(u1[k], a11, fmaf(u0[k], a01, acc[k]));
 }
 
-template <typename VT, int VEC>
-__device__ __forceinline__ void fwd_pass(float (&acc)[VEC], const PassIn& f, int s0, int LP, int& l, int& pt,
-                                         const SampleParams& p, const VT* hlds, const VT* __restrict__ vs) {
+// kStaged: every level is staged in LDS (no L2 gather path is compiled).
+template <typename VT, int VEC, int N, bool kStaged>
+__device__ __forceinline__ void fwd_pass(float (&acc)[VEC], const SampleIn<N>& f, int s0, int LP, int& l, int& pt,
+                                         const SampleParams& p, const VT* hlds, const VT* __restrict__ vs, int rot) {
   const int D = p.dim;
 #pragma unroll
-  for (int u = 0; u < kPassBatch; ++u) {
+  for (int u = 0; u < N; ++u) {
     if (s0 + u < LP) {
       const LevelDesc L = p.lv[l];
       const Bilinear c = bilinear(f.xy[u].x, f.xy[u].y, L, D);
       // Separate LDS and global paths: a pointer that may be either compiles to flat loads.
-      if (L.lds >= 0) fwd_corners<VT, VEC, true>(acc, hlds + L.lds, c, f.a[u]);
-      else fwd_corners<VT, VEC, false>(acc, vs + static_cast<int64_t>(L.start) * D, c, f.a[u]);
+      if (kStaged || L.lds >= 0) fwd_corners<VT, VEC, true>(acc, hlds + L.lds, c, f.a[u], rot);
+      else fwd_corners<VT, VEC, false>(acc, vs + static_cast<int64_t>(L.start) * D, c, f.a[u], rot);
       if (++pt == p.points) {
         pt = 0;
         ++l;
@@ -463,13 +558,14 @@ __device__ __forceinline__ void fwd_pass(float (&acc)[VEC], const PassIn& f, int
 
 // Four waves per SIMD (<= 128 VGPRs): latency is hidden by other waves rather than by
 // registers holding the next query's inputs (measured faster on MI355X).
-template <typename VT, int VEC>
+template <typename VT, int VEC, int NS, bool kStaged>
 __global__ void __launch_bounds__(kSampleMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
 fwd_kernel(const SampleParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   VT* lds = reinterpret_cast<VT*>(lds_raw);
   const SampleItem it = sample_item(p);
-  const SampleLane ln = sample_lane<VEC>(p);
+  const SampleLane ln = sample_lane<VT, VEC>(p);
+  const int rot = ln.rot;
   const int D = p.dim;
   const int64_t slice_elems = p.len_value * D;
   const VT* __restrict__ vg = static_cast<const VT*>(p.value) + (static_cast<int64_t>(it.b) * p.heads + it.h0) * slice_elems;
@@ -478,24 +574,52 @@ fwd_kernel(const SampleParams p) {
   const int q_lo = it.qb * p.qblock;
   const int q_hi = min(p.queries, q_lo + p.qblock);
   const float2* __restrict__ loc2 = reinterpret_cast<const float2*>(p.loc);
+  constexpr int QU = query_group(NS, VEC, false);
+  const int q_first = q_lo + ln.qs;
+  const int64_t row_first = (static_cast<int64_t>(it.b) * p.queries + q_first) * p.heads + h;  // (b, q, h)
+  const int64_t row_step = static_cast<int64_t>(ln.qpp) * p.heads;
+  SampleIn<NS == 0 ? 1 : NS> in[QU];
+  // The first group's inputs are requested before the staging copy, so their latency overlaps it.
+  if constexpr (NS > 0)
+    if (ln.active) load_group<NS, QU>(in, loc2, p.attn, row_first, row_step, q_first, ln.qpp, q_hi, LP);
   stage_group(p, lds, vg);
   __syncthreads();
   if (!ln.active) return;  // no barrier follows
 
   const VT* __restrict__ vs = vg + ln.hl * slice_elems + ln.c0;  // this head's slice in global memory
   const VT* hlds = lds + ln.hl * p.head_lds + ln.c0;
-  for (int q = q_lo + ln.qs; q < q_hi; q += ln.qpp) {
-    const int64_t row = (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h;  // (b, q, h)
-    float acc[VEC];
+  if constexpr (NS > 0) {
+    for (int qg = q_first; qg < q_hi; qg += QU * ln.qpp) {
+      const int64_t row0 = row_first + static_cast<int64_t>((qg - q_first) / ln.qpp) * row_step;
+      if (qg != q_first) load_group<NS, QU>(in, loc2, p.attn, row0, row_step, qg, ln.qpp, q_hi, LP);
+      wait_vmem();
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
-    int l = 0, pt = 0;  // level and point of the next sample (level-major order, ops.py:285)
-    for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
-      PassIn f;
-      load_pass(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
-      fwd_pass<VT, VEC>(acc, f, s0, LP, l, pt, p, hlds, vs);
+      for (int i = 0; i < QU; ++i) {
+        if (qg + i * ln.qpp < q_hi) {
+          const int64_t row = row0 + i * row_step;
+          float acc[VEC];
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
+          int l = 0, pt = 0;  // level and point of the next sample (level-major order, ops.py:285)
+          fwd_pass<VT, VEC, NS, kStaged>(acc, in[i], 0, LP, l, pt, p, hlds, vs, rot);
+          if (ln.lane_on) store_any_rot<VT, VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, rot, acc);
+        }
+      }
     }
-    if (ln.lane_on) store_any<VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, acc);
+  } else {
+    for (int q = q_first; q < q_hi; q += ln.qpp) {
+      const int64_t row = (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h;
+      float acc[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
+      int l = 0, pt = 0;
+      for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
+        SampleIn<kPassBatch> f;
+        load_in<kPassBatch>(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
+        fwd_pass<VT, VEC, kPassBatch, kStaged>(acc, f, s0, LP, l, pt, p, hlds, vs, rot);
+      }
+      if (ln.lane_on) store_any_rot<VT, VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, rot, acc);
+    }
   }
 }
 
@@ -504,15 +628,10 @@ fwd_kernel(const SampleParams p) {
 
 template <typename VT, int VEC, bool kLds>
 __device__ __forceinline__ void corner_dots(const VT* base, const Bilinear& c, const float (&g)[VEC], float& d00,
-                                            float& d10, float& d01, float& d11) {
+                                            float& d10, float& d01, float& d11, int rot) {
   float u0[VEC], u1[VEC];
-  if constexpr (kLds) {
-    load_vec_lds<VT, VEC>(base + c.o00, u0);
-    load_vec_lds<VT, VEC>(base + c.o10, u1);
-  } else {
-    load_vec<VT, VEC>(base + c.o00, u0);
-    load_vec<VT, VEC>(base + c.o10, u1);
-  }
+  load_rot<VT, VEC, kLds>(base + c.o00, rot, u0);
+  load_rot<VT, VEC, kLds>(base + c.o10, rot, u1);
   d00 = 0.0f;
   d10 = 0.0f;
 #pragma unroll
@@ -520,13 +639,8 @@ __device__ __forceinline__ void corner_dots(const VT* base, const Bilinear& c, c
     d00 = fmaf(g[k], u0[k], d00);
     d10 = fmaf(g[k], u1[k], d10);
   }
-  if constexpr (kLds) {
-    load_vec_lds<VT, VEC>(base + c.o01, u0);
-    load_vec_lds<VT, VEC>(base + c.o11, u1);
-  } else {
-    load_vec<VT, VEC>(base + c.o01, u0);
-    load_vec<VT, VEC>(base + c.o11, u1);
-  }
+  load_rot<VT, VEC, kLds>(base + c.o01, rot, u0);
+  load_rot<VT, VEC, kLds>(base + c.o11, rot, u1);
   d01 = 0.0f;
   d11 = 0.0f;
 #pragma unroll
@@ -545,21 +659,21 @@ __device__ __forceinline__ void emit_record(const SampleParams& p, int* lcnt, in
   p.bins[((n * p.nwork + item) * p.nqb + qb) * static_cast<int64_t>(p.qblock) * p.points + pos] = payload;
 }
 
-template <typename VT, int VEC>
-__device__ __forceinline__ void bwd_pass(const PassIn& f, const float (&g)[VEC], int s0, int LP, int& l, int& pt,
+template <typename VT, int VEC, int N, bool kStaged>
+__device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const float (&g)[VEC], int s0, int LP, int& l, int& pt,
                                          const SampleParams& p, const SampleLane& ln, const VT* hlds,
                                          const VT* __restrict__ vs, int64_t row, int* lcnt, int qoff, int64_t n, int qb) {
   const int D = p.dim;
   const int lpq = 1 << p.lpq_shift;
 #pragma unroll
-  for (int u = 0; u < kPassBatch; ++u) {
+  for (int u = 0; u < N; ++u) {
     if (s0 + u < LP) {
       const LevelDesc L = p.lv[l];
       const Bilinear c = bilinear(f.xy[u].x, f.xy[u].y, L, D);
       const float a = f.a[u];
       float d00, d10, d01, d11;
-      if (L.lds >= 0) corner_dots<VT, VEC, true>(hlds + L.lds, c, g, d00, d10, d01, d11);
-      else corner_dots<VT, VEC, false>(vs + static_cast<int64_t>(L.start) * D, c, g, d00, d10, d01, d11);
+      if (kStaged || L.lds >= 0) corner_dots<VT, VEC, true>(hlds + L.lds, c, g, d00, d10, d01, d11, ln.rot);
+      else corner_dots<VT, VEC, false>(vs + static_cast<int64_t>(L.start) * D, c, g, d00, d10, d01, d11, ln.rot);
       d00 = group_sum(d00, lpq);
       d10 = group_sum(d10, lpq);
       d01 = group_sum(d01, lpq);
@@ -601,13 +715,13 @@ __device__ __forceinline__ void bwd_pass(const PassIn& f, const float (&g)[VEC],
   }
 }
 
-template <typename VT, int VEC>
+template <typename VT, int VEC, int NS, bool kStaged>
 __global__ void __launch_bounds__(kSampleMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
 bwd_sample_kernel(const SampleParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   VT* lds = reinterpret_cast<VT*>(lds_raw);
   const SampleItem it = sample_item(p);
-  const SampleLane ln = sample_lane<VEC>(p);
+  const SampleLane ln = sample_lane<VT, VEC>(p);
   const int D = p.dim;
   const int64_t slice_elems = p.len_value * D;
   const VT* __restrict__ vg = static_cast<const VT*>(p.value) + (static_cast<int64_t>(it.b) * p.heads + it.h0) * slice_elems;
@@ -622,24 +736,65 @@ bwd_sample_kernel(const SampleParams p) {
   int* lcnt = reinterpret_cast<int*>(lds_raw + align16i(p.hg * p.head_lds * static_cast<int>(sizeof(VT))));
   const int ncnt = p.bins ? p.hg * p.nwork : 0;
   for (int i = threadIdx.x; i < ncnt; i += blockDim.x) lcnt[i] = 0;
+  constexpr int QU = query_group(NS, VEC, true);
+  const int q_first = q_lo + ln.qs;
+  const int64_t row_first = (static_cast<int64_t>(it.b) * p.queries + q_first) * p.heads + h;  // (b, q, h)
+  const int64_t row_step = static_cast<int64_t>(ln.qpp) * p.heads;
+  SampleIn<NS == 0 ? 1 : NS> in[QU];
+  float g[QU][VEC];
+  // grad_output rows and sample inputs of a group of queries are requested together; the first
+  // group's before the staging copy, so their latency overlaps it.
+  auto load_gout = [&](int64_t row0, int q0) {
+#pragma unroll
+    for (int i = 0; i < QU; ++i) {
+      if (q0 + i * ln.qpp < q_hi) {
+        if (ln.lane_on) {
+          load_any_rot<VT, VEC>(p.gout, (row0 + i * row_step) * D + ln.c0, gbf, ln.rot, g[i]);
+        } else {
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) g[i][k] = 0.0f;
+        }
+      }
+    }
+  };
+  if constexpr (NS > 0) {
+    if (ln.active) {
+      load_gout(row_first, q_first);
+      load_group<NS, QU>(in, loc2, p.attn, row_first, row_step, q_first, ln.qpp, q_hi, LP);
+    }
+  }
   stage_group(p, lds, vg);
   __syncthreads();
 
   const VT* __restrict__ vs = vg + ln.hl * slice_elems + ln.c0;
   const VT* hlds = lds + ln.hl * p.head_lds + ln.c0;
-  for (int q = q_lo + ln.qs; ln.active && q < q_hi; q += ln.qpp) {
-    const int64_t row = (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h;  // (b, q, h)
-    float g[VEC];
-    load_any<VEC>(p.gout, row * D + ln.c0, gbf, g);
-    if (!ln.lane_on) {
+  if constexpr (NS > 0) {
+    for (int qg = q_first; ln.active && qg < q_hi; qg += QU * ln.qpp) {
+      const int64_t row0 = row_first + static_cast<int64_t>((qg - q_first) / ln.qpp) * row_step;
+      if (qg != q_first) {
+        load_gout(row0, qg);
+        load_group<NS, QU>(in, loc2, p.attn, row0, row_step, qg, ln.qpp, q_hi, LP);
+      }
+      wait_vmem();
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) g[k] = 0.0f;
+      for (int i = 0; i < QU; ++i) {
+        const int q = qg + i * ln.qpp;
+        if (q < q_hi) {
+          int l = 0, pt = 0;
+          bwd_pass<VT, VEC, NS, kStaged>(in[i], g[i], 0, LP, l, pt, p, ln, hlds, vs, row0 + i * row_step, lcnt, q - q_lo, n, it.qb);
+        }
+      }
     }
-    int l = 0, pt = 0;
-    for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
-      PassIn f;
-      load_pass(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
-      bwd_pass<VT, VEC>(f, g, s0, LP, l, pt, p, ln, hlds, vs, row, lcnt, q - q_lo, n, it.qb);
+  } else {
+    for (int q = q_first; ln.active && q < q_hi; q += ln.qpp) {
+      const int64_t row = (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h;
+      load_gout(row, q);
+      int l = 0, pt = 0;
+      for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
+        SampleIn<kPassBatch> f;
+        load_in<kPassBatch>(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
+        bwd_pass<VT, VEC, kPassBatch, kStaged>(f, g[0], s0, LP, l, pt, p, ln, hlds, vs, row, lcnt, q - q_lo, n, it.qb);
+      }
     }
   }
   if (!p.bins) return;
@@ -712,7 +867,11 @@ __device__ __forceinline__ void load_gc(const void* __restrict__ base, bool bf16
   }
 }
 
-// CG: channels per gather lane (4). NACC: 4 = one accumulator per bilinear corner (conflict-free,
+// grad_output rows a grad_value lane fetches together (with their weights): as many as the register
+// budget holds next to the lane's 4 * CG corner sums.
+constexpr int gather_batch(int cg) { return cg >= 8 ? 4 : 8; }
+
+// CG: channels per gather lane (4 or 8). NACC: 4 = one accumulator per bilinear corner (conflict-free,
 // no colour passes); 1 = a single accumulator updated in four colour passes per round of tasks
 // (cells of one x/y parity never share a pixel), for bands where four accumulators do not fit.
 // Four waves per SIMD (<= 128 VGPRs) let two 512-thread workgroups share a CU.
@@ -875,6 +1034,7 @@ bwd_value_kernel(const ValueParams p) {
       for (int k = 0; k < 4; ++k)
 #pragma unroll
         for (int e = 0; e < CG; ++e) s[k][e] = 0.0f;
+      constexpr int kGatherBatch = gather_batch(CG);
       for (int e0 = ebeg; e0 < eend; e0 += kGatherBatch) {
         float u[kGatherBatch], v[kGatherBatch], fy[kGatherBatch];
         float g[kGatherBatch][CG];
@@ -926,7 +1086,9 @@ bwd_value_kernel(const ValueParams p) {
                   *reinterpret_cast<float4*>(ap + e) = o;
                 }
               } else {
-                for (int e = 0; e < nch; ++e) ap[e] += s[k][e];
+#pragma unroll
+                for (int e = 0; e < CG; ++e)
+                  if (e < nch) ap[e] += s[k][e];
               }
             }
           }

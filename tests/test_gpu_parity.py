@@ -186,17 +186,25 @@ def test_global_gather_path_and_many_bands(monkeypatch):
     assert_close(ga, g["grad_attn"], 1e-4, "grad_attn")
 
 
+@pytest.mark.parametrize("channels", [4, 8])
 @pytest.mark.parametrize("accumulators", [1, 4])
-@pytest.mark.parametrize("list_cap", [None, 256])
-def test_grad_value_accumulator_modes_and_segments(monkeypatch, accumulators, list_cap):
-    """grad_value with one band accumulator (colour passes) and with one per bilinear corner, with a
-    record list large enough for one segment per band and small enough to force several."""
+@pytest.mark.parametrize("segments", [False, True])
+def test_grad_value_accumulator_modes_and_segments(monkeypatch, accumulators, segments, channels):
+    """grad_value with one band accumulator (colour passes) and with one per bilinear corner, with
+    4 and 8 channels per gather lane, with each workgroup's records in one list segment and in
+    several."""
     monkeypatch.setenv("MSDA_BWD_ACCUMULATORS", str(accumulators))
-    if list_cap:
-        monkeypatch.setenv("MSDA_BWD_LIST", str(list_cap))
-    shapes = ((24, 24), (12, 12))
-    value, loc, attn, grad = make_inputs(77, 2, 4, 16, 700, shapes, 2)
-    _note(f"accumulators={accumulators} list_cap={list_cap}")
+    monkeypatch.setenv("MSDA_BWD_VALUE_CG", str(channels))
+    if not segments:
+        shapes, batch, heads, queries = ((24, 24), (12, 12)), 2, 4, 700
+    elif accumulators == 1:
+        shapes, batch, heads, queries = ((24, 24), (12, 12)), 2, 4, 700
+        monkeypatch.setenv("MSDA_BWD_LIST", "256")
+    else:
+        # a long query axis puts several list capacities' worth of records in each band
+        shapes, batch, heads, queries = ((24, 24),), 1, 2, 12000
+    value, loc, attn, grad = make_inputs(77, batch, heads, 16, queries, shapes, 2)
+    _note(f"accumulators={accumulators} segments={segments} channels={channels} queries={queries}")
     out, (gv, gl, ga) = _run(value, shapes, loc, attn, grad)
     rv, rl, ra = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
     assert_close(gv, rv, 1e-4, "grad_value")
