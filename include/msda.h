@@ -87,9 +87,10 @@ int msda_fwd(const void* value, int value_dtype,
 
 /*
  * Device workspace msda_bwd needs for this shape, in bytes (>= 0), or a negative MSDA_ERR_* code.
- * It holds one 16-byte record per sample (batch * n_heads * n_levels * len_query * n_points),
- * written by the per-sample pass and read by the grad_value pass, and is only needed when
- * grad_value is requested. It plays the role of the scratch an XLA FFI handler obtains from
+ * It holds 16-byte per-sample records binned by (batch * head slice, band of image rows, block of
+ * queries), with a count per bin, written by the per-sample pass and read by the grad_value pass;
+ * it is only needed when grad_value is requested. The size depends on the shape and the device
+ * (its CU count and LDS size), not on the dtypes. It plays the role of the scratch an XLA FFI handler obtains from
  * ffi::ScratchAllocator (the reference has no counterpart: JAX autodiff materialises its own
  * intermediates, ops.py:120-134).
  */
@@ -109,6 +110,8 @@ int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_qu
  * grad_output_dtype (the forward's output dtype). workspace: 16-byte aligned device memory of at
  * least msda_bwd_workspace_size() bytes (workspace_bytes says how many), or NULL when grad_value
  * is NULL; its contents on entry do not matter. Calls that share a workspace must not overlap.
+ * Limits (MSDA_ERR_UNSUPPORTED beyond them): levels of at most 32000 rows and columns, and
+ * len_query * n_heads * head_dim < 2^30.
  */
 int msda_bwd(const void* value, int value_dtype,
              const float* sampling_locations, const float* attention_weights,

@@ -529,8 +529,9 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   for (int l = 0; l < n_levels; ++l)
     if (s.h[l] > 32000 || s.w[l] > 32000)
       return fail(MSDA_ERR_UNSUPPORTED, "level %d (%d x %d) exceeds 32000 rows or columns", l, s.h[l], s.w[l]);
-  if (static_cast<int64_t>(len_query) * n_heads * head_dim > 0x7fffffff)
-    return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * head_dim exceeds 2^31");
+  // grad_value gathers address one batch entry's grad_output rows by 32-bit byte offsets
+  if (static_cast<int64_t>(len_query) * n_heads * head_dim >= (int64_t{1} << 30))
+    return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * head_dim reaches 2^30");
   const int vec = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 16), {{value, vbytes}, {grad_output, gbytes}});
   const int ns = env_int("MSDA_BWD_GROUPED", 0) ? samples_bound(n_levels, n_points) : 0;
   const int shift = lpq_shift_for(head_dim, vec);

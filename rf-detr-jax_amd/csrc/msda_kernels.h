@@ -867,9 +867,78 @@ __device__ __forceinline__ void load_gc(const void* __restrict__ base, bool bf16
   }
 }
 
+// One grad_value task: s[k][e] += w_k * g[q][ch0 + e] over the records [ebeg, eend) of one cell,
+// w_k the record's corner weights (ops.py:123-128 with the attention weight folded in, corner order
+// 00, 10, 01, 11). MODE 0 / 1: f32 / bf16 rows of CG channels at 16-byte-aligned offsets, addressed
+// by a 32-bit byte offset from the slice's first row (one address operation per row); MODE 2:
+// any dtype, alignment and partial channel group.
+template <int CG, int MODE>
+__device__ __forceinline__ void cell_sums(const float4* list, int ebeg, int eend, const void* gbase, bool gbf, bool gv4,
+                                          int ch0, int nch, int Q, int gqstride, float (&s)[4][CG]);
+
 // grad_output rows a grad_value lane fetches together (with their weights): as many as the register
 // budget holds next to the lane's 4 * CG corner sums.
 constexpr int gather_batch(int cg) { return cg >= 8 ? 4 : 8; }
+
+template <int CG, int MODE>
+__device__ __forceinline__ void cell_sums(const float4* list, int ebeg, int eend, const void* gbase, bool gbf, bool gv4,
+                                          int ch0, int nch, int Q, int gqstride, float (&s)[4][CG]) {
+  constexpr int kGatherBatch = gather_batch(CG);
+  const char* gb = static_cast<const char*>(gbase);
+  for (int e0 = ebeg; e0 < eend; e0 += kGatherBatch) {
+    float u[kGatherBatch], v[kGatherBatch], fy[kGatherBatch];
+    float g[kGatherBatch][CG];
+#pragma unroll
+    for (int i = 0; i < kGatherBatch; ++i) {
+      if (e0 + i < eend) {
+        const float4 w = list[e0 + i];
+        u[i] = w.x;
+        v[i] = w.y;
+        fy[i] = w.z;
+        // the record's grad_output row offset (q * H * D, q clamped to Q - 1 when placed; < 2^30,
+        // host-checked) plus this lane's channel group
+        const unsigned el = static_cast<unsigned>(__float_as_int(w.w)) + static_cast<unsigned>(ch0);
+        if constexpr (MODE == 0) {
+          const float4* r = reinterpret_cast<const float4*>(gb + el * 4u);
+#pragma unroll
+          for (int k = 0; k < CG; k += 4) {
+            const float4 x = r[k / 4];
+            g[i][k] = x.x;
+            g[i][k + 1] = x.y;
+            g[i][k + 2] = x.z;
+            g[i][k + 3] = x.w;
+          }
+        } else if constexpr (MODE == 1) {
+          const uint2* r = reinterpret_cast<const uint2*>(gb + el * 2u);
+#pragma unroll
+          for (int k = 0; k < CG; k += 4) {
+            const uint2 x = r[k / 4];
+            g[i][k] = __uint_as_float(x.x << 16);
+            g[i][k + 1] = __uint_as_float(x.x & 0xffff0000u);
+            g[i][k + 2] = __uint_as_float(x.y << 16);
+            g[i][k + 3] = __uint_as_float(x.y & 0xffff0000u);
+          }
+        } else {
+          load_gc<CG>(gbase, gbf, gv4, static_cast<int>(el), nch, g[i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kGatherBatch; ++i) {
+      if (e0 + i < eend) {
+        const float w00 = u[i] * (1.0f - fy[i]), w10 = v[i] * (1.0f - fy[i]);
+        const float w01 = u[i] * fy[i], w11 = v[i] * fy[i];
+#pragma unroll
+        for (int e = 0; e < CG; ++e) {
+          s[0][e] = fmaf(w00, g[i][e], s[0][e]);
+          s[1][e] = fmaf(w10, g[i][e], s[1][e]);
+          s[2][e] = fmaf(w01, g[i][e], s[2][e]);
+          s[3][e] = fmaf(w11, g[i][e], s[3][e]);
+        }
+      }
+    }
+  }
+}
 
 // CG: channels per gather lane (4 or 8). NACC: 4 = one accumulator per bilinear corner (conflict-free,
 // no colour passes); 1 = a single accumulator updated in four colour passes per round of tasks
@@ -1008,7 +1077,7 @@ bwd_value_kernel(const ValueParams p) {
         for (int u = 0; u < U; ++u)
           if (pos[u] >= 0 && pos[u] < p.cap)
             list[pos[u]] = make_float4(__uint_as_float(rr[u].y), __uint_as_float(rr[u].z), __uint_as_float(rr[u].w),
-                                       __int_as_float(qbs[u] * p.qblock + static_cast<int>(rr[u].x >> 16)));
+                                       __int_as_float(min(qbs[u] * p.qblock + static_cast<int>(rr[u].x >> 16), Q - 1) * gqstride));
       }
     }
     __syncthreads();
@@ -1034,37 +1103,12 @@ bwd_value_kernel(const ValueParams p) {
       for (int k = 0; k < 4; ++k)
 #pragma unroll
         for (int e = 0; e < CG; ++e) s[k][e] = 0.0f;
-      constexpr int kGatherBatch = gather_batch(CG);
-      for (int e0 = ebeg; e0 < eend; e0 += kGatherBatch) {
-        float u[kGatherBatch], v[kGatherBatch], fy[kGatherBatch];
-        float g[kGatherBatch][CG];
-#pragma unroll
-        for (int i = 0; i < kGatherBatch; ++i) {
-          if (e0 + i < eend) {
-            const float4 w = list[e0 + i];
-            u[i] = w.x;
-            v[i] = w.y;
-            fy[i] = w.z;
-            // the query index is < Q by construction; the clamp only keeps a broken invariant in bounds
-            const int q = static_cast<int>(min(static_cast<unsigned>(__float_as_int(w.w)), static_cast<unsigned>(Q - 1)));
-            load_gc<CG>(gbase, gbf, gv4, q * gqstride + ch0, nch, g[i]);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < kGatherBatch; ++i) {
-          if (e0 + i < eend) {
-            const float w00 = u[i] * (1.0f - fy[i]), w10 = v[i] * (1.0f - fy[i]);
-            const float w01 = u[i] * fy[i], w11 = v[i] * fy[i];
-#pragma unroll
-            for (int e = 0; e < CG; ++e) {
-              s[0][e] = fmaf(w00, g[i][e], s[0][e]);
-              s[1][e] = fmaf(w10, g[i][e], s[1][e]);
-              s[2][e] = fmaf(w01, g[i][e], s[2][e]);
-              s[3][e] = fmaf(w11, g[i][e], s[3][e]);
-            }
-          }
-        }
-      }
+      // row loads specialised outside the record loop: f32 or bf16 rows of full 16-byte-aligned
+      // channel groups, or the general path
+      const int mode = (nch == CG && gv4) ? (gbf ? 1 : 0) : 2;
+      if (mode == 0) cell_sums<CG, 0>(list, ebeg, eend, gbase, gbf, gv4, ch0, nch, Q, gqstride, s);
+      else if (mode == 1) cell_sums<CG, 1>(list, ebeg, eend, gbase, gbf, gv4, ch0, nch, Q, gqstride, s);
+      else cell_sums<CG, 2>(list, ebeg, eend, gbase, gbf, gv4, ch0, nch, Q, gqstride, s);
       // With one accumulator, cells of one colour (x and y parity) are updated per pass.
       const int color = (kx & 1) | ((ky & 1) << 1);
       for (int c = 0; c < (NACC == 4 ? 1 : 4); ++c) {
