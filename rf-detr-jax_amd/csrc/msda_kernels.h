@@ -1032,16 +1032,24 @@ bwd_value_kernel(const ValueParams p) {
   // Segments of at most `cap` records (a segment's records all fit the list).
   for (int s_lo = 0; s_lo < NR;) {
     const int s_hi = min(NR, s_lo + p.cap);
+    // When the segment is at most U records per thread, pass A also copies each record into the
+    // (not yet used) list LDS at its load position, and pass B reads it from there instead of
+    // loading it from global memory again.
+    const bool one_pass = s_hi - s_lo <= U * nt;
+    uint4* stage = reinterpret_cast<uint4*>(list);
     // ---- pass A: per-cell counts
     {
       int qb = 0;
       for (int f = s_lo + t; f < s_hi; f += U * nt) {
-        uint32_t keys[U];
+        uint4 rr[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) keys[u] = (f + u * nt < s_hi) ? record(f + u * nt, qb).x & 0xffffu : 0xffffu;
+        for (int u = 0; u < U; ++u) rr[u] = (f + u * nt < s_hi) ? record(f + u * nt, qb) : make_uint4(0xffffu, 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-          if (static_cast<int>(keys[u]) < ncell_max) atomicAdd(&cnt[keys[u]], 1);
+        for (int u = 0; u < U; ++u) {
+          const uint32_t key = rr[u].x & 0xffffu;
+          if (static_cast<int>(key) < ncell_max) atomicAdd(&cnt[key], 1);
+          if (one_pass && f + u * nt < s_hi) stage[f + u * nt - s_lo] = rr[u];
+        }
       }
     }
     __syncthreads();
@@ -1057,7 +1065,36 @@ bwd_value_kernel(const ValueParams p) {
       if (busy) nonempty[base + __popcll(mask & ((uint64_t{1} << lane) - 1))] = static_cast<uint16_t>(key);
     }
     // ---- pass B: each record goes to its place in cell order
-    {
+    auto entry = [&](const uint4& r, int qb) {
+      return make_float4(__uint_as_float(r.y), __uint_as_float(r.z), __uint_as_float(r.w),
+                         __int_as_float(min(qb * p.qblock + static_cast<int>(r.x >> 16), Q - 1) * gqstride));
+    };
+    if (one_pass) {
+      // records from the staging copy; every thread reads its records before any is placed
+      uint4 rr[U];
+      int qbs[U], pos[U];
+      int qb = 0;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int f = s_lo + t + u * nt;
+        if (f < s_hi) {
+          while (binpre[qb + 1] <= f) ++qb;
+          rr[u] = stage[f - s_lo];
+        } else {
+          rr[u] = make_uint4(0xffffu, 0, 0, 0);
+        }
+        qbs[u] = qb;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int key = static_cast<int>(rr[u].x & 0xffffu);
+        pos[u] = key < ncell_max ? off[key] + atomicAdd(&cnt[key], 1) : -1;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (pos[u] >= 0 && pos[u] < p.cap) list[pos[u]] = entry(rr[u], qbs[u]);
+    } else {
       int qb = 0;
       for (int f = s_lo + t; f < s_hi; f += U * nt) {
         uint4 rr[U];
@@ -1075,9 +1112,7 @@ bwd_value_kernel(const ValueParams p) {
         }
 #pragma unroll
         for (int u = 0; u < U; ++u)
-          if (pos[u] >= 0 && pos[u] < p.cap)
-            list[pos[u]] = make_float4(__uint_as_float(rr[u].y), __uint_as_float(rr[u].z), __uint_as_float(rr[u].w),
-                                       __int_as_float(min(qbs[u] * p.qblock + static_cast<int>(rr[u].x >> 16), Q - 1) * gqstride));
+          if (pos[u] >= 0 && pos[u] < p.cap) list[pos[u]] = entry(rr[u], qbs[u]);
       }
     }
     __syncthreads();
