@@ -260,6 +260,7 @@ msda::LevelDesc level_desc(const Shape& s, int l, int lds, int band_rows, int ba
   d.lds = lds;
   d.band_rows = band_rows;
   d.band_first = band_first;
+  d.band_magic = band_rows > 1 ? static_cast<uint32_t>(((uint64_t{1} << 32) + band_rows - 1) / band_rows) : 0u;
   return d;
 }
 
@@ -625,7 +626,12 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
       for (int l = 0; l < n_levels; ++l) {
         p.lv[l].band_rows = vp.lv[l].band_rows;
         p.lv[l].band_first = vp.lv[l].band_first;
+        p.lv[l].band_magic = vp.lv[l].band_magic;
       }
+      // a workgroup's bin region: 16-byte records addressed by 32-bit byte offsets
+      const int64_t region = static_cast<int64_t>(p.hg) * bp.nwork * bp.nqb * bp.qblock * n_points;
+      if (region >= (int64_t{1} << 28)) return fail(MSDA_ERR_UNSUPPORTED, "grad_value record bins of a workgroup reach 2^28 records");
+      p.small_bins = region < (int64_t{1} << 24) ? 1 : 0;
       // per (head, item) record counters after the staged value rows
       plan.lds = align16(plan.lds) + align16(static_cast<int64_t>(p.hg) * bp.nwork * 4);
       if (plan.lds > dev.lds_bytes) return fail(MSDA_ERR_UNSUPPORTED, "per-sample pass needs %d bytes of LDS", plan.lds);

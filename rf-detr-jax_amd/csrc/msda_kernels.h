@@ -53,7 +53,14 @@ struct LevelDesc {
   int lds;         // per-sample kernels: element offset of the staged level inside a head's LDS region, -1 = L2
   int band_rows;   // grad_value kernel: image rows per band
   int band_first;  // grad_value kernel: index of the level's first band among a slice's (level, band) items
+  uint32_t band_magic;  // ceil(2^32 / band_rows) (0 when band_rows == 1): row / band_rows = umulhi(row, magic)
 };
+
+// row / band_rows for 0 <= row < 2^16 and band_rows < 2^16: with magic = ceil(2^32 / band_rows),
+// row * magic / 2^32 exceeds row / band_rows by less than 2^-16 < 1 / band_rows, so the floor is exact.
+__device__ __forceinline__ int band_of(int row, const LevelDesc& L) {
+  return L.band_rows == 1 ? row : static_cast<int>(__umulhi(static_cast<uint32_t>(row), L.band_magic));
+}
 
 // Forward and per-sample backward kernels.
 struct SampleParams {
@@ -67,6 +74,7 @@ struct SampleParams {
   float* dloc;       // backward: grad_sampling_locations, or null
   float* dattn;      // backward: grad_attention_weights, or null
   uint4* bins;       // backward: grad_value records, binned by (slice, level band), or null
+  int small_bins;    // a workgroup's bin region holds < 2^24 records (24-bit index arithmetic)
   int* bin_counts;   // backward: records per (slice, level band, query block)
   int nwork;         // backward: (level, band) items per slice
   int heads, dim, queries, levels, points;
@@ -345,6 +353,22 @@ __device__ __forceinline__ void load_any_rot(const void* base, int64_t off, bool
 #pragma unroll
       for (int i = 0; i < E; ++i) o[k * E + i] = t[i];
     }
+  }
+}
+
+// load_any_rot with a 32-bit element offset from a byte base (byte offset formed in 32 bits)
+template <typename VT, int VEC>
+__device__ __forceinline__ void load_any_rot32(const char* base, uint32_t off, bool is_bf16, int rot, float (&o)[VEC]) {
+  constexpr int N = rot_chunks<VT, VEC>();
+  constexpr int E = VEC / N;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const uint32_t e = off + static_cast<uint32_t>(((k + rot) & (N - 1)) * E);
+    float t[E];
+    if (is_bf16) load_vec<bf16_t, E>(reinterpret_cast<const bf16_t*>(base + e * 2u), t);
+    else load_vec<float, E>(reinterpret_cast<const float*>(base + e * 4u), t);
+#pragma unroll
+    for (int i = 0; i < E; ++i) o[k * E + i] = t[i];
   }
 }
 
@@ -652,17 +676,49 @@ __device__ __forceinline__ void corner_dots(const VT* base, const Bilinear& c, c
 
 // Appends a record to the bin of (slice n, item) for this workgroup's query block; the rank comes
 // from the workgroup's LDS counter of that (head, item).
-__device__ __forceinline__ void emit_record(const SampleParams& p, int* lcnt, int hl, int item, int key, int qoff, int64_t n,
-                                            int qb, uint4 payload) {
+// base[idx] with the byte offset formed in 32 bits (the caller guarantees idx * sizeof(T) < 2^32):
+// a uniform base plus a 32-bit lane offset compiles to one address operand per access.
+template <typename T>
+__device__ __forceinline__ T* at(T* base, uint32_t idx) {
+  using C = typename std::conditional<std::is_const<T>::value, const char, char>::type;
+  return reinterpret_cast<T*>(reinterpret_cast<C*>(base) + idx * static_cast<uint32_t>(sizeof(T)));
+}
+
+// Per-workgroup bases of the per-sample pass: row (b, q_lo, h0) of the [B, Q, H, ...] tensors and
+// the record bins of slice (b, h0). Lanes index them with 32-bit offsets.
+struct SampleBases {
+  const float2* loc;
+  const float* attn;
+  const char* gout;  // bytes
+  float* dattn;
+  float2* dloc;
+  uint4* bins;
+};
+
+__device__ __forceinline__ void emit_record(const SampleParams& p, const SampleBases& sb, int* lcnt, int hl, int item, int key,
+                                            int qoff, int qb, uint4 payload) {
   const int pos = atomicAdd(&lcnt[hl * p.nwork + item], 1);
   payload.x = static_cast<uint32_t>(key) | (static_cast<uint32_t>(qoff) << 16);
-  p.bins[((n * p.nwork + item) * p.nqb + qb) * static_cast<int64_t>(p.qblock) * p.points + pos] = payload;
+  // bins of the workgroup's slices: [hg][nwork][nqb][qblock * points]; below 2^24 records in all
+  // (small_bins) every factor fits a 24-bit multiply, and the region stays below 2^28 records
+  // (16-byte offsets in 32 bits) in any case (both checked on the host)
+  const uint32_t subcap = static_cast<uint32_t>(p.qblock) * static_cast<uint32_t>(p.points);
+  uint32_t idx;
+  if (p.small_bins) {
+    const uint32_t bin = __umul24(__umul24(static_cast<uint32_t>(hl), static_cast<uint32_t>(p.nwork)) + static_cast<uint32_t>(item),
+                                  static_cast<uint32_t>(p.nqb)) + static_cast<uint32_t>(qb);
+    idx = __umul24(bin, subcap) + static_cast<uint32_t>(pos);
+  } else {
+    idx = ((static_cast<uint32_t>(hl) * p.nwork + item) * p.nqb + qb) * subcap + static_cast<uint32_t>(pos);
+  }
+  *at(sb.bins, idx) = payload;
 }
 
 template <typename VT, int VEC, int N, bool kStaged>
 __device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const float (&g)[VEC], int s0, int LP, int& l, int& pt,
                                          const SampleParams& p, const SampleLane& ln, const VT* hlds,
-                                         const VT* __restrict__ vs, int64_t row, int* lcnt, int qoff, int64_t n, int qb) {
+                                         const VT* __restrict__ vs, const SampleBases& sb, uint32_t lrow, int* lcnt, int qoff,
+                                         int qb) {
   const int D = p.dim;
   const int lpq = 1 << p.lpq_shift;
 #pragma unroll
@@ -679,16 +735,15 @@ __device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const float (&g)[
       d01 = group_sum(d01, lpq);
       d11 = group_sum(d11, lpq);
       if (ln.j == 0) {
-        const int64_t si = row * LP + s0 + u;  // sample index in [B, Q, H, L, P]
+        const uint32_t si = lrow * static_cast<uint32_t>(LP) + static_cast<uint32_t>(s0 + u);  // sample, from the workgroup's row
         // dA = sum_c w_c D_c (the sample itself); d out / d ix = gy (m10 D10 - m00 D00) + fy (m11 D11 - m01 D01)
-        if (p.dattn) p.dattn[si] = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
-        if (p.dloc) {
+        if (sb.dattn) *at(sb.dattn, si) = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
+        if (sb.dloc) {
           const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
           const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
           const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
           // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
-          *reinterpret_cast<float2*>(p.dloc + 2 * si) =
-              make_float2(a * L.fw * dx, a * L.fh * dy);
+          *at(sb.dloc, si) = make_float2(a * L.fw * dx, a * L.fh * dy);
         }
         if (p.bins) {
           // Non-finite weights (NaN or infinite coordinates) go to the clipped first corner's cell,
@@ -700,10 +755,15 @@ __device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const float (&g)[
           if (x0 >= -1 && x0 <= L.w - 1) {
             const int ya = y0 >= 0 && y0 < L.h ? y0 : -1;
             const int yb = y0 + 1 >= 0 && y0 + 1 < L.h ? y0 + 1 : -1;
-            const int ba = ya >= 0 ? ya / L.band_rows : -1;
-            const int bb = yb >= 0 ? yb / L.band_rows : -1;
-            if (ba >= 0) emit_record(p, lcnt, ln.hl, L.band_first + ba, (y0 - ba * L.band_rows + 1) * (L.w + 1) + x0 + 1, qoff, n, qb, payload);
-            if (bb >= 0 && bb != ba) emit_record(p, lcnt, ln.hl, L.band_first + bb, (y0 - bb * L.band_rows + 1) * (L.w + 1) + x0 + 1, qoff, n, qb, payload);
+            const int ba = ya >= 0 ? band_of(ya, L) : -1;
+            const int bb = yb >= 0 ? band_of(yb, L) : -1;
+            // key: the cell's (row within the band + 1, x0 + 1), row-major over (band_rows + 1) x (w + 1)
+            auto key = [&](int band) {
+              const uint32_t r = static_cast<uint32_t>(y0 + 1) - __umul24(static_cast<uint32_t>(band), static_cast<uint32_t>(L.band_rows));
+              return static_cast<int>(__umul24(r, static_cast<uint32_t>(L.w + 1)) + static_cast<uint32_t>(x0 + 1));
+            };
+            if (ba >= 0) emit_record(p, sb, lcnt, ln.hl, L.band_first + ba, key(ba), qoff, qb, payload);
+            if (bb >= 0 && bb != ba) emit_record(p, sb, lcnt, ln.hl, L.band_first + bb, key(bb), qoff, qb, payload);
           }
         }
       }
@@ -725,31 +785,41 @@ bwd_sample_kernel(const SampleParams p) {
   const int D = p.dim;
   const int64_t slice_elems = p.len_value * D;
   const VT* __restrict__ vg = static_cast<const VT*>(p.value) + (static_cast<int64_t>(it.b) * p.heads + it.h0) * slice_elems;
-  const int h = it.h0 + ln.hl;
   const int LP = p.levels * p.points;
   const int q_lo = it.qb * p.qblock;
   const int q_hi = min(p.queries, q_lo + p.qblock);
-  const float2* __restrict__ loc2 = reinterpret_cast<const float2*>(p.loc);
   const bool gbf = p.gout_bf16 != 0;
-  const int64_t n = static_cast<int64_t>(it.b) * p.heads + h;
+  // the workgroup's row (b, q_lo, h0) of the [B, Q, H, ...] tensors and its slices' record bins;
+  // lane row r = (q - q_lo) * H + hl indexes them with 32-bit offsets
+  const int64_t wrow = (static_cast<int64_t>(it.b) * p.queries + q_lo) * p.heads + it.h0;
+  SampleBases sb;
+  sb.loc = reinterpret_cast<const float2*>(p.loc) + wrow * LP;
+  sb.attn = p.attn + wrow * LP;
+  sb.gout = static_cast<const char*>(p.gout) + wrow * D * (gbf ? 2 : 4);
+  sb.dattn = p.dattn ? p.dattn + wrow * LP : nullptr;
+  sb.dloc = p.dloc ? reinterpret_cast<float2*>(p.dloc) + wrow * LP : nullptr;
+  sb.bins = p.bins ? p.bins + (static_cast<int64_t>(it.b) * p.heads + it.h0) * p.nwork * p.nqb * static_cast<int64_t>(p.qblock) * p.points
+                   : nullptr;
+  auto lrow_of = [&](int q) { return __umul24(static_cast<uint32_t>(q - q_lo), static_cast<uint32_t>(p.heads)) + static_cast<uint32_t>(ln.hl); };
   // per (head, item) record counters of this workgroup, after the staged value rows
   int* lcnt = reinterpret_cast<int*>(lds_raw + align16i(p.hg * p.head_lds * static_cast<int>(sizeof(VT))));
   const int ncnt = p.bins ? p.hg * p.nwork : 0;
   for (int i = threadIdx.x; i < ncnt; i += blockDim.x) lcnt[i] = 0;
   constexpr int QU = query_group(NS, VEC, true);
   const int q_first = q_lo + ln.qs;
-  const int64_t row_first = (static_cast<int64_t>(it.b) * p.queries + q_first) * p.heads + h;  // (b, q, h)
-  const int64_t row_step = static_cast<int64_t>(ln.qpp) * p.heads;
+  const uint32_t lrow_first = lrow_of(q_first);
+  const uint32_t lrow_step = __umul24(static_cast<uint32_t>(ln.qpp), static_cast<uint32_t>(p.heads));
   SampleIn<NS == 0 ? 1 : NS> in[QU];
   float g[QU][VEC];
   // grad_output rows and sample inputs of a group of queries are requested together; the first
   // group's before the staging copy, so their latency overlaps it.
-  auto load_gout = [&](int64_t row0, int q0) {
+  auto load_gout = [&](uint32_t lrow0, int q0) {
 #pragma unroll
     for (int i = 0; i < QU; ++i) {
       if (q0 + i * ln.qpp < q_hi) {
         if (ln.lane_on) {
-          load_any_rot<VT, VEC>(p.gout, (row0 + i * row_step) * D + ln.c0, gbf, ln.rot, g[i]);
+          load_any_rot32<VT, VEC>(sb.gout, (lrow0 + i * lrow_step) * static_cast<uint32_t>(D) + static_cast<uint32_t>(ln.c0), gbf,
+                                  ln.rot, g[i]);
         } else {
 #pragma unroll
           for (int k = 0; k < VEC; ++k) g[i][k] = 0.0f;
@@ -757,10 +827,18 @@ bwd_sample_kernel(const SampleParams p) {
       }
     }
   };
+  auto load_inputs = [&](uint32_t lrow0, int q0) {
+#pragma unroll
+    for (int i = 0; i < QU; ++i)
+      if (q0 + i * ln.qpp < q_hi) {
+        const uint32_t r = (lrow0 + i * lrow_step) * static_cast<uint32_t>(LP);
+        load_in<NS == 0 ? 1 : NS>(in[i], at(sb.loc, r), at(sb.attn, r), 0, LP);
+      }
+  };
   if constexpr (NS > 0) {
     if (ln.active) {
-      load_gout(row_first, q_first);
-      load_group<NS, QU>(in, loc2, p.attn, row_first, row_step, q_first, ln.qpp, q_hi, LP);
+      load_gout(lrow_first, q_first);
+      load_inputs(lrow_first, q_first);
     }
   }
   stage_group(p, lds, vg);
@@ -769,11 +847,11 @@ bwd_sample_kernel(const SampleParams p) {
   const VT* __restrict__ vs = vg + ln.hl * slice_elems + ln.c0;
   const VT* hlds = lds + ln.hl * p.head_lds + ln.c0;
   if constexpr (NS > 0) {
-    for (int qg = q_first; ln.active && qg < q_hi; qg += QU * ln.qpp) {
-      const int64_t row0 = row_first + static_cast<int64_t>((qg - q_first) / ln.qpp) * row_step;
+    uint32_t lrow0 = lrow_first;
+    for (int qg = q_first; ln.active && qg < q_hi; qg += QU * ln.qpp, lrow0 += QU * lrow_step) {
       if (qg != q_first) {
-        load_gout(row0, qg);
-        load_group<NS, QU>(in, loc2, p.attn, row0, row_step, qg, ln.qpp, q_hi, LP);
+        load_gout(lrow0, qg);
+        load_inputs(lrow0, qg);
       }
       wait_vmem();
 #pragma unroll
@@ -781,19 +859,20 @@ bwd_sample_kernel(const SampleParams p) {
         const int q = qg + i * ln.qpp;
         if (q < q_hi) {
           int l = 0, pt = 0;
-          bwd_pass<VT, VEC, NS, kStaged>(in[i], g[i], 0, LP, l, pt, p, ln, hlds, vs, row0 + i * row_step, lcnt, q - q_lo, n, it.qb);
+          bwd_pass<VT, VEC, NS, kStaged>(in[i], g[i], 0, LP, l, pt, p, ln, hlds, vs, sb, lrow0 + i * lrow_step, lcnt, q - q_lo, it.qb);
         }
       }
     }
   } else {
-    for (int q = q_first; ln.active && q < q_hi; q += ln.qpp) {
-      const int64_t row = (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h;
-      load_gout(row, q);
+    uint32_t lrow = lrow_first;
+    for (int q = q_first; ln.active && q < q_hi; q += ln.qpp, lrow += lrow_step) {
+      load_gout(lrow, q);
       int l = 0, pt = 0;
+      const uint32_t r = lrow * static_cast<uint32_t>(LP);
       for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
         SampleIn<kPassBatch> f;
-        load_in<kPassBatch>(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
-        bwd_pass<VT, VEC, kPassBatch, kStaged>(f, g[0], s0, LP, l, pt, p, ln, hlds, vs, row, lcnt, q - q_lo, n, it.qb);
+        load_in<kPassBatch>(f, at(sb.loc, r), at(sb.attn, r), s0, LP);
+        bwd_pass<VT, VEC, kPassBatch, kStaged>(f, g[0], s0, LP, l, pt, p, ln, hlds, vs, sb, lrow, lcnt, q - q_lo, it.qb);
       }
     }
   }
