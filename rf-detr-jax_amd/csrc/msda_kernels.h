@@ -389,8 +389,18 @@ __device__ __forceinline__ void store_any_rot(void* base, int64_t off, bool is_b
   }
 }
 
-// Cooperative copy global -> LDS of `count` elements. Each thread issues a batch of loads before
-// any store, so the copy is bounded by bandwidth rather than by one load latency per step.
+// Waits until every vector-memory operation this wave issued has completed (gfx9 s_waitcnt
+// encoding: vmcnt 0, expcnt and lgkmcnt left at their maxima). Placed where a group of loads is
+// about to be consumed and before the group's stores: vmcnt counts loads and stores in issue order,
+// so once the wait is explicit the compiler needs no later vmcnt waits, which would otherwise also
+// wait for the acknowledgement of every store issued before them.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Cooperative copy global -> LDS of `count` elements. With 16-byte rows the copy goes straight
+// from global memory into LDS (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at the
+// wave's LDS base + 16 i, no registers involved), each wave streaming whole 1 KB blocks, so every
+// block is in flight at once; the wave waits for its own transfers before returning (the caller's
+// barrier then publishes them). Otherwise each thread issues a batch of loads before any store.
 template <typename VT>
 __device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, int count, bool vec16) {
   constexpr int U = 8;
@@ -399,15 +409,12 @@ __device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, 
     const int n16 = static_cast<int>((static_cast<int64_t>(count) * sizeof(VT)) / 16);
     const uint4* s = reinterpret_cast<const uint4*>(src);
     uint4* d = reinterpret_cast<uint4*>(dst);
-    int i = threadIdx.x;
-    for (; i + (U - 1) * nt < n16; i += U * nt) {
-      uint4 r[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) r[u] = s[i + u * nt];
-#pragma unroll
-      for (int u = 0; u < U; ++u) d[i + u * nt] = r[u];
-    }
-    for (; i < n16; i += nt) d[i] = s[i];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = nt >> 6;
+    const int nblk = n16 >> 6;  // whole 1 KB blocks
+    for (int blk = wave; blk < nblk; blk += nwaves)
+      __builtin_amdgcn_global_load_lds(s + blk * 64 + lane, (MSDA_LDS void*)(d + blk * 64), 16, 0, 0);
+    for (int i = (nblk << 6) + static_cast<int>(threadIdx.x); i < n16; i += nt) d[i] = s[i];
+    wait_vmem();
   } else {
     int i = threadIdx.x;
     for (; i + (U - 1) * nt < count; i += U * nt) {
@@ -421,12 +428,6 @@ __device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, 
   }
 }
 
-// Waits until every vector-memory operation this wave issued has completed (gfx9 s_waitcnt
-// encoding: vmcnt 0, expcnt and lgkmcnt left at their maxima). Placed where a group of loads is
-// about to be consumed and before the group's stores: vmcnt counts loads and stores in issue order,
-// so once the wait is explicit the compiler needs no later vmcnt waits, which would otherwise also
-// wait for the acknowledgement of every store issued before them.
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 __device__ __forceinline__ float group_sum(float v, int lpq) {
   for (int o = 1; o < lpq; o <<= 1) v += __shfl_xor(v, o, 64);
