@@ -495,6 +495,9 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
   p.vec16 = rows_16b(s, vbytes, value, nullptr);
   SamplePlan plan;
   if ((rc = plan_sample(s, vbytes, dev, "MSDA_FWD", shift, &p, &plan)) != MSDA_OK) return rc;
+  // one level, two points, two lanes per (query, head), every level staged: the two lanes split the
+  // samples' coordinate work (fwd_pair)
+  p.pair_share = (n_levels == 1 && n_points == 2 && shift == 1 && p.all_staged && ns == 2 && env_int("MSDA_FWD_PAIR", 1)) ? 1 : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (value_dtype == MSDA_DTYPE_BF16) return dispatch_sample<msda::bf16_t>(false, vec, ns, p, plan.grid, plan.threads, plan.lds, st);
   return dispatch_sample<float>(false, vec, ns, p, plan.grid, plan.threads, plan.lds, st);

@@ -75,6 +75,7 @@ struct SampleParams {
   float* dattn;      // backward: grad_attention_weights, or null
   uint4* bins;       // backward: grad_value records, binned by (slice, level band), or null
   int small_bins;    // a workgroup's bin region holds < 2^24 records (24-bit index arithmetic)
+  int pair_share;    // forward: one level, two points, two lanes per (query, head) (fwd_pair)
   int* bin_counts;   // backward: records per (slice, level band, query block)
   int nwork;         // backward: (level, band) items per slice
   int heads, dim, queries, levels, points;
@@ -581,6 +582,38 @@ __device__ __forceinline__ void fwd_pass(float (&acc)[VEC], const SampleIn<N>& f
   }
 }
 
+// One level, two points, two lanes per (query, head) (pair_share): lane j computes the corner
+// offsets and weights of sample j only and the two lanes exchange them, so each sample's
+// coordinates are computed once; each lane then adds its own sample first (the order of the two
+// f32 additions per channel is the only difference from fwd_pass).
+template <typename VT, int VEC>
+__device__ __forceinline__ void fwd_pair(float (&acc)[VEC], const SampleIn<2>& f, const SampleParams& p, const VT* hlds,
+                                         int rot, int j) {
+  const LevelDesc L = p.lv[0];
+  const float2 xy = j ? f.xy[1] : f.xy[0];
+  const float a = j ? f.a[1] : f.a[0];
+  const Bilinear c = bilinear(xy.x, xy.y, L, p.dim);
+  // lane swap with the neighbour: DPP quad_perm [1, 0, 3, 2] (a register move, no LDS traffic)
+  auto swap_i = [](int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); };
+  auto swap_f = [&](float v) { return __int_as_float(swap_i(__float_as_int(v))); };
+  Bilinear o;  // the partner's sample: offsets and attention-weighted corner weights
+  o.o00 = swap_i(c.o00);
+  o.o10 = swap_i(c.o10);
+  o.o01 = swap_i(c.o01);
+  o.o11 = swap_i(c.o11);
+  Bilinear m = c;
+  m.w00 = a * c.w00;
+  m.w10 = a * c.w10;
+  m.w01 = a * c.w01;
+  m.w11 = a * c.w11;
+  o.w00 = swap_f(m.w00);
+  o.w10 = swap_f(m.w10);
+  o.w01 = swap_f(m.w01);
+  o.w11 = swap_f(m.w11);
+  fwd_corners<VT, VEC, true>(acc, hlds + L.lds, m, 1.0f, rot);
+  fwd_corners<VT, VEC, true>(acc, hlds + L.lds, o, 1.0f, rot);
+}
+
 // Four waves per SIMD (<= 128 VGPRs): latency is hidden by other waves rather than by
 // registers holding the next query's inputs (measured faster on MI355X).
 template <typename VT, int VEC, int NS, bool kStaged>
@@ -625,6 +658,13 @@ fwd_kernel(const SampleParams p) {
           float acc[VEC];
 #pragma unroll
           for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
+          if constexpr (NS == 2 && kStaged) {
+            if (p.pair_share) {
+              fwd_pair<VT, VEC>(acc, in[i], p, hlds, rot, ln.j);
+              if (ln.lane_on) store_any_rot<VT, VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, rot, acc);
+              continue;
+            }
+          }
           int l = 0, pt = 0;  // level and point of the next sample (level-major order, ops.py:285)
           fwd_pass<VT, VEC, NS, kStaged>(acc, in[i], 0, LP, l, pt, p, hlds, vs, rot);
           if (ln.lane_on) store_any_rot<VT, VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, rot, acc);

@@ -212,6 +212,18 @@ def test_grad_value_accumulator_modes_and_segments(monkeypatch, accumulators, se
     assert_close(ga, ra, 1e-4, "grad_attn")
 
 
+@pytest.mark.parametrize("pair", [0, 1])
+def test_forward_paired_lanes(monkeypatch, pair):
+    """One level, two points, 16 channels (two lanes of 8 per query-head): the forward with the
+    two lanes splitting the samples' coordinate work (pair=1, the default) and without (pair=0)."""
+    monkeypatch.setenv("MSDA_FWD_PAIR", str(pair))
+    shapes = ((24, 24),)
+    value, loc, attn, grad = make_inputs(91, 2, 8, 16, 1000, shapes, 2)
+    _note(f"pair={pair}")
+    out, _ = _run(value, shapes, loc, attn, grad)
+    assert_close(out, R.ms_deform_attn_core_rows(value, shapes, loc, attn), 1e-5, "out")
+
+
 def test_level_larger_than_lds():
     """A 200x120 f32 level (1.5 MB per slice) plus a small one: global-gather forward, banded backward."""
     shapes = ((200, 120), (10, 12))
