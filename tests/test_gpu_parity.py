@@ -224,6 +224,30 @@ def test_forward_paired_lanes(monkeypatch, pair):
     assert_close(out, R.ms_deform_attn_core_rows(value, shapes, loc, attn), 1e-5, "out")
 
 
+@pytest.mark.parametrize("variant", [
+    {"MSDA_BWD_GROUPED": "1"},
+    {"MSDA_FWD_GROUPED": "0"},
+    {"MSDA_FWD_MAX_VEC": "16"},
+    {"MSDA_BWD_MAX_VEC": "8"},
+    {"MSDA_FWD_HEADS": "2", "MSDA_BWDS_HEADS": "2"},
+], ids=lambda v: ",".join(f"{k}={x}" for k, x in v.items()))
+@pytest.mark.parametrize("shapes", [((24, 24),), ((24, 24), (12, 12))], ids=["one_level", "two_levels"])
+def test_kernel_variants(monkeypatch, variant, shapes):
+    """The per-sample kernels' other launch variants (grouped query inputs in the backward, one
+    query at a time in the forward, 16- and 8-channel lanes, two-head workgroups) against the
+    float64 oracle."""
+    for k, v in variant.items():
+        monkeypatch.setenv(k, v)
+    value, loc, attn, grad = make_inputs(5, 2, 8, 16, 700, shapes, 2)
+    _note(f"variant={variant} shapes={shapes}")
+    out, (gv, gl, ga) = _run(value, shapes, loc, attn, grad)
+    assert_close(out, R.ms_deform_attn_core_rows(value, shapes, loc, attn), 1e-5, "out")
+    rv, rl, ra = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
+    assert_close(gv, rv, 1e-4, "grad_value")
+    assert_close(gl, rl, 1e-4, "grad_loc")
+    assert_close(ga, ra, 1e-4, "grad_attn")
+
+
 def test_level_larger_than_lds():
     """A 200x120 f32 level (1.5 MB per slice) plus a small one: global-gather forward, banded backward."""
     shapes = ((200, 120), (10, 12))
