@@ -120,6 +120,29 @@ def test_config_full_size(cfg):
     assert math.isclose(float(np.sum(ga.astype(np.float64) * attn)), inner, rel_tol=1e-4)
 
 
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+def test_multi_scale_training_shape(bf16):
+    """A four-level, 32-channel, 4-point shape of the larger RF-DETR variants (levels 80x80 down
+    to 10x10, so the large levels are gathered through L2 and every query has 16 samples) against
+    the C oracle, plus <G,out> = <dV,V> = <dA,A>."""
+    shapes = ((80, 80), (40, 40), (20, 20), (10, 10))
+    value, loc, attn, grad = make_inputs(123, 2, 8, 32, 300, shapes, 4)
+    if bf16:
+        value = R.bf16_round(value)
+    _note(f"multi-scale training shape bf16={bf16}")
+    out, (gv, gl, ga) = _run(value, shapes, loc, attn, grad, bf16)
+    tol = 2e-2 if bf16 else 1e-5
+    assert_close(out, cref.forward(value, shapes, loc, attn), tol, "out")
+    cv, cl, ca = cref.backward(value, shapes, loc, attn, grad)
+    tg = 2e-2 if bf16 else 1e-4
+    assert_close(gv, cv, tg, "grad_value")
+    assert_close(gl, cl, tg, "grad_loc")
+    assert_close(ga, ca, tg, "grad_attn")
+    inner = float(np.sum(out.astype(np.float64) * grad))
+    assert math.isclose(float(np.sum(gv.astype(np.float64) * value)), inner, rel_tol=1e-2 if bf16 else 1e-4)
+    assert math.isclose(float(np.sum(ga.astype(np.float64) * attn)), inner, rel_tol=1e-4)
+
+
 # --------------------------------------------------------------------------------------------
 # the differentiable entry points (autograd.Function over the C ABI)
 
