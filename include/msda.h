@@ -122,6 +122,63 @@ int msda_bwd(const void* value, int value_dtype,
              const int32_t* spatial_shapes, const int32_t* level_start_index,
              int64_t len_value, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * The MSDeformAttn prologue fused into the kernels. These entry points take what the module's
+ * projections produce and form the core's inputs inside the kernels, so sampling locations and
+ * attention weights never exist in memory:
+ *   sampling_locations = reference_points + sampling_offsets / (W_l, H_l)        (ref_dim == 2)
+ *                      = ref[..., :2] + sampling_offsets / n_points * ref[..., 2:] * 0.5
+ *                                                                                 (ref_dim == 4)
+ *   attention_weights  = softmax(attention_logits) over the n_levels * n_points axis, in f32.
+ * Replaces the body of MSDeformAttn.__call__ from the offsets to the core call,
+ * src/rfdetr_jax/models/ops.py:388-410 (locations :388-399 with precise_divide :46-62, softmax
+ * :403-404, core :408-410), and its JAX autodiff VJP.
+ * Layouts:
+ *   reference_points  [batch, len_query, n_levels, ref_dim]                     f32 (ref_dim 2 or 4)
+ *   sampling_offsets  [batch, len_query, n_heads, n_levels, n_points, 2]         f32
+ *   attention_logits  [batch, len_query, n_heads, n_levels * n_points]           f32
+ * Other arguments as msda_fwd; reference_points must be aligned to 4 * ref_dim bytes.
+ */
+int msda_fused_fwd(const void* value, int value_dtype,
+                   const float* reference_points, int ref_dim,
+                   const float* sampling_offsets, const float* attention_logits,
+                   void* output, int output_dtype,
+                   int batch, int n_heads, int head_dim, int len_query,
+                   int n_levels, int n_points,
+                   const int32_t* spatial_shapes, const int32_t* level_start_index,
+                   int64_t len_value, void* stream);
+
+/*
+ * Workspace of msda_fused_bwd, in bytes, or a negative MSDA_ERR_* code: msda_bwd's record bins
+ * plus per-head-group partial sums of the reference-point gradient (up to
+ * batch * len_query * n_heads * n_levels * ref_dim floats), summed by a small second kernel.
+ */
+int64_t msda_fused_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_query,
+                                      int n_levels, int n_points, int ref_dim,
+                                      const int32_t* spatial_shapes, const int32_t* level_start_index,
+                                      int64_t len_value);
+
+/*
+ * Backward of msda_fused_fwd:
+ *   grad_value              [batch*n_heads, len_value, head_dim]   value_dtype
+ *   grad_sampling_offsets   [batch, len_query, n_heads, n_levels, n_points, 2]  f32
+ *   grad_attention_logits   [batch, len_query, n_heads, n_levels*n_points]      f32
+ *   grad_reference_points   [batch, len_query, n_levels, ref_dim]               f32
+ * Any gradient pointer may be NULL to skip it. The workspace (16-byte aligned, at least
+ * msda_fused_bwd_workspace_size() bytes) is needed when grad_value or grad_reference_points is
+ * requested. Limits as msda_bwd.
+ */
+int msda_fused_bwd(const void* value, int value_dtype,
+                   const float* reference_points, int ref_dim,
+                   const float* sampling_offsets, const float* attention_logits,
+                   const void* grad_output, int grad_output_dtype,
+                   void* grad_value, float* grad_sampling_offsets, float* grad_attention_logits,
+                   float* grad_reference_points,
+                   int batch, int n_heads, int head_dim, int len_query,
+                   int n_levels, int n_points,
+                   const int32_t* spatial_shapes, const int32_t* level_start_index,
+                   int64_t len_value, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,6 +5,7 @@
 // (LDS per workgroup, CU count) once per device.
 #include "msda.h"
 #include "msda_kernels.h"
+#include "msda_launch.h"
 
 #include <hip/hip_runtime.h>
 
@@ -16,8 +17,10 @@
 #include <string>
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
+
+namespace msda_host {
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -28,6 +31,37 @@ int fail(int code, const char* fmt, ...) {
   g_last_error = buf;
   return code;
 }
+
+// The attribute is raised once per (instantiation, device) to the largest size requested so far,
+// so steady-state launches (including ones under stream capture) make no extra runtime call.
+int raise_lds_limit(const void* kernel, int bytes, std::atomic<int>* granted) {
+  if (bytes <= 65536) return MSDA_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return fail(MSDA_ERR_DEVICE, "hipGetDevice failed");
+  if (granted[dev].load(std::memory_order_relaxed) >= bytes) return MSDA_OK;
+  hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MSDA_ERR_LAUNCH, "hipFuncSetAttribute(%d bytes LDS): %s", bytes, hipGetErrorString(e));
+  }
+  int cur = granted[dev].load(std::memory_order_relaxed);
+  while (cur < bytes && !granted[dev].compare_exchange_weak(cur, bytes)) {
+  }
+  return MSDA_OK;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MSDA_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return MSDA_OK;
+}
+
+}  // namespace msda_host
+
+namespace {
+
+using msda_host::fail;
+using msda_host::kMaxDevices;
 
 // ------------------------------------------------------------------------------------------
 // shape validation shared by forward and backward
@@ -111,7 +145,6 @@ struct DevInfo {
   int cus;
 };
 
-constexpr int kMaxDevices = 64;
 std::atomic<int> g_dev_lds[kMaxDevices];
 std::atomic<int> g_dev_cus[kMaxDevices];
 
@@ -143,110 +176,12 @@ int env_int(const char* name, int dflt) {
 
 inline int align16(int64_t x) { return static_cast<int>((x + 15) & ~int64_t{15}); }
 
-// Allow a kernel instantiation to use more than 64 KB of dynamic LDS. The attribute is raised
-// once per (instantiation, device) to the largest size requested so far, so steady-state launches
-// (including ones under stream capture) make no extra runtime call.
-template <typename K>
-int allow_lds(K kernel, int bytes, std::atomic<int> (&granted)[kMaxDevices]) {
-  if (bytes <= 65536) return MSDA_OK;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return fail(MSDA_ERR_DEVICE, "hipGetDevice failed");
-  if (granted[dev].load(std::memory_order_relaxed) >= bytes) return MSDA_OK;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(MSDA_ERR_LAUNCH, "hipFuncSetAttribute(%d bytes LDS): %s", bytes, hipGetErrorString(e));
-  }
-  int cur = granted[dev].load(std::memory_order_relaxed);
-  while (cur < bytes && !granted[dev].compare_exchange_weak(cur, bytes)) {
-  }
-  return MSDA_OK;
-}
-
-int check_launch(const char* what) {
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(MSDA_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
-  return MSDA_OK;
-}
-
-// ------------------------------------------------------------------------------------------
-// dispatch
-
-template <typename VT, int VEC, int NS, bool STAGED>
-int launch_fwd(const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
-  static std::atomic<int> granted[kMaxDevices];  // per instantiation
-  auto k = msda::fwd_kernel<VT, VEC, NS, STAGED>;
-  int rc = allow_lds(k, lds, granted);
-  if (rc != MSDA_OK) return rc;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
-  return check_launch("msda forward");
-}
-
-template <typename VT, int VEC, int NS, bool STAGED>
-int launch_bwd_sample(const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
-  static std::atomic<int> granted[kMaxDevices];
-  auto k = msda::bwd_sample_kernel<VT, VEC, NS, STAGED>;
-  int rc = allow_lds(k, lds, granted);
-  if (rc != MSDA_OK) return rc;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
-  return check_launch("msda backward (per-sample pass)");
-}
-
-template <typename VT, int CG, int NACC>
-int launch_bwd_value(const msda::ValueParams& p, int grid, int threads, int lds, hipStream_t stream) {
-  static std::atomic<int> granted[kMaxDevices];
-  auto k = msda::bwd_value_kernel<VT, CG, NACC>;
-  int rc = allow_lds(k, lds, granted);
-  if (rc != MSDA_OK) return rc;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
-  return check_launch("msda backward (grad_value pass)");
-}
-
-template <typename VT, int VEC, int NS, bool STAGED>
-int launch_sample(bool backward, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
-  return backward ? launch_bwd_sample<VT, VEC, NS, STAGED>(p, grid, threads, lds, stream)
-                  : launch_fwd<VT, VEC, NS, STAGED>(p, grid, threads, lds, stream);
-}
-
-// Grouped-query kernels come in two forms: every level staged in LDS (no L2 gather path) or not.
-template <typename VT, int VEC>
-int dispatch_ns(bool backward, int ns, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
-  const bool staged = p.all_staged != 0;
-  switch (ns) {
-    case 2: return staged ? launch_sample<VT, VEC, 2, true>(backward, p, grid, threads, lds, stream)
-                          : launch_sample<VT, VEC, 2, false>(backward, p, grid, threads, lds, stream);
-    case 4: return staged ? launch_sample<VT, VEC, 4, true>(backward, p, grid, threads, lds, stream)
-                          : launch_sample<VT, VEC, 4, false>(backward, p, grid, threads, lds, stream);
-    default: return launch_sample<VT, VEC, 0, false>(backward, p, grid, threads, lds, stream);
-  }
-}
-
 // Samples per (query, head) = levels * points. Up to four, the count is a compile-time bound of
 // the kernel, which then loads several queries' inputs at once; beyond that a query's samples are
 // processed in chunks.
 inline int samples_bound(int levels, int points) {
   const int lp = levels * points;
   return lp <= 2 ? 2 : lp <= 4 ? 4 : 0;
-}
-
-template <typename VT>
-int dispatch_value(int cg, int nacc, const msda::ValueParams& vp, int grid, int threads, int lds, hipStream_t st) {
-  if (cg == 8)
-    return nacc == 4 ? launch_bwd_value<VT, 8, 4>(vp, grid, threads, lds, st) : launch_bwd_value<VT, 8, 1>(vp, grid, threads, lds, st);
-  return nacc == 4 ? launch_bwd_value<VT, 4, 4>(vp, grid, threads, lds, st) : launch_bwd_value<VT, 4, 1>(vp, grid, threads, lds, st);
-}
-
-template <typename VT>
-int dispatch_sample(bool backward, int vec, int ns, const msda::SampleParams& p, int grid, int threads, int lds,
-                    hipStream_t stream) {
-  switch (vec) {
-    case 1: return dispatch_ns<VT, 1>(backward, ns, p, grid, threads, lds, stream);
-    case 2: return dispatch_ns<VT, 2>(backward, ns, p, grid, threads, lds, stream);
-    case 4: return dispatch_ns<VT, 4>(backward, ns, p, grid, threads, lds, stream);
-    case 8: return dispatch_ns<VT, 8>(backward, ns, p, grid, threads, lds, stream);
-    case 16: return dispatch_ns<VT, 16>(backward, ns, p, grid, threads, lds, stream);
-  }
-  return fail(MSDA_ERR_UNSUPPORTED, "no kernel for %d channels per lane", vec);
 }
 
 msda::LevelDesc level_desc(const Shape& s, int l, int lds, int band_rows, int band_first) {
@@ -280,7 +215,7 @@ struct SamplePlan {
 // halve the location / weight rows fetched per query). Then one resident wave of workgroups:
 // fewer, longer workgroups amortise the value staging.
 int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* prefix, int shift, msda::SampleParams* p,
-                SamplePlan* out, int forced_qblock = 0, int extra_lds = 0) {
+                SamplePlan* out, int forced_qblock = 0, int extra_lds = 0, int max_group_lanes = 0) {
   auto knob = [&](const char* name, int dflt) {
     std::string key = std::string(prefix) + name;
     return env_int(key.c_str(), dflt);
@@ -302,7 +237,11 @@ int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* pref
   int hg = 1;
   const int hg_cap = std::max(1, knob("_HEADS", 4));
   const int group_budget = std::min(budget, knob("_GROUP_LDS", dev.lds_bytes));
-  while (hg * 2 <= hg_cap && s.heads % (hg * 2) == 0 && (hg * 2) * head_bytes <= group_budget) hg *= 2;
+  // max_group_lanes: a head group's lanes of one query must fit in that many (one wave when they
+  // exchange values by shuffles)
+  while (hg * 2 <= hg_cap && s.heads % (hg * 2) == 0 && (hg * 2) * head_bytes <= group_budget &&
+         (max_group_lanes == 0 || ((hg * 2) << shift) <= max_group_lanes))
+    hg *= 2;
   // With every level staged a head's region is its whole value slice; regions stay 16-byte aligned.
   const int head_stride = all_staged ? static_cast<int>(s.len_value * s.dim) : static_cast<int>(head_bytes / vbytes);
   p->head_lds = head_stride;
@@ -448,27 +387,71 @@ int plan_bins(const Shape& s, const DevInfo& dev, BinPlan* bp) {
 
 }  // namespace
 
-extern "C" {
+namespace msda {
 
-const char* msda_version(void) { return "msda-gfx950 0.2.0"; }
+// grad_reference_points [B, Q, L, ref_dim] = the sum over head groups of the per-group partials.
+__global__ void __launch_bounds__(256) ref_grad_kernel(const float* __restrict__ part, float* __restrict__ dref, int64_t n,
+                                                       int groups, int lr) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t bq = i / lr;
+    const int k = static_cast<int>(i - bq * lr);
+    const float* s = part + bq * groups * lr + k;
+    float acc = 0.0f;
+    for (int g = 0; g < groups; ++g) acc += s[static_cast<int64_t>(g) * lr];
+    dref[i] = acc;
+  }
+}
 
-const char* msda_last_error(void) { return g_last_error.c_str(); }
+}  // namespace msda
 
-int msda_fwd(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
-             void* output, int output_dtype, int batch, int n_heads, int head_dim, int len_query, int n_levels,
-             int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value,
-             void* stream) {
+namespace {
+
+// What the fused-prologue entry points add (msda_fused_fwd / msda_fused_bwd): the reference
+// points, and the reference-point gradient the backward returns.
+struct Fused {
+  const float* ref;
+  int ref_dim;
+  float* dref;
+};
+
+int check_fused(const Fused& fz, int len_query) {
+  if (fz.ref_dim != 2 && fz.ref_dim != 4) return fail(MSDA_ERR_INVALID_ARGUMENT, "ref_dim must be 2 or 4, got %d", fz.ref_dim);
+  if (len_query > 0 && fz.ref == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "reference_points is NULL");
+  if (!aligned(fz.ref, 4 * static_cast<size_t>(fz.ref_dim)))
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "reference_points must be %d-byte aligned", 4 * fz.ref_dim);
+  if (!aligned(fz.dref, 4)) return fail(MSDA_ERR_INVALID_ARGUMENT, "grad_reference_points must be 4-byte aligned");
+  return MSDA_OK;
+}
+
+// Bytes of per-head-group reference-point partial sums the fused backward may need: one row per
+// (batch, query, head) in the worst case of one-head groups.
+int64_t ref_part_bytes(const Shape& s, int ref_dim) {
+  return align16(static_cast<int64_t>(s.batch) * s.queries * s.heads * s.levels * ref_dim * 4);
+}
+
+void fill_fused(msda::SampleParams* p, const Fused* fz, int n_points) {
+  if (fz == nullptr) return;
+  p->ref = fz->ref;
+  p->ref_dim = fz->ref_dim;
+  p->fpoints = static_cast<float>(n_points);
+}
+
+int fwd_impl(const void* value, int value_dtype, const float* loc, const float* attn, void* output, int output_dtype, int batch,
+             int n_heads, int head_dim, int len_query, int n_levels, int n_points, const int32_t* spatial_shapes,
+             const int32_t* level_start_index, int64_t len_value, void* stream, const Fused* fz) {
   g_last_error.clear();
   Shape s;
   int rc = validate(&s, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value);
   if (rc != MSDA_OK) return rc;
   if ((rc = check_dtype(value_dtype, "value")) != MSDA_OK) return rc;
   if ((rc = check_dtype(output_dtype, "output")) != MSDA_OK) return rc;
+  if (fz != nullptr && (rc = check_fused(*fz, batch == 0 ? 0 : len_query)) != MSDA_OK) return rc;
   if (batch == 0 || len_query == 0) return MSDA_OK;
-  if (value == nullptr || sampling_locations == nullptr || attention_weights == nullptr || output == nullptr)
-    return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_fwd: NULL tensor pointer");
-  if (!aligned(sampling_locations, 8) || !aligned(attention_weights, 4))
-    return fail(MSDA_ERR_INVALID_ARGUMENT, "sampling_locations must be 8-byte aligned and attention_weights 4-byte aligned");
+  if (value == nullptr || loc == nullptr || attn == nullptr || output == nullptr)
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "%s: NULL tensor pointer", fz ? "msda_fused_fwd" : "msda_fwd");
+  if (!aligned(loc, 8) || !aligned(attn, 4))
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "%s must be 8-byte aligned and %s 4-byte aligned", fz ? "sampling_offsets" : "sampling_locations",
+                fz ? "attention_logits" : "attention_weights");
   const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   const int obytes = output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   if (!aligned(value, vbytes) || !aligned(output, obytes)) return fail(MSDA_ERR_INVALID_ARGUMENT, "value/output not aligned to their element size");
@@ -482,8 +465,8 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
 
   msda::SampleParams p{};
   p.value = value;
-  p.loc = sampling_locations;
-  p.attn = attention_weights;
+  p.loc = loc;
+  p.attn = attn;
   p.out = output;
   p.out_bf16 = output_dtype == MSDA_DTYPE_BF16;
   p.heads = n_heads;
@@ -493,56 +476,61 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
   p.points = n_points;
   p.len_value = len_value;
   p.vec16 = rows_16b(s, vbytes, value, nullptr);
+  fill_fused(&p, fz, n_points);
   SamplePlan plan;
   if ((rc = plan_sample(s, vbytes, dev, "MSDA_FWD", shift, &p, &plan)) != MSDA_OK) return rc;
   // one level, two points, two lanes per (query, head), every level staged: the two lanes split the
   // samples' coordinate work (fwd_pair)
   p.pair_share = (n_levels == 1 && n_points == 2 && shift == 1 && p.all_staged && ns == 2 && env_int("MSDA_FWD_PAIR", 1)) ? 1 : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (value_dtype == MSDA_DTYPE_BF16) return dispatch_sample<msda::bf16_t>(false, vec, ns, p, plan.grid, plan.threads, plan.lds, st);
-  return dispatch_sample<float>(false, vec, ns, p, plan.grid, plan.threads, plan.lds, st);
+  const bool fused = fz != nullptr;
+  if (value_dtype == MSDA_DTYPE_BF16)
+    return msda_host::dispatch_fwd<msda::bf16_t>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st);
+  return msda_host::dispatch_fwd<float>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st);
 }
 
-int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_query, int n_levels, int n_points,
-                                const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value) {
+int64_t workspace_impl(int batch, int n_heads, int head_dim, int len_query, int n_levels, int n_points, const int32_t* spatial_shapes,
+                       const int32_t* level_start_index, int64_t len_value, int ref_dim) {
   g_last_error.clear();
   Shape s;
   int rc = validate(&s, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value);
   if (rc != MSDA_OK) return rc;
+  if (ref_dim != 0 && ref_dim != 2 && ref_dim != 4) return fail(MSDA_ERR_INVALID_ARGUMENT, "ref_dim must be 2 or 4, got %d", ref_dim);
   if (batch == 0 || len_query == 0) return 0;
   DevInfo dev;
   if ((rc = device_info(&dev)) != MSDA_OK) return rc;
   BinPlan bp;
   if ((rc = plan_bins(s, dev, &bp)) != MSDA_OK) return rc;
-  return bp.total_bytes;
+  return bp.total_bytes + (ref_dim ? ref_part_bytes(s, ref_dim) : 0);
 }
 
-int msda_bwd(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
-             const void* grad_output, int grad_output_dtype, void* grad_value, float* grad_sampling_locations,
-             float* grad_attention_weights, int batch, int n_heads, int head_dim, int len_query, int n_levels,
-             int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value,
-             void* workspace, int64_t workspace_bytes, void* stream) {
+int bwd_impl(const void* value, int value_dtype, const float* loc, const float* attn, const void* grad_output, int grad_output_dtype,
+             void* grad_value, float* grad_loc, float* grad_attn, int batch, int n_heads, int head_dim, int len_query, int n_levels,
+             int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value, void* workspace,
+             int64_t workspace_bytes, void* stream, const Fused* fz) {
   g_last_error.clear();
   Shape s;
   int rc = validate(&s, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value);
   if (rc != MSDA_OK) return rc;
   if ((rc = check_dtype(value_dtype, "value")) != MSDA_OK) return rc;
   if ((rc = check_dtype(grad_output_dtype, "grad_output")) != MSDA_OK) return rc;
+  const char* name = fz ? "msda_fused_bwd" : "msda_bwd";
+  if (fz != nullptr && (rc = check_fused(*fz, batch == 0 ? 0 : len_query)) != MSDA_OK) return rc;
   if (batch == 0) return MSDA_OK;
-  if (grad_value == nullptr && grad_sampling_locations == nullptr && grad_attention_weights == nullptr) return MSDA_OK;
-  if (value == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_bwd: value is NULL");
-  if (len_query > 0 && (sampling_locations == nullptr || attention_weights == nullptr || grad_output == nullptr))
-    return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_bwd: NULL tensor pointer");
-  if (!aligned(sampling_locations, 8) || !aligned(attention_weights, 4) || !aligned(grad_sampling_locations, 8) ||
-      !aligned(grad_attention_weights, 4))
+  const bool want_dref = fz != nullptr && fz->dref != nullptr && len_query > 0;
+  if (grad_value == nullptr && grad_loc == nullptr && grad_attn == nullptr && !want_dref) return MSDA_OK;
+  if (value == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "%s: value is NULL", name);
+  if (len_query > 0 && (loc == nullptr || attn == nullptr || grad_output == nullptr))
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "%s: NULL tensor pointer", name);
+  if (!aligned(loc, 8) || !aligned(attn, 4) || !aligned(grad_loc, 8) || !aligned(grad_attn, 4))
     return fail(MSDA_ERR_INVALID_ARGUMENT, "location tensors must be 8-byte aligned and weight tensors 4-byte aligned");
   const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   const int gbytes = grad_output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   if (!aligned(value, vbytes) || !aligned(grad_value, vbytes) || !aligned(grad_output, gbytes))
     return fail(MSDA_ERR_INVALID_ARGUMENT, "value/grad_value/grad_output not aligned to their element size");
   const bool want_dv = grad_value != nullptr;
-  if (want_dv && len_query > 0) {
-    if (workspace == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace is NULL (see msda_bwd_workspace_size)");
+  if ((want_dv || want_dref) && len_query > 0) {
+    if (workspace == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace is NULL (see the workspace size query)");
     if (!aligned(workspace, 16)) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   }
   for (int l = 0; l < n_levels; ++l)
@@ -551,8 +539,10 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   // grad_value gathers address one batch entry's grad_output rows by 32-bit byte offsets
   if (static_cast<int64_t>(len_query) * n_heads * head_dim >= (int64_t{1} << 30))
     return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * head_dim reaches 2^30");
-  const int vec = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 16), {{value, vbytes}, {grad_output, gbytes}});
-  const int ns = env_int("MSDA_BWD_GROUPED", 0) ? samples_bound(n_levels, n_points) : 0;
+  // the fused variant's per-sample reference points leave no registers for 16-channel lanes
+  const int max_vec = fz ? env_int("MSDA_FUSED_BWD_MAX_VEC", 8) : env_int("MSDA_BWD_MAX_VEC", 16);
+  const int vec = pick_vec(head_dim, max_vec, {{value, vbytes}, {grad_output, gbytes}});
+  const int ns = fz == nullptr && env_int("MSDA_BWD_GROUPED", 0) ? samples_bound(n_levels, n_points) : 0;
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
 
@@ -563,11 +553,10 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   // ---- grad_value plan (checked, with the workspace, before anything is launched)
   BinPlan bp{};
   msda::ValueParams vp{};
+  int64_t ws_needed = 0;
   if (want_dv && len_query > 0) {
     if ((rc = plan_bins(s, dev, &bp)) != MSDA_OK) return rc;
-    if (workspace_bytes < bp.total_bytes)
-      return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace of %lld bytes needed, got %lld", static_cast<long long>(bp.total_bytes),
-                  static_cast<long long>(workspace_bytes));
+    ws_needed = bp.total_bytes;
     vp.bins = static_cast<const msda::SampleRec*>(workspace);
     vp.bin_counts = reinterpret_cast<const int*>(static_cast<const char*>(workspace) + bp.bins_bytes);
     vp.nqb = bp.nqb;
@@ -618,16 +607,16 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     vp.vec16 = rows_16b(s, vbytes, grad_value, nullptr);
   }
 
-  // ---- per-sample pass: grad_attention_weights, grad_sampling_locations, grad_value records
+  // ---- per-sample pass: grad of weights (logits) and locations (offsets), grad_value records
   if (len_query > 0) {
     msda::SampleParams p{};
     p.value = value;
-    p.loc = sampling_locations;
-    p.attn = attention_weights;
+    p.loc = loc;
+    p.attn = attn;
     p.gout = grad_output;
     p.gout_bf16 = grad_output_dtype == MSDA_DTYPE_BF16;
-    p.dloc = grad_sampling_locations;
-    p.dattn = grad_attention_weights;
+    p.dloc = grad_loc;
+    p.dattn = grad_attn;
     p.heads = n_heads;
     p.dim = head_dim;
     p.queries = len_query;
@@ -635,8 +624,24 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
     p.points = n_points;
     p.len_value = len_value;
     p.vec16 = rows_16b(s, vbytes, value, nullptr);
+    fill_fused(&p, fz, n_points);
     SamplePlan plan;
-    if ((rc = plan_sample(s, vbytes, dev, "MSDA_BWDS", shift, &p, &plan, want_dv ? bp.qblock : 0, 0)) != MSDA_OK) return rc;
+    // the fused backward sums reference-point gradients over a head group by shuffles in one wave
+    if ((rc = plan_sample(s, vbytes, dev, "MSDA_BWDS", shift, &p, &plan, want_dv ? bp.qblock : 0, 0, fz ? 64 : 0)) != MSDA_OK) return rc;
+    const int groups = n_heads / p.hg;
+    float* ref_part = nullptr;  // per-group partials, summed by ref_grad_kernel (groups > 1)
+    if (want_dref) {
+      if (groups == 1) {
+        p.dref = fz->dref;
+      } else {
+        ref_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws_needed);
+        ws_needed += ref_part_bytes(s, fz->ref_dim);
+        p.dref = ref_part;
+      }
+    }
+    if (workspace_bytes < ws_needed && ws_needed > 0)
+      return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace of %lld bytes needed, got %lld", static_cast<long long>(ws_needed),
+                  static_cast<long long>(workspace_bytes));
     if (want_dv) {
       p.bins = static_cast<uint4*>(workspace);
       p.bin_counts = reinterpret_cast<int*>(static_cast<char*>(workspace) + bp.bins_bytes);
@@ -654,17 +659,84 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
       plan.lds = align16(plan.lds) + align16(static_cast<int64_t>(p.hg) * bp.nwork * 4);
       if (plan.lds > dev.lds_bytes) return fail(MSDA_ERR_UNSUPPORTED, "per-sample pass needs %d bytes of LDS", plan.lds);
     }
-    rc = value_dtype == MSDA_DTYPE_BF16 ? dispatch_sample<msda::bf16_t>(true, vec, ns, p, plan.grid, plan.threads, plan.lds, st)
-                                        : dispatch_sample<float>(true, vec, ns, p, plan.grid, plan.threads, plan.lds, st);
+    const bool fused = fz != nullptr;
+    rc = value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_bwd_sample<msda::bf16_t>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st)
+                                        : msda_host::dispatch_bwd_sample<float>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st);
     if (rc != MSDA_OK) return rc;
+    if (ref_part != nullptr) {
+      const int64_t n = static_cast<int64_t>(batch) * len_query * n_levels * fz->ref_dim;
+      const int grid = static_cast<int>(std::min<int64_t>((n + 255) / 256, static_cast<int64_t>(dev.cus) * 8));
+      hipLaunchKernelGGL(msda::ref_grad_kernel, dim3(grid), dim3(256), 0, st, ref_part, fz->dref, n, groups, n_levels * fz->ref_dim);
+      if ((rc = msda_host::check_launch("msda fused backward (reference points)")) != MSDA_OK) return rc;
+    }
   }
   if (!want_dv) return MSDA_OK;
   const int64_t vgrid = static_cast<int64_t>(batch) * n_heads * vp.nwork;
   if (vgrid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
   const int vthreads = bp.threads;
   const int g = static_cast<int>(vgrid);
-  return value_dtype == MSDA_DTYPE_BF16 ? dispatch_value<msda::bf16_t>(bp.cg, bp.nacc, vp, g, vthreads, bp.lds, st)
-                                        : dispatch_value<float>(bp.cg, bp.nacc, vp, g, vthreads, bp.lds, st);
+  return value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_value<msda::bf16_t>(bp.cg, bp.nacc, vp, g, vthreads, bp.lds, st)
+                                        : msda_host::dispatch_value<float>(bp.cg, bp.nacc, vp, g, vthreads, bp.lds, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* msda_version(void) { return "msda-gfx950 0.3.0"; }
+
+const char* msda_last_error(void) { return g_last_error.c_str(); }
+
+int msda_fwd(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
+             void* output, int output_dtype, int batch, int n_heads, int head_dim, int len_query, int n_levels,
+             int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value,
+             void* stream) {
+  return fwd_impl(value, value_dtype, sampling_locations, attention_weights, output, output_dtype, batch, n_heads, head_dim, len_query,
+                  n_levels, n_points, spatial_shapes, level_start_index, len_value, stream, nullptr);
+}
+
+int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_query, int n_levels, int n_points,
+                                const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value) {
+  return workspace_impl(batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value, 0);
+}
+
+int msda_bwd(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
+             const void* grad_output, int grad_output_dtype, void* grad_value, float* grad_sampling_locations,
+             float* grad_attention_weights, int batch, int n_heads, int head_dim, int len_query, int n_levels,
+             int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value,
+             void* workspace, int64_t workspace_bytes, void* stream) {
+  return bwd_impl(value, value_dtype, sampling_locations, attention_weights, grad_output, grad_output_dtype, grad_value,
+                  grad_sampling_locations, grad_attention_weights, batch, n_heads, head_dim, len_query, n_levels, n_points,
+                  spatial_shapes, level_start_index, len_value, workspace, workspace_bytes, stream, nullptr);
+}
+
+int msda_fused_fwd(const void* value, int value_dtype, const float* reference_points, int ref_dim, const float* sampling_offsets,
+                   const float* attention_logits, void* output, int output_dtype, int batch, int n_heads, int head_dim,
+                   int len_query, int n_levels, int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index,
+                   int64_t len_value, void* stream) {
+  const Fused fz{reference_points, ref_dim, nullptr};
+  return fwd_impl(value, value_dtype, sampling_offsets, attention_logits, output, output_dtype, batch, n_heads, head_dim, len_query,
+                  n_levels, n_points, spatial_shapes, level_start_index, len_value, stream, &fz);
+}
+
+int64_t msda_fused_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_query, int n_levels, int n_points, int ref_dim,
+                                      const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value) {
+  if (ref_dim != 2 && ref_dim != 4) {
+    g_last_error.clear();
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "ref_dim must be 2 or 4, got %d", ref_dim);
+  }
+  return workspace_impl(batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value, ref_dim);
+}
+
+int msda_fused_bwd(const void* value, int value_dtype, const float* reference_points, int ref_dim, const float* sampling_offsets,
+                   const float* attention_logits, const void* grad_output, int grad_output_dtype, void* grad_value,
+                   float* grad_sampling_offsets, float* grad_attention_logits, float* grad_reference_points, int batch, int n_heads,
+                   int head_dim, int len_query, int n_levels, int n_points, const int32_t* spatial_shapes,
+                   const int32_t* level_start_index, int64_t len_value, void* workspace, int64_t workspace_bytes, void* stream) {
+  const Fused fz{reference_points, ref_dim, grad_reference_points};
+  return bwd_impl(value, value_dtype, sampling_offsets, attention_logits, grad_output, grad_output_dtype, grad_value,
+                  grad_sampling_offsets, grad_attention_logits, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes,
+                  level_start_index, len_value, workspace, workspace_bytes, stream, &fz);
 }
 
 }  // extern "C"

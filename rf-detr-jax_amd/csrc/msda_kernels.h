@@ -87,6 +87,12 @@ struct SampleParams {
   int head_lds;    // LDS elements of one head's staged levels
   int all_staged;  // every level is staged, so a head group's value rows are one contiguous copy
   int vec16;       // value staging may use 16-byte vectors
+  // MSDeformAttn prologue fused in (kFused kernels, ops.py:388-404): `loc` then holds the raw
+  // sampling offsets and `attn` the attention logits, and `dloc` / `dattn` receive their gradients.
+  const float* ref;  // reference points [B, Q, L, ref_dim]
+  int ref_dim;       // 2 (points) or 4 (boxes: centre, width, height)
+  float fpoints;     // n_points as a float: the box form divides the offsets by it
+  float* dref;       // backward: reference-point gradient per head group [B, Q, H / hg, L, ref_dim], or null
   LevelDesc lv[kMaxLevels];
 };
 
@@ -522,13 +528,18 @@ __device__ __forceinline__ void load_in(SampleIn<N>& f, const float2* __restrict
 // before the first is used, so a lane waits one memory latency per group rather than per query;
 // the backward also holds each query's grad_output row (VEC floats), so it groups fewer (sized so
 // that no instantiation spills registers at four waves per SIMD).
-constexpr int query_group(int ns, int vec, bool backward) {
+constexpr int query_group(int ns, int vec, bool backward, bool fused = false) {
   if (ns == 0) return 1;
+  if (fused) return vec >= 8 ? (ns <= 2 ? 2 : 1) : (ns <= 2 ? 4 : 2);  // + a reference point per sample
   if (!backward) return ns <= 2 ? 4 : 2;
   if (vec >= 16) return ns <= 2 ? 2 : 1;
   if (vec == 8) return 2;
   return ns <= 2 ? 4 : 2;
 }
+
+// Samples per chunk of the per-query loop (NS = 0); the fused prologue's per-sample reference
+// points and box offsets make the chunk half as long, within the same register budget.
+constexpr int pass_batch(bool fused) { return fused ? 2 : kPassBatch; }
 
 template <int NS, int QU>
 __device__ __forceinline__ void load_group(SampleIn<NS> (&in)[QU], const float2* __restrict__ loc2, const float* __restrict__ attn,
@@ -540,6 +551,149 @@ __device__ __forceinline__ void load_group(SampleIn<NS> (&in)[QU], const float2*
       load_in<NS>(in[i], loc2 + row * LP, attn + row * LP, 0, LP);
     }
   }
+}
+
+// ---------------------------------------------------------------------------------------------
+// MSDeformAttn prologue fused into the per-sample kernels (ops.py:388-404): sample locations from
+// reference points and raw offsets, attention weights from a softmax over each (query, head)'s
+// L*P logits; and, in the backward, the gradients of offsets, logits and reference points.
+
+// What the prologue adds per sample: the reference point of the sample's level (x, y, and for
+// boxes w, h), and the offset the box form scales (off / n_points; the raw offset for points).
+template <int N, bool kFused>
+struct FusedIn {};
+template <int N>
+struct FusedIn<N, true> {
+  float4 r[N];
+  float2 t[N];
+};
+
+// Reference point of level l for query row bq = b * Q + q.
+__device__ __forceinline__ float4 load_ref(const SampleParams& p, int64_t bq, int l) {
+  const int64_t i = bq * p.levels + l;
+  if (p.ref_dim == 4) return *reinterpret_cast<const float4*>(p.ref + i * 4);
+  const float2 v = *reinterpret_cast<const float2*>(p.ref + i * 2);
+  return make_float4(v.x, v.y, 0.0f, 0.0f);
+}
+
+// Reference points of samples s0 .. s0 + N - 1, the first at level l, point pt.
+template <int N>
+__device__ __forceinline__ void load_refs(FusedIn<N, true>& x, const SampleParams& p, int64_t bq, int s0, int LP, int l, int pt) {
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    if (s0 + u < LP) {
+      x.r[u] = load_ref(p, bq, l);
+      if (++pt == p.points) {
+        pt = 0;
+        ++l;
+      }
+    }
+  }
+}
+
+// jax.nn.softmax as ops.py:403-404 calls it, in f32: weight = exp(x - max) / sum(exp(x - max)).
+// The statistics are formed in sample order, from memory or from registers, with the same
+// operations, so both give the same weights.
+struct SoftmaxStats {
+  float m, s;
+};
+
+__device__ __forceinline__ float softmax_weight(float x, SoftmaxStats st) { return expf(x - st.m) / st.s; }
+
+__device__ __forceinline__ SoftmaxStats softmax_stats(const float* __restrict__ x, int LP) {
+  SoftmaxStats st{-__builtin_inff(), 0.0f};
+  for (int k = 0; k < LP; ++k) st.m = fmaxf(st.m, x[k]);
+  for (int k = 0; k < LP; ++k) st.s += expf(x[k] - st.m);
+  return st;
+}
+
+template <int N>
+__device__ __forceinline__ SoftmaxStats softmax_stats(const SampleIn<N>& f, int LP) {
+  SoftmaxStats st{-__builtin_inff(), 0.0f};
+#pragma unroll
+  for (int u = 0; u < N; ++u)
+    if (u < LP) st.m = fmaxf(st.m, f.a[u]);
+#pragma unroll
+  for (int u = 0; u < N; ++u)
+    if (u < LP) st.s += expf(f.a[u] - st.m);
+  return st;
+}
+
+// ops.py:388-399 for one sample. Points: ref + off / (W_l, H_l). Boxes: ref_xy + off / n_points *
+// ref_wh * 0.5, evaluated left to right. Each division is one IEEE rounding (precise_divide,
+// ops.py:46-62; hipcc's f32 division is correctly rounded) and nothing is contracted.
+__device__ __forceinline__ float2 fused_location(float2 off, float4 r, float2& t, const LevelDesc& L, const SampleParams& p) {
+#pragma clang fp contract(off)
+  if (p.ref_dim == 2) {
+    t = off;
+    return make_float2(r.x + off.x / L.fw, r.y + off.y / L.fh);
+  }
+  t = make_float2(off.x / p.fpoints, off.y / p.fpoints);
+  return make_float2(r.x + (t.x * r.z) * 0.5f, r.y + (t.y * r.w) * 0.5f);
+}
+
+// Turns loaded (offset, logit) pairs of samples s0 .. s0 + N - 1 into (location, weight).
+template <int N>
+__device__ __forceinline__ void fused_prologue(SampleIn<N>& f, FusedIn<N, true>& x, SoftmaxStats st, const SampleParams& p,
+                                               int s0, int LP, int l, int pt) {
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    if (s0 + u < LP) {
+      f.a[u] = softmax_weight(f.a[u], st);
+      f.xy[u] = fused_location(f.xy[u], x.r[u], x.t[u], p.lv[l], p);
+      if (++pt == p.points) {
+        pt = 0;
+        ++l;
+      }
+    }
+  }
+}
+
+// Backward state of one (query, head) row: sum_k a_k dA_k for the softmax VJP, and the running
+// reference-point gradient of the current level (x, y, and w, h for boxes).
+struct FusedAcc {
+  float S;
+  float r[4];
+};
+
+// Gradients of one sample from the core's (grad_loc, dA): the offset gradient (the transpose of
+// fused_location: grad_loc / (W_l, H_l), or ((grad_loc * 0.5) * ref_wh) / n_points) and the
+// sample's share of the reference-point gradient (grad_loc, and (grad_loc * 0.5) * t for w, h).
+__device__ __forceinline__ float2 fused_sample_grads(float2 gl, float a, float dA, float4 r, float2 t, const LevelDesc& L,
+                                                     const SampleParams& p, FusedAcc& fa) {
+  fa.S += a * dA;
+  fa.r[0] += gl.x;
+  fa.r[1] += gl.y;
+  if (p.ref_dim == 2) return make_float2(gl.x / L.fw, gl.y / L.fh);
+  const float hx = gl.x * 0.5f, hy = gl.y * 0.5f;
+  fa.r[2] += hx * t.x;
+  fa.r[3] += hy * t.y;
+  return make_float2((hx * r.z) / p.fpoints, (hy * r.w) / p.fpoints);
+}
+
+// End of a level: sums the reference-point gradient over the head group's lanes (hg * lanes per
+// (query, head) <= 64, a power of two, so the group is aligned inside one wave) and writes it for
+// (b, q, head group, level); the sum over groups is ref_grad_kernel's.
+__device__ __forceinline__ void flush_ref_grad(FusedAcc& fa, const SampleParams& p, int hl, int j, int64_t bq, int group,
+                                               int l) {
+  const int lpq = 1 << p.lpq_shift;
+  for (int o = lpq; o < (lpq * p.hg); o <<= 1) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) fa.r[k] += __shfl_xor(fa.r[k], o, 64);
+  }
+  if (p.dref != nullptr && hl == 0 && j == 0) {
+    float* d = p.dref + ((bq * (p.heads / p.hg) + group) * p.levels + l) * p.ref_dim;
+    for (int k = 0; k < p.ref_dim; ++k) d[k] = fa.r[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) fa.r[k] = 0.0f;
+}
+
+// Softmax VJP of one row, after every sample's dA is in grad_logits:
+// grad_logit_k = a_k * (dA_k - sum_j a_j dA_j) (the transpose of jax.nn.softmax's JVP).
+__device__ __forceinline__ void fused_logit_grads(const float* __restrict__ logits, float* glog, int LP, SoftmaxStats st,
+                                                  float S) {
+  for (int k = 0; k < LP; ++k) glog[k] = softmax_weight(logits[k], st) * (glog[k] - S);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -616,7 +770,8 @@ __device__ __forceinline__ void fwd_pair(float (&acc)[VEC], const SampleIn<2>& f
 
 // Four waves per SIMD (<= 128 VGPRs): latency is hidden by other waves rather than by
 // registers holding the next query's inputs (measured faster on MI355X).
-template <typename VT, int VEC, int NS, bool kStaged>
+// kFused: `loc` / `attn` are raw offsets and logits, turned into locations and weights first.
+template <typename VT, int VEC, int NS, bool kStaged, bool kFused>
 __global__ void __launch_bounds__(kSampleMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
 fwd_kernel(const SampleParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -632,14 +787,27 @@ fwd_kernel(const SampleParams p) {
   const int q_lo = it.qb * p.qblock;
   const int q_hi = min(p.queries, q_lo + p.qblock);
   const float2* __restrict__ loc2 = reinterpret_cast<const float2*>(p.loc);
-  constexpr int QU = query_group(NS, VEC, false);
+  constexpr int QU = query_group(NS, VEC, false, kFused);
+  constexpr int NI = NS == 0 ? 1 : NS;
   const int q_first = q_lo + ln.qs;
   const int64_t row_first = (static_cast<int64_t>(it.b) * p.queries + q_first) * p.heads + h;  // (b, q, h)
   const int64_t row_step = static_cast<int64_t>(ln.qpp) * p.heads;
-  SampleIn<NS == 0 ? 1 : NS> in[QU];
+  const int64_t bq0 = static_cast<int64_t>(it.b) * p.queries;  // query row b * Q of the reference points
+  SampleIn<NI> in[QU];
+  FusedIn<NI, kFused> fin[QU];
+  auto load_refs_group = [&](int q0) {
+    if constexpr (kFused) {
+#pragma unroll
+      for (int i = 0; i < QU; ++i)
+        if (q0 + i * ln.qpp < q_hi) load_refs<NI>(fin[i], p, bq0 + q0 + i * ln.qpp, 0, LP, 0, 0);
+    }
+  };
   // The first group's inputs are requested before the staging copy, so their latency overlaps it.
   if constexpr (NS > 0)
-    if (ln.active) load_group<NS, QU>(in, loc2, p.attn, row_first, row_step, q_first, ln.qpp, q_hi, LP);
+    if (ln.active) {
+      load_group<NS, QU>(in, loc2, p.attn, row_first, row_step, q_first, ln.qpp, q_hi, LP);
+      load_refs_group(q_first);
+    }
   stage_group(p, lds, vg);
   __syncthreads();
   if (!ln.active) return;  // no barrier follows
@@ -649,8 +817,16 @@ fwd_kernel(const SampleParams p) {
   if constexpr (NS > 0) {
     for (int qg = q_first; qg < q_hi; qg += QU * ln.qpp) {
       const int64_t row0 = row_first + static_cast<int64_t>((qg - q_first) / ln.qpp) * row_step;
-      if (qg != q_first) load_group<NS, QU>(in, loc2, p.attn, row0, row_step, qg, ln.qpp, q_hi, LP);
+      if (qg != q_first) {
+        load_group<NS, QU>(in, loc2, p.attn, row0, row_step, qg, ln.qpp, q_hi, LP);
+        load_refs_group(qg);
+      }
       wait_vmem();
+      if constexpr (kFused) {
+#pragma unroll
+        for (int i = 0; i < QU; ++i)
+          if (qg + i * ln.qpp < q_hi) fused_prologue<NS>(in[i], fin[i], softmax_stats<NS>(in[i], LP), p, 0, LP, 0, 0);
+      }
 #pragma unroll
       for (int i = 0; i < QU; ++i) {
         if (qg + i * ln.qpp < q_hi) {
@@ -678,10 +854,18 @@ fwd_kernel(const SampleParams p) {
 #pragma unroll
       for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
       int l = 0, pt = 0;
-      for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
-        SampleIn<kPassBatch> f;
-        load_in<kPassBatch>(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
-        fwd_pass<VT, VEC, kPassBatch, kStaged>(acc, f, s0, LP, l, pt, p, hlds, vs, rot);
+      SoftmaxStats st{};
+      if constexpr (kFused) st = softmax_stats(p.attn + row * LP, LP);
+      constexpr int PB = pass_batch(kFused);
+      for (int s0 = 0; s0 < LP; s0 += PB) {
+        SampleIn<PB> f;
+        load_in<PB>(f, loc2 + row * LP, p.attn + row * LP, s0, LP);
+        if constexpr (kFused) {
+          FusedIn<PB, true> x;
+          load_refs<PB>(x, p, bq0 + q, s0, LP, l, pt);
+          fused_prologue<PB>(f, x, st, p, s0, LP, l, pt);
+        }
+        fwd_pass<VT, VEC, PB, kStaged>(acc, f, s0, LP, l, pt, p, hlds, vs, rot);
       }
       if (ln.lane_on) store_any_rot<VT, VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, rot, acc);
     }
@@ -755,11 +939,11 @@ __device__ __forceinline__ void emit_record(const SampleParams& p, const SampleB
   *at(sb.bins, idx) = payload;
 }
 
-template <typename VT, int VEC, int N, bool kStaged>
-__device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const float (&g)[VEC], int s0, int LP, int& l, int& pt,
-                                         const SampleParams& p, const SampleLane& ln, const VT* hlds,
-                                         const VT* __restrict__ vs, const SampleBases& sb, uint32_t lrow, int* lcnt, int qoff,
-                                         int qb) {
+template <typename VT, int VEC, int N, bool kStaged, bool kFused>
+__device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const FusedIn<N, kFused>& x, FusedAcc& fa, const float (&g)[VEC],
+                                         int s0, int LP, int& l, int& pt, const SampleParams& p, const SampleLane& ln,
+                                         const VT* hlds, const VT* __restrict__ vs, const SampleBases& sb, uint32_t lrow, int* lcnt,
+                                         int qoff, int qb, int64_t bq, int group) {
   const int D = p.dim;
   const int lpq = 1 << p.lpq_shift;
 #pragma unroll
@@ -775,16 +959,33 @@ __device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const float (&g)[
       d10 = group_sum(d10, lpq);
       d01 = group_sum(d01, lpq);
       d11 = group_sum(d11, lpq);
+      const uint32_t si = lrow * static_cast<uint32_t>(LP) + static_cast<uint32_t>(s0 + u);  // sample, from the workgroup's row
+      if constexpr (kFused) {
+        // every lane of the head group forms the sample's gradients (their sums over heads are
+        // shuffled between lanes at the end of the level); lane 0 of the (query, head) writes
+        const float dA = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
+        const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
+        const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
+        const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
+        const float2 gl = make_float2(a * L.fw * dx, a * L.fh * dy);
+        const float2 goff = fused_sample_grads(gl, a, dA, x.r[u], x.t[u], L, p, fa);
+        if (ln.j == 0) {
+          if (sb.dattn) *at(sb.dattn, si) = dA;  // grad_logits holds dA until fused_logit_grads
+          if (sb.dloc) *at(sb.dloc, si) = goff;
+        }
+        if (p.dref != nullptr && pt + 1 == p.points) flush_ref_grad(fa, p, ln.hl, ln.j, bq, group, l);
+      }
       if (ln.j == 0) {
-        const uint32_t si = lrow * static_cast<uint32_t>(LP) + static_cast<uint32_t>(s0 + u);  // sample, from the workgroup's row
-        // dA = sum_c w_c D_c (the sample itself); d out / d ix = gy (m10 D10 - m00 D00) + fy (m11 D11 - m01 D01)
-        if (sb.dattn) *at(sb.dattn, si) = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
-        if (sb.dloc) {
-          const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
-          const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
-          const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
-          // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
-          *at(sb.dloc, si) = make_float2(a * L.fw * dx, a * L.fh * dy);
+        if constexpr (!kFused) {
+          // dA = sum_c w_c D_c (the sample itself); d out / d ix = gy (m10 D10 - m00 D00) + fy (m11 D11 - m01 D01)
+          if (sb.dattn) *at(sb.dattn, si) = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
+          if (sb.dloc) {
+            const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
+            const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
+            const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
+            // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
+            *at(sb.dloc, si) = make_float2(a * L.fw * dx, a * L.fh * dy);
+          }
         }
         if (p.bins) {
           // Non-finite weights (NaN or infinite coordinates) go to the clipped first corner's cell,
@@ -816,9 +1017,12 @@ __device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const float (&g)[
   }
 }
 
-template <typename VT, int VEC, int NS, bool kStaged>
+// kFused (only with NS == 0): `loc` / `attn` are raw offsets and logits; `dloc` / `dattn` receive
+// grad_offsets / grad_logits and `dref` the per-head-group reference-point gradients.
+template <typename VT, int VEC, int NS, bool kStaged, bool kFused>
 __global__ void __launch_bounds__(kSampleMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
 bwd_sample_kernel(const SampleParams p) {
+  static_assert(!kFused || NS == 0, "the fused prologue runs in the per-query sample loop");
   extern __shared__ __align__(16) unsigned char lds_raw[];
   VT* lds = reinterpret_cast<VT*>(lds_raw);
   const SampleItem it = sample_item(p);
@@ -847,10 +1051,13 @@ bwd_sample_kernel(const SampleParams p) {
   const int ncnt = p.bins ? p.hg * p.nwork : 0;
   for (int i = threadIdx.x; i < ncnt; i += blockDim.x) lcnt[i] = 0;
   constexpr int QU = query_group(NS, VEC, true);
+  constexpr int NI = NS == 0 ? 1 : NS;
   const int q_first = q_lo + ln.qs;
   const uint32_t lrow_first = lrow_of(q_first);
   const uint32_t lrow_step = __umul24(static_cast<uint32_t>(ln.qpp), static_cast<uint32_t>(p.heads));
-  SampleIn<NS == 0 ? 1 : NS> in[QU];
+  const int64_t bq0 = static_cast<int64_t>(it.b) * p.queries;
+  const int group = it.h0 / p.hg;
+  SampleIn<NI> in[QU];
   float g[QU][VEC];
   // grad_output rows and sample inputs of a group of queries are requested together; the first
   // group's before the staging copy, so their latency overlaps it.
@@ -873,7 +1080,7 @@ bwd_sample_kernel(const SampleParams p) {
     for (int i = 0; i < QU; ++i)
       if (q0 + i * ln.qpp < q_hi) {
         const uint32_t r = (lrow0 + i * lrow_step) * static_cast<uint32_t>(LP);
-        load_in<NS == 0 ? 1 : NS>(in[i], at(sb.loc, r), at(sb.attn, r), 0, LP);
+        load_in<NI>(in[i], at(sb.loc, r), at(sb.attn, r), 0, LP);
       }
   };
   if constexpr (NS > 0) {
@@ -900,7 +1107,10 @@ bwd_sample_kernel(const SampleParams p) {
         const int q = qg + i * ln.qpp;
         if (q < q_hi) {
           int l = 0, pt = 0;
-          bwd_pass<VT, VEC, NS, kStaged>(in[i], g[i], 0, LP, l, pt, p, ln, hlds, vs, sb, lrow0 + i * lrow_step, lcnt, q - q_lo, it.qb);
+          FusedIn<NI, false> none;
+          FusedAcc fa{};
+          bwd_pass<VT, VEC, NS, kStaged, false>(in[i], none, fa, g[i], 0, LP, l, pt, p, ln, hlds, vs, sb, lrow0 + i * lrow_step, lcnt,
+                                                q - q_lo, it.qb, 0, 0);
         }
       }
     }
@@ -910,11 +1120,23 @@ bwd_sample_kernel(const SampleParams p) {
       load_gout(lrow, q);
       int l = 0, pt = 0;
       const uint32_t r = lrow * static_cast<uint32_t>(LP);
-      for (int s0 = 0; s0 < LP; s0 += kPassBatch) {
-        SampleIn<kPassBatch> f;
-        load_in<kPassBatch>(f, at(sb.loc, r), at(sb.attn, r), s0, LP);
-        bwd_pass<VT, VEC, kPassBatch, kStaged>(f, g[0], s0, LP, l, pt, p, ln, hlds, vs, sb, lrow, lcnt, q - q_lo, it.qb);
+      SoftmaxStats st{};
+      FusedAcc fa{};
+      if constexpr (kFused) st = softmax_stats(at(sb.attn, r), LP);
+      constexpr int PB = pass_batch(kFused);
+      for (int s0 = 0; s0 < LP; s0 += PB) {
+        SampleIn<PB> f;
+        FusedIn<PB, kFused> x;
+        load_in<PB>(f, at(sb.loc, r), at(sb.attn, r), s0, LP);
+        if constexpr (kFused) {
+          load_refs<PB>(x, p, bq0 + q, s0, LP, l, pt);
+          fused_prologue<PB>(f, x, st, p, s0, LP, l, pt);
+        }
+        bwd_pass<VT, VEC, PB, kStaged, kFused>(f, x, fa, g[0], s0, LP, l, pt, p, ln, hlds, vs, sb, lrow, lcnt, q - q_lo, it.qb,
+                                               bq0 + q, group);
       }
+      if constexpr (kFused)
+        if (sb.dattn && ln.j == 0) fused_logit_grads(at(sb.attn, r), at(sb.dattn, r), LP, st, fa.S);
     }
   }
   if (!p.bins) return;

@@ -1,0 +1,126 @@
+// msda_launch.h — host-side launchers and kernel dispatch, shared by the translation units that
+// instantiate the kernels (one per value dtype and direction, so the build compiles them in
+// parallel) and by the C ABI (msda_abi.hip), which sees only the extern declarations below.
+#pragma once
+
+#include "msda.h"
+#include "msda_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+
+namespace msda_host {
+
+constexpr int kMaxDevices = 64;
+
+// Defined in msda_abi.hip.
+int fail(int code, const char* fmt, ...);
+int raise_lds_limit(const void* kernel, int bytes, std::atomic<int>* granted);
+int check_launch(const char* what);
+
+// Allow a kernel instantiation to use more than 64 KB of dynamic LDS (once per instantiation and
+// device; `granted` is that instantiation's per-device record).
+template <typename K>
+int allow_lds(K kernel, int bytes, std::atomic<int> (&granted)[kMaxDevices]) {
+  return raise_lds_limit(reinterpret_cast<const void*>(kernel), bytes, granted);
+}
+
+template <typename VT, int VEC, int NS, bool STAGED, bool FUSED>
+int launch_fwd(const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
+  static std::atomic<int> granted[kMaxDevices];  // per instantiation
+  auto k = msda::fwd_kernel<VT, VEC, NS, STAGED, FUSED>;
+  int rc = allow_lds(k, lds, granted);
+  if (rc != MSDA_OK) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
+  return check_launch("msda forward");
+}
+
+template <typename VT, int VEC, int NS, bool STAGED, bool FUSED>
+int launch_bwd_sample(const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
+  static std::atomic<int> granted[kMaxDevices];
+  auto k = msda::bwd_sample_kernel<VT, VEC, NS, STAGED, FUSED>;
+  int rc = allow_lds(k, lds, granted);
+  if (rc != MSDA_OK) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
+  return check_launch("msda backward (per-sample pass)");
+}
+
+template <typename VT, int CG, int NACC>
+int launch_bwd_value(const msda::ValueParams& p, int grid, int threads, int lds, hipStream_t stream) {
+  static std::atomic<int> granted[kMaxDevices];
+  auto k = msda::bwd_value_kernel<VT, CG, NACC>;
+  int rc = allow_lds(k, lds, granted);
+  if (rc != MSDA_OK) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
+  return check_launch("msda backward (grad_value pass)");
+}
+
+// Grouped-query forward kernels come in two forms: every level staged in LDS (no L2 gather path)
+// or not; NS = 0 handles any sample count and either kind of level.
+template <typename VT, int VEC, bool FUSED>
+int fwd_ns(int ns, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t st) {
+  const bool staged = p.all_staged != 0;
+  switch (ns) {
+    case 2: return staged ? launch_fwd<VT, VEC, 2, true, FUSED>(p, grid, threads, lds, st)
+                          : launch_fwd<VT, VEC, 2, false, FUSED>(p, grid, threads, lds, st);
+    case 4: return staged ? launch_fwd<VT, VEC, 4, true, FUSED>(p, grid, threads, lds, st)
+                          : launch_fwd<VT, VEC, 4, false, FUSED>(p, grid, threads, lds, st);
+    default: return launch_fwd<VT, VEC, 0, false, FUSED>(p, grid, threads, lds, st);
+  }
+}
+
+// The fused prologue's backward runs in the per-query sample loop (NS = 0) only.
+template <typename VT, int VEC>
+int bwd_ns(int ns, bool fused, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t st) {
+  if (fused) return launch_bwd_sample<VT, VEC, 0, false, true>(p, grid, threads, lds, st);
+  const bool staged = p.all_staged != 0;
+  switch (ns) {
+    case 2: return staged ? launch_bwd_sample<VT, VEC, 2, true, false>(p, grid, threads, lds, st)
+                          : launch_bwd_sample<VT, VEC, 2, false, false>(p, grid, threads, lds, st);
+    case 4: return staged ? launch_bwd_sample<VT, VEC, 4, true, false>(p, grid, threads, lds, st)
+                          : launch_bwd_sample<VT, VEC, 4, false, false>(p, grid, threads, lds, st);
+    default: return launch_bwd_sample<VT, VEC, 0, false, false>(p, grid, threads, lds, st);
+  }
+}
+
+template <typename VT>
+int dispatch_fwd(int vec, int ns, bool fused, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t st) {
+  switch (vec) {
+    case 1: return fused ? fwd_ns<VT, 1, true>(ns, p, grid, threads, lds, st) : fwd_ns<VT, 1, false>(ns, p, grid, threads, lds, st);
+    case 2: return fused ? fwd_ns<VT, 2, true>(ns, p, grid, threads, lds, st) : fwd_ns<VT, 2, false>(ns, p, grid, threads, lds, st);
+    case 4: return fused ? fwd_ns<VT, 4, true>(ns, p, grid, threads, lds, st) : fwd_ns<VT, 4, false>(ns, p, grid, threads, lds, st);
+    case 8: return fused ? fwd_ns<VT, 8, true>(ns, p, grid, threads, lds, st) : fwd_ns<VT, 8, false>(ns, p, grid, threads, lds, st);
+    case 16: return fused ? fwd_ns<VT, 16, true>(ns, p, grid, threads, lds, st) : fwd_ns<VT, 16, false>(ns, p, grid, threads, lds, st);
+  }
+  return fail(MSDA_ERR_UNSUPPORTED, "no kernel for %d channels per lane", vec);
+}
+
+template <typename VT>
+int dispatch_bwd_sample(int vec, int ns, bool fused, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t st) {
+  switch (vec) {
+    case 1: return bwd_ns<VT, 1>(ns, fused, p, grid, threads, lds, st);
+    case 2: return bwd_ns<VT, 2>(ns, fused, p, grid, threads, lds, st);
+    case 4: return bwd_ns<VT, 4>(ns, fused, p, grid, threads, lds, st);
+    case 8: return bwd_ns<VT, 8>(ns, fused, p, grid, threads, lds, st);
+    case 16: return bwd_ns<VT, 16>(ns, fused, p, grid, threads, lds, st);
+  }
+  return fail(MSDA_ERR_UNSUPPORTED, "no kernel for %d channels per lane", vec);
+}
+
+template <typename VT>
+int dispatch_value(int cg, int nacc, const msda::ValueParams& vp, int grid, int threads, int lds, hipStream_t st) {
+  if (cg == 8)
+    return nacc == 4 ? launch_bwd_value<VT, 8, 4>(vp, grid, threads, lds, st) : launch_bwd_value<VT, 8, 1>(vp, grid, threads, lds, st);
+  return nacc == 4 ? launch_bwd_value<VT, 4, 4>(vp, grid, threads, lds, st) : launch_bwd_value<VT, 4, 1>(vp, grid, threads, lds, st);
+}
+
+// Instantiated in msda_fwd_f32.hip, msda_fwd_bf16.hip, msda_bwd_f32.hip and msda_bwd_bf16.hip.
+extern template int dispatch_fwd<float>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
+extern template int dispatch_fwd<msda::bf16_t>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
+extern template int dispatch_bwd_sample<float>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
+extern template int dispatch_bwd_sample<msda::bf16_t>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
+extern template int dispatch_value<float>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
+extern template int dispatch_value<msda::bf16_t>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
+
+}  // namespace msda_host

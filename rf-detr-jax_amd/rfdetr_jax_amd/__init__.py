@@ -12,6 +12,9 @@ from .ops import (
     ms_deform_attn_core,
     ms_deform_attn_core_rows,
     ms_deform_attn_forward,
+    ms_deform_attn_fused,
+    ms_deform_attn_fused_backward,
+    ms_deform_attn_fused_forward,
 )
 
 __all__ = [
@@ -21,4 +24,7 @@ __all__ = [
     "ms_deform_attn_core",
     "ms_deform_attn_core_rows",
     "ms_deform_attn_forward",
+    "ms_deform_attn_fused",
+    "ms_deform_attn_fused_backward",
+    "ms_deform_attn_fused_forward",
 ]

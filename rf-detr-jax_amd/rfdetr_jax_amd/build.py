@@ -11,6 +11,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)  # rf-detr-jax_amd/
@@ -19,8 +20,12 @@ CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 LIB_NAME = "libmsda_gfx950.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = [os.path.join(CSRC, "msda_abi.hip")]
-HEADERS = [os.path.join(CSRC, "msda_kernels.h"), os.path.join(INCLUDE, "msda.h")]
+# The C ABI, and the kernel instantiations split by value dtype and direction so they compile in
+# parallel.
+SOURCES = [os.path.join(CSRC, f) for f in ("msda_abi.hip", "msda_fwd_f32.hip", "msda_fwd_bf16.hip", "msda_bwd_f32.hip",
+                                           "msda_bwd_bf16.hip")]
+HEADERS = [os.path.join(CSRC, "msda_kernels.h"), os.path.join(CSRC, "msda_launch.h"), os.path.join(INCLUDE, "msda.h")]
+BUILD_DIR = os.path.join(ROOT, "_build")
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [
@@ -28,7 +33,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-Wall",
     # Keep the compiler from forming packed-f32 (v_pk_*_f32) instructions.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -42,19 +46,31 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None, out: str | None = None) -> str:
-    """Compile the library; returns its path. Always recompiles (it is the build check)."""
-    out = out or LIB_PATH
-    tmp = out + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), "-I", INCLUDE, "-I", CSRC, *SOURCES, "-o", tmp]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}: {' '.join(cmd[-3:])}")
     if verbose and proc.stderr.strip():
         sys.stderr.write(proc.stderr)
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None, out: str | None = None) -> str:
+    """Compile the library; returns its path. Always recompiles (it is the build check)."""
+    out = out or LIB_PATH
+    tmp = out + ".tmp"
+    objdir = os.path.join(BUILD_DIR, os.path.basename(out) + ".objs")
+    os.makedirs(objdir, exist_ok=True)
+    flags = [*HIPCC_FLAGS, *(extra_flags or []), "-I", INCLUDE, "-I", CSRC]
+    objs = [os.path.join(objdir, os.path.basename(src) + ".o") for src in SOURCES]
+    jobs = [[hipcc(), *flags, "-c", src, "-o", obj] for src, obj in zip(SOURCES, objs)]
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", "0") or 0) or (os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        for f in [pool.submit(_run, cmd, verbose) for cmd in jobs]:
+            f.result()
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
     os.replace(tmp, out)
     return out
 

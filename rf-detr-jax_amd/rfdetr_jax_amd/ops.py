@@ -249,3 +249,149 @@ def ms_deform_attn_core(value, spatial_shapes, sampling_locations, attention_wei
     batch, n_heads, head_dim, length = value.shape
     rows = value.transpose(2, 3).reshape(batch * n_heads, length, head_dim)
     return ms_deform_attn_core_rows(rows, spatial_shapes, sampling_locations, attention_weights)
+
+
+# ------------------------------------------------------------------------------------------------
+# The MSDeformAttn prologue fused into the kernels (ops.py:388-410)
+
+
+def _check_fused_inputs(value, shapes, reference_points, sampling_offsets, attention_logits):
+    if sampling_offsets.dim() != 6 or sampling_offsets.shape[-1] != 2:
+        raise ValueError(
+            f"sampling_offsets must be [B, Lq, n_heads, n_levels, n_points, 2], got {tuple(sampling_offsets.shape)}"
+        )
+    batch, len_query, n_heads, n_levels, n_points, _ = sampling_offsets.shape
+    ref_dim = reference_points.shape[-1] if reference_points.dim() == 4 else -1
+    if ref_dim not in (2, 4) or tuple(reference_points.shape[:3]) != (batch, len_query, n_levels):
+        # ops.py:400 raises ValueError for a trailing dimension other than 2 or 4
+        raise ValueError(
+            f"reference_points must be [B, Lq, n_levels, 2 or 4] = {(batch, len_query, n_levels)} + (2|4,), "
+            f"got {tuple(reference_points.shape)}"
+        )
+    dims = _check_inputs(value, shapes, sampling_offsets, attention_logits)
+    if reference_points.device != value.device:
+        raise RuntimeError("reference_points must be on the value's device")
+    return dims, ref_dim
+
+
+def ms_deform_attn_fused_forward(value, spatial_shapes, reference_points, sampling_offsets, attention_logits,
+                                 level_start_index=None, out_dtype=None):
+    """One forward launch of the fused op (no autograd): returns ``[B, Q, H*D]``.
+
+    ``sampling_locations`` and ``attention_weights`` are formed inside the kernel from
+    ``reference_points [B, Q, L, 2|4]``, ``sampling_offsets [B, Q, H, L, P, 2]`` and
+    ``attention_logits [B, Q, H, L*P]`` exactly as ops.py:388-404 forms them.
+    """
+    shapes = _as_shapes(spatial_shapes)
+    _check_level_start_index(level_start_index, shapes)
+    (batch, len_query, n_heads, n_levels, n_points, head_dim), ref_dim = _check_fused_inputs(
+        value, shapes, reference_points, sampling_offsets, attention_logits
+    )
+    out_dtype = out_dtype or _out_dtype(value, attention_logits)
+    value = value.contiguous()
+    ref = reference_points.to(torch.float32).contiguous()
+    off = sampling_offsets.to(torch.float32).contiguous()
+    logits = attention_logits.to(torch.float32).contiguous()
+    out = torch.empty((batch, len_query, n_heads * head_dim), dtype=out_dtype, device=value.device)
+    arr, starts = _shape_arrays(shapes)
+    lib = _native.lib()
+    with torch.cuda.device(value.device):
+        rc = lib.msda_fused_fwd(
+            _ptr(value), _VALUE_DTYPES[value.dtype], _ptr(ref), ref_dim, _ptr(off), _ptr(logits), _ptr(out),
+            _VALUE_DTYPES[out_dtype], batch, n_heads, head_dim, len_query, n_levels, n_points, arr, starts, value.shape[1],
+            _stream(value.device),
+        )
+    _native.check(rc)
+    return out
+
+
+def ms_deform_attn_fused_backward(value, spatial_shapes, reference_points, sampling_offsets, attention_logits, grad_output,
+                                  level_start_index=None, needs=(True, True, True, True)):
+    """One backward launch of the fused op.
+
+    Returns ``(grad_value, grad_reference_points, grad_sampling_offsets, grad_attention_logits)``;
+    entries of ``needs`` (same order) that are false come back as ``None`` and are not computed.
+    """
+    shapes = _as_shapes(spatial_shapes)
+    _check_level_start_index(level_start_index, shapes)
+    (batch, len_query, n_heads, n_levels, n_points, head_dim), ref_dim = _check_fused_inputs(
+        value, shapes, reference_points, sampling_offsets, attention_logits
+    )
+    if tuple(grad_output.shape) != (batch, len_query, n_heads * head_dim):
+        raise ValueError(f"grad_output must be {(batch, len_query, n_heads * head_dim)}, got {tuple(grad_output.shape)}")
+    value = value.contiguous()
+    ref = reference_points.to(torch.float32).contiguous()
+    off = sampling_offsets.to(torch.float32).contiguous()
+    logits = attention_logits.to(torch.float32).contiguous()
+    if grad_output.dtype not in _VALUE_DTYPES:
+        grad_output = grad_output.to(torch.float32)
+    grad_output = grad_output.contiguous()
+    dev = value.device
+    grad_value = torch.empty_like(value) if needs[0] else None
+    grad_ref = torch.empty(ref.shape, dtype=torch.float32, device=dev) if needs[1] else None
+    grad_off = torch.empty(off.shape, dtype=torch.float32, device=dev) if needs[2] else None
+    grad_logits = torch.empty(logits.shape, dtype=torch.float32, device=dev) if needs[3] else None
+    arr, starts = _shape_arrays(shapes)
+    lib = _native.lib()
+    workspace, ws_bytes = None, 0
+    if grad_value is not None or grad_ref is not None:
+        ws_bytes = lib.msda_fused_bwd_workspace_size(batch, n_heads, head_dim, len_query, n_levels, n_points, ref_dim, arr,
+                                                     starts, value.shape[1])
+        if ws_bytes < 0:
+            _native.check(int(ws_bytes))
+        workspace = torch.empty((max(1, ws_bytes // 16), 4), dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.msda_fused_bwd(
+            _ptr(value), _VALUE_DTYPES[value.dtype], _ptr(ref), ref_dim, _ptr(off), _ptr(logits), _ptr(grad_output),
+            _VALUE_DTYPES[grad_output.dtype], _ptr(grad_value), _ptr(grad_off), _ptr(grad_logits), _ptr(grad_ref),
+            batch, n_heads, head_dim, len_query, n_levels, n_points, arr, starts, value.shape[1],
+            _ptr(workspace), ws_bytes, _stream(dev),
+        )
+    _native.check(rc)
+    return grad_value, grad_ref, grad_off, grad_logits
+
+
+class _MSDeformAttnFusedFunction(torch.autograd.Function):
+    """custom-VJP pair of the fused op: forward = msda_fused_fwd, backward = msda_fused_bwd."""
+
+    @staticmethod
+    def forward(ctx, value, reference_points, sampling_offsets, attention_logits, shapes):
+        out = ms_deform_attn_fused_forward(value, shapes, reference_points, sampling_offsets, attention_logits)
+        ctx.save_for_backward(value, reference_points, sampling_offsets, attention_logits)
+        ctx.shapes = shapes
+        ctx.out_dtype = out.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        value, ref, off, logits = ctx.saved_tensors
+        needs = ctx.needs_input_grad[:4]
+        grads = ms_deform_attn_fused_backward(value, ctx.shapes, ref, off, logits, grad_output.to(ctx.out_dtype), needs=needs)
+        out = []
+        for g, src in zip(grads, (value, ref, off, logits)):
+            out.append(g.to(src.dtype) if g is not None and g.dtype != src.dtype else g)
+        return (*out, None)
+
+
+def ms_deform_attn_fused(value, spatial_shapes, reference_points, sampling_offsets, attention_logits):
+    """``MSDeformAttn``'s core from the projected query: ops.py:388-410 in one differentiable op.
+
+    Args:
+        value: ``[B * n_heads, sum(H*W), head_dim]`` (the module's projected value, ops.py:405-407).
+        spatial_shapes: per-level ``(H, W)`` pairs.
+        reference_points: ``[B, Lq, n_levels, 2]`` points or ``[B, Lq, n_levels, 4]`` boxes in
+            ``[0, 1]``.
+        sampling_offsets: ``[B, Lq, n_heads, n_levels, n_points, 2]`` (the ``sampling_offsets``
+            projection, reshaped as ops.py:384-386 does).
+        attention_logits: ``[B, Lq, n_heads, n_levels * n_points]`` before the softmax
+            (ops.py:381-383).
+
+    Returns:
+        ``[B, Lq, n_heads * head_dim]``; differentiable in all four tensors.
+
+    Raises:
+        ValueError: a ``reference_points`` trailing dimension other than 2 or 4 (as ops.py:400),
+            or inconsistent shapes.
+    """
+    shapes = _as_shapes(spatial_shapes)
+    return _MSDeformAttnFusedFunction.apply(value, reference_points, sampling_offsets, attention_logits, shapes)

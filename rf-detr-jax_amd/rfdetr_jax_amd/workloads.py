@@ -121,3 +121,38 @@ def workload_inputs(w: Workload, with_grad: bool | None = None):
     """Inputs of a workload, seeded by its config id."""
     return make_inputs(w.cfg_id, w.batch, w.heads, w.head_dim, w.queries, w.shapes, w.points, w.value_dtype,
                        w.uniform_locations, w.backward if with_grad is None else with_grad)
+
+
+def make_fused_inputs(seed: int, batch, n_heads, head_dim, len_query, spatial_shapes, n_points, ref_dim=4,
+                      value_dtype="f32", with_grad=True):
+    """Synthetic inputs of the fused-prologue op (``ms_deform_attn_fused``), drawn from
+    ``numpy.random.default_rng(seed)`` in this order:
+
+    1. value ~ N(0,1) ``[B*H, S, D]`` (rounded to bf16 for bf16 workloads);
+    2. reference points ``[B,Q,L,ref_dim]``: centres ~ U[0.05, 0.95]^2 and, for boxes
+       (``ref_dim`` 4), sizes ~ U[0.05, 0.5]^2, the same for every level (as the decoder
+       broadcasts one box to all levels, transformer.py:446-449);
+    3. sampling offsets ~ N(0, 2) ``[B,Q,H,L,P,2]`` (pixels of the level for points; units of
+       box / (2 P) for boxes, ops.py:391-397);
+    4. attention logits ~ N(0, 2) ``[B,Q,H,L*P]``;
+    5. G ~ N(0,1) ``[B,Q,H*D]`` f32 (when ``with_grad``).
+
+    Returns float32 NumPy arrays ``(value, ref, offsets, logits, grad)``.
+    """
+    rng = np.random.default_rng(seed)
+    n_levels = len(spatial_shapes)
+    s = sum(int(h) * int(w) for h, w in spatial_shapes)
+    value = rng.standard_normal((batch * n_heads, s, head_dim), dtype=np.float32)
+    if value_dtype == "bf16":
+        value = bf16_round(value)
+    centre = rng.uniform(0.05, 0.95, (batch, len_query, 1, 2))
+    if ref_dim == 4:
+        size = rng.uniform(0.05, 0.5, (batch, len_query, 1, 2))
+        ref = np.concatenate([centre, size], axis=-1)
+    else:
+        ref = centre
+    ref = np.ascontiguousarray(np.broadcast_to(ref, (batch, len_query, n_levels, ref_dim))).astype(np.float32)
+    off = rng.normal(0.0, 2.0, (batch, len_query, n_heads, n_levels, n_points, 2)).astype(np.float32)
+    logits = rng.normal(0.0, 2.0, (batch, len_query, n_heads, n_levels * n_points)).astype(np.float32)
+    grad = rng.standard_normal((batch, len_query, n_heads * head_dim), dtype=np.float32) if with_grad else None
+    return value, ref, off, logits, grad

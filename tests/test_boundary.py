@@ -208,3 +208,100 @@ def test_unsupported_value_dtype():
     value, loc, attn = _cpu_inputs()
     with pytest.raises(TypeError, match="not supported"):
         hip_ops.ms_deform_attn_forward(value.double(), ((4, 4),), loc, attn)
+
+
+# --------------------------------------------------------------------------------------------
+# fused-prologue entry points (msda_fused_fwd / msda_fused_bwd)
+
+
+def _ffwd(**kw):
+    args = dict(value=1 << 20, vdt=0, ref=1 << 20, ref_dim=4, off=1 << 20, logits=1 << 20, out=1 << 20, odt=0, batch=1,
+                heads=2, dim=16, queries=4, levels=1, points=2, shapes=_shapes([(4, 4)]), starts=_starts([0]), len_value=16)
+    args.update(kw)
+    lib = _native.lib()
+    rc = lib.msda_fused_fwd(
+        ctypes.c_void_p(args["value"]), args["vdt"], ctypes.c_void_p(args["ref"]), args["ref_dim"],
+        ctypes.c_void_p(args["off"]), ctypes.c_void_p(args["logits"]), ctypes.c_void_p(args["out"]), args["odt"],
+        args["batch"], args["heads"], args["dim"], args["queries"], args["levels"], args["points"], args["shapes"],
+        args["starts"], args["len_value"], None,
+    )
+    return rc, lib.msda_last_error().decode()
+
+
+def _fbwd(**kw):
+    args = dict(value=1 << 20, vdt=0, ref=1 << 20, ref_dim=2, off=1 << 20, logits=1 << 20, gout=1 << 20, gdt=0,
+                dv=1 << 20, doff=1 << 20, dlog=1 << 20, dref=1 << 20, batch=1, heads=2, dim=16, queries=4, levels=1,
+                points=2, shapes=_shapes([(4, 4)]), starts=_starts([0]), len_value=16, ws=1 << 20, ws_bytes=1 << 20)
+    args.update(kw)
+    lib = _native.lib()
+    rc = lib.msda_fused_bwd(
+        ctypes.c_void_p(args["value"]), args["vdt"], ctypes.c_void_p(args["ref"]), args["ref_dim"],
+        ctypes.c_void_p(args["off"]), ctypes.c_void_p(args["logits"]), ctypes.c_void_p(args["gout"]), args["gdt"],
+        ctypes.c_void_p(args["dv"]), ctypes.c_void_p(args["doff"]), ctypes.c_void_p(args["dlog"]),
+        ctypes.c_void_p(args["dref"]), args["batch"], args["heads"], args["dim"], args["queries"], args["levels"],
+        args["points"], args["shapes"], args["starts"], args["len_value"], ctypes.c_void_p(args["ws"]), args["ws_bytes"],
+        None,
+    )
+    return rc, lib.msda_last_error().decode()
+
+
+@pytest.mark.parametrize("call", [_ffwd, _fbwd])
+@pytest.mark.parametrize(
+    "kw, code, message",
+    [
+        (dict(ref_dim=3), _native.ERR_INVALID_ARGUMENT, "ref_dim"),
+        (dict(ref_dim=0), _native.ERR_INVALID_ARGUMENT, "ref_dim"),
+        (dict(ref=0), _native.ERR_INVALID_ARGUMENT, "reference_points is NULL"),
+        (dict(ref=(1 << 20) + 4), _native.ERR_INVALID_ARGUMENT, "reference_points must be"),
+        (dict(starts=_starts([3])), _native.ERR_INVALID_ARGUMENT, "level_start_index"),
+        (dict(vdt=7), _native.ERR_UNSUPPORTED, "dtype"),
+        (dict(off=(1 << 20) + 4), _native.ERR_INVALID_ARGUMENT, "aligned"),
+    ],
+)
+def test_fused_invalid_arguments_are_reported(call, kw, code, message):
+    rc, msg = call(**kw)
+    assert rc == code, msg
+    assert message in msg
+
+
+def test_fused_workspace_size_validates_first():
+    lib = _native.lib()
+    f = lib.msda_fused_bwd_workspace_size
+    assert f(1, 2, 16, 4, 1, 2, 3, _shapes([(4, 4)]), _starts([0]), 16) == _native.ERR_INVALID_ARGUMENT
+    assert "ref_dim" in lib.msda_last_error().decode()
+    assert f(1, 2, 16, 4, 1, 2, 4, _shapes([(4, 4)]), _starts([3]), 16) == _native.ERR_INVALID_ARGUMENT
+    assert f(0, 2, 16, 4, 1, 2, 4, _shapes([(4, 4)]), _starts([0]), 16) == 0
+    assert f(1, 2, 16, 0, 1, 2, 2, _shapes([(4, 4)]), _starts([0]), 16) == 0
+
+
+def test_fused_workspace_needed_for_grad_value_or_reference_points():
+    rc, msg = _fbwd(ws=0)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "workspace" in msg
+    rc, msg = _fbwd(ws=0, dv=0)  # grad_reference_points alone may still need the partial sums
+    assert rc == _native.ERR_INVALID_ARGUMENT and "workspace" in msg
+
+
+def test_fused_empty_calls_are_no_ops():
+    assert _ffwd(batch=0)[0] == _native.OK
+    assert _ffwd(queries=0)[0] == _native.OK
+    assert _fbwd(batch=0)[0] == _native.OK
+    assert _fbwd(dv=0, doff=0, dlog=0, dref=0)[0] == _native.OK
+
+
+def _cpu_fused_inputs(ref_dim=4, b=1, q=3, h=2, l=1, p=2, d=4, shapes=((4, 4),)):
+    value, off, logits = _cpu_inputs(b, q, h, l, p, d, shapes)
+    return value, torch.zeros(b, q, l, ref_dim), off, logits
+
+
+def test_fused_mirror_rejects_bad_reference_points():
+    value, ref, off, logits = _cpu_fused_inputs()
+    with pytest.raises(ValueError, match="2 or 4"):
+        hip_ops.ms_deform_attn_fused_forward(value, ((4, 4),), torch.zeros(1, 3, 1, 3), off, logits)
+    with pytest.raises(ValueError, match="reference_points"):
+        hip_ops.ms_deform_attn_fused_forward(value, ((4, 4),), torch.zeros(1, 2, 1, 4), off, logits)
+
+
+def test_fused_cpu_tensors_fail_loudly():
+    value, ref, off, logits = _cpu_fused_inputs()
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        hip_ops.ms_deform_attn_fused(value, ((4, 4),), ref, off, logits)

@@ -1,0 +1,202 @@
+"""Parity of the fused-prologue op (msda_fused_fwd / msda_fused_bwd through the C ABI) on an MI355X.
+
+The expected values are the prologue oracle (oracle/prologue_ref.py: locations and softmax weights
+in f32 as ops.py:388-404 forms them, and the VJP in float64) composed with the core oracles: the
+float64 NumPy one at reduced sizes, the f32 C one at the benchmark's full size. Tolerances are the
+core's (``max|got - want| <= tol * max(1, max|want|)``): f32 forward 1e-5, gradients 1e-4; bf16
+value 2e-2.
+"""
+
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cref
+from oracle import msda_ref as R
+from oracle import prologue_ref as PR
+from rfdetr_jax_amd import ops as hip
+from rfdetr_jax_amd.workloads import make_fused_inputs
+from tests._util import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev():
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    return torch.device("cuda:0")
+
+
+def _note(msg):
+    sys.stderr.write(f"[gpu] {msg}\n")
+    sys.stderr.flush()
+
+
+def _np(t):
+    return None if t is None else t.detach().float().cpu().numpy()
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(_dev())
+
+
+def _run_fused(value, shapes, ref, off, logits, grad, bf16=False, needs=(True, True, True, True)):
+    v = _t(value)
+    if bf16:
+        v = v.to(torch.bfloat16)
+    r, o, lg = _t(ref), _t(off), _t(logits)
+    out = hip.ms_deform_attn_fused_forward(v, shapes, r, o, lg)
+    grads = hip.ms_deform_attn_fused_backward(v, shapes, r, o, lg, _t(grad), needs=needs) if grad is not None else None
+    torch.cuda.synchronize()
+    return _np(out), None if grads is None else [_np(g) for g in grads]
+
+
+def _oracle64(value, shapes, ref, off, logits, grad, p):
+    loc, attn = PR.prologue(ref, off, logits, shapes, p)
+    out = R.ms_deform_attn_core_rows(value, shapes, loc, attn)
+    gv, gl, ga = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
+    goff, glog, gref = PR.prologue_vjp(ref, off, logits, shapes, p, gl, ga)
+    return out, (gv, gref, goff, glog)
+
+
+def _check(got_out, got_grads, want_out, want_grads, bf16):
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    assert_close(got_out, want_out, tf, "out")
+    for name, g, w in zip(("grad_value", "grad_reference_points", "grad_sampling_offsets", "grad_attention_logits"),
+                          got_grads, want_grads):
+        assert_close(g, w, tg, name)
+
+
+CASES = {
+    # one 24x24 level, 2 points: the grouped forward with paired lanes (the Nano decoder's shape)
+    "nano": dict(shapes=((24, 24),), heads=16, dim=16, points=2, queries=300),
+    # two levels x 2 points: four samples per (query, head), the NS = 4 grouped forward
+    "two_levels_p2": dict(shapes=((20, 30), (10, 15)), heads=8, dim=32, points=2, queries=200),
+    # two levels x 4 points with a level too large for LDS: the per-query forward, L2 gathers
+    "two_levels_p4": dict(shapes=((80, 80), (20, 20)), heads=16, dim=16, points=4, queries=150),
+    # four levels x 4 points, 8 heads x 32 (the larger variants' decoder)
+    "four_levels": dict(shapes=((40, 40), (20, 20), (10, 10), (5, 5)), heads=8, dim=32, points=4, queries=120),
+}
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+@pytest.mark.parametrize("ref_dim", [2, 4])
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_fused_against_float64_oracle(case, ref_dim, bf16):
+    c = CASES[case]
+    _note(f"fused {case} ref_dim={ref_dim} bf16={bf16}")
+    value, ref, off, logits, grad = make_fused_inputs(7, 2, c["heads"], c["dim"], c["queries"], c["shapes"], c["points"],
+                                                      ref_dim, "bf16" if bf16 else "f32")
+    out, grads = _run_fused(value, c["shapes"], ref, off, logits, grad, bf16)
+    want_out, want_grads = _oracle64(value, c["shapes"], ref, off, logits, grad, c["points"])
+    _check(out, grads, want_out, want_grads, bf16)
+
+
+@pytest.mark.parametrize("ref_dim", [2, 4])
+def test_fused_full_size_against_c_oracle(ref_dim):
+    """The benchmark's config-2 shape (B=8, Q=3900, one 24x24 level, 16 heads x 16, 2 points) with
+    the prologue fused, against the f32 C oracle, plus <G, out> = <dV, V>."""
+    shapes = ((24, 24),)
+    _note(f"fused full size ref_dim={ref_dim}")
+    value, ref, off, logits, grad = make_fused_inputs(2, 8, 16, 16, 3900, shapes, 2, ref_dim)
+    out, (gv, gref, goff, glog) = _run_fused(value, shapes, ref, off, logits, grad)
+    loc, attn = PR.prologue(ref, off, logits, shapes, 2)
+    assert_close(out, cref.forward(value, shapes, loc, attn), 1e-5, "out")
+    cv, cl, ca = cref.backward(value, shapes, loc, attn, grad)
+    w_off, w_log, w_ref = PR.prologue_vjp(ref, off, logits, shapes, 2, cl, ca)
+    assert_close(gv, cv, 1e-4, "grad_value")
+    assert_close(goff, w_off, 1e-4, "grad_sampling_offsets")
+    assert_close(glog, w_log, 1e-4, "grad_attention_logits")
+    assert_close(gref, w_ref, 1e-4, "grad_reference_points")
+    inner = float(np.sum(out.astype(np.float64) * grad))
+    assert math.isclose(float(np.sum(gv.astype(np.float64) * value)), inner, rel_tol=1e-4)
+
+
+@pytest.mark.parametrize("variant", [
+    {"MSDA_FWD_GROUPED": "0"},          # per-query forward loop
+    {"MSDA_FWD_PAIR": "0"},             # grouped forward without paired lanes
+    {"MSDA_FUSED_BWD_MAX_VEC": "16"},   # one lane per (query, head) in the backward
+    {"MSDA_FUSED_BWD_MAX_VEC": "4"},    # four lanes per (query, head): head-group shuffles over 16 lanes
+    {"MSDA_BWDS_HEADS": "1"},           # one head per group: 16 partial sums per reference point
+    {"MSDA_BWDS_HEADS": "2"},
+], ids=lambda v: ",".join(f"{k}={x}" for k, x in v.items()))
+def test_fused_kernel_variants(monkeypatch, variant):
+    for k, x in variant.items():
+        monkeypatch.setenv(k, x)
+    shapes = ((24, 24), (12, 12))
+    _note(f"fused variant {variant}")
+    value, ref, off, logits, grad = make_fused_inputs(11, 2, 16, 16, 250, shapes, 2, 4)
+    out, grads = _run_fused(value, shapes, ref, off, logits, grad)
+    want_out, want_grads = _oracle64(value, shapes, ref, off, logits, grad, 2)
+    _check(out, grads, want_out, want_grads, False)
+
+
+def test_fused_all_heads_in_one_group():
+    """Four heads and a small level: one head group holds every head, so the kernel writes
+    grad_reference_points directly (no partial sums, no second kernel)."""
+    shapes = ((16, 16),)
+    value, ref, off, logits, grad = make_fused_inputs(12, 3, 4, 16, 97, shapes, 3, 2)
+    out, grads = _run_fused(value, shapes, ref, off, logits, grad)
+    want_out, want_grads = _oracle64(value, shapes, ref, off, logits, grad, 3)
+    _check(out, grads, want_out, want_grads, False)
+
+
+@pytest.mark.parametrize("which", range(4))
+def test_fused_single_gradient_requests(which):
+    shapes = ((24, 24),)
+    value, ref, off, logits, grad = make_fused_inputs(13, 2, 16, 16, 120, shapes, 2, 4)
+    needs = tuple(i == which for i in range(4))
+    _, grads = _run_fused(value, shapes, ref, off, logits, grad, needs=needs)
+    _, want = _oracle64(value, shapes, ref, off, logits, grad, 2)
+    for i, (g, w) in enumerate(zip(grads, want)):
+        if i == which:
+            assert_close(g, w, 1e-4, f"gradient {i}")
+        else:
+            assert g is None
+
+
+def test_fused_masked_logits():
+    """Logits of -inf (masked samples) get weight 0 and gradient 0, as jax.nn.softmax gives."""
+    shapes = ((24, 24),)
+    value, ref, off, logits, grad = make_fused_inputs(14, 1, 16, 16, 64, shapes, 4, 2)
+    logits[:, ::3, :, 1] = -np.inf
+    logits[:, 1::5, 2, :3] = -np.inf
+    out, grads = _run_fused(value, shapes, ref, off, logits, grad)
+    want_out, want_grads = _oracle64(value, shapes, ref, off, logits, grad, 4)
+    assert np.isfinite(out).all()
+    _check(out, grads, want_out, want_grads, False)
+    assert (grads[3][:, ::3, :, 1] == 0).all()
+
+
+def test_fused_matches_composed_torch_prologue():
+    """Autograd through the fused op equals autograd through the prologue written in torch (f32,
+    on the GPU) followed by the core op."""
+    shapes = ((24, 24), (12, 12))
+    value, ref, off, logits, grad = make_fused_inputs(15, 2, 16, 16, 200, shapes, 2, 4)
+    leaves = [_t(x).requires_grad_(True) for x in (value, ref, off, logits)]
+    out = hip.ms_deform_attn_fused(leaves[0], shapes, *leaves[1:])
+    out.backward(_t(grad))
+    fused = [_np(out)] + [_np(x.grad) for x in leaves]
+
+    leaves2 = [_t(x).requires_grad_(True) for x in (value, ref, off, logits)]
+    v, r, o, lg = leaves2
+    loc = r[:, :, None, :, None, :2] + o / 2 * r[:, :, None, :, None, 2:] * 0.5
+    attn = torch.softmax(lg, dim=-1)
+    out2 = hip.ms_deform_attn_core_rows(v, shapes, loc, attn)
+    out2.backward(_t(grad))
+    composed = [_np(out2)] + [_np(x.grad) for x in leaves2]
+    assert_close(fused[0], composed[0], 1e-5, "out")
+    for name, a, b in zip(("value", "ref", "offsets", "logits"), fused[1:], composed[1:]):
+        assert_close(a, b, 1e-4, f"grad {name}")
+
+
+def test_fused_empty_queries():
+    shapes = ((8, 8),)
+    value, ref, off, logits, grad = make_fused_inputs(16, 2, 4, 8, 0, shapes, 2, 4)
+    out, (gv, gref, goff, glog) = _run_fused(value, shapes, ref, off, logits, grad)
+    assert out.shape == (2, 0, 32) and gref.shape == (2, 0, 1, 4) and goff.shape == (2, 0, 4, 1, 2, 2)
+    assert (gv == 0).all()
