@@ -98,6 +98,81 @@ class Calls:
             self.check(rc)
 
 
+class FusedCalls:
+    """Pre-built C-ABI calls of the fused-prologue op (msda_fused_fwd / msda_fused_bwd) on a
+    workload's shape: box reference points, raw offsets and logits in, every gradient out."""
+
+    def __init__(self, w, dev, ref_dim=4):
+        import torch
+
+        from rfdetr_jax_amd import _native
+        from rfdetr_jax_amd.workloads import make_fused_inputs
+
+        self.w = w
+        value, ref, off, logits, grad = make_fused_inputs(w.cfg_id, w.batch, w.heads, w.head_dim, w.queries, w.shapes,
+                                                          w.points, ref_dim, w.value_dtype)
+        bf16 = w.value_dtype == "bf16"
+        t = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+        self.v = t(value).to(torch.bfloat16) if bf16 else t(value)
+        self.ref, self.off, self.logits, self.grad = t(ref), t(off), t(logits), t(grad)
+        self.out = torch.empty(w.batch, w.queries, w.heads * w.head_dim, device=dev)
+        self.dv = torch.empty_like(self.v)
+        self.dref, self.doff, self.dlog = torch.empty_like(self.ref), torch.empty_like(self.off), torch.empty_like(self.logits)
+        flat = [x for hw in w.shapes for x in hw]
+        self._shapes = (ctypes.c_int32 * len(flat))(*flat)
+        starts, acc = [], 0
+        for h, wd in w.shapes:
+            starts.append(acc)
+            acc += h * wd
+        self._starts = (ctypes.c_int32 * len(starts))(*starts)
+        vdt = _native.DTYPE_BF16 if bf16 else _native.DTYPE_F32
+        shape_args = (w.batch, w.heads, w.head_dim, w.queries, w.levels, w.points, self._shapes, self._starts,
+                      w.len_value)
+        p = lambda x: ctypes.c_void_p(x.data_ptr())  # noqa: E731
+        self.lib = _native.lib()
+        ws_bytes = self.lib.msda_fused_bwd_workspace_size(w.batch, w.heads, w.head_dim, w.queries, w.levels, w.points,
+                                                          ref_dim, self._shapes, self._starts, w.len_value)
+        if ws_bytes < 0:
+            _native.check(int(ws_bytes))
+        self.ws = torch.empty((max(1, ws_bytes // 16), 4), dtype=torch.int32, device=dev)
+        self.fargs = (p(self.v), vdt, p(self.ref), ref_dim, p(self.off), p(self.logits), p(self.out),
+                      _native.DTYPE_F32) + shape_args
+        self.bargs = (p(self.v), vdt, p(self.ref), ref_dim, p(self.off), p(self.logits), p(self.grad), _native.DTYPE_F32,
+                      p(self.dv), p(self.doff), p(self.dlog), p(self.dref)) + shape_args + (p(self.ws), ctypes.c_int64(ws_bytes))
+        self.check = _native.check
+        # the same step with the prologue in torch around the core op (what the fused op replaces)
+        self.core = Calls(w, dev)
+        self.core_loc = torch.empty_like(self.off)
+        self.core_attn = torch.empty_like(self.logits)
+
+    def fwd(self, stream):
+        rc = self.lib.msda_fused_fwd(*self.fargs, stream)
+        if rc:
+            self.check(rc)
+
+    def bwd(self, stream):
+        rc = self.lib.msda_fused_bwd(*self.bargs, stream)
+        if rc:
+            self.check(rc)
+
+    def unfused_step(self, stream):
+        """ops.py:395-404 in torch, msda_fwd, msda_bwd, then the prologue's VJP in torch."""
+        import torch
+
+        c, P = self.core, float(self.w.points)
+        wh = self.ref[:, :, None, :, None, 2:]
+        t = self.off / P
+        torch.add(self.ref[:, :, None, :, None, :2], t * wh * 0.5, out=c.loc)
+        c.attn.copy_(torch.softmax(self.logits, dim=-1))
+        c.fwd(stream)
+        c.bwd(stream)
+        half = c.dloc * 0.5
+        torch.div(half * wh, P, out=self.doff)
+        self.dref[..., :2] = c.dloc.sum(dim=(2, 4))
+        self.dref[..., 2:] = (half * t).sum(dim=(2, 4))
+        self.dlog.copy_(torch.ops.aten._softmax_backward_data(c.dattn, c.attn, -1, torch.float32))
+
+
 def _stream_handle():
     import torch
 
@@ -174,6 +249,28 @@ def measure(w, dev, steps, warmup):
     return res, calls
 
 
+def measure_fused(w, dev, steps, warmup):
+    """The fused-prologue op on a workload's shape, beside the same step with the prologue in torch."""
+    fc = FusedCalls(w, dev)
+    h = _stream_handle()
+    for _ in range(warmup):
+        fc.fwd(h)
+        fc.bwd(h)
+        fc.unfused_step(h)
+
+    def step(hs):
+        fc.fwd(hs)
+        fc.bwd(hs)
+
+    return {
+        "fused_step_us": round(time_graph(step, steps)[0], 3),
+        "fused_fwd_us": round(time_graph(fc.fwd, steps)[0], 3),
+        "fused_bwd_us": round(time_graph(fc.bwd, steps)[0], 3),
+        "unfused_step_us": round(time_graph(fc.unfused_step, steps)[0], 3),
+        "reference_points": "boxes [B,Q,L,4]",
+    }
+
+
 def cpu_baseline(calls, budget_s=3.0, max_reps=20):
     """fwd+bwd of the C oracle on the same inputs; median us/call."""
     from oracle import cref
@@ -205,11 +302,11 @@ def cpu_baseline(calls, budget_s=3.0, max_reps=20):
     }
 
 
-def profile_run(w, dev, steps, warmup, copy_mb):
+def profile_run(w, dev, steps, warmup, copy_mb, fused=False):
     """Eager launches only (every dispatch visible to a counter profiler), plus a copy kernel."""
     import torch
 
-    calls = Calls(w, dev)
+    calls = FusedCalls(w, dev) if fused else Calls(w, dev)
     h = _stream_handle()
     for _ in range(warmup):
         calls.fwd(h)
@@ -241,6 +338,7 @@ def main():
                     help="for rocprofv3 runs: W + K eager steps of the workload, then K plain copies of a "
                          "--copy-mb buffer (counter calibration); prints one JSON line of timings")
     ap.add_argument("--copy-mb", type=int, default=256)
+    ap.add_argument("--fused", action="store_true", help="with --profile: the fused-prologue op instead of the core")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): the deformable-attention op needs no "
@@ -257,7 +355,7 @@ def main():
     dev = torch.device("cuda:0")
     w = CONFIGS[args.config]
     if args.profile:
-        profile_run(w, dev, args.steps, args.warmup, args.copy_mb)
+        profile_run(w, dev, args.steps, args.warmup, args.copy_mb, args.fused)
         return
     log(f"workload {w.name}: warmup {args.warmup}, steps {args.steps}")
     res, calls = measure(w, dev, args.steps, args.warmup)
@@ -290,6 +388,9 @@ def main():
             if cw.backward:
                 entry.update({"bwd_us": round(r["bwd_us"], 3), "bwd_hbm_gbps": round(r["bwd_gbps"], 1)})
             per_config[cw.name] = entry
+        if w.backward:
+            log("fused prologue")
+            per_config[f"fused_prologue_{w.name}"] = measure_fused(w, dev, max(50, args.steps // 2), 10)
 
     cpu = None
     if not args.no_cpu_baseline:

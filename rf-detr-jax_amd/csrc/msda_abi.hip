@@ -389,17 +389,10 @@ int plan_bins(const Shape& s, const DevInfo& dev, BinPlan* bp) {
 
 namespace msda {
 
-// grad_reference_points [B, Q, L, ref_dim] = the sum over head groups of the per-group partials.
+// grad_reference_points from the per-group partials, when no grad_value pass runs to do it.
 __global__ void __launch_bounds__(256) ref_grad_kernel(const float* __restrict__ part, float* __restrict__ dref, int64_t n,
-                                                       int groups, int lr) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256) {
-    const int64_t bq = i / lr;
-    const int k = static_cast<int>(i - bq * lr);
-    const float* s = part + bq * groups * lr + k;
-    float acc = 0.0f;
-    for (int g = 0; g < groups; ++g) acc += s[static_cast<int64_t>(g) * lr];
-    dref[i] = acc;
-  }
+                                                       int groups) {
+  ref_grad_sum(part, dref, n, groups, static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x, static_cast<int64_t>(gridDim.x) * 256);
 }
 
 }  // namespace msda
@@ -434,6 +427,7 @@ void fill_fused(msda::SampleParams* p, const Fused* fz, int n_points) {
   p->ref = fz->ref;
   p->ref_dim = fz->ref_dim;
   p->fpoints = static_cast<float>(n_points);
+  p->inv_points = (n_points & (n_points - 1)) == 0 ? 1.0f / static_cast<float>(n_points) : 0.0f;
 }
 
 int fwd_impl(const void* value, int value_dtype, const float* loc, const float* attn, void* output, int output_dtype, int batch,
@@ -539,10 +533,12 @@ int bwd_impl(const void* value, int value_dtype, const float* loc, const float* 
   // grad_value gathers address one batch entry's grad_output rows by 32-bit byte offsets
   if (static_cast<int64_t>(len_query) * n_heads * head_dim >= (int64_t{1} << 30))
     return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * head_dim reaches 2^30");
-  // the fused variant's per-sample reference points leave no registers for 16-channel lanes
-  const int max_vec = fz ? env_int("MSDA_FUSED_BWD_MAX_VEC", 8) : env_int("MSDA_BWD_MAX_VEC", 16);
+  const int max_vec = fz ? env_int("MSDA_FUSED_BWD_MAX_VEC", 16) : env_int("MSDA_BWD_MAX_VEC", 16);
   const int vec = pick_vec(head_dim, max_vec, {{value, vbytes}, {grad_output, gbytes}});
-  const int ns = fz == nullptr && env_int("MSDA_BWD_GROUPED", 0) ? samples_bound(n_levels, n_points) : 0;
+  // the fused variant loads a group of queries' inputs at once and keeps dA in registers for the
+  // softmax VJP (the per-query loop would wait on memory three times per query)
+  const int grouped = fz ? env_int("MSDA_FUSED_BWD_GROUPED", 1) : env_int("MSDA_BWD_GROUPED", 0);
+  const int ns = grouped ? samples_bound(n_levels, n_points) : 0;
   const int shift = lpq_shift_for(head_dim, vec);
   if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
 
@@ -625,6 +621,7 @@ int bwd_impl(const void* value, int value_dtype, const float* loc, const float* 
     p.len_value = len_value;
     p.vec16 = rows_16b(s, vbytes, value, nullptr);
     fill_fused(&p, fz, n_points);
+    p.bq_total = static_cast<int64_t>(batch) * len_query;
     SamplePlan plan;
     // the fused backward sums reference-point gradients over a head group by shuffles in one wave
     if ((rc = plan_sample(s, vbytes, dev, "MSDA_BWDS", shift, &p, &plan, want_dv ? bp.qblock : 0, 0, fz ? 64 : 0)) != MSDA_OK) return rc;
@@ -663,10 +660,16 @@ int bwd_impl(const void* value, int value_dtype, const float* loc, const float* 
     rc = value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_bwd_sample<msda::bf16_t>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st)
                                         : msda_host::dispatch_bwd_sample<float>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st);
     if (rc != MSDA_OK) return rc;
-    if (ref_part != nullptr) {
+    if (ref_part != nullptr && want_dv) {
+      // the grad_value pass sums the partials before its own work (saves a launch)
+      vp.ref_part = ref_part;
+      vp.dref = fz->dref;
+      vp.ref_n = static_cast<int64_t>(batch) * len_query * n_levels * fz->ref_dim;
+      vp.ref_groups = groups;
+    } else if (ref_part != nullptr) {
       const int64_t n = static_cast<int64_t>(batch) * len_query * n_levels * fz->ref_dim;
       const int grid = static_cast<int>(std::min<int64_t>((n + 255) / 256, static_cast<int64_t>(dev.cus) * 8));
-      hipLaunchKernelGGL(msda::ref_grad_kernel, dim3(grid), dim3(256), 0, st, ref_part, fz->dref, n, groups, n_levels * fz->ref_dim);
+      hipLaunchKernelGGL(msda::ref_grad_kernel, dim3(grid), dim3(256), 0, st, ref_part, fz->dref, n, groups);
       if ((rc = msda_host::check_launch("msda fused backward (reference points)")) != MSDA_OK) return rc;
     }
   }

@@ -92,7 +92,9 @@ struct SampleParams {
   const float* ref;  // reference points [B, Q, L, ref_dim]
   int ref_dim;       // 2 (points) or 4 (boxes: centre, width, height)
   float fpoints;     // n_points as a float: the box form divides the offsets by it
-  float* dref;       // backward: reference-point gradient per head group [B, Q, H / hg, L, ref_dim], or null
+  float inv_points;  // 1 / n_points when n_points is a power of two (x / P == x * (1 / P) exactly), else 0
+  float* dref;       // backward: reference-point gradient per head group [H / hg, B * Q, L, ref_dim], or null
+  int64_t bq_total;  // B * Q (rows per head group of `dref`)
   LevelDesc lv[kMaxLevels];
 };
 
@@ -119,8 +121,32 @@ struct ValueParams {
   int cap;     // records listed per segment (LDS list capacity)
   int g_vec4;  // grad_output rows may be read 4 channels at a time
   int vec16;   // grad_value rows may be written 16 bytes at a time
+  // fused prologue: the reference-point gradient's sum over head groups, done by this kernel's
+  // threads before their own work (ref_grad_sum), or ref_n = 0
+  const float* ref_part;
+  float* dref;
+  int64_t ref_n;
+  int ref_groups;
   LevelDesc lv[kMaxLevels];
 };
+
+// grad_reference_points [B, Q, L, ref_dim] (n elements) = the sum over head groups of the
+// per-group partials [groups][n], added in group order, four groups' loads in flight at once.
+// Thread `tid` of `nthreads` handles elements tid, tid + nthreads, ...
+__device__ __forceinline__ void ref_grad_sum(const float* __restrict__ part, float* __restrict__ dref, int64_t n, int groups,
+                                             int64_t tid, int64_t nthreads) {
+  for (int64_t i = tid; i < n; i += nthreads) {
+    const float* s = part + i;
+    float acc = 0.0f;
+    int g = 0;
+    for (; g + 4 <= groups; g += 4) {
+      const float a0 = s[(g + 0) * n], a1 = s[(g + 1) * n], a2 = s[(g + 2) * n], a3 = s[(g + 3) * n];
+      acc = (((acc + a0) + a1) + a2) + a3;
+    }
+    for (; g < groups; ++g) acc += s[g * n];
+    dref[i] = acc;
+  }
+}
 
 // LDS carve-up of one grad_value workgroup; shared by the host planner and the kernel. Every
 // region starts on a 16-byte boundary.
@@ -530,7 +556,8 @@ __device__ __forceinline__ void load_in(SampleIn<N>& f, const float2* __restrict
 // that no instantiation spills registers at four waves per SIMD).
 constexpr int query_group(int ns, int vec, bool backward, bool fused = false) {
   if (ns == 0) return 1;
-  if (fused) return vec >= 8 ? (ns <= 2 ? 2 : 1) : (ns <= 2 ? 4 : 2);  // + a reference point per sample
+  // + a reference point and a box offset per sample, and the backward's dA per sample
+  if (fused) return backward ? 1 : vec >= 8 ? (ns <= 2 ? 2 : 1) : (ns <= 2 ? 4 : 2);
   if (!backward) return ns <= 2 ? 4 : 2;
   if (vec >= 16) return ns <= 2 ? 2 : 1;
   if (vec == 8) return 2;
@@ -607,16 +634,23 @@ __device__ __forceinline__ SoftmaxStats softmax_stats(const float* __restrict__ 
   return st;
 }
 
+// From registers, when every sample of the row is loaded: the logits become the weights in place,
+// each exponential computed once.
 template <int N>
-__device__ __forceinline__ SoftmaxStats softmax_stats(const SampleIn<N>& f, int LP) {
-  SoftmaxStats st{-__builtin_inff(), 0.0f};
+__device__ __forceinline__ void softmax_regs(SampleIn<N>& f, int LP) {
+  float m = -__builtin_inff(), s = 0.0f;
 #pragma unroll
   for (int u = 0; u < N; ++u)
-    if (u < LP) st.m = fmaxf(st.m, f.a[u]);
+    if (u < LP) m = fmaxf(m, f.a[u]);
 #pragma unroll
   for (int u = 0; u < N; ++u)
-    if (u < LP) st.s += expf(f.a[u] - st.m);
-  return st;
+    if (u < LP) {
+      f.a[u] = expf(f.a[u] - m);
+      s += f.a[u];
+    }
+#pragma unroll
+  for (int u = 0; u < N; ++u)
+    if (u < LP) f.a[u] = f.a[u] / s;
 }
 
 // ops.py:388-399 for one sample. Points: ref + off / (W_l, H_l). Boxes: ref_xy + off / n_points *
@@ -628,18 +662,18 @@ __device__ __forceinline__ float2 fused_location(float2 off, float4 r, float2& t
     t = off;
     return make_float2(r.x + off.x / L.fw, r.y + off.y / L.fh);
   }
-  t = make_float2(off.x / p.fpoints, off.y / p.fpoints);
+  t = p.inv_points != 0.0f ? make_float2(off.x * p.inv_points, off.y * p.inv_points)
+                           : make_float2(off.x / p.fpoints, off.y / p.fpoints);
   return make_float2(r.x + (t.x * r.z) * 0.5f, r.y + (t.y * r.w) * 0.5f);
 }
 
-// Turns loaded (offset, logit) pairs of samples s0 .. s0 + N - 1 into (location, weight).
+// Turns loaded offsets of samples s0 .. s0 + N - 1 into locations.
 template <int N>
-__device__ __forceinline__ void fused_prologue(SampleIn<N>& f, FusedIn<N, true>& x, SoftmaxStats st, const SampleParams& p,
-                                               int s0, int LP, int l, int pt) {
+__device__ __forceinline__ void fused_locations(SampleIn<N>& f, FusedIn<N, true>& x, const SampleParams& p, int s0, int LP, int l,
+                                                int pt) {
 #pragma unroll
   for (int u = 0; u < N; ++u) {
     if (s0 + u < LP) {
-      f.a[u] = softmax_weight(f.a[u], st);
       f.xy[u] = fused_location(f.xy[u], x.r[u], x.t[u], p.lv[l], p);
       if (++pt == p.points) {
         pt = 0;
@@ -647,6 +681,24 @@ __device__ __forceinline__ void fused_prologue(SampleIn<N>& f, FusedIn<N, true>&
       }
     }
   }
+}
+
+// Turns loaded (offset, logit) pairs of samples s0 .. s0 + N - 1 into (location, weight), with the
+// row's softmax statistics.
+template <int N>
+__device__ __forceinline__ void fused_prologue(SampleIn<N>& f, FusedIn<N, true>& x, SoftmaxStats st, const SampleParams& p,
+                                               int s0, int LP, int l, int pt) {
+#pragma unroll
+  for (int u = 0; u < N; ++u)
+    if (s0 + u < LP) f.a[u] = softmax_weight(f.a[u], st);
+  fused_locations<N>(f, x, p, s0, LP, l, pt);
+}
+
+// The same when the row's samples are all in registers (s0 = 0, N >= LP).
+template <int N>
+__device__ __forceinline__ void fused_prologue_row(SampleIn<N>& f, FusedIn<N, true>& x, const SampleParams& p, int LP) {
+  softmax_regs<N>(f, LP);
+  fused_locations<N>(f, x, p, 0, LP, 0, 0);
 }
 
 // Backward state of one (query, head) row: sum_k a_k dA_k for the softmax VJP, and the running
@@ -668,12 +720,13 @@ __device__ __forceinline__ float2 fused_sample_grads(float2 gl, float a, float d
   const float hx = gl.x * 0.5f, hy = gl.y * 0.5f;
   fa.r[2] += hx * t.x;
   fa.r[3] += hy * t.y;
+  if (p.inv_points != 0.0f) return make_float2((hx * r.z) * p.inv_points, (hy * r.w) * p.inv_points);
   return make_float2((hx * r.z) / p.fpoints, (hy * r.w) / p.fpoints);
 }
 
 // End of a level: sums the reference-point gradient over the head group's lanes (hg * lanes per
 // (query, head) <= 64, a power of two, so the group is aligned inside one wave) and writes it for
-// (b, q, head group, level); the sum over groups is ref_grad_kernel's.
+// (head group, b, q, level); the sum over groups is ref_grad_kernel's.
 __device__ __forceinline__ void flush_ref_grad(FusedAcc& fa, const SampleParams& p, int hl, int j, int64_t bq, int group,
                                                int l) {
   const int lpq = 1 << p.lpq_shift;
@@ -682,8 +735,11 @@ __device__ __forceinline__ void flush_ref_grad(FusedAcc& fa, const SampleParams&
     for (int k = 0; k < 4; ++k) fa.r[k] += __shfl_xor(fa.r[k], o, 64);
   }
   if (p.dref != nullptr && hl == 0 && j == 0) {
-    float* d = p.dref + ((bq * (p.heads / p.hg) + group) * p.levels + l) * p.ref_dim;
-    for (int k = 0; k < p.ref_dim; ++k) d[k] = fa.r[k];
+    // group-major [H / hg][B * Q][L][ref_dim], so the reduction reads each group's rows contiguously
+    float* d = p.dref + ((static_cast<int64_t>(group) * p.bq_total + bq) * p.levels + l) * p.ref_dim;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < p.ref_dim) d[k] = fa.r[k];  // constant indices keep fa.r in registers
   }
 #pragma unroll
   for (int k = 0; k < 4; ++k) fa.r[k] = 0.0f;
@@ -825,7 +881,7 @@ fwd_kernel(const SampleParams p) {
       if constexpr (kFused) {
 #pragma unroll
         for (int i = 0; i < QU; ++i)
-          if (qg + i * ln.qpp < q_hi) fused_prologue<NS>(in[i], fin[i], softmax_stats<NS>(in[i], LP), p, 0, LP, 0, 0);
+          if (qg + i * ln.qpp < q_hi) fused_prologue_row<NS>(in[i], fin[i], p, LP);
       }
 #pragma unroll
       for (int i = 0; i < QU; ++i) {
@@ -939,11 +995,13 @@ __device__ __forceinline__ void emit_record(const SampleParams& p, const SampleB
   *at(sb.bins, idx) = payload;
 }
 
-template <typename VT, int VEC, int N, bool kStaged, bool kFused>
+// kKeepDA (fused, grouped path): each sample's dA stays in dA_out for the softmax VJP, instead
+// of passing through grad_logits in memory.
+template <typename VT, int VEC, int N, bool kStaged, bool kFused, bool kKeepDA = false>
 __device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const FusedIn<N, kFused>& x, FusedAcc& fa, const float (&g)[VEC],
                                          int s0, int LP, int& l, int& pt, const SampleParams& p, const SampleLane& ln,
                                          const VT* hlds, const VT* __restrict__ vs, const SampleBases& sb, uint32_t lrow, int* lcnt,
-                                         int qoff, int qb, int64_t bq, int group) {
+                                         int qoff, int qb, int64_t bq, int group, float (&dA_out)[N]) {
   const int D = p.dim;
   const int lpq = 1 << p.lpq_shift;
 #pragma unroll
@@ -969,8 +1027,9 @@ __device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const FusedIn<N, 
         const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
         const float2 gl = make_float2(a * L.fw * dx, a * L.fh * dy);
         const float2 goff = fused_sample_grads(gl, a, dA, x.r[u], x.t[u], L, p, fa);
+        if constexpr (kKeepDA) dA_out[u] = dA;
         if (ln.j == 0) {
-          if (sb.dattn) *at(sb.dattn, si) = dA;  // grad_logits holds dA until fused_logit_grads
+          if (!kKeepDA && sb.dattn) *at(sb.dattn, si) = dA;  // grad_logits holds dA until fused_logit_grads
           if (sb.dloc) *at(sb.dloc, si) = goff;
         }
         if (p.dref != nullptr && pt + 1 == p.points) flush_ref_grad(fa, p, ln.hl, ln.j, bq, group, l);
@@ -1017,12 +1076,11 @@ __device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const FusedIn<N, 
   }
 }
 
-// kFused (only with NS == 0): `loc` / `attn` are raw offsets and logits; `dloc` / `dattn` receive
-// grad_offsets / grad_logits and `dref` the per-head-group reference-point gradients.
+// kFused: `loc` / `attn` are raw offsets and logits; `dloc` / `dattn` receive grad_offsets /
+// grad_logits and `dref` the per-head-group reference-point gradients.
 template <typename VT, int VEC, int NS, bool kStaged, bool kFused>
 __global__ void __launch_bounds__(kSampleMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
 bwd_sample_kernel(const SampleParams p) {
-  static_assert(!kFused || NS == 0, "the fused prologue runs in the per-query sample loop");
   extern __shared__ __align__(16) unsigned char lds_raw[];
   VT* lds = reinterpret_cast<VT*>(lds_raw);
   const SampleItem it = sample_item(p);
@@ -1050,7 +1108,7 @@ bwd_sample_kernel(const SampleParams p) {
   int* lcnt = reinterpret_cast<int*>(lds_raw + align16i(p.hg * p.head_lds * static_cast<int>(sizeof(VT))));
   const int ncnt = p.bins ? p.hg * p.nwork : 0;
   for (int i = threadIdx.x; i < ncnt; i += blockDim.x) lcnt[i] = 0;
-  constexpr int QU = query_group(NS, VEC, true);
+  constexpr int QU = query_group(NS, VEC, true, kFused);
   constexpr int NI = NS == 0 ? 1 : NS;
   const int q_first = q_lo + ln.qs;
   const uint32_t lrow_first = lrow_of(q_first);
@@ -1075,12 +1133,14 @@ bwd_sample_kernel(const SampleParams p) {
       }
     }
   };
+  FusedIn<NI, kFused> fin[QU];
   auto load_inputs = [&](uint32_t lrow0, int q0) {
 #pragma unroll
     for (int i = 0; i < QU; ++i)
       if (q0 + i * ln.qpp < q_hi) {
         const uint32_t r = (lrow0 + i * lrow_step) * static_cast<uint32_t>(LP);
         load_in<NI>(in[i], at(sb.loc, r), at(sb.attn, r), 0, LP);
+        if constexpr (kFused) load_refs<NI>(fin[i], p, bq0 + q0 + i * ln.qpp, 0, LP, 0, 0);
       }
   };
   if constexpr (NS > 0) {
@@ -1107,10 +1167,20 @@ bwd_sample_kernel(const SampleParams p) {
         const int q = qg + i * ln.qpp;
         if (q < q_hi) {
           int l = 0, pt = 0;
-          FusedIn<NI, false> none;
           FusedAcc fa{};
-          bwd_pass<VT, VEC, NS, kStaged, false>(in[i], none, fa, g[i], 0, LP, l, pt, p, ln, hlds, vs, sb, lrow0 + i * lrow_step, lcnt,
-                                                q - q_lo, it.qb, 0, 0);
+          float dA[NI];
+          if constexpr (kFused) fused_prologue_row<NI>(in[i], fin[i], p, LP);
+          const uint32_t lrow = lrow0 + i * lrow_step;
+          bwd_pass<VT, VEC, NS, kStaged, kFused, kFused>(in[i], fin[i], fa, g[i], 0, LP, l, pt, p, ln, hlds, vs, sb, lrow, lcnt,
+                                                         q - q_lo, it.qb, bq0 + q, group, dA);
+          if constexpr (kFused) {
+            // softmax VJP from registers: grad_logit_u = a_u (dA_u - sum_k a_k dA_k)
+            if (sb.dattn && ln.j == 0) {
+#pragma unroll
+              for (int u = 0; u < NI; ++u)
+                if (u < LP) *at(sb.dattn, lrow * static_cast<uint32_t>(LP) + u) = in[i].a[u] * (dA[u] - fa.S);
+            }
+          }
         }
       }
     }
@@ -1132,8 +1202,9 @@ bwd_sample_kernel(const SampleParams p) {
           load_refs<PB>(x, p, bq0 + q, s0, LP, l, pt);
           fused_prologue<PB>(f, x, st, p, s0, LP, l, pt);
         }
+        float unused[PB];
         bwd_pass<VT, VEC, PB, kStaged, kFused>(f, x, fa, g[0], s0, LP, l, pt, p, ln, hlds, vs, sb, lrow, lcnt, q - q_lo, it.qb,
-                                               bq0 + q, group);
+                                               bq0 + q, group, unused);
       }
       if constexpr (kFused)
         if (sb.dattn && ln.j == 0) fused_logit_grads(at(sb.attn, r), at(sb.dattn, r), LP, st, fa.S);
@@ -1290,6 +1361,9 @@ template <typename VT, int CG, int NACC>
 __global__ void __launch_bounds__(kValueMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
 bwd_value_kernel(const ValueParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
+  if (p.ref_n > 0)
+    ref_grad_sum(p.ref_part, p.dref, p.ref_n, p.ref_groups, static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x,
+                 static_cast<int64_t>(gridDim.x) * blockDim.x);
 
   const int lid = xcd_logical(blockIdx.x, gridDim.x);
   const int h = lid % p.heads;

@@ -70,17 +70,15 @@ int fwd_ns(int ns, const msda::SampleParams& p, int grid, int threads, int lds, 
   }
 }
 
-// The fused prologue's backward runs in the per-query sample loop (NS = 0) only.
-template <typename VT, int VEC>
-int bwd_ns(int ns, bool fused, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t st) {
-  if (fused) return launch_bwd_sample<VT, VEC, 0, false, true>(p, grid, threads, lds, st);
+template <typename VT, int VEC, bool FUSED>
+int bwd_ns(int ns, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t st) {
   const bool staged = p.all_staged != 0;
   switch (ns) {
-    case 2: return staged ? launch_bwd_sample<VT, VEC, 2, true, false>(p, grid, threads, lds, st)
-                          : launch_bwd_sample<VT, VEC, 2, false, false>(p, grid, threads, lds, st);
-    case 4: return staged ? launch_bwd_sample<VT, VEC, 4, true, false>(p, grid, threads, lds, st)
-                          : launch_bwd_sample<VT, VEC, 4, false, false>(p, grid, threads, lds, st);
-    default: return launch_bwd_sample<VT, VEC, 0, false, false>(p, grid, threads, lds, st);
+    case 2: return staged ? launch_bwd_sample<VT, VEC, 2, true, FUSED>(p, grid, threads, lds, st)
+                          : launch_bwd_sample<VT, VEC, 2, false, FUSED>(p, grid, threads, lds, st);
+    case 4: return staged ? launch_bwd_sample<VT, VEC, 4, true, FUSED>(p, grid, threads, lds, st)
+                          : launch_bwd_sample<VT, VEC, 4, false, FUSED>(p, grid, threads, lds, st);
+    default: return launch_bwd_sample<VT, VEC, 0, false, FUSED>(p, grid, threads, lds, st);
   }
 }
 
@@ -99,11 +97,11 @@ int dispatch_fwd(int vec, int ns, bool fused, const msda::SampleParams& p, int g
 template <typename VT>
 int dispatch_bwd_sample(int vec, int ns, bool fused, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t st) {
   switch (vec) {
-    case 1: return bwd_ns<VT, 1>(ns, fused, p, grid, threads, lds, st);
-    case 2: return bwd_ns<VT, 2>(ns, fused, p, grid, threads, lds, st);
-    case 4: return bwd_ns<VT, 4>(ns, fused, p, grid, threads, lds, st);
-    case 8: return bwd_ns<VT, 8>(ns, fused, p, grid, threads, lds, st);
-    case 16: return bwd_ns<VT, 16>(ns, fused, p, grid, threads, lds, st);
+    case 1: return fused ? bwd_ns<VT, 1, true>(ns, p, grid, threads, lds, st) : bwd_ns<VT, 1, false>(ns, p, grid, threads, lds, st);
+    case 2: return fused ? bwd_ns<VT, 2, true>(ns, p, grid, threads, lds, st) : bwd_ns<VT, 2, false>(ns, p, grid, threads, lds, st);
+    case 4: return fused ? bwd_ns<VT, 4, true>(ns, p, grid, threads, lds, st) : bwd_ns<VT, 4, false>(ns, p, grid, threads, lds, st);
+    case 8: return fused ? bwd_ns<VT, 8, true>(ns, p, grid, threads, lds, st) : bwd_ns<VT, 8, false>(ns, p, grid, threads, lds, st);
+    case 16: return fused ? bwd_ns<VT, 16, true>(ns, p, grid, threads, lds, st) : bwd_ns<VT, 16, false>(ns, p, grid, threads, lds, st);
   }
   return fail(MSDA_ERR_UNSUPPORTED, "no kernel for %d channels per lane", vec);
 }
