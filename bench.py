@@ -271,6 +271,57 @@ def measure_fused(w, dev, steps, warmup):
     }
 
 
+def measure_point_sample(dev, steps, masks=400, size=112, ratio=16):
+    """The segmentation loss's point sampling (criterion.py:482-488, segmentation.py:200-233) on
+    one-channel size x size mask logits: point_sample on 3 x P uncertainty candidates, on the P
+    chosen points with the gradient of the logits, and nearest sampling of the labels at the same
+    points (P = size^2 / ratio). Beside it, the same three samplings with torch's F.grid_sample."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from rfdetr_jax_amd import _native
+    from rfdetr_jax_amd.grid_sample import grid_sample_backward, grid_sample_forward
+
+    rng = np.random.default_rng(7)
+    npts = size * size // ratio
+    logits = torch.from_numpy(rng.standard_normal((masks, 1, size, size), dtype=np.float32)).to(dev)
+    labels = torch.from_numpy((rng.uniform(0, 1, (masks, 1, size, size)) > 0.5).astype(np.float32)).to(dev)
+    cand = torch.from_numpy(rng.uniform(0, 1, (masks, 3 * npts, 2)).astype(np.float32)).to(dev)
+    pts = torch.from_numpy(rng.uniform(0, 1, (masks, npts, 2)).astype(np.float32)).to(dev)
+    gout = torch.from_numpy(rng.standard_normal((masks, 1, npts), dtype=np.float32)).to(dev)
+    unit, border = _native.GRID_UNIT_POINTS, _native.PADDING["border"]
+    bil, near = _native.SAMPLE_BILINEAR, _native.SAMPLE_NEAREST
+
+    def ours(_h):
+        grid_sample_forward(logits, cand, unit, border, bil)
+        grid_sample_forward(logits, pts, unit, border, bil)
+        grid_sample_backward(logits, pts, gout, unit, border, bil, needs=(True, False))
+        grid_sample_forward(labels, pts, unit, border, near)
+
+    cgrid, pgrid = (2 * cand - 1)[:, :, None, :], (2 * pts - 1)[:, :, None, :]
+    lg = logits.clone().requires_grad_(True)
+
+    def torch_step(_h):
+        with torch.no_grad():
+            F.grid_sample(logits, cgrid, mode="bilinear", padding_mode="border", align_corners=False)
+        out = F.grid_sample(lg, pgrid, mode="bilinear", padding_mode="border", align_corners=False)
+        torch.autograd.grad(out, lg, gout[..., None])
+        with torch.no_grad():
+            F.grid_sample(labels, pgrid, mode="nearest", padding_mode="border", align_corners=False)
+
+    for _ in range(3):
+        ours(None)
+        torch_step(None)
+    torch.cuda.synchronize()
+    return {
+        "masks": masks, "mask_size": size, "points": npts, "candidates": 3 * npts,
+        "step_us": round(time_graph(ours, steps)[0], 3),
+        "torch_grid_sample_step_us": round(time_eager(torch_step, steps), 3),
+        "step_us_eager": round(time_eager(ours, steps), 3),
+    }
+
+
 def cpu_baseline(calls, budget_s=3.0, max_reps=20):
     """fwd+bwd of the C oracle on the same inputs; median us/call."""
     from oracle import cref
@@ -339,6 +390,8 @@ def main():
                          "--copy-mb buffer (counter calibration); prints one JSON line of timings")
     ap.add_argument("--copy-mb", type=int, default=256)
     ap.add_argument("--fused", action="store_true", help="with --profile: the fused-prologue op instead of the core")
+    ap.add_argument("--profile-point-sample", action="store_true",
+                    help="for rocprofv3 runs: K eager steps of the segmentation loss's point sampling, ours then torch's")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): the deformable-attention op needs no "
@@ -356,6 +409,9 @@ def main():
     w = CONFIGS[args.config]
     if args.profile:
         profile_run(w, dev, args.steps, args.warmup, args.copy_mb, args.fused)
+        return
+    if args.profile_point_sample:
+        print(json.dumps(measure_point_sample(dev, args.steps)), flush=True)
         return
     log(f"workload {w.name}: warmup {args.warmup}, steps {args.steps}")
     res, calls = measure(w, dev, args.steps, args.warmup)
@@ -391,6 +447,8 @@ def main():
         if w.backward:
             log("fused prologue")
             per_config[f"fused_prologue_{w.name}"] = measure_fused(w, dev, max(50, args.steps // 2), 10)
+        log("point sample (segmentation loss)")
+        per_config["point_sample_mask_loss_400x112x112"] = measure_point_sample(dev, max(50, args.steps // 2))
 
     cpu = None
     if not args.no_cpu_baseline:

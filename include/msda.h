@@ -179,6 +179,44 @@ int msda_fused_bwd(const void* value, int value_dtype,
                    const int32_t* spatial_shapes, const int32_t* level_start_index,
                    int64_t len_value, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Grid sampling of channels-first feature maps: bilinear_grid_sample and point_sample of the
+ * segmentation head. Replaces
+ *   bilinear_grid_sample(inputs, grid, padding_mode)   src/rfdetr_jax/models/ops.py:189-205
+ *     (the sampler _sample_rows with padding_mode,    ops.py:64-134)
+ *   point_sample(inputs, point_coords, mode)           src/rfdetr_jax/models/heads/segmentation.py:146-170
+ *     (nearest sampling, _nearest_grid_sample,         segmentation.py:173-186)
+ * and their JAX autodiff VJPs.
+ * Layouts (row-major, contiguous):
+ *   input        [n, channels, height, width]   dtype (MSDA_DTYPE_F32 or MSDA_DTYPE_BF16)
+ *   grid         [n, n_points, 2] f32 (x, y): grid coordinates in [-1, 1] (MSDA_GRID_COORDS,
+ *                bilinear_grid_sample; n_points = Hg * Wg) or point_sample's points in [0, 1]
+ *                (MSDA_GRID_UNIT_POINTS; the kernel forms grid = 2 p - 1, segmentation.py:166)
+ *   output       [n, channels, n_points]        dtype
+ * Semantics: torch grid_sample(align_corners=False) as ops.py:64-134 writes it; zero padding masks
+ * out-of-bounds corners, border padding clips them (the unmasked weights replicate the edge);
+ * nearest sampling rounds half to even and clips, with border padding only.
+ */
+enum msda_grid_kind { MSDA_GRID_COORDS = 0, MSDA_GRID_UNIT_POINTS = 1 };
+enum msda_padding { MSDA_PADDING_ZEROS = 0, MSDA_PADDING_BORDER = 1 };
+enum msda_sample_mode { MSDA_SAMPLE_BILINEAR = 0, MSDA_SAMPLE_NEAREST = 1 };
+
+int msda_grid_sample_fwd(const void* input, int dtype, const float* grid, int grid_kind,
+                         void* output, int n, int channels, int height, int width, int n_points,
+                         int padding_mode, int sample_mode, void* stream);
+
+/*
+ * Backward of msda_grid_sample_fwd for cotangent grad_output [n, channels, n_points] (dtype):
+ *   grad_input [n, channels, height, width] dtype (accumulated in f32, fully written: no
+ *              zero-fill needed), and grad_grid [n, n_points, 2] f32 (the gradient of the grid
+ *              coordinates or of the unit points, per grid_kind; zero for nearest sampling).
+ * Either output may be NULL. Widths above 16384 are MSDA_ERR_UNSUPPORTED for grad_input.
+ */
+int msda_grid_sample_bwd(const void* input, int dtype, const float* grid, int grid_kind,
+                         const void* grad_output, void* grad_input, float* grad_grid,
+                         int n, int channels, int height, int width, int n_points,
+                         int padding_mode, int sample_mode, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

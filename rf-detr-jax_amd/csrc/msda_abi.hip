@@ -50,6 +50,8 @@ int raise_lds_limit(const void* kernel, int bytes, std::atomic<int>* granted) {
   return MSDA_OK;
 }
 
+void clear_error() { g_last_error.clear(); }
+
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MSDA_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
@@ -386,6 +388,19 @@ int plan_bins(const Shape& s, const DevInfo& dev, BinPlan* bp) {
 }
 
 }  // namespace
+
+namespace msda_host {
+bool env_flag(const char* name) { return env_int(name, 0) != 0; }
+
+int device_attrs(int* lds_bytes, int* cus) {
+  DevInfo d;
+  const int rc = device_info(&d);
+  if (rc != MSDA_OK) return rc;
+  *lds_bytes = d.lds_bytes;
+  *cus = d.cus;
+  return MSDA_OK;
+}
+}  // namespace msda_host
 
 namespace msda {
 

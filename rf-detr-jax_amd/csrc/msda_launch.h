@@ -15,9 +15,14 @@ namespace msda_host {
 constexpr int kMaxDevices = 64;
 
 // Defined in msda_abi.hip.
-int fail(int code, const char* fmt, ...);
+int fail(int code, const char* fmt, ...);  // records the message for msda_last_error(), returns code
+void clear_error();                          // at the start of every C-ABI call
 int raise_lds_limit(const void* kernel, int bytes, std::atomic<int>* granted);
 int check_launch(const char* what);
+int device_attrs(int* lds_bytes, int* cus);  // of the current device, cached per device
+bool env_flag(const char* name);              // an environment switch set to a non-zero integer
+
+inline bool aligned_to(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // Allow a kernel instantiation to use more than 64 KB of dynamic LDS (once per instantiation and
 // device; `granted` is that instantiation's per-device record).

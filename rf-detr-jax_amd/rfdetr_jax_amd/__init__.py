@@ -5,6 +5,7 @@ Host-side mirror of the reference interface ``rfdetr_jax.models.ops``
 backed by hand-written HIP kernels through the C ABI in include/msda.h.
 """
 
+from .grid_sample import bilinear_grid_sample, point_sample
 from .ops import (
     SAMPLERS,
     ms_deform_attn,
@@ -19,6 +20,8 @@ from .ops import (
 
 __all__ = [
     "SAMPLERS",
+    "bilinear_grid_sample",
+    "point_sample",
     "ms_deform_attn",
     "ms_deform_attn_backward",
     "ms_deform_attn_core",

@@ -36,7 +36,15 @@ SIGNATURES = {
     "msda_fused_fwd": ([_P, _I, _P, _I, _P, _P, _P, _I] + _DIMS + [_P], _I),
     "msda_fused_bwd_workspace_size": ([_I] * 7 + [_I32P, _I32P, _I64], _I64),
     "msda_fused_bwd": ([_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P] + _DIMS + [_P, _I64, _P], _I),
+    "msda_grid_sample_fwd": ([_P, _I, _P, _I, _P] + [_I] * 7 + [_P], _I),
+    "msda_grid_sample_bwd": ([_P, _I, _P, _I, _P, _P, _P] + [_I] * 7 + [_P], _I),
 }
+
+GRID_COORDS = 0
+GRID_UNIT_POINTS = 1
+PADDING = {"zeros": 0, "border": 1}
+SAMPLE_BILINEAR = 0
+SAMPLE_NEAREST = 1
 
 _lock = threading.Lock()
 _lib = None

@@ -305,3 +305,70 @@ def test_fused_cpu_tensors_fail_loudly():
     value, ref, off, logits = _cpu_fused_inputs()
     with pytest.raises(RuntimeError, match="no CPU path"):
         hip_ops.ms_deform_attn_fused(value, ((4, 4),), ref, off, logits)
+
+
+# --------------------------------------------------------------------------------------------
+# grid sampling (msda_grid_sample_fwd / msda_grid_sample_bwd) and its mirror
+
+
+def _gs_fwd(**kw):
+    args = dict(inp=1 << 20, dt=0, grid=1 << 20, kind=0, out=1 << 20, n=2, c=1, h=8, w=8, p=16, pad=0, mode=0)
+    args.update(kw)
+    lib = _native.lib()
+    rc = lib.msda_grid_sample_fwd(ctypes.c_void_p(args["inp"]), args["dt"], ctypes.c_void_p(args["grid"]), args["kind"],
+                                  ctypes.c_void_p(args["out"]), args["n"], args["c"], args["h"], args["w"], args["p"],
+                                  args["pad"], args["mode"], None)
+    return rc, lib.msda_last_error().decode()
+
+
+def _gs_bwd(**kw):
+    args = dict(inp=1 << 20, dt=0, grid=1 << 20, kind=1, gout=1 << 20, gin=1 << 20, ggrid=1 << 20, n=2, c=1, h=8, w=8, p=16,
+                pad=1, mode=0)
+    args.update(kw)
+    lib = _native.lib()
+    rc = lib.msda_grid_sample_bwd(ctypes.c_void_p(args["inp"]), args["dt"], ctypes.c_void_p(args["grid"]), args["kind"],
+                                  ctypes.c_void_p(args["gout"]), ctypes.c_void_p(args["gin"]), ctypes.c_void_p(args["ggrid"]),
+                                  args["n"], args["c"], args["h"], args["w"], args["p"], args["pad"], args["mode"], None)
+    return rc, lib.msda_last_error().decode()
+
+
+@pytest.mark.parametrize("call", [_gs_fwd, _gs_bwd])
+@pytest.mark.parametrize(
+    "kw, code, message",
+    [
+        (dict(dt=5), _native.ERR_UNSUPPORTED, "dtype"),
+        (dict(pad=2), _native.ERR_INVALID_ARGUMENT, "padding_mode"),
+        (dict(kind=3), _native.ERR_INVALID_ARGUMENT, "grid_kind"),
+        (dict(mode=2), _native.ERR_INVALID_ARGUMENT, "sample mode"),
+        (dict(mode=1, pad=0), _native.ERR_UNSUPPORTED, "border padding only"),
+        (dict(c=0), _native.ERR_INVALID_ARGUMENT, "channels"),
+        (dict(n=-1), _native.ERR_INVALID_ARGUMENT, "n ("),
+        (dict(grid=0), _native.ERR_INVALID_ARGUMENT, "NULL"),
+        (dict(grid=(1 << 20) + 4), _native.ERR_INVALID_ARGUMENT, "aligned"),
+    ],
+)
+def test_grid_sample_invalid_arguments_are_reported(call, kw, code, message):
+    rc, msg = call(**kw)
+    assert rc == code, msg
+    assert message in msg
+
+
+def test_grid_sample_empty_calls_are_no_ops():
+    assert _gs_fwd(n=0)[0] == _native.OK
+    assert _gs_fwd(p=0)[0] == _native.OK
+    assert _gs_bwd(n=0)[0] == _native.OK
+    assert _gs_bwd(gin=0, ggrid=0)[0] == _native.OK
+
+
+def test_grid_sample_mirror_errors():
+    from rfdetr_jax_amd import grid_sample as gs
+
+    inputs, grid = torch.zeros(1, 1, 2, 2), torch.zeros(1, 1, 1, 2)
+    with pytest.raises(ValueError, match="padding_mode"):
+        gs.bilinear_grid_sample(inputs, grid, "reflection")
+    with pytest.raises(ValueError, match="bilinear and nearest"):
+        gs.point_sample(inputs, torch.zeros(1, 1, 2), mode="bicubic")
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        gs.point_sample(inputs, torch.zeros(1, 1, 2))
+    with pytest.raises(TypeError, match="not supported"):
+        gs.bilinear_grid_sample(inputs.double(), grid)
