@@ -322,6 +322,48 @@ def measure_point_sample(dev, steps, masks=400, size=112, ratio=16):
     }
 
 
+def measure_value_proj(dev, steps, batch=8, seq=576, d_model=256, heads=16):
+    """MSDeformAttn's value path at the config-2 memory shape (8 x 24x24 positions, d_model 256, 16
+    heads): the fused projection (msda_value_proj_fwd, then _bwd for all three gradients) beside
+    torch's F.linear + masked_fill + view/permute/contiguous and its autograd backward."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from rfdetr_jax_amd.value_proj import value_proj_backward, value_proj_forward
+
+    rng = np.random.default_rng(9)
+    x = torch.from_numpy(rng.standard_normal((batch, seq, d_model), dtype=np.float32)).to(dev)
+    w = torch.from_numpy((rng.standard_normal((d_model, d_model)) / 16).astype(np.float32)).to(dev)
+    b = torch.from_numpy(rng.standard_normal(d_model).astype(np.float32)).to(dev)
+    mask = torch.from_numpy(rng.uniform(0, 1, (batch, seq)) < 0.05).to(dev)
+    d = d_model // heads
+    gv = torch.from_numpy(rng.standard_normal((batch * heads, seq, d), dtype=np.float32)).to(dev)
+
+    def ours(_h):
+        value_proj_forward(x, w, b, heads, mask)
+        value_proj_backward(x, w, heads, gv, mask)
+
+    xt, wt, bt = (t.clone().requires_grad_(True) for t in (x, w, b))
+
+    def torch_step(_h):
+        y = F.linear(xt, wt, bt).masked_fill(mask[..., None], 0.0)
+        v = y.view(batch, seq, heads, d).permute(0, 2, 1, 3).reshape(batch * heads, seq, d)
+        torch.autograd.grad(v, (xt, wt, bt), gv)
+
+    for _ in range(3):
+        ours(None)
+        torch_step(None)
+    torch.cuda.synchronize()
+    return {
+        "shape": {"batch": batch, "len_in": seq, "d_model": d_model, "heads": heads},
+        "fwd_us": round(time_graph(lambda h: value_proj_forward(x, w, b, heads, mask), steps)[0], 3),
+        "step_us": round(time_graph(ours, steps)[0], 3),
+        "step_us_eager": round(time_eager(ours, steps), 3),
+        "torch_step_us_eager": round(time_eager(torch_step, steps), 3),
+    }
+
+
 def cpu_baseline(calls, budget_s=3.0, max_reps=20):
     """fwd+bwd of the C oracle on the same inputs; median us/call."""
     from oracle import cref
@@ -392,6 +434,8 @@ def main():
     ap.add_argument("--fused", action="store_true", help="with --profile: the fused-prologue op instead of the core")
     ap.add_argument("--profile-point-sample", action="store_true",
                     help="for rocprofv3 runs: K eager steps of the segmentation loss's point sampling, ours then torch's")
+    ap.add_argument("--profile-value-proj", action="store_true",
+                    help="for rocprofv3 runs: K eager steps of the value projection fwd+bwd, ours then torch's")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): the deformable-attention op needs no "
@@ -412,6 +456,9 @@ def main():
         return
     if args.profile_point_sample:
         print(json.dumps(measure_point_sample(dev, args.steps)), flush=True)
+        return
+    if args.profile_value_proj:
+        print(json.dumps(measure_value_proj(dev, args.steps)), flush=True)
         return
     log(f"workload {w.name}: warmup {args.warmup}, steps {args.steps}")
     res, calls = measure(w, dev, args.steps, args.warmup)
@@ -447,6 +494,8 @@ def main():
         if w.backward:
             log("fused prologue")
             per_config[f"fused_prologue_{w.name}"] = measure_fused(w, dev, max(50, args.steps // 2), 10)
+        log("value projection")
+        per_config["value_proj_b8_s576_c256_h16"] = measure_value_proj(dev, max(50, args.steps // 2))
         log("point sample (segmentation loss)")
         per_config["point_sample_mask_loss_400x112x112"] = measure_point_sample(dev, max(50, args.steps // 2))
 

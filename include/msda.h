@@ -217,6 +217,39 @@ int msda_grid_sample_bwd(const void* input, int dtype, const float* grid, int gr
                          int n, int channels, int height, int width, int n_points,
                          int padding_mode, int sample_mode, void* stream);
 
+/*
+ * MSDeformAttn's value projection with its epilogue fused in: one MFMA product writes
+ *   value[(b * n_heads + h) * len_in + s][d] = padded[b, s] ? 0 : (input[b, s, :] . W[h * head_dim + d, :] + bias[h * head_dim + d])
+ * Replaces value_proj (Linear, src/rfdetr_jax/models/layers.py:258-280: x @ W^T + b in the input
+ * dtype), the padding mask (ops.py:377-379) and the head split (ops.py:405-407) of
+ * MSDeformAttn.__call__, so the [B, S, C] projection and its transpose never exist in memory.
+ * Layouts:
+ *   input         [batch, len_in, in_features]           dtype (MSDA_DTYPE_F32 or MSDA_DTYPE_BF16)
+ *   weight        [n_heads * head_dim, in_features] f32  (torch Linear layout; rounded to bf16 when
+ *                                                        the input is bf16, as weight.astype(x.dtype))
+ *   bias          [n_heads * head_dim] f32 or NULL
+ *   padding_mask  [batch, len_in] uint8 (non-zero = padded) or NULL
+ *   value         [batch * n_heads, len_in, head_dim]    dtype (the core's value layout)
+ */
+int msda_value_proj_fwd(const void* input, int dtype, const float* weight, const float* bias,
+                        const uint8_t* padding_mask, void* value,
+                        int batch, int len_in, int in_features, int n_heads, int head_dim, void* stream);
+
+/* Workspace of msda_value_proj_bwd in bytes (a function of the shape only), or a negative code. */
+int64_t msda_value_proj_bwd_workspace_size(int batch, int len_in, int in_features, int n_heads, int head_dim);
+
+/*
+ * Backward of msda_value_proj_fwd for cotangent grad_value [batch * n_heads, len_in, head_dim]:
+ *   grad_input  [batch, len_in, in_features] dtype, grad_weight [n_heads * head_dim, in_features]
+ *   f32, grad_bias [n_heads * head_dim] f32; padded rows contribute nothing. Any of the three may be
+ * NULL. The workspace (16-byte aligned) holds grad_weight's split partial sums and is needed when
+ * grad_weight or grad_bias is requested; they are added in a fixed order (deterministic).
+ */
+int msda_value_proj_bwd(const void* input, int dtype, const float* weight, const uint8_t* padding_mask,
+                        const void* grad_value, void* grad_input, float* grad_weight, float* grad_bias,
+                        int batch, int len_in, int in_features, int n_heads, int head_dim,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

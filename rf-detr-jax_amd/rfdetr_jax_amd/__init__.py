@@ -2,7 +2,9 @@
 
 Host-side mirror of the reference interface ``rfdetr_jax.models.ops``
 (src/rfdetr_jax/models/ops.py:208-314): the same function names, argument meanings and errors,
-backed by hand-written HIP kernels through the C ABI in include/msda.h.
+backed by hand-written HIP kernels through the C ABI in include/msda.h. Also the module around it
+(``MSDeformAttn``, ops.py:326-411) with its prologue, value projection and head split fused into the
+kernels, and the segmentation head's point sampling (``bilinear_grid_sample``, ``point_sample``).
 """
 
 from .grid_sample import bilinear_grid_sample, point_sample
@@ -17,11 +19,12 @@ from .ops import (
     ms_deform_attn_fused_backward,
     ms_deform_attn_fused_forward,
 )
+from .value_proj import MSDeformAttn, value_proj_rows
 
 __all__ = [
+    "MSDeformAttn",
     "SAMPLERS",
     "bilinear_grid_sample",
-    "point_sample",
     "ms_deform_attn",
     "ms_deform_attn_backward",
     "ms_deform_attn_core",
@@ -30,4 +33,6 @@ __all__ = [
     "ms_deform_attn_fused",
     "ms_deform_attn_fused_backward",
     "ms_deform_attn_fused_forward",
+    "point_sample",
+    "value_proj_rows",
 ]

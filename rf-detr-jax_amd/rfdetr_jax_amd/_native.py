@@ -38,6 +38,9 @@ SIGNATURES = {
     "msda_fused_bwd": ([_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P] + _DIMS + [_P, _I64, _P], _I),
     "msda_grid_sample_fwd": ([_P, _I, _P, _I, _P] + [_I] * 7 + [_P], _I),
     "msda_grid_sample_bwd": ([_P, _I, _P, _I, _P, _P, _P] + [_I] * 7 + [_P], _I),
+    "msda_value_proj_fwd": ([_P, _I, _P, _P, _P, _P] + [_I] * 5 + [_P], _I),
+    "msda_value_proj_bwd_workspace_size": ([_I] * 5, _I64),
+    "msda_value_proj_bwd": ([_P, _I, _P, _P, _P, _P, _P, _P] + [_I] * 5 + [_P, _I64, _P], _I),
 }
 
 GRID_COORDS = 0

@@ -372,3 +372,75 @@ def test_grid_sample_mirror_errors():
         gs.point_sample(inputs, torch.zeros(1, 1, 2))
     with pytest.raises(TypeError, match="not supported"):
         gs.bilinear_grid_sample(inputs.double(), grid)
+
+
+# --------------------------------------------------------------------------------------------
+# value projection (msda_value_proj_fwd / msda_value_proj_bwd)
+
+
+def _vp_fwd(**kw):
+    args = dict(x=1 << 20, dt=0, w=1 << 20, b=1 << 20, m=0, v=1 << 20, batch=2, s=16, k=32, h=2, d=16)
+    args.update(kw)
+    lib = _native.lib()
+    rc = lib.msda_value_proj_fwd(ctypes.c_void_p(args["x"]), args["dt"], ctypes.c_void_p(args["w"]), ctypes.c_void_p(args["b"]),
+                                 ctypes.c_void_p(args["m"]), ctypes.c_void_p(args["v"]), args["batch"], args["s"], args["k"],
+                                 args["h"], args["d"], None)
+    return rc, lib.msda_last_error().decode()
+
+
+def _vp_bwd(**kw):
+    args = dict(x=1 << 20, dt=0, w=1 << 20, m=0, gv=1 << 20, gx=1 << 20, gw=1 << 20, gb=1 << 20, batch=2, s=16, k=32, h=2, d=16,
+                ws=1 << 20, ws_bytes=1 << 24)
+    args.update(kw)
+    lib = _native.lib()
+    rc = lib.msda_value_proj_bwd(ctypes.c_void_p(args["x"]), args["dt"], ctypes.c_void_p(args["w"]), ctypes.c_void_p(args["m"]),
+                                 ctypes.c_void_p(args["gv"]), ctypes.c_void_p(args["gx"]), ctypes.c_void_p(args["gw"]),
+                                 ctypes.c_void_p(args["gb"]), args["batch"], args["s"], args["k"], args["h"], args["d"],
+                                 ctypes.c_void_p(args["ws"]), args["ws_bytes"], None)
+    return rc, lib.msda_last_error().decode()
+
+
+@pytest.mark.parametrize("call", [_vp_fwd, _vp_bwd])
+@pytest.mark.parametrize(
+    "kw, code, message",
+    [
+        (dict(dt=9), _native.ERR_UNSUPPORTED, "dtype"),
+        (dict(batch=-1), _native.ERR_INVALID_ARGUMENT, "batch"),
+        (dict(k=0), _native.ERR_INVALID_ARGUMENT, "in_features"),
+        (dict(h=0), _native.ERR_INVALID_ARGUMENT, "n_heads"),
+        (dict(w=0), _native.ERR_INVALID_ARGUMENT, "NULL"),
+        (dict(w=(1 << 20) + 2), _native.ERR_INVALID_ARGUMENT, "aligned"),
+    ],
+)
+def test_value_proj_invalid_arguments_are_reported(call, kw, code, message):
+    rc, msg = call(**kw)
+    assert rc == code, msg
+    assert message in msg
+
+
+def test_value_proj_workspace():
+    lib = _native.lib()
+    size = lib.msda_value_proj_bwd_workspace_size(2, 16, 32, 2, 16)
+    assert size == 1 * 32 * 33 * 4  # one split of the 32 rows; [splits][N][K + 1] f32
+    assert lib.msda_value_proj_bwd_workspace_size(2, 16, 0, 2, 16) == _native.ERR_INVALID_ARGUMENT
+    rc, msg = _vp_bwd(ws=0)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "workspace" in msg
+    rc, msg = _vp_bwd(ws_bytes=16)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "workspace of" in msg
+    assert _vp_bwd(gw=0, gb=0, gx=0)[0] == _native.OK  # nothing requested
+    assert _vp_fwd(batch=0)[0] == _native.OK
+
+
+def test_ms_deform_attn_module_mirror_errors():
+    from rfdetr_jax_amd import MSDeformAttn
+    from rfdetr_jax_amd.value_proj import value_proj_rows
+
+    m = MSDeformAttn(d_model=32, n_levels=1, n_heads=4, n_points=2)
+    names = {n for n, _ in m.named_parameters()}
+    assert names == {f"{p}.{w}" for p in ("sampling_offsets", "attention_weights", "value_proj", "output_proj") for w in ("weight", "bias")}
+    with pytest.raises(ValueError, match="Last dim of reference_points must be 2 or 4"):
+        m(torch.zeros(1, 3, 32), torch.zeros(1, 3, 1, 3), torch.zeros(1, 16, 32), ((4, 4),))
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        value_proj_rows(torch.zeros(1, 4, 8), torch.zeros(8, 8), None, 2)
+    with pytest.raises(ValueError, match="divisible"):
+        MSDeformAttn(d_model=30, n_heads=4)
