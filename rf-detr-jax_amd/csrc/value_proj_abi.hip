@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <cstdlib>
 
 namespace {
 
@@ -40,8 +42,52 @@ int64_t vp_workspace(int batch, int len_in, int in_features, int n_heads, int he
   return static_cast<int64_t>(vp_splits(m)) * n_heads * head_dim * (in_features + 1) * 4;
 }
 
-int tiles(int64_t rows, int64_t cols) {
-  return static_cast<int>(((rows + msda::kGemmBM - 1) / msda::kGemmBM) * ((cols + msda::kGemmBN - 1) / msda::kGemmBN));
+// The 16-byte operand kernels need every 4-element vector they load contiguous and aligned: the
+// reduction and column extents K and D multiples of 4 (so N is too), and the tensors they read
+// aligned to 4 elements. MSDA_VP_SCALAR forces the element-wise kernels.
+bool vec_path(const msda::ValueProjParams& p, size_t eb, const void* a, const void* b) {
+  if (msda_host::env_flag("MSDA_VP_SCALAR")) return false;
+  return p.k % 4 == 0 && p.dim % 4 == 0 && aligned_to(p.w, 16) && (a == nullptr || aligned_to(a, 4 * eb)) &&
+         (b == nullptr || aligned_to(b, 4 * eb));
+}
+
+template <int KIND, typename VT, int BM>
+int launch_g4(const msda::ValueProjParams& p, int grid, hipStream_t st) {
+  static std::atomic<int> granted[msda_host::kMaxDevices];  // per instantiation
+  auto k = msda::gemm4_kernel<KIND, VT, BM>;
+  const int rc = msda_host::allow_lds(k, msda::G4<BM>::kLdsBytes, granted);
+  if (rc != MSDA_OK) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(msda::G4<BM>::kThreads), msda::G4<BM>::kLdsBytes, st, p);
+  return MSDA_OK;
+}
+
+// One product: rows x cols outputs (times `splits` slices of the reduction). The 16-byte kernels
+// take 32-row tiles when 64-row tiles would be fewer than four per CU (a CU with one tile more
+// than another finishes a whole tile later; smaller tiles even that out), else 64-row tiles;
+// MSDA_VP_BM=32 or 64 forces one.
+template <int KIND, typename VT>
+int launch_gemm(const msda::ValueProjParams& p, int64_t rows, int64_t cols, int splits, bool vec, hipStream_t st, const char* what) {
+  int rc = MSDA_OK;
+  const int64_t ct = (cols + msda::kGemmBN - 1) / msda::kGemmBN;
+  if (vec) {
+    int lds = 0, cus = 0;
+    if ((rc = msda_host::device_attrs(&lds, &cus)) != MSDA_OK) return rc;
+    const int64_t t64 = (rows + 63) / 64 * ct * splits;
+    int bm = t64 < 4 * static_cast<int64_t>(cus) ? 32 : 64;
+    if (const char* e = std::getenv("MSDA_VP_BM")) bm = std::atoi(e) == 32 ? 32 : std::atoi(e) == 64 ? 64 : bm;
+    if (bm == 32) rc = launch_g4<KIND, VT, 32>(p, static_cast<int>((rows + 31) / 32 * ct * splits), st);
+    else rc = launch_g4<KIND, VT, 64>(p, static_cast<int>(t64), st);
+    if (rc != MSDA_OK) return rc;
+  } else {
+    hipLaunchKernelGGL((msda::gemm_kernel<KIND, VT>), dim3(static_cast<unsigned>((rows + 63) / 64 * ct * splits)), dim3(256), 0, st, p);
+  }
+  return msda_host::check_launch(what);
+}
+
+template <int KIND>
+int launch_gemm_dt(const msda::ValueProjParams& p, int64_t rows, int64_t cols, int splits, bool vec, hipStream_t st, const char* what) {
+  return p.bf16 ? launch_gemm<KIND, msda::bf16_t>(p, rows, cols, splits, vec, st, what)
+                : launch_gemm<KIND, float>(p, rows, cols, splits, vec, st, what);
 }
 
 }  // namespace
@@ -73,11 +119,8 @@ int msda_value_proj_fwd(const void* input, int dtype, const float* weight, const
   p.dim = head_dim;
   p.dim_magic = static_cast<uint32_t>(((uint64_t{1} << 32) + head_dim - 1) / head_dim);
   p.seq_magic = static_cast<uint32_t>(((uint64_t{1} << 32) + len_in - 1) / len_in);
-  const int g = tiles(static_cast<int64_t>(batch) * len_in, p.n);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (p.bf16) hipLaunchKernelGGL((msda::gemm_kernel<msda::kGemmForward, msda::bf16_t>), dim3(g), dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((msda::gemm_kernel<msda::kGemmForward, float>), dim3(g), dim3(256), 0, st, p);
-  return msda_host::check_launch("value projection forward");
+  return launch_gemm_dt<msda::kGemmForward>(p, static_cast<int64_t>(batch) * len_in, p.n, 1, vec_path(p, eb, input, nullptr),
+                                            static_cast<hipStream_t>(stream), "value projection forward");
 }
 
 int64_t msda_value_proj_bwd_workspace_size(int batch, int len_in, int in_features, int n_heads, int head_dim) {
@@ -133,16 +176,18 @@ int msda_value_proj_bwd(const void* input, int dtype, const float* weight, const
   p.seq_magic = len_in > 0 ? static_cast<uint32_t>(((uint64_t{1} << 32) + len_in - 1) / len_in) : 0u;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (grad_input != nullptr && m > 0) {
-    if (p.bf16) hipLaunchKernelGGL((msda::gemm_kernel<msda::kGemmGradInput, msda::bf16_t>), dim3(tiles(m, in_features)), dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((msda::gemm_kernel<msda::kGemmGradInput, float>), dim3(tiles(m, in_features)), dim3(256), 0, st, p);
-    if ((rc = msda_host::check_launch("value projection backward (input)")) != MSDA_OK) return rc;
+    const bool vec = vec_path(p, eb, grad_value, nullptr);
+    if ((rc = launch_gemm_dt<msda::kGemmGradInput>(p, m, in_features, 1, vec, st, "value projection backward (input)")) != MSDA_OK)
+      return rc;
   }
   if (want_w) {
-    // with no rows the partial sums are zero: the product still runs (every partial is written)
-    const int64_t g = static_cast<int64_t>(tiles(p.n, static_cast<int64_t>(in_features) + 1)) * p.splits;
-    if (p.bf16) hipLaunchKernelGGL((msda::gemm_kernel<msda::kGemmGradWeight, msda::bf16_t>), dim3(static_cast<unsigned>(g)), dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((msda::gemm_kernel<msda::kGemmGradWeight, float>), dim3(static_cast<unsigned>(g)), dim3(256), 0, st, p);
-    if ((rc = msda_host::check_launch("value projection backward (weight)")) != MSDA_OK) return rc;
+    // with no rows the partial sums are zero: the product still runs (every partial is written).
+    // The element-wise kernel forms the bias gradient as a column of ones (K + 1 columns); the
+    // 16-byte kernel sums dY^T rows instead (K columns).
+    const bool vec = vec_path(p, eb, grad_value, input);
+    if ((rc = launch_gemm_dt<msda::kGemmGradWeight>(p, p.n, static_cast<int64_t>(in_features) + (vec ? 0 : 1), p.splits, vec, st,
+                                                     "value projection backward (weight)")) != MSDA_OK)
+      return rc;
     const int64_t total = static_cast<int64_t>(p.n) * (in_features + 1);
     hipLaunchKernelGGL(msda::wg_reduce_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 4096))), dim3(256), 0, st,
                        p);

@@ -47,6 +47,8 @@ SHAPES = {
     "nano_memory": dict(b=2, s=576, k=256, h=16, d=16),   # 24x24 encoder memory, d_model 256
     "odd": dict(b=3, s=37, k=48, h=3, d=20),              # edge tiles in every dimension
     "base": dict(b=1, s=1700, k=256, h=8, d=32),          # 8 heads x 32 (larger variants)
+    "odd_steps": dict(b=1, s=130, k=160, h=4, d=12),      # odd reduction step counts; 64 % D != 0
+    "elementwise": dict(b=2, s=45, k=30, h=2, d=5),       # K, D not multiples of 4: element-wise kernels
 }
 
 
@@ -164,3 +166,33 @@ def test_msdeform_attn_module_against_torch_module(ref_dim):
     assert_close(_np(out), want, 1e-5, "module output")
     for k, v in m.named_parameters():
         assert_close(_np(v.grad), want_grads[k], 1e-4, f"grad {k}")
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+def test_vector_and_elementwise_kernels_agree(monkeypatch, bf16):
+    """The 16-byte operand kernels with 32- and 64-row tiles (MSDA_VP_BM) and the element-wise ones
+    (MSDA_VP_SCALAR) on the same inputs, all against the oracle: they differ in tiling, staging and
+    in how the bias gradient is formed."""
+    rng = np.random.default_rng(34)
+    b, s, k, h, d = 2, 300, 128, 8, 16
+    x = rng.standard_normal((b, s, k)).astype(np.float32)
+    w = (rng.standard_normal((h * d, k)) / np.sqrt(k)).astype(np.float32)
+    bias = rng.standard_normal(h * d).astype(np.float32)
+    mask = rng.uniform(0, 1, (b, s)) < 0.3
+    g = rng.standard_normal((b * h, s, d)).astype(np.float32)
+    if bf16:
+        x, g = bf16_round(x), bf16_round(g)
+    dt = torch.bfloat16 if bf16 else None
+    wq = bf16_round(w) if bf16 else w
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    want = [VP.value_proj_rows(x, wq, bias, h, mask), *VP.value_proj_rows_vjp(x, wq, h, g, mask)]
+    for mode in ("bm32", "bm64", "scalar"):
+        if mode == "scalar":
+            monkeypatch.setenv("MSDA_VP_SCALAR", "1")
+        else:
+            monkeypatch.setenv("MSDA_VP_BM", mode[2:])
+        out = value_proj_forward(_t(x, dt), _t(w), _t(bias), h, _t(mask))
+        got = [out, *value_proj_backward(_t(x, dt), _t(w), h, _t(g, dt), _t(mask))]
+        torch.cuda.synchronize()
+        for name, a, ref, tol in zip(("value", "grad_input", "grad_weight", "grad_bias"), got, want, (tf, tg, tg, tg)):
+            assert_close(_np(a), ref, tol, f"{name} {mode}")
