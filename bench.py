@@ -364,6 +364,62 @@ def measure_value_proj(dev, steps, batch=8, seq=576, d_model=256, heads=16):
     }
 
 
+def measure_attention(dev, steps, batch=8, groups=13, per=300, heads=8, head_dim=32):
+    """The decoder's grouped self-attention at the config-2 shape (8 images x 13 groups x 300
+    queries, 8 heads x 32, f32): the attention alone (msda_attention_fwd, then _bwd for q, k and v)
+    on the [B, G * P, C] rows in place, beside torch's F.scaled_dot_product_attention on the same
+    tensors split into groups and heads (the reference's _split_groups + head transposes) with its
+    autograd backward. Algorithmic FLOPs: forward 4 L^2 D per (slice, head) (two products), backward
+    twice that (dV, dP, dQ, dK; the kernels' recomputation of the scores is not counted)."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from rfdetr_jax_amd.attention import _Layout, attention_backward, attention_forward
+
+    c = heads * head_dim
+    rng = np.random.default_rng(10)
+    qk = torch.from_numpy(rng.standard_normal((batch, groups * per, 2 * c), dtype=np.float32)).to(dev)
+    v = torch.from_numpy(rng.standard_normal((batch, groups * per, c), dtype=np.float32)).to(dev)
+    g = torch.from_numpy(rng.standard_normal((batch, groups * per, c), dtype=np.float32)).to(dev)
+    q, k = qk[..., :c], qk[..., c:]
+    lay = _Layout(batch, groups, heads, per, head_dim)
+    out, stats = attention_forward(q, k, v, lay, lay.strides_rows)
+
+    def fwd(_h):
+        attention_forward(q, k, v, lay, lay.strides_rows)
+
+    def ours(_h):
+        o, st = attention_forward(q, k, v, lay, lay.strides_rows)
+        attention_backward(q, k, v, o, st, g, lay, lay.strides_rows)
+
+    def split(x):  # [B, G P, C] -> [G B, H, P, D]
+        return x.reshape(batch, groups, per, heads, head_dim).permute(1, 0, 3, 2, 4).reshape(groups * batch, heads, per, head_dim)
+
+    tq, tk, tv = (split(x).detach().clone().requires_grad_(True) for x in (q, k, v))
+    tg = split(g).contiguous()
+
+    def torch_step(_h):
+        o = F.scaled_dot_product_attention(tq, tk, tv)
+        torch.autograd.grad(o, (tq, tk, tv), tg)
+
+    for _ in range(3):
+        ours(None)
+        torch_step(None)
+    torch.cuda.synchronize()
+    flops_fwd = 4 * per * per * head_dim * batch * groups * heads
+    fwd_us = time_graph(fwd, steps)[0]
+    step_us = time_graph(ours, steps)[0]
+    return {
+        "shape": {"batch": batch, "groups": groups, "queries_per_group": per, "heads": heads, "head_dim": head_dim, "dtype": "f32"},
+        "fwd_us": round(fwd_us, 3),
+        "step_us": round(step_us, 3),
+        "fwd_tflops": round(flops_fwd / fwd_us / 1e6, 1),
+        "step_tflops": round(3 * flops_fwd / step_us / 1e6, 1),
+        "torch_step_us_eager": round(time_eager(torch_step, steps), 3),
+    }
+
+
 def cpu_baseline(calls, budget_s=3.0, max_reps=20):
     """fwd+bwd of the C oracle on the same inputs; median us/call."""
     from oracle import cref
@@ -436,6 +492,8 @@ def main():
                     help="for rocprofv3 runs: K eager steps of the segmentation loss's point sampling, ours then torch's")
     ap.add_argument("--profile-value-proj", action="store_true",
                     help="for rocprofv3 runs: K eager steps of the value projection fwd+bwd, ours then torch's")
+    ap.add_argument("--profile-attention", action="store_true",
+                    help="for rocprofv3 runs: K steps of the decoder self-attention fwd+bwd, ours then torch's")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): the deformable-attention op needs no "
@@ -459,6 +517,9 @@ def main():
         return
     if args.profile_value_proj:
         print(json.dumps(measure_value_proj(dev, args.steps)), flush=True)
+        return
+    if args.profile_attention:
+        print(json.dumps(measure_attention(dev, args.steps)), flush=True)
         return
     log(f"workload {w.name}: warmup {args.warmup}, steps {args.steps}")
     res, calls = measure(w, dev, args.steps, args.warmup)
@@ -496,6 +557,8 @@ def main():
             per_config[f"fused_prologue_{w.name}"] = measure_fused(w, dev, max(50, args.steps // 2), 10)
         log("value projection")
         per_config["value_proj_b8_s576_c256_h16"] = measure_value_proj(dev, max(50, args.steps // 2))
+        log("decoder self-attention")
+        per_config["self_attention_b8_g13_p300_h8_d32_f32"] = measure_attention(dev, max(20, args.steps // 8))
         log("point sample (segmentation loss)")
         per_config["point_sample_mask_loss_400x112x112"] = measure_point_sample(dev, max(50, args.steps // 2))
 

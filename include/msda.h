@@ -250,6 +250,46 @@ int msda_value_proj_bwd(const void* input, int dtype, const float* weight, const
                         int batch, int len_in, int in_features, int n_heads, int head_dim,
                         void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- Decoder self-attention -----------------------------------------------------------------
+ * scaled_dot_product_attention (src/rfdetr_jax/models/layers.py:54-99, the XLA path) as used by
+ * MultiheadAttention (layers.py:491-548) in the decoder's grouped self-attention
+ * (src/rfdetr_jax/models/transformer.py:200-210): per slice z and head h,
+ *   out = softmax(q k^T / sqrt(D), blocked positions -> finfo(float32).min) v
+ * over len queries and len keys of head_dim = D channels (32 or 64). The slices are
+ * z = g * batch + b for b < batch, g < groups, the order of _split_groups (transformer.py:350-354):
+ * with groups > 1 the caller passes the unsplit [batch, groups * len, C] rows and the kernels read
+ * group g of image b in place. Every tensor is addressed as
+ *   base + b * s_b + g * s_g + h * s_h + row * s_row + channel
+ * with the four element strides given per tensor in `strides` (in that order; each a multiple of 4,
+ * base pointers aligned to 4 elements). Examples: [Z, H, L, D] contiguous (the reference
+ * function's layout): (H L D, 0, L D, D) with groups = 1; the decoder's [B, G P, C] rows with
+ * C = H D: (G P C, P C, D, C).
+ *
+ * mask: [len, len] bytes (non-zero blocks a key for a query: torch's boolean convention,
+ * layers.py:69, :93-94) or NULL. dtype: MSDA_DTYPE_F32 or MSDA_DTYPE_BF16 for every tensor;
+ * arithmetic is f32 (v_mfma_f32_32x32x2_f32), softmax in f32.
+ * stats: [batch * groups * heads * len][4] f32, 16-byte aligned, z-major (z = g * batch + b), then
+ * head, then query: the forward writes entries 0 and 1 (the row maximum and log2 of the softmax
+ * denominator, in units of log2(e) q.k / sqrt(D)); the backward reads them and uses entry 2 for
+ * rowsum(grad_out * out).
+ * Dropout on the attention weights (layers.py:537-544, active only with dropout > 0 in training)
+ * is not part of this function. len is at most 65536.
+ */
+int msda_attention_fwd(const void* q, const void* k, const void* v, int dtype, void* out, float* stats,
+                       int batch, int groups, int heads, int len, int head_dim,
+                       const int64_t* strides /* [4 tensors: q, k, v, out][4] */, const uint8_t* mask, void* stream);
+
+/*
+ * Backward of msda_attention_fwd for the cotangent grad_out: grad_q, grad_k, grad_v (each may be
+ * NULL to skip it; same layouts and dtype rules). out and stats are the forward's (stats entry 2
+ * is overwritten).
+ * strides: [8 tensors: q, k, v, out, grad_out, grad_q, grad_k, grad_v][4].
+ */
+int msda_attention_bwd(const void* q, const void* k, const void* v, const void* out, float* stats,
+                       const void* grad_out, int dtype, void* grad_q, void* grad_k, void* grad_v,
+                       int batch, int groups, int heads, int len, int head_dim,
+                       const int64_t* strides, const uint8_t* mask, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

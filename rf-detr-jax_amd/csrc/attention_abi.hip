@@ -1,0 +1,155 @@
+// attention_abi.hip — C ABI of the decoder self-attention kernels (include/msda.h): validation,
+// launch planning, kernel launches. Validation runs before any HIP call.
+#include "msda.h"
+#include "msda_launch.h"
+#include "attention_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+
+namespace {
+
+using msda_host::aligned_to;
+using msda_host::fail;
+
+int lds_bytes(int d) { return (d == 32 ? msda::at_lds_floats<32>() : msda::at_lds_floats<64>()) * 4; }
+
+int at_validate(int dtype, int batch, int groups, int heads, int len, int head_dim, const int64_t* strides, int ntensors) {
+  if (dtype != MSDA_DTYPE_F32 && dtype != MSDA_DTYPE_BF16) return fail(MSDA_ERR_UNSUPPORTED, "attention: unsupported dtype code %d", dtype);
+  if (batch < 0 || groups < 0 || heads < 0 || len < 0) return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: negative extent");
+  if (head_dim != 32 && head_dim != 64) return fail(MSDA_ERR_UNSUPPORTED, "attention: head_dim %d (32 or 64 supported)", head_dim);
+  if (static_cast<int64_t>(batch) * groups * heads >= (int64_t{1} << 31) || len > 65536)
+    return fail(MSDA_ERR_UNSUPPORTED, "attention: too many slices or rows");
+  if (strides == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: NULL strides");
+  for (int i = 0; i < 4 * ntensors; ++i)
+    if (strides[i] < 0 || strides[i] % 4 != 0)
+      return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: stride %d (%lld) must be a non-negative multiple of 4", i,
+                  static_cast<long long>(strides[i]));
+  return MSDA_OK;
+}
+
+msda::AttnParams at_params(int dtype, int batch, int groups, int heads, int len, int head_dim, const int64_t* strides, int ntensors,
+                           const int* order) {
+  msda::AttnParams p{};
+  p.batch = batch;
+  p.groups = groups;
+  p.heads = heads;
+  p.len = len;
+  p.scale = 1.0f / std::sqrt(static_cast<float>(head_dim));
+  p.scale2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
+  for (int t = 0; t < ntensors; ++t)
+    for (int j = 0; j < 4; ++j) p.st[order[t]][j] = strides[4 * t + j];
+  (void)dtype;
+  return p;
+}
+
+template <typename K>
+int at_launch(K kernel, std::atomic<int> (&granted)[msda_host::kMaxDevices], const msda::AttnParams& p, int lds, hipStream_t st,
+              const char* what) {
+  const int rc = msda_host::allow_lds(kernel, lds, granted);
+  if (rc != MSDA_OK) return rc;
+  // (slice, head) pairs x chunks of 4 row blocks of 32 (one per wave)
+  const int64_t chunks = ((p.len + 31) / 32 + msda::kAtRowBlocks - 1) / msda::kAtRowBlocks;
+  const int64_t grid = static_cast<int64_t>(p.batch) * p.groups * p.heads * chunks;
+  if (grid >= (int64_t{1} << 31)) return fail(MSDA_ERR_UNSUPPORTED, "attention: too many workgroups");
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(msda::kAtThreads), lds, st, p);
+  return msda_host::check_launch(what);
+}
+
+// The mask is a template parameter: without one the kernels carry no per-score mask code (and
+// need fewer registers).
+template <typename VT, int D, bool MASK>
+int fwd_typed(const msda::AttnParams& p, hipStream_t st) {
+  static std::atomic<int> granted[msda_host::kMaxDevices];
+  return at_launch(msda::attn_fwd_kernel<VT, D, MASK>, granted, p, lds_bytes(D), st, "attention forward");
+}
+
+template <typename VT, int D, bool MASK>
+int bwd_typed(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
+  int rc = MSDA_OK;
+  {  // grad_q, and rowsum(dO * O) into the statistics for the key side (alone when grad_q is NULL)
+    static std::atomic<int> granted[msda_host::kMaxDevices];
+    if ((rc = at_launch(msda::attn_bwd_q_kernel<VT, D, MASK>, granted, p, lds_bytes(D), st, "attention backward (queries)")) != MSDA_OK)
+      return rc;
+  }
+  if (want_kv) {
+    static std::atomic<int> granted[msda_host::kMaxDevices];
+    rc = at_launch(msda::attn_bwd_kv_kernel<VT, D, MASK>, granted, p, lds_bytes(D), st, "attention backward (keys, values)");
+  }
+  return rc;
+}
+
+template <typename VT>
+int fwd_dispatch(const msda::AttnParams& p, int d, hipStream_t st) {
+  const bool m = p.mask != nullptr;
+  if (d == 32) return m ? fwd_typed<VT, 32, true>(p, st) : fwd_typed<VT, 32, false>(p, st);
+  return m ? fwd_typed<VT, 64, true>(p, st) : fwd_typed<VT, 64, false>(p, st);
+}
+
+template <typename VT>
+int bwd_dispatch(const msda::AttnParams& p, int d, bool want_kv, hipStream_t st) {
+  const bool m = p.mask != nullptr;
+  if (d == 32) return m ? bwd_typed<VT, 32, true>(p, want_kv, st) : bwd_typed<VT, 32, false>(p, want_kv, st);
+  return m ? bwd_typed<VT, 64, true>(p, want_kv, st) : bwd_typed<VT, 64, false>(p, want_kv, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int msda_attention_fwd(const void* q, const void* k, const void* v, int dtype, void* out, float* stats, int batch, int groups, int heads,
+                       int len, int head_dim, const int64_t* strides, const uint8_t* mask, void* stream) {
+  msda_host::clear_error();
+  int rc = at_validate(dtype, batch, groups, heads, len, head_dim, strides, 4);
+  if (rc != MSDA_OK) return rc;
+  if (batch == 0 || groups == 0 || heads == 0 || len == 0) return MSDA_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || stats == nullptr)
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_attention_fwd: NULL tensor pointer");
+  const size_t a = dtype == MSDA_DTYPE_BF16 ? 8 : 16;
+  if (!aligned_to(q, a) || !aligned_to(k, a) || !aligned_to(v, a) || !aligned_to(out, a / 4) || !aligned_to(stats, 16))
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: q, k, v must be aligned to 4 elements");
+  static const int order[4] = {msda::kAtQ, msda::kAtK, msda::kAtV, msda::kAtO};
+  msda::AttnParams p = at_params(dtype, batch, groups, heads, len, head_dim, strides, 4, order);
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.out = out;
+  p.stats = stats;
+  p.mask = mask;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dtype == MSDA_DTYPE_BF16 ? fwd_dispatch<msda::bf16_t>(p, head_dim, st) : fwd_dispatch<float>(p, head_dim, st);
+}
+
+int msda_attention_bwd(const void* q, const void* k, const void* v, const void* out, float* stats, const void* grad_out, int dtype,
+                       void* grad_q, void* grad_k, void* grad_v, int batch, int groups, int heads, int len, int head_dim,
+                       const int64_t* strides, const uint8_t* mask, void* stream) {
+  msda_host::clear_error();
+  int rc = at_validate(dtype, batch, groups, heads, len, head_dim, strides, 8);
+  if (rc != MSDA_OK) return rc;
+  const bool want_q = grad_q != nullptr, want_kv = grad_k != nullptr || grad_v != nullptr;
+  if (batch == 0 || groups == 0 || heads == 0 || len == 0 || (!want_q && !want_kv)) return MSDA_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || stats == nullptr || grad_out == nullptr)
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_attention_bwd: NULL tensor pointer");
+  const size_t a = dtype == MSDA_DTYPE_BF16 ? 8 : 16;
+  if (!aligned_to(q, a) || !aligned_to(k, a) || !aligned_to(v, a) || !aligned_to(out, a) || !aligned_to(grad_out, a) ||
+      !aligned_to(grad_q, a / 4) || !aligned_to(grad_k, a / 4) || !aligned_to(grad_v, a / 4) || !aligned_to(stats, 16))
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: q, k, v, out, grad_out must be aligned to 4 elements");
+  static const int order[8] = {msda::kAtQ, msda::kAtK, msda::kAtV, msda::kAtO, msda::kAtGO, msda::kAtGQ, msda::kAtGK, msda::kAtGV};
+  msda::AttnParams p = at_params(dtype, batch, groups, heads, len, head_dim, strides, 8, order);
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = out;
+  p.go = grad_out;
+  p.gq = grad_q;
+  p.gk = grad_k;
+  p.gv = grad_v;
+  p.stats = stats;
+  p.mask = mask;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dtype == MSDA_DTYPE_BF16 ? bwd_dispatch<msda::bf16_t>(p, head_dim, want_kv, st) : bwd_dispatch<float>(p, head_dim, want_kv, st);
+}
+
+}  // extern "C"

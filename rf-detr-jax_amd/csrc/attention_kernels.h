@@ -1,0 +1,495 @@
+// attention_kernels.h — gfx950 device code for the decoder's softmax self-attention
+// (scaled_dot_product_attention, src/rfdetr_jax/models/layers.py:54-99, inside MultiheadAttention,
+// :491-548, with query groups folded onto the batch, src/rfdetr_jax/models/transformer.py:200-210).
+//
+// A slice z (= g * batch + b, the order of _split_groups, transformer.py:350-354) and head h is one
+// workgroup: its L keys and values (or queries and output gradients) are staged in LDS as f32 rows
+// of D + 8 floats, and each wave owns blocks of 32 queries (or keys). Tensors are read and written
+// in place through element strides (batch, group, head, row; channels contiguous), so the
+// decoder's [B, G * P, C] activations need no split, merge or head transposes.
+//
+// Products run on v_mfma_f32_32x32x2_f32 (lane l supplies A[l % 32][l / 32] and B[l / 32][l % 32];
+// its 16 results are D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32]). Scores are formed transposed
+// (keys x queries) so that a lane owns one query: its softmax statistics stay in the lane, and the
+// probabilities in its result registers are already the B operand of the next product (the same
+// reduction slot assignment is used for both operands).
+//
+// Softmax: scores are scaled by log2(e) / sqrt(D) and exponentiated with exp2 (one rounding
+// different from exp of q.k / sqrt(D)); the forward is one pass over the key blocks with a running
+// maximum (rescaling the partial sums), and stores per query the final maximum m and log2 of the
+// denominator l for the backward, which recomputes the probabilities as exp2((x - m) - log2 l).
+// Blocked positions take the score finfo(float32).min as in the reference (:93-96); keys past L
+// take -inf (weight 0).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace msda {
+
+typedef float at_f4 __attribute__((ext_vector_type(4)));
+typedef float at_f16 __attribute__((ext_vector_type(16)));
+
+enum AttnTensor { kAtQ = 0, kAtK, kAtV, kAtO, kAtGO, kAtGQ, kAtGK, kAtGV, kAtTensors };
+
+struct AttnParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;        // backward: the forward output
+  const void* go;       // backward: grad of the output
+  void* out;            // forward output
+  void* gq;             // backward outputs (each may be null)
+  void* gk;
+  void* gv;
+  float* stats;         // [Z * H * L][4]: m, log2 l (forward), rowsum(dO * O) (backward), unused
+  const uint8_t* mask;  // [L, L], non-zero blocks a position, or null
+  int64_t st[kAtTensors][4];  // element strides (batch, group, head, row) of each tensor
+  int batch, groups, heads, len;
+  float scale;   // 1 / sqrt(D)
+  float scale2;  // log2(e) / sqrt(D)
+};
+
+constexpr float kAtMaskScore = -3.4028234663852886e38f;  // finfo(float32).min
+
+template <typename VT>
+__device__ __forceinline__ at_f4 at_ld4(const VT* p, int64_t i) {  // elements i .. i + 3 as f32
+  if constexpr (sizeof(VT) == 2) {
+    const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p) + i);
+    return at_f4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                 __uint_as_float(u.y & 0xffff0000u)};
+  } else {
+    return *reinterpret_cast<const at_f4*>(p + i);
+  }
+}
+
+template <typename VT>
+__device__ __forceinline__ void at_st1(VT* p, int64_t i, float v) {
+  if constexpr (sizeof(VT) == 2) {
+    uint32_t u = __float_as_uint(v);  // nearest even, quiet NaN
+    if ((u & 0x7fffffffu) > 0x7f800000u) u = (u | 0x00400000u) & 0xffff0000u;
+    else u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+    reinterpret_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(u >> 16);
+  } else {
+    p[i] = v;
+  }
+}
+
+// 2^x by v_exp_f32 alone: results below 2^-126 flush to zero (a weight that small is below the
+// f32 resolution of any row sum it enters), 2^-inf = 0.
+__device__ __forceinline__ float at_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ at_f16 at_zero16() {
+  at_f16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+// A (slice, head) pair zh = z * H + h, and a tensor's base offset there.
+struct AttnSlice {
+  int z, h, b, g;
+  __device__ AttnSlice(const AttnParams& p, int zh) {
+    z = zh / p.heads;
+    h = zh - z * p.heads;
+    g = z / p.batch;
+    b = z - g * p.batch;
+  }
+  __device__ int64_t base(const AttnParams& p, int t) const {
+    return b * p.st[t][0] + g * p.st[t][1] + h * p.st[t][2];
+  }
+};
+
+// Work split: a workgroup is (slice, head, 4 blocks of 32 rows on its own side: queries for the
+// forward and dQ, keys for dK / dV), one block per wave; the other side streams through LDS in
+// chunks of 64 rows (two blocks), staged from registers loaded one chunk ahead. A workgroup needs
+// 2 x 64 rows of D + 8 floats (20 KB at D = 32), so several share a CU and their waves fill each
+// other's barrier and staging gaps.
+constexpr int kAtThreads = 256;
+constexpr int kAtRowBlocks = kAtThreads / 64;  // row blocks (waves) per workgroup
+constexpr int kAtChunk = 64;                   // streamed rows per LDS chunk
+
+template <int D>
+constexpr int at_lds_floats() { return 2 * kAtChunk * (D + 8) + 3 * kAtChunk; }  // two row tiles, three per-row floats
+
+// One tensor's slice of a 64-row chunk in registers: the thread's 4-element vectors, clamped to
+// row L - 1 (zeroed when stored).
+template <typename VT, int D>
+struct AtChunk {
+  static constexpr int C4 = D / 4, NV = kAtChunk * C4 / kAtThreads;
+  at_f4 v[NV];
+  __device__ void load(const VT* src, int64_t rs, int r0, int L) {
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int idx = threadIdx.x + kAtThreads * u, row = idx / C4, c4 = idx - row * C4;
+      v[u] = at_ld4<VT>(src, min(r0 + row, L - 1) * rs + 4 * c4);
+    }
+  }
+  __device__ void store(float* dst, int r0, int L) const {
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int idx = threadIdx.x + kAtThreads * u, row = idx / C4, c4 = idx - row * C4;
+      const bool ok = r0 + row < L;
+      *reinterpret_cast<at_f4*>(&dst[row * (D + 8) + 4 * c4]) =
+          ok ? v[u] : at_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+};
+
+// Transposed scores of two 32-row blocks of X (LDS rows b * 32 .., row stride D + 8) against the
+// lane's column (registers xr[c] = channels 8 c + 4 (l / 32) .. + 3): two independent MFMA chains.
+template <int D>
+__device__ __forceinline__ void at_scores2(at_f16& s0, at_f16& s1, const float* Xs, const at_f4 (&xr)[D / 8], int col, int grp) {
+  constexpr int LD = D + 8;
+  s0 = at_zero16();
+  s1 = at_zero16();
+#pragma unroll
+  for (int c = 0; c < D / 8; ++c) {
+    const at_f4 a0 = *reinterpret_cast<const at_f4*>(&Xs[col * LD + 8 * c + 4 * grp]);
+    const at_f4 a1 = *reinterpret_cast<const at_f4*>(&Xs[(32 + col) * LD + 8 * c + 4 * grp]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], xr[c][j], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], xr[c][j], s1, 0, 0, 0);
+    }
+  }
+}
+
+// Scores of one 32-row block of X against two register operands (two chains): s0 with xr, s1 with yr.
+template <int D>
+__device__ __forceinline__ void at_scores_pair(at_f16& s0, at_f16& s1, const float* Xs, const float* Ys, const at_f4 (&xr)[D / 8],
+                                               const at_f4 (&yr)[D / 8], int col, int grp) {
+  constexpr int LD = D + 8;
+  s0 = at_zero16();
+  s1 = at_zero16();
+#pragma unroll
+  for (int c = 0; c < D / 8; ++c) {
+    const at_f4 a0 = *reinterpret_cast<const at_f4*>(&Xs[col * LD + 8 * c + 4 * grp]);
+    const at_f4 a1 = *reinterpret_cast<const at_f4*>(&Ys[col * LD + 8 * c + 4 * grp]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], xr[c][j], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], yr[c][j], s1, 0, 0, 0);
+    }
+  }
+}
+
+// acc0 += X0^T w0 and acc1 += X1^T w1 (two chains): X rows from LDS (32-row blocks at X0s, X1s,
+// row stride D + 8) one channel per lane, w in result-layout registers (register i is row
+// 8 (i / 4) + 4 (l / 32) + i % 4 of the block); acc holds channels 32 nd + .. of the lane's column.
+template <int D>
+__device__ __forceinline__ void at_accum2(at_f16 (&acc0)[D / 32], at_f16 (&acc1)[D / 32], const float* X0s, const float* X1s,
+                                          const at_f16& w0, const at_f16& w1, int col, int grp) {
+  constexpr int LD = D + 8;
+#pragma unroll
+  for (int nd = 0; nd < D / 32; ++nd)
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = (8 * c4 + 4 * grp + j) * LD + 32 * nd + col;
+        acc0[nd] = __builtin_amdgcn_mfma_f32_32x32x2f32(X0s[r], w0[4 * c4 + j], acc0[nd], 0, 0, 0);
+        acc1[nd] = __builtin_amdgcn_mfma_f32_32x32x2f32(X1s[r], w1[4 * c4 + j], acc1[nd], 0, 0, 0);
+      }
+}
+
+// Scale two transposed score blocks (keys k0 + 32 h + 8 (i / 4) + 4 grp + i % 4 of register i, the
+// lane's query qi) by scale2, give keys past L the score -inf and blocked keys finfo.min (the mask
+// row of qi; qi < 0: no row), and take their maximum into bm. The mask test is hoisted out of the
+// per-score code, and full chunks skip the key-range test.
+template <bool MASK>
+__device__ __forceinline__ void at_scale_scores(at_f16& s0, at_f16& s1, int k0, int L, float scale2, const uint8_t* mask, int qi, int grp,
+                                                float& bm) {
+  const bool full = k0 + kAtChunk <= L;
+  if (!MASK && full) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s0[i] *= scale2;
+      s1[i] *= scale2;
+      bm = fmaxf(bm, fmaxf(s0[i], s1[i]));
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int key0 = k0 + 8 * (i >> 2) + 4 * grp + (i & 3), key1 = key0 + 32;
+    float x0 = s0[i] * scale2, x1 = s1[i] * scale2;
+    if (MASK && qi >= 0) {
+      const uint8_t* mr = mask + static_cast<int64_t>(qi) * L;
+      if (key0 < L && mr[key0] != 0) x0 = kAtMaskScore;
+      if (key1 < L && mr[key1] != 0) x1 = kAtMaskScore;
+    }
+    s0[i] = key0 < L ? x0 : -INFINITY;
+    s1[i] = key1 < L ? x1 : -INFINITY;
+    bm = fmaxf(bm, fmaxf(s0[i], s1[i]));
+  }
+}
+
+// The workgroup's (slice, head) and row chunk: blockIdx.x = (z * H + h) * chunks + rc.
+struct AttnWork {
+  int zh, rc;
+  AttnSlice sl;
+  __device__ AttnWork(const AttnParams& p, int chunks) : zh(static_cast<int>(blockIdx.x) / chunks),
+      rc(static_cast<int>(blockIdx.x) - zh * chunks), sl(p, zh) {}
+};
+
+// Forward: out = softmax(q k^T / sqrt(D), blocked -> finfo.min) v. Each wave owns 32 queries; K and
+// V stream through LDS; the running maximum rescales the partial sums.
+template <typename VT, int D, bool MASK>
+__global__ void __launch_bounds__(kAtThreads, D == 32 ? 3 : 2) attn_fwd_kernel(const AttnParams p) {
+  constexpr int LD = D + 8, ND = D / 32;
+  extern __shared__ __align__(16) float at_lds[];
+  float* Ks = at_lds;
+  float* Vs = at_lds + kAtChunk * LD;
+  const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
+  const AttnWork w(p, (nb + kAtRowBlocks - 1) / kAtRowBlocks);
+  const VT* kp = static_cast<const VT*>(p.k) + w.sl.base(p, kAtK);
+  const VT* vp = static_cast<const VT*>(p.v) + w.sl.base(p, kAtV);
+  const int lane = threadIdx.x & 63, grp = lane >> 5, col = lane & 31;
+  const int qb = w.rc * kAtRowBlocks + (threadIdx.x >> 6), qi = qb * 32 + col;
+  const bool qv = qi < L;
+  at_f4 qr[D / 8];
+  {
+    const VT* qp = static_cast<const VT*>(p.q) + w.sl.base(p, kAtQ);
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) qr[c] = at_ld4<VT>(qp, min(qi, L - 1) * p.st[kAtQ][3] + 8 * c + 4 * grp);
+  }
+  float m = -INFINITY, l = 0.0f;
+  at_f16 o0[ND], o1[ND];
+#pragma unroll
+  for (int nd = 0; nd < ND; ++nd) o0[nd] = o1[nd] = at_zero16();
+  AtChunk<VT, D> kc, vc;
+  kc.load(kp, p.st[kAtK][3], 0, L);
+  vc.load(vp, p.st[kAtV][3], 0, L);
+  for (int j = 0; j < nchunks; ++j) {
+    __syncthreads();  // every wave is done with the previous chunk
+    kc.store(Ks, j * kAtChunk, L);
+    vc.store(Vs, j * kAtChunk, L);
+    __syncthreads();
+    if (j + 1 < nchunks) {  // in flight during this chunk's arithmetic
+      kc.load(kp, p.st[kAtK][3], (j + 1) * kAtChunk, L);
+      vc.load(vp, p.st[kAtV][3], (j + 1) * kAtChunk, L);
+    }
+    if (qb >= nb) continue;
+    at_f16 s0, s1;
+    at_scores2<D>(s0, s1, Ks, qr, col, grp);
+    float bm = -INFINITY;
+    at_scale_scores<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, qv ? qi : -1, grp, bm);
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);  // finite: every chunk holds a key below L
+    const float alpha = at_exp2(m - mn);
+    float rs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s0[i] = at_exp2(s0[i] - mn);
+      s1[i] = at_exp2(s1[i] - mn);
+      rs += s0[i] + s1[i];
+    }
+    rs += __shfl_xor(rs, 32, 64);
+    l = l * alpha + rs;
+    m = mn;
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd) {
+      o0[nd] *= alpha;
+      o1[nd] *= alpha;
+    }
+    at_accum2<D>(o0, o1, Vs, Vs + 32 * LD, s0, s1, col, grp);  // O^T += V^T P^T, one chain per key block
+  }
+  if (qv) {
+    VT* op = static_cast<VT*>(p.out) + w.sl.base(p, kAtO);
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        at_st1<VT>(op, qi * p.st[kAtO][3] + 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3), (o0[nd][i] + o1[nd][i]) * inv);
+    if (grp == 0) {
+      float* stats = p.stats + (static_cast<int64_t>(w.zh) * L + qi) * 4;
+      stats[0] = m;
+      stats[1] = log2f(l);
+    }
+  }
+}
+
+// Backward, query side: dQ = dS K / sqrt(D) with dS = P (dP - rowsum(dO * O)), dP = dO V^T and P
+// recomputed from the stored statistics. Each wave owns 32 queries; K and V stream through LDS.
+// Also stores rowsum(dO * O) of its queries in the statistics for the key-side kernel (with no
+// grad_q requested, that is all it does).
+template <typename VT, int D, bool MASK>
+__global__ void __launch_bounds__(kAtThreads, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_q_kernel(const AttnParams p) {
+  constexpr int LD = D + 8, ND = D / 32;
+  extern __shared__ __align__(16) float at_lds[];
+  float* Ks = at_lds;
+  float* Vs = at_lds + kAtChunk * LD;
+  const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
+  const AttnWork w(p, (nb + kAtRowBlocks - 1) / kAtRowBlocks);
+  const VT* kp = static_cast<const VT*>(p.k) + w.sl.base(p, kAtK);
+  const VT* vp = static_cast<const VT*>(p.v) + w.sl.base(p, kAtV);
+  const int lane = threadIdx.x & 63, grp = lane >> 5, col = lane & 31;
+  const int qb = w.rc * kAtRowBlocks + (threadIdx.x >> 6), qi = qb * 32 + col;
+  const bool qv = qi < L;
+  const int qc = min(qi, L - 1);
+  at_f4 qr[D / 8], gr[D / 8];
+  float dsum = 0.0f;  // rowsum(dO * O) over this lane's half of the channels, then both halves
+  {
+    const VT* qp = static_cast<const VT*>(p.q) + w.sl.base(p, kAtQ);
+    const VT* gop = static_cast<const VT*>(p.go) + w.sl.base(p, kAtGO);
+    const VT* opp = static_cast<const VT*>(p.o) + w.sl.base(p, kAtO);
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) {
+      qr[c] = at_ld4<VT>(qp, qc * p.st[kAtQ][3] + 8 * c + 4 * grp);
+      gr[c] = at_ld4<VT>(gop, qc * p.st[kAtGO][3] + 8 * c + 4 * grp);
+      const at_f4 ov = at_ld4<VT>(opp, qc * p.st[kAtO][3] + 8 * c + 4 * grp);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) dsum += gr[c][jj] * ov[jj];
+    }
+  }
+  dsum += __shfl_xor(dsum, 32, 64);
+  float* stats = p.stats + (static_cast<int64_t>(w.zh) * L + qc) * 4;
+  const float m = stats[0], ll = stats[1];
+  if (qv && grp == 0 && qb < nb) stats[2] = dsum;  // read by the key-side kernel, launched after this one
+  if (p.gq == nullptr) return;                      // only the row sums were asked for
+  at_f16 dq0[ND], dq1[ND];
+#pragma unroll
+  for (int nd = 0; nd < ND; ++nd) dq0[nd] = dq1[nd] = at_zero16();
+  AtChunk<VT, D> kc, vc;
+  kc.load(kp, p.st[kAtK][3], 0, L);
+  vc.load(vp, p.st[kAtV][3], 0, L);
+  for (int j = 0; j < nchunks; ++j) {
+    __syncthreads();
+    kc.store(Ks, j * kAtChunk, L);
+    vc.store(Vs, j * kAtChunk, L);
+    __syncthreads();
+    if (j + 1 < nchunks) {
+      kc.load(kp, p.st[kAtK][3], (j + 1) * kAtChunk, L);
+      vc.load(vp, p.st[kAtV][3], (j + 1) * kAtChunk, L);
+    }
+    if (qb >= nb) continue;
+    at_f16 s[2], dp[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)  // the chunk's two key blocks: S^T and dP^T = V dO^T, two chains each
+      at_scores_pair<D>(s[h2], dp[h2], Ks + 32 * h2 * LD, Vs + 32 * h2 * LD, qr, gr, col, grp);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = j * kAtChunk + 32 * h2 + 8 * (i >> 2) + 4 * grp + (i & 3);
+        float x = s[h2][i] * p.scale2;
+        if (key >= L) x = -INFINITY;
+        else if (MASK && qv && p.mask[static_cast<int64_t>(qi) * L + key] != 0) x = kAtMaskScore;
+        s[h2][i] = at_exp2((x - m) - ll) * (dp[h2][i] - dsum);  // dS^T
+      }
+    at_accum2<D>(dq0, dq1, Ks, Ks + 32 * LD, s[0], s[1], col, grp);  // dQ^T += K^T dS^T, one chain per key block
+  }
+  if (qv) {
+    VT* gqp = static_cast<VT*>(p.gq) + w.sl.base(p, kAtGQ);
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        at_st1<VT>(gqp, qi * p.st[kAtGQ][3] + 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3), (dq0[nd][i] + dq1[nd][i]) * p.scale);
+  }
+}
+
+// Backward, key side: dV = P^T dO and dK = dS^T Q / sqrt(D). Each wave owns 32 keys (K and V rows
+// in registers) and forms S and dP untransposed (queries x keys), so a lane owns one key; Q, dO and
+// the per-query statistics (with rowsum(dO * O), written by the query-side kernel) stream through
+// LDS.
+template <typename VT, int D, bool MASK>
+__global__ void __launch_bounds__(kAtThreads, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_kv_kernel(const AttnParams p) {
+  constexpr int LD = D + 8, ND = D / 32;
+  extern __shared__ __align__(16) float at_lds[];
+  float* Qs = at_lds;
+  float* Gs = Qs + kAtChunk * LD;
+  float* Ms = Gs + kAtChunk * LD;  // [64][2]: m, log2 l (rows past L: +inf, so their weight is 0)
+  float* Ds = Ms + 2 * kAtChunk;   // [64]: rowsum(dO * O)
+  const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
+  const AttnWork w(p, (nb + kAtRowBlocks - 1) / kAtRowBlocks);
+  const VT* qp = static_cast<const VT*>(p.q) + w.sl.base(p, kAtQ);
+  const VT* gop = static_cast<const VT*>(p.go) + w.sl.base(p, kAtGO);
+  const float* stats = p.stats + static_cast<int64_t>(w.zh) * L * 4;
+  const int t = threadIdx.x, lane = t & 63, grp = lane >> 5, col = lane & 31;
+  const int kb = w.rc * kAtRowBlocks + (t >> 6), key = kb * 32 + col;
+  const bool kv = key < L;
+  at_f4 kr[D / 8], vr[D / 8];
+  {
+    const VT* kp = static_cast<const VT*>(p.k) + w.sl.base(p, kAtK);
+    const VT* vp = static_cast<const VT*>(p.v) + w.sl.base(p, kAtV);
+    const int kcl = min(key, L - 1);
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) {
+      kr[c] = at_ld4<VT>(kp, kcl * p.st[kAtK][3] + 8 * c + 4 * grp);
+      vr[c] = at_ld4<VT>(vp, kcl * p.st[kAtV][3] + 8 * c + 4 * grp);
+    }
+  }
+  at_f16 dk[ND], dv[ND];
+#pragma unroll
+  for (int nd = 0; nd < ND; ++nd) dk[nd] = dv[nd] = at_zero16();
+  AtChunk<VT, D> qc, gc;
+  at_f4 sq = {0.0f, 0.0f, 0.0f, 0.0f};  // threads < 64: m, log2 l, rowsum(dO * O) of chunk row t
+  auto prefetch = [&](int r0) {
+    qc.load(qp, p.st[kAtQ][3], r0, L);
+    gc.load(gop, p.st[kAtGO][3], r0, L);
+    if (t < kAtChunk) sq = *reinterpret_cast<const at_f4*>(&stats[4 * min(r0 + t, L - 1)]);
+  };
+  prefetch(0);
+  // per query block of a chunk: S = Q K^T and dP = dO V^T (two chains), the probabilities and dS,
+  // then dV^T += dO^T P and dK^T += Q^T dS (two chains)
+  auto block = [&](int r0, int h2) {
+    at_f16 s, dp;
+    at_scores_pair<D>(s, dp, Qs + 32 * h2 * LD, Gs + 32 * h2 * LD, kr, vr, col, grp);
+    at_f16 pw;
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      const int ql = 32 * h2 + 8 * c4 + 4 * grp;  // chunk rows of registers 4 c4 .. 4 c4 + 3
+      const at_f4 ms0 = *reinterpret_cast<const at_f4*>(&Ms[2 * ql]), ms1 = *reinterpret_cast<const at_f4*>(&Ms[2 * ql + 4]);
+      const at_f4 dd = *reinterpret_cast<const at_f4*>(&Ds[ql]);
+      const float mq[4] = {ms0[0], ms0[2], ms1[0], ms1[2]}, lq[4] = {ms0[1], ms0[3], ms1[1], ms1[3]};
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int i = 4 * c4 + jj;
+        float x = s[i] * p.scale2;
+        if constexpr (MASK) {
+          const int q = r0 + ql + jj;
+          if (q < L && p.mask[static_cast<int64_t>(q) * L + key] != 0) x = kAtMaskScore;
+        }
+        // a lane past L holds the clamped last key: finite scores, dropped here
+        pw[i] = kv ? at_exp2((x - mq[jj]) - lq[jj]) : 0.0f;
+        s[i] = pw[i] * (dp[i] - dd[jj]);  // dS
+      }
+    }
+    at_accum2<D>(dv, dk, Gs + 32 * h2 * LD, Qs + 32 * h2 * LD, pw, s, col, grp);
+  };
+  for (int j = 0; j < nchunks; ++j) {
+    const int r0 = j * kAtChunk;
+    __syncthreads();
+    qc.store(Qs, r0, L);
+    gc.store(Gs, r0, L);
+    if (t < kAtChunk) {
+      const bool in = r0 + t < L;
+      Ms[2 * t] = in ? sq[0] : INFINITY;
+      Ms[2 * t + 1] = in ? sq[1] : 0.0f;
+      Ds[t] = in ? sq[2] : 0.0f;
+    }
+    __syncthreads();
+    if (j + 1 < nchunks) prefetch(r0 + kAtChunk);
+    if (kb >= nb) continue;
+    block(r0, 0);
+    block(r0, 1);
+  }
+  if (kv) {
+    VT* gkp = static_cast<VT*>(p.gk) + w.sl.base(p, kAtGK);
+    VT* gvp = static_cast<VT*>(p.gv) + w.sl.base(p, kAtGV);
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3);
+        if (p.gk != nullptr) at_st1<VT>(gkp, key * p.st[kAtGK][3] + d, dk[nd][i] * p.scale);
+        if (p.gv != nullptr) at_st1<VT>(gvp, key * p.st[kAtGV][3] + d, dv[nd][i]);
+      }
+  }
+}
+
+}  // namespace msda

@@ -41,6 +41,8 @@ SIGNATURES = {
     "msda_value_proj_fwd": ([_P, _I, _P, _P, _P, _P] + [_I] * 5 + [_P], _I),
     "msda_value_proj_bwd_workspace_size": ([_I] * 5, _I64),
     "msda_value_proj_bwd": ([_P, _I, _P, _P, _P, _P, _P, _P] + [_I] * 5 + [_P, _I64, _P], _I),
+    "msda_attention_fwd": ([_P, _P, _P, _I, _P, _P] + [_I] * 5 + [_P, _P, _P], _I),
+    "msda_attention_bwd": ([_P, _P, _P, _P, _P, _P, _I, _P, _P, _P] + [_I] * 5 + [_P, _P, _P], _I),
 }
 
 GRID_COORDS = 0

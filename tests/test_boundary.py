@@ -444,3 +444,75 @@ def test_ms_deform_attn_module_mirror_errors():
         value_proj_rows(torch.zeros(1, 4, 8), torch.zeros(8, 8), None, 2)
     with pytest.raises(ValueError, match="divisible"):
         MSDeformAttn(d_model=30, n_heads=4)
+
+
+# --------------------------------------------------------------------------------------------
+# decoder self-attention (msda_attention_fwd / msda_attention_bwd)
+
+
+def _at_fwd(**kw):
+    args = dict(q=1 << 20, k=1 << 20, v=1 << 20, dt=0, o=1 << 20, st=1 << 20, batch=2, groups=1, heads=2, len=9, d=32,
+                strides=[2 * 9 * 32, 0, 9 * 32, 32] * 4, m=0)
+    args.update(kw)
+    lib = _native.lib()
+    strides = (ctypes.c_int64 * len(args["strides"]))(*args["strides"])
+    rc = lib.msda_attention_fwd(ctypes.c_void_p(args["q"]), ctypes.c_void_p(args["k"]), ctypes.c_void_p(args["v"]), args["dt"],
+                                ctypes.c_void_p(args["o"]), ctypes.c_void_p(args["st"]), args["batch"], args["groups"], args["heads"],
+                                args["len"], args["d"], strides, ctypes.c_void_p(args["m"]), None)
+    return rc, lib.msda_last_error().decode()
+
+
+def _at_bwd(**kw):
+    args = dict(q=1 << 20, k=1 << 20, v=1 << 20, o=1 << 20, st=1 << 20, go=1 << 20, dt=0, gq=1 << 20, gk=1 << 20, gv=1 << 20,
+                batch=2, groups=1, heads=2, len=9, d=32, strides=[2 * 9 * 32, 0, 9 * 32, 32] * 8, m=0)
+    args.update(kw)
+    lib = _native.lib()
+    strides = (ctypes.c_int64 * len(args["strides"]))(*args["strides"])
+    rc = lib.msda_attention_bwd(ctypes.c_void_p(args["q"]), ctypes.c_void_p(args["k"]), ctypes.c_void_p(args["v"]),
+                                ctypes.c_void_p(args["o"]), ctypes.c_void_p(args["st"]), ctypes.c_void_p(args["go"]), args["dt"],
+                                ctypes.c_void_p(args["gq"]), ctypes.c_void_p(args["gk"]), ctypes.c_void_p(args["gv"]), args["batch"],
+                                args["groups"], args["heads"], args["len"], args["d"], strides, ctypes.c_void_p(args["m"]), None)
+    return rc, lib.msda_last_error().decode()
+
+
+@pytest.mark.parametrize("call", [_at_fwd, _at_bwd])
+@pytest.mark.parametrize(
+    "kw, code, message",
+    [
+        (dict(dt=9), _native.ERR_UNSUPPORTED, "dtype"),
+        (dict(d=48), _native.ERR_UNSUPPORTED, "head_dim"),
+        (dict(len=-1), _native.ERR_INVALID_ARGUMENT, "negative"),
+        (dict(strides=[2 * 9 * 32, 0, 9 * 32, 30] * 8), _native.ERR_INVALID_ARGUMENT, "multiple of 4"),
+        (dict(q=0), _native.ERR_INVALID_ARGUMENT, "NULL"),
+        (dict(k=(1 << 20) + 4), _native.ERR_INVALID_ARGUMENT, "aligned"),
+    ],
+)
+def test_attention_invalid_arguments_are_reported(call, kw, code, message):
+    rc, msg = call(**kw)
+    assert rc == code, msg
+    assert message in msg
+
+
+def test_attention_empty_calls_do_nothing():
+    assert _at_fwd(len=0)[0] == _native.OK
+    assert _at_fwd(batch=0)[0] == _native.OK
+    assert _at_bwd(gq=0, gk=0, gv=0)[0] == _native.OK  # nothing requested
+
+
+def test_attention_module_mirror_errors():
+    from rfdetr_jax_amd.attention import MultiheadAttention, grouped_attention, scaled_dot_product_attention
+
+    m = MultiheadAttention(64, 2)
+    assert {n for n, _ in m.named_parameters()} == {"in_proj_weight", "in_proj_bias", "out_proj.weight", "out_proj.bias"}
+    assert tuple(m.in_proj_weight.shape) == (192, 64)
+    with pytest.raises(ValueError, match="divisible"):
+        MultiheadAttention(30, 4)
+    with pytest.raises(ValueError, match="one shape"):
+        scaled_dot_product_attention(torch.zeros(1, 2, 3, 32), torch.zeros(1, 2, 4, 32), torch.zeros(1, 2, 3, 32))
+    with pytest.raises(ValueError, match="groups"):
+        grouped_attention(torch.zeros(1, 10, 64), torch.zeros(1, 10, 64), torch.zeros(1, 10, 64), 2, groups=3)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        scaled_dot_product_attention(torch.zeros(1, 2, 3, 32), torch.zeros(1, 2, 3, 32), torch.zeros(1, 2, 3, 32))
+    m_drop = MultiheadAttention(64, 2, dropout=0.1).train()
+    with pytest.raises(NotImplementedError, match="dropout"):
+        m_drop(torch.zeros(1, 3, 64), torch.zeros(1, 3, 64), torch.zeros(1, 3, 64))

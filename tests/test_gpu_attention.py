@@ -1,0 +1,193 @@
+"""Parity of the decoder self-attention kernels (msda_attention_fwd / _bwd through the C ABI, via
+the torch mirror rfdetr_jax_amd.attention) on an MI355X.
+
+Expected values: oracle/attention_ref.py (float64); for the module, torch's
+``nn.MultiheadAttention`` in float64 on the CPU, run per (image, group). Tolerances
+(``max|got - want| <= tol * max(1, max|want|)``): f32 forward 1e-5, gradients 1e-4; bf16 2e-2.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_ref as AT
+from oracle.msda_ref import bf16_round
+from rfdetr_jax_amd.attention import (
+    MultiheadAttention,
+    decoder_self_attention,
+    grouped_attention,
+    scaled_dot_product_attention,
+)
+from tests._util import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev():
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    return torch.device("cuda:0")
+
+
+def _note(msg):
+    sys.stderr.write(f"[gpu] {msg}\n")
+    sys.stderr.flush()
+
+
+def _t(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(_dev())
+    return t if dtype is None else t.to(dtype)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+SHAPES = {
+    "decoder": (6, 8, 300, 32),   # 300 queries per group, 8 heads x 32 (config-2 slices, fewer of them)
+    "small": (2, 3, 9, 32),
+    "ragged": (2, 2, 37, 64),     # head_dim 64, rows not a multiple of 32
+    "one": (1, 1, 1, 32),
+    "long": (1, 2, 480, 32),      # 8 chunks of keys
+    "long64": (1, 1, 1000, 64),   # head_dim 64, 16 chunks
+}
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+@pytest.mark.parametrize("masked", [False, True], ids=["nomask", "mask"])
+@pytest.mark.parametrize("shape", sorted(SHAPES))
+def test_sdpa_against_oracle(shape, masked, bf16):
+    b, h, length, d = SHAPES[shape]
+    _note(f"sdpa {shape} masked={masked} bf16={bf16}")
+    rng = np.random.default_rng(41)
+    q, k, v, g = (rng.standard_normal((b, h, length, d)).astype(np.float32) for _ in range(4))
+    mask = None
+    if masked:
+        mask = rng.uniform(0, 1, (length, length)) < 0.2
+        mask[:, -3:] = True  # tests/test_attention.py:37-40
+        mask[length // 2] = True  # a fully blocked row: uniform weights
+    if bf16:
+        q, k, v, g = (bf16_round(t) for t in (q, k, v, g))
+    dt = torch.bfloat16 if bf16 else None
+    tq, tk, tv = (_t(x, dt).requires_grad_(True) for x in (q, k, v))
+    out = scaled_dot_product_attention(tq, tk, tv, None if mask is None else _t(mask))
+    out.backward(_t(g, dt))
+    torch.cuda.synchronize()
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    assert_close(_np(out), AT.sdpa(q, k, v, mask), tf, "out")
+    for name, t, want in zip("qkv", (tq, tk, tv), AT.sdpa_vjp(q, k, v, g, mask)):
+        assert_close(_np(t.grad), want, tg, f"grad_{name}")
+
+
+def test_reference_known_answers():
+    """tests/test_attention.py:104-119 (at head_dim 32): equal scores give the mean of V, and the
+    padding of the key blocks takes no weight."""
+    q = torch.ones((2, 3, 145, 32), device=_dev())
+    k = -torch.ones((2, 3, 145, 32), device=_dev())
+    v = _t(np.random.default_rng(0).standard_normal((2, 3, 145, 32)).astype(np.float32))
+    out = _np(scaled_dot_product_attention(q, k, v))
+    want = _np(v).astype(np.float64).mean(axis=2, keepdims=True)
+    assert_close(out, np.broadcast_to(want, out.shape), 1e-5, "mean")
+
+
+def test_grouped_rows_layout_against_split_groups():
+    """[B, G * P, C] rows with q and k read in place from a fused [B, Q, 2C] projection (row stride
+    2C): the same as splitting the groups onto the batch, attending per head and merging back."""
+    batch, groups, per, heads, d = 2, 13, 30, 8, 32
+    c = heads * d
+    rng = np.random.default_rng(42)
+    qk = rng.standard_normal((batch, groups * per, 2 * c)).astype(np.float32)
+    v = rng.standard_normal((batch, groups * per, c)).astype(np.float32)
+    g = rng.standard_normal((batch, groups * per, c)).astype(np.float32)
+    tqk = _t(qk).requires_grad_(True)
+    tv = _t(v).requires_grad_(True)
+    out = grouped_attention(tqk[..., :c], tqk[..., c:], tv, heads, groups)
+    out.backward(_t(g))
+
+    def heads_of(x):  # [G B, P, C] -> [G B, H, P, D]
+        return x.reshape(x.shape[0], per, heads, d).transpose(0, 2, 1, 3)
+
+    qs, ks, vs = (heads_of(AT.split_groups(x, per)) for x in (qk[..., :c], qk[..., c:], v))
+    gs = heads_of(AT.split_groups(g, per))
+    want = AT.merge_groups(AT.sdpa(qs, ks, vs).transpose(0, 2, 1, 3).reshape(groups * batch, per, c), batch)
+    assert_close(_np(out), want, 1e-5, "out")
+    dq, dk, dv = (AT.merge_groups(x.transpose(0, 2, 1, 3).reshape(groups * batch, per, c), batch) for x in AT.sdpa_vjp(qs, ks, vs, gs))
+    gqk = _np(tqk.grad)
+    assert_close(gqk[..., :c], dq, 1e-4, "grad_q")
+    assert_close(gqk[..., c:], dk, 1e-4, "grad_k")
+    assert_close(_np(tv.grad), dv, 1e-4, "grad_v")
+
+
+def _torch_reference(m, tgt, pos, groups, heads, grad):
+    """The decoder self-attention written with torch's float64 nn.MultiheadAttention on the CPU, one
+    (image, group) block at a time, with the parameter gradients."""
+    c = tgt.shape[-1]
+    ref = torch.nn.MultiheadAttention(c, heads, batch_first=True, dtype=torch.float64)
+    with torch.no_grad():
+        ref.in_proj_weight.copy_(m.in_proj_weight.detach().double().cpu())
+        ref.in_proj_bias.copy_(m.in_proj_bias.detach().double().cpu())
+        ref.out_proj.weight.copy_(m.out_proj.weight.detach().double().cpu())
+        ref.out_proj.bias.copy_(m.out_proj.bias.detach().double().cpu())
+    t = torch.tensor(tgt, dtype=torch.float64, requires_grad=True)
+    p = torch.tensor(pos, dtype=torch.float64)
+    batch, total, _ = tgt.shape
+    per = total // groups
+    query = t + p
+    outs = []
+    for b in range(batch):
+        row = []
+        for g in range(groups):
+            sl = slice(g * per, (g + 1) * per)
+            o, _ = ref(query[b:b + 1, sl], query[b:b + 1, sl], t[b:b + 1, sl], need_weights=False)
+            row.append(o)
+        outs.append(torch.cat(row, 1))
+    out = torch.cat(outs, 0)
+    out.backward(torch.tensor(grad, dtype=torch.float64))
+    grads = {"in_proj_weight": ref.in_proj_weight.grad, "in_proj_bias": ref.in_proj_bias.grad,
+             "out_proj.weight": ref.out_proj.weight.grad, "out_proj.bias": ref.out_proj.bias.grad}
+    return out.detach().numpy(), t.grad.numpy(), {k: v.numpy() for k, v in grads.items()}
+
+
+@pytest.mark.parametrize("groups", [1, 3])
+def test_decoder_self_attention_module(groups):
+    """The whole block (fused q/k projection, attention per group, out_proj) and every gradient."""
+    torch.manual_seed(0)
+    heads, c, batch, per = 8, 256, 2, 40
+    m = MultiheadAttention(c, heads).to(_dev())
+    with torch.no_grad():
+        m.in_proj_bias.normal_(0, 0.1)
+        m.out_proj.bias.normal_(0, 0.1)
+    rng = np.random.default_rng(43)
+    tgt = rng.standard_normal((batch, groups * per, c)).astype(np.float32)
+    pos = rng.standard_normal((batch, groups * per, c)).astype(np.float32)
+    grad = rng.standard_normal((batch, groups * per, c)).astype(np.float32)
+    tt = _t(tgt).requires_grad_(True)
+    out = decoder_self_attention(tt, _t(pos), m, groups)
+    out.backward(_t(grad))
+    want, want_dt, want_grads = _torch_reference(m, tgt, pos, groups, heads, grad)
+    assert_close(_np(out), want, 1e-5, "out")
+    assert_close(_np(tt.grad), want_dt, 1e-4, "grad tgt")
+    for name, p in m.named_parameters():
+        assert_close(_np(p.grad), want_grads[name], 1e-4, f"grad {name}")
+
+
+def test_single_gradient_requests():
+    from rfdetr_jax_amd.attention import _Layout, attention_backward, attention_forward
+
+    rng = np.random.default_rng(44)
+    q, k, v, g = (rng.standard_normal((2, 2, 50, 32)).astype(np.float32) for _ in range(4))
+    lay = _Layout(2, 1, 2, 50, 32)
+    tq, tk, tv = _t(q), _t(k), _t(v)
+    out, stats = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
+    want = AT.sdpa_vjp(q, k, v, g)
+    for i in range(3):
+        needs = tuple(j == i for j in range(3))
+        got = attention_backward(tq, tk, tv, out, stats, _t(g), lay, lay.strides_bhld, None, needs)
+        for j in range(3):
+            if j == i:
+                assert_close(_np(got[j]), want[j], 1e-4, f"gradient {j}")
+            else:
+                assert got[j] is None
