@@ -45,40 +45,59 @@ msda::AttnParams at_params(int dtype, int batch, int groups, int heads, int len,
   return p;
 }
 
+// Row blocks per workgroup: 4, unless that leaves more waves without a block than 2 does (at
+// 300 rows, 10 blocks: 4 per workgroup idles 2 of 12 waves, 2 per workgroup none).
+int at_row_blocks(int len) {
+  const int nb = (len + 31) / 32;
+  const int idle4 = (4 - nb % 4) % 4, idle2 = nb % 2;
+  return idle2 < idle4 ? 2 : 4;
+}
+
 template <typename K>
-int at_launch(K kernel, std::atomic<int> (&granted)[msda_host::kMaxDevices], const msda::AttnParams& p, int lds, hipStream_t st,
+int at_launch(K kernel, std::atomic<int> (&granted)[msda_host::kMaxDevices], const msda::AttnParams& p, int lds, int rb, hipStream_t st,
               const char* what) {
   const int rc = msda_host::allow_lds(kernel, lds, granted);
   if (rc != MSDA_OK) return rc;
-  // (slice, head) pairs x chunks of 4 row blocks of 32 (one per wave)
-  const int64_t chunks = ((p.len + 31) / 32 + msda::kAtRowBlocks - 1) / msda::kAtRowBlocks;
+  // (slice, head) pairs x chunks of rb row blocks of 32 (one per wave)
+  const int64_t chunks = ((p.len + 31) / 32 + rb - 1) / rb;
   const int64_t grid = static_cast<int64_t>(p.batch) * p.groups * p.heads * chunks;
   if (grid >= (int64_t{1} << 31)) return fail(MSDA_ERR_UNSUPPORTED, "attention: too many workgroups");
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(msda::kAtThreads), lds, st, p);
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * rb), lds, st, p);
   return msda_host::check_launch(what);
 }
 
 // The mask is a template parameter: without one the kernels carry no per-score mask code (and
 // need fewer registers).
+template <typename VT, int D, bool MASK, int RB>
+int fwd_rb(const msda::AttnParams& p, hipStream_t st) {
+  static std::atomic<int> granted[msda_host::kMaxDevices];
+  return at_launch(msda::attn_fwd_kernel<VT, D, MASK, RB>, granted, p, lds_bytes(D), RB, st, "attention forward");
+}
+
 template <typename VT, int D, bool MASK>
 int fwd_typed(const msda::AttnParams& p, hipStream_t st) {
-  static std::atomic<int> granted[msda_host::kMaxDevices];
-  return at_launch(msda::attn_fwd_kernel<VT, D, MASK>, granted, p, lds_bytes(D), st, "attention forward");
+  return at_row_blocks(p.len) == 2 ? fwd_rb<VT, D, MASK, 2>(p, st) : fwd_rb<VT, D, MASK, 4>(p, st);
+}
+
+template <typename VT, int D, bool MASK, int RB>
+int bwd_rb(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
+  int rc = MSDA_OK;
+  {  // grad_q, and rowsum(dO * O) into the statistics for the key side (alone when grad_q is NULL)
+    static std::atomic<int> granted[msda_host::kMaxDevices];
+    if ((rc = at_launch(msda::attn_bwd_q_kernel<VT, D, MASK, RB>, granted, p, lds_bytes(D), RB, st, "attention backward (queries)")) !=
+        MSDA_OK)
+      return rc;
+  }
+  if (want_kv) {  // 4 key blocks per workgroup: with 2, the staging registers of the Q and dO chunks cost an occupancy step
+    static std::atomic<int> granted[msda_host::kMaxDevices];
+    rc = at_launch(msda::attn_bwd_kv_kernel<VT, D, MASK, 4>, granted, p, lds_bytes(D), 4, st, "attention backward (keys, values)");
+  }
+  return rc;
 }
 
 template <typename VT, int D, bool MASK>
 int bwd_typed(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
-  int rc = MSDA_OK;
-  {  // grad_q, and rowsum(dO * O) into the statistics for the key side (alone when grad_q is NULL)
-    static std::atomic<int> granted[msda_host::kMaxDevices];
-    if ((rc = at_launch(msda::attn_bwd_q_kernel<VT, D, MASK>, granted, p, lds_bytes(D), st, "attention backward (queries)")) != MSDA_OK)
-      return rc;
-  }
-  if (want_kv) {
-    static std::atomic<int> granted[msda_host::kMaxDevices];
-    rc = at_launch(msda::attn_bwd_kv_kernel<VT, D, MASK>, granted, p, lds_bytes(D), st, "attention backward (keys, values)");
-  }
-  return rc;
+  return at_row_blocks(p.len) == 2 ? bwd_rb<VT, D, MASK, 2>(p, want_kv, st) : bwd_rb<VT, D, MASK, 4>(p, want_kv, st);
 }
 
 template <typename VT>

@@ -101,35 +101,34 @@ struct AttnSlice {
   }
 };
 
-// Work split: a workgroup is (slice, head, 4 blocks of 32 rows on its own side: queries for the
-// forward and dQ, keys for dK / dV), one block per wave; the other side streams through LDS in
-// chunks of 64 rows (two blocks), staged from registers loaded one chunk ahead. A workgroup needs
-// 2 x 64 rows of D + 8 floats (20 KB at D = 32), so several share a CU and their waves fill each
-// other's barrier and staging gaps.
-constexpr int kAtThreads = 256;
-constexpr int kAtRowBlocks = kAtThreads / 64;  // row blocks (waves) per workgroup
-constexpr int kAtChunk = 64;                   // streamed rows per LDS chunk
+// Work split: a workgroup is (slice, head, RB = 2 or 4 blocks of 32 rows on its own side: queries
+// for the forward and dQ, keys for dK / dV), one block per wave (the host picks the RB that leaves
+// fewest waves without a block); the other side streams through LDS in chunks of 64 rows (two
+// blocks), staged from registers loaded one chunk ahead. A workgroup needs 2 x 64 rows of D + 8
+// floats (20 KB at D = 32), so several share a CU and their waves fill each other's barrier and
+// staging gaps.
+constexpr int kAtChunk = 64;  // streamed rows per LDS chunk
 
 template <int D>
 constexpr int at_lds_floats() { return 2 * kAtChunk * (D + 8) + 3 * kAtChunk; }  // two row tiles, three per-row floats
 
 // One tensor's slice of a 64-row chunk in registers: the thread's 4-element vectors, clamped to
 // row L - 1 (zeroed when stored).
-template <typename VT, int D>
+template <typename VT, int D, int NT>
 struct AtChunk {
-  static constexpr int C4 = D / 4, NV = kAtChunk * C4 / kAtThreads;
+  static constexpr int C4 = D / 4, NV = kAtChunk * C4 / NT;
   at_f4 v[NV];
   __device__ void load(const VT* src, int64_t rs, int r0, int L) {
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
-      const int idx = threadIdx.x + kAtThreads * u, row = idx / C4, c4 = idx - row * C4;
+      const int idx = threadIdx.x + NT * u, row = idx / C4, c4 = idx - row * C4;
       v[u] = at_ld4<VT>(src, min(r0 + row, L - 1) * rs + 4 * c4);
     }
   }
   __device__ void store(float* dst, int r0, int L) const {
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
-      const int idx = threadIdx.x + kAtThreads * u, row = idx / C4, c4 = idx - row * C4;
+      const int idx = threadIdx.x + NT * u, row = idx / C4, c4 = idx - row * C4;
       const bool ok = r0 + row < L;
       *reinterpret_cast<at_f4*>(&dst[row * (D + 8) + 4 * c4]) =
           ok ? v[u] : at_f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -236,18 +235,19 @@ struct AttnWork {
 
 // Forward: out = softmax(q k^T / sqrt(D), blocked -> finfo.min) v. Each wave owns 32 queries; K and
 // V stream through LDS; the running maximum rescales the partial sums.
-template <typename VT, int D, bool MASK>
-__global__ void __launch_bounds__(kAtThreads, D == 32 ? 3 : 2) attn_fwd_kernel(const AttnParams p) {
+template <typename VT, int D, bool MASK, int RB>
+__global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_kernel(const AttnParams p) {
+  constexpr int NT = 64 * RB;
   constexpr int LD = D + 8, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
   float* Ks = at_lds;
   float* Vs = at_lds + kAtChunk * LD;
   const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
-  const AttnWork w(p, (nb + kAtRowBlocks - 1) / kAtRowBlocks);
+  const AttnWork w(p, (nb + RB - 1) / RB);
   const VT* kp = static_cast<const VT*>(p.k) + w.sl.base(p, kAtK);
   const VT* vp = static_cast<const VT*>(p.v) + w.sl.base(p, kAtV);
   const int lane = threadIdx.x & 63, grp = lane >> 5, col = lane & 31;
-  const int qb = w.rc * kAtRowBlocks + (threadIdx.x >> 6), qi = qb * 32 + col;
+  const int qb = w.rc * RB + (threadIdx.x >> 6), qi = qb * 32 + col;
   const bool qv = qi < L;
   at_f4 qr[D / 8];
   {
@@ -259,7 +259,7 @@ __global__ void __launch_bounds__(kAtThreads, D == 32 ? 3 : 2) attn_fwd_kernel(c
   at_f16 o0[ND], o1[ND];
 #pragma unroll
   for (int nd = 0; nd < ND; ++nd) o0[nd] = o1[nd] = at_zero16();
-  AtChunk<VT, D> kc, vc;
+  AtChunk<VT, D, NT> kc, vc;
   kc.load(kp, p.st[kAtK][3], 0, L);
   vc.load(vp, p.st[kAtV][3], 0, L);
   for (int j = 0; j < nchunks; ++j) {
@@ -316,18 +316,19 @@ __global__ void __launch_bounds__(kAtThreads, D == 32 ? 3 : 2) attn_fwd_kernel(c
 // recomputed from the stored statistics. Each wave owns 32 queries; K and V stream through LDS.
 // Also stores rowsum(dO * O) of its queries in the statistics for the key-side kernel (with no
 // grad_q requested, that is all it does).
-template <typename VT, int D, bool MASK>
-__global__ void __launch_bounds__(kAtThreads, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_q_kernel(const AttnParams p) {
+template <typename VT, int D, bool MASK, int RB>
+__global__ void __launch_bounds__(64 * RB, D == 32 ? ((MASK || RB == 2) ? 2 : 3) : 1) attn_bwd_q_kernel(const AttnParams p) {
+  constexpr int NT = 64 * RB;
   constexpr int LD = D + 8, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
   float* Ks = at_lds;
   float* Vs = at_lds + kAtChunk * LD;
   const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
-  const AttnWork w(p, (nb + kAtRowBlocks - 1) / kAtRowBlocks);
+  const AttnWork w(p, (nb + RB - 1) / RB);
   const VT* kp = static_cast<const VT*>(p.k) + w.sl.base(p, kAtK);
   const VT* vp = static_cast<const VT*>(p.v) + w.sl.base(p, kAtV);
   const int lane = threadIdx.x & 63, grp = lane >> 5, col = lane & 31;
-  const int qb = w.rc * kAtRowBlocks + (threadIdx.x >> 6), qi = qb * 32 + col;
+  const int qb = w.rc * RB + (threadIdx.x >> 6), qi = qb * 32 + col;
   const bool qv = qi < L;
   const int qc = min(qi, L - 1);
   at_f4 qr[D / 8], gr[D / 8];
@@ -353,7 +354,7 @@ __global__ void __launch_bounds__(kAtThreads, D == 32 ? (MASK ? 2 : 3) : 1) attn
   at_f16 dq0[ND], dq1[ND];
 #pragma unroll
   for (int nd = 0; nd < ND; ++nd) dq0[nd] = dq1[nd] = at_zero16();
-  AtChunk<VT, D> kc, vc;
+  AtChunk<VT, D, NT> kc, vc;
   kc.load(kp, p.st[kAtK][3], 0, L);
   vc.load(vp, p.st[kAtV][3], 0, L);
   for (int j = 0; j < nchunks; ++j) {
@@ -396,8 +397,9 @@ __global__ void __launch_bounds__(kAtThreads, D == 32 ? (MASK ? 2 : 3) : 1) attn
 // in registers) and forms S and dP untransposed (queries x keys), so a lane owns one key; Q, dO and
 // the per-query statistics (with rowsum(dO * O), written by the query-side kernel) stream through
 // LDS.
-template <typename VT, int D, bool MASK>
-__global__ void __launch_bounds__(kAtThreads, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_kv_kernel(const AttnParams p) {
+template <typename VT, int D, bool MASK, int RB>
+__global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_kv_kernel(const AttnParams p) {
+  constexpr int NT = 64 * RB;
   constexpr int LD = D + 8, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
   float* Qs = at_lds;
@@ -405,12 +407,12 @@ __global__ void __launch_bounds__(kAtThreads, D == 32 ? (MASK ? 2 : 3) : 1) attn
   float* Ms = Gs + kAtChunk * LD;  // [64][2]: m, log2 l (rows past L: +inf, so their weight is 0)
   float* Ds = Ms + 2 * kAtChunk;   // [64]: rowsum(dO * O)
   const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
-  const AttnWork w(p, (nb + kAtRowBlocks - 1) / kAtRowBlocks);
+  const AttnWork w(p, (nb + RB - 1) / RB);
   const VT* qp = static_cast<const VT*>(p.q) + w.sl.base(p, kAtQ);
   const VT* gop = static_cast<const VT*>(p.go) + w.sl.base(p, kAtGO);
   const float* stats = p.stats + static_cast<int64_t>(w.zh) * L * 4;
   const int t = threadIdx.x, lane = t & 63, grp = lane >> 5, col = lane & 31;
-  const int kb = w.rc * kAtRowBlocks + (t >> 6), key = kb * 32 + col;
+  const int kb = w.rc * RB + (t >> 6), key = kb * 32 + col;
   const bool kv = key < L;
   at_f4 kr[D / 8], vr[D / 8];
   {
@@ -426,7 +428,7 @@ __global__ void __launch_bounds__(kAtThreads, D == 32 ? (MASK ? 2 : 3) : 1) attn
   at_f16 dk[ND], dv[ND];
 #pragma unroll
   for (int nd = 0; nd < ND; ++nd) dk[nd] = dv[nd] = at_zero16();
-  AtChunk<VT, D> qc, gc;
+  AtChunk<VT, D, NT> qc, gc;
   at_f4 sq = {0.0f, 0.0f, 0.0f, 0.0f};  // threads < 64: m, log2 l, rowsum(dO * O) of chunk row t
   auto prefetch = [&](int r0) {
     qc.load(qp, p.st[kAtQ][3], r0, L);
