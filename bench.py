@@ -364,7 +364,7 @@ def measure_value_proj(dev, steps, batch=8, seq=576, d_model=256, heads=16):
     }
 
 
-def measure_attention(dev, steps, batch=8, groups=13, per=300, heads=8, head_dim=32):
+def measure_attention(dev, steps, batch=8, groups=13, per=300, heads=8, head_dim=32, dtype="f32"):
     """The decoder's grouped self-attention at the config-2 shape (8 images x 13 groups x 300
     queries, 8 heads x 32, f32): the attention alone (msda_attention_fwd, then _bwd for q, k and v)
     on the [B, G * P, C] rows in place, beside torch's F.scaled_dot_product_attention on the same
@@ -378,10 +378,11 @@ def measure_attention(dev, steps, batch=8, groups=13, per=300, heads=8, head_dim
     from rfdetr_jax_amd.attention import _Layout, attention_backward, attention_forward
 
     c = heads * head_dim
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     rng = np.random.default_rng(10)
-    qk = torch.from_numpy(rng.standard_normal((batch, groups * per, 2 * c), dtype=np.float32)).to(dev)
-    v = torch.from_numpy(rng.standard_normal((batch, groups * per, c), dtype=np.float32)).to(dev)
-    g = torch.from_numpy(rng.standard_normal((batch, groups * per, c), dtype=np.float32)).to(dev)
+    qk = torch.from_numpy(rng.standard_normal((batch, groups * per, 2 * c), dtype=np.float32)).to(dev, tdt)
+    v = torch.from_numpy(rng.standard_normal((batch, groups * per, c), dtype=np.float32)).to(dev, tdt)
+    g = torch.from_numpy(rng.standard_normal((batch, groups * per, c), dtype=np.float32)).to(dev, tdt)
     q, k = qk[..., :c], qk[..., c:]
     lay = _Layout(batch, groups, heads, per, head_dim)
     out, stats = attention_forward(q, k, v, lay, lay.strides_rows)
@@ -411,7 +412,7 @@ def measure_attention(dev, steps, batch=8, groups=13, per=300, heads=8, head_dim
     fwd_us = time_graph(fwd, steps)[0]
     step_us = time_graph(ours, steps)[0]
     return {
-        "shape": {"batch": batch, "groups": groups, "queries_per_group": per, "heads": heads, "head_dim": head_dim, "dtype": "f32"},
+        "shape": {"batch": batch, "groups": groups, "queries_per_group": per, "heads": heads, "head_dim": head_dim, "dtype": dtype},
         "fwd_us": round(fwd_us, 3),
         "step_us": round(step_us, 3),
         "fwd_tflops": round(flops_fwd / fwd_us / 1e6, 1),
@@ -494,6 +495,7 @@ def main():
                     help="for rocprofv3 runs: K eager steps of the value projection fwd+bwd, ours then torch's")
     ap.add_argument("--profile-attention", action="store_true",
                     help="for rocprofv3 runs: K steps of the decoder self-attention fwd+bwd, ours then torch's")
+    ap.add_argument("--attention-dtype", choices=["f32", "bf16"], default="f32", help="with --profile-attention")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): the deformable-attention op needs no "
@@ -519,7 +521,7 @@ def main():
         print(json.dumps(measure_value_proj(dev, args.steps)), flush=True)
         return
     if args.profile_attention:
-        print(json.dumps(measure_attention(dev, args.steps)), flush=True)
+        print(json.dumps(measure_attention(dev, args.steps, dtype=args.attention_dtype)), flush=True)
         return
     log(f"workload {w.name}: warmup {args.warmup}, steps {args.steps}")
     res, calls = measure(w, dev, args.steps, args.warmup)
@@ -559,6 +561,7 @@ def main():
         per_config["value_proj_b8_s576_c256_h16"] = measure_value_proj(dev, max(50, args.steps // 2))
         log("decoder self-attention")
         per_config["self_attention_b8_g13_p300_h8_d32_f32"] = measure_attention(dev, max(20, args.steps // 8))
+        per_config["self_attention_b8_g13_p300_h8_d32_bf16"] = measure_attention(dev, max(20, args.steps // 8), dtype="bf16")
         log("point sample (segmentation loss)")
         per_config["point_sample_mask_loss_400x112x112"] = measure_point_sample(dev, max(50, args.steps // 2))
 

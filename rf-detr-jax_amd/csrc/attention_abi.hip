@@ -16,6 +16,11 @@ using msda_host::fail;
 
 int lds_bytes(int d) { return (d == 32 ? msda::at_lds_floats<32>() : msda::at_lds_floats<64>()) * 4; }
 
+// bf16 kernels: row tiles [64][D + 8] and transposed tiles [D][72] of bf16, and per-row floats
+int lds_bf16(int d, int row_tiles, int t_tiles, bool rows_f32) {
+  return (row_tiles * msda::kAtChunk * (d + 8) + t_tiles * d * msda::kAtLdt) * 2 + (rows_f32 ? 3 * msda::kAtChunk * 4 : 0);
+}
+
 int at_validate(int dtype, int batch, int groups, int heads, int len, int head_dim, const int64_t* strides, int ntensors) {
   if (dtype != MSDA_DTYPE_F32 && dtype != MSDA_DTYPE_BF16) return fail(MSDA_ERR_UNSUPPORTED, "attention: unsupported dtype code %d", dtype);
   if (batch < 0 || groups < 0 || heads < 0 || len < 0) return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: negative extent");
@@ -100,18 +105,57 @@ int bwd_typed(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
   return at_row_blocks(p.len) == 2 ? bwd_rb<VT, D, MASK, 2>(p, want_kv, st) : bwd_rb<VT, D, MASK, 4>(p, want_kv, st);
 }
 
-template <typename VT>
-int fwd_dispatch(const msda::AttnParams& p, int d, hipStream_t st) {
-  const bool m = p.mask != nullptr;
-  if (d == 32) return m ? fwd_typed<VT, 32, true>(p, st) : fwd_typed<VT, 32, false>(p, st);
-  return m ? fwd_typed<VT, 64, true>(p, st) : fwd_typed<VT, 64, false>(p, st);
+// bf16 inputs: the bf16-MFMA kernels
+template <int D, bool MASK, int RB>
+int fwd_b_rb(const msda::AttnParams& p, hipStream_t st) {
+  static std::atomic<int> granted[msda_host::kMaxDevices];
+  return at_launch(msda::attn_fwd_bf16_kernel<D, MASK, RB>, granted, p, lds_bf16(D, 1, 1, false), RB, st, "attention forward");
 }
 
-template <typename VT>
-int bwd_dispatch(const msda::AttnParams& p, int d, bool want_kv, hipStream_t st) {
+template <int D, bool MASK>
+int fwd_b(const msda::AttnParams& p, hipStream_t st) {
+  return at_row_blocks(p.len) == 2 ? fwd_b_rb<D, MASK, 2>(p, st) : fwd_b_rb<D, MASK, 4>(p, st);
+}
+
+template <int D, bool MASK, int RB>
+int bwd_b_rb(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
+  int rc = MSDA_OK;
+  {
+    static std::atomic<int> granted[msda_host::kMaxDevices];
+    if ((rc = at_launch(msda::attn_bwd_q_bf16_kernel<D, MASK, RB>, granted, p, lds_bf16(D, 2, 1, false), RB, st,
+                        "attention backward (queries)")) != MSDA_OK)
+      return rc;
+  }
+  if (want_kv) {
+    static std::atomic<int> granted[msda_host::kMaxDevices];
+    rc = at_launch(msda::attn_bwd_kv_bf16_kernel<D, MASK, 4>, granted, p, lds_bf16(D, 2, 2, true), 4, st, "attention backward (keys, values)");
+  }
+  return rc;
+}
+
+template <int D, bool MASK>
+int bwd_b(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
+  return at_row_blocks(p.len) == 2 ? bwd_b_rb<D, MASK, 2>(p, want_kv, st) : bwd_b_rb<D, MASK, 4>(p, want_kv, st);
+}
+
+int fwd_dispatch(const msda::AttnParams& p, int d, bool bf16, hipStream_t st) {
   const bool m = p.mask != nullptr;
-  if (d == 32) return m ? bwd_typed<VT, 32, true>(p, want_kv, st) : bwd_typed<VT, 32, false>(p, want_kv, st);
-  return m ? bwd_typed<VT, 64, true>(p, want_kv, st) : bwd_typed<VT, 64, false>(p, want_kv, st);
+  if (bf16) {
+    if (d == 32) return m ? fwd_b<32, true>(p, st) : fwd_b<32, false>(p, st);
+    return m ? fwd_b<64, true>(p, st) : fwd_b<64, false>(p, st);
+  }
+  if (d == 32) return m ? fwd_typed<float, 32, true>(p, st) : fwd_typed<float, 32, false>(p, st);
+  return m ? fwd_typed<float, 64, true>(p, st) : fwd_typed<float, 64, false>(p, st);
+}
+
+int bwd_dispatch(const msda::AttnParams& p, int d, bool bf16, bool want_kv, hipStream_t st) {
+  const bool m = p.mask != nullptr;
+  if (bf16) {
+    if (d == 32) return m ? bwd_b<32, true>(p, want_kv, st) : bwd_b<32, false>(p, want_kv, st);
+    return m ? bwd_b<64, true>(p, want_kv, st) : bwd_b<64, false>(p, want_kv, st);
+  }
+  if (d == 32) return m ? bwd_typed<float, 32, true>(p, want_kv, st) : bwd_typed<float, 32, false>(p, want_kv, st);
+  return m ? bwd_typed<float, 64, true>(p, want_kv, st) : bwd_typed<float, 64, false>(p, want_kv, st);
 }
 
 }  // namespace
@@ -138,7 +182,7 @@ int msda_attention_fwd(const void* q, const void* k, const void* v, int dtype, v
   p.stats = stats;
   p.mask = mask;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return dtype == MSDA_DTYPE_BF16 ? fwd_dispatch<msda::bf16_t>(p, head_dim, st) : fwd_dispatch<float>(p, head_dim, st);
+  return fwd_dispatch(p, head_dim, dtype == MSDA_DTYPE_BF16, st);
 }
 
 int msda_attention_bwd(const void* q, const void* k, const void* v, const void* out, float* stats, const void* grad_out, int dtype,
@@ -168,7 +212,7 @@ int msda_attention_bwd(const void* q, const void* k, const void* v, const void* 
   p.stats = stats;
   p.mask = mask;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return dtype == MSDA_DTYPE_BF16 ? bwd_dispatch<msda::bf16_t>(p, head_dim, want_kv, st) : bwd_dispatch<float>(p, head_dim, want_kv, st);
+  return bwd_dispatch(p, head_dim, dtype == MSDA_DTYPE_BF16, want_kv, st);
 }
 
 }  // extern "C"

@@ -26,6 +26,8 @@
 
 #include <cstdint>
 
+#include "msda_kernels.h"  // bf16_t
+
 namespace msda {
 
 typedef float at_f4 __attribute__((ext_vector_type(4)));
@@ -225,6 +227,48 @@ __device__ __forceinline__ void at_scale_scores(at_f16& s0, at_f16& s1, int k0, 
   }
 }
 
+// Online softmax over one chunk's two score blocks (raw dot products in s0, s1; keys
+// k0 + 32 h + 8 (i / 4) + 4 grp + i % 4 of register i, the lane's query qi): turns them into
+// exp2(x - m_new) with x = s log2(e) / sqrt(D) (blocked: finfo.min; past L: -inf), updates the
+// running maximum m and sum l, and returns the factor alpha that rescales earlier partial sums.
+// Without a mask, on a full chunk, the maximum is taken on the raw scores (the scale is positive)
+// and each score costs one fma before the exp2.
+template <bool MASK>
+__device__ __forceinline__ float at_softmax_chunk(at_f16& s0, at_f16& s1, int k0, int L, float scale2, const uint8_t* mask, int qi, int grp,
+                                                  float& m, float& l) {
+  float mn;
+  if (!MASK && k0 + kAtChunk <= L) {
+    float bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bm = fmaxf(bm, fmaxf(s0[i], s1[i]));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    mn = fmaxf(m, bm * scale2);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s0[i] = at_exp2(fmaf(s0[i], scale2, -mn));
+      s1[i] = at_exp2(fmaf(s1[i], scale2, -mn));
+    }
+  } else {
+    float bm = -INFINITY;
+    at_scale_scores<MASK>(s0, s1, k0, L, scale2, mask, qi, grp, bm);
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    mn = fmaxf(m, bm);  // finite: every chunk holds a key below L
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s0[i] = at_exp2(s0[i] - mn);
+      s1[i] = at_exp2(s1[i] - mn);
+    }
+  }
+  float rs = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) rs += s0[i] + s1[i];
+  rs += __shfl_xor(rs, 32, 64);
+  const float alpha = at_exp2(m - mn);
+  l = l * alpha + rs;
+  m = mn;
+  return alpha;
+}
+
 // The workgroup's (slice, head) and row chunk: blockIdx.x = (z * H + h) * chunks + rc.
 struct AttnWork {
   int zh, rc;
@@ -236,7 +280,7 @@ struct AttnWork {
 // Forward: out = softmax(q k^T / sqrt(D), blocked -> finfo.min) v. Each wave owns 32 queries; K and
 // V stream through LDS; the running maximum rescales the partial sums.
 template <typename VT, int D, bool MASK, int RB>
-__global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_kernel(const AttnParams p) {
+__global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : (MASK ? 1 : 2)) attn_fwd_kernel(const AttnParams p) {
   constexpr int NT = 64 * RB;
   constexpr int LD = D + 8, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
@@ -274,21 +318,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_kernel(cons
     if (qb >= nb) continue;
     at_f16 s0, s1;
     at_scores2<D>(s0, s1, Ks, qr, col, grp);
-    float bm = -INFINITY;
-    at_scale_scores<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, qv ? qi : -1, grp, bm);
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    const float mn = fmaxf(m, bm);  // finite: every chunk holds a key below L
-    const float alpha = at_exp2(m - mn);
-    float rs = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s0[i] = at_exp2(s0[i] - mn);
-      s1[i] = at_exp2(s1[i] - mn);
-      rs += s0[i] + s1[i];
-    }
-    rs += __shfl_xor(rs, 32, 64);
-    l = l * alpha + rs;
-    m = mn;
+    const float alpha = at_softmax_chunk<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, qv ? qi : -1, grp, m, l);
 #pragma unroll
     for (int nd = 0; nd < ND; ++nd) {
       o0[nd] *= alpha;
@@ -398,7 +428,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? ((MASK || RB == 2) ? 2 : 3)
 // the per-query statistics (with rowsum(dO * O), written by the query-side kernel) stream through
 // LDS.
 template <typename VT, int D, bool MASK, int RB>
-__global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_kv_kernel(const AttnParams p) {
+__global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bwd_kv_kernel(const AttnParams p) {
   constexpr int NT = 64 * RB;
   constexpr int LD = D + 8, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
@@ -490,6 +520,342 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
         const int d = 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3);
         if (p.gk != nullptr) at_st1<VT>(gkp, key * p.st[kAtGK][3] + d, dk[nd][i] * p.scale);
         if (p.gv != nullptr) at_st1<VT>(gvp, key * p.st[kAtGV][3] + d, dv[nd][i]);
+      }
+  }
+}
+
+// ---- bf16 inputs: products on v_mfma_f32_32x32x16_bf16 -------------------------------------
+// Same work split, streaming and softmax as the f32 kernels. Operands stay bf16 in LDS: row tiles
+// [64][D + 8] (operands along the channels: one 16-byte read per MFMA) and transposed tiles
+// [D][64 + 8] (operands along the streamed rows: two 8-byte reads). v_mfma_f32_32x32x16_bf16: lane
+// l supplies 8 elements of A row l % 32 and of B column l % 32 in reduction slots 8 (l / 32) + j,
+// and the product pairs slot j of both operands, so any reduction-index assignment shared by A and
+// B gives the sum; the result layout is that of the f32 32 x 32 products. Probabilities and dS
+// are rounded to bf16 (v_cvt_pk_bf16_f32, nearest even) for the products they enter, as the
+// reference rounds the softmax weights to the input dtype (layers.py:96-98); sums are f32.
+
+typedef __bf16 at_bf8 __attribute__((ext_vector_type(8)));
+typedef float at_f8 __attribute__((ext_vector_type(8)));
+
+constexpr int kAtLdt = kAtChunk + 8;  // row stride of a transposed bf16 tile
+
+template <int D>
+constexpr int at_lds_bytes_bf16() { return (4 * kAtChunk * (D + 8) + 4 * D * kAtLdt) * 2 + 3 * kAtChunk * 4; }
+
+__device__ __forceinline__ at_bf8 at_bf8_of(uint2 lo, uint2 hi) { return __builtin_bit_cast(at_bf8, uint4{lo.x, lo.y, hi.x, hi.y}); }
+
+// registers i0 .. i0 + 7 of a result block, rounded to bf16
+__device__ __forceinline__ at_bf8 at_bf8_regs(const at_f16& v, int i0) {
+  const at_f8 f = {v[i0], v[i0 + 1], v[i0 + 2], v[i0 + 3], v[i0 + 4], v[i0 + 5], v[i0 + 6], v[i0 + 7]};
+  return __builtin_convertvector(f, at_bf8);
+}
+
+// channels 16 s + 8 (l / 32) .. + 7 of one row, s < D / 16 (two 8-byte loads: rows are 8-byte aligned)
+template <int D>
+__device__ __forceinline__ void at_row_bf8(at_bf8 (&r)[D / 16], const uint16_t* src, int64_t off, int grp) {
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) {
+    const uint16_t* e = src + off + 16 * s + 8 * grp;
+    r[s] = at_bf8_of(*reinterpret_cast<const uint2*>(e), *reinterpret_cast<const uint2*>(e + 4));
+  }
+}
+
+// A raw bf16 chunk (64 rows x D) in registers: 4-element vectors, rows clamped to L - 1.
+template <int D, int NT>
+struct AtChunkB {
+  static constexpr int C4 = D / 4, NV = kAtChunk * C4 / NT;
+  uint2 v[NV];
+  __device__ void load(const uint16_t* src, int64_t rs, int r0, int L) {
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int idx = threadIdx.x + NT * u, row = idx / C4, c4 = idx - row * C4;
+      v[u] = *reinterpret_cast<const uint2*>(src + min(r0 + row, L - 1) * rs + 4 * c4);
+    }
+  }
+  __device__ void store_rows(uint16_t* dst, int r0, int L) const {  // [64][D + 8]
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int idx = threadIdx.x + NT * u, row = idx / C4, c4 = idx - row * C4;
+      *reinterpret_cast<uint2*>(&dst[row * (D + 8) + 4 * c4]) = r0 + row < L ? v[u] : uint2{0u, 0u};
+    }
+  }
+  __device__ void store_t(uint16_t* dst, int r0, int L) const {  // [D][64 + 8]
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int idx = threadIdx.x + NT * u, row = idx / C4, c4 = idx - row * C4;
+      const uint2 w = r0 + row < L ? v[u] : uint2{0u, 0u};
+      dst[(4 * c4) * kAtLdt + row] = static_cast<uint16_t>(w.x);
+      dst[(4 * c4 + 1) * kAtLdt + row] = static_cast<uint16_t>(w.x >> 16);
+      dst[(4 * c4 + 2) * kAtLdt + row] = static_cast<uint16_t>(w.y);
+      dst[(4 * c4 + 3) * kAtLdt + row] = static_cast<uint16_t>(w.y >> 16);
+    }
+  }
+};
+
+// Result-layout scores of two 32-row blocks against register operands: s0 = X0 . xr, s1 = X1 . yr
+// (X rows from a row tile, the lane's row of X at col; two chains).
+template <int D>
+__device__ __forceinline__ void at_scores_b(at_f16& s0, at_f16& s1, const uint16_t* X0, const uint16_t* X1, const at_bf8 (&xr)[D / 16],
+                                            const at_bf8 (&yr)[D / 16], int col, int grp) {
+  constexpr int LDR = D + 8;
+  s0 = at_zero16();
+  s1 = at_zero16();
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) {
+    const at_bf8 a0 = __builtin_bit_cast(at_bf8, *reinterpret_cast<const uint4*>(&X0[col * LDR + 16 * s + 8 * grp]));
+    const at_bf8 a1 = __builtin_bit_cast(at_bf8, *reinterpret_cast<const uint4*>(&X1[col * LDR + 16 * s + 8 * grp]));
+    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, xr[s], s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, yr[s], s1, 0, 0, 0);
+  }
+}
+
+// acc0 += X0^T w0 and acc1 += X1^T w1 over one 32-row block (two chains): X from transposed tiles
+// (X0t, X1t at the block's first row), w in result-layout registers (register i is row
+// 8 (i / 4) + 4 (l / 32) + i % 4; slots 0..7 of MFMA s are registers 8 s .. 8 s + 7, rows
+// 16 s + 4 (l / 32) + 0..3 and 16 s + 8 + 4 (l / 32) + 0..3).
+template <int D>
+__device__ __forceinline__ void at_accum_b(at_f16 (&acc0)[D / 32], at_f16 (&acc1)[D / 32], const uint16_t* X0t, const uint16_t* X1t,
+                                           const at_f16& w0, const at_f16& w1, int col, int grp) {
+  at_bf8 b0[2], b1[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    b0[s] = at_bf8_regs(w0, 8 * s);
+    b1[s] = at_bf8_regs(w1, 8 * s);
+  }
+#pragma unroll
+  for (int nd = 0; nd < D / 32; ++nd)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int o = (32 * nd + col) * kAtLdt + 16 * s + 4 * grp;
+      const at_bf8 a0 = at_bf8_of(*reinterpret_cast<const uint2*>(&X0t[o]), *reinterpret_cast<const uint2*>(&X0t[o + 8]));
+      const at_bf8 a1 = at_bf8_of(*reinterpret_cast<const uint2*>(&X1t[o]), *reinterpret_cast<const uint2*>(&X1t[o + 8]));
+      acc0[nd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0[s], acc0[nd], 0, 0, 0);
+      acc1[nd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1[s], acc1[nd], 0, 0, 0);
+    }
+}
+
+template <int D, bool MASK, int RB>
+__global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel(const AttnParams p) {
+  constexpr int NT = 64 * RB, LDR = D + 8, ND = D / 32;
+  extern __shared__ __align__(16) float at_lds[];
+  uint16_t* Kr = reinterpret_cast<uint16_t*>(at_lds);
+  uint16_t* Vt = Kr + kAtChunk * LDR;
+  const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
+  const AttnWork w(p, (nb + RB - 1) / RB);
+  const uint16_t* kp = static_cast<const uint16_t*>(p.k) + w.sl.base(p, kAtK);
+  const uint16_t* vp = static_cast<const uint16_t*>(p.v) + w.sl.base(p, kAtV);
+  const int lane = threadIdx.x & 63, grp = lane >> 5, col = lane & 31;
+  const int qb = w.rc * RB + (threadIdx.x >> 6), qi = qb * 32 + col;
+  const bool qv = qi < L;
+  at_bf8 qr[D / 16];
+  at_row_bf8<D>(qr, static_cast<const uint16_t*>(p.q) + w.sl.base(p, kAtQ), min(qi, L - 1) * p.st[kAtQ][3], grp);
+  float m = -INFINITY, l = 0.0f;
+  at_f16 o0[ND], o1[ND];
+#pragma unroll
+  for (int nd = 0; nd < ND; ++nd) o0[nd] = o1[nd] = at_zero16();
+  AtChunkB<D, NT> kc, vc;
+  kc.load(kp, p.st[kAtK][3], 0, L);
+  vc.load(vp, p.st[kAtV][3], 0, L);
+  for (int j = 0; j < nchunks; ++j) {
+    __syncthreads();
+    kc.store_rows(Kr, j * kAtChunk, L);
+    vc.store_t(Vt, j * kAtChunk, L);
+    __syncthreads();
+    if (j + 1 < nchunks) {
+      kc.load(kp, p.st[kAtK][3], (j + 1) * kAtChunk, L);
+      vc.load(vp, p.st[kAtV][3], (j + 1) * kAtChunk, L);
+    }
+    if (qb >= nb) continue;
+    at_f16 s0, s1;
+    at_scores_b<D>(s0, s1, Kr, Kr + 32 * LDR, qr, qr, col, grp);  // S^T for the chunk's two key blocks
+    const float alpha = at_softmax_chunk<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, qv ? qi : -1, grp, m, l);
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd) {
+      o0[nd] *= alpha;
+      o1[nd] *= alpha;
+    }
+    at_accum_b<D>(o0, o1, Vt, Vt + 32, s0, s1, col, grp);  // O^T += V^T P^T
+  }
+  if (qv) {
+    bf16_t* op = static_cast<bf16_t*>(p.out) + w.sl.base(p, kAtO);
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        at_st1<bf16_t>(op, qi * p.st[kAtO][3] + 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3), (o0[nd][i] + o1[nd][i]) * inv);
+    if (grp == 0) {
+      float* stats = p.stats + (static_cast<int64_t>(w.zh) * L + qi) * 4;
+      stats[0] = m;
+      stats[1] = log2f(l);
+    }
+  }
+}
+
+template <int D, bool MASK, int RB>
+__global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_q_bf16_kernel(const AttnParams p) {
+  constexpr int NT = 64 * RB, LDR = D + 8, ND = D / 32;
+  extern __shared__ __align__(16) float at_lds[];
+  uint16_t* Kr = reinterpret_cast<uint16_t*>(at_lds);
+  uint16_t* Vr = Kr + kAtChunk * LDR;
+  uint16_t* Kt = Vr + kAtChunk * LDR;
+  const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
+  const AttnWork w(p, (nb + RB - 1) / RB);
+  const uint16_t* kp = static_cast<const uint16_t*>(p.k) + w.sl.base(p, kAtK);
+  const uint16_t* vp = static_cast<const uint16_t*>(p.v) + w.sl.base(p, kAtV);
+  const int lane = threadIdx.x & 63, grp = lane >> 5, col = lane & 31;
+  const int qb = w.rc * RB + (threadIdx.x >> 6), qi = qb * 32 + col;
+  const bool qv = qi < L;
+  const int qc = min(qi, L - 1);
+  at_bf8 qr[D / 16], gr[D / 16];
+  float dsum = 0.0f;
+  {
+    const uint16_t* qp = static_cast<const uint16_t*>(p.q) + w.sl.base(p, kAtQ);
+    const uint16_t* gop = static_cast<const uint16_t*>(p.go) + w.sl.base(p, kAtGO);
+    const uint16_t* opp = static_cast<const uint16_t*>(p.o) + w.sl.base(p, kAtO);
+    at_row_bf8<D>(qr, qp, qc * p.st[kAtQ][3], grp);
+    at_row_bf8<D>(gr, gop, qc * p.st[kAtGO][3], grp);
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t off = 16 * s + 8 * grp + 4 * h;
+        const at_f4 g = at_ld4<bf16_t>(reinterpret_cast<const bf16_t*>(gop), qc * p.st[kAtGO][3] + off);
+        const at_f4 o = at_ld4<bf16_t>(reinterpret_cast<const bf16_t*>(opp), qc * p.st[kAtO][3] + off);
+        dsum += g[0] * o[0] + g[1] * o[1] + g[2] * o[2] + g[3] * o[3];
+      }
+  }
+  dsum += __shfl_xor(dsum, 32, 64);
+  float* stats = p.stats + (static_cast<int64_t>(w.zh) * L + qc) * 4;
+  const float m = stats[0], ll = stats[1];
+  if (qv && grp == 0 && qb < nb) stats[2] = dsum;
+  if (p.gq == nullptr) return;
+  at_f16 dq0[ND], dq1[ND];
+#pragma unroll
+  for (int nd = 0; nd < ND; ++nd) dq0[nd] = dq1[nd] = at_zero16();
+  AtChunkB<D, NT> kc, vc;
+  kc.load(kp, p.st[kAtK][3], 0, L);
+  vc.load(vp, p.st[kAtV][3], 0, L);
+  for (int j = 0; j < nchunks; ++j) {
+    __syncthreads();
+    kc.store_rows(Kr, j * kAtChunk, L);
+    kc.store_t(Kt, j * kAtChunk, L);
+    vc.store_rows(Vr, j * kAtChunk, L);
+    __syncthreads();
+    if (j + 1 < nchunks) {
+      kc.load(kp, p.st[kAtK][3], (j + 1) * kAtChunk, L);
+      vc.load(vp, p.st[kAtV][3], (j + 1) * kAtChunk, L);
+    }
+    if (qb >= nb) continue;
+    at_f16 s[2], dp[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) at_scores_b<D>(s[h2], dp[h2], Kr + 32 * h2 * LDR, Vr + 32 * h2 * LDR, qr, gr, col, grp);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = j * kAtChunk + 32 * h2 + 8 * (i >> 2) + 4 * grp + (i & 3);
+        float x = s[h2][i] * p.scale2;
+        if (key >= L) x = -INFINITY;
+        else if (MASK && qv && p.mask[static_cast<int64_t>(qi) * L + key] != 0) x = kAtMaskScore;
+        s[h2][i] = at_exp2((x - m) - ll) * (dp[h2][i] - dsum);  // dS^T
+      }
+    at_accum_b<D>(dq0, dq1, Kt, Kt + 32, s[0], s[1], col, grp);  // dQ^T += K^T dS^T
+  }
+  if (qv) {
+    bf16_t* gqp = static_cast<bf16_t*>(p.gq) + w.sl.base(p, kAtGQ);
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        at_st1<bf16_t>(gqp, qi * p.st[kAtGQ][3] + 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3), (dq0[nd][i] + dq1[nd][i]) * p.scale);
+  }
+}
+
+template <int D, bool MASK, int RB>
+__global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_kv_bf16_kernel(const AttnParams p) {
+  constexpr int NT = 64 * RB, LDR = D + 8, ND = D / 32;
+  extern __shared__ __align__(16) float at_lds[];
+  uint16_t* Qr = reinterpret_cast<uint16_t*>(at_lds);
+  uint16_t* Gr = Qr + kAtChunk * LDR;
+  uint16_t* Qt = Gr + kAtChunk * LDR;
+  uint16_t* Gt = Qt + D * kAtLdt;
+  float* Ms = reinterpret_cast<float*>(Gt + D * kAtLdt);  // [64][2]: m, log2 l (rows past L: +inf)
+  float* Ds = Ms + 2 * kAtChunk;                          // [64]: rowsum(dO * O)
+  const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
+  const AttnWork w(p, (nb + RB - 1) / RB);
+  const uint16_t* qp = static_cast<const uint16_t*>(p.q) + w.sl.base(p, kAtQ);
+  const uint16_t* gop = static_cast<const uint16_t*>(p.go) + w.sl.base(p, kAtGO);
+  const float* stats = p.stats + static_cast<int64_t>(w.zh) * L * 4;
+  const int t = threadIdx.x, lane = t & 63, grp = lane >> 5, col = lane & 31;
+  const int kb = w.rc * RB + (t >> 6), key = kb * 32 + col;
+  const bool kv = key < L;
+  at_bf8 kr[D / 16], vr[D / 16];
+  at_row_bf8<D>(kr, static_cast<const uint16_t*>(p.k) + w.sl.base(p, kAtK), min(key, L - 1) * p.st[kAtK][3], grp);
+  at_row_bf8<D>(vr, static_cast<const uint16_t*>(p.v) + w.sl.base(p, kAtV), min(key, L - 1) * p.st[kAtV][3], grp);
+  at_f16 dk[ND], dv[ND];
+#pragma unroll
+  for (int nd = 0; nd < ND; ++nd) dk[nd] = dv[nd] = at_zero16();
+  AtChunkB<D, NT> qc, gc;
+  at_f4 sq = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto prefetch = [&](int r0) {
+    qc.load(qp, p.st[kAtQ][3], r0, L);
+    gc.load(gop, p.st[kAtGO][3], r0, L);
+    if (t < kAtChunk) sq = *reinterpret_cast<const at_f4*>(&stats[4 * min(r0 + t, L - 1)]);
+  };
+  prefetch(0);
+  for (int j = 0; j < nchunks; ++j) {
+    const int r0 = j * kAtChunk;
+    __syncthreads();
+    qc.store_rows(Qr, r0, L);
+    qc.store_t(Qt, r0, L);
+    gc.store_rows(Gr, r0, L);
+    gc.store_t(Gt, r0, L);
+    if (t < kAtChunk) {
+      const bool in = r0 + t < L;
+      Ms[2 * t] = in ? sq[0] : INFINITY;
+      Ms[2 * t + 1] = in ? sq[1] : 0.0f;
+      Ds[t] = in ? sq[2] : 0.0f;
+    }
+    __syncthreads();
+    if (j + 1 < nchunks) prefetch(r0 + kAtChunk);
+    if (kb >= nb) continue;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {  // the chunk's two query blocks
+      at_f16 s, dp;
+      at_scores_b<D>(s, dp, Qr + 32 * h2 * LDR, Gr + 32 * h2 * LDR, kr, vr, col, grp);  // S = Q K^T, dP = dO V^T
+      at_f16 pw;
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {
+        const int ql = 32 * h2 + 8 * c4 + 4 * grp;
+        const at_f4 ms0 = *reinterpret_cast<const at_f4*>(&Ms[2 * ql]), ms1 = *reinterpret_cast<const at_f4*>(&Ms[2 * ql + 4]);
+        const at_f4 dd = *reinterpret_cast<const at_f4*>(&Ds[ql]);
+        const float mq[4] = {ms0[0], ms0[2], ms1[0], ms1[2]}, lq[4] = {ms0[1], ms0[3], ms1[1], ms1[3]};
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int i = 4 * c4 + jj;
+          float x = s[i] * p.scale2;
+          if constexpr (MASK) {
+            const int q = r0 + ql + jj;
+            if (q < L && p.mask[static_cast<int64_t>(q) * L + key] != 0) x = kAtMaskScore;
+          }
+          pw[i] = kv ? at_exp2((x - mq[jj]) - lq[jj]) : 0.0f;
+          s[i] = pw[i] * (dp[i] - dd[jj]);  // dS
+        }
+      }
+      at_accum_b<D>(dv, dk, Gt + 32 * h2, Qt + 32 * h2, pw, s, col, grp);  // dV^T += dO^T P, dK^T += Q^T dS
+    }
+  }
+  if (kv) {
+    bf16_t* gkp = static_cast<bf16_t*>(p.gk) + w.sl.base(p, kAtGK);
+    bf16_t* gvp = static_cast<bf16_t*>(p.gv) + w.sl.base(p, kAtGV);
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3);
+        if (p.gk != nullptr) at_st1<bf16_t>(gkp, key * p.st[kAtGK][3] + d, dk[nd][i] * p.scale);
+        if (p.gv != nullptr) at_st1<bf16_t>(gvp, key * p.st[kAtGV][3] + d, dv[nd][i]);
       }
   }
 }
