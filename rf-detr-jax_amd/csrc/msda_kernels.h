@@ -324,10 +324,13 @@ __device__ __forceinline__ void store_vec(VT* __restrict__ p, const float (&a)[V
     for (int k = 0; k < VEC; ++k) v[k] = a[k];
     *reinterpret_cast<typename VecT<float, VEC>::type*>(p) = v;
   } else {
+    // bf16 rows (outputs, grad_value) are written once and not read back by the writing kernel:
+    // non-temporal stores (measured on MI355X: the two_level_fwdbwd_b8_bf16 backward 3.5 % faster;
+    // f32 rows stay ordinary stores, whose rotated 16-byte chunks were slower non-temporal)
     typename VecT<bf16_t, VEC>::type v;
 #pragma unroll
     for (int k = 0; k < VEC; ++k) v[k] = f32_to_bf16(a[k]);
-    *reinterpret_cast<typename VecT<bf16_t, VEC>::type*>(p) = v;
+    __builtin_nontemporal_store(v, reinterpret_cast<typename VecT<bf16_t, VEC>::type*>(p));
   }
 }
 
