@@ -1371,7 +1371,10 @@ bwd_value_kernel(const ValueParams p) {
   const int lid = xcd_logical(blockIdx.x, gridDim.x);
   const int h = lid % p.heads;
   const int rest = lid / p.heads;
-  const int wk = rest % p.nwork;
+  // Items in reverse order: the bands of the coarsest level start first. A level's samples are
+  // split over its bands, so a coarse level's few bands hold the most records each; started last
+  // (behind a fine level's many light bands), they would set the kernel's tail.
+  const int wk = p.nwork - 1 - rest % p.nwork;
   const int b = rest / p.nwork;
   int l = 0;
   while (l + 1 < p.levels && wk >= p.lv[l + 1].band_first) ++l;
