@@ -70,6 +70,16 @@ const char* msda_version(void);
 const char* msda_last_error(void);
 
 /*
+ * Process-wide override of a launch-tuning knob (an MSDA_* name, e.g. "MSDA_BWD_BANDS"); value
+ * NULL removes the override. Knobs otherwise come from the environment, read once per name at its
+ * first use. They choose launch shapes only: results stay within the documented tolerances and no
+ * buffer or workspace size depends on them. Not to be called while another thread launches.
+ * No counterpart in the reference; for benchmarks and tests that compare launch variants.
+ * Returns MSDA_OK, or MSDA_ERR_INVALID_ARGUMENT for a name that does not start with "MSDA_".
+ */
+int msda_set_tuning(const char* name, const char* value);
+
+/*
  * Forward: output = sum_{l,p} A[b,q,h,l*P+p] * bilinear(value[b*H+h], level l, loc[b,q,h,l,p]).
  * Replaces ms_deform_attn_core_rows (src/rfdetr_jax/models/ops.py:208-292) and its "pallas"
  * branch (ops.py:243-263 -> deform_pallas.py:193-228 sample_weighted).
@@ -86,13 +96,11 @@ int msda_fwd(const void* value, int value_dtype,
              int64_t len_value, void* stream);
 
 /*
- * Device workspace msda_bwd needs for this shape, in bytes (>= 0), or a negative MSDA_ERR_* code.
- * It holds 16-byte per-sample records binned by (batch * head slice, band of image rows, block of
- * queries), with a count per bin, written by the per-sample pass and read by the grad_value pass;
- * it is only needed when grad_value is requested. The size depends on the shape and the device
- * (its CU count and LDS size), not on the dtypes. It plays the role of the scratch an XLA FFI handler obtains from
- * ffi::ScratchAllocator (the reference has no counterpart: JAX autodiff materialises its own
- * intermediates, ops.py:120-134).
+ * Device workspace msda_bwd needs for this shape, in bytes, or a negative MSDA_ERR_* code. The
+ * backward is one kernel whose scratch lives in LDS, so this is 0 for every valid shape; the
+ * query stays so that a caller written against a workspace contract (an XLA FFI handler asking
+ * ffi::ScratchAllocator, the reference having no counterpart: JAX autodiff materialises its own
+ * intermediates, ops.py:120-134) keeps working unchanged.
  */
 int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_query,
                                 int n_levels, int n_points,
@@ -107,9 +115,9 @@ int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_qu
  *   grad_attention_weights  [batch, len_query, n_heads, n_levels*n_points]     f32
  * Replaces the JAX autodiff VJP of ops.py:64-134/289 and deform_pallas.py:157-175 (_sample_bwd).
  * Any of the three gradient pointers may be NULL to skip that gradient. grad_output has
- * grad_output_dtype (the forward's output dtype). workspace: 16-byte aligned device memory of at
- * least msda_bwd_workspace_size() bytes (workspace_bytes says how many), or NULL when grad_value
- * is NULL; its contents on entry do not matter. Calls that share a workspace must not overlap.
+ * grad_output_dtype (the forward's output dtype). grad_value is accumulated in f64 (every product
+ * a * w * g of f32 values is exact) and rounded once to value_dtype; every element has one writer.
+ * workspace / workspace_bytes are not read (msda_bwd_workspace_size() is 0) and may be NULL / 0.
  * Limits (MSDA_ERR_UNSUPPORTED beyond them): levels of at most 32000 rows and columns, and
  * len_query * n_heads * head_dim < 2^30.
  */

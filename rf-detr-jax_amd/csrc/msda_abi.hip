@@ -14,7 +14,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <string>
+#include <unordered_map>
 
 namespace {
 thread_local std::string g_last_error;
@@ -170,10 +172,24 @@ int device_info(DevInfo* info) {
   return MSDA_OK;
 }
 
+// Tuning knobs (MSDA_* names): launch-shape choices only; no buffer or workspace size depends on
+// them. Each is read from the environment once, at its first use, and msda_set_tuning() overrides
+// it for the rest of the process, so a plan does not change between calls unless asked to.
+std::mutex g_knob_mu;
+std::unordered_map<std::string, std::pair<bool, int>> g_knob_env;  // name -> (set, value)
+std::unordered_map<std::string, std::pair<bool, int>> g_knob_set;  // msda_set_tuning overrides
+
 int env_int(const char* name, int dflt) {
-  const char* v = std::getenv(name);
-  if (v == nullptr || *v == 0) return dflt;
-  return std::atoi(v);
+  std::lock_guard<std::mutex> lock(g_knob_mu);
+  auto o = g_knob_set.find(name);
+  if (o != g_knob_set.end()) return o->second.first ? o->second.second : dflt;
+  auto it = g_knob_env.find(name);
+  if (it == g_knob_env.end()) {
+    const char* v = std::getenv(name);
+    const bool set = v != nullptr && *v != 0;
+    it = g_knob_env.emplace(name, std::make_pair(set, set ? std::atoi(v) : 0)).first;
+  }
+  return it->second.first ? it->second.second : dflt;
 }
 
 inline int align16(int64_t x) { return static_cast<int>((x + 15) & ~int64_t{15}); }
@@ -387,10 +403,200 @@ int plan_bins(const Shape& s, const DevInfo& dev, BinPlan* bp) {
   return rc;
 }
 
+// ------------------------------------------------------------------------------------------
+// planning of the backward kernel (bwd_band_kernel)
+
+// LDS of one workgroup of the backward kernel for a band of `rows` rows of a level `w` wide: the
+// staged value rows (the band and one halo row), the f64 accumulator of the band, the sample list
+// (`cap` 16-bit entries) and its counter, and the two grad_output row buffers (`gbuf` bytes each).
+struct BandLayout {
+  int acc, list, cnt, gbuf, total;
+};
+
+BandLayout band_layout(int rows, int w, int dim, int vbytes, int cap, int gbuf) {
+  BandLayout b;
+  const int64_t row = static_cast<int64_t>(w) * dim;
+  int64_t o = align16(row * (rows + 1) * vbytes);
+  b.acc = static_cast<int>(o);
+  o += align16((row * rows + 2 * dim) * 8);  // the band's cells and a guard cell on each side
+  b.list = static_cast<int>(o);
+  o += align16(static_cast<int64_t>(cap) * 4);
+  b.cnt = static_cast<int>(o);
+  o += 16;
+  b.gbuf = gbuf > 0 ? static_cast<int>(o) : -1;
+  o += 2 * static_cast<int64_t>(gbuf);
+  b.total = o > (int64_t{1} << 30) ? (1 << 30) : static_cast<int>(o);
+  return b;
+}
+
+struct BandPlan {
+  int ch, lps_shift, threads, qpass, cap, lds, nwork;
+  int nqb, qblock;  // query blocks per (slice, item); nqb > 1 needs the partial-sum workspace
+  int rows[msda::kMaxLevels], bands[msda::kMaxLevels];
+  BandLayout layout;  // every workgroup gets the largest level's layout
+};
+
+// Bytes of the backward's workspace for a plan: the query blocks' partial grad_value sums.
+int64_t band_workspace(const Shape& s, const BandPlan& bp) {
+  return bp.nqb > 1 ? align16(static_cast<int64_t>(bp.nqb) * s.batch * s.heads * s.len_value * s.dim * 4) : 0;
+}
+
+// Two kinds of plan.
+// * Every level fits the LDS whole (its value rows and f64 accumulator): one band per level, and the
+//   slice's queries are split into blocks until the grid fills the CUs (as many workgroups per CU as
+//   the LDS holds). Blocks write partial grad_value sums that a second kernel adds in block order.
+//   This depends on the shape and the device only (so does the workspace size).
+// * Otherwise every level is cut into bands of whole image rows that fit the LDS share of `per_cu`
+//   workgroups per CU; then bands are added, to the level with the fewest (each level holds the same
+//   number of samples, Q * P per slice), until the grid has `per_cu` workgroups per CU. Each band
+//   scans its level's locations and lists the queries with a point in it (at most `qpass` queries
+//   per pass).
+// Workgroup size: up to 1024 threads per CU in all (the kernel's register budget allows 16 waves).
+int plan_band(const Shape& s, int vbytes, int ch, const DevInfo& dev, BandPlan* bp) {
+  bp->ch = ch;
+  bp->lps_shift = lpq_shift_for(s.dim, ch);
+  const int lps = 1 << bp->lps_shift;
+  const int64_t N = static_cast<int64_t>(s.batch) * s.heads;
+  // whole levels
+  int whole_lds = 0;
+  bool all_whole = true;
+  for (int l = 0; l < s.levels; ++l) {
+    const BandLayout lay = band_layout(s.h[l], s.w[l], s.dim, vbytes, 0, 0);
+    whole_lds = std::max(whole_lds, lay.total);
+    if (lay.total > dev.lds_bytes) all_whole = false;
+  }
+  int per_cu;
+  if (all_whole && env_int("MSDA_BWD_FORCE_BANDS", 0) == 0) {
+    per_cu = std::max(1, dev.lds_bytes / whole_lds);
+    bp->cap = 0;
+    bp->qpass = std::max(1, s.queries);
+    for (int l = 0; l < s.levels; ++l) bp->bands[l] = 1;
+    const int64_t units = N * s.levels;
+    int nqb = static_cast<int>(std::max<int64_t>(1, (static_cast<int64_t>(per_cu) * dev.cus + units - 1) / units));
+    nqb = std::min(nqb, std::max(1, s.queries / 256));  // blocks of at least 256 queries
+    bp->nqb = std::max(1, nqb);
+  } else {
+    per_cu = std::max(1, env_int("MSDA_BWD_WGS_PER_CU", 2));
+    bp->nqb = 1;
+    // the query list: one 32-bit entry per query of a pass, the query offset in 16 bits
+    const int max_cap = std::max(64, std::min(8192, env_int("MSDA_BWD_LIST", 8192)));
+    bp->qpass = std::max(1, std::min(s.queries, max_cap));
+    bp->cap = bp->qpass;
+    const int budget = dev.lds_bytes / per_cu - 512;
+    int64_t nb_total = 0;
+    for (int l = 0; l < s.levels; ++l) {
+      int rows = s.h[l];
+      while (rows > 1 && band_layout(rows, s.w[l], s.dim, vbytes, bp->cap, 0).total > budget) --rows;
+      if (band_layout(rows, s.w[l], s.dim, vbytes, bp->cap, 0).total > dev.lds_bytes)
+        return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], s.dim);
+      bp->bands[l] = (s.h[l] + rows - 1) / rows;
+      nb_total += bp->bands[l];
+    }
+    const int forced = env_int("MSDA_BWD_BANDS", 0);
+    const int64_t target = std::max(1, env_int("MSDA_BWD_TARGET_WGS", per_cu * dev.cus));
+    if (forced > 0) {
+      for (int l = 0; l < s.levels; ++l) bp->bands[l] = std::max(bp->bands[l], std::min(forced, s.h[l]));
+    } else {
+      while (N * nb_total < target) {
+        int best = -1;
+        for (int l = 0; l < s.levels; ++l)
+          if (bp->bands[l] < s.h[l] && (best < 0 || bp->bands[l] < bp->bands[best])) best = l;
+        if (best < 0) break;
+        ++bp->bands[best];
+        ++nb_total;
+      }
+    }
+  }
+  bp->qblock = std::max(1, (s.queries + bp->nqb - 1) / bp->nqb);
+  int threads = env_int("MSDA_BWD_THREADS", 0);
+  if (threads <= 0) threads = std::min(1024 / per_cu, std::max(256, ((std::min(s.queries, bp->qblock) * lps + 63) / 64) * 64));
+  threads = std::max(64, std::min(msda::kBandMaxThreads, (threads / 64) * 64));
+  if (lps > threads) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large", s.dim);
+  bp->threads = threads;
+  // one layout for all levels: the list after the largest value and accumulator regions
+  int vmax = 0, amax = 0;
+  bp->nwork = 0;
+  for (int l = 0; l < s.levels; ++l) {
+    bp->rows[l] = (s.h[l] + bp->bands[l] - 1) / bp->bands[l];
+    bp->bands[l] = (s.h[l] + bp->rows[l] - 1) / bp->rows[l];
+    bp->nwork += bp->bands[l];
+    const int64_t row = static_cast<int64_t>(s.w[l]) * s.dim;
+    vmax = std::max(vmax, align16(row * std::min(bp->rows[l] + 1, s.h[l]) * vbytes));
+    amax = std::max(amax, align16((row * bp->rows[l] + 2 * s.dim) * 8));
+  }
+  bp->layout.acc = vmax;
+  bp->layout.list = vmax + amax;
+  bp->layout.cnt = bp->layout.list + align16(static_cast<int64_t>(bp->cap) * 4);
+  bp->layout.gbuf = -1;
+  bp->layout.total = bp->layout.cnt + 16;
+  bp->lds = bp->layout.total;
+  if (bp->lds > dev.lds_bytes) return fail(MSDA_ERR_UNSUPPORTED, "backward needs %d bytes of LDS", bp->lds);
+  if (N * bp->nwork * bp->nqb > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
+  return MSDA_OK;
+}
+
+int bwd_band_impl(const Shape& s, int ch, const void* value, int value_dtype, const float* loc, const float* attn,
+                  const void* grad_output, int grad_output_dtype, void* grad_value, float* grad_loc, float* grad_attn, void* workspace,
+                  int64_t workspace_bytes, const DevInfo& dev, hipStream_t st) {
+  const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
+  BandPlan bp;
+  int rc = plan_band(s, vbytes, ch, dev, &bp);
+  if (rc != MSDA_OK) return rc;
+  const bool partial = bp.nqb > 1 && grad_value != nullptr;
+  if (partial) {
+    const int64_t need = band_workspace(s, bp);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace of %lld bytes needed, got %lld (see the workspace size query)",
+                  static_cast<long long>(need), static_cast<long long>(workspace == nullptr ? 0 : workspace_bytes));
+    if (!aligned(workspace, 16)) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  }
+  msda::BandParams p{};
+  p.value = value;
+  p.loc = loc;
+  p.attn = attn;
+  p.gout = grad_output;
+  p.gout_bf16 = grad_output_dtype == MSDA_DTYPE_BF16;
+  p.dvalue = grad_value;
+  p.dloc = grad_loc;
+  p.dattn = grad_attn;
+  p.heads = s.heads;
+  p.dim = s.dim;
+  p.queries = s.queries;
+  p.levels = s.levels;
+  p.points = s.points;
+  p.len_value = s.len_value;
+  p.nwork = bp.nwork;
+  p.nqb = bp.nqb;
+  p.qblock = bp.qblock;
+  p.part = partial ? static_cast<float*>(workspace) : nullptr;
+  p.part_stride = static_cast<int64_t>(s.batch) * s.heads * s.len_value * s.dim;
+  p.qpass = bp.qpass;
+  p.lps_shift = bp.lps_shift;
+  p.vec16 = rows_16b(s, vbytes, value, grad_value) ? 1 : 0;
+  p.lds_acc = bp.layout.acc + s.dim * 8;  // after the leading guard cell
+  p.lds_list = bp.layout.list;
+  p.lds_cnt = bp.layout.cnt;
+  int first = 0;
+  for (int l = 0; l < s.levels; ++l) {
+    p.lv[l] = level_desc(s, l, 0, bp.rows[l], first);
+    first += bp.bands[l];
+  }
+  const int grid = static_cast<int>(static_cast<int64_t>(s.batch) * s.heads * bp.nwork * p.nqb);
+  rc = value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_bwd_band<msda::bf16_t>(ch, p, grid, bp.threads, bp.lds, st)
+                                      : msda_host::dispatch_bwd_band<float>(ch, p, grid, bp.threads, bp.lds, st);
+  if (rc != MSDA_OK || !partial) return rc;
+  const int64_t quads = (p.part_stride + 3) / 4;
+  const int sgrid = static_cast<int>((quads + 255) / 256);
+  return value_dtype == MSDA_DTYPE_BF16 ? msda_host::launch_part_sum<msda::bf16_t>(p.part, p.nqb, p.part_stride, grad_value, sgrid, st)
+                                        : msda_host::launch_part_sum<float>(p.part, p.nqb, p.part_stride, grad_value, sgrid, st);
+}
+
+
 }  // namespace
 
 namespace msda_host {
 bool env_flag(const char* name) { return env_int(name, 0) != 0; }
+int knob(const char* name, int dflt) { return env_int(name, dflt); }
 
 int device_attrs(int* lds_bytes, int* cus) {
   DevInfo d;
@@ -508,9 +714,20 @@ int64_t workspace_impl(int batch, int n_heads, int head_dim, int len_query, int 
   if (batch == 0 || len_query == 0) return 0;
   DevInfo dev;
   if ((rc = device_info(&dev)) != MSDA_OK) return rc;
+  if (ref_dim == 0) {
+    // the query blocks' partial sums; the plan depends on the value dtype, which the query does not
+    // name, so the larger of the two
+    int64_t need = 0;
+    for (int vbytes : {2, 4}) {
+      BandPlan bp;
+      if ((rc = plan_band(s, vbytes, 16, dev, &bp)) != MSDA_OK) return rc;
+      need = std::max(need, band_workspace(s, bp));
+    }
+    return need;
+  }
   BinPlan bp;
   if ((rc = plan_bins(s, dev, &bp)) != MSDA_OK) return rc;
-  return bp.total_bytes + (ref_dim ? ref_part_bytes(s, ref_dim) : 0);
+  return bp.total_bytes + ref_part_bytes(s, ref_dim);
 }
 
 int bwd_impl(const void* value, int value_dtype, const float* loc, const float* attn, const void* grad_output, int grad_output_dtype,
@@ -538,6 +755,25 @@ int bwd_impl(const void* value, int value_dtype, const float* loc, const float* 
   if (!aligned(value, vbytes) || !aligned(grad_value, vbytes) || !aligned(grad_output, gbytes))
     return fail(MSDA_ERR_INVALID_ARGUMENT, "value/grad_value/grad_output not aligned to their element size");
   const bool want_dv = grad_value != nullptr;
+  if (fz == nullptr) {
+    // the core's backward is one kernel and needs no workspace
+    for (int l = 0; l < n_levels; ++l)
+      if (s.h[l] > 32000 || s.w[l] > 32000)
+        return fail(MSDA_ERR_UNSUPPORTED, "level %d (%d x %d) exceeds 32000 rows or columns", l, s.h[l], s.w[l]);
+    if (static_cast<int64_t>(len_query) * n_heads * head_dim >= (int64_t{1} << 30))
+      return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * head_dim reaches 2^30");
+    // a workgroup addresses one batch entry's sample rows with 32-bit offsets (24-bit multiplies)
+    if (static_cast<int64_t>(len_query) * n_heads * n_levels * n_points >= (int64_t{1} << 24) ||
+        static_cast<int64_t>(n_heads) * head_dim * 4 >= (int64_t{1} << 24))
+      return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * n_levels * n_points reaches 2^24");
+    const int gb = grad_output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
+    const int ch = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 16), {{value, vbytes}, {grad_output, gb}});
+    if (lpq_shift_for(head_dim, ch) > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d)", head_dim, 64 * ch);
+    DevInfo dev;
+    if ((rc = device_info(&dev)) != MSDA_OK) return rc;
+    return bwd_band_impl(s, ch, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn,
+                         workspace, workspace_bytes, dev, static_cast<hipStream_t>(stream));
+  }
   if ((want_dv || want_dref) && len_query > 0) {
     if (workspace == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace is NULL (see the workspace size query)");
     if (!aligned(workspace, 16)) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
@@ -704,6 +940,20 @@ extern "C" {
 const char* msda_version(void) { return "msda-gfx950 0.3.0"; }
 
 const char* msda_last_error(void) { return g_last_error.c_str(); }
+
+int msda_set_tuning(const char* name, const char* value) {
+  g_last_error.clear();
+  if (name == nullptr || std::string(name).rfind("MSDA_", 0) != 0)
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "tuning knob names start with MSDA_");
+  std::lock_guard<std::mutex> lock(g_knob_mu);
+  if (value == nullptr) {
+    g_knob_set.erase(name);
+  } else {
+    const bool set = *value != 0;
+    g_knob_set[name] = std::make_pair(set, set ? std::atoi(value) : 0);
+  }
+  return MSDA_OK;
+}
 
 int msda_fwd(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
              void* output, int output_dtype, int batch, int n_heads, int head_dim, int len_query, int n_levels,

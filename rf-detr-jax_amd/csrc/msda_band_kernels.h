@@ -1,0 +1,526 @@
+// msda_band_kernels.h — gfx950 backward of the deformable-attention core in one kernel.
+//
+// The VJP of RF-DETR-JAX's gather sampler (src/rfdetr_jax/models/ops.py:64-134, :208-292; the
+// hand-written form of the same transpose is deform_pallas.py:97-120): for every sample
+// (b, q, h, l, p) with corner weights w_c and attention weight a,
+//   grad_value[cell_c] += w_c * a * g          (g = grad_output[b, q, h*D:(h+1)*D])
+//   D_c = <g, value[cell_c]>,  grad_attn = sum_c w_c D_c,
+//   grad_loc = a * (W, H) * (d/dix, d/diy) sum_c w_c D_c   (masks and floor have zero gradient).
+//
+// bwd_band_kernel: one workgroup per (slice n = b*H + h, item = (level l, band of image rows
+// [r0, r1))). The workgroup owns grad_value rows [r0, r1) of level l of slice n, so every
+// grad_value element has exactly one writer and nothing needs zeroing or a second pass.
+//  1. Stage the band's value rows plus one halo row below into LDS (the rows a corner dot of a
+//     sample whose floor row lies in the band can touch), zero an f64 accumulator for the band.
+//  2. Scan: the threads read the locations of all queries (a pass holds as many queries as the
+//     list can hold samples of; one pass at the usual shapes) at level l, several queries' loads in
+//     flight per thread, and append the samples whose clipped corner rows meet the band to an LDS
+//     list (wave ballot compaction), so the second phase runs on full waves.
+//  3. One lane per sample (one lane per 16 channels for head_dim > 16): the band that holds the
+//     sample's clipped floor row computes the corner dots from the staged rows and writes
+//     grad_attention_weights and grad_sampling_locations; every band the sample's corner rows
+//     meet adds a*w_c*g for its corners into the accumulator with ds_add_f64 (exact products of
+//     f32 values, summed in f64).
+//  4. Round the accumulator once to the value dtype and write the band's grad_value rows.
+//
+// Measured on MI355X (per CU, 64-lane instructions): ds_add_f64 ~9.3 cycles and ds_add_u64
+// ~7.2 when the 64 lanes hit 64 distinct 8-byte bank pairs, but ds_add_f32 ~189 cycles (also with
+// f32 denormals flushed) and ds_pk_add_f16 ~189. Lane i of a sample-lane layout therefore adds
+// channel (t + r_i) mod 16 in instruction t, r_i = i mod 16: the lanes of one instruction then
+// cover all 32 bank pairs of a 256-byte bank row twice (the same channel for every lane costs
+// 63.5 cycles, a rotation by 16-byte chunks only 32.8).
+#pragma once
+
+#include "msda_kernels.h"
+
+namespace msda {
+
+constexpr int kBandMaxThreads = 1024;
+
+struct BandParams {
+  const void* value;  // [B*H, S, D]
+  const float* loc;   // [B, Q, H, L, P, 2]
+  const float* attn;  // [B, Q, H, L*P]
+  const void* gout;   // [B, Q, H*D]
+  int gout_bf16;
+  void* dvalue;       // [B*H, S, D] in the value dtype, or null
+  float* dloc;        // as loc, or null
+  float* dattn;       // as attn, or null
+  int heads, dim, queries, levels, points;
+  int64_t len_value;
+  int nwork;       // (level, band) items per slice
+  int nqb;         // query blocks per (slice, item); with part, each block writes a partial sum
+  int qblock;      // queries per block
+  float* part;     // nqb > 1 and grad_value requested: partial grad_value sums [nqb][B*H][S][D] (f32),
+                   // summed by bwd_part_sum_kernel; else null
+  int64_t part_stride;  // B * H * S * D
+  int qpass;       // queries scanned per pass (the list holds one entry per query)
+  int lps_shift;   // log2(lanes per sample)
+  int vec16;       // value rows and grad_value rows allow 16-byte accesses
+  int lds_acc;     // byte offset of the f64 accumulator's first cell in LDS (one guard cell precedes
+                   // it; the staged value rows start at 0)
+  int lds_list;    // byte offset of the query list (entries: query offset << 16 | point mask)
+  int lds_cnt;     // byte offset of the list counter
+  LevelDesc lv[kMaxLevels];  // band_rows, band_first per level
+};
+
+// Item k of a slice: level l (the last whose first item <= k) and band k - band_first.
+struct BandItem {
+  int l, r0, r1;
+};
+
+__device__ __forceinline__ BandItem band_item(const BandParams& p, int k) {
+  int l = 0;
+  while (l + 1 < p.levels && p.lv[l + 1].band_first <= k) ++l;
+  BandItem it;
+  it.l = l;
+  it.r0 = (k - p.lv[l].band_first) * p.lv[l].band_rows;
+  it.r1 = min(it.r0 + p.lv[l].band_rows, p.lv[l].h);
+  return it;
+}
+
+// The clipped rows of a sample's two corner rows (ops.py:103-118 clip y0 and y0 + 1 into the
+// level); a non-finite coordinate clamps to -2, i.e. both rows clip to 0, where bilinear() puts it.
+__device__ __forceinline__ int2 clipped_rows(float ly, const LevelDesc& L) {
+  const float iy = pixel_coord(ly, L.fh);
+  const int y0 = static_cast<int>(fminf(fmaxf(floorf(iy), -2.0f), L.fh));
+  return make_int2(min(max(y0, 0), L.h - 1), min(max(y0 + 1, 0), L.h - 1));
+}
+
+// Appends `entry` for the lanes with `flag` to an LDS list of 32-bit entries: one counter atomic
+// per wave.
+__device__ __forceinline__ void list_append32(bool flag, uint32_t entry, uint32_t* list, int* cnt) {
+  const uint64_t m = __ballot(flag);
+  if (m == 0) return;
+  const int lane = threadIdx.x & 63;
+  const int leader = __ffsll(static_cast<long long>(m)) - 1;
+  int base = 0;
+  if (lane == leader) base = atomicAdd(cnt, __popcll(m));
+  base = __shfl(base, leader, 64);
+  const uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
+  const int rank = static_cast<int>(__builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u)));
+  if (flag) list[base + rank] = entry;
+}
+
+// dst = (bit `lane` of mask) ? a : b. Written as the instruction itself: a C++ select between two
+// array elements is folded by the compiler into a load at a selected index, which after unrolling
+// becomes a dynamic register index (a 16-way select chain per element).
+__device__ __forceinline__ float lane_select(float a, float b, uint64_t mask) {
+  float r;
+  asm("v_cndmask_b32_e64 %0, %2, %1, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+  return r;
+}
+
+// x rotated down by b places (x[t] <- x[(t + b) mod N]), b < 2^STEPS: stage s rotates by 2^s in
+// the lanes whose bit s of b is set.
+template <int N, int STEPS>
+__device__ __forceinline__ void rotate_regs(float (&x)[N], int b) {
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int k = 1 << s;
+    const uint64_t on = __ballot((b >> s) & 1);
+    float y[N];
+#pragma unroll
+    for (int t = 0; t < N; ++t) y[t] = lane_select(x[(t + k) % N], x[t], on);
+#pragma unroll
+    for (int t = 0; t < N; ++t) x[t] = y[t];
+  }
+}
+
+__device__ __forceinline__ void lds_add_f64(uint32_t byte_addr, double v) {
+  __hip_atomic_fetch_add(reinterpret_cast<MSDA_LDS double*>(static_cast<uintptr_t>(byte_addr)), v, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// One lane's CH channels of one sample: D_c = <g, v_c> for the four corners, from the staged rows
+// (element offsets relative to the first staged row), summed in channel order (the same order on
+// every lane, so the result does not depend on which lane a sample lands on). Two corner rows in
+// flight at a time, one for 16-channel lanes (register budget).
+template <typename VT, int CH>
+__device__ __forceinline__ float row_dot(const VT* row, const float (&g)[CH]) {
+  float u[CH];
+  load_vec_lds<VT, CH>(row, u);
+  float d = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) d = fmaf(g[k], u[k], d);
+  return d;
+}
+
+template <typename VT, int CH>
+__device__ __forceinline__ void band_dots(const VT* rows, const Bilinear& c, int rel, const float (&g)[CH], float& d00, float& d10,
+                                          float& d01, float& d11) {
+  d00 = row_dot<VT, CH>(rows + (c.o00 - rel), g);
+  d10 = row_dot<VT, CH>(rows + (c.o10 - rel), g);
+  d01 = row_dot<VT, CH>(rows + (c.o01 - rel), g);
+  d11 = row_dot<VT, CH>(rows + (c.o11 - rel), g);
+}
+
+// The sample's grad_value contributions of the corners in rows [r0, r1): (a * w_c) * g, the
+// product formed exactly (f32 factors, f64 product) and added in f64, one atomic per channel.
+// `gr` holds the lane's channels rotated by `rr` places (gr[t] = channel (t + rr) mod CH), so
+// instruction t of the lanes of a wave adds distinct channel slots. KD: head_dim when known at
+// compile time (the accumulator cell size is then an immediate offset), else 0.
+// Fast path (finite weights and grad_output): a row with both weights zero is skipped; otherwise
+// both of its corners are added, at cells x0 and x0 + 1 of the accumulator row (a masked corner's
+// weight is exactly 0, so it adds +0.0; the accumulator has one guard cell before its first and
+// after its last cell, for x0 = -1 on the first row and x0 + 1 = W on the last). Otherwise every
+// corner is added at its clipped cell, as the reference's scatter-add of w * (a * g) does (a NaN
+// location gives NaN weights; an infinite grad_output times a masked weight gives NaN).
+template <int CH, int KD>
+__device__ __forceinline__ void band_scatter(uint32_t acc, int W, int H, int D, int r0, int r1, const Bilinear& c, float a,
+                                             const float (&gr)[CH], int rr, int j, bool fast) {
+  const uint32_t cell = static_cast<uint32_t>(KD > 0 ? KD : D) * 8u;  // bytes per accumulator cell
+  const uint32_t lane_ch = static_cast<uint32_t>(j * CH) * 8u;          // this lane's channel group
+  const double ad = static_cast<double>(a);
+  const double aw[4] = {ad * c.w00, ad * c.w10, ad * c.w01, ad * c.w11};
+  if (fast) {
+#pragma unroll
+    for (int dy = 0; dy < 2; ++dy) {
+      const int y = c.y0 + dy;
+      const double wl = aw[2 * dy], wr = aw[2 * dy + 1];
+      if (y < r0 || y >= r1 || (wl == 0.0 && wr == 0.0)) continue;
+      // -1 <= x0 <= W - 1 here (an unmasked corner); the base is formed modulo 2^32
+      const uint32_t base = acc + static_cast<uint32_t>((y - r0) * W + c.x0) * cell + lane_ch;
+#pragma unroll
+      for (int t = 0; t < CH; ++t) {
+        const uint32_t o = base + static_cast<uint32_t>((t + rr) & (CH - 1)) * 8u;
+        const double gt = static_cast<double>(gr[t]);
+        lds_add_f64(o, wl * gt);
+        lds_add_f64(o + cell, wr * gt);
+      }
+    }
+    return;
+  }
+  const int ry[2] = {c.cy0, min(max(c.y0 + 1, 0), H - 1)};
+  const int rx[2] = {c.cx0, min(max(c.x0 + 1, 0), W - 1)};
+#pragma unroll 1
+  for (int k = 0; k < 4; ++k) {
+    const int y = ry[k >> 1];
+    if (y < r0 || y >= r1) continue;
+    const uint32_t base = acc + static_cast<uint32_t>((y - r0) * W + rx[k & 1]) * cell + lane_ch;
+#pragma unroll
+    for (int t = 0; t < CH; ++t)
+      lds_add_f64(base + static_cast<uint32_t>((t + rr) & (CH - 1)) * 8u, aw[k] * static_cast<double>(gr[t]));
+  }
+}
+
+// Per-workgroup views of the [B, Q, H, ...] tensors at (b, q = 0, h) and level l: sample (q, pt)
+// of the workgroup is element q * qstride + pt, addressed with 32-bit offsets (the host bounds
+// Q * H * L * P and Q * H * D).
+template <typename GT>
+struct BandViews {
+  const float2* loc;
+  const float* attn;
+  float2* dloc;
+  float* dattn;
+  const GT* gout;    // this lane's first channel of row (b, 0, h)
+  uint32_t qstride;  // H * L * P
+  uint32_t gstride;  // H * D (grad_output elements between queries)
+};
+
+// Value rows in LDS (VT) and grad_output rows in global memory (GT), CH channels, channel order.
+template <typename GT, int CH>
+__device__ __forceinline__ void load_g(const GT* row, float (&g)[CH]) {
+  load_vec<GT, CH>(row, g);
+}
+
+// A query's P points at level l: locations (P * 8 bytes) and weights (P * 4 bytes) are contiguous,
+// so two or four points load as one vector each when aligned.
+template <int PB>
+__device__ __forceinline__ void load_points(const float2* loc, const float* attn, uint32_t si0, int p0, int P, uint32_t pmask,
+                                            float2 (&xy)[PB], float (&a)[PB]) {
+  if constexpr (PB == 2) {
+    if (P == 2 && (si0 & 1u) == 0 && p0 == 0) {
+      const float4 l4 = *reinterpret_cast<const float4*>(at(loc, si0));
+      const float2 a2 = *reinterpret_cast<const float2*>(at(attn, si0));
+      xy[0] = make_float2(l4.x, l4.y);
+      xy[1] = make_float2(l4.z, l4.w);
+      a[0] = a2.x;
+      a[1] = a2.y;
+      return;
+    }
+  } else if constexpr (PB == 4) {
+    if (P == 4 && (si0 & 3u) == 0 && p0 == 0) {
+      const float4 l0 = *reinterpret_cast<const float4*>(at(loc, si0));
+      const float4 l1 = *reinterpret_cast<const float4*>(at(loc, si0 + 2));
+      const float4 a4 = *reinterpret_cast<const float4*>(at(attn, si0));
+      xy[0] = make_float2(l0.x, l0.y);
+      xy[1] = make_float2(l0.z, l0.w);
+      xy[2] = make_float2(l1.x, l1.y);
+      xy[3] = make_float2(l1.z, l1.w);
+      a[0] = a4.x;
+      a[1] = a4.y;
+      a[2] = a4.z;
+      a[3] = a4.w;
+      return;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PB; ++i) {
+    if (p0 + i < P && ((pmask >> ((p0 + i) & 31)) & 1)) {
+      xy[i] = *at(loc, si0 + p0 + i);
+      a[i] = *at(attn, si0 + p0 + i);
+    }
+  }
+}
+
+// VT: value dtype, GT: grad_output dtype, CH: channels per lane, KD: head_dim when it is 16 or 32
+// and a multiple of CH (every lane then has channels), else 0.
+// Work item: (batch b, level-band item, query block, head h), batch-major. A band that is a whole
+// level takes every sample of its query block directly (lanes walk the queries in order); a level
+// cut into bands is scanned first, and the queries with a point in the band are listed.
+template <typename VT, typename GT, int CH, int KD>
+__global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandParams p) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int nt = blockDim.x, tid = threadIdx.x;
+  const int lid = xcd_logical(blockIdx.x, gridDim.x);
+  // batch-major logical order: the workgroups of one batch entry (which share its location,
+  // weight and grad_output rows) run on one XCD
+  const int per_b = p.heads * p.nwork * p.nqb;
+  const int b = lid / per_b;
+  int rest = lid - b * per_b;
+  const int item = rest / (p.heads * p.nqb);
+  rest -= item * p.heads * p.nqb;
+  const int qb = rest / p.heads;
+  const int h = rest - qb * p.heads;
+  const BandItem bi = band_item(p, item);
+  const LevelDesc L = p.lv[bi.l];
+  const int W = L.w, D = KD > 0 ? KD : p.dim, Q = p.queries, P = p.points, LP = p.levels * p.points;
+  const int r0 = bi.r0, r1 = bi.r1, rv1 = min(r1 + 1, L.h);  // owned rows, staged rows
+  const bool whole = r0 == 0 && r1 == L.h;                    // the band is the whole level
+  const int q_lo = qb * p.qblock, q_hi = min(Q, q_lo + p.qblock);
+  const int64_t n = static_cast<int64_t>(b) * p.heads + h;
+  const int64_t slice = p.len_value * D;
+  VT* vrows = reinterpret_cast<VT*>(lds_raw);
+  // LDS byte address of the accumulator (an address-space cast, not the generic pointer's bits)
+  const uint32_t acc = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((MSDA_LDS unsigned char*)(lds_raw + p.lds_acc)));
+  double* accp = reinterpret_cast<double*>(lds_raw + p.lds_acc);
+  uint32_t* list = reinterpret_cast<uint32_t*>(lds_raw + p.lds_list);
+  int* cnt = reinterpret_cast<int*>(lds_raw + p.lds_cnt);
+  const bool want_dv = p.dvalue != nullptr;
+  const bool want_dots = p.dloc != nullptr || p.dattn != nullptr;
+  const int owned_elems = (r1 - r0) * W * D;
+
+  // 1. staging (issued here, waited for before the barrier that precedes its use) and accumulator
+  if (tid == 0) cnt[0] = 0;
+  if (!whole) __syncthreads();  // the counter, before any append
+  if (want_dots)
+    stage_copy<VT, false>(vrows, static_cast<const VT*>(p.value) + n * slice + static_cast<int64_t>(L.start + r0 * W) * D,
+                          (rv1 - r0) * W * D, p.vec16 != 0);
+  if (want_dv)  // the band's cells and the guard cell on each side
+    for (int i = tid; i < owned_elems + 2 * D; i += nt) accp[i - D] = 0.0;
+
+  // lane layout of the query phase
+  const int lps = KD > 0 ? KD / CH : 1 << p.lps_shift;
+  const int j = tid & (lps - 1);  // channel group of the lane
+  const int sl = tid / lps;       // query slot
+  const bool lane_on = KD > 0 || j * CH < D;
+  const int c0 = lane_on ? j * CH : 0;
+  const int rr = sl & (CH - 1);   // channel rotation of the lane's f64 adds
+  const int rel = r0 * W * D;     // level element offset of the first staged row
+  const bool all_points = whole || P > 16;  // otherwise list entries carry a point mask
+
+  BandViews<GT> vw;
+  {
+    const int64_t row0 = static_cast<int64_t>(b) * Q * p.heads + h;  // row (b, 0, h)
+    const int64_t s0 = row0 * LP + bi.l * P;
+    vw.loc = reinterpret_cast<const float2*>(p.loc) + s0;
+    vw.attn = p.attn + s0;
+    vw.dloc = p.dloc ? reinterpret_cast<float2*>(p.dloc) + s0 : nullptr;
+    vw.dattn = p.dattn ? p.dattn + s0 : nullptr;
+    vw.gout = static_cast<const GT*>(p.gout) + row0 * D + c0;
+    vw.qstride = static_cast<uint32_t>(p.heads * LP);
+    vw.gstride = static_cast<uint32_t>(p.heads * D);
+  }
+
+  // One query: its grad_output row (one read) and its locations and weights at level l serve all of
+  // its points in `pmask`; the band holding a point's clipped floor row writes its gradients of the
+  // location and weight, every band its rows meet adds its grad_value terms.
+  auto do_query = [&](uint32_t q, uint32_t pmask) {
+    const uint32_t si0 = __umul24(q, vw.qstride);
+    float g[CH];
+    if (lane_on) {
+      load_g<GT, CH>(vw.gout + __umul24(q, vw.gstride), g);
+    } else {
+#pragma unroll
+      for (int t = 0; t < CH; ++t) g[t] = 0.0f;
+    }
+    // grad_output rotated for the grad_value adds: gr[t] = channel (t + rr) mod CH
+    float gr[CH];
+    bool gfin = true;
+    if (want_dv) {
+      float z = 0.0f;  // any infinite or NaN channel makes z NaN (inf * 0)
+#pragma unroll
+      for (int t = 0; t < CH; ++t) {
+        gr[t] = g[t];
+        z = fmaf(g[t], 0.0f, z);
+      }
+      gfin = z == 0.0f;
+      rotate_regs<CH, (CH >= 16 ? 4 : CH >= 8 ? 3 : CH >= 4 ? 2 : CH >= 2 ? 1 : 0)>(gr, rr);
+    }
+    // points whose inputs are loaded together (fewer for 16-channel lanes: register budget)
+    constexpr int PB = CH >= 16 ? 2 : 4;
+    for (int p0 = 0; p0 < P; p0 += PB) {
+      float2 xy[PB];
+      float a[PB];
+      load_points<PB>(vw.loc, vw.attn, si0, p0, P, pmask, xy, a);
+#pragma unroll
+      for (int i = 0; i < PB; ++i) {
+        if (!(p0 + i < P && ((pmask >> ((p0 + i) & 31)) & 1))) continue;
+        const uint32_t si = si0 + p0 + i;
+        const Bilinear c = bilinear(xy[i].x, xy[i].y, L, D);
+        if (want_dots && c.cy0 >= r0 && c.cy0 < r1) {
+          float d00, d10, d01, d11;
+          band_dots<VT, CH>(vrows + c0, c, rel, g, d00, d10, d01, d11);
+          for (int o = 1; o < lps; o <<= 1) {
+            d00 += __shfl_xor(d00, o, 64);
+            d10 += __shfl_xor(d10, o, 64);
+            d01 += __shfl_xor(d01, o, 64);
+            d11 += __shfl_xor(d11, o, 64);
+          }
+          if (j == 0) {
+            if (vw.dattn) *at(vw.dattn, si) = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
+            if (vw.dloc) {
+              const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
+              const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
+              const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
+              // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
+              *at(vw.dloc, si) = make_float2(a[i] * L.fw * dx, a[i] * L.fh * dy);
+            }
+          }
+        }
+        if (want_dv && lane_on) {
+          const bool fast = gfin && isfinite(a[i]) && isfinite(c.fx) && isfinite(c.fy);
+          band_scatter<CH, KD>(acc, W, L.h, D, r0, r1, c, a[i], gr, rr, j, fast);
+        }
+      }
+    }
+  };
+
+  // Work is handed out a wave at a time from an LDS counter (one atomic per wave and chunk of 64 /
+  // lps queries), so waves that run ahead take more and the workgroup ends within one chunk.
+  const int lane = tid & 63;
+  const int qpw = 64 / lps;  // queries per wave chunk
+  auto grab = [&](int* counter) {
+    int base = 0;
+    if (lane == 0) base = atomicAdd(counter, qpw);
+    return __shfl(base, 0, 64) + lane / lps;
+  };
+  if (whole) {
+    // 2'. every sample of the block belongs to this workgroup: waves take chunks of its queries
+    if (tid == 0) cnt[1] = 0;
+    wait_vmem();  // this wave's staging transfers, before the barrier publishes them
+    __syncthreads();
+    const int qcount = q_hi - q_lo;
+    for (int e = grab(&cnt[1]); __shfl(e, 0, 64) < qcount; e = grab(&cnt[1]))
+      if (e < qcount) do_query(static_cast<uint32_t>(q_lo + e), 0xffffffffu);
+  } else {
+    for (int q0 = q_lo; q0 < q_hi; q0 += p.qpass) {
+      const int qn = min(p.qpass, q_hi - q0);
+      if (q0 > q_lo) {
+        __syncthreads();  // the previous pass's list is consumed
+        if (tid == 0) cnt[0] = 0;
+        __syncthreads();
+      }
+      // 2. scan: one query per thread; its P locations at level l, four at a time. A query is
+      //    listed when any of its points meets the band, with the mask of those points.
+      for (int qq = 0; qq < qn; qq += nt) {
+        const int qo = qq + tid;
+        const bool qv = qo < qn;
+        const float2* lq = at(vw.loc, __umul24(static_cast<uint32_t>(q0 + (qv ? qo : 0)), vw.qstride));
+        uint32_t mask = 0;
+        for (int p0 = 0; p0 < P; p0 += 4) {
+          float ly[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (qv && p0 + i < P) ly[i] = lq[p0 + i].y;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (qv && p0 + i < P) {
+              const int2 ry = clipped_rows(ly[i], L);
+              if ((ry.x >= r0 && ry.x < r1) || (ry.y >= r0 && ry.y < r1)) mask |= 1u << ((p0 + i) & 15);
+            }
+          }
+        }
+        if (qv && all_points && mask) mask = 0xffffu;
+        list_append32(mask != 0, (static_cast<uint32_t>(qo) << 16) | mask, list, cnt);
+      }
+      if (tid == 0) cnt[1] = 0;
+      wait_vmem();  // this wave's staging transfers, before the barrier publishes them
+      __syncthreads();
+      // 3. one lane per listed query (lps lanes for wide heads), no barrier: waves drift apart, so
+      //    the VALU-heavy and the LDS-atomic-heavy parts of different waves overlap
+      const int nlist = cnt[0];
+      for (int e = grab(&cnt[1]); __shfl(e, 0, 64) < nlist; e = grab(&cnt[1])) {
+        if (e < nlist) {
+          const uint32_t ent = list[e];
+          do_query(static_cast<uint32_t>(q0) + (ent >> 16), all_points ? 0xffffffffu : (ent & 0xffffu));
+        }
+      }
+    }
+  }
+  if (!want_dv) return;
+  __syncthreads();
+  // 4. the band's grad_value rows, rounded once to the value dtype, or this query block's partial
+  //    sums (f32) when the slice's queries are split over several workgroups
+  const int64_t row_off = n * slice + static_cast<int64_t>(L.start + r0 * W) * D;
+  if (p.part != nullptr) {
+    float* __restrict__ dst = p.part + static_cast<int64_t>(qb) * p.part_stride + row_off;
+    if (p.vec16) {
+      for (int i = tid * 4; i < owned_elems; i += nt * 4)
+        *reinterpret_cast<float4*>(dst + i) = make_float4(static_cast<float>(accp[i]), static_cast<float>(accp[i + 1]),
+                                                          static_cast<float>(accp[i + 2]), static_cast<float>(accp[i + 3]));
+    } else {
+      for (int i = tid; i < owned_elems; i += nt) dst[i] = static_cast<float>(accp[i]);
+    }
+    return;
+  }
+  VT* __restrict__ dv = static_cast<VT*>(p.dvalue) + row_off;
+  if (p.vec16) {
+    constexpr int E = 16 / sizeof(VT);
+    for (int i = tid * E; i < owned_elems; i += nt * E) {
+      float f[E];
+#pragma unroll
+      for (int e2 = 0; e2 < E; ++e2) f[e2] = static_cast<float>(accp[i + e2]);
+      store_vec<VT, E>(dv + i, f);
+    }
+  } else {
+    for (int i = tid; i < owned_elems; i += nt) {
+      float f[1] = {static_cast<float>(accp[i])};
+      store_vec<VT, 1>(dv + i, f);
+    }
+  }
+}
+
+// grad_value = the sum of the query blocks' partial sums, in block order (deterministic), rounded
+// once to the value dtype. Four elements per thread.
+template <typename VT>
+__global__ void __launch_bounds__(256) bwd_part_sum_kernel(const float* __restrict__ part, int nqb, int64_t stride, VT* __restrict__ dv) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= stride) return;
+  if (i + 4 <= stride) {
+    float4 s = *reinterpret_cast<const float4*>(part + i);
+    for (int k = 1; k < nqb; ++k) {
+      const float4 t = *reinterpret_cast<const float4*>(part + k * stride + i);
+      s.x += t.x;
+      s.y += t.y;
+      s.z += t.z;
+      s.w += t.w;
+    }
+    float f[4] = {s.x, s.y, s.z, s.w};
+    if constexpr (std::is_same<VT, float>::value) {
+      *reinterpret_cast<float4*>(dv + i) = s;
+    } else {
+      for (int e = 0; e < 4; ++e) dv[i + e] = f32_to_bf16(f[e]);
+    }
+    return;
+  }
+  for (int64_t e = i; e < stride; ++e) {
+    float s = part[e];
+    for (int k = 1; k < nqb; ++k) s += part[k * stride + e];
+    if constexpr (std::is_same<VT, float>::value) dv[e] = s;
+    else dv[e] = f32_to_bf16(s);
+  }
+}
+
+}  // namespace msda

@@ -5,4 +5,6 @@
 namespace msda_host {
 template int dispatch_bwd_sample<msda::bf16_t>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
 template int dispatch_value<msda::bf16_t>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
+template int dispatch_bwd_band<msda::bf16_t>(int, const msda::BandParams&, int, int, int, hipStream_t);
+template int launch_part_sum<msda::bf16_t>(const float*, int, int64_t, void*, int, hipStream_t);
 }  // namespace msda_host

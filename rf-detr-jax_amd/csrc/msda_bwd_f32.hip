@@ -5,4 +5,6 @@
 namespace msda_host {
 template int dispatch_bwd_sample<float>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
 template int dispatch_value<float>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
+template int dispatch_bwd_band<float>(int, const msda::BandParams&, int, int, int, hipStream_t);
+template int launch_part_sum<float>(const float*, int, int64_t, void*, int, hipStream_t);
 }  // namespace msda_host

@@ -437,7 +437,8 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // wave's LDS base + 16 i, no registers involved), each wave streaming whole 1 KB blocks, so every
 // block is in flight at once; the wave waits for its own transfers before returning (the caller's
 // barrier then publishes them). Otherwise each thread issues a batch of loads before any store.
-template <typename VT>
+// kWait = false leaves the 16-byte path's transfers outstanding (the caller waits before its barrier).
+template <typename VT, bool kWait = true>
 __device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, int count, bool vec16) {
   constexpr int U = 8;
   const int nt = blockDim.x;
@@ -450,7 +451,7 @@ __device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, 
     for (int blk = wave; blk < nblk; blk += nwaves)
       __builtin_amdgcn_global_load_lds(s + blk * 64 + lane, (MSDA_LDS void*)(d + blk * 64), 16, 0, 0);
     for (int i = (nblk << 6) + static_cast<int>(threadIdx.x); i < n16; i += nt) d[i] = s[i];
-    wait_vmem();
+    if constexpr (kWait) wait_vmem();
   } else {
     int i = threadIdx.x;
     for (; i + (U - 1) * nt < count; i += U * nt) {

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "msda.h"
+#include "msda_band_kernels.h"
 #include "msda_kernels.h"
 
 #include <hip/hip_runtime.h>
@@ -20,7 +21,8 @@ void clear_error();                          // at the start of every C-ABI call
 int raise_lds_limit(const void* kernel, int bytes, std::atomic<int>* granted);
 int check_launch(const char* what);
 int device_attrs(int* lds_bytes, int* cus);  // of the current device, cached per device
-bool env_flag(const char* name);              // an environment switch set to a non-zero integer
+bool env_flag(const char* name);              // a tuning switch (MSDA_* knob) set to a non-zero integer
+int knob(const char* name, int dflt);         // a tuning knob's value, or dflt when unset
 
 inline bool aligned_to(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
@@ -59,6 +61,48 @@ int launch_bwd_value(const msda::ValueParams& p, int grid, int threads, int lds,
   if (rc != MSDA_OK) return rc;
   hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
   return check_launch("msda backward (grad_value pass)");
+}
+
+template <typename VT, typename GT, int CH, int KD>
+int launch_bwd_band(const msda::BandParams& p, int grid, int threads, int lds, hipStream_t stream) {
+  static std::atomic<int> granted[kMaxDevices];
+  auto k = msda::bwd_band_kernel<VT, GT, CH, KD>;
+  int rc = allow_lds(k, lds, granted);
+  if (rc != MSDA_OK) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
+  return check_launch("msda backward");
+}
+
+// Channels per lane of the backward kernel (16, 8, 4, 2 or 1); head_dim 16 and 32 with 8- or
+// 16-channel lanes have kernels that know head_dim at compile time.
+template <typename VT, typename GT>
+int dispatch_bwd_band_g(int ch, const msda::BandParams& p, int grid, int threads, int lds, hipStream_t st) {
+  switch (ch) {
+    case 1: return launch_bwd_band<VT, GT, 1, 0>(p, grid, threads, lds, st);
+    case 2: return launch_bwd_band<VT, GT, 2, 0>(p, grid, threads, lds, st);
+    case 4: return launch_bwd_band<VT, GT, 4, 0>(p, grid, threads, lds, st);
+    case 8:
+      if (p.dim == 16) return launch_bwd_band<VT, GT, 8, 16>(p, grid, threads, lds, st);
+      if (p.dim == 32) return launch_bwd_band<VT, GT, 8, 32>(p, grid, threads, lds, st);
+      return launch_bwd_band<VT, GT, 8, 0>(p, grid, threads, lds, st);
+    case 16:
+      if (p.dim == 16) return launch_bwd_band<VT, GT, 16, 16>(p, grid, threads, lds, st);
+      if (p.dim == 32) return launch_bwd_band<VT, GT, 16, 32>(p, grid, threads, lds, st);
+      return launch_bwd_band<VT, GT, 16, 0>(p, grid, threads, lds, st);
+  }
+  return fail(MSDA_ERR_UNSUPPORTED, "no backward kernel for %d channels per lane", ch);
+}
+
+template <typename VT>
+int launch_part_sum(const float* part, int nqb, int64_t stride, void* dv, int grid, hipStream_t st) {
+  hipLaunchKernelGGL(msda::bwd_part_sum_kernel<VT>, dim3(grid), dim3(256), 0, st, part, nqb, stride, static_cast<VT*>(dv));
+  return check_launch("msda backward (partial sums)");
+}
+
+template <typename VT>
+int dispatch_bwd_band(int ch, const msda::BandParams& p, int grid, int threads, int lds, hipStream_t st) {
+  return p.gout_bf16 ? dispatch_bwd_band_g<VT, msda::bf16_t>(ch, p, grid, threads, lds, st)
+                     : dispatch_bwd_band_g<VT, float>(ch, p, grid, threads, lds, st);
 }
 
 // Grouped-query forward kernels come in two forms: every level staged in LDS (no L2 gather path)
@@ -125,5 +169,9 @@ extern template int dispatch_bwd_sample<float>(int, int, bool, const msda::Sampl
 extern template int dispatch_bwd_sample<msda::bf16_t>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
 extern template int dispatch_value<float>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
 extern template int dispatch_value<msda::bf16_t>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
+extern template int dispatch_bwd_band<float>(int, const msda::BandParams&, int, int, int, hipStream_t);
+extern template int dispatch_bwd_band<msda::bf16_t>(int, const msda::BandParams&, int, int, int, hipStream_t);
+extern template int launch_part_sum<float>(const float*, int, int64_t, void*, int, hipStream_t);
+extern template int launch_part_sum<msda::bf16_t>(const float*, int, int64_t, void*, int, hipStream_t);
 
 }  // namespace msda_host

@@ -74,7 +74,8 @@ int launch_gemm(const msda::ValueProjParams& p, int64_t rows, int64_t cols, int 
     if ((rc = msda_host::device_attrs(&lds, &cus)) != MSDA_OK) return rc;
     const int64_t t64 = (rows + 63) / 64 * ct * splits;
     int bm = t64 < 4 * static_cast<int64_t>(cus) ? 32 : 64;
-    if (const char* e = std::getenv("MSDA_VP_BM")) bm = std::atoi(e) == 32 ? 32 : std::atoi(e) == 64 ? 64 : bm;
+    const int e = msda_host::knob("MSDA_VP_BM", 0);
+    bm = e == 32 ? 32 : e == 64 ? 64 : bm;
     if (bm == 32) rc = launch_g4<KIND, VT, 32>(p, static_cast<int>((rows + 31) / 32 * ct * splits), st);
     else rc = launch_g4<KIND, VT, 64>(p, static_cast<int>(t64), st);
     if (rc != MSDA_OK) return rc;

@@ -6,6 +6,7 @@ needs it fails loudly.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -30,6 +31,7 @@ _DIMS = [_I] * 6 + [_I32P, _I32P, _I64]  # batch .. n_points, spatial_shapes, le
 SIGNATURES = {
     "msda_version": ([], ctypes.c_char_p),
     "msda_last_error": ([], ctypes.c_char_p),
+    "msda_set_tuning": ([ctypes.c_char_p, ctypes.c_char_p], _I),
     "msda_fwd": ([_P, _I, _P, _P, _P, _I] + _DIMS + [_P], _I),
     "msda_bwd_workspace_size": (list(_DIMS), _I64),
     "msda_bwd": ([_P, _I, _P, _P, _P, _I, _P, _P, _P] + _DIMS + [_P, _I64, _P], _I),
@@ -91,3 +93,19 @@ def check(rc: int) -> None:
     if rc != OK:
         msg = lib().msda_last_error().decode("utf-8", "replace")
         raise MsdaError(rc, msg)
+
+
+@contextlib.contextmanager
+def tuning(knobs: dict):
+    """Override launch-tuning knobs (``{"MSDA_BWD_BANDS": 7, ...}``) for the duration of a block;
+    the library reads them from the environment only once, so this is how a process switches
+    launch variants (benchmarks, tests)."""
+    set_ = []
+    try:
+        for name, value in knobs.items():
+            check(lib().msda_set_tuning(name.encode(), str(value).encode()))
+            set_.append(name)
+        yield
+    finally:
+        for name in set_:
+            lib().msda_set_tuning(name.encode(), None)

@@ -18,3 +18,24 @@ for path in (ROOT, os.path.join(ROOT, "rf-detr-jax_amd")):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")
+
+
+import pytest  # noqa: E402
+
+
+@pytest.fixture
+def tune():
+    """``tune({"MSDA_BWD_BANDS": 7})`` overrides launch-tuning knobs of the HIP library until the
+    test ends (the library reads MSDA_* environment variables only once per process)."""
+    from rfdetr_jax_amd import _native
+
+    names = []
+
+    def set_(knobs):
+        for name, value in knobs.items():
+            _native.check(_native.lib().msda_set_tuning(name.encode(), str(value).encode()))
+            names.append(name)
+
+    yield set_
+    for name in names:
+        _native.lib().msda_set_tuning(name.encode(), None)

@@ -124,9 +124,9 @@ def test_fused_full_size_against_c_oracle(ref_dim):
     {"MSDA_BWDS_HEADS": "1"},           # one head per group: 16 partial sums per reference point
     {"MSDA_BWDS_HEADS": "2"},
 ], ids=lambda v: ",".join(f"{k}={x}" for k, x in v.items()))
-def test_fused_kernel_variants(monkeypatch, variant):
+def test_fused_kernel_variants(tune, variant):
     for k, x in variant.items():
-        monkeypatch.setenv(k, x)
+        tune({k: x})
     shapes = ((24, 24), (12, 12))
     _note(f"fused variant {variant}")
     value, ref, off, logits, grad = make_fused_inputs(11, 2, 16, 16, 250, shapes, 2, 4)

@@ -162,10 +162,10 @@ def test_mask_loss_shape_point_sample():
 
 
 @pytest.mark.parametrize("staged", [True, False], ids=["lds", "l2"])
-def test_forward_paths_agree(monkeypatch, staged):
+def test_forward_paths_agree(tune, staged):
     """Planes that fit in LDS are staged there; MSDA_GS_NO_LDS forces the L2 gather path."""
     if not staged:
-        monkeypatch.setenv("MSDA_GS_NO_LDS", "1")
+        tune({"MSDA_GS_NO_LDS": "1"})
     rng = np.random.default_rng(25)
     inputs = rng.standard_normal((20, 3, 40, 50)).astype(np.float32)
     pts = rng.uniform(-0.2, 1.2, (20, 700, 2)).astype(np.float32)

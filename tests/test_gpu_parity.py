@@ -197,11 +197,11 @@ def test_bf16_weights_give_bf16_output():
 # alternative kernel paths and edge cases
 
 
-def test_global_gather_path_and_many_bands(monkeypatch):
+def test_global_gather_path_and_many_bands(tune):
     """Forward without LDS staging (levels read through L2) and backward split into many bands."""
     g = load_golden("nano_small")
-    monkeypatch.setenv("MSDA_FWD_LDS_BUDGET", "0")
-    monkeypatch.setenv("MSDA_BWD_BANDS", "7")
+    tune({"MSDA_FWD_LDS_BUDGET": "0"})
+    tune({"MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_BANDS": "7"})
     out, (gv, gl, ga) = _run(g["value"], g["shapes"], g["loc"], g["attn"], g["grad"])
     assert_close(out, g["out"], 1e-5, "out")
     assert_close(gv, g["grad_value"], 1e-4, "grad_value")
@@ -209,25 +209,27 @@ def test_global_gather_path_and_many_bands(monkeypatch):
     assert_close(ga, g["grad_attn"], 1e-4, "grad_attn")
 
 
-@pytest.mark.parametrize("channels", [4, 8])
-@pytest.mark.parametrize("accumulators", [1, 4])
-@pytest.mark.parametrize("segments", [False, True])
-def test_grad_value_accumulator_modes_and_segments(monkeypatch, accumulators, segments, channels):
-    """grad_value with one band accumulator (colour passes) and with one per bilinear corner, with
-    4 and 8 channels per gather lane, with each workgroup's records in one list segment and in
-    several."""
-    monkeypatch.setenv("MSDA_BWD_ACCUMULATORS", str(accumulators))
-    monkeypatch.setenv("MSDA_BWD_VALUE_CG", str(channels))
-    if not segments:
-        shapes, batch, heads, queries = ((24, 24), (12, 12)), 2, 4, 700
-    elif accumulators == 1:
-        shapes, batch, heads, queries = ((24, 24), (12, 12)), 2, 4, 700
-        monkeypatch.setenv("MSDA_BWD_LIST", "256")
-    else:
-        # a long query axis puts several list capacities' worth of records in each band
-        shapes, batch, heads, queries = ((24, 24),), 1, 2, 12000
-    value, loc, attn, grad = make_inputs(77, batch, heads, 16, queries, shapes, 2)
-    _note(f"accumulators={accumulators} segments={segments} channels={channels} queries={queries}")
+@pytest.mark.parametrize("variant", [
+    {},                                                         # whole levels, queries split in blocks
+    {"MSDA_BWD_THREADS": "64"},                                 # one-wave workgroups
+    {"MSDA_BWD_FORCE_BANDS": "1"},                              # row bands, scanned and listed
+    {"MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_BANDS": "24"},      # one row per band: points straddle bands
+    {"MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_LIST": "64"},       # several list passes per band
+    {"MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_THREADS": "64"},
+    {"MSDA_BWD_MAX_VEC": "8"},                                  # two lanes per query
+    {"MSDA_BWD_MAX_VEC": "4"},                                  # four lanes per query
+    {"MSDA_BWD_MAX_VEC": "1"},                                  # one channel per lane
+], ids=lambda v: ",".join(f"{k}={x}" for k, x in v.items()) or "default")
+@pytest.mark.parametrize("queries", [700, 5000])
+def test_backward_launch_variants(tune, variant, queries):
+    """The backward kernel's launch shapes against the float64 oracle: whole levels with the
+    queries split in blocks (partial sums added by a second kernel), row bands from one per level to
+    one per image row with one or several list passes, workgroups of one to sixteen waves, and one to
+    sixteen lanes per query."""
+    tune(variant)
+    shapes = ((24, 24), (12, 12))
+    value, loc, attn, grad = make_inputs(77, 2, 4, 16, queries, shapes, 2)
+    _note(f"variant={variant} queries={queries}")
     out, (gv, gl, ga) = _run(value, shapes, loc, attn, grad)
     rv, rl, ra = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
     assert_close(gv, rv, 1e-4, "grad_value")
@@ -236,10 +238,10 @@ def test_grad_value_accumulator_modes_and_segments(monkeypatch, accumulators, se
 
 
 @pytest.mark.parametrize("pair", [0, 1])
-def test_forward_paired_lanes(monkeypatch, pair):
+def test_forward_paired_lanes(tune, pair):
     """One level, two points, 16 channels (two lanes of 8 per query-head): the forward with the
     two lanes splitting the samples' coordinate work (pair=1, the default) and without (pair=0)."""
-    monkeypatch.setenv("MSDA_FWD_PAIR", str(pair))
+    tune({"MSDA_FWD_PAIR": str(pair)})
     shapes = ((24, 24),)
     value, loc, attn, grad = make_inputs(91, 2, 8, 16, 1000, shapes, 2)
     _note(f"pair={pair}")
@@ -248,19 +250,18 @@ def test_forward_paired_lanes(monkeypatch, pair):
 
 
 @pytest.mark.parametrize("variant", [
-    {"MSDA_BWD_GROUPED": "1"},
     {"MSDA_FWD_GROUPED": "0"},
     {"MSDA_FWD_MAX_VEC": "16"},
     {"MSDA_BWD_MAX_VEC": "8"},
     {"MSDA_FWD_HEADS": "2", "MSDA_BWDS_HEADS": "2"},
 ], ids=lambda v: ",".join(f"{k}={x}" for k, x in v.items()))
 @pytest.mark.parametrize("shapes", [((24, 24),), ((24, 24), (12, 12))], ids=["one_level", "two_levels"])
-def test_kernel_variants(monkeypatch, variant, shapes):
+def test_kernel_variants(tune, variant, shapes):
     """The per-sample kernels' other launch variants (grouped query inputs in the backward, one
     query at a time in the forward, 16- and 8-channel lanes, two-head workgroups) against the
     float64 oracle."""
     for k, v in variant.items():
-        monkeypatch.setenv(k, v)
+        tune({k: v})
     value, loc, attn, grad = make_inputs(5, 2, 8, 16, 700, shapes, 2)
     _note(f"variant={variant} shapes={shapes}")
     out, (gv, gl, ga) = _run(value, shapes, loc, attn, grad)

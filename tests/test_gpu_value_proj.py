@@ -169,7 +169,7 @@ def test_msdeform_attn_module_against_torch_module(ref_dim):
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
-def test_vector_and_elementwise_kernels_agree(monkeypatch, bf16):
+def test_vector_and_elementwise_kernels_agree(tune, bf16):
     """The 16-byte operand kernels with 32- and 64-row tiles (MSDA_VP_BM) and the element-wise ones
     (MSDA_VP_SCALAR) on the same inputs, all against the oracle: they differ in tiling, staging and
     in how the bias gradient is formed."""
@@ -188,9 +188,9 @@ def test_vector_and_elementwise_kernels_agree(monkeypatch, bf16):
     want = [VP.value_proj_rows(x, wq, bias, h, mask), *VP.value_proj_rows_vjp(x, wq, h, g, mask)]
     for mode in ("bm32", "bm64", "scalar"):
         if mode == "scalar":
-            monkeypatch.setenv("MSDA_VP_SCALAR", "1")
+            tune({"MSDA_VP_SCALAR": "1"})
         else:
-            monkeypatch.setenv("MSDA_VP_BM", mode[2:])
+            tune({"MSDA_VP_BM": mode[2:]})
         out = value_proj_forward(_t(x, dt), _t(w), _t(bias), h, _t(mask))
         got = [out, *value_proj_backward(_t(x, dt), _t(w), h, _t(g, dt), _t(mask))]
         torch.cuda.synchronize()
