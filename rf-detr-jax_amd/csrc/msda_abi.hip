@@ -591,6 +591,176 @@ int bwd_band_impl(const Shape& s, int ch, const void* value, int value_dtype, co
                                         : msda_host::launch_part_sum<float>(p.part, p.nqb, p.part_stride, grad_value, sgrid, st);
 }
 
+// ------------------------------------------------------------------------------------------
+// planning of the sorted-gather backward (bwd_gather_kernel)
+
+struct GatherPlan {
+  int threads, qblock, nqb, lds;
+  int g, wt, key, cnt, scan, val;  // LDS byte offsets (val -1: value rows read from global memory)
+};
+
+// LDS of a workgroup holding `qb` queries with `nt` threads: grad_output rows in f32 (the area also
+// holds one partial row per thread after the gather), a weight / dot slot per (sample, corner),
+// the sorted entries (u16, padded to whole rows of `nt`), the cell counters of the largest level
+// plus one, one scan slot per wave, and optionally the largest level's value rows.
+void gather_layout(const Shape& s, int qb, int nt, int vbytes, bool stage, GatherPlan* gp) {
+  int cmax = 0;
+  for (int l = 0; l < s.levels; ++l) cmax = std::max(cmax, s.h[l] * s.w[l]);
+  const int64_t ns = static_cast<int64_t>(qb) * s.points;
+  int64_t o = 0;
+  gp->g = 0;
+  o += align16(static_cast<int64_t>(std::max(qb, nt)) * (s.dim + 4) * 4);  // rows padded by 16 bytes
+  gp->wt = static_cast<int>(o);
+  o += align16(ns * 16);
+  gp->key = static_cast<int>(o);
+  o += align16((ns * 4 + nt) * 2);
+  gp->cnt = static_cast<int>(o);
+  o += align16((static_cast<int64_t>(cmax) + 1) * 4);
+  gp->scan = static_cast<int>(o);
+  o += 64;
+  gp->val = -1;
+  if (stage) {
+    gp->val = static_cast<int>(o);
+    o += align16(static_cast<int64_t>(cmax) * s.dim * vbytes);
+  }
+  gp->lds = o > (int64_t{1} << 30) ? (1 << 30) : static_cast<int>(o);
+}
+
+int gather_threads(int qb, int points, int max_threads) {
+  // every thread holds at most kGatherSpt samples through the sort; about 12 entries per thread
+  const int64_t ns = static_cast<int64_t>(qb) * points;
+  const int64_t need = (ns + msda::kGatherSpt - 1) / msda::kGatherSpt;
+  const int64_t want = (ns * 4 + 11) / 12;
+  int64_t t = std::max(need, std::min<int64_t>(want, max_threads));
+  t = std::max<int64_t>(64, ((t + 63) / 64) * 64);
+  const int forced = env_int("MSDA_BWD_GATHER_THREADS", 0);
+  if (forced > 0) t = std::max<int64_t>(t, ((forced + 63) / 64) * 64);
+  return static_cast<int>(std::min<int64_t>(t, max_threads));
+}
+
+// Whether the sorted gather takes this shape: head_dim 16 or 32, every level under 2^15 cells,
+// and at least one query block that fits the LDS.
+bool gather_eligible(const Shape& s) {
+  // off by default: measured on MI355X slower than the band kernel at every benchmarked shape
+  // (one workgroup per CU, so its barrier-separated phases do not overlap; nano_groupdetr
+  // config: 73 us against 37 us)
+  if (env_int("MSDA_BWD_GATHER", 0) == 0) return false;
+  if (s.dim != 16 && s.dim != 32) return false;
+  for (int l = 0; l < s.levels; ++l)
+    if (static_cast<int64_t>(s.h[l]) * s.w[l] >= (int64_t{1} << msda::kGatherCellBits)) return false;
+  return true;
+}
+
+// Query blocks: as many queries per workgroup as `per_cu` workgroups per CU leave LDS for (and the
+// threads can hold), then more blocks while the grid has fewer workgroups than per_cu * CUs. Blocks
+// of one (slice, level) write f32 partial rows that a second kernel adds.
+int plan_gather_with(const Shape& s, int vbytes, const DevInfo& dev, bool stage, GatherPlan* gp) {
+  const int max_threads = s.dim == 16 ? 1024 : 512;
+  const int per_cu = std::max(1, env_int("MSDA_BWD_GATHER_WGS_PER_CU", 1));
+  const int budget = dev.lds_bytes / per_cu;
+  auto fits = [&](int qb) {
+    GatherPlan t;
+    gather_layout(s, qb, gather_threads(qb, s.points, max_threads), vbytes, stage, &t);
+    return t.lds <= budget && static_cast<int64_t>(qb) * s.points <= static_cast<int64_t>(max_threads) * msda::kGatherSpt &&
+           static_cast<int64_t>(qb) * s.points * 4 < 65536;
+  };
+  int qmax = std::min(s.queries, max_threads * msda::kGatherSpt / std::max(1, s.points));
+  while (qmax > 1 && !fits(qmax)) qmax = std::max(1, qmax * 15 / 16);
+  if (!fits(qmax)) return fail(MSDA_ERR_UNSUPPORTED, "sorted-gather backward does not fit in LDS");
+  const int64_t units = static_cast<int64_t>(s.batch) * s.heads * s.levels;
+  int nqb = (s.queries + qmax - 1) / qmax;
+  const int forced = env_int("MSDA_BWD_GATHER_QB", 0);
+  if (forced > 0) {
+    nqb = std::max(nqb, (s.queries + forced - 1) / forced);
+  } else {
+    const int64_t target = static_cast<int64_t>(per_cu) * dev.cus;
+    while (units * nqb < target && (s.queries + nqb) / (nqb + 1) >= 64) ++nqb;
+  }
+  gp->nqb = nqb;
+  gp->qblock = (s.queries + nqb - 1) / nqb;
+  gp->threads = gather_threads(gp->qblock, s.points, max_threads);
+  gather_layout(s, gp->qblock, gp->threads, vbytes, stage, gp);
+  if (gp->lds > dev.lds_bytes) return fail(MSDA_ERR_UNSUPPORTED, "sorted-gather backward needs %d bytes of LDS", gp->lds);
+  if (units * nqb > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
+  return MSDA_OK;
+}
+
+bool gather_aligned(const void* value, const void* grad_value, const void* grad_output, int gbytes) {
+  return aligned(value, 16) && aligned(grad_value, 16) && aligned(grad_output, 4 * static_cast<size_t>(gbytes));
+}
+
+// The level's value rows are staged in LDS (the corner dots then read LDS instead of L2) when that
+// costs at most one more query block than reading them from global memory.
+int plan_gather(const Shape& s, int vbytes, const DevInfo& dev, GatherPlan* gp) {
+  const int stage = env_int("MSDA_BWD_GATHER_STAGE", -1);
+  if (stage >= 0) return plan_gather_with(s, vbytes, dev, stage != 0, gp);
+  int rc = plan_gather_with(s, vbytes, dev, false, gp);
+  if (rc != MSDA_OK) return rc;
+  GatherPlan st;
+  if (plan_gather_with(s, vbytes, dev, true, &st) == MSDA_OK && st.nqb <= gp->nqb + 1) *gp = st;
+  g_last_error.clear();
+  return MSDA_OK;
+}
+
+int64_t gather_workspace(const Shape& s, const GatherPlan& gp) {
+  return gp.nqb > 1 ? align16(static_cast<int64_t>(gp.nqb) * s.batch * s.heads * s.len_value * s.dim * 4) : 0;
+}
+
+int bwd_gather_impl(const Shape& s, const void* value, int value_dtype, const float* loc, const float* attn, const void* grad_output,
+                    int grad_output_dtype, void* grad_value, float* grad_loc, float* grad_attn, void* workspace,
+                    int64_t workspace_bytes, const DevInfo& dev, hipStream_t st) {
+  const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
+  GatherPlan gp;
+  int rc = plan_gather(s, vbytes, dev, &gp);
+  if (rc != MSDA_OK) return rc;
+  const bool partial = gp.nqb > 1 && grad_value != nullptr;
+  if (partial) {
+    const int64_t need = gather_workspace(s, gp);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace of %lld bytes needed, got %lld (see the workspace size query)",
+                  static_cast<long long>(need), static_cast<long long>(workspace == nullptr ? 0 : workspace_bytes));
+    if (!aligned(workspace, 16)) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  }
+  const int gbytes = grad_output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
+  // rows are moved 16 bytes (value, grad_value, f32 partials) or 8 bytes (bf16 grad_output) at a time
+  if (!gather_aligned(value, grad_value, grad_output, gbytes))
+    return fail(MSDA_ERR_UNSUPPORTED, "sorted-gather backward needs 16-byte aligned value rows");
+  msda::GatherParams p{};
+  p.value = value;
+  p.loc = loc;
+  p.attn = attn;
+  p.gout = grad_output;
+  p.dvalue = grad_value;
+  p.dloc = grad_loc;
+  p.dattn = grad_attn;
+  p.part = partial ? static_cast<float*>(workspace) : nullptr;
+  p.part_stride = static_cast<int64_t>(s.batch) * s.heads * s.len_value * s.dim;
+  p.heads = s.heads;
+  p.queries = s.queries;
+  p.levels = s.levels;
+  p.points = s.points;
+  p.len_value = s.len_value;
+  p.nqb = gp.nqb;
+  p.qblock = gp.qblock;
+  p.p_shift = (s.points & (s.points - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(s.points)) : -1;
+  p.lds_g = gp.g;
+  p.lds_wt = gp.wt;
+  p.lds_key = gp.key;
+  p.lds_cnt = gp.cnt;
+  p.lds_scan = gp.scan;
+  p.lds_val = gp.val;
+  for (int l = 0; l < s.levels; ++l) p.lv[l] = level_desc(s, l, 0, 1, 0);
+  const int grid = static_cast<int>(static_cast<int64_t>(s.batch) * s.heads * s.levels * gp.nqb);
+  const bool gb = grad_output_dtype == MSDA_DTYPE_BF16;
+  rc = value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_bwd_gather<msda::bf16_t>(s.dim, gb, p, grid, gp.threads, gp.lds, st)
+                                      : msda_host::dispatch_bwd_gather<float>(s.dim, gb, p, grid, gp.threads, gp.lds, st);
+  if (rc != MSDA_OK || !partial) return rc;
+  const int64_t quads = (p.part_stride + 3) / 4;
+  const int sgrid = static_cast<int>((quads + 255) / 256);
+  return value_dtype == MSDA_DTYPE_BF16 ? msda_host::launch_part_sum<msda::bf16_t>(p.part, p.nqb, p.part_stride, grad_value, sgrid, st)
+                                        : msda_host::launch_part_sum<float>(p.part, p.nqb, p.part_stride, grad_value, sgrid, st);
+}
+
 
 }  // namespace
 
@@ -716,13 +886,17 @@ int64_t workspace_impl(int batch, int n_heads, int head_dim, int len_query, int 
   if ((rc = device_info(&dev)) != MSDA_OK) return rc;
   if (ref_dim == 0) {
     // the query blocks' partial sums; the plan depends on the value dtype, which the query does not
-    // name, so the larger of the two
+    // name, so the larger of the two; and either kernel may run (the sorted gather needs aligned
+    // rows), so the larger of the two kernels' needs
     int64_t need = 0;
     for (int vbytes : {2, 4}) {
       BandPlan bp;
       if ((rc = plan_band(s, vbytes, 16, dev, &bp)) != MSDA_OK) return rc;
       need = std::max(need, band_workspace(s, bp));
+      GatherPlan gp;
+      if (gather_eligible(s) && plan_gather(s, vbytes, dev, &gp) == MSDA_OK) need = std::max(need, gather_workspace(s, gp));
     }
+    g_last_error.clear();
     return need;
   }
   BinPlan bp;
@@ -767,10 +941,18 @@ int bwd_impl(const void* value, int value_dtype, const float* loc, const float* 
         static_cast<int64_t>(n_heads) * head_dim * 4 >= (int64_t{1} << 24))
       return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * n_levels * n_points reaches 2^24");
     const int gb = grad_output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
-    const int ch = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 16), {{value, vbytes}, {grad_output, gb}});
+    // 8-channel lanes: measured on MI355X faster than 16 at head_dim 16 (nano 12.1 vs 13.4 us,
+    // nano_groupdetr 36.9 vs 43.0, two_level 58.5 vs 82.6)
+    const int ch = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 8), {{value, vbytes}, {grad_output, gb}});
     if (lpq_shift_for(head_dim, ch) > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d)", head_dim, 64 * ch);
     DevInfo dev;
     if ((rc = device_info(&dev)) != MSDA_OK) return rc;
+    GatherPlan gp;
+    if (len_query > 0 && gather_eligible(s) && gather_aligned(value, grad_value, grad_output, gb) &&
+        plan_gather(s, vbytes, dev, &gp) == MSDA_OK)
+      return bwd_gather_impl(s, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn,
+                             workspace, workspace_bytes, dev, static_cast<hipStream_t>(stream));
+    g_last_error.clear();
     return bwd_band_impl(s, ch, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn,
                          workspace, workspace_bytes, dev, static_cast<hipStream_t>(stream));
   }

@@ -7,4 +7,5 @@ template int dispatch_bwd_sample<msda::bf16_t>(int, int, bool, const msda::Sampl
 template int dispatch_value<msda::bf16_t>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
 template int dispatch_bwd_band<msda::bf16_t>(int, const msda::BandParams&, int, int, int, hipStream_t);
 template int launch_part_sum<msda::bf16_t>(const float*, int, int64_t, void*, int, hipStream_t);
+template int dispatch_bwd_gather<msda::bf16_t>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);
 }  // namespace msda_host

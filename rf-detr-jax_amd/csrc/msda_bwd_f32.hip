@@ -7,4 +7,5 @@ template int dispatch_bwd_sample<float>(int, int, bool, const msda::SampleParams
 template int dispatch_value<float>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
 template int dispatch_bwd_band<float>(int, const msda::BandParams&, int, int, int, hipStream_t);
 template int launch_part_sum<float>(const float*, int, int64_t, void*, int, hipStream_t);
+template int dispatch_bwd_gather<float>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);
 }  // namespace msda_host

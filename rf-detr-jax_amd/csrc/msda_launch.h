@@ -5,6 +5,7 @@
 
 #include "msda.h"
 #include "msda_band_kernels.h"
+#include "msda_gather_kernels.h"
 #include "msda_kernels.h"
 
 #include <hip/hip_runtime.h>
@@ -105,6 +106,28 @@ int dispatch_bwd_band(int ch, const msda::BandParams& p, int grid, int threads, 
                      : dispatch_bwd_band_g<VT, float>(ch, p, grid, threads, lds, st);
 }
 
+template <typename VT, typename GT, int KD, int NT>
+int launch_bwd_gather(const msda::GatherParams& p, int grid, int threads, int lds, hipStream_t stream) {
+  static std::atomic<int> granted[kMaxDevices];
+  auto k = msda::bwd_gather_kernel<VT, GT, KD, NT>;
+  int rc = allow_lds(k, lds, granted);
+  if (rc != MSDA_OK) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
+  return check_launch("msda backward (sorted gather)");
+}
+
+// head_dim 16 (up to 1024 threads) or 32 (up to 512: twice the registers per thread).
+template <typename VT>
+int dispatch_bwd_gather(int dim, bool gout_bf16, const msda::GatherParams& p, int grid, int threads, int lds, hipStream_t st) {
+  if (dim == 16)
+    return gout_bf16 ? launch_bwd_gather<VT, msda::bf16_t, 16, 1024>(p, grid, threads, lds, st)
+                     : launch_bwd_gather<VT, float, 16, 1024>(p, grid, threads, lds, st);
+  if (dim == 32)
+    return gout_bf16 ? launch_bwd_gather<VT, msda::bf16_t, 32, 512>(p, grid, threads, lds, st)
+                     : launch_bwd_gather<VT, float, 32, 512>(p, grid, threads, lds, st);
+  return fail(MSDA_ERR_UNSUPPORTED, "no sorted-gather backward for head_dim %d", dim);
+}
+
 // Grouped-query forward kernels come in two forms: every level staged in LDS (no L2 gather path)
 // or not; NS = 0 handles any sample count and either kind of level.
 template <typename VT, int VEC, bool FUSED>
@@ -173,5 +196,7 @@ extern template int dispatch_bwd_band<float>(int, const msda::BandParams&, int, 
 extern template int dispatch_bwd_band<msda::bf16_t>(int, const msda::BandParams&, int, int, int, hipStream_t);
 extern template int launch_part_sum<float>(const float*, int, int64_t, void*, int, hipStream_t);
 extern template int launch_part_sum<msda::bf16_t>(const float*, int, int64_t, void*, int, hipStream_t);
+extern template int dispatch_bwd_gather<float>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);
+extern template int dispatch_bwd_gather<msda::bf16_t>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);
 
 }  // namespace msda_host

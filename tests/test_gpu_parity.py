@@ -201,7 +201,7 @@ def test_global_gather_path_and_many_bands(tune):
     """Forward without LDS staging (levels read through L2) and backward split into many bands."""
     g = load_golden("nano_small")
     tune({"MSDA_FWD_LDS_BUDGET": "0"})
-    tune({"MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_BANDS": "7"})
+    tune({"MSDA_BWD_GATHER": "0", "MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_BANDS": "7"})
     out, (gv, gl, ga) = _run(g["value"], g["shapes"], g["loc"], g["attn"], g["grad"])
     assert_close(out, g["out"], 1e-5, "out")
     assert_close(gv, g["grad_value"], 1e-4, "grad_value")
@@ -209,23 +209,35 @@ def test_global_gather_path_and_many_bands(tune):
     assert_close(ga, g["grad_attn"], 1e-4, "grad_attn")
 
 
+_BAND = {"MSDA_BWD_GATHER": "0"}  # the atomic-accumulation band kernel (the default)
+_GATHER = {"MSDA_BWD_GATHER": "1"}  # the sorted-gather kernel
+
+
 @pytest.mark.parametrize("variant", [
-    {},                                                         # whole levels, queries split in blocks
-    {"MSDA_BWD_THREADS": "64"},                                 # one-wave workgroups
-    {"MSDA_BWD_FORCE_BANDS": "1"},                              # row bands, scanned and listed
-    {"MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_BANDS": "24"},      # one row per band: points straddle bands
-    {"MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_LIST": "64"},       # several list passes per band
-    {"MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_THREADS": "64"},
-    {"MSDA_BWD_MAX_VEC": "8"},                                  # two lanes per query
-    {"MSDA_BWD_MAX_VEC": "4"},                                  # four lanes per query
-    {"MSDA_BWD_MAX_VEC": "1"},                                  # one channel per lane
+    {**_GATHER},                                                # sorted gather, default blocks
+    {**_GATHER, "MSDA_BWD_GATHER_QB": "64"},                    # many query blocks: partial sums
+    {**_GATHER, "MSDA_BWD_GATHER_QB": "333"},                   # ragged last block
+    {**_GATHER, "MSDA_BWD_GATHER_THREADS": "1024"},             # short runs: cells span many threads
+    {**_GATHER, "MSDA_BWD_GATHER_STAGE": "0"},                  # value rows from global memory
+    {**_GATHER, "MSDA_BWD_GATHER_STAGE": "1"},                  # value rows staged in LDS
+    {**_GATHER, "MSDA_BWD_GATHER_WGS_PER_CU": "2"},
+    {**_BAND},                                                  # band kernel: whole levels, query blocks
+    {**_BAND, "MSDA_BWD_THREADS": "64"},                        # one-wave workgroups
+    {**_BAND, "MSDA_BWD_FORCE_BANDS": "1"},                     # row bands, scanned and listed
+    {**_BAND, "MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_BANDS": "24"},  # one row per band: points straddle
+    {**_BAND, "MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_LIST": "64"},   # several list passes per band
+    {**_BAND, "MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_THREADS": "64"},
+    {**_BAND, "MSDA_BWD_MAX_VEC": "16"},                        # one lane per query
+    {**_BAND, "MSDA_BWD_MAX_VEC": "4"},                         # four lanes per query
+    {**_BAND, "MSDA_BWD_MAX_VEC": "1"},                         # one channel per lane
 ], ids=lambda v: ",".join(f"{k}={x}" for k, x in v.items()) or "default")
 @pytest.mark.parametrize("queries", [700, 5000])
 def test_backward_launch_variants(tune, variant, queries):
-    """The backward kernel's launch shapes against the float64 oracle: whole levels with the
-    queries split in blocks (partial sums added by a second kernel), row bands from one per level to
-    one per image row with one or several list passes, workgroups of one to sixteen waves, and one to
-    sixteen lanes per query."""
+    """The backward kernels' launch shapes against the float64 oracle. Sorted gather: query blocks
+    from 64 queries to the LDS limit (partial sums added by a second kernel), 8 to 16 waves, value
+    rows from global memory or LDS. Band kernel: whole levels with the queries split in blocks, row
+    bands from one per level to one per image row with one or several list passes, workgroups of
+    one to sixteen waves, and one to sixteen lanes per query."""
     tune(variant)
     shapes = ((24, 24), (12, 12))
     value, loc, attn, grad = make_inputs(77, 2, 4, 16, queries, shapes, 2)
@@ -252,7 +264,7 @@ def test_forward_paired_lanes(tune, pair):
 @pytest.mark.parametrize("variant", [
     {"MSDA_FWD_GROUPED": "0"},
     {"MSDA_FWD_MAX_VEC": "16"},
-    {"MSDA_BWD_MAX_VEC": "8"},
+    {**_BAND, "MSDA_BWD_MAX_VEC": "16"},
     {"MSDA_FWD_HEADS": "2", "MSDA_BWDS_HEADS": "2"},
 ], ids=lambda v: ",".join(f"{k}={x}" for k, x in v.items()))
 @pytest.mark.parametrize("shapes", [((24, 24),), ((24, 24), (12, 12))], ids=["one_level", "two_levels"])
