@@ -96,11 +96,13 @@ int msda_fwd(const void* value, int value_dtype,
              int64_t len_value, void* stream);
 
 /*
- * Device workspace msda_bwd needs for this shape, in bytes, or a negative MSDA_ERR_* code. The
- * backward is one kernel whose scratch lives in LDS, so this is 0 for every valid shape; the
- * query stays so that a caller written against a workspace contract (an XLA FFI handler asking
- * ffi::ScratchAllocator, the reference having no counterpart: JAX autodiff materialises its own
- * intermediates, ops.py:120-134) keeps working unchanged.
+ * Device workspace msda_bwd needs for this shape, in bytes, or a negative MSDA_ERR_* code: the f32
+ * partial grad_value sums of the query blocks when the backward splits each (slice, level)'s
+ * queries over several workgroups (n_blocks * batch * n_heads * len_value * head_dim * 4 bytes),
+ * else 0. It depends on the shape, the device and the MSDA_* tuning knobs in force (read from the
+ * environment once, or set by msda_set_tuning); with no knob set, on the shape and the device
+ * only. The reference has no counterpart: JAX autodiff materialises its own intermediates
+ * (ops.py:120-134); an XLA FFI handler asks ffi::ScratchAllocator for this many bytes.
  */
 int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_query,
                                 int n_levels, int n_points,
@@ -115,11 +117,14 @@ int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_qu
  *   grad_attention_weights  [batch, len_query, n_heads, n_levels*n_points]     f32
  * Replaces the JAX autodiff VJP of ops.py:64-134/289 and deform_pallas.py:157-175 (_sample_bwd).
  * Any of the three gradient pointers may be NULL to skip that gradient. grad_output has
- * grad_output_dtype (the forward's output dtype). grad_value is accumulated in f64 (every product
- * a * w * g of f32 values is exact) and rounded once to value_dtype; every element has one writer.
- * workspace / workspace_bytes are not read (msda_bwd_workspace_size() is 0) and may be NULL / 0.
- * Limits (MSDA_ERR_UNSUPPORTED beyond them): levels of at most 32000 rows and columns, and
- * len_query * n_heads * head_dim < 2^30.
+ * grad_output_dtype (the forward's output dtype). grad_value is accumulated in LDS in f64 (every
+ * product a * w * g of f32 values is exact); a workgroup owns a (slice, level band) and writes its
+ * rows once, rounded to value_dtype, or, when a level's queries are split over several
+ * workgroups, writes f32 partial rows into the workspace that a second kernel adds in block order.
+ * workspace must hold msda_bwd_workspace_size() bytes (16-byte aligned); it may be NULL when that
+ * size is 0 or grad_value is NULL.
+ * Limits (MSDA_ERR_UNSUPPORTED beyond them): levels of at most 32000 rows and columns,
+ * len_query * n_heads * head_dim < 2^30 and len_query * n_heads * n_levels * n_points < 2^24.
  */
 int msda_bwd(const void* value, int value_dtype,
              const float* sampling_locations, const float* attention_weights,
@@ -129,6 +134,25 @@ int msda_bwd(const void* value, int value_dtype,
              int n_levels, int n_points,
              const int32_t* spatial_shapes, const int32_t* level_start_index,
              int64_t len_value, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * msda_bwd without a workspace argument and without any device allocation, for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The partial sums go to a file-scope device array of
+ * 16 MiB that the library holds on every GPU it runs on until the process ends; a shape whose
+ * msda_bwd_workspace_size() exceeds it returns MSDA_ERR_UNSUPPORTED. Every call on one GPU uses
+ * that GPU's array: calls that overlap on one GPU (different streams, or threads) race. Nothing in
+ * the array needs clearing (every partial element is written before it is read). Arguments and
+ * results otherwise as msda_bwd.
+ */
+int msda_bwd_noalloc(const void* value, int value_dtype,
+                     const float* sampling_locations, const float* attention_weights,
+                     const void* grad_output, int grad_output_dtype,
+                     void* grad_value, float* grad_sampling_locations, float* grad_attention_weights,
+                     int batch, int n_heads, int head_dim, int len_query,
+                     int n_levels, int n_points,
+                     const int32_t* spatial_shapes, const int32_t* level_start_index,
+                     int64_t len_value, void* stream);
 
 /*
  * The MSDeformAttn prologue fused into the kernels. These entry points take what the module's

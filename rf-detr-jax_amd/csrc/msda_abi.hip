@@ -1115,6 +1115,33 @@ int bwd_impl(const void* value, int value_dtype, const float* loc, const float* 
                                         : msda_host::dispatch_value<float>(bp.cg, bp.nacc, vp, g, vthreads, bp.lds, st);
 }
 
+// The scratch of msda_bwd_noalloc: a file-scope device array (each GPU the library runs on holds
+// its own copy until the process ends). Host code never uses the array's name as an address (on
+// the host it is only a stand-in for the symbol): its device address is looked up once per device
+// with hipGetSymbolAddress, with that device current, and kept here.
+// 16 MiB: the nano group-DETR backward (batch 8, 16 heads, one 24x24 level, 3900 queries) needs
+// 9.4 MiB of partial sums; query blocks exist only while the grid is short of one resident wave of
+// workgroups, so most shapes need less or none. Shapes that need more are refused.
+constexpr int64_t kNoAllocScratchBytes = int64_t{16} << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MSDA_ERR_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MSDA_ERR_DEVICE, "device index %d out of range", dev);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(MSDA_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return MSDA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1158,6 +1185,27 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   return bwd_impl(value, value_dtype, sampling_locations, attention_weights, grad_output, grad_output_dtype, grad_value,
                   grad_sampling_locations, grad_attention_weights, batch, n_heads, head_dim, len_query, n_levels, n_points,
                   spatial_shapes, level_start_index, len_value, workspace, workspace_bytes, stream, nullptr);
+}
+
+int msda_bwd_noalloc(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
+                     const void* grad_output, int grad_output_dtype, void* grad_value, float* grad_sampling_locations,
+                     float* grad_attention_weights, int batch, int n_heads, int head_dim, int len_query, int n_levels,
+                     int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value,
+                     void* stream) {
+  const int64_t need = workspace_impl(batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index,
+                                      len_value, 0);
+  if (need < 0) return static_cast<int>(need);
+  if (need > kNoAllocScratchBytes)
+    return fail(MSDA_ERR_UNSUPPORTED, "msda_bwd_noalloc: this shape needs %lld bytes of scratch, the library holds %lld",
+                static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = noalloc_scratch(&ws);
+    if (rc != MSDA_OK) return rc;
+  }
+  return bwd_impl(value, value_dtype, sampling_locations, attention_weights, grad_output, grad_output_dtype, grad_value,
+                  grad_sampling_locations, grad_attention_weights, batch, n_heads, head_dim, len_query, n_levels, n_points,
+                  spatial_shapes, level_start_index, len_value, ws, need > 0 ? kNoAllocScratchBytes : 0, stream, nullptr);
 }
 
 int msda_fused_fwd(const void* value, int value_dtype, const float* reference_points, int ref_dim, const float* sampling_offsets,

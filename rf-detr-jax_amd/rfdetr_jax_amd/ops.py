@@ -171,7 +171,7 @@ def ms_deform_attn_backward(value, spatial_shapes, sampling_locations, attention
         ws_bytes = lib.msda_bwd_workspace_size(*dims)
         if ws_bytes < 0:
             _native.check(int(ws_bytes))
-        # scratch for the per-sample records (16 bytes each); torch's caching allocator serves it
+        # the query blocks' partial grad_value sums (f32); torch's caching allocator serves it
         workspace = torch.empty((max(1, ws_bytes // 16), 4), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         rc = lib.msda_bwd(
