@@ -6,6 +6,7 @@
 #include "msda.h"
 #include "msda_kernels.h"
 #include "msda_launch.h"
+#include "msda_fused_bwd_kernels.h"
 
 #include <hip/hip_runtime.h>
 
@@ -213,12 +214,11 @@ msda::LevelDesc level_desc(const Shape& s, int l, int lds, int band_rows, int ba
   d.lds = lds;
   d.band_rows = band_rows;
   d.band_first = band_first;
-  d.band_magic = band_rows > 1 ? static_cast<uint32_t>(((uint64_t{1} << 32) + band_rows - 1) / band_rows) : 0u;
   return d;
 }
 
 // ------------------------------------------------------------------------------------------
-// planning of the per-sample kernels (forward and the backward's per-sample pass)
+// planning of the forward kernel
 
 struct SamplePlan {
   int grid, threads, lds;
@@ -233,7 +233,7 @@ struct SamplePlan {
 // halve the location / weight rows fetched per query). Then one resident wave of workgroups:
 // fewer, longer workgroups amortise the value staging.
 int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* prefix, int shift, msda::SampleParams* p,
-                SamplePlan* out, int forced_qblock = 0, int extra_lds = 0, int max_group_lanes = 0) {
+                SamplePlan* out) {
   auto knob = [&](const char* name, int dflt) {
     std::string key = std::string(prefix) + name;
     return env_int(key.c_str(), dflt);
@@ -255,11 +255,7 @@ int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* pref
   int hg = 1;
   const int hg_cap = std::max(1, knob("_HEADS", 4));
   const int group_budget = std::min(budget, knob("_GROUP_LDS", dev.lds_bytes));
-  // max_group_lanes: a head group's lanes of one query must fit in that many (one wave when they
-  // exchange values by shuffles)
-  while (hg * 2 <= hg_cap && s.heads % (hg * 2) == 0 && (hg * 2) * head_bytes <= group_budget &&
-         (max_group_lanes == 0 || ((hg * 2) << shift) <= max_group_lanes))
-    hg *= 2;
+  while (hg * 2 <= hg_cap && s.heads % (hg * 2) == 0 && (hg * 2) * head_bytes <= group_budget) hg *= 2;
   // With every level staged a head's region is its whole value slice; regions stay 16-byte aligned.
   const int head_stride = all_staged ? static_cast<int>(s.len_value * s.dim) : static_cast<int>(head_bytes / vbytes);
   p->head_lds = head_stride;
@@ -279,9 +275,7 @@ int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* pref
   const int64_t units = static_cast<int64_t>(s.batch) * (s.heads / hg);
   const int target = knob("_TARGET_WGS", dev.cus * std::min(per_cu, 8));
   const int max_blocks = std::max(1, (s.queries + qpp - 1) / qpp);
-  if (forced_qblock > 0) {
-    p->qblock = forced_qblock;  // the grad_value bins fix the query blocks
-  } else {
+  {
     const int nqb = static_cast<int>(std::min<int64_t>(max_blocks, std::max<int64_t>(1, (target + units - 1) / units)));
     const int per = (s.queries + nqb - 1) / nqb;
     p->qblock = std::max(qpp, ((per + qpp - 1) / qpp) * qpp);
@@ -291,8 +285,8 @@ int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* pref
   if (grid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "grid too large");
   out->grid = static_cast<int>(grid);
   out->threads = threads;
-  out->lds = align16(lds) + extra_lds;
-  if (out->lds > dev.lds_bytes) return fail(MSDA_ERR_UNSUPPORTED, "per-sample pass needs %d bytes of LDS", out->lds);
+  out->lds = align16(lds);
+  if (out->lds > dev.lds_bytes) return fail(MSDA_ERR_UNSUPPORTED, "forward needs %d bytes of LDS", out->lds);
   return MSDA_OK;
 }
 
@@ -307,101 +301,6 @@ bool rows_16b(const Shape& s, int vbytes, const void* a, const void* b) {
   return true;
 }
 
-
-// Geometry of the grad_value pass and of the records that feed it; depends on the shape and the
-// device only, so the workspace size can be queried before the tensors exist.
-struct BinPlan {
-  int qblock, nqb;  // query blocks of the per-sample pass (records are binned per block)
-  int nwork;        // (level, band) items per slice
-  int rb[msda::kMaxLevels];
-  int cap;          // records listed per grad_value segment
-  int nacc;         // grad_value accumulators: 4 (one per corner) or 1 (colour passes)
-  int threads;      // grad_value workgroup size
-  int cg;           // channels per grad_value gather lane (8 when head_dim allows, else 4)
-  int lds;          // grad_value workgroup LDS
-  int64_t bins_bytes, counts_bytes, total_bytes;
-};
-
-int plan_bins_for(const Shape& s, const DevInfo& dev, BinPlan* bp, int target) {
-  const int64_t N = static_cast<int64_t>(s.batch) * s.heads;
-  // query blocks: about two workgroups of the per-sample pass per CU with two-head groups, and
-  // offsets inside a block fit 16 bits
-  const int64_t units = std::max<int64_t>(1, N / 2);
-  int nqb = static_cast<int>(std::max<int64_t>(1, (env_int("MSDA_BWDS_TARGET_WGS", 2 * dev.cus) + units - 1) / units));
-  nqb = std::max(nqb, (s.queries + 65534) / 65535);
-  nqb = std::max(1, std::min(nqb, std::max(1, s.queries)));
-  bp->qblock = std::max(1, (s.queries + nqb - 1) / nqb);
-  bp->nqb = std::max(1, (s.queries + bp->qblock - 1) / bp->qblock);
-  // Bands of image rows: each (slice, level, band) workgroup owns the band's grad_value rows.
-  // Rows per band are chosen so the grid reaches the target and the LDS layout (accumulator,
-  // cell tables, record list) fits the budget; the list holds as many records as fit.
-  // half a CU's LDS (less allocation-granularity slack) keeps two workgroups per CU
-  const int budget = std::min(dev.lds_bytes, env_int("MSDA_BWD_LDS_BUDGET", dev.lds_bytes / 2 - 1024));
-  const int64_t want_items = std::max<int64_t>(1, (target + N - 1) / std::max<int64_t>(1, N));
-  int64_t total_area = 0;
-  for (int l = 0; l < s.levels; ++l) total_area += static_cast<int64_t>(s.h[l]) * s.w[l];
-  const int records = std::max(1, s.queries * s.points);
-  const int cap_want = std::min({65535, records, std::max(256, env_int("MSDA_BWD_LIST", 65535))});
-  bp->threads = std::max(64, std::min(msda::kValueMaxThreads, (env_int("MSDA_BWD_VALUE_THREADS", 512) / 64) * 64));
-  const int cap_min = std::min(256, cap_want);
-  int cap = cap_want;
-  auto target_rows = [&](int l) {
-    const int64_t area = static_cast<int64_t>(s.h[l]) * s.w[l];
-    int nb = static_cast<int>((want_items * area + total_area / 2) / total_area);
-    const int forced = env_int("MSDA_BWD_BANDS", 0);
-    if (forced > 0) nb = forced;
-    nb = std::min(s.h[l], std::max(1, nb));
-    return (s.h[l] + nb - 1) / nb;
-  };
-  // Four accumulators (no colour passes) when every level's target band fits with them and room
-  // for a sizeable list; otherwise one accumulator, so bands need not shrink.
-  bp->nacc = 4;
-  for (int l = 0; l < s.levels; ++l)
-    if (msda::value_layout(target_rows(l), s.w[l], s.dim, std::min(cap_want, 1024), bp->nqb, 4).total + 32 > budget) bp->nacc = 1;
-  const int forced_acc = env_int("MSDA_BWD_ACCUMULATORS", 0);
-  if (forced_acc == 1 || forced_acc == 4) bp->nacc = forced_acc;
-  // Channels per gather lane: 8 with one accumulator (its colour passes then run half as many
-  // tasks), 4 with four (measured on MI355X: 8 is ~10-20 % faster in the first case, 4 ~5 % in the
-  // second).
-  const int cg_env = env_int("MSDA_BWD_VALUE_CG", bp->nacc == 1 ? 8 : 4);
-  bp->cg = (cg_env == 8 && s.dim % 8 == 0) ? 8 : 4;
-  for (int l = 0; l < s.levels; ++l) {
-    int rb = target_rows(l);
-    // 16 bytes of LDS per listed record, 32 of alignment slack; shrink the band until a list of
-    // cap_min records fits
-    auto fixed = [&](int r) { return msda::value_layout(r, s.w[l], s.dim, 0, bp->nqb, bp->nacc).total + 32; };
-    while (rb > 1 && (budget - fixed(rb)) / 16 < cap_min) --rb;
-    if ((rb + 1) * (s.w[l] + 1) > 65535 || (dev.lds_bytes - fixed(rb)) / 16 < cap_min)
-      return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], s.dim);
-    bp->rb[l] = rb;
-    cap = std::min(cap, (std::max(budget, fixed(rb) + 16 * cap_min) - fixed(rb)) / 16);
-  }
-  bp->cap = std::max(1, cap);
-  bp->nwork = 0;
-  bp->lds = 0;
-  for (int l = 0; l < s.levels; ++l) {
-    bp->nwork += (s.h[l] + bp->rb[l] - 1) / bp->rb[l];
-    bp->lds = std::max(bp->lds, msda::value_layout(bp->rb[l], s.w[l], s.dim, bp->cap, bp->nqb, bp->nacc).total);
-  }
-  const int64_t sub = static_cast<int64_t>(bp->qblock) * s.points;  // records per (slice, item, block) at most
-  bp->bins_bytes = N * bp->nwork * bp->nqb * sub * static_cast<int64_t>(sizeof(msda::SampleRec));
-  bp->counts_bytes = align16(N * bp->nwork * bp->nqb * 4);
-  bp->total_bytes = bp->bins_bytes + bp->counts_bytes;
-  return MSDA_OK;
-}
-
-// Grid target of the grad_value pass: two workgroups per CU. When LDS limits force more items
-// than that anyway (wide levels), a second round of workgroups runs regardless, and planning for
-// twice the target gives shorter, better balanced workgroups (measured on MI355X: 62.6 against
-// 70 us for the two-level bf16 workload).
-int plan_bins(const Shape& s, const DevInfo& dev, BinPlan* bp) {
-  const int forced = env_int("MSDA_BWD_TARGET_WGS", 0);
-  const int target = forced > 0 ? forced : 2 * dev.cus;
-  int rc = plan_bins_for(s, dev, bp, target);
-  if (rc != MSDA_OK || forced > 0) return rc;
-  if (static_cast<int64_t>(s.batch) * s.heads * bp->nwork > target) rc = plan_bins_for(s, dev, bp, 2 * target);
-  return rc;
-}
 
 // ------------------------------------------------------------------------------------------
 // planning of the backward kernel (bwd_band_kernel)
@@ -778,15 +677,6 @@ int device_attrs(int* lds_bytes, int* cus) {
 }
 }  // namespace msda_host
 
-namespace msda {
-
-// grad_reference_points from the per-group partials, when no grad_value pass runs to do it.
-__global__ void __launch_bounds__(256) ref_grad_kernel(const float* __restrict__ part, float* __restrict__ dref, int64_t n,
-                                                       int groups) {
-  ref_grad_sum(part, dref, n, groups, static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x, static_cast<int64_t>(gridDim.x) * 256);
-}
-
-}  // namespace msda
 
 namespace {
 
@@ -805,12 +695,6 @@ int check_fused(const Fused& fz, int len_query) {
     return fail(MSDA_ERR_INVALID_ARGUMENT, "reference_points must be %d-byte aligned", 4 * fz.ref_dim);
   if (!aligned(fz.dref, 4)) return fail(MSDA_ERR_INVALID_ARGUMENT, "grad_reference_points must be 4-byte aligned");
   return MSDA_OK;
-}
-
-// Bytes of per-head-group reference-point partial sums the fused backward may need: one row per
-// (batch, query, head) in the worst case of one-head groups.
-int64_t ref_part_bytes(const Shape& s, int ref_dim) {
-  return align16(static_cast<int64_t>(s.batch) * s.queries * s.heads * s.levels * ref_dim * 4);
 }
 
 void fill_fused(msda::SampleParams* p, const Fused* fz, int n_points) {
@@ -874,6 +758,80 @@ int fwd_impl(const void* value, int value_dtype, const float* loc, const float* 
   return msda_host::dispatch_fwd<float>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st);
 }
 
+// ------------------------------------------------------------------------------------------
+// the fused-prologue backward: prologue kernel, the core's band kernel, epilogue kernel
+
+// Workspace of msda_fused_bwd: the rows' locations and weights formed by the prologue, the
+// locations' gradient when grad_sampling_offsets is not requested but the reference points' is,
+// and the core's partial sums.
+struct FusedLayout {
+  int64_t loc, attn, dloc, band, total;
+};
+
+FusedLayout fused_layout(const Shape& s, int64_t band_bytes) {
+  const int64_t samples = static_cast<int64_t>(s.batch) * s.queries * s.heads * s.levels * s.points;
+  FusedLayout f;
+  f.loc = 0;
+  f.attn = align16(samples * 8);
+  f.dloc = f.attn + align16(samples * 4);
+  f.band = f.dloc + align16(samples * 8);
+  f.total = f.band + band_bytes;
+  return f;
+}
+
+int fused_bwd_impl(const Shape& s, int ch, const void* value, int value_dtype, const float* offsets, const float* logits,
+                   const void* grad_output, int grad_output_dtype, void* grad_value, float* grad_offsets, float* grad_logits,
+                   const Fused& fz, void* workspace, int64_t workspace_bytes, const DevInfo& dev, hipStream_t st) {
+  const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
+  if (s.queries == 0)  // grad_value is zero; nothing else has elements
+    return bwd_band_impl(s, ch, value, value_dtype, nullptr, nullptr, grad_output, grad_output_dtype, grad_value, nullptr, nullptr,
+                         nullptr, 0, dev, st);
+  BandPlan bp;
+  int rc = plan_band(s, vbytes, ch, dev, &bp);
+  if (rc != MSDA_OK) return rc;
+  const FusedLayout lay = fused_layout(s, band_workspace(s, bp));
+  if (workspace == nullptr || workspace_bytes < lay.total)
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace of %lld bytes needed, got %lld (see the workspace size query)",
+                static_cast<long long>(lay.total), static_cast<long long>(workspace == nullptr ? 0 : workspace_bytes));
+  if (!aligned(workspace, 16)) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  char* ws = static_cast<char*>(workspace);
+  msda::FusedRowParams fp{};
+  fp.ref = fz.ref;
+  fp.off = offsets;
+  fp.logits = logits;
+  fp.loc = reinterpret_cast<float*>(ws + lay.loc);
+  fp.attn = reinterpret_cast<float*>(ws + lay.attn);
+  fp.ref_dim = fz.ref_dim;
+  fp.heads = s.heads;
+  fp.levels = s.levels;
+  fp.points = s.points;
+  fp.bq_total = static_cast<int64_t>(s.batch) * s.queries;
+  fp.fpoints = static_cast<float>(s.points);
+  fp.inv_points = (s.points & (s.points - 1)) == 0 ? 1.0f / static_cast<float>(s.points) : 0.0f;
+  for (int l = 0; l < s.levels; ++l) {
+    fp.fw[l] = static_cast<float>(s.w[l]);
+    fp.fh[l] = static_cast<float>(s.h[l]);
+  }
+  const int64_t rows = fp.bq_total * s.heads;
+  hipLaunchKernelGGL(msda::fused_prologue_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256), 0, st, fp);
+  if ((rc = msda_host::check_launch("msda fused backward (prologue)")) != MSDA_OK) return rc;
+  float* dloc = grad_offsets != nullptr ? grad_offsets : (fz.dref != nullptr ? reinterpret_cast<float*>(ws + lay.dloc) : nullptr);
+  rc = bwd_band_impl(s, ch, value, value_dtype, fp.loc, fp.attn, grad_output, grad_output_dtype, grad_value, dloc, grad_logits,
+                     ws + lay.band, workspace_bytes - lay.band, dev, st);
+  if (rc != MSDA_OK) return rc;
+  if (dloc == nullptr && grad_logits == nullptr) return MSDA_OK;
+  fp.dloc = dloc;
+  fp.doff = grad_offsets;
+  fp.dlogits = grad_logits;
+  fp.dref = fz.dref;
+  int hp_shift = 0;
+  while ((1 << hp_shift) < s.heads) ++hp_shift;
+  const int64_t per_block = 256 >> hp_shift;
+  hipLaunchKernelGGL(msda::fused_epilogue_kernel, dim3(static_cast<unsigned>((fp.bq_total + per_block - 1) / per_block)), dim3(256),
+                     0, st, fp, hp_shift);
+  return msda_host::check_launch("msda fused backward (epilogue)");
+}
+
 int64_t workspace_impl(int batch, int n_heads, int head_dim, int len_query, int n_levels, int n_points, const int32_t* spatial_shapes,
                        const int32_t* level_start_index, int64_t len_value, int ref_dim) {
   g_last_error.clear();
@@ -899,9 +857,13 @@ int64_t workspace_impl(int batch, int n_heads, int head_dim, int len_query, int 
     g_last_error.clear();
     return need;
   }
-  BinPlan bp;
-  if ((rc = plan_bins(s, dev, &bp)) != MSDA_OK) return rc;
-  return bp.total_bytes + ref_part_bytes(s, ref_dim);
+  int64_t need = 0;
+  for (int vbytes : {2, 4}) {
+    BandPlan bp;
+    if ((rc = plan_band(s, vbytes, 16, dev, &bp)) != MSDA_OK) return rc;
+    need = std::max(need, fused_layout(s, band_workspace(s, bp)).total);
+  }
+  return need;
 }
 
 int bwd_impl(const void* value, int value_dtype, const float* loc, const float* attn, const void* grad_output, int grad_output_dtype,
@@ -928,191 +890,37 @@ int bwd_impl(const void* value, int value_dtype, const float* loc, const float* 
   const int gbytes = grad_output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   if (!aligned(value, vbytes) || !aligned(grad_value, vbytes) || !aligned(grad_output, gbytes))
     return fail(MSDA_ERR_INVALID_ARGUMENT, "value/grad_value/grad_output not aligned to their element size");
-  const bool want_dv = grad_value != nullptr;
-  if (fz == nullptr) {
-    // the core's backward is one kernel and needs no workspace
-    for (int l = 0; l < n_levels; ++l)
-      if (s.h[l] > 32000 || s.w[l] > 32000)
-        return fail(MSDA_ERR_UNSUPPORTED, "level %d (%d x %d) exceeds 32000 rows or columns", l, s.h[l], s.w[l]);
-    if (static_cast<int64_t>(len_query) * n_heads * head_dim >= (int64_t{1} << 30))
-      return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * head_dim reaches 2^30");
-    // a workgroup addresses one batch entry's sample rows with 32-bit offsets (24-bit multiplies)
-    if (static_cast<int64_t>(len_query) * n_heads * n_levels * n_points >= (int64_t{1} << 24) ||
-        static_cast<int64_t>(n_heads) * head_dim * 4 >= (int64_t{1} << 24))
-      return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * n_levels * n_points reaches 2^24");
-    const int gb = grad_output_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
-    // 8-channel lanes: measured on MI355X faster than 16 at head_dim 16 (nano 12.1 vs 13.4 us,
-    // nano_groupdetr 36.9 vs 43.0, two_level 58.5 vs 82.6)
-    const int ch = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 8), {{value, vbytes}, {grad_output, gb}});
-    if (lpq_shift_for(head_dim, ch) > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d)", head_dim, 64 * ch);
-    DevInfo dev;
-    if ((rc = device_info(&dev)) != MSDA_OK) return rc;
-    GatherPlan gp;
-    if (len_query > 0 && gather_eligible(s) && gather_aligned(value, grad_value, grad_output, gb) &&
-        plan_gather(s, vbytes, dev, &gp) == MSDA_OK)
-      return bwd_gather_impl(s, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn,
-                             workspace, workspace_bytes, dev, static_cast<hipStream_t>(stream));
-    g_last_error.clear();
-    return bwd_band_impl(s, ch, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn,
-                         workspace, workspace_bytes, dev, static_cast<hipStream_t>(stream));
-  }
-  if ((want_dv || want_dref) && len_query > 0) {
-    if (workspace == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace is NULL (see the workspace size query)");
-    if (!aligned(workspace, 16)) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
-  }
   for (int l = 0; l < n_levels; ++l)
     if (s.h[l] > 32000 || s.w[l] > 32000)
       return fail(MSDA_ERR_UNSUPPORTED, "level %d (%d x %d) exceeds 32000 rows or columns", l, s.h[l], s.w[l]);
-  // grad_value gathers address one batch entry's grad_output rows by 32-bit byte offsets
   if (static_cast<int64_t>(len_query) * n_heads * head_dim >= (int64_t{1} << 30))
     return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * head_dim reaches 2^30");
-  const int max_vec = fz ? env_int("MSDA_FUSED_BWD_MAX_VEC", 16) : env_int("MSDA_BWD_MAX_VEC", 16);
-  const int vec = pick_vec(head_dim, max_vec, {{value, vbytes}, {grad_output, gbytes}});
-  // the fused variant loads a group of queries' inputs at once and keeps dA in registers for the
-  // softmax VJP (the per-query loop would wait on memory three times per query)
-  const int grouped = fz ? env_int("MSDA_FUSED_BWD_GROUPED", 1) : env_int("MSDA_BWD_GROUPED", 0);
-  const int ns = grouped ? samples_bound(n_levels, n_points) : 0;
-  const int shift = lpq_shift_for(head_dim, vec);
-  if (shift > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d for this dtype)", head_dim, 64 * vec);
-
+  // a workgroup addresses one batch entry's sample rows with 32-bit offsets (24-bit multiplies)
+  if (static_cast<int64_t>(len_query) * n_heads * n_levels * n_points >= (int64_t{1} << 24) ||
+      static_cast<int64_t>(n_heads) * head_dim * 4 >= (int64_t{1} << 24))
+    return fail(MSDA_ERR_UNSUPPORTED, "len_query * n_heads * n_levels * n_points reaches 2^24");
+  if (fz != nullptr && n_heads > 64) return fail(MSDA_ERR_UNSUPPORTED, "msda_fused_bwd supports at most 64 heads, got %d", n_heads);
+  // the fused backward keeps the prologue's locations and weights in the workspace
+  if (fz != nullptr && len_query > 0 && workspace == nullptr)
+    return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_fused_bwd: workspace is NULL (see the workspace size query)");
+  // 8-channel lanes: measured on MI355X faster than 16 at head_dim 16 (nano 12.1 vs 13.4 us,
+  // nano_groupdetr 36.9 vs 43.0, two_level 58.5 vs 82.6)
+  const int ch = pick_vec(head_dim, env_int("MSDA_BWD_MAX_VEC", 8), {{value, vbytes}, {grad_output, gbytes}});
+  if (lpq_shift_for(head_dim, ch) > 6) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large (max %d)", head_dim, 64 * ch);
   DevInfo dev;
   if ((rc = device_info(&dev)) != MSDA_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-
-  // ---- grad_value plan (checked, with the workspace, before anything is launched)
-  BinPlan bp{};
-  msda::ValueParams vp{};
-  int64_t ws_needed = 0;
-  if (want_dv && len_query > 0) {
-    if ((rc = plan_bins(s, dev, &bp)) != MSDA_OK) return rc;
-    ws_needed = bp.total_bytes;
-    vp.bins = static_cast<const msda::SampleRec*>(workspace);
-    vp.bin_counts = reinterpret_cast<const int*>(static_cast<const char*>(workspace) + bp.bins_bytes);
-    vp.nqb = bp.nqb;
-    vp.qblock = bp.qblock;
-    vp.cap = bp.cap;
-    vp.nwork = bp.nwork;
-  } else if (want_dv) {
-    // no queries: grad_value is zero; one band per level and an empty record list
-    bp.nqb = 1;
-    bp.qblock = 1;
-    bp.cap = 1;
-    bp.nacc = 1;
-    bp.threads = 256;
-    bp.cg = 4;
-    bp.nwork = 0;
-    bp.lds = 0;
-    for (int l = 0; l < n_levels; ++l) {
-      bp.rb[l] = 1;
-      while (bp.rb[l] < s.h[l] && msda::value_layout(bp.rb[l] + 1, s.w[l], head_dim, 1, 1, 1).total <= dev.lds_bytes / 2) ++bp.rb[l];
-      if (msda::value_layout(bp.rb[l], s.w[l], head_dim, 1, 1, 1).total > dev.lds_bytes)
-        return fail(MSDA_ERR_UNSUPPORTED, "level %d (width %d, head_dim %d) does not fit in LDS", l, s.w[l], head_dim);
-      bp.nwork += (s.h[l] + bp.rb[l] - 1) / bp.rb[l];
-      bp.lds = std::max(bp.lds, msda::value_layout(bp.rb[l], s.w[l], head_dim, 1, 1, 1).total);
-    }
-    vp.bins = nullptr;
-    vp.bin_counts = nullptr;
-    vp.nqb = 1;
-    vp.qblock = 1;
-    vp.cap = 1;
-    vp.nwork = bp.nwork;
-  }
-  int nwork_acc = 0;
-  if (want_dv) {
-    for (int l = 0; l < n_levels; ++l) {
-      vp.lv[l] = level_desc(s, l, -1, bp.rb[l], nwork_acc);
-      nwork_acc += (s.h[l] + bp.rb[l] - 1) / bp.rb[l];
-    }
-    vp.gout = grad_output;
-    vp.gout_bf16 = grad_output_dtype == MSDA_DTYPE_BF16;
-    vp.dvalue = grad_value;
-    vp.heads = n_heads;
-    vp.dim = head_dim;
-    vp.queries = len_query;
-    vp.levels = n_levels;
-    vp.points = n_points;
-    vp.len_value = len_value;
-    vp.g_vec4 = (head_dim % 4 == 0) && aligned(grad_output, grad_output_dtype == MSDA_DTYPE_BF16 ? 8 : 16);
-    vp.vec16 = rows_16b(s, vbytes, grad_value, nullptr);
-  }
-
-  // ---- per-sample pass: grad of weights (logits) and locations (offsets), grad_value records
-  if (len_query > 0) {
-    msda::SampleParams p{};
-    p.value = value;
-    p.loc = loc;
-    p.attn = attn;
-    p.gout = grad_output;
-    p.gout_bf16 = grad_output_dtype == MSDA_DTYPE_BF16;
-    p.dloc = grad_loc;
-    p.dattn = grad_attn;
-    p.heads = n_heads;
-    p.dim = head_dim;
-    p.queries = len_query;
-    p.levels = n_levels;
-    p.points = n_points;
-    p.len_value = len_value;
-    p.vec16 = rows_16b(s, vbytes, value, nullptr);
-    fill_fused(&p, fz, n_points);
-    p.bq_total = static_cast<int64_t>(batch) * len_query;
-    SamplePlan plan;
-    // the fused backward sums reference-point gradients over a head group by shuffles in one wave
-    if ((rc = plan_sample(s, vbytes, dev, "MSDA_BWDS", shift, &p, &plan, want_dv ? bp.qblock : 0, 0, fz ? 64 : 0)) != MSDA_OK) return rc;
-    const int groups = n_heads / p.hg;
-    float* ref_part = nullptr;  // per-group partials, summed by ref_grad_kernel (groups > 1)
-    if (want_dref) {
-      if (groups == 1) {
-        p.dref = fz->dref;
-      } else {
-        ref_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws_needed);
-        ws_needed += ref_part_bytes(s, fz->ref_dim);
-        p.dref = ref_part;
-      }
-    }
-    if (workspace_bytes < ws_needed && ws_needed > 0)
-      return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace of %lld bytes needed, got %lld", static_cast<long long>(ws_needed),
-                  static_cast<long long>(workspace_bytes));
-    if (want_dv) {
-      p.bins = static_cast<uint4*>(workspace);
-      p.bin_counts = reinterpret_cast<int*>(static_cast<char*>(workspace) + bp.bins_bytes);
-      p.nwork = bp.nwork;
-      for (int l = 0; l < n_levels; ++l) {
-        p.lv[l].band_rows = vp.lv[l].band_rows;
-        p.lv[l].band_first = vp.lv[l].band_first;
-        p.lv[l].band_magic = vp.lv[l].band_magic;
-      }
-      // a workgroup's bin region: 16-byte records addressed by 32-bit byte offsets
-      const int64_t region = static_cast<int64_t>(p.hg) * bp.nwork * bp.nqb * bp.qblock * n_points;
-      if (region >= (int64_t{1} << 28)) return fail(MSDA_ERR_UNSUPPORTED, "grad_value record bins of a workgroup reach 2^28 records");
-      p.small_bins = region < (int64_t{1} << 24) ? 1 : 0;
-      // per (head, item) record counters after the staged value rows
-      plan.lds = align16(plan.lds) + align16(static_cast<int64_t>(p.hg) * bp.nwork * 4);
-      if (plan.lds > dev.lds_bytes) return fail(MSDA_ERR_UNSUPPORTED, "per-sample pass needs %d bytes of LDS", plan.lds);
-    }
-    const bool fused = fz != nullptr;
-    rc = value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_bwd_sample<msda::bf16_t>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st)
-                                        : msda_host::dispatch_bwd_sample<float>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st);
-    if (rc != MSDA_OK) return rc;
-    if (ref_part != nullptr && want_dv) {
-      // the grad_value pass sums the partials before its own work (saves a launch)
-      vp.ref_part = ref_part;
-      vp.dref = fz->dref;
-      vp.ref_n = static_cast<int64_t>(batch) * len_query * n_levels * fz->ref_dim;
-      vp.ref_groups = groups;
-    } else if (ref_part != nullptr) {
-      const int64_t n = static_cast<int64_t>(batch) * len_query * n_levels * fz->ref_dim;
-      const int grid = static_cast<int>(std::min<int64_t>((n + 255) / 256, static_cast<int64_t>(dev.cus) * 8));
-      hipLaunchKernelGGL(msda::ref_grad_kernel, dim3(grid), dim3(256), 0, st, ref_part, fz->dref, n, groups);
-      if ((rc = msda_host::check_launch("msda fused backward (reference points)")) != MSDA_OK) return rc;
-    }
-  }
-  if (!want_dv) return MSDA_OK;
-  const int64_t vgrid = static_cast<int64_t>(batch) * n_heads * vp.nwork;
-  if (vgrid > 0x7fffffff) return fail(MSDA_ERR_UNSUPPORTED, "backward grid too large");
-  const int vthreads = bp.threads;
-  const int g = static_cast<int>(vgrid);
-  return value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_value<msda::bf16_t>(bp.cg, bp.nacc, vp, g, vthreads, bp.lds, st)
-                                        : msda_host::dispatch_value<float>(bp.cg, bp.nacc, vp, g, vthreads, bp.lds, st);
+  if (fz != nullptr)
+    return fused_bwd_impl(s, ch, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn, *fz,
+                          workspace, workspace_bytes, dev, st);
+  GatherPlan gp;
+  if (len_query > 0 && gather_eligible(s) && gather_aligned(value, grad_value, grad_output, gbytes) &&
+      plan_gather(s, vbytes, dev, &gp) == MSDA_OK)
+    return bwd_gather_impl(s, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn,
+                           workspace, workspace_bytes, dev, st);
+  g_last_error.clear();
+  return bwd_band_impl(s, ch, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn,
+                       workspace, workspace_bytes, dev, st);
 }
 
 // The scratch of msda_bwd_noalloc: a file-scope device array (each GPU the library runs on holds

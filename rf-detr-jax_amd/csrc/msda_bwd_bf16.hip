@@ -1,10 +1,8 @@
-// Backward kernels for a bf16 value map: the per-sample pass (core and fused-prologue variants)
-// and the grad_value pass. A translation unit of its own so the build compiles them in parallel.
+// Backward kernels for a bf16 value map (band kernel, partial sums, sorted gather). A translation
+// unit of its own so the build compiles them in parallel.
 #include "msda_launch.h"
 
 namespace msda_host {
-template int dispatch_bwd_sample<msda::bf16_t>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
-template int dispatch_value<msda::bf16_t>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
 template int dispatch_bwd_band<msda::bf16_t>(int, const msda::BandParams&, int, int, int, hipStream_t);
 template int launch_part_sum<msda::bf16_t>(const float*, int, int64_t, void*, int, hipStream_t);
 template int dispatch_bwd_gather<msda::bf16_t>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);

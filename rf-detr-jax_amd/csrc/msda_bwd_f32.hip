@@ -1,10 +1,8 @@
-// Backward kernels for an f32 value map: the per-sample pass (core and fused-prologue variants)
-// and the grad_value pass. A translation unit of its own so the build compiles them in parallel.
+// Backward kernels for an f32 value map (band kernel, partial sums, sorted gather). A translation
+// unit of its own so the build compiles them in parallel.
 #include "msda_launch.h"
 
 namespace msda_host {
-template int dispatch_bwd_sample<float>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
-template int dispatch_value<float>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
 template int dispatch_bwd_band<float>(int, const msda::BandParams&, int, int, int, hipStream_t);
 template int launch_part_sum<float>(const float*, int, int64_t, void*, int, hipStream_t);
 template int dispatch_bwd_gather<float>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);

@@ -1,33 +1,20 @@
-// msda_kernels.h — gfx950 device code for multi-scale deformable attention (forward and VJP).
+// msda_kernels.h — gfx950 device code for multi-scale deformable attention: the forward kernel
+// and the device helpers the backward kernels share (msda_band_kernels.h, msda_gather_kernels.h,
+// msda_fused_bwd_kernels.h).
 //
 // Semantics follow RF-DETR-JAX's gather sampler, src/rfdetr_jax/models/ops.py:64-134 and
 // ops.py:208-292: grid_sample(bilinear, zeros, align_corners=False) of each (batch, head) value
 // slice at 2*loc-1, corner order (x0,y0),(x1,y0),(x0,y1),(x1,y1), masked weights multiplied onto
-// values read at clipped indices, level-major point sum. Gradients are the VJP of those lines.
+// values read at clipped indices, level-major point sum.
 //
-// Kernels:
-//  * fwd_kernel — one workgroup per (batch b, group of hg heads, block of queries). The group's
-//    value slices (the levels that fit) are staged into LDS with one batched copy; levels that do
-//    not fit are gathered through L2. Lanes are laid out channel group, then head, then query, so
-//    the lanes of one query read locations / weights and write output rows as contiguous runs of
-//    the [B, Q, H, ...] tensors. Each lane group computes a sample's coordinates once.
-//  * bwd_sample_kernel — the same decomposition for the backward pass: per sample, the dot
-//    products D_c = <g, v_c> with the four corners give grad_attention_weights and
-//    grad_sampling_locations, and a 16-byte record (floor cell, a*(1-fx), a*fx, fy) is written to
-//    a workspace in slice-major order [b*H+h][l][q][p], which grad_value reads contiguously.
-//  * bwd_value_kernel — one workgroup per (slice, level, band of rows). It reads its slice's
-//    records, counting-sorts those whose cell touches the band by cell into LDS (integer LDS
-//    atomics count and rank them), and has one lane per (cell, 4 channels) sum
-//    a * w_k * g over the cell's records in registers, grad_output rows being gathered from global
-//    memory. Corner k's sum goes to the k-th of four f32 band accumulators: for a fixed corner,
-//    distinct cells hit distinct pixels, so no two lanes ever update one element and no atomics on
-//    floats are needed; each grad_value element is written once, as the sum of the four, in the
-//    value dtype.
+// fwd_kernel — one workgroup per (batch b, group of hg heads, block of queries). The group's value
+// slices (the levels that fit) are staged into LDS with one batched copy; levels that do not fit
+// are gathered through L2. Lanes are laid out channel group, then head, then query, so the lanes of
+// one query read locations / weights and write output rows as contiguous runs of the
+// [B, Q, H, ...] tensors. Each lane group computes a sample's coordinates once.
 //
-// Measured on MI355X (per CU): LDS float atomics (ds_add_f32) cost ~195 cycles per wave
-// instruction against ~6 for integer ones, and device-wide f32 atomics reach ~1.3 TB/s at best;
-// hence no float atomics anywhere. Generic (flat) pointers to LDS cost vector-memory issue slots,
-// so LDS reads go through address_space(3) pointers.
+// Generic (flat) pointers to LDS cost vector-memory issue slots, so LDS reads go through
+// address_space(3) pointers.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -39,8 +26,7 @@ namespace msda {
 
 constexpr int kMaxLevels = 16;
 constexpr int kXcds = 8;               // MI355X: 8 accelerator complex dies, workgroups dispatched round-robin
-constexpr int kSampleMaxThreads = 1024;  // forward and per-sample backward workgroups
-constexpr int kValueMaxThreads = 1024;  // grad_value workgroups
+constexpr int kSampleMaxThreads = 1024;  // forward workgroups
 constexpr int kPassBatch = 4;           // samples whose location / weight loads are issued together
 
 using bf16_t = uint16_t;
@@ -51,33 +37,18 @@ struct LevelDesc {
   int small;       // h * w * dim < 2^24: corner offsets fit 24-bit multiplies
   int start;       // first position of the level in the value slice
   int lds;         // per-sample kernels: element offset of the staged level inside a head's LDS region, -1 = L2
-  int band_rows;   // grad_value kernel: image rows per band
-  int band_first;  // grad_value kernel: index of the level's first band among a slice's (level, band) items
-  uint32_t band_magic;  // ceil(2^32 / band_rows) (0 when band_rows == 1): row / band_rows = umulhi(row, magic)
+  int band_rows;   // backward band kernel: image rows per band
+  int band_first;  // backward band kernel: index of the level's first band among a slice's (level, band) items
 };
 
-// row / band_rows for 0 <= row < 2^16 and band_rows < 2^16: with magic = ceil(2^32 / band_rows),
-// row * magic / 2^32 exceeds row / band_rows by less than 2^-16 < 1 / band_rows, so the floor is exact.
-__device__ __forceinline__ int band_of(int row, const LevelDesc& L) {
-  return L.band_rows == 1 ? row : static_cast<int>(__umulhi(static_cast<uint32_t>(row), L.band_magic));
-}
-
-// Forward and per-sample backward kernels.
+// Forward kernels.
 struct SampleParams {
   const void* value;
   const float* loc;
   const float* attn;
   void* out;         // forward: output [B, Q, H*D]
   int out_bf16;
-  const void* gout;  // backward: grad_output [B, Q, H*D]
-  int gout_bf16;
-  float* dloc;       // backward: grad_sampling_locations, or null
-  float* dattn;      // backward: grad_attention_weights, or null
-  uint4* bins;       // backward: grad_value records, binned by (slice, level band), or null
-  int small_bins;    // a workgroup's bin region holds < 2^24 records (24-bit index arithmetic)
   int pair_share;    // forward: one level, two points, two lanes per (query, head) (fwd_pair)
-  int* bin_counts;   // backward: records per (slice, level band, query block)
-  int nwork;         // backward: (level, band) items per slice
   int heads, dim, queries, levels, points;
   int64_t len_value;
   int lpq_shift;   // log2(lanes per (query, head)); each lane owns VEC channels
@@ -88,88 +59,13 @@ struct SampleParams {
   int all_staged;  // every level is staged, so a head group's value rows are one contiguous copy
   int vec16;       // value staging may use 16-byte vectors
   // MSDeformAttn prologue fused in (kFused kernels, ops.py:388-404): `loc` then holds the raw
-  // sampling offsets and `attn` the attention logits, and `dloc` / `dattn` receive their gradients.
+  // sampling offsets and `attn` the attention logits.
   const float* ref;  // reference points [B, Q, L, ref_dim]
   int ref_dim;       // 2 (points) or 4 (boxes: centre, width, height)
   float fpoints;     // n_points as a float: the box form divides the offsets by it
   float inv_points;  // 1 / n_points when n_points is a power of two (x / P == x * (1 / P) exactly), else 0
-  float* dref;       // backward: reference-point gradient per head group [H / hg, B * Q, L, ref_dim], or null
-  int64_t bq_total;  // B * Q (rows per head group of `dref`)
   LevelDesc lv[kMaxLevels];
 };
-
-// A sample's record for grad_value, one per (sample, band its bilinear cell touches), in the bin of
-// (slice, level band) and query block that produced it: `key` is the cell's index in the band's
-// cell grid ((ky * (W + 1) + kx) with kx = x0 + 1, ky = y0 - r0 + 1; for non-finite weights the
-// clipped first corner's cell), packed with the query's offset inside its query block; then
-// u = a * (1 - fx), v = a * fx and fy, so that the corner weights are u*(1-fy), v*(1-fy), u*fy, v*fy.
-struct __align__(16) SampleRec {
-  uint32_t key_q;  // key | (query offset in block) << 16
-  float u, v, fy;
-};
-
-struct ValueParams {
-  const SampleRec* bins;   // [slice][item][query block][qblock * points]
-  const int* bin_counts;   // [slice][item][query block]
-  int nqb, qblock;         // query blocks of the per-sample pass, and their size
-  const void* gout;
-  int gout_bf16;
-  void* dvalue;
-  int heads, dim, queries, levels, points;
-  int64_t len_value;
-  int nwork;   // (level, band) items per slice
-  int cap;     // records listed per segment (LDS list capacity)
-  int g_vec4;  // grad_output rows may be read 4 channels at a time
-  int vec16;   // grad_value rows may be written 16 bytes at a time
-  // fused prologue: the reference-point gradient's sum over head groups, done by this kernel's
-  // threads before their own work (ref_grad_sum), or ref_n = 0
-  const float* ref_part;
-  float* dref;
-  int64_t ref_n;
-  int ref_groups;
-  LevelDesc lv[kMaxLevels];
-};
-
-// grad_reference_points [B, Q, L, ref_dim] (n elements) = the sum over head groups of the
-// per-group partials [groups][n], added in group order, four groups' loads in flight at once.
-// Thread `tid` of `nthreads` handles elements tid, tid + nthreads, ...
-__device__ __forceinline__ void ref_grad_sum(const float* __restrict__ part, float* __restrict__ dref, int64_t n, int groups,
-                                             int64_t tid, int64_t nthreads) {
-  for (int64_t i = tid; i < n; i += nthreads) {
-    const float* s = part + i;
-    float acc = 0.0f;
-    int g = 0;
-    for (; g + 4 <= groups; g += 4) {
-      const float a0 = s[(g + 0) * n], a1 = s[(g + 1) * n], a2 = s[(g + 2) * n], a3 = s[(g + 3) * n];
-      acc = (((acc + a0) + a1) + a2) + a3;
-    }
-    for (; g < groups; ++g) acc += s[g * n];
-    dref[i] = acc;
-  }
-}
-
-// LDS carve-up of one grad_value workgroup; shared by the host planner and the kernel. Every
-// region starts on a 16-byte boundary.
-struct ValueLayout {
-  int acc, cnt, off, misc, nonempty, binpre, list, total;
-};
-
-__host__ __device__ inline int align16i(int x) { return (x + 15) & ~15; }
-
-__host__ __device__ inline ValueLayout value_layout(int band_rows, int w, int dim, int cap, int nqb, int nacc) {
-  ValueLayout L;
-  const int ncell = (band_rows + 1) * (w + 1);
-  int o = 0;
-  L.acc = o;      o += nacc * align16i(band_rows * w * dim * 4);  // one per bilinear corner, or one in all
-  L.cnt = o;      o += align16i((ncell + 1) * 4);
-  L.off = o;      o += align16i((ncell + 1) * 4);
-  L.misc = o;     o += 128;  // 4 counters + one scan slot per wave (<= 16 waves) + spare
-  L.nonempty = o; o += align16i(ncell * 2);
-  L.binpre = o;   o += align16i((nqb + 1) * 4);
-  L.list = o;     o += cap * 16;
-  L.total = o;
-  return L;
-}
 
 // ---------------------------------------------------------------------------------------------
 // scalar helpers
@@ -555,16 +451,12 @@ __device__ __forceinline__ void load_in(SampleIn<N>& f, const float2* __restrict
 
 // Queries per lane whose inputs are loaded together when a query's samples fit NS (NS = 0: one
 // query at a time, its samples in chunks of kPassBatch). The loads of a group are all in flight
-// before the first is used, so a lane waits one memory latency per group rather than per query;
-// the backward also holds each query's grad_output row (VEC floats), so it groups fewer (sized so
-// that no instantiation spills registers at four waves per SIMD).
-constexpr int query_group(int ns, int vec, bool backward, bool fused = false) {
+// before the first is used, so a lane waits one memory latency per group rather than per query
+// (sized so that no instantiation spills registers at four waves per SIMD).
+constexpr int query_group(int ns, int vec, bool fused = false) {
   if (ns == 0) return 1;
-  // + a reference point and a box offset per sample, and the backward's dA per sample
-  if (fused) return backward ? 1 : vec >= 8 ? (ns <= 2 ? 2 : 1) : (ns <= 2 ? 4 : 2);
-  if (!backward) return ns <= 2 ? 4 : 2;
-  if (vec >= 16) return ns <= 2 ? 2 : 1;
-  if (vec == 8) return 2;
+  // + a reference point and a box offset per sample
+  if (fused) return vec >= 8 ? (ns <= 2 ? 2 : 1) : (ns <= 2 ? 4 : 2);
   return ns <= 2 ? 4 : 2;
 }
 
@@ -585,9 +477,9 @@ __device__ __forceinline__ void load_group(SampleIn<NS> (&in)[QU], const float2*
 }
 
 // ---------------------------------------------------------------------------------------------
-// MSDeformAttn prologue fused into the per-sample kernels (ops.py:388-404): sample locations from
+// MSDeformAttn prologue fused into the forward kernel (ops.py:388-404): sample locations from
 // reference points and raw offsets, attention weights from a softmax over each (query, head)'s
-// L*P logits; and, in the backward, the gradients of offsets, logits and reference points.
+// L*P logits; fused_offset_grad is the transpose the fused backward's epilogue applies.
 
 // What the prologue adds per sample: the reference point of the sample's level (x, y, and for
 // boxes w, h), and the offset the box form scales (off / n_points; the raw offset for points).
@@ -660,15 +552,20 @@ __device__ __forceinline__ void softmax_regs(SampleIn<N>& f, int LP) {
 // ops.py:388-399 for one sample. Points: ref + off / (W_l, H_l). Boxes: ref_xy + off / n_points *
 // ref_wh * 0.5, evaluated left to right. Each division is one IEEE rounding (precise_divide,
 // ops.py:46-62; hipcc's f32 division is correctly rounded) and nothing is contracted.
-__device__ __forceinline__ float2 fused_location(float2 off, float4 r, float2& t, const LevelDesc& L, const SampleParams& p) {
+// t: the offset term that multiplies ref_wh (boxes), kept for the reference-point gradient.
+__device__ __forceinline__ float2 fused_location_at(float2 off, float4 r, float2& t, float fw, float fh, int ref_dim,
+                                                    float inv_points, float fpoints) {
 #pragma clang fp contract(off)
-  if (p.ref_dim == 2) {
+  if (ref_dim == 2) {
     t = off;
-    return make_float2(r.x + off.x / L.fw, r.y + off.y / L.fh);
+    return make_float2(r.x + off.x / fw, r.y + off.y / fh);
   }
-  t = p.inv_points != 0.0f ? make_float2(off.x * p.inv_points, off.y * p.inv_points)
-                           : make_float2(off.x / p.fpoints, off.y / p.fpoints);
+  t = inv_points != 0.0f ? make_float2(off.x * inv_points, off.y * inv_points) : make_float2(off.x / fpoints, off.y / fpoints);
   return make_float2(r.x + (t.x * r.z) * 0.5f, r.y + (t.y * r.w) * 0.5f);
+}
+
+__device__ __forceinline__ float2 fused_location(float2 off, float4 r, float2& t, const LevelDesc& L, const SampleParams& p) {
+  return fused_location_at(off, r, t, L.fw, L.fh, p.ref_dim, p.inv_points, p.fpoints);
 }
 
 // Turns loaded offsets of samples s0 .. s0 + N - 1 into locations.
@@ -705,55 +602,18 @@ __device__ __forceinline__ void fused_prologue_row(SampleIn<N>& f, FusedIn<N, tr
   fused_locations<N>(f, x, p, 0, LP, 0, 0);
 }
 
-// Backward state of one (query, head) row: sum_k a_k dA_k for the softmax VJP, and the running
-// reference-point gradient of the current level (x, y, and w, h for boxes).
-struct FusedAcc {
-  float S;
-  float r[4];
-};
-
-// Gradients of one sample from the core's (grad_loc, dA): the offset gradient (the transpose of
-// fused_location: grad_loc / (W_l, H_l), or ((grad_loc * 0.5) * ref_wh) / n_points) and the
-// sample's share of the reference-point gradient (grad_loc, and (grad_loc * 0.5) * t for w, h).
-__device__ __forceinline__ float2 fused_sample_grads(float2 gl, float a, float dA, float4 r, float2 t, const LevelDesc& L,
-                                                     const SampleParams& p, FusedAcc& fa) {
-  fa.S += a * dA;
-  fa.r[0] += gl.x;
-  fa.r[1] += gl.y;
-  if (p.ref_dim == 2) return make_float2(gl.x / L.fw, gl.y / L.fh);
+// The transpose of fused_location_at for one sample: the offset gradient, and the sample's share of
+// the reference-point gradient added into r (x, y, and w, h for boxes).
+__device__ __forceinline__ float2 fused_offset_grad(float2 gl, float4 ref, float2 t, float fw, float fh, int ref_dim,
+                                                    float inv_points, float fpoints, float (&r)[4]) {
+  r[0] += gl.x;
+  r[1] += gl.y;
+  if (ref_dim == 2) return make_float2(gl.x / fw, gl.y / fh);
   const float hx = gl.x * 0.5f, hy = gl.y * 0.5f;
-  fa.r[2] += hx * t.x;
-  fa.r[3] += hy * t.y;
-  if (p.inv_points != 0.0f) return make_float2((hx * r.z) * p.inv_points, (hy * r.w) * p.inv_points);
-  return make_float2((hx * r.z) / p.fpoints, (hy * r.w) / p.fpoints);
-}
-
-// End of a level: sums the reference-point gradient over the head group's lanes (hg * lanes per
-// (query, head) <= 64, a power of two, so the group is aligned inside one wave) and writes it for
-// (head group, b, q, level); the sum over groups is ref_grad_kernel's.
-__device__ __forceinline__ void flush_ref_grad(FusedAcc& fa, const SampleParams& p, int hl, int j, int64_t bq, int group,
-                                               int l) {
-  const int lpq = 1 << p.lpq_shift;
-  for (int o = lpq; o < (lpq * p.hg); o <<= 1) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) fa.r[k] += __shfl_xor(fa.r[k], o, 64);
-  }
-  if (p.dref != nullptr && hl == 0 && j == 0) {
-    // group-major [H / hg][B * Q][L][ref_dim], so the reduction reads each group's rows contiguously
-    float* d = p.dref + ((static_cast<int64_t>(group) * p.bq_total + bq) * p.levels + l) * p.ref_dim;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (k < p.ref_dim) d[k] = fa.r[k];  // constant indices keep fa.r in registers
-  }
-#pragma unroll
-  for (int k = 0; k < 4; ++k) fa.r[k] = 0.0f;
-}
-
-// Softmax VJP of one row, after every sample's dA is in grad_logits:
-// grad_logit_k = a_k * (dA_k - sum_j a_j dA_j) (the transpose of jax.nn.softmax's JVP).
-__device__ __forceinline__ void fused_logit_grads(const float* __restrict__ logits, float* glog, int LP, SoftmaxStats st,
-                                                  float S) {
-  for (int k = 0; k < LP; ++k) glog[k] = softmax_weight(logits[k], st) * (glog[k] - S);
+  r[2] += hx * t.x;
+  r[3] += hy * t.y;
+  if (inv_points != 0.0f) return make_float2((hx * ref.z) * inv_points, (hy * ref.w) * inv_points);
+  return make_float2((hx * ref.z) / fpoints, (hy * ref.w) / fpoints);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -847,7 +707,7 @@ fwd_kernel(const SampleParams p) {
   const int q_lo = it.qb * p.qblock;
   const int q_hi = min(p.queries, q_lo + p.qblock);
   const float2* __restrict__ loc2 = reinterpret_cast<const float2*>(p.loc);
-  constexpr int QU = query_group(NS, VEC, false, kFused);
+  constexpr int QU = query_group(NS, VEC, kFused);
   constexpr int NI = NS == 0 ? 1 : NS;
   const int q_first = q_lo + ln.qs;
   const int64_t row_first = (static_cast<int64_t>(it.b) * p.queries + q_first) * p.heads + h;  // (b, q, h)
@@ -932,705 +792,12 @@ fwd_kernel(const SampleParams p) {
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// backward, per sample: grad_attention_weights, grad_sampling_locations, grad_value records
-
-template <typename VT, int VEC, bool kLds>
-__device__ __forceinline__ void corner_dots(const VT* base, const Bilinear& c, const float (&g)[VEC], float& d00,
-                                            float& d10, float& d01, float& d11, int rot) {
-  float u0[VEC], u1[VEC];
-  load_rot<VT, VEC, kLds>(base + c.o00, rot, u0);
-  load_rot<VT, VEC, kLds>(base + c.o10, rot, u1);
-  d00 = 0.0f;
-  d10 = 0.0f;
-#pragma unroll
-  for (int k = 0; k < VEC; ++k) {
-    d00 = fmaf(g[k], u0[k], d00);
-    d10 = fmaf(g[k], u1[k], d10);
-  }
-  load_rot<VT, VEC, kLds>(base + c.o01, rot, u0);
-  load_rot<VT, VEC, kLds>(base + c.o11, rot, u1);
-  d01 = 0.0f;
-  d11 = 0.0f;
-#pragma unroll
-  for (int k = 0; k < VEC; ++k) {
-    d01 = fmaf(g[k], u0[k], d01);
-    d11 = fmaf(g[k], u1[k], d11);
-  }
-}
-
-// Appends a record to the bin of (slice n, item) for this workgroup's query block; the rank comes
-// from the workgroup's LDS counter of that (head, item).
 // base[idx] with the byte offset formed in 32 bits (the caller guarantees idx * sizeof(T) < 2^32):
 // a uniform base plus a 32-bit lane offset compiles to one address operand per access.
 template <typename T>
 __device__ __forceinline__ T* at(T* base, uint32_t idx) {
   using C = typename std::conditional<std::is_const<T>::value, const char, char>::type;
   return reinterpret_cast<T*>(reinterpret_cast<C*>(base) + idx * static_cast<uint32_t>(sizeof(T)));
-}
-
-// Per-workgroup bases of the per-sample pass: row (b, q_lo, h0) of the [B, Q, H, ...] tensors and
-// the record bins of slice (b, h0). Lanes index them with 32-bit offsets.
-struct SampleBases {
-  const float2* loc;
-  const float* attn;
-  const char* gout;  // bytes
-  float* dattn;
-  float2* dloc;
-  uint4* bins;
-};
-
-__device__ __forceinline__ void emit_record(const SampleParams& p, const SampleBases& sb, int* lcnt, int hl, int item, int key,
-                                            int qoff, int qb, uint4 payload) {
-  const int pos = atomicAdd(&lcnt[hl * p.nwork + item], 1);
-  payload.x = static_cast<uint32_t>(key) | (static_cast<uint32_t>(qoff) << 16);
-  // bins of the workgroup's slices: [hg][nwork][nqb][qblock * points]; below 2^24 records in all
-  // (small_bins) every factor fits a 24-bit multiply, and the region stays below 2^28 records
-  // (16-byte offsets in 32 bits) in any case (both checked on the host)
-  const uint32_t subcap = static_cast<uint32_t>(p.qblock) * static_cast<uint32_t>(p.points);
-  uint32_t idx;
-  if (p.small_bins) {
-    const uint32_t bin = __umul24(__umul24(static_cast<uint32_t>(hl), static_cast<uint32_t>(p.nwork)) + static_cast<uint32_t>(item),
-                                  static_cast<uint32_t>(p.nqb)) + static_cast<uint32_t>(qb);
-    idx = __umul24(bin, subcap) + static_cast<uint32_t>(pos);
-  } else {
-    idx = ((static_cast<uint32_t>(hl) * p.nwork + item) * p.nqb + qb) * subcap + static_cast<uint32_t>(pos);
-  }
-  *at(sb.bins, idx) = payload;
-}
-
-// kKeepDA (fused, grouped path): each sample's dA stays in dA_out for the softmax VJP, instead
-// of passing through grad_logits in memory.
-template <typename VT, int VEC, int N, bool kStaged, bool kFused, bool kKeepDA = false>
-__device__ __forceinline__ void bwd_pass(const SampleIn<N>& f, const FusedIn<N, kFused>& x, FusedAcc& fa, const float (&g)[VEC],
-                                         int s0, int LP, int& l, int& pt, const SampleParams& p, const SampleLane& ln,
-                                         const VT* hlds, const VT* __restrict__ vs, const SampleBases& sb, uint32_t lrow, int* lcnt,
-                                         int qoff, int qb, int64_t bq, int group, float (&dA_out)[N]) {
-  const int D = p.dim;
-  const int lpq = 1 << p.lpq_shift;
-#pragma unroll
-  for (int u = 0; u < N; ++u) {
-    if (s0 + u < LP) {
-      const LevelDesc L = p.lv[l];
-      const Bilinear c = bilinear(f.xy[u].x, f.xy[u].y, L, D);
-      const float a = f.a[u];
-      float d00, d10, d01, d11;
-      if (kStaged || L.lds >= 0) corner_dots<VT, VEC, true>(hlds + L.lds, c, g, d00, d10, d01, d11, ln.rot);
-      else corner_dots<VT, VEC, false>(vs + static_cast<int64_t>(L.start) * D, c, g, d00, d10, d01, d11, ln.rot);
-      d00 = group_sum(d00, lpq);
-      d10 = group_sum(d10, lpq);
-      d01 = group_sum(d01, lpq);
-      d11 = group_sum(d11, lpq);
-      const uint32_t si = lrow * static_cast<uint32_t>(LP) + static_cast<uint32_t>(s0 + u);  // sample, from the workgroup's row
-      if constexpr (kFused) {
-        // every lane of the head group forms the sample's gradients (their sums over heads are
-        // shuffled between lanes at the end of the level); lane 0 of the (query, head) writes
-        const float dA = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
-        const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
-        const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
-        const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
-        const float2 gl = make_float2(a * L.fw * dx, a * L.fh * dy);
-        const float2 goff = fused_sample_grads(gl, a, dA, x.r[u], x.t[u], L, p, fa);
-        if constexpr (kKeepDA) dA_out[u] = dA;
-        if (ln.j == 0) {
-          if (!kKeepDA && sb.dattn) *at(sb.dattn, si) = dA;  // grad_logits holds dA until fused_logit_grads
-          if (sb.dloc) *at(sb.dloc, si) = goff;
-        }
-        if (p.dref != nullptr && pt + 1 == p.points) flush_ref_grad(fa, p, ln.hl, ln.j, bq, group, l);
-      }
-      if (ln.j == 0) {
-        if constexpr (!kFused) {
-          // dA = sum_c w_c D_c (the sample itself); d out / d ix = gy (m10 D10 - m00 D00) + fy (m11 D11 - m01 D01)
-          if (sb.dattn) *at(sb.dattn, si) = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
-          if (sb.dloc) {
-            const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
-            const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
-            const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
-            // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
-            *at(sb.dloc, si) = make_float2(a * L.fw * dx, a * L.fh * dy);
-          }
-        }
-        if (p.bins) {
-          // Non-finite weights (NaN or infinite coordinates) go to the clipped first corner's cell,
-          // where the reference's scatter-add puts them.
-          const bool finite = isfinite(c.w00) && isfinite(c.w10) && isfinite(c.w01) && isfinite(c.w11);
-          const int x0 = finite ? c.x0 : c.cx0, y0 = finite ? c.y0 : c.cy0;
-          const uint4 payload = make_uint4(0u, __float_as_uint(a * (1.0f - c.fx)), __float_as_uint(a * c.fx), __float_as_uint(c.fy));
-          // the cell's rows y0, y0 + 1 that lie in the level, and the band of each
-          if (x0 >= -1 && x0 <= L.w - 1) {
-            const int ya = y0 >= 0 && y0 < L.h ? y0 : -1;
-            const int yb = y0 + 1 >= 0 && y0 + 1 < L.h ? y0 + 1 : -1;
-            const int ba = ya >= 0 ? band_of(ya, L) : -1;
-            const int bb = yb >= 0 ? band_of(yb, L) : -1;
-            // key: the cell's (row within the band + 1, x0 + 1), row-major over (band_rows + 1) x (w + 1)
-            auto key = [&](int band) {
-              const uint32_t r = static_cast<uint32_t>(y0 + 1) - __umul24(static_cast<uint32_t>(band), static_cast<uint32_t>(L.band_rows));
-              return static_cast<int>(__umul24(r, static_cast<uint32_t>(L.w + 1)) + static_cast<uint32_t>(x0 + 1));
-            };
-            if (ba >= 0) emit_record(p, sb, lcnt, ln.hl, L.band_first + ba, key(ba), qoff, qb, payload);
-            if (bb >= 0 && bb != ba) emit_record(p, sb, lcnt, ln.hl, L.band_first + bb, key(bb), qoff, qb, payload);
-          }
-        }
-      }
-      if (++pt == p.points) {
-        pt = 0;
-        ++l;
-      }
-    }
-  }
-}
-
-// kFused: `loc` / `attn` are raw offsets and logits; `dloc` / `dattn` receive grad_offsets /
-// grad_logits and `dref` the per-head-group reference-point gradients.
-template <typename VT, int VEC, int NS, bool kStaged, bool kFused>
-__global__ void __launch_bounds__(kSampleMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
-bwd_sample_kernel(const SampleParams p) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  VT* lds = reinterpret_cast<VT*>(lds_raw);
-  const SampleItem it = sample_item(p);
-  const SampleLane ln = sample_lane<VT, VEC>(p);
-  const int D = p.dim;
-  const int64_t slice_elems = p.len_value * D;
-  const VT* __restrict__ vg = static_cast<const VT*>(p.value) + (static_cast<int64_t>(it.b) * p.heads + it.h0) * slice_elems;
-  const int LP = p.levels * p.points;
-  const int q_lo = it.qb * p.qblock;
-  const int q_hi = min(p.queries, q_lo + p.qblock);
-  const bool gbf = p.gout_bf16 != 0;
-  // the workgroup's row (b, q_lo, h0) of the [B, Q, H, ...] tensors and its slices' record bins;
-  // lane row r = (q - q_lo) * H + hl indexes them with 32-bit offsets
-  const int64_t wrow = (static_cast<int64_t>(it.b) * p.queries + q_lo) * p.heads + it.h0;
-  SampleBases sb;
-  sb.loc = reinterpret_cast<const float2*>(p.loc) + wrow * LP;
-  sb.attn = p.attn + wrow * LP;
-  sb.gout = static_cast<const char*>(p.gout) + wrow * D * (gbf ? 2 : 4);
-  sb.dattn = p.dattn ? p.dattn + wrow * LP : nullptr;
-  sb.dloc = p.dloc ? reinterpret_cast<float2*>(p.dloc) + wrow * LP : nullptr;
-  sb.bins = p.bins ? p.bins + (static_cast<int64_t>(it.b) * p.heads + it.h0) * p.nwork * p.nqb * static_cast<int64_t>(p.qblock) * p.points
-                   : nullptr;
-  auto lrow_of = [&](int q) { return __umul24(static_cast<uint32_t>(q - q_lo), static_cast<uint32_t>(p.heads)) + static_cast<uint32_t>(ln.hl); };
-  // per (head, item) record counters of this workgroup, after the staged value rows
-  int* lcnt = reinterpret_cast<int*>(lds_raw + align16i(p.hg * p.head_lds * static_cast<int>(sizeof(VT))));
-  const int ncnt = p.bins ? p.hg * p.nwork : 0;
-  for (int i = threadIdx.x; i < ncnt; i += blockDim.x) lcnt[i] = 0;
-  constexpr int QU = query_group(NS, VEC, true, kFused);
-  constexpr int NI = NS == 0 ? 1 : NS;
-  const int q_first = q_lo + ln.qs;
-  const uint32_t lrow_first = lrow_of(q_first);
-  const uint32_t lrow_step = __umul24(static_cast<uint32_t>(ln.qpp), static_cast<uint32_t>(p.heads));
-  const int64_t bq0 = static_cast<int64_t>(it.b) * p.queries;
-  const int group = it.h0 / p.hg;
-  SampleIn<NI> in[QU];
-  float g[QU][VEC];
-  // grad_output rows and sample inputs of a group of queries are requested together; the first
-  // group's before the staging copy, so their latency overlaps it.
-  auto load_gout = [&](uint32_t lrow0, int q0) {
-#pragma unroll
-    for (int i = 0; i < QU; ++i) {
-      if (q0 + i * ln.qpp < q_hi) {
-        if (ln.lane_on) {
-          load_any_rot32<VT, VEC>(sb.gout, (lrow0 + i * lrow_step) * static_cast<uint32_t>(D) + static_cast<uint32_t>(ln.c0), gbf,
-                                  ln.rot, g[i]);
-        } else {
-#pragma unroll
-          for (int k = 0; k < VEC; ++k) g[i][k] = 0.0f;
-        }
-      }
-    }
-  };
-  FusedIn<NI, kFused> fin[QU];
-  auto load_inputs = [&](uint32_t lrow0, int q0) {
-#pragma unroll
-    for (int i = 0; i < QU; ++i)
-      if (q0 + i * ln.qpp < q_hi) {
-        const uint32_t r = (lrow0 + i * lrow_step) * static_cast<uint32_t>(LP);
-        load_in<NI>(in[i], at(sb.loc, r), at(sb.attn, r), 0, LP);
-        if constexpr (kFused) load_refs<NI>(fin[i], p, bq0 + q0 + i * ln.qpp, 0, LP, 0, 0);
-      }
-  };
-  if constexpr (NS > 0) {
-    if (ln.active) {
-      load_gout(lrow_first, q_first);
-      load_inputs(lrow_first, q_first);
-    }
-  }
-  stage_group(p, lds, vg);
-  __syncthreads();
-
-  const VT* __restrict__ vs = vg + ln.hl * slice_elems + ln.c0;
-  const VT* hlds = lds + ln.hl * p.head_lds + ln.c0;
-  if constexpr (NS > 0) {
-    uint32_t lrow0 = lrow_first;
-    for (int qg = q_first; ln.active && qg < q_hi; qg += QU * ln.qpp, lrow0 += QU * lrow_step) {
-      if (qg != q_first) {
-        load_gout(lrow0, qg);
-        load_inputs(lrow0, qg);
-      }
-      wait_vmem();
-#pragma unroll
-      for (int i = 0; i < QU; ++i) {
-        const int q = qg + i * ln.qpp;
-        if (q < q_hi) {
-          int l = 0, pt = 0;
-          FusedAcc fa{};
-          float dA[NI];
-          if constexpr (kFused) fused_prologue_row<NI>(in[i], fin[i], p, LP);
-          const uint32_t lrow = lrow0 + i * lrow_step;
-          bwd_pass<VT, VEC, NS, kStaged, kFused, kFused>(in[i], fin[i], fa, g[i], 0, LP, l, pt, p, ln, hlds, vs, sb, lrow, lcnt,
-                                                         q - q_lo, it.qb, bq0 + q, group, dA);
-          if constexpr (kFused) {
-            // softmax VJP from registers: grad_logit_u = a_u (dA_u - sum_k a_k dA_k)
-            if (sb.dattn && ln.j == 0) {
-#pragma unroll
-              for (int u = 0; u < NI; ++u)
-                if (u < LP) *at(sb.dattn, lrow * static_cast<uint32_t>(LP) + u) = in[i].a[u] * (dA[u] - fa.S);
-            }
-          }
-        }
-      }
-    }
-  } else {
-    uint32_t lrow = lrow_first;
-    for (int q = q_first; ln.active && q < q_hi; q += ln.qpp, lrow += lrow_step) {
-      load_gout(lrow, q);
-      int l = 0, pt = 0;
-      const uint32_t r = lrow * static_cast<uint32_t>(LP);
-      SoftmaxStats st{};
-      FusedAcc fa{};
-      if constexpr (kFused) st = softmax_stats(at(sb.attn, r), LP);
-      constexpr int PB = pass_batch(kFused);
-      for (int s0 = 0; s0 < LP; s0 += PB) {
-        SampleIn<PB> f;
-        FusedIn<PB, kFused> x;
-        load_in<PB>(f, at(sb.loc, r), at(sb.attn, r), s0, LP);
-        if constexpr (kFused) {
-          load_refs<PB>(x, p, bq0 + q, s0, LP, l, pt);
-          fused_prologue<PB>(f, x, st, p, s0, LP, l, pt);
-        }
-        float unused[PB];
-        bwd_pass<VT, VEC, PB, kStaged, kFused>(f, x, fa, g[0], s0, LP, l, pt, p, ln, hlds, vs, sb, lrow, lcnt, q - q_lo, it.qb,
-                                               bq0 + q, group, unused);
-      }
-      if constexpr (kFused)
-        if (sb.dattn && ln.j == 0) fused_logit_grads(at(sb.attn, r), at(sb.dattn, r), LP, st, fa.S);
-    }
-  }
-  if (!p.bins) return;
-  // records per (slice, item) of this query block, for the grad_value pass
-  __syncthreads();
-  for (int i = threadIdx.x; i < ncnt; i += blockDim.x) {
-    const int hh = i / p.nwork, item = i - hh * p.nwork;
-    const int64_t nn = static_cast<int64_t>(it.b) * p.heads + it.h0 + hh;
-    p.bin_counts[(nn * p.nwork + item) * p.nqb + it.qb] = lcnt[i];
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// backward, grad_value: one workgroup per (slice, level, band of rows [r0, r1))
-
-// Exclusive prefix sum of cnt[0, n) into off[0, n] (off[n] = total); block-wide, ends in a barrier.
-// cnt is cleared for reuse. `tmp` holds one int per wave.
-__device__ __forceinline__ void block_scan_counts(int* cnt, int* off, int n, int* tmp) {
-  const int nt = blockDim.x, t = threadIdx.x, lane = t & 63;
-  const int per = (n + nt - 1) / nt;
-  const int b0 = min(n, t * per), b1 = min(n, b0 + per);
-  int sum = 0;
-  for (int i = b0; i < b1; ++i) sum += cnt[i];
-  int incl = sum;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int v = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += v;
-  }
-  if (lane == 63) tmp[t >> 6] = incl;
-  __syncthreads();
-  int run = incl - sum;
-  for (int w = 0; w < (t >> 6); ++w) run += tmp[w];
-  for (int i = b0; i < b1; ++i) {
-    off[i] = run;
-    run += cnt[i];
-    cnt[i] = 0;
-  }
-  if (t == nt - 1) off[n] = run;
-  __syncthreads();
-}
-
-// CG channels of a grad_output row: `base` is the (b, q=0, h) row of this workgroup's slice and
-// `off` a 32-bit element offset from it (nch channels valid; the rest read as 0).
-template <int CG>
-__device__ __forceinline__ void load_gc(const void* __restrict__ base, bool bf16, bool vec4, int off, int nch, float (&o)[CG]) {
-  if (nch == CG && vec4) {
-#pragma unroll
-    for (int k = 0; k < CG; k += 4) {
-      if (bf16) {
-        const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const bf16_t*>(base) + off + k);
-        o[k] = __uint_as_float(r.x << 16);
-        o[k + 1] = __uint_as_float(r.x & 0xffff0000u);
-        o[k + 2] = __uint_as_float(r.y << 16);
-        o[k + 3] = __uint_as_float(r.y & 0xffff0000u);
-      } else {
-        const float4 r = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + off + k);
-        o[k] = r.x;
-        o[k + 1] = r.y;
-        o[k + 2] = r.z;
-        o[k + 3] = r.w;
-      }
-    }
-    return;
-  }
-#pragma unroll
-  for (int e = 0; e < CG; ++e) {
-    float x[1] = {0.0f};
-    if (e < nch) load_any<1>(base, off + e, bf16, x);
-    o[e] = x[0];
-  }
-}
-
-// One grad_value task: s[k][e] += w_k * g[q][ch0 + e] over the records [ebeg, eend) of one cell,
-// w_k the record's corner weights (ops.py:123-128 with the attention weight folded in, corner order
-// 00, 10, 01, 11). MODE 0 / 1: f32 / bf16 rows of CG channels at 16-byte-aligned offsets, addressed
-// by a 32-bit byte offset from the slice's first row (one address operation per row); MODE 2:
-// any dtype, alignment and partial channel group.
-template <int CG, int MODE>
-__device__ __forceinline__ void cell_sums(const float4* list, int ebeg, int eend, const void* gbase, bool gbf, bool gv4,
-                                          int ch0, int nch, int Q, int gqstride, float (&s)[4][CG]);
-
-// grad_output rows a grad_value lane fetches together (with their weights): as many as the register
-// budget holds next to the lane's 4 * CG corner sums.
-constexpr int gather_batch(int cg) { return cg >= 8 ? 4 : 8; }
-
-template <int CG, int MODE>
-__device__ __forceinline__ void cell_sums(const float4* list, int ebeg, int eend, const void* gbase, bool gbf, bool gv4,
-                                          int ch0, int nch, int Q, int gqstride, float (&s)[4][CG]) {
-  constexpr int kGatherBatch = gather_batch(CG);
-  const char* gb = static_cast<const char*>(gbase);
-  for (int e0 = ebeg; e0 < eend; e0 += kGatherBatch) {
-    float u[kGatherBatch], v[kGatherBatch], fy[kGatherBatch];
-    float g[kGatherBatch][CG];
-#pragma unroll
-    for (int i = 0; i < kGatherBatch; ++i) {
-      if (e0 + i < eend) {
-        const float4 w = list[e0 + i];
-        u[i] = w.x;
-        v[i] = w.y;
-        fy[i] = w.z;
-        // the record's grad_output row offset (q * H * D, q clamped to Q - 1 when placed; < 2^30,
-        // host-checked) plus this lane's channel group
-        const unsigned el = static_cast<unsigned>(__float_as_int(w.w)) + static_cast<unsigned>(ch0);
-        if constexpr (MODE == 0) {
-          const float4* r = reinterpret_cast<const float4*>(gb + el * 4u);
-#pragma unroll
-          for (int k = 0; k < CG; k += 4) {
-            const float4 x = r[k / 4];
-            g[i][k] = x.x;
-            g[i][k + 1] = x.y;
-            g[i][k + 2] = x.z;
-            g[i][k + 3] = x.w;
-          }
-        } else if constexpr (MODE == 1) {
-          const uint2* r = reinterpret_cast<const uint2*>(gb + el * 2u);
-#pragma unroll
-          for (int k = 0; k < CG; k += 4) {
-            const uint2 x = r[k / 4];
-            g[i][k] = __uint_as_float(x.x << 16);
-            g[i][k + 1] = __uint_as_float(x.x & 0xffff0000u);
-            g[i][k + 2] = __uint_as_float(x.y << 16);
-            g[i][k + 3] = __uint_as_float(x.y & 0xffff0000u);
-          }
-        } else {
-          load_gc<CG>(gbase, gbf, gv4, static_cast<int>(el), nch, g[i]);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kGatherBatch; ++i) {
-      if (e0 + i < eend) {
-        const float w00 = u[i] * (1.0f - fy[i]), w10 = v[i] * (1.0f - fy[i]);
-        const float w01 = u[i] * fy[i], w11 = v[i] * fy[i];
-#pragma unroll
-        for (int e = 0; e < CG; ++e) {
-          s[0][e] = fmaf(w00, g[i][e], s[0][e]);
-          s[1][e] = fmaf(w10, g[i][e], s[1][e]);
-          s[2][e] = fmaf(w01, g[i][e], s[2][e]);
-          s[3][e] = fmaf(w11, g[i][e], s[3][e]);
-        }
-      }
-    }
-  }
-}
-
-// CG: channels per gather lane (4 or 8). NACC: 4 = one accumulator per bilinear corner (conflict-free,
-// no colour passes); 1 = a single accumulator updated in four colour passes per round of tasks
-// (cells of one x/y parity never share a pixel), for bands where four accumulators do not fit.
-// Four waves per SIMD (<= 128 VGPRs) let two 512-thread workgroups share a CU.
-template <typename VT, int CG, int NACC>
-__global__ void __launch_bounds__(kValueMaxThreads) __attribute__((amdgpu_waves_per_eu(4)))
-bwd_value_kernel(const ValueParams p) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  if (p.ref_n > 0)
-    ref_grad_sum(p.ref_part, p.dref, p.ref_n, p.ref_groups, static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x,
-                 static_cast<int64_t>(gridDim.x) * blockDim.x);
-
-  const int lid = xcd_logical(blockIdx.x, gridDim.x);
-  const int h = lid % p.heads;
-  const int rest = lid / p.heads;
-  // Items in reverse order: the bands of the coarsest level start first. A level's samples are
-  // split over its bands, so a coarse level's few bands hold the most records each; started last
-  // (behind a fine level's many light bands), they would set the kernel's tail.
-  const int wk = p.nwork - 1 - rest % p.nwork;
-  const int b = rest / p.nwork;
-  int l = 0;
-  while (l + 1 < p.levels && wk >= p.lv[l + 1].band_first) ++l;
-  const LevelDesc L = p.lv[l];
-  const int W = L.w;
-  const int r0 = (wk - L.band_first) * L.band_rows;
-  const int r1 = min(L.h, r0 + L.band_rows);
-  const int rb = r1 - r0;
-  const int D = p.dim;
-  const int P = p.points;
-  const int Q = p.queries;
-  const int ncell = (rb + 1) * (W + 1);
-  const int64_t n = static_cast<int64_t>(b) * p.heads + h;
-  const int nt = blockDim.x, t = threadIdx.x, lane = t & 63;
-
-  const ValueLayout lay = value_layout(L.band_rows, W, D, p.cap, p.nqb, NACC);
-  float* acc = reinterpret_cast<float*>(lds_raw + lay.acc);
-  int* cnt = reinterpret_cast<int*>(lds_raw + lay.cnt);
-  int* off = reinterpret_cast<int*>(lds_raw + lay.off);
-  int* misc = reinterpret_cast<int*>(lds_raw + lay.misc);  // [2] non-empty cells, [4..] scan scratch
-  uint16_t* nonempty = reinterpret_cast<uint16_t*>(lds_raw + lay.nonempty);
-  int* binpre = reinterpret_cast<int*>(lds_raw + lay.binpre);
-  float4* list = reinterpret_cast<float4*>(lds_raw + lay.list);  // segment's records, in cell order
-
-  // With four accumulators, one per bilinear corner k, a cell adds its corner-k sum to accumulator
-  // k, and distinct cells hit distinct pixels for a fixed k, so no two lanes ever update one element.
-  const int acc_stride = align16i(L.band_rows * W * D * 4) / 4;  // floats between accumulators
-  {
-    const int na = (NACC - 1) * acc_stride + rb * W * D;
-    float4* a4 = reinterpret_cast<float4*>(acc);
-    for (int i = t; i < (na >> 2); i += nt) a4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int i = (na & ~3) + t; i < na; i += nt) acc[i] = 0.0f;
-    for (int i = t; i < ncell; i += nt) cnt[i] = 0;
-    if (t < 4) misc[t] = 0;
-  }
-
-  // This workgroup's records: the bins of (slice n, item wk), one per query block of the
-  // per-sample pass, with their counts; prefix sums of the counts in LDS.
-  const int64_t subcap = static_cast<int64_t>(p.qblock) * P;
-  const SampleRec* __restrict__ R = p.bins ? p.bins + (n * p.nwork + wk) * p.nqb * subcap : nullptr;
-  const int* __restrict__ C = p.bin_counts ? p.bin_counts + (n * p.nwork + wk) * p.nqb : nullptr;
-  // counts loaded in parallel, then an exclusive scan by the first wave (no bins without queries)
-  for (int i = t; i < p.nqb; i += nt) binpre[i + 1] = C ? C[i] : 0;
-  if (t == 0) binpre[0] = 0;
-  __syncthreads();
-  if (t < 64) {
-    int carry = 0;
-    for (int i0 = 0; i0 < p.nqb; i0 += 64) {
-      const int i = i0 + lane;
-      int v = i < p.nqb ? binpre[i + 1] : 0;
-      for (int o = 1; o < 64; o <<= 1) {
-        const int x = __shfl_up(v, o, 64);
-        if (lane >= o) v += x;
-      }
-      if (i < p.nqb) binpre[i + 1] = carry + v;
-      carry += __shfl(v, 63, 64);
-    }
-  }
-  constexpr int U = 8;  // records loaded per thread before use
-  // grad_output row (b, q=0, h); row q is q * H * D elements further (fits 32 bits: checked on the host)
-  const int64_t grow0 = (static_cast<int64_t>(b) * Q * p.heads + h) * D;
-  const void* gbase = p.gout_bf16 ? static_cast<const void*>(static_cast<const bf16_t*>(p.gout) + grow0)
-                                  : static_cast<const void*>(static_cast<const float*>(p.gout) + grow0);
-  const bool gbf = p.gout_bf16 != 0, gv4 = p.g_vec4 != 0;
-  const int gqstride = p.heads * D;
-  const int gpp = (D + CG - 1) / CG;  // channel groups per cell
-  __syncthreads();  // counters cleared, prefix ready
-  const int NR = binpre[p.nqb];
-  // Record f of the workgroup lives in bin `qb` with binpre[qb] <= f < binpre[qb + 1]; a thread's f
-  // only grows, so its bin index only moves forward.
-  auto record = [&](int f, int& qb) {
-    while (binpre[qb + 1] <= f) ++qb;
-    return *reinterpret_cast<const uint4*>(R + qb * subcap + (f - binpre[qb]));
-  };
-  const int ncell_max = ncell;
-
-  // Segments of at most `cap` records (a segment's records all fit the list).
-  for (int s_lo = 0; s_lo < NR;) {
-    const int s_hi = min(NR, s_lo + p.cap);
-    // When the segment is at most U records per thread, pass A also copies each record into the
-    // (not yet used) list LDS at its load position, and pass B reads it from there instead of
-    // loading it from global memory again.
-    const bool one_pass = s_hi - s_lo <= U * nt;
-    uint4* stage = reinterpret_cast<uint4*>(list);
-    // ---- pass A: per-cell counts
-    {
-      int qb = 0;
-      for (int f = s_lo + t; f < s_hi; f += U * nt) {
-        uint4 rr[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) rr[u] = (f + u * nt < s_hi) ? record(f + u * nt, qb) : make_uint4(0xffffu, 0, 0, 0);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const uint32_t key = rr[u].x & 0xffffu;
-          if (static_cast<int>(key) < ncell_max) atomicAdd(&cnt[key], 1);
-          if (one_pass && f + u * nt < s_hi) stage[f + u * nt - s_lo] = rr[u];
-        }
-      }
-    }
-    __syncthreads();
-    // ---- cell offsets (counts cleared: they become the placement cursors) and non-empty cells
-    block_scan_counts(cnt, off, ncell, misc + 4);
-    for (int k0 = 0; k0 < ncell; k0 += nt) {
-      const int key = k0 + t;
-      const bool busy = key < ncell && off[key + 1] > off[key];
-      const uint64_t mask = __ballot(busy);
-      int base = 0;
-      if (lane == 0 && mask) base = atomicAdd(&misc[2], __popcll(mask));
-      base = __shfl(base, 0, 64);
-      if (busy) nonempty[base + __popcll(mask & ((uint64_t{1} << lane) - 1))] = static_cast<uint16_t>(key);
-    }
-    // ---- pass B: each record goes to its place in cell order
-    auto entry = [&](const uint4& r, int qb) {
-      return make_float4(__uint_as_float(r.y), __uint_as_float(r.z), __uint_as_float(r.w),
-                         __int_as_float(min(qb * p.qblock + static_cast<int>(r.x >> 16), Q - 1) * gqstride));
-    };
-    if (one_pass) {
-      // records from the staging copy; every thread reads its records before any is placed
-      uint4 rr[U];
-      int qbs[U], pos[U];
-      int qb = 0;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int f = s_lo + t + u * nt;
-        if (f < s_hi) {
-          while (binpre[qb + 1] <= f) ++qb;
-          rr[u] = stage[f - s_lo];
-        } else {
-          rr[u] = make_uint4(0xffffu, 0, 0, 0);
-        }
-        qbs[u] = qb;
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int key = static_cast<int>(rr[u].x & 0xffffu);
-        pos[u] = key < ncell_max ? off[key] + atomicAdd(&cnt[key], 1) : -1;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (pos[u] >= 0 && pos[u] < p.cap) list[pos[u]] = entry(rr[u], qbs[u]);
-    } else {
-      int qb = 0;
-      for (int f = s_lo + t; f < s_hi; f += U * nt) {
-        uint4 rr[U];
-        int qbs[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          rr[u] = (f + u * nt < s_hi) ? record(f + u * nt, qb) : make_uint4(0xffffu, 0, 0, 0);
-          qbs[u] = qb;
-        }
-        int pos[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int key = static_cast<int>(rr[u].x & 0xffffu);
-          pos[u] = key < ncell_max ? off[key] + atomicAdd(&cnt[key], 1) : -1;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          if (pos[u] >= 0 && pos[u] < p.cap) list[pos[u]] = entry(rr[u], qbs[u]);
-      }
-    }
-    __syncthreads();
-    const int ntask = misc[2] * gpp;
-    // ---- one lane per (non-empty cell, CG channels) task: sum a * w_k * g over the cell's records
-    //      in registers, kGatherBatch grad_output rows in flight, then add corner k's sum to
-    //      accumulator k (conflict-free, so tasks need no barriers between them).
-    for (int t0 = 0; t0 < ntask; t0 += nt) {
-      const int task = t0 + t;
-      int kx = 0, ky = 0, ch0 = 0, nch = 0, ebeg = 0, eend = 0;
-      if (task < ntask) {
-        const int ci = task / gpp, grp = task - ci * gpp;
-        const int key = nonempty[ci];
-        ky = key / (W + 1);
-        kx = key - ky * (W + 1);
-        ch0 = grp * CG;
-        nch = min(CG, D - ch0);
-        ebeg = off[key];
-        eend = off[key + 1];
-      }
-      float s[4][CG];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int e = 0; e < CG; ++e) s[k][e] = 0.0f;
-      // row loads specialised outside the record loop: f32 or bf16 rows of full 16-byte-aligned
-      // channel groups, or the general path
-      const int mode = (nch == CG && gv4) ? (gbf ? 1 : 0) : 2;
-      if (mode == 0) cell_sums<CG, 0>(list, ebeg, eend, gbase, gbf, gv4, ch0, nch, Q, gqstride, s);
-      else if (mode == 1) cell_sums<CG, 1>(list, ebeg, eend, gbase, gbf, gv4, ch0, nch, Q, gqstride, s);
-      else cell_sums<CG, 2>(list, ebeg, eend, gbase, gbf, gv4, ch0, nch, Q, gqstride, s);
-      // With one accumulator, cells of one colour (x and y parity) are updated per pass.
-      const int color = (kx & 1) | ((ky & 1) << 1);
-      for (int c = 0; c < (NACC == 4 ? 1 : 4); ++c) {
-        if (task < ntask && (NACC == 4 || color == c)) {
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            // corner k of cell (kx, ky) is pixel (kx - 1 + (k & 1), ky - 1 + (k >> 1)) of the band
-            const int px = kx - 1 + (k & 1), py = ky - 1 + (k >> 1);
-            if (px >= 0 && px < W && py >= 0 && py < rb) {
-              float* ap = acc + (NACC == 4 ? k * acc_stride : 0) + (py * W + px) * D + ch0;
-              if (nch == CG && (D & 3) == 0) {
-#pragma unroll
-                for (int e = 0; e < CG; e += 4) {
-                  float4 o = *reinterpret_cast<float4*>(ap + e);
-                  o.x += s[k][e];
-                  o.y += s[k][e + 1];
-                  o.z += s[k][e + 2];
-                  o.w += s[k][e + 3];
-                  *reinterpret_cast<float4*>(ap + e) = o;
-                }
-              } else {
-#pragma unroll
-                for (int e = 0; e < CG; ++e)
-                  if (e < nch) ap[e] += s[k][e];
-              }
-            }
-          }
-        }
-        if (NACC == 1) __syncthreads();
-      }
-    }
-    __syncthreads();  // every task done before the cell tables are reused
-    // the placement cursors start the next segment at zero
-    for (int i = t; i < ncell; i += nt) cnt[i] = 0;
-    if (t == 0) misc[2] = 0;
-    __syncthreads();
-    s_lo = s_hi;
-  }
-
-  // ---- the band's grad_value rows, once, in the value dtype (the sum of the accumulators)
-  VT* dst = static_cast<VT*>(p.dvalue) + (n * p.len_value + L.start + static_cast<int64_t>(r0) * W) * D;
-  const int na = rb * W * D;
-  if (p.vec16 && (na & 3) == 0) {
-    for (int i = t; i < (na >> 2); i += nt) {
-      float4 a = reinterpret_cast<const float4*>(acc)[i];
-#pragma unroll
-      for (int k = 1; k < NACC; ++k) {
-        const float4 b = reinterpret_cast<const float4*>(acc + k * acc_stride)[i];
-        a.x += b.x;
-        a.y += b.y;
-        a.z += b.z;
-        a.w += b.w;
-      }
-      const float o[4] = {a.x, a.y, a.z, a.w};
-      store_vec<VT, 4>(dst + 4 * i, o);
-    }
-  } else {
-    for (int i = t; i < na; i += nt) {
-      float o[1] = {acc[i]};
-#pragma unroll
-      for (int k = 1; k < NACC; ++k) o[0] += acc[i + k * acc_stride];
-      store_vec<VT, 1>(dst + i, o);
-    }
-  }
 }
 
 }  // namespace msda

@@ -44,26 +44,6 @@ int launch_fwd(const msda::SampleParams& p, int grid, int threads, int lds, hipS
   return check_launch("msda forward");
 }
 
-template <typename VT, int VEC, int NS, bool STAGED, bool FUSED>
-int launch_bwd_sample(const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t stream) {
-  static std::atomic<int> granted[kMaxDevices];
-  auto k = msda::bwd_sample_kernel<VT, VEC, NS, STAGED, FUSED>;
-  int rc = allow_lds(k, lds, granted);
-  if (rc != MSDA_OK) return rc;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
-  return check_launch("msda backward (per-sample pass)");
-}
-
-template <typename VT, int CG, int NACC>
-int launch_bwd_value(const msda::ValueParams& p, int grid, int threads, int lds, hipStream_t stream) {
-  static std::atomic<int> granted[kMaxDevices];
-  auto k = msda::bwd_value_kernel<VT, CG, NACC>;
-  int rc = allow_lds(k, lds, granted);
-  if (rc != MSDA_OK) return rc;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
-  return check_launch("msda backward (grad_value pass)");
-}
-
 template <typename VT, typename GT, int CH, int KD>
 int launch_bwd_band(const msda::BandParams& p, int grid, int threads, int lds, hipStream_t stream) {
   static std::atomic<int> granted[kMaxDevices];
@@ -142,18 +122,6 @@ int fwd_ns(int ns, const msda::SampleParams& p, int grid, int threads, int lds, 
   }
 }
 
-template <typename VT, int VEC, bool FUSED>
-int bwd_ns(int ns, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t st) {
-  const bool staged = p.all_staged != 0;
-  switch (ns) {
-    case 2: return staged ? launch_bwd_sample<VT, VEC, 2, true, FUSED>(p, grid, threads, lds, st)
-                          : launch_bwd_sample<VT, VEC, 2, false, FUSED>(p, grid, threads, lds, st);
-    case 4: return staged ? launch_bwd_sample<VT, VEC, 4, true, FUSED>(p, grid, threads, lds, st)
-                          : launch_bwd_sample<VT, VEC, 4, false, FUSED>(p, grid, threads, lds, st);
-    default: return launch_bwd_sample<VT, VEC, 0, false, FUSED>(p, grid, threads, lds, st);
-  }
-}
-
 template <typename VT>
 int dispatch_fwd(int vec, int ns, bool fused, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t st) {
   switch (vec) {
@@ -166,32 +134,9 @@ int dispatch_fwd(int vec, int ns, bool fused, const msda::SampleParams& p, int g
   return fail(MSDA_ERR_UNSUPPORTED, "no kernel for %d channels per lane", vec);
 }
 
-template <typename VT>
-int dispatch_bwd_sample(int vec, int ns, bool fused, const msda::SampleParams& p, int grid, int threads, int lds, hipStream_t st) {
-  switch (vec) {
-    case 1: return fused ? bwd_ns<VT, 1, true>(ns, p, grid, threads, lds, st) : bwd_ns<VT, 1, false>(ns, p, grid, threads, lds, st);
-    case 2: return fused ? bwd_ns<VT, 2, true>(ns, p, grid, threads, lds, st) : bwd_ns<VT, 2, false>(ns, p, grid, threads, lds, st);
-    case 4: return fused ? bwd_ns<VT, 4, true>(ns, p, grid, threads, lds, st) : bwd_ns<VT, 4, false>(ns, p, grid, threads, lds, st);
-    case 8: return fused ? bwd_ns<VT, 8, true>(ns, p, grid, threads, lds, st) : bwd_ns<VT, 8, false>(ns, p, grid, threads, lds, st);
-    case 16: return fused ? bwd_ns<VT, 16, true>(ns, p, grid, threads, lds, st) : bwd_ns<VT, 16, false>(ns, p, grid, threads, lds, st);
-  }
-  return fail(MSDA_ERR_UNSUPPORTED, "no kernel for %d channels per lane", vec);
-}
-
-template <typename VT>
-int dispatch_value(int cg, int nacc, const msda::ValueParams& vp, int grid, int threads, int lds, hipStream_t st) {
-  if (cg == 8)
-    return nacc == 4 ? launch_bwd_value<VT, 8, 4>(vp, grid, threads, lds, st) : launch_bwd_value<VT, 8, 1>(vp, grid, threads, lds, st);
-  return nacc == 4 ? launch_bwd_value<VT, 4, 4>(vp, grid, threads, lds, st) : launch_bwd_value<VT, 4, 1>(vp, grid, threads, lds, st);
-}
-
 // Instantiated in msda_fwd_f32.hip, msda_fwd_bf16.hip, msda_bwd_f32.hip and msda_bwd_bf16.hip.
 extern template int dispatch_fwd<float>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
 extern template int dispatch_fwd<msda::bf16_t>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
-extern template int dispatch_bwd_sample<float>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
-extern template int dispatch_bwd_sample<msda::bf16_t>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
-extern template int dispatch_value<float>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
-extern template int dispatch_value<msda::bf16_t>(int, int, const msda::ValueParams&, int, int, int, hipStream_t);
 extern template int dispatch_bwd_band<float>(int, const msda::BandParams&, int, int, int, hipStream_t);
 extern template int dispatch_bwd_band<msda::bf16_t>(int, const msda::BandParams&, int, int, int, hipStream_t);
 extern template int launch_part_sum<float>(const float*, int, int64_t, void*, int, hipStream_t);

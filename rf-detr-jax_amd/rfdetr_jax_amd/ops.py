@@ -333,13 +333,12 @@ def ms_deform_attn_fused_backward(value, spatial_shapes, reference_points, sampl
     grad_logits = torch.empty(logits.shape, dtype=torch.float32, device=dev) if needs[3] else None
     arr, starts = _shape_arrays(shapes)
     lib = _native.lib()
-    workspace, ws_bytes = None, 0
-    if grad_value is not None or grad_ref is not None:
-        ws_bytes = lib.msda_fused_bwd_workspace_size(batch, n_heads, head_dim, len_query, n_levels, n_points, ref_dim, arr,
-                                                     starts, value.shape[1])
-        if ws_bytes < 0:
-            _native.check(int(ws_bytes))
-        workspace = torch.empty((max(1, ws_bytes // 16), 4), dtype=torch.int32, device=dev)
+    # the prologue's locations and weights and the query blocks' partial sums (any gradient needs it)
+    ws_bytes = lib.msda_fused_bwd_workspace_size(batch, n_heads, head_dim, len_query, n_levels, n_points, ref_dim, arr,
+                                                 starts, value.shape[1])
+    if ws_bytes < 0:
+        _native.check(int(ws_bytes))
+    workspace = torch.empty((max(1, ws_bytes // 16), 4), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         rc = lib.msda_fused_bwd(
             _ptr(value), _VALUE_DTYPES[value.dtype], _ptr(ref), ref_dim, _ptr(off), _ptr(logits), _ptr(grad_output),

@@ -276,10 +276,11 @@ def test_fused_workspace_size_validates_first():
     assert f(1, 2, 16, 0, 1, 2, 2, _shapes([(4, 4)]), _starts([0]), 16) == 0
 
 
-def test_fused_workspace_needed_for_grad_value_or_reference_points():
+def test_fused_workspace_needed_for_any_gradient():
+    """The prologue's locations and weights live in the workspace, whatever gradient is asked."""
     rc, msg = _fbwd(ws=0)
     assert rc == _native.ERR_INVALID_ARGUMENT and "workspace" in msg
-    rc, msg = _fbwd(ws=0, dv=0)  # grad_reference_points alone may still need the partial sums
+    rc, msg = _fbwd(ws=0, dv=0, dref=0, dlog=0)  # grad_sampling_offsets alone
     assert rc == _native.ERR_INVALID_ARGUMENT and "workspace" in msg
 
 

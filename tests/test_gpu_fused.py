@@ -119,10 +119,9 @@ def test_fused_full_size_against_c_oracle(ref_dim):
 @pytest.mark.parametrize("variant", [
     {"MSDA_FWD_GROUPED": "0"},          # per-query forward loop
     {"MSDA_FWD_PAIR": "0"},             # grouped forward without paired lanes
-    {"MSDA_FUSED_BWD_MAX_VEC": "16"},   # one lane per (query, head) in the backward
-    {"MSDA_FUSED_BWD_MAX_VEC": "4"},    # four lanes per (query, head): head-group shuffles over 16 lanes
-    {"MSDA_BWDS_HEADS": "1"},           # one head per group: 16 partial sums per reference point
-    {"MSDA_BWDS_HEADS": "2"},
+    {"MSDA_BWD_MAX_VEC": "16"},         # backward band kernel: one lane per (query, head)
+    {"MSDA_BWD_MAX_VEC": "4"},          # four lanes per (query, head)
+    {"MSDA_BWD_FORCE_BANDS": "1", "MSDA_BWD_BANDS": "5"},  # row bands: points straddle bands
 ], ids=lambda v: ",".join(f"{k}={x}" for k, x in v.items()))
 def test_fused_kernel_variants(tune, variant):
     for k, x in variant.items():
@@ -135,9 +134,9 @@ def test_fused_kernel_variants(tune, variant):
     _check(out, grads, want_out, want_grads, False)
 
 
-def test_fused_all_heads_in_one_group():
-    """Four heads and a small level: one head group holds every head, so the kernel writes
-    grad_reference_points directly (no partial sums, no second kernel)."""
+def test_fused_three_points_four_heads():
+    """Four heads, three points (n_points not a power of two: the box form divides), one small
+    level; the epilogue sums grad_reference_points over four head lanes."""
     shapes = ((16, 16),)
     value, ref, off, logits, grad = make_fused_inputs(12, 3, 4, 16, 97, shapes, 3, 2)
     out, grads = _run_fused(value, shapes, ref, off, logits, grad)
