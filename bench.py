@@ -11,6 +11,12 @@ not what is measured) between two events on the launch stream, synchronised on b
 same K steps launched eagerly from Python are reported beside it. The dominant kernel's
 average duration is measured with events around graph replays of that kernel alone.
 
+Roofline: the dominant kernel's algorithmic HBM bytes (Workload.hbm_bytes) against 8 TB/s and its
+algorithmic LDS bytes (Workload.lds_bytes) against the LDS read peak measured in the same run by
+the library's probe (msda_probe_lds_read); `bound` is the resource whose time is larger. Configs
+2 and 4 are also timed Infinity-Cache-cold ("cold" in per_config): the steps cycle through enough
+copies of the buffers that one pass over them exceeds the 256 MiB cache.
+
 CPU baseline: the repository's C restatement of the reference gather path (oracle/msda_ref.c,
 OpenMP over slices) on the same inputs, on this host's cores (at most 16), rank 0 only.
 
@@ -35,7 +41,8 @@ for _p in (ROOT, os.path.join(ROOT, "rf-detr-jax_amd")):
 
 METRIC = "deform-attn fwd+bwd μs/call + achieved HBM GB/s (% peak), Nano group-DETR shape"
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
-LDS_PEAK_GBPS = 256 * 128 * 2.4  # 256 CUs x 128 B/clk x 2.4 GHz (conservative)
+LDS_PEAK_NOMINAL_GBPS = 256 * 128 * 2.4  # 256 CUs x 128 B/clk x 2.4 GHz, used only if the probe fails
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
 
 
 def log(msg):
@@ -421,6 +428,66 @@ def measure_attention(dev, steps, batch=8, groups=13, per=300, heads=8, head_dim
     }
 
 
+def lds_peak(dev, blocks=5120, reps=256, trials=5):
+    """Device LDS read bandwidth (GB/s), measured with the library's probe (msda_probe_lds_read:
+    ds_read_b128, contiguous 1 KB per wave instruction) on the current stream: best of `trials`."""
+    import torch
+
+    from rfdetr_jax_amd import _native
+
+    lib = _native.lib()
+    out = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    ptr = ctypes.c_void_p(out.data_ptr())
+    nbytes = lib.msda_probe_lds_read_bytes(blocks, reps)
+    h = _stream_handle()
+    _native.check(0 if lib.msda_probe_lds_read(ptr, blocks, reps, h) == 0 else _native.ERR_LAUNCH)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(trials):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        lib.msda_probe_lds_read(ptr, blocks, reps, h)
+        end.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1000.0
+        best = us if best is None else min(best, us)
+    return {"gbps": round(nbytes / best / 1e3, 1), "bytes": nbytes, "us": round(best, 3), "blocks": blocks, "reps": reps,
+            "probe": "msda_probe_lds_read (ds_read_b128, 1 KB per wave instruction)"}
+
+
+def measure_cold(w, dev, steps):
+    """The step with its inputs and outputs not cache-resident: enough copies of the workload's
+    buffers (at least three) that one pass over them exceeds the 256 MiB Infinity Cache; a HIP
+    graph replays the steps cycling through the copies, so each step finds its data evicted by the
+    steps of the other copies."""
+    per_set = w.hbm_bytes()["total"]
+    sets = max(3, -(-(MALL_BYTES + (64 << 20)) // per_set))
+    calls = [Calls(w, dev) for _ in range(sets)]
+
+    def step(h):
+        for c in calls:
+            c.fwd(h)
+            if w.backward:
+                c.bwd(h)
+
+    def only(k):
+        def fn(h):
+            for c in calls:
+                getattr(c, k)(h)
+        return fn
+
+    reps = max(1, steps // sets)
+    res = {"sets": sets, "bytes_per_set": per_set}
+    us, n = time_graph(step, reps, iters_per_graph=max(1, min(20, reps)))
+    res["step_us"] = round(us / sets, 3)
+    res["fwd_us"] = round(time_graph(only("fwd"), reps, iters_per_graph=max(1, min(20, reps)))[0] / sets, 3)
+    if w.backward:
+        res["bwd_us"] = round(time_graph(only("bwd"), reps, iters_per_graph=max(1, min(20, reps)))[0] / sets, 3)
+    res["step_hbm_frac"] = round(per_set / (res["step_us"] * 1e3) / HBM_PEAK_GBPS, 4)
+    del calls
+    return res
+
+
 def cpu_baseline(calls, budget_s=3.0, max_reps=20):
     """fwd+bwd of the C oracle on the same inputs; median us/call."""
     from oracle import cref
@@ -528,17 +595,34 @@ def main():
     log(f"step {res['step_us_graph']:.2f} us (graph), {res['step_us_eager']:.2f} us (eager); fwd {res['fwd_us']:.2f} us"
         + (f", bwd {res['bwd_us']:.2f} us" if w.backward else ""))
 
+    log("LDS peak (probe)")
+    try:
+        lds = lds_peak(dev)
+    except Exception as e:  # the probe is a measurement aid; the roofline then uses the nominal peak
+        log(f"LDS probe failed ({e}); nominal {LDS_PEAK_NOMINAL_GBPS:.0f} GB/s")
+        lds = {"gbps": LDS_PEAK_NOMINAL_GBPS, "probe": "nominal (probe failed)"}
+    lds_peak_gbps = lds["gbps"]
+    log(f"LDS read peak {lds_peak_gbps:.0f} GB/s")
+
     kernels = {"fwd": (res["fwd_us"], res["hbm_bytes"]["fwd"])}
     if w.backward:
         kernels["bwd"] = (res["bwd_us"], res["hbm_bytes"]["bwd"])
     dom = max(kernels, key=lambda k: kernels[k][0])
     dom_us, dom_bytes = kernels[dom]
-    achieved = dom_bytes / dom_us / 1e3
+    dom_lds = w.lds_bytes()[dom]
+    t_hbm = dom_bytes / HBM_PEAK_GBPS / 1e3  # us
+    t_lds = dom_lds / lds_peak_gbps / 1e3
+    bound = "hbm" if t_hbm >= t_lds else "lds"
+    achieved = (dom_bytes if bound == "hbm" else dom_lds) / dom_us / 1e3
+    peak = HBM_PEAK_GBPS if bound == "hbm" else lds_peak_gbps
     traffic = None
+    lds_counters = None
     tfile = os.path.join(ROOT, "profiles", f"traffic_{w.name}.json")
     if os.path.exists(tfile):
         # calibrated FETCH_SIZE + WRITE_SIZE of the kernel, from the rocprofv3 counter passes that file records
-        traffic = json.load(open(tfile)).get("kernels", {}).get(dom, {}).get("hbm_bytes_per_launch")
+        tinfo = json.load(open(tfile))
+        traffic = tinfo.get("kernels", {}).get(dom, {}).get("hbm_bytes_per_launch")
+        lds_counters = tinfo.get("lds", {}).get(dom)
 
     per_config = {}
     if not args.no_per_config:
@@ -548,11 +632,18 @@ def main():
             else:
                 log(f"workload {cw.name}")
                 r, _ = measure(cw, dev, max(50, args.steps // 4), 10)
+            lb = cw.lds_bytes()
             entry = {"step_us": round(r["step_us_graph"], 3), "fwd_us": round(r["fwd_us"], 3),
                      "fwd_hbm_gbps": round(r["fwd_gbps"], 1), "hbm_bytes": r["hbm_bytes"]["total"],
-                     "step_hbm_frac": round(r["step_gbps"] / HBM_PEAK_GBPS, 4)}
+                     "step_hbm_frac": round(r["step_gbps"] / HBM_PEAK_GBPS, 4),
+                     "lds_bytes": lb["total"], "fwd_lds_gbps": round(lb["fwd"] / r["fwd_us"] / 1e3, 1),
+                     "step_lds_frac": round(lb["total"] / r["step_us_graph"] / 1e3 / lds_peak_gbps, 4)}
             if cw.backward:
-                entry.update({"bwd_us": round(r["bwd_us"], 3), "bwd_hbm_gbps": round(r["bwd_gbps"], 1)})
+                entry.update({"bwd_us": round(r["bwd_us"], 3), "bwd_hbm_gbps": round(r["bwd_gbps"], 1),
+                              "bwd_lds_gbps": round(lb["bwd"] / r["bwd_us"] / 1e3, 1)})
+            if cid in (2, 4):
+                log(f"workload {cw.name}: Infinity-Cache-cold steps")
+                entry["cold"] = measure_cold(cw, dev, max(60, args.steps // 2))
             per_config[cw.name] = entry
         if w.backward:
             log("fused prologue")
@@ -590,9 +681,15 @@ def main():
         "achieved_hbm_gbps": round(res["step_gbps"], 1),
         "hbm_peak_frac": round(res["step_gbps"] / HBM_PEAK_GBPS, 4),
         "eager_us_per_call": round(res["step_us_eager"], 3),
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "algorithmic_bytes": dom_bytes, "avg_launch_us": round(dom_us, 3)},
+        "cold_us_per_call": per_config.get(w.name, {}).get("cold", {}).get("step_us"),
+        "roofline": {"bound": bound, "kernel": dom, "achieved": round(achieved, 1), "peak": peak,
+                     "unit": "GB/s", "frac": round(achieved / peak, 4), "traffic": traffic,
+                     "algorithmic_bytes": dom_bytes, "avg_launch_us": round(dom_us, 3),
+                     "hbm": {"algorithmic_bytes": dom_bytes, "achieved": round(dom_bytes / dom_us / 1e3, 1),
+                             "peak": HBM_PEAK_GBPS, "time_us": round(t_hbm, 3)},
+                     "lds": {"algorithmic_bytes": dom_lds, "achieved": round(dom_lds / dom_us / 1e3, 1),
+                             "peak": lds_peak_gbps, "peak_source": lds.get("probe"), "time_us": round(t_lds, 3),
+                             "counters": lds_counters}},
         "cpu_baseline": cpu,
         "per_config": per_config,
     }

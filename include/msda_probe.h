@@ -1,0 +1,31 @@
+/*
+ * msda_probe.h — device probes of the gfx950 library, for the benchmark's roofline (no
+ * counterpart in the reference: RF-DETR-JAX has no on-device measurement of its own).
+ */
+#ifndef MSDA_PROBE_H_
+#define MSDA_PROBE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * LDS read bandwidth: launches `blocks` workgroups of 256 threads on `stream`, each streaming
+ * 16-byte LDS reads (ds_read_b128, contiguous 1 KB per wave instruction) `reps` times over eight
+ * 1 KB blocks; writes one 32-bit word per thread to `out` (blocks * 256 words, device memory) so
+ * that the reads are kept. The caller times the launch (for example with events on `stream`) and
+ * divides msda_probe_lds_read_bytes(blocks, reps) by the time. Returns 0, -1 on a bad argument,
+ * -3 on a launch failure.
+ */
+int msda_probe_lds_read(unsigned* out, int blocks, int reps, void* stream);
+
+/* Bytes of LDS the probe reads for (blocks, reps): blocks * 256 threads * reps * 8 reads * 16 B. */
+int64_t msda_probe_lds_read_bytes(int blocks, int reps);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSDA_PROBE_H_ */

@@ -336,8 +336,24 @@ struct BandPlan {
 };
 
 // Bytes of the backward's workspace for a plan: the query blocks' partial grad_value sums.
+// f32 partial sums of one query block: every grad_value element, rounded up to whole quads
+int64_t part_block_stride(const Shape& s) { return (static_cast<int64_t>(s.batch) * s.heads * s.len_value * s.dim + 3) / 4 * 4; }
+
 int64_t band_workspace(const Shape& s, const BandPlan& bp) {
-  return bp.nqb > 1 ? align16(static_cast<int64_t>(bp.nqb) * s.batch * s.heads * s.len_value * s.dim * 4) : 0;
+  return bp.nqb > 1 ? static_cast<int64_t>(bp.nqb) * part_block_stride(s) * 4 : 0;
+}
+
+// The second kernel of a split backward: grad_value = sum of the blocks' partials, in block order.
+int launch_partial_sums(const Shape& s, int value_dtype, const float* part, int nqb, void* grad_value, const DevInfo& dev,
+                        hipStream_t st) {
+  const int64_t n = static_cast<int64_t>(s.batch) * s.heads * s.len_value * s.dim;
+  const int64_t quads = n / 4;
+  // a resident wave of workgroups, each thread four quads per pass
+  const int grid = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((quads + 1023) / 1024, static_cast<int64_t>(dev.cus) * 8)));
+  const int vec = aligned(grad_value, value_dtype == MSDA_DTYPE_BF16 ? 8 : 16) ? 1 : 0;
+  const int64_t stride = part_block_stride(s);
+  return value_dtype == MSDA_DTYPE_BF16 ? msda_host::launch_part_sum<msda::bf16_t>(part, nqb, n, stride, grad_value, vec, grid, st)
+                                        : msda_host::launch_part_sum<float>(part, nqb, n, stride, grad_value, vec, grid, st);
 }
 
 // Two kinds of plan.
@@ -468,7 +484,7 @@ int bwd_band_impl(const Shape& s, int ch, const void* value, int value_dtype, co
   p.nqb = bp.nqb;
   p.qblock = bp.qblock;
   p.part = partial ? static_cast<float*>(workspace) : nullptr;
-  p.part_stride = static_cast<int64_t>(s.batch) * s.heads * s.len_value * s.dim;
+  p.part_stride = part_block_stride(s);
   p.qpass = bp.qpass;
   p.lps_shift = bp.lps_shift;
   p.vec16 = rows_16b(s, vbytes, value, grad_value) ? 1 : 0;
@@ -484,10 +500,7 @@ int bwd_band_impl(const Shape& s, int ch, const void* value, int value_dtype, co
   rc = value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_bwd_band<msda::bf16_t>(ch, p, grid, bp.threads, bp.lds, st)
                                       : msda_host::dispatch_bwd_band<float>(ch, p, grid, bp.threads, bp.lds, st);
   if (rc != MSDA_OK || !partial) return rc;
-  const int64_t quads = (p.part_stride + 3) / 4;
-  const int sgrid = static_cast<int>((quads + 255) / 256);
-  return value_dtype == MSDA_DTYPE_BF16 ? msda_host::launch_part_sum<msda::bf16_t>(p.part, p.nqb, p.part_stride, grad_value, sgrid, st)
-                                        : msda_host::launch_part_sum<float>(p.part, p.nqb, p.part_stride, grad_value, sgrid, st);
+  return launch_partial_sums(s, value_dtype, p.part, p.nqb, grad_value, dev, st);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -602,7 +615,7 @@ int plan_gather(const Shape& s, int vbytes, const DevInfo& dev, GatherPlan* gp) 
 }
 
 int64_t gather_workspace(const Shape& s, const GatherPlan& gp) {
-  return gp.nqb > 1 ? align16(static_cast<int64_t>(gp.nqb) * s.batch * s.heads * s.len_value * s.dim * 4) : 0;
+  return gp.nqb > 1 ? static_cast<int64_t>(gp.nqb) * part_block_stride(s) * 4 : 0;
 }
 
 int bwd_gather_impl(const Shape& s, const void* value, int value_dtype, const float* loc, const float* attn, const void* grad_output,
@@ -633,7 +646,7 @@ int bwd_gather_impl(const Shape& s, const void* value, int value_dtype, const fl
   p.dloc = grad_loc;
   p.dattn = grad_attn;
   p.part = partial ? static_cast<float*>(workspace) : nullptr;
-  p.part_stride = static_cast<int64_t>(s.batch) * s.heads * s.len_value * s.dim;
+  p.part_stride = part_block_stride(s);
   p.heads = s.heads;
   p.queries = s.queries;
   p.levels = s.levels;
@@ -654,10 +667,7 @@ int bwd_gather_impl(const Shape& s, const void* value, int value_dtype, const fl
   rc = value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_bwd_gather<msda::bf16_t>(s.dim, gb, p, grid, gp.threads, gp.lds, st)
                                       : msda_host::dispatch_bwd_gather<float>(s.dim, gb, p, grid, gp.threads, gp.lds, st);
   if (rc != MSDA_OK || !partial) return rc;
-  const int64_t quads = (p.part_stride + 3) / 4;
-  const int sgrid = static_cast<int>((quads + 255) / 256);
-  return value_dtype == MSDA_DTYPE_BF16 ? msda_host::launch_part_sum<msda::bf16_t>(p.part, p.nqb, p.part_stride, grad_value, sgrid, st)
-                                        : msda_host::launch_part_sum<float>(p.part, p.nqb, p.part_stride, grad_value, sgrid, st);
+  return launch_partial_sums(s, value_dtype, p.part, p.nqb, grad_value, dev, st);
 }
 
 

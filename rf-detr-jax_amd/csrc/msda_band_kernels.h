@@ -493,33 +493,64 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
 }
 
 // grad_value = the sum of the query blocks' partial sums, in block order (deterministic), rounded
-// once to the value dtype. Four elements per thread.
+// once to the value dtype. `n` elements; block k starts at k * stride (stride: n rounded up to a
+// multiple of 4, so every block's quads are 16-byte aligned). Workgroup w (in XCD-contiguous
+// logical order, as the band kernel's) sums one contiguous range of quads: with the band kernel's
+// batch-major order, the partials an XCD reads are mostly those its own workgroups wrote. U quads
+// per thread and pass, every block's loads issued before the sums. vec: dv allows 16-byte (f32)
+// or 8-byte (bf16) stores of a quad.
 template <typename VT>
-__global__ void __launch_bounds__(256) bwd_part_sum_kernel(const float* __restrict__ part, int nqb, int64_t stride, VT* __restrict__ dv) {
-  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
-  if (i >= stride) return;
-  if (i + 4 <= stride) {
-    float4 s = *reinterpret_cast<const float4*>(part + i);
+__global__ void __launch_bounds__(256) bwd_part_sum_kernel(const float* __restrict__ part, int nqb, int64_t n, int64_t stride,
+                                                           VT* __restrict__ dv, int vec) {
+  constexpr int U = 4;
+  const int64_t nq = n / 4;
+  const int64_t T = 256;
+  const int64_t per = (nq + gridDim.x - 1) / gridDim.x;
+  const int64_t lo = static_cast<int64_t>(xcd_logical(blockIdx.x, gridDim.x)) * per;
+  const int64_t hi = min(nq, lo + per);
+  const float4* __restrict__ p4 = reinterpret_cast<const float4*>(part);
+  const int64_t bq = stride / 4;  // quads per block
+  for (int64_t q0 = lo + threadIdx.x; q0 < hi; q0 += T * U) {
+    float4 s[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t q = q0 + u * T;
+      s[u] = p4[q < hi ? q : lo];
+    }
     for (int k = 1; k < nqb; ++k) {
-      const float4 t = *reinterpret_cast<const float4*>(part + k * stride + i);
-      s.x += t.x;
-      s.y += t.y;
-      s.z += t.z;
-      s.w += t.w;
+      float4 t[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t q = q0 + u * T;
+        t[u] = p4[k * bq + (q < hi ? q : lo)];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        s[u].x += t[u].x;
+        s[u].y += t[u].y;
+        s[u].z += t[u].z;
+        s[u].w += t[u].w;
+      }
     }
-    float f[4] = {s.x, s.y, s.z, s.w};
-    if constexpr (std::is_same<VT, float>::value) {
-      *reinterpret_cast<float4*>(dv + i) = s;
-    } else {
-      for (int e = 0; e < 4; ++e) dv[i + e] = f32_to_bf16(f[e]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t q = q0 + u * T;
+      if (q >= hi) continue;
+      const float f[4] = {s[u].x, s[u].y, s[u].z, s[u].w};
+      if (vec) {
+        store_vec<VT, 4>(dv + q * 4, f);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) store_vec<VT, 1>(dv + q * 4 + e, {f[e]});
+      }
     }
-    return;
   }
-  for (int64_t e = i; e < stride; ++e) {
-    float s = part[e];
-    for (int k = 1; k < nqb; ++k) s += part[k * stride + e];
-    if constexpr (std::is_same<VT, float>::value) dv[e] = s;
-    else dv[e] = f32_to_bf16(s);
+  // the last n mod 4 elements
+  if (blockIdx.x == 0 && threadIdx.x < n - nq * 4) {
+    const int64_t e = nq * 4 + threadIdx.x;
+    float x = part[e];
+    for (int k = 1; k < nqb; ++k) x += part[k * stride + e];
+    store_vec<VT, 1>(dv + e, {x});
   }
 }
 

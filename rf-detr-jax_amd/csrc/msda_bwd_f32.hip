@@ -4,6 +4,6 @@
 
 namespace msda_host {
 template int dispatch_bwd_band<float>(int, const msda::BandParams&, int, int, int, hipStream_t);
-template int launch_part_sum<float>(const float*, int, int64_t, void*, int, hipStream_t);
+template int launch_part_sum<float>(const float*, int, int64_t, int64_t, void*, int, int, hipStream_t);
 template int dispatch_bwd_gather<float>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);
 }  // namespace msda_host

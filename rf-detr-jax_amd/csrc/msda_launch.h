@@ -75,8 +75,8 @@ int dispatch_bwd_band_g(int ch, const msda::BandParams& p, int grid, int threads
 }
 
 template <typename VT>
-int launch_part_sum(const float* part, int nqb, int64_t stride, void* dv, int grid, hipStream_t st) {
-  hipLaunchKernelGGL(msda::bwd_part_sum_kernel<VT>, dim3(grid), dim3(256), 0, st, part, nqb, stride, static_cast<VT*>(dv));
+int launch_part_sum(const float* part, int nqb, int64_t n, int64_t stride, void* dv, int vec, int grid, hipStream_t st) {
+  hipLaunchKernelGGL(msda::bwd_part_sum_kernel<VT>, dim3(grid), dim3(256), 0, st, part, nqb, n, stride, static_cast<VT*>(dv), vec);
   return check_launch("msda backward (partial sums)");
 }
 
@@ -139,8 +139,8 @@ extern template int dispatch_fwd<float>(int, int, bool, const msda::SampleParams
 extern template int dispatch_fwd<msda::bf16_t>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
 extern template int dispatch_bwd_band<float>(int, const msda::BandParams&, int, int, int, hipStream_t);
 extern template int dispatch_bwd_band<msda::bf16_t>(int, const msda::BandParams&, int, int, int, hipStream_t);
-extern template int launch_part_sum<float>(const float*, int, int64_t, void*, int, hipStream_t);
-extern template int launch_part_sum<msda::bf16_t>(const float*, int, int64_t, void*, int, hipStream_t);
+extern template int launch_part_sum<float>(const float*, int, int64_t, int64_t, void*, int, int, hipStream_t);
+extern template int launch_part_sum<msda::bf16_t>(const float*, int, int64_t, int64_t, void*, int, int, hipStream_t);
 extern template int dispatch_bwd_gather<float>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);
 extern template int dispatch_bwd_gather<msda::bf16_t>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);
 

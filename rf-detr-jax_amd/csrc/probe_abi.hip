@@ -1,0 +1,62 @@
+// probe_abi.hip — LDS read-bandwidth probe of the device, for the benchmark's LDS roofline.
+//
+// Every wave of every workgroup streams 16-byte LDS reads (ds_read_b128: the 64 lanes of a wave
+// read one contiguous 1 KB block per instruction; eight instructions in flight before one wait)
+// over a 32 KB buffer. The loads are written as the instructions themselves so that the compiler
+// neither narrows nor drops them, and one VALU operation per load folds a 32-bit word of it into
+// the result, so the measured rate is the LDS's rather than the vector ALU's.
+#include "msda_probe.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+constexpr int kProbeThreads = 256;
+constexpr int kProbeBytes = 32768;  // LDS per workgroup: several workgroups fit a CU
+
+typedef unsigned probe_u4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(kProbeThreads) lds_read_probe_kernel(unsigned* out, int reps) {
+  __shared__ __align__(16) unsigned buf[kProbeBytes / 4];
+  for (int i = threadIdx.x; i < kProbeBytes / 4; i += kProbeThreads) buf[i] = static_cast<unsigned>(i) * 2654435761u;
+  __syncthreads();
+  const unsigned lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const unsigned base = static_cast<unsigned>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned*)(buf)));
+  unsigned acc = 0;
+  unsigned off = (wave * 8192u) & (kProbeBytes - 1);
+  for (int r = 0; r < reps; ++r) {
+    // eight consecutive 1 KB blocks [off, off + 8 KB), inside the buffer (off is 8 KB aligned)
+    const unsigned a = base + off + lane * 16u;
+    probe_u4 x0, x1, x2, x3, x4, x5, x6, x7;
+    asm volatile(
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %8 offset:1024\n\t"
+        "ds_read_b128 %2, %8 offset:2048\n\t"
+        "ds_read_b128 %3, %8 offset:3072\n\t"
+        "ds_read_b128 %4, %8 offset:4096\n\t"
+        "ds_read_b128 %5, %8 offset:5120\n\t"
+        "ds_read_b128 %6, %8 offset:6144\n\t"
+        "ds_read_b128 %7, %8 offset:7168\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(x4), "=&v"(x5), "=&v"(x6), "=&v"(x7)
+        : "v"(a)
+        : "memory");
+    acc += x0.x ^ x1.y ^ x2.z ^ x3.w ^ x4.x ^ x5.y ^ x6.z ^ x7.w;
+    off = (off + 8192u) & (kProbeBytes - 1);
+  }
+  out[blockIdx.x * kProbeThreads + threadIdx.x] = acc;
+}
+
+}  // namespace
+
+extern "C" int msda_probe_lds_read(unsigned* out, int blocks, int reps, void* stream) {
+  if (out == nullptr || blocks < 1 || reps < 1) return -1;
+  hipLaunchKernelGGL(lds_read_probe_kernel, dim3(blocks), dim3(kProbeThreads), 0, static_cast<hipStream_t>(stream), out, reps);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int64_t msda_probe_lds_read_bytes(int blocks, int reps) {
+  return static_cast<int64_t>(blocks) * kProbeThreads * reps * 8 * 16;
+}

@@ -24,10 +24,10 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 # parallel.
 SOURCES = [os.path.join(CSRC, f) for f in ("msda_abi.hip", "msda_fwd_f32.hip", "msda_fwd_bf16.hip", "msda_bwd_f32.hip",
                                            "msda_bwd_bf16.hip", "grid_sample_abi.hip", "value_proj_abi.hip",
-                                           "attention_abi.hip")]
+                                           "attention_abi.hip", "probe_abi.hip")]
 HEADERS = [os.path.join(CSRC, f) for f in ("msda_kernels.h", "msda_band_kernels.h", "msda_gather_kernels.h", "msda_fused_bwd_kernels.h", "msda_launch.h", "grid_sample_kernels.h",
                                            "value_proj_kernels.h", "attention_kernels.h")] + [
-    os.path.join(INCLUDE, "msda.h")]
+    os.path.join(INCLUDE, "msda.h"), os.path.join(INCLUDE, "msda_probe.h")]
 BUILD_DIR = os.path.join(ROOT, "_build")
 
 ARCH = "gfx950"

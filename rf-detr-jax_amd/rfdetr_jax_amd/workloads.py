@@ -62,6 +62,17 @@ class Workload:
         bwd = (value + loc + attn + out) + (value + loc + attn) if self.backward else 0  # reads G, writes dV/dloc/dA
         return {"fwd": fwd, "bwd": bwd, "total": fwd + bwd}
 
+    def lds_bytes(self) -> dict:
+        """Algorithmic LDS bytes: the forward reads four corner rows per sample and stages each value
+        slice once; the backward reads the corner rows, accumulates four grad_value rows per sample
+        (f32), stages the value slices and flushes the grad_value slices."""
+        sv = 2 if self.value_dtype == "bf16" else 4
+        slices = self.batch * self.heads * self.len_value * self.head_dim
+        corners = self.samples * 4 * self.head_dim
+        fwd = corners * sv + slices * sv
+        bwd = corners * sv + corners * 4 + slices * sv + slices * 4 if self.backward else 0
+        return {"fwd": fwd, "bwd": bwd, "total": fwd + bwd}
+
     def scaled(self, batch: int | None = None, queries: int | None = None) -> "Workload":
         return Workload(self.cfg_id, self.name, batch or self.batch, self.heads, self.head_dim, queries or self.queries,
                         self.shapes, self.points, self.value_dtype, self.backward, self.uniform_locations)

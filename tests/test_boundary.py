@@ -1,6 +1,6 @@
 """The C ABI and the host-side mirror, without a GPU.
 
-* The HIP library loads and exports every function include/msda.h declares.
+* The HIP library loads and exports every function the headers under include/ declare.
 * Malformed calls return the documented error codes and messages; validation runs before any HIP
   call, so these run on any host (no kernel is launched).
 * The Python mirror of ``ms_deform_attn_core_rows`` rejects unknown samplers and inconsistent
@@ -10,6 +10,7 @@
 from __future__ import annotations
 
 import ctypes
+import glob
 import os
 import re
 
@@ -20,13 +21,16 @@ from rfdetr_jax_amd import _native
 from rfdetr_jax_amd import ops as hip_ops
 from rfdetr_jax_amd.build import LIB_PATH
 
-HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "msda.h")
+INCLUDE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
 
 
 def _declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(msda_\w+)\s*\(", text)))
+    """Every msda_* function the headers under include/ declare."""
+    names = set()
+    for header in sorted(glob.glob(os.path.join(INCLUDE, "*.h"))):
+        text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+        names.update(re.findall(r"\b(msda_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_is_built():
@@ -38,8 +42,8 @@ def test_library_exports_every_declared_function():
     assert {"msda_fwd", "msda_bwd", "msda_bwd_workspace_size", "msda_version", "msda_last_error"} <= set(declared)
     lib = ctypes.CDLL(LIB_PATH)
     for name in declared:
-        assert hasattr(lib, name), f"{name} declared in include/msda.h but not exported"
-    assert set(declared) == set(_native.SIGNATURES), "ctypes signatures out of sync with include/msda.h"
+        assert hasattr(lib, name), f"{name} declared under include/ but not exported"
+    assert set(declared) == set(_native.SIGNATURES), "ctypes signatures out of sync with include/*.h"
 
 
 def test_version():
