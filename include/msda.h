@@ -72,8 +72,10 @@ const char* msda_last_error(void);
 /*
  * Process-wide override of a launch-tuning knob (an MSDA_* name, e.g. "MSDA_BWD_BANDS"); value
  * NULL removes the override. Knobs otherwise come from the environment, read once per name at its
- * first use. They choose launch shapes only: results stay within the documented tolerances and no
- * buffer or workspace size depends on them. Not to be called while another thread launches.
+ * first use. They choose launch shapes: results stay within the documented tolerances. The knobs
+ * that select the opt-in sorted-gather backward (MSDA_BWD_GATHER*) or force banded backward plans
+ * (MSDA_BWD_FORCE_BANDS) change msda_bwd_workspace_size's answer: query it after setting them.
+ * Not to be called while another thread launches.
  * No counterpart in the reference; for benchmarks and tests that compare launch variants.
  * Returns MSDA_OK, or MSDA_ERR_INVALID_ARGUMENT for a name that does not start with "MSDA_".
  */

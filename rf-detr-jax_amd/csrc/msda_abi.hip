@@ -173,9 +173,12 @@ int device_info(DevInfo* info) {
   return MSDA_OK;
 }
 
-// Tuning knobs (MSDA_* names): launch-shape choices only; no buffer or workspace size depends on
-// them. Each is read from the environment once, at its first use, and msda_set_tuning() overrides
-// it for the rest of the process, so a plan does not change between calls unless asked to.
+// Tuning knobs (MSDA_* names): launch-shape choices. With every knob at its default the plans and
+// the backward's workspace size depend on the shape and the device only; the knobs that opt into
+// the sorted-gather backward (MSDA_BWD_GATHER*) or force banded plans (MSDA_BWD_FORCE_BANDS) change
+// the size the query returns, so a caller that sets them queries the size afterwards. Each is read
+// from the environment once, at its first use, and msda_set_tuning() overrides it for the rest of
+// the process, so a plan does not change between calls unless asked to.
 std::mutex g_knob_mu;
 std::unordered_map<std::string, std::pair<bool, int>> g_knob_env;  // name -> (set, value)
 std::unordered_map<std::string, std::pair<bool, int>> g_knob_set;  // msda_set_tuning overrides
@@ -306,8 +309,9 @@ bool rows_16b(const Shape& s, int vbytes, const void* a, const void* b) {
 // planning of the backward kernel (bwd_band_kernel)
 
 // LDS of one workgroup of the backward kernel for a band of `rows` rows of a level `w` wide: the
-// staged value rows (the band and one halo row), the f64 accumulator of the band, the sample list
-// (`cap` 16-bit entries) and its counter, and the two grad_output row buffers (`gbuf` bytes each).
+// staged value rows (the band and one halo row), the f64 accumulator of the band, the list of the
+// pass's points (`cap` 32-bit entries) and its counter, and the two grad_output row buffers (`gbuf`
+// bytes each).
 struct BandLayout {
   int acc, list, cnt, gbuf, total;
 };
@@ -364,8 +368,8 @@ int launch_partial_sums(const Shape& s, int value_dtype, const float* part, int 
 // * Otherwise every level is cut into bands of whole image rows that fit the LDS share of `per_cu`
 //   workgroups per CU; then bands are added, to the level with the fewest (each level holds the same
 //   number of samples, Q * P per slice), until the grid has `per_cu` workgroups per CU. Each band
-//   scans its level's locations and lists the queries with a point in it (at most `qpass` queries
-//   per pass).
+//   scans its level's locations and lists the points whose corner rows meet it (the points of at
+//   most `qpass` queries per pass).
 // Workgroup size: up to 1024 threads per CU in all (the kernel's register budget allows 16 waves).
 int plan_band(const Shape& s, int vbytes, int ch, const DevInfo& dev, BandPlan* bp) {
   bp->ch = ch;
@@ -391,12 +395,15 @@ int plan_band(const Shape& s, int vbytes, int ch, const DevInfo& dev, BandPlan* 
     nqb = std::min(nqb, std::max(1, s.queries / 256));  // blocks of at least 256 queries
     bp->nqb = std::max(1, nqb);
   } else {
-    per_cu = std::max(1, env_int("MSDA_BWD_WGS_PER_CU", 2));
+    // one workgroup per CU: measured faster than two at the two-level shape (47.9 vs 53.7 us), its
+    // fixed phases (staging, scan, barriers, write-out) amortised over bands twice as tall
+    per_cu = std::max(1, env_int("MSDA_BWD_WGS_PER_CU", 1));
     bp->nqb = 1;
-    // the query list: one 32-bit entry per query of a pass, the query offset in 16 bits
+    // the point list: one 32-bit entry per point of a pass (query offset << 16 | point)
+    if (s.points >= 65536) return fail(MSDA_ERR_UNSUPPORTED, "n_points %d: at most 65535 with banded levels", s.points);
     const int max_cap = std::max(64, std::min(8192, env_int("MSDA_BWD_LIST", 8192)));
-    bp->qpass = std::max(1, std::min(s.queries, max_cap));
-    bp->cap = bp->qpass;
+    bp->qpass = std::max(1, std::min(s.queries, std::max(1, max_cap / s.points)));
+    bp->cap = bp->qpass * s.points;
     const int budget = dev.lds_bytes / per_cu - 512;
     int64_t nb_total = 0;
     for (int l = 0; l < s.levels; ++l) {

@@ -8,20 +8,26 @@
 //   grad_loc = a * (W, H) * (d/dix, d/diy) sum_c w_c D_c   (masks and floor have zero gradient).
 //
 // bwd_band_kernel: one workgroup per (slice n = b*H + h, item = (level l, band of image rows
-// [r0, r1))). The workgroup owns grad_value rows [r0, r1) of level l of slice n, so every
-// grad_value element has exactly one writer and nothing needs zeroing or a second pass.
+// [r0, r1)), query block). With one query block the workgroup owns grad_value rows [r0, r1) of
+// level l of slice n: every element has exactly one writer and nothing needs zeroing. When a
+// level fits the LDS whole but the slices are too few to fill the CUs, the queries are split into
+// blocks; each block writes an f32 partial sum of the rows, and bwd_part_sum_kernel adds the
+// partials in block order.
 //  1. Stage the band's value rows plus one halo row below into LDS (the rows a corner dot of a
 //     sample whose floor row lies in the band can touch), zero an f64 accumulator for the band.
-//  2. Scan: the threads read the locations of all queries (a pass holds as many queries as the
-//     list can hold samples of; one pass at the usual shapes) at level l, several queries' loads in
-//     flight per thread, and append the samples whose clipped corner rows meet the band to an LDS
-//     list (wave ballot compaction), so the second phase runs on full waves.
-//  3. One lane per sample (one lane per 16 channels for head_dim > 16): the band that holds the
-//     sample's clipped floor row computes the corner dots from the staged rows and writes
-//     grad_attention_weights and grad_sampling_locations; every band the sample's corner rows
-//     meet adds a*w_c*g for its corners into the accumulator with ds_add_f64 (exact products of
-//     f32 values, summed in f64).
-//  4. Round the accumulator once to the value dtype and write the band's grad_value rows.
+//  2. Banded levels only: scan. The threads read the locations of all queries at level l (a pass
+//     holds as many queries as the list can hold points of; one pass at the usual shapes), several
+//     loads in flight per thread, and append every point whose clipped corner rows meet the band to
+//     an LDS list (wave ballot compaction), so the third phase runs on full waves.
+//  3. Work items: a whole level's queries (all of a query's points), or the listed points; lps
+//     lanes per item, CH channels each (lps = head_dim / CH). Waves take chunks of items from an
+//     LDS counter, and a lane loads its next item's inputs before working on the current one. Per
+//     point, the band that holds its clipped floor row computes the corner dots from the staged rows
+//     and writes grad_attention_weights and grad_sampling_locations; every band its corner rows meet
+//     adds a*w_c*g for its corners into the accumulator with ds_add_f64 (exact products of f32
+//     values, summed in f64).
+//  4. Round the accumulator once to the value dtype and write the band's grad_value rows (or the
+//     block's f32 partial rows).
 //
 // Measured on MI355X (per CU, 64-lane instructions): ds_add_f64 ~9.3 cycles and ds_add_u64
 // ~7.2 when the 64 lanes hit 64 distinct 8-byte bank pairs, but ds_add_f32 ~189 cycles (also with
@@ -54,12 +60,12 @@ struct BandParams {
   float* part;     // nqb > 1 and grad_value requested: partial grad_value sums [nqb][B*H][S][D] (f32),
                    // summed by bwd_part_sum_kernel; else null
   int64_t part_stride;  // B * H * S * D
-  int qpass;       // queries scanned per pass (the list holds one entry per query)
+  int qpass;       // queries scanned per pass (the list holds one entry per point of a pass)
   int lps_shift;   // log2(lanes per sample)
   int vec16;       // value rows and grad_value rows allow 16-byte accesses
   int lds_acc;     // byte offset of the f64 accumulator's first cell in LDS (one guard cell precedes
                    // it; the staged value rows start at 0)
-  int lds_list;    // byte offset of the query list (entries: query offset << 16 | point mask)
+  int lds_list;    // byte offset of the point list (entries: query offset << 16 | point)
   int lds_cnt;     // byte offset of the list counter
   LevelDesc lv[kMaxLevels];  // band_rows, band_first per level
 };
@@ -318,7 +324,6 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
   const int c0 = lane_on ? j * CH : 0;
   const int rr = sl & (CH - 1);   // channel rotation of the lane's f64 adds
   const int rel = r0 * W * D;     // level element offset of the first staged row
-  const bool all_points = whole || P > 16;  // otherwise list entries carry a point mask
 
   BandViews<GT> vw;
   {
@@ -336,64 +341,74 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
   // One query: its grad_output row (one read) and its locations and weights at level l serve all of
   // its points in `pmask`; the band holding a point's clipped floor row writes its gradients of the
   // location and weight, every band its rows meet adds its grad_value terms.
-  auto do_query = [&](uint32_t q, uint32_t pmask) {
-    const uint32_t si0 = __umul24(q, vw.qstride);
-    float g[CH];
+  // Points whose inputs are loaded together (fewer for 16-channel lanes: register budget).
+  constexpr int PB = CH >= 16 ? 2 : 4;
+  auto load_grad = [&](uint32_t q, float (&g)[CH]) {
     if (lane_on) {
       load_g<GT, CH>(vw.gout + __umul24(q, vw.gstride), g);
     } else {
 #pragma unroll
       for (int t = 0; t < CH; ++t) g[t] = 0.0f;
     }
-    // grad_output rotated for the grad_value adds: gr[t] = channel (t + rr) mod CH
-    float gr[CH];
-    bool gfin = true;
-    if (want_dv) {
-      float z = 0.0f;  // any infinite or NaN channel makes z NaN (inf * 0)
+  };
+  // grad_output rotated for the grad_value adds (gr[t] = channel (t + rr) mod CH); false when a
+  // channel is infinite or NaN
+  auto rotate_grad = [&](const float (&g)[CH], float (&gr)[CH]) {
+    float z = 0.0f;  // any infinite or NaN channel makes z NaN (inf * 0)
 #pragma unroll
-      for (int t = 0; t < CH; ++t) {
-        gr[t] = g[t];
-        z = fmaf(g[t], 0.0f, z);
-      }
-      gfin = z == 0.0f;
-      rotate_regs<CH, (CH >= 16 ? 4 : CH >= 8 ? 3 : CH >= 4 ? 2 : CH >= 2 ? 1 : 0)>(gr, rr);
+    for (int t = 0; t < CH; ++t) {
+      gr[t] = g[t];
+      z = fmaf(g[t], 0.0f, z);
     }
-    // points whose inputs are loaded together (fewer for 16-channel lanes: register budget)
-    constexpr int PB = CH >= 16 ? 2 : 4;
+    rotate_regs<CH, (CH >= 16 ? 4 : CH >= 8 ? 3 : CH >= 4 ? 2 : CH >= 2 ? 1 : 0)>(gr, rr);
+    return z == 0.0f;
+  };
+  // the points p0 + i, i < NB, of a query whose inputs are in xy and a (`every`: all NB of them are
+  // points of the query and in pmask)
+  auto do_points = [&](uint32_t si0, int p0, uint32_t pmask, const float (&g)[CH], const float (&gr)[CH], bool gfin,
+                       const auto& xy, const auto& a, bool every) {
+    constexpr int NB = sizeof(a) / sizeof(float);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      if (!every && !(p0 + i < P && ((pmask >> ((p0 + i) & 31)) & 1))) continue;
+      const uint32_t si = si0 + p0 + i;
+      const Bilinear c = bilinear(xy[i].x, xy[i].y, L, D);
+      if (want_dots && c.cy0 >= r0 && c.cy0 < r1) {
+        float d00, d10, d01, d11;
+        band_dots<VT, CH>(vrows + c0, c, rel, g, d00, d10, d01, d11);
+        for (int o = 1; o < lps; o <<= 1) {
+          d00 += __shfl_xor(d00, o, 64);
+          d10 += __shfl_xor(d10, o, 64);
+          d01 += __shfl_xor(d01, o, 64);
+          d11 += __shfl_xor(d11, o, 64);
+        }
+        if (j == 0) {
+          if (vw.dattn) *at(vw.dattn, si) = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
+          if (vw.dloc) {
+            const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
+            const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
+            const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
+            // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
+            *at(vw.dloc, si) = make_float2(a[i] * L.fw * dx, a[i] * L.fh * dy);
+          }
+        }
+      }
+      if (want_dv && lane_on) {
+        const bool fast = gfin && isfinite(a[i]) && isfinite(c.fx) && isfinite(c.fy);
+        band_scatter<CH, KD>(acc, W, L.h, D, r0, r1, c, a[i], gr, rr, j, fast);
+      }
+    }
+  };
+  auto do_query = [&](uint32_t q, uint32_t pmask) {
+    const uint32_t si0 = __umul24(q, vw.qstride);
+    float g[CH], gr[CH];
+    load_grad(q, g);
+    const bool gfin = want_dv ? rotate_grad(g, gr) : true;
     for (int p0 = 0; p0 < P; p0 += PB) {
       float2 xy[PB];
       float a[PB];
       load_points<PB>(vw.loc, vw.attn, si0, p0, P, pmask, xy, a);
-#pragma unroll
-      for (int i = 0; i < PB; ++i) {
-        if (!(p0 + i < P && ((pmask >> ((p0 + i) & 31)) & 1))) continue;
-        const uint32_t si = si0 + p0 + i;
-        const Bilinear c = bilinear(xy[i].x, xy[i].y, L, D);
-        if (want_dots && c.cy0 >= r0 && c.cy0 < r1) {
-          float d00, d10, d01, d11;
-          band_dots<VT, CH>(vrows + c0, c, rel, g, d00, d10, d01, d11);
-          for (int o = 1; o < lps; o <<= 1) {
-            d00 += __shfl_xor(d00, o, 64);
-            d10 += __shfl_xor(d10, o, 64);
-            d01 += __shfl_xor(d01, o, 64);
-            d11 += __shfl_xor(d11, o, 64);
-          }
-          if (j == 0) {
-            if (vw.dattn) *at(vw.dattn, si) = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
-            if (vw.dloc) {
-              const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
-              const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
-              const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
-              // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
-              *at(vw.dloc, si) = make_float2(a[i] * L.fw * dx, a[i] * L.fh * dy);
-            }
-          }
-        }
-        if (want_dv && lane_on) {
-          const bool fast = gfin && isfinite(a[i]) && isfinite(c.fx) && isfinite(c.fy);
-          band_scatter<CH, KD>(acc, W, L.h, D, r0, r1, c, a[i], gr, rr, j, fast);
-        }
-      }
+      do_points(si0, p0, pmask, g, gr, gfin, xy, a, false);
     }
   };
 
@@ -406,8 +421,94 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
     if (lane == 0) base = atomicAdd(counter, qpw);
     return __shfl(base, 0, 64) + lane / lps;
   };
-  if (whole) {
-    // 2'. every sample of the block belongs to this workgroup: waves take chunks of its queries
+  // Software-pipelined loop over `count` work items, NP points each: item e is the points
+  // [p0, p0 + NP) of query q, (q, p0) = locate(e). Waves take chunks of qpw items, the first chunk
+  // by wave index, the next ones from the counter cnt[1] (which the caller sets to nwaves * qpw
+  // before a barrier). A lane issues the loads of its next item before it works on the current
+  // one, so the memory latency overlaps the VALU and LDS work; the loads are unconditional (the
+  // item index clamped into range), so no wait depends on a branch. `first_early`: the first
+  // items' inputs load before the barrier that ends the staging (whole levels, where the items are
+  // known before it). NP 2 and 4 use 16-byte loads (the caller checks the alignment).
+  auto pipelined = [&](auto np_tag, int count, auto locate, bool first_early) {
+    constexpr int NP = decltype(np_tag)::value;
+    auto load_item = [&](int e, uint32_t& si, float (&g)[CH], float2 (&xy)[NP], float (&a)[NP]) {
+      const uint2 qp = locate(min(e, count - 1));
+      load_grad(qp.x, g);
+      si = __umul24(qp.x, vw.qstride) + qp.y;
+      if constexpr (NP == 1) {
+        xy[0] = *at(vw.loc, si);
+        a[0] = *at(vw.attn, si);
+      } else {
+#pragma unroll
+        for (int k = 0; k < NP / 2; ++k) {
+          const float4 l4 = *reinterpret_cast<const float4*>(at(vw.loc, si + 2 * k));
+          xy[2 * k] = make_float2(l4.x, l4.y);
+          xy[2 * k + 1] = make_float2(l4.z, l4.w);
+        }
+        if constexpr (NP == 4) {
+          const float4 a4 = *reinterpret_cast<const float4*>(at(vw.attn, si));
+          a[0] = a4.x;
+          a[1] = a4.y;
+          a[2] = a4.z;
+          a[3] = a4.w;
+        } else {
+          const float2 a2 = *reinterpret_cast<const float2*>(at(vw.attn, si));
+          a[0] = a2.x;
+          a[1] = a2.y;
+        }
+      }
+    };
+    int e = (tid >> 6) * qpw + lane / lps;
+    uint32_t si;
+    float g[CH];
+    float2 xy[NP];
+    float a[NP];
+    if (first_early) {
+      if (count > 0) load_item(e, si, g, xy, a);
+      wait_vmem();  // this wave's staging transfers, before the barrier publishes them
+      __syncthreads();
+    }
+    if (count == 0) return;
+    if (!first_early) load_item(e, si, g, xy, a);
+    while (__shfl(e, 0, 64) < count) {
+      const int en = grab(&cnt[1]);
+      uint32_t sin;
+      float gn[CH];
+      float2 xyn[NP];
+      float an[NP];
+      load_item(en, sin, gn, xyn, an);
+      if (e < count) {
+        float gr[CH];
+        const bool gfin = want_dv ? rotate_grad(g, gr) : true;
+        do_points(si, 0, 0xffffffffu, g, gr, gfin, xy, a, true);
+      }
+      e = en;
+      si = sin;
+#pragma unroll
+      for (int t = 0; t < CH; ++t) g[t] = gn[t];
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        xy[i] = xyn[i];
+        a[i] = an[i];
+      }
+    }
+  };
+  const int nwaves = nt >> 6;
+  // 16-byte alignment of the query rows' locations (and weights for four points): the row offsets
+  // are multiples of P, so the base pointers decide
+  const bool rows16 = (reinterpret_cast<uintptr_t>(vw.loc) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(vw.attn) & (P == 4 ? 15 : 7)) == 0;
+  if (whole && rows16 && (P == 2 || (P == 4 && CH < 16))) {
+    // 2'. every sample of the block belongs to this workgroup: one item per query
+    if (tid == 0) cnt[1] = nwaves * qpw;
+    auto locate = [&](int e) { return make_uint2(static_cast<uint32_t>(q_lo + e), 0u); };
+    if (P == 2)
+      pipelined(std::integral_constant<int, 2>{}, q_hi - q_lo, locate, true);
+    else
+      pipelined(std::integral_constant<int, 4>{}, q_hi - q_lo, locate, true);
+  } else if (whole) {
+    // every sample of the block belongs to this workgroup, points per query other than 2 or 4
+    // (or unaligned rows): waves take chunks of its queries from the counter
     if (tid == 0) cnt[1] = 0;
     wait_vmem();  // this wave's staging transfers, before the barrier publishes them
     __syncthreads();
@@ -422,13 +523,12 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
         if (tid == 0) cnt[0] = 0;
         __syncthreads();
       }
-      // 2. scan: one query per thread; its P locations at level l, four at a time. A query is
-      //    listed when any of its points meets the band, with the mask of those points.
+      // 2. scan: one query per thread, its P locations at level l four at a time; every point
+      //    whose clipped corner rows meet the band is listed as (query offset << 16 | point)
       for (int qq = 0; qq < qn; qq += nt) {
         const int qo = qq + tid;
         const bool qv = qo < qn;
         const float2* lq = at(vw.loc, __umul24(static_cast<uint32_t>(q0 + (qv ? qo : 0)), vw.qstride));
-        uint32_t mask = 0;
         for (int p0 = 0; p0 < P; p0 += 4) {
           float ly[4];
 #pragma unroll
@@ -436,60 +536,60 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
             if (qv && p0 + i < P) ly[i] = lq[p0 + i].y;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            if (qv && p0 + i < P) {
+            if (p0 + i >= P) break;  // uniform
+            bool in = false;
+            if (qv) {
               const int2 ry = clipped_rows(ly[i], L);
-              if ((ry.x >= r0 && ry.x < r1) || (ry.y >= r0 && ry.y < r1)) mask |= 1u << ((p0 + i) & 15);
+              in = (ry.x >= r0 && ry.x < r1) || (ry.y >= r0 && ry.y < r1);
             }
+            list_append32(in, (static_cast<uint32_t>(qo) << 16) | static_cast<uint32_t>(p0 + i), list, cnt);
           }
         }
-        if (qv && all_points && mask) mask = 0xffffu;
-        list_append32(mask != 0, (static_cast<uint32_t>(qo) << 16) | mask, list, cnt);
       }
-      if (tid == 0) cnt[1] = 0;
+      if (tid == 0) cnt[1] = nwaves * qpw;
       wait_vmem();  // this wave's staging transfers, before the barrier publishes them
       __syncthreads();
-      // 3. one lane per listed query (lps lanes for wide heads), no barrier: waves drift apart, so
+      // 3. one item per listed point (lps lanes for wide heads), no barrier: waves drift apart, so
       //    the VALU-heavy and the LDS-atomic-heavy parts of different waves overlap
       const int nlist = cnt[0];
-      for (int e = grab(&cnt[1]); __shfl(e, 0, 64) < nlist; e = grab(&cnt[1])) {
-        if (e < nlist) {
-          const uint32_t ent = list[e];
-          do_query(static_cast<uint32_t>(q0) + (ent >> 16), all_points ? 0xffffffffu : (ent & 0xffffu));
-        }
-      }
+      auto locate = [&](int e) {
+        const uint32_t ent = list[e];
+        return make_uint2(static_cast<uint32_t>(q0) + (ent >> 16), ent & 0xffffu);
+      };
+      pipelined(std::integral_constant<int, 1>{}, nlist, locate, false);
     }
   }
   if (!want_dv) return;
   __syncthreads();
   // 4. the band's grad_value rows, rounded once to the value dtype, or this query block's partial
-  //    sums (f32) when the slice's queries are split over several workgroups
+  //    sums (f32) when the slice's queries are split over several workgroups. With aligned rows a
+  //    lane takes two consecutive accumulator elements per pass: its 16-byte LDS read sits at a
+  //    16-byte lane stride (no bank conflicts; wider runs per lane conflict), and a wave stores one
+  //    contiguous run.
   const int64_t row_off = n * slice + static_cast<int64_t>(L.start + r0 * W) * D;
-  if (p.part != nullptr) {
-    float* __restrict__ dst = p.part + static_cast<int64_t>(qb) * p.part_stride + row_off;
+  auto write_rows = [&](auto* dst) {
+    using OT = std::remove_pointer_t<decltype(dst)>;
     if (p.vec16) {
-      for (int i = tid * 4; i < owned_elems; i += nt * 4)
-        *reinterpret_cast<float4*>(dst + i) = make_float4(static_cast<float>(accp[i]), static_cast<float>(accp[i + 1]),
-                                                          static_cast<float>(accp[i + 2]), static_cast<float>(accp[i + 3]));
+      const int pairs = owned_elems >> 1;
+      for (int i = tid; i < pairs; i += nt) {
+        float f[2] = {static_cast<float>(accp[2 * i]), static_cast<float>(accp[2 * i + 1])};
+        store_vec<OT, 2>(dst + 2 * i, f);
+      }
+      if ((owned_elems & 1) && tid == 0) {
+        float f[1] = {static_cast<float>(accp[owned_elems - 1])};
+        store_vec<OT, 1>(dst + owned_elems - 1, f);
+      }
     } else {
-      for (int i = tid; i < owned_elems; i += nt) dst[i] = static_cast<float>(accp[i]);
+      for (int i = tid; i < owned_elems; i += nt) {
+        float f[1] = {static_cast<float>(accp[i])};
+        store_vec<OT, 1>(dst + i, f);
+      }
     }
-    return;
-  }
-  VT* __restrict__ dv = static_cast<VT*>(p.dvalue) + row_off;
-  if (p.vec16) {
-    constexpr int E = 16 / sizeof(VT);
-    for (int i = tid * E; i < owned_elems; i += nt * E) {
-      float f[E];
-#pragma unroll
-      for (int e2 = 0; e2 < E; ++e2) f[e2] = static_cast<float>(accp[i + e2]);
-      store_vec<VT, E>(dv + i, f);
-    }
-  } else {
-    for (int i = tid; i < owned_elems; i += nt) {
-      float f[1] = {static_cast<float>(accp[i])};
-      store_vec<VT, 1>(dv + i, f);
-    }
-  }
+  };
+  if (p.part != nullptr)
+    write_rows(p.part + static_cast<int64_t>(qb) * p.part_stride + row_off);
+  else
+    write_rows(static_cast<VT*>(p.dvalue) + row_off);
 }
 
 // grad_value = the sum of the query blocks' partial sums, in block order (deterministic), rounded
