@@ -29,6 +29,11 @@ retyping of these formulas):
 * ``ms_deform_attn_core_rows_vjp``: torch autograd through ``F.grid_sample`` in float64; central
   finite differences of the float64 forward; linearity of the output in value and in weights
   (``<G, out> = <dV, V>`` and ``= <dA, A>``).
+* ``ms_deform_attn_core_rows_bf16_gather`` (the reference's bf16 rounding points of the ``gather``
+  sampler, ops.py:88-91 and :123-134, for documenting how far the kernels' f32 interpolation lies
+  from them): equal to the float64 forward where every fraction, weight and product is exact in
+  bf16 (quarter-pixel positions, small integer values); a planted mistake (the coordinate rounded to
+  bf16 instead of its fraction) changes the result.
 """
 
 from __future__ import annotations
@@ -39,6 +44,7 @@ __all__ = [
     "level_offsets",
     "ms_deform_attn_core_rows",
     "ms_deform_attn_core_rows_vjp",
+    "ms_deform_attn_core_rows_bf16_gather",
     "brute_force_forward",
     "bf16_round",
 ]
@@ -191,6 +197,43 @@ def ms_deform_attn_core_rows_vjp(value, spatial_shapes, sampling_locations, atte
         grad_loc,
         grad_attn.reshape(batch, len_query, n_heads, n_levels * n_points),
     )
+
+
+def ms_deform_attn_core_rows_bf16_gather(value, spatial_shapes, sampling_locations, attention_weights,
+                                         _round_coordinate=False):
+    """Forward of ops.py:208-292 with the ``gather`` sampler on a bf16 value map, rounding where the
+    reference's bf16 computation rounds: the fractions ``wx1 = (ix - ix0).astype(bf16)`` (ops.py:88-89),
+    ``1 - w`` and the corner-weight products in bf16 (:90-91, :123), the mask (:125-128), each corner
+    product ``stacked * weight`` in bf16 and the four-corner sum rounded to bf16 (:134; the sum itself
+    taken in f32, as XLA accumulates bf16 reductions); then the einsum with the f32 attention weights
+    in f32 or wider (:289). ``value`` holds bf16-representable values as float32. Float64 result.
+    ``_round_coordinate`` plants a mistake for the oracle's own tests (the coordinate is rounded to
+    bf16 before the floor, instead of the fraction after it)."""
+    batch, len_query, n_heads, n_levels, n_points, d, offsets = _split(value, spatial_shapes, sampling_locations)
+    v32 = np.asarray(value, dtype=np.float32).reshape(batch, n_heads, -1, d)
+    attn = np.asarray(attention_weights, dtype=np.float64).reshape(batch, len_query, n_heads, n_levels, n_points)
+    out = np.zeros((batch, len_query, n_heads, d), np.float64)
+    one = np.float32(1)
+    for level, (height, width) in enumerate(spatial_shapes):
+        v_l = v32[:, :, offsets[level] : offsets[level + 1], :]
+        loc = sampling_locations[:, :, :, level]
+        ix = _pixel_coords(loc[..., 0], width).astype(np.float32)
+        iy = _pixel_coords(loc[..., 1], height).astype(np.float32)
+        if _round_coordinate:
+            ix, iy = bf16_round(ix), bf16_round(iy)
+        ix0, iy0 = np.floor(ix), np.floor(iy)
+        wx1 = bf16_round(ix - ix0)
+        wy1 = bf16_round(iy - iy0)
+        wx0 = bf16_round(one - wx1)
+        wy0 = bf16_round(one - wy1)
+        weight = np.stack([bf16_round(wx0 * wy0), bf16_round(wx1 * wy0), bf16_round(wx0 * wy1), bf16_round(wx1 * wy1)], -1)
+        idx, _, m, _, _ = _corners(loc[..., 0], loc[..., 1], height, width)
+        weight = weight * m.astype(np.float32)  # exact: the mask is 0 or 1
+        corners = _gather(v_l, idx)  # [B,Q,H,P,4,D] float32, bf16 values
+        prods = bf16_round(corners * weight[..., None])
+        sample = bf16_round(prods.sum(axis=-2, dtype=np.float32))
+        out += np.einsum("bqhp,bqhpd->bqhd", attn[:, :, :, level], sample.astype(np.float64))
+    return out.reshape(batch, len_query, n_heads * d)
 
 
 def brute_force_forward(value, spatial_shapes, sampling_locations, attention_weights):

@@ -246,3 +246,41 @@ def test_bf16_round():
     assert r[2] == np.float32(1.0078125)
     assert r[3] == -2.5 and np.isinf(r[5])
     assert np.isnan(R.bf16_round(np.array([np.nan], np.float32))[0])
+
+
+def test_bf16_gather_emulation_exact_where_bf16_is_exact():
+    """The emulation of the reference's bf16 rounding points (ops.py:88-91, :123-134) equals the
+    float64 forward when every rounding it applies is exact: quarter-pixel positions on 8-wide and
+    4-high levels (fractions and weight products are multiples of 1/16), integer values in [-2, 2]
+    (corner products and four-corner sums need at most 6 significant bits)."""
+    rng = np.random.default_rng(11)
+    shapes = ((8, 8), (4, 8))
+    b, q, h, d, p = 2, 9, 2, 4, 3
+    s = sum(hh * ww for hh, ww in shapes)
+    value = rng.integers(-2, 3, size=(b * h, s, d)).astype(np.float32)
+    loc = np.empty((b, q, h, len(shapes), p, 2), np.float32)
+    for lvl, (hh, ww) in enumerate(shapes):
+        # ix = loc * W - 0.5 in quarter pixels from -1.5 to W + 0.5 (edges and outside included)
+        ix = rng.integers(-6, 4 * ww + 3, size=(b, q, h, p)) / 4.0
+        iy = rng.integers(-6, 4 * hh + 3, size=(b, q, h, p)) / 4.0
+        loc[:, :, :, lvl, :, 0] = (ix + 0.5) / ww
+        loc[:, :, :, lvl, :, 1] = (iy + 0.5) / hh
+    attn = rng.random((b, q, h, len(shapes) * p)).astype(np.float32)
+    want = R.ms_deform_attn_core_rows(value, shapes, loc, attn)
+    got = R.ms_deform_attn_core_rows_bf16_gather(value, shapes, loc, attn)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_bf16_gather_emulation_planted_mistake_and_gap():
+    """Rounding the coordinate instead of its fraction (a plausible misreading of ops.py:88) changes
+    the result on an 80-wide level; and the emulated reference stays within the bf16 parity
+    tolerance (2e-2) of the f32 interpolation the kernels compute, at the two-level shape."""
+    shapes = ((80, 80), (20, 20))
+    value, loc, attn, _ = make_inputs(3, 1, 4, 16, 120, shapes, 4)
+    value = R.bf16_round(value)
+    emu = R.ms_deform_attn_core_rows_bf16_gather(value, shapes, loc, attn)
+    planted = R.ms_deform_attn_core_rows_bf16_gather(value, shapes, loc, attn, _round_coordinate=True)
+    assert np.abs(planted - emu).max() > 1e-2
+    f32_path = R.ms_deform_attn_core_rows(value, shapes, loc, attn)
+    gap = np.abs(emu - f32_path).max() / max(1.0, np.abs(f32_path).max())
+    assert 1e-4 < gap < 2e-2, gap
