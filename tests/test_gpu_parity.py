@@ -458,4 +458,3 @@ def test_library_loaded_from_tree():
 
     maps = open(f"/proc/{os.getpid()}/maps").read()
     assert os.path.realpath(LIB_PATH) in maps or LIB_PATH in maps
-
