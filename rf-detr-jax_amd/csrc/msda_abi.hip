@@ -347,17 +347,20 @@ int64_t band_workspace(const Shape& s, const BandPlan& bp) {
   return bp.nqb > 1 ? static_cast<int64_t>(bp.nqb) * part_block_stride(s) * 4 : 0;
 }
 
-// The second kernel of a split backward: grad_value = sum of the blocks' partials, in block order.
+// The second kernel of a split backward: grad_value = sum of the blocks' partials, in block order;
+// with rpart, also the fused backward's reference-point gradient (the heads' partials in order).
 int launch_partial_sums(const Shape& s, int value_dtype, const float* part, int nqb, void* grad_value, const DevInfo& dev,
-                        hipStream_t st) {
+                        hipStream_t st, const float* rpart = nullptr, float* dref = nullptr, int ref_dim = 0) {
   const int64_t n = static_cast<int64_t>(s.batch) * s.heads * s.len_value * s.dim;
   const int64_t quads = n / 4;
   // a resident wave of workgroups, each thread four quads per pass
   const int grid = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((quads + 1023) / 1024, static_cast<int64_t>(dev.cus) * 8)));
   const int vec = aligned(grad_value, value_dtype == MSDA_DTYPE_BF16 ? 8 : 16) ? 1 : 0;
   const int64_t stride = part_block_stride(s);
-  return value_dtype == MSDA_DTYPE_BF16 ? msda_host::launch_part_sum<msda::bf16_t>(part, nqb, n, stride, grad_value, vec, grid, st)
-                                        : msda_host::launch_part_sum<float>(part, nqb, n, stride, grad_value, vec, grid, st);
+  const int64_t nref = static_cast<int64_t>(s.batch) * s.queries * ref_dim;
+  return value_dtype == MSDA_DTYPE_BF16
+             ? msda_host::launch_part_sum<msda::bf16_t>(part, nqb, n, stride, grad_value, vec, grid, st, rpart, dref, s.heads, nref)
+             : msda_host::launch_part_sum<float>(part, nqb, n, stride, grad_value, vec, grid, st, rpart, dref, s.heads, nref);
 }
 
 // Two kinds of plan.
@@ -457,9 +460,19 @@ int plan_band(const Shape& s, int vbytes, int ch, const DevInfo& dev, BandPlan* 
   return MSDA_OK;
 }
 
+// The MSDeformAttn prologue and epilogue inside the band kernel (one whole level): `loc` / `attn`
+// are then the sampling offsets and attention logits, `grad_loc` / `grad_attn` their gradients.
+struct BandFusedArgs {
+  const float* ref;
+  int ref_dim;
+  float inv_points, fpoints;
+  float* dref_part;  // [H][B * Q][ref_dim] per-head partials (workspace), or null
+  float* dref;       // grad_reference_points: the partials summed over heads, or null
+};
+
 int bwd_band_impl(const Shape& s, int ch, const void* value, int value_dtype, const float* loc, const float* attn,
                   const void* grad_output, int grad_output_dtype, void* grad_value, float* grad_loc, float* grad_attn, void* workspace,
-                  int64_t workspace_bytes, const DevInfo& dev, hipStream_t st) {
+                  int64_t workspace_bytes, const DevInfo& dev, hipStream_t st, const BandFusedArgs* fa = nullptr) {
   const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   BandPlan bp;
   int rc = plan_band(s, vbytes, ch, dev, &bp);
@@ -504,10 +517,26 @@ int bwd_band_impl(const Shape& s, int ch, const void* value, int value_dtype, co
     first += bp.bands[l];
   }
   const int grid = static_cast<int>(static_cast<int64_t>(s.batch) * s.heads * bp.nwork * p.nqb);
-  rc = value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_bwd_band<msda::bf16_t>(ch, p, grid, bp.threads, bp.lds, st)
-                                      : msda_host::dispatch_bwd_band<float>(ch, p, grid, bp.threads, bp.lds, st);
-  if (rc != MSDA_OK || !partial) return rc;
-  return launch_partial_sums(s, value_dtype, p.part, p.nqb, grad_value, dev, st);
+  if (fa != nullptr) {
+    p.ref = fa->ref;
+    p.ref_dim = fa->ref_dim;
+    p.inv_points = fa->inv_points;
+    p.fpoints = fa->fpoints;
+    p.dref_part = fa->dref_part;
+    p.bq_total = static_cast<int64_t>(s.batch) * s.queries;
+  }
+  rc = value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_bwd_band<msda::bf16_t>(ch, p, grid, bp.threads, bp.lds, st, fa != nullptr)
+                                      : msda_host::dispatch_bwd_band<float>(ch, p, grid, bp.threads, bp.lds, st, fa != nullptr);
+  if (rc != MSDA_OK) return rc;
+  const bool ref_sum = fa != nullptr && fa->dref_part != nullptr && fa->dref != nullptr;
+  if (partial)
+    return launch_partial_sums(s, value_dtype, p.part, p.nqb, grad_value, dev, st, ref_sum ? fa->dref_part : nullptr,
+                               ref_sum ? fa->dref : nullptr, ref_sum ? fa->ref_dim : 0);
+  if (!ref_sum) return MSDA_OK;
+  const int64_t nref = static_cast<int64_t>(s.batch) * s.queries * fa->ref_dim;
+  const int rgrid = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((nref + 255) / 256, static_cast<int64_t>(dev.cus) * 4)));
+  hipLaunchKernelGGL(msda::ref_head_sum_kernel, dim3(rgrid), dim3(256), 0, st, fa->dref_part, fa->dref, s.heads, nref);
+  return msda_host::check_launch("msda fused backward (reference points)");
 }
 
 // ------------------------------------------------------------------------------------------
@@ -812,6 +841,19 @@ int fused_bwd_impl(const Shape& s, int ch, const void* value, int value_dtype, c
                 static_cast<long long>(lay.total), static_cast<long long>(workspace == nullptr ? 0 : workspace_bytes));
   if (!aligned(workspace, 16)) return fail(MSDA_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   char* ws = static_cast<char*>(workspace);
+  const float inv_points = (s.points & (s.points - 1)) == 0 ? 1.0f / static_cast<float>(s.points) : 0.0f;
+  // One level that fits the LDS whole, 2 or 4 points, head_dim 16 or 32: the band kernel applies
+  // the prologue and epilogue per (query, head) row itself (no row kernels, no location / weight
+  // round trip through memory); the reference-point partials of the heads go to the locations'
+  // region of the workspace (H * B * Q * ref_dim floats <= B * Q * H * P * 2).
+  if (s.levels == 1 && bp.nwork == 1 && (s.points == 2 || s.points == 4) && ch == 8 && (s.dim == 16 || s.dim == 32) &&
+      aligned(offsets, 16) && aligned(logits, s.points == 4 ? 16 : 8) && aligned(fz.ref, fz.ref_dim * 4) &&
+      env_int("MSDA_FUSED_IN_KERNEL", 1) != 0) {
+    float* dref_part = fz.dref != nullptr ? reinterpret_cast<float*>(ws + lay.loc) : nullptr;
+    const BandFusedArgs fa{fz.ref, fz.ref_dim, inv_points, static_cast<float>(s.points), dref_part, fz.dref};
+    return bwd_band_impl(s, ch, value, value_dtype, offsets, logits, grad_output, grad_output_dtype, grad_value, grad_offsets,
+                         grad_logits, ws + lay.band, workspace_bytes - lay.band, dev, st, &fa);
+  }
   msda::FusedRowParams fp{};
   fp.ref = fz.ref;
   fp.off = offsets;
@@ -824,7 +866,7 @@ int fused_bwd_impl(const Shape& s, int ch, const void* value, int value_dtype, c
   fp.points = s.points;
   fp.bq_total = static_cast<int64_t>(s.batch) * s.queries;
   fp.fpoints = static_cast<float>(s.points);
-  fp.inv_points = (s.points & (s.points - 1)) == 0 ? 1.0f / static_cast<float>(s.points) : 0.0f;
+  fp.inv_points = inv_points;
   for (int l = 0; l < s.levels; ++l) {
     fp.fw[l] = static_cast<float>(s.w[l]);
     fp.fh[l] = static_cast<float>(s.h[l]);

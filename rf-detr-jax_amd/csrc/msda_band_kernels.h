@@ -68,6 +68,17 @@ struct BandParams {
   int lds_list;    // byte offset of the point list (entries: query offset << 16 | point)
   int lds_cnt;     // byte offset of the list counter
   LevelDesc lv[kMaxLevels];  // band_rows, band_first per level
+  // The MSDeformAttn prologue in the kernel (FZ instantiations; one level, whole): `loc` holds the
+  // sampling offsets and `attn` the attention logits, `dloc` receives grad_sampling_offsets and
+  // `dattn` grad_attention_logits; locations and softmax weights are formed per (query, head) row
+  // as the forward forms them (fused_location_at, softmax_regs), and the row's softmax VJP and
+  // offset gradient follow its points. dref_part: [H][B * Q][ref_dim] per-head partial gradients
+  // of the reference points (summed over the row's points in order), or null.
+  const float* ref;  // [B, Q, 1, ref_dim]
+  int ref_dim;
+  float inv_points, fpoints;
+  float* dref_part;
+  int64_t bq_total;  // B * Q
 };
 
 // Item k of a slice: level l (the last whose first item <= k) and band k - band_first.
@@ -275,7 +286,7 @@ __device__ __forceinline__ void load_points(const float2* loc, const float* attn
 // Work item: (batch b, level-band item, query block, head h), batch-major. A band that is a whole
 // level takes every sample of its query block directly (lanes walk the queries in order); a level
 // cut into bands is scanned first, and the queries with a point in the band are listed.
-template <typename VT, typename GT, int CH, int KD>
+template <typename VT, typename GT, int CH, int KD, bool FZ = false>
 __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const int nt = blockDim.x, tid = threadIdx.x;
@@ -304,7 +315,7 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
   uint32_t* list = reinterpret_cast<uint32_t*>(lds_raw + p.lds_list);
   int* cnt = reinterpret_cast<int*>(lds_raw + p.lds_cnt);
   const bool want_dv = p.dvalue != nullptr;
-  const bool want_dots = p.dloc != nullptr || p.dattn != nullptr;
+  const bool want_dots = p.dloc != nullptr || p.dattn != nullptr || (FZ && p.dref_part != nullptr);
   const int owned_elems = (r1 - r0) * W * D;
 
   // 1. staging (issued here, waited for before the barrier that precedes its use) and accumulator
@@ -365,8 +376,14 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
   };
   // the points p0 + i, i < NB, of a query whose inputs are in xy and a (`every`: all NB of them are
   // points of the query and in pmask)
+  // The point's weight and location gradients go to `sink(i, si, da, dl)` in lane j = 0 (the
+  // default writes them; the fused epilogue keeps da and turns dl into the offset gradient).
+  auto write_grads = [&](int, uint32_t si, float da, float2 dl) {
+    if (vw.dattn) *at(vw.dattn, si) = da;
+    if (vw.dloc) *at(vw.dloc, si) = dl;
+  };
   auto do_points = [&](uint32_t si0, int p0, uint32_t pmask, const float (&g)[CH], const float (&gr)[CH], bool gfin,
-                       const auto& xy, const auto& a, bool every) {
+                       const auto& xy, const auto& a, bool every, auto&& sink) {
     constexpr int NB = sizeof(a) / sizeof(float);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -383,14 +400,12 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
           d11 += __shfl_xor(d11, o, 64);
         }
         if (j == 0) {
-          if (vw.dattn) *at(vw.dattn, si) = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
-          if (vw.dloc) {
-            const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
-            const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
-            const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
-            // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
-            *at(vw.dloc, si) = make_float2(a[i] * L.fw * dx, a[i] * L.fh * dy);
-          }
+          const float da = c.w00 * d00 + c.w10 * d10 + c.w01 * d01 + c.w11 * d11;
+          const float g00 = c.m00 * d00, g10 = c.m10 * d10, g01 = c.m01 * d01, g11 = c.m11 * d11;
+          const float dx = (1.0f - c.fy) * (g10 - g00) + c.fy * (g11 - g01);
+          const float dy = (1.0f - c.fx) * (g01 - g00) + c.fx * (g11 - g10);
+          // d ix / d loc = W (ops.py:270, :83): grid = 2 loc - 1, ix = ((grid + 1) W - 1) / 2
+          sink(i, si, da, make_float2(a[i] * L.fw * dx, a[i] * L.fh * dy));
         }
       }
       if (want_dv && lane_on) {
@@ -408,7 +423,7 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
       float2 xy[PB];
       float a[PB];
       load_points<PB>(vw.loc, vw.attn, si0, p0, P, pmask, xy, a);
-      do_points(si0, p0, pmask, g, gr, gfin, xy, a, false);
+      do_points(si0, p0, pmask, g, gr, gfin, xy, a, false, write_grads);
     }
   };
 
@@ -431,10 +446,20 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
   // known before it). NP 2 and 4 use 16-byte loads (the caller checks the alignment).
   auto pipelined = [&](auto np_tag, int count, auto locate, bool first_early) {
     constexpr int NP = decltype(np_tag)::value;
-    auto load_item = [&](int e, uint32_t& si, float (&g)[CH], float2 (&xy)[NP], float (&a)[NP]) {
+    auto load_item = [&](int e, uint32_t& si, uint32_t& qi, float (&g)[CH], float2 (&xy)[NP], float (&a)[NP], float4& rf) {
       const uint2 qp = locate(min(e, count - 1));
       load_grad(qp.x, g);
+      qi = qp.x;
       si = __umul24(qp.x, vw.qstride) + qp.y;
+      if constexpr (FZ) {  // the reference point of row (b, q) at the (only) level
+        const int64_t i = static_cast<int64_t>(b) * Q + qp.x;
+        if (p.ref_dim == 4) {
+          rf = *reinterpret_cast<const float4*>(p.ref + i * 4);
+        } else {
+          const float2 r2 = *reinterpret_cast<const float2*>(p.ref + i * 2);
+          rf = make_float4(r2.x, r2.y, 0.0f, 0.0f);
+        }
+      }
       if constexpr (NP == 1) {
         xy[0] = *at(vw.loc, si);
         a[0] = *at(vw.attn, si);
@@ -459,31 +484,79 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
       }
     };
     int e = (tid >> 6) * qpw + lane / lps;
-    uint32_t si;
+    uint32_t si, qi;
     float g[CH];
     float2 xy[NP];
     float a[NP];
+    float4 rf = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (first_early) {
-      if (count > 0) load_item(e, si, g, xy, a);
+      if (count > 0) load_item(e, si, qi, g, xy, a, rf);
       wait_vmem();  // this wave's staging transfers, before the barrier publishes them
       __syncthreads();
     }
     if (count == 0) return;
-    if (!first_early) load_item(e, si, g, xy, a);
+    if (!first_early) load_item(e, si, qi, g, xy, a, rf);
     while (__shfl(e, 0, 64) < count) {
       const int en = grab(&cnt[1]);
-      uint32_t sin;
+      uint32_t sin, qin;
       float gn[CH];
       float2 xyn[NP];
       float an[NP];
-      load_item(en, sin, gn, xyn, an);
+      float4 rfn;
+      load_item(en, sin, qin, gn, xyn, an, rfn);
       if (e < count) {
         float gr[CH];
         const bool gfin = want_dv ? rotate_grad(g, gr) : true;
-        do_points(si, 0, 0xffffffffu, g, gr, gfin, xy, a, true);
+        if constexpr (FZ) {
+          // the row's softmax weights (softmax_regs' operations) and locations (fused_location_at)
+          float m = -__builtin_inff(), sum = 0.0f;
+#pragma unroll
+          for (int i = 0; i < NP; ++i) m = fmaxf(m, a[i]);
+#pragma unroll
+          for (int i = 0; i < NP; ++i) {
+            a[i] = expf(a[i] - m);
+            sum += a[i];
+          }
+#pragma unroll
+          for (int i = 0; i < NP; ++i) a[i] = a[i] / sum;
+          float2 tt[NP];
+#pragma unroll
+          for (int i = 0; i < NP; ++i) xy[i] = fused_location_at(xy[i], rf, tt[i], L.fw, L.fh, p.ref_dim, p.inv_points, p.fpoints);
+          // per point, in order: keep dA, turn the location gradient into the offset gradient and
+          // the reference point's share (the transpose of fused_location_at)
+          float dA[NP];
+          float r4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          auto fused_sink = [&](int i, uint32_t sp, float da, float2 dl) {
+            dA[i] = da;
+            const float2 go = fused_offset_grad(dl, rf, tt[i], L.fw, L.fh, p.ref_dim, p.inv_points, p.fpoints, r4);
+            if (vw.dloc) *at(vw.dloc, sp) = go;
+          };
+          do_points(si, 0, 0xffffffffu, g, gr, gfin, xy, a, true, fused_sink);
+          if (j == 0 && want_dots) {
+            // softmax VJP in place: grad_logit_k = a_k (dA_k - sum_j a_j dA_j)
+            float S = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NP; ++i) S += a[i] * dA[i];
+            if (vw.dattn) {
+#pragma unroll
+              for (int i = 0; i < NP; ++i) *at(vw.dattn, si + i) = a[i] * (dA[i] - S);
+            }
+            if (p.dref_part != nullptr) {
+              const int64_t bq = static_cast<int64_t>(b) * Q + qi;
+              float* d = p.dref_part + (static_cast<int64_t>(h) * p.bq_total + bq) * p.ref_dim;
+#pragma unroll
+              for (int c = 0; c < 4; ++c)
+                if (c < p.ref_dim) d[c] = r4[c];
+            }
+          }
+        } else {
+          do_points(si, 0, 0xffffffffu, g, gr, gfin, xy, a, true, write_grads);
+        }
       }
       e = en;
       si = sin;
+      qi = qin;
+      rf = rfn;
 #pragma unroll
       for (int t = 0; t < CH; ++t) g[t] = gn[t];
 #pragma unroll
@@ -506,7 +579,7 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
       pipelined(std::integral_constant<int, 2>{}, q_hi - q_lo, locate, true);
     else
       pipelined(std::integral_constant<int, 4>{}, q_hi - q_lo, locate, true);
-  } else if (whole) {
+  } else if (!FZ && whole) {
     // every sample of the block belongs to this workgroup, points per query other than 2 or 4
     // (or unaligned rows): waves take chunks of its queries from the counter
     if (tid == 0) cnt[1] = 0;
@@ -515,7 +588,7 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
     const int qcount = q_hi - q_lo;
     for (int e = grab(&cnt[1]); __shfl(e, 0, 64) < qcount; e = grab(&cnt[1]))
       if (e < qcount) do_query(static_cast<uint32_t>(q_lo + e), 0xffffffffu);
-  } else {
+  } else if (!FZ) {
     for (int q0 = q_lo; q0 < q_hi; q0 += p.qpass) {
       const int qn = min(p.qpass, q_hi - q0);
       if (q0 > q_lo) {
@@ -592,16 +665,39 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
     write_rows(static_cast<VT*>(p.dvalue) + row_off);
 }
 
+// grad_reference_points of the fused backward at one level: the per-head partials part[H][n]
+// (n = B * Q * ref_dim) added in head order, for elements i0, i0 + step, ...
+__device__ __forceinline__ void ref_head_sum(const float* __restrict__ part, float* __restrict__ dref, int heads, int64_t n, int64_t i0,
+                                             int64_t step) {
+  constexpr int U = 8;  // heads' partials in flight per thread
+  for (int64_t i = i0; i < n; i += step) {
+    float sum = 0.0f;
+    for (int h0 = 0; h0 < heads; h0 += U) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = h0 + u < heads ? part[(h0 + u) * n + i] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (h0 + u < heads) sum += v[u];
+    }
+    dref[i] = sum;
+  }
+}
+
 // grad_value = the sum of the query blocks' partial sums, in block order (deterministic), rounded
 // once to the value dtype. `n` elements; block k starts at k * stride (stride: n rounded up to a
 // multiple of 4, so every block's quads are 16-byte aligned). Workgroup w (in XCD-contiguous
 // logical order, as the band kernel's) sums one contiguous range of quads: with the band kernel's
 // batch-major order, the partials an XCD reads are mostly those its own workgroups wrote. U quads
 // per thread and pass, every block's loads issued before the sums. vec: dv allows 16-byte (f32)
-// or 8-byte (bf16) stores of a quad.
+// or 8-byte (bf16) stores of a quad. rpart (or null): the fused backward's per-head reference-point
+// partials, added into dref by the same launch (ref_head_sum).
 template <typename VT>
 __global__ void __launch_bounds__(256) bwd_part_sum_kernel(const float* __restrict__ part, int nqb, int64_t n, int64_t stride,
-                                                           VT* __restrict__ dv, int vec) {
+                                                           VT* __restrict__ dv, int vec, const float* rpart, float* dref, int heads,
+                                                           int64_t nref) {
+  if (rpart != nullptr)
+    ref_head_sum(rpart, dref, heads, nref, static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x, static_cast<int64_t>(gridDim.x) * 256);
   constexpr int U = 4;
   const int64_t nq = n / 4;
   const int64_t T = 256;

@@ -12,9 +12,13 @@
 //  3. fused_epilogue_kernel: per row, the softmax VJP in place (grad_logit_k = a_k (dA_k -
 //     sum_j a_j dA_j)), the offsets' gradient (the transpose of fused_location_at), and the
 //     reference points' gradient summed over points (in order) and heads (a fixed shuffle tree).
+// At one level that fits the LDS whole (2 or 4 points, head_dim 16 or 32), the band kernel's
+// FZ instantiation does steps 1 and 3 itself, per (query, head) work item, and its per-head
+// reference-point partials are added in head order by the part-sum kernel (with query blocks) or
+// ref_head_sum_kernel.
 #pragma once
 
-#include "msda_kernels.h"
+#include "msda_band_kernels.h"
 
 namespace msda {
 
@@ -106,6 +110,12 @@ __global__ void __launch_bounds__(256) fused_epilogue_kernel(const FusedRowParam
       }
     }
   }
+}
+
+// The reference-point gradient of the band kernel's fused epilogue when no part-sum kernel runs:
+// the per-head partials added in head order (ref_head_sum).
+__global__ void __launch_bounds__(256) ref_head_sum_kernel(const float* part, float* dref, int heads, int64_t n) {
+  ref_head_sum(part, dref, heads, n, static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x, static_cast<int64_t>(gridDim.x) * 256);
 }
 
 }  // namespace msda

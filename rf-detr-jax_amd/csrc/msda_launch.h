@@ -44,10 +44,10 @@ int launch_fwd(const msda::SampleParams& p, int grid, int threads, int lds, hipS
   return check_launch("msda forward");
 }
 
-template <typename VT, typename GT, int CH, int KD>
+template <typename VT, typename GT, int CH, int KD, bool FZ = false>
 int launch_bwd_band(const msda::BandParams& p, int grid, int threads, int lds, hipStream_t stream) {
   static std::atomic<int> granted[kMaxDevices];
-  auto k = msda::bwd_band_kernel<VT, GT, CH, KD>;
+  auto k = msda::bwd_band_kernel<VT, GT, CH, KD, FZ>;
   int rc = allow_lds(k, lds, granted);
   if (rc != MSDA_OK) return rc;
   hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, stream, p);
@@ -56,8 +56,15 @@ int launch_bwd_band(const msda::BandParams& p, int grid, int threads, int lds, h
 
 // Channels per lane of the backward kernel (16, 8, 4, 2 or 1); head_dim 16 and 32 with 8- or
 // 16-channel lanes have kernels that know head_dim at compile time.
+// fused: the instantiations with the MSDeformAttn prologue and epilogue (8-channel lanes, head_dim
+// 16 or 32; the host checks the rest of the conditions).
 template <typename VT, typename GT>
-int dispatch_bwd_band_g(int ch, const msda::BandParams& p, int grid, int threads, int lds, hipStream_t st) {
+int dispatch_bwd_band_g(int ch, const msda::BandParams& p, int grid, int threads, int lds, hipStream_t st, bool fused) {
+  if (fused) {
+    if (ch == 8 && p.dim == 16) return launch_bwd_band<VT, GT, 8, 16, true>(p, grid, threads, lds, st);
+    if (ch == 8 && p.dim == 32) return launch_bwd_band<VT, GT, 8, 32, true>(p, grid, threads, lds, st);
+    return fail(MSDA_ERR_UNSUPPORTED, "no fused backward kernel for %d channels per lane, head_dim %d", ch, p.dim);
+  }
   switch (ch) {
     case 1: return launch_bwd_band<VT, GT, 1, 0>(p, grid, threads, lds, st);
     case 2: return launch_bwd_band<VT, GT, 2, 0>(p, grid, threads, lds, st);
@@ -75,15 +82,17 @@ int dispatch_bwd_band_g(int ch, const msda::BandParams& p, int grid, int threads
 }
 
 template <typename VT>
-int launch_part_sum(const float* part, int nqb, int64_t n, int64_t stride, void* dv, int vec, int grid, hipStream_t st) {
-  hipLaunchKernelGGL(msda::bwd_part_sum_kernel<VT>, dim3(grid), dim3(256), 0, st, part, nqb, n, stride, static_cast<VT*>(dv), vec);
+int launch_part_sum(const float* part, int nqb, int64_t n, int64_t stride, void* dv, int vec, int grid, hipStream_t st,
+                    const float* rpart, float* dref, int heads, int64_t nref) {
+  hipLaunchKernelGGL(msda::bwd_part_sum_kernel<VT>, dim3(grid), dim3(256), 0, st, part, nqb, n, stride, static_cast<VT*>(dv), vec,
+                     rpart, dref, heads, nref);
   return check_launch("msda backward (partial sums)");
 }
 
 template <typename VT>
-int dispatch_bwd_band(int ch, const msda::BandParams& p, int grid, int threads, int lds, hipStream_t st) {
-  return p.gout_bf16 ? dispatch_bwd_band_g<VT, msda::bf16_t>(ch, p, grid, threads, lds, st)
-                     : dispatch_bwd_band_g<VT, float>(ch, p, grid, threads, lds, st);
+int dispatch_bwd_band(int ch, const msda::BandParams& p, int grid, int threads, int lds, hipStream_t st, bool fused) {
+  return p.gout_bf16 ? dispatch_bwd_band_g<VT, msda::bf16_t>(ch, p, grid, threads, lds, st, fused)
+                     : dispatch_bwd_band_g<VT, float>(ch, p, grid, threads, lds, st, fused);
 }
 
 template <typename VT, typename GT, int KD, int NT>
@@ -137,10 +146,10 @@ int dispatch_fwd(int vec, int ns, bool fused, const msda::SampleParams& p, int g
 // Instantiated in msda_fwd_f32.hip, msda_fwd_bf16.hip, msda_bwd_f32.hip and msda_bwd_bf16.hip.
 extern template int dispatch_fwd<float>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
 extern template int dispatch_fwd<msda::bf16_t>(int, int, bool, const msda::SampleParams&, int, int, int, hipStream_t);
-extern template int dispatch_bwd_band<float>(int, const msda::BandParams&, int, int, int, hipStream_t);
-extern template int dispatch_bwd_band<msda::bf16_t>(int, const msda::BandParams&, int, int, int, hipStream_t);
-extern template int launch_part_sum<float>(const float*, int, int64_t, int64_t, void*, int, int, hipStream_t);
-extern template int launch_part_sum<msda::bf16_t>(const float*, int, int64_t, int64_t, void*, int, int, hipStream_t);
+extern template int dispatch_bwd_band<float>(int, const msda::BandParams&, int, int, int, hipStream_t, bool);
+extern template int dispatch_bwd_band<msda::bf16_t>(int, const msda::BandParams&, int, int, int, hipStream_t, bool);
+extern template int launch_part_sum<float>(const float*, int, int64_t, int64_t, void*, int, int, hipStream_t, const float*, float*, int, int64_t);
+extern template int launch_part_sum<msda::bf16_t>(const float*, int, int64_t, int64_t, void*, int, int, hipStream_t, const float*, float*, int, int64_t);
 extern template int dispatch_bwd_gather<float>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);
 extern template int dispatch_bwd_gather<msda::bf16_t>(int, bool, const msda::GatherParams&, int, int, int, hipStream_t);
 
