@@ -537,7 +537,9 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bw
 typedef __bf16 at_bf8 __attribute__((ext_vector_type(8)));
 typedef float at_f8 __attribute__((ext_vector_type(8)));
 
-constexpr int kAtLdt = kAtChunk + 8;  // row stride of a transposed bf16 tile
+// Row stride of a transposed bf16 tile: 136 bytes, so the 8-byte operand reads of 32 consecutive
+// rows fall on 32 distinct bank pairs (a 144-byte stride put rows c and c + 16 on the same pair).
+constexpr int kAtLdt = kAtChunk + 4;
 
 template <int D>
 constexpr int at_lds_bytes_bf16() { return (4 * kAtChunk * (D + 8) + 4 * D * kAtLdt) * 2 + 3 * kAtChunk * 4; }
