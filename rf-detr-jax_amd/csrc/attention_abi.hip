@@ -32,6 +32,10 @@ int at_validate(int dtype, int batch, int groups, int heads, int len, int head_d
     if (strides[i] < 0 || strides[i] % 4 != 0)
       return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: stride %d (%lld) must be a non-negative multiple of 4", i,
                   static_cast<long long>(strides[i]));
+  for (int t = 0; t < ntensors; ++t)  // the kernels form row offsets within a (slice, head) in 32 bits
+    if (strides[4 * t + 3] >= (int64_t{1} << 24) || static_cast<int64_t>(len) * strides[4 * t + 3] >= (int64_t{1} << 31))
+      return fail(MSDA_ERR_UNSUPPORTED, "attention: row stride %lld of tensor %d too large for %d rows",
+                  static_cast<long long>(strides[4 * t + 3]), t, len);
   return MSDA_OK;
 }
 

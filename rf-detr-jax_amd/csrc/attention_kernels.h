@@ -16,8 +16,9 @@
 //
 // Softmax: scores are scaled by log2(e) / sqrt(D) and exponentiated with exp2 (one rounding
 // different from exp of q.k / sqrt(D)); the forward is one pass over the key blocks with a running
-// maximum (rescaling the partial sums), and stores per query the final maximum m and log2 of the
-// denominator l for the backward, which recomputes the probabilities as exp2((x - m) - log2 l).
+// reference score m (moved, and the partial sums rescaled, only when a chunk's maximum exceeds it
+// by more than kAtLazy), and stores per query m and log2 of the denominator l relative to m for
+// the backward, which recomputes the probabilities as exp2((x - m) - log2 l).
 // Blocked positions take the score finfo(float32).min as in the reference (:93-96); keys past L
 // take -inf (weight 0).
 #pragma once
@@ -114,6 +115,10 @@ constexpr int kAtChunk = 64;  // streamed rows per LDS chunk
 template <int D>
 constexpr int at_lds_floats() { return 2 * kAtChunk * (D + 8) + 3 * kAtChunk; }  // two row tiles, three per-row floats
 
+// Element offset of row r of a tensor with row stride rs, in 32 bits by the full-rate 24-bit
+// multiply (the host bounds rs < 2^24 and L * rs < 2^31).
+__device__ __forceinline__ uint32_t at_row_off(int r, int64_t rs) { return __umul24(static_cast<uint32_t>(r), static_cast<uint32_t>(rs)); }
+
 // One tensor's slice of a 64-row chunk in registers: the thread's 4-element vectors, clamped to
 // row L - 1 (zeroed when stored).
 template <typename VT, int D, int NT>
@@ -124,7 +129,7 @@ struct AtChunk {
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
       const int idx = threadIdx.x + NT * u, row = idx / C4, c4 = idx - row * C4;
-      v[u] = at_ld4<VT>(src, min(r0 + row, L - 1) * rs + 4 * c4);
+      v[u] = at_ld4<VT>(src, at_row_off(min(r0 + row, L - 1), rs) + 4 * c4);
     }
   }
   __device__ void store(float* dst, int r0, int L) const {
@@ -195,6 +200,18 @@ __device__ __forceinline__ void at_accum2(at_f16 (&acc0)[D / 32], at_f16 (&acc1)
       }
 }
 
+// Reductions over the two halves of a wave (lanes l and l ^ 32, which hold the same query) by
+// v_permlane32_swap: both lanes get the same bits.
+__device__ __forceinline__ float at_max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float at_sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Scale two transposed score blocks (keys k0 + 32 h + 8 (i / 4) + 4 grp + i % 4 of register i, the
 // lane's query qi) by scale2, give keys past L the score -inf and blocked keys finfo.min (the mask
 // row of qi; qi < 0: no row), and take their maximum into bm. The mask test is hoisted out of the
@@ -229,43 +246,35 @@ __device__ __forceinline__ void at_scale_scores(at_f16& s0, at_f16& s1, int k0, 
 
 // Online softmax over one chunk's two score blocks (raw dot products in s0, s1; keys
 // k0 + 32 h + 8 (i / 4) + 4 grp + i % 4 of register i, the lane's query qi): turns them into
-// exp2(x - m_new) with x = s log2(e) / sqrt(D) (blocked: finfo.min; past L: -inf), updates the
-// running maximum m and sum l, and returns the factor alpha that rescales earlier partial sums.
-// Without a mask, on a full chunk, the maximum is taken on the raw scores (the scale is positive)
-// and each score costs one fma before the exp2.
+// exp2(x - m) with x = s log2(e) / sqrt(D) (blocked: finfo.min; past L: -inf) and adds them to the
+// running sum l. The reference score m moves only when the chunk's maximum exceeds it by more than
+// kAtLazy (then to that maximum, and the function returns the factor alpha = exp2(m_old - m_new)
+// that rescales l here and the caller's partial sums; otherwise alpha = 1 and nothing is
+// rescaled): weights stay within 2^kAtLazy, which f32 sums and the bf16 operands hold exactly as
+// well as weights within 1. The scores are scaled before their maximum is taken (a product is a
+// canonical float, so the maximum needs no quieting of its operands).
+constexpr float kAtLazy = 8.0f;
+
 template <bool MASK>
 __device__ __forceinline__ float at_softmax_chunk(at_f16& s0, at_f16& s1, int k0, int L, float scale2, const uint8_t* mask, int qi, int grp,
                                                   float& m, float& l) {
-  float mn;
-  if (!MASK && k0 + kAtChunk <= L) {
-    float bm = -INFINITY;
+  float bm = -INFINITY;
+  at_scale_scores<MASK>(s0, s1, k0, L, scale2, mask, qi, grp, bm);
+  bm = at_max_halves(bm);  // finite: every chunk holds a key below L
+  float alpha = 1.0f;
+  if (bm > m + kAtLazy) {  // also the first chunk (m = -inf); the same for both lanes of a query
+    alpha = at_exp2(m - bm);
+    m = bm;
+  }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) bm = fmaxf(bm, fmaxf(s0[i], s1[i]));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    mn = fmaxf(m, bm * scale2);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s0[i] = at_exp2(fmaf(s0[i], scale2, -mn));
-      s1[i] = at_exp2(fmaf(s1[i], scale2, -mn));
-    }
-  } else {
-    float bm = -INFINITY;
-    at_scale_scores<MASK>(s0, s1, k0, L, scale2, mask, qi, grp, bm);
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    mn = fmaxf(m, bm);  // finite: every chunk holds a key below L
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s0[i] = at_exp2(s0[i] - mn);
-      s1[i] = at_exp2(s1[i] - mn);
-    }
+  for (int i = 0; i < 16; ++i) {
+    s0[i] = at_exp2(s0[i] - m);
+    s1[i] = at_exp2(s1[i] - m);
   }
   float rs = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) rs += s0[i] + s1[i];
-  rs += __shfl_xor(rs, 32, 64);
-  const float alpha = at_exp2(m - mn);
-  l = l * alpha + rs;
-  m = mn;
+  l = l * alpha + at_sum_halves(rs);
   return alpha;
 }
 
@@ -319,10 +328,12 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : (MASK ? 1 
     at_f16 s0, s1;
     at_scores2<D>(s0, s1, Ks, qr, col, grp);
     const float alpha = at_softmax_chunk<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, qv ? qi : -1, grp, m, l);
+    if (alpha != 1.0f) {
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd) {
-      o0[nd] *= alpha;
-      o1[nd] *= alpha;
+      for (int nd = 0; nd < ND; ++nd) {
+        o0[nd] *= alpha;
+        o1[nd] *= alpha;
+      }
     }
     at_accum2<D>(o0, o1, Vs, Vs + 32 * LD, s0, s1, col, grp);  // O^T += V^T P^T, one chain per key block
   }
@@ -376,7 +387,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? ((MASK || RB == 2) ? 2 : 3)
       for (int jj = 0; jj < 4; ++jj) dsum += gr[c][jj] * ov[jj];
     }
   }
-  dsum += __shfl_xor(dsum, 32, 64);
+  dsum = at_sum_halves(dsum);
   float* stats = p.stats + (static_cast<int64_t>(w.zh) * L + qc) * 4;
   const float m = stats[0], ll = stats[1];
   if (qv && grp == 0 && qb < nb) stats[2] = dsum;  // read by the key-side kernel, launched after this one
@@ -481,13 +492,16 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bw
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int i = 4 * c4 + jj;
-        float x = s[i] * p.scale2;
+        // A lane past L holds the clamped last key: finite values in its own result column only,
+        // which is not stored. Rows past L have m = +inf: weight 0.
         if constexpr (MASK) {
           const int q = r0 + ql + jj;
+          float x = s[i] * p.scale2;
           if (q < L && p.mask[static_cast<int64_t>(q) * L + key] != 0) x = kAtMaskScore;
+          pw[i] = at_exp2((x - mq[jj]) - lq[jj]);
+        } else {
+          pw[i] = at_exp2(fmaf(s[i], p.scale2, -mq[jj]) - lq[jj]);
         }
-        // a lane past L holds the clamped last key: finite scores, dropped here
-        pw[i] = kv ? at_exp2((x - mq[jj]) - lq[jj]) : 0.0f;
         s[i] = pw[i] * (dp[i] - dd[jj]);  // dS
       }
     }
@@ -571,7 +585,7 @@ struct AtChunkB {
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
       const int idx = threadIdx.x + NT * u, row = idx / C4, c4 = idx - row * C4;
-      v[u] = *reinterpret_cast<const uint2*>(src + min(r0 + row, L - 1) * rs + 4 * c4);
+      v[u] = *reinterpret_cast<const uint2*>(src + at_row_off(min(r0 + row, L - 1), rs) + 4 * c4);
     }
   }
   __device__ void store_rows(uint16_t* dst, int r0, int L) const {  // [64][D + 8]
@@ -671,10 +685,12 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
     at_f16 s0, s1;
     at_scores_b<D>(s0, s1, Kr, Kr + 32 * LDR, qr, qr, col, grp);  // S^T for the chunk's two key blocks
     const float alpha = at_softmax_chunk<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, qv ? qi : -1, grp, m, l);
+    if (alpha != 1.0f) {
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd) {
-      o0[nd] *= alpha;
-      o1[nd] *= alpha;
+      for (int nd = 0; nd < ND; ++nd) {
+        o0[nd] *= alpha;
+        o1[nd] *= alpha;
+      }
     }
     at_accum_b<D>(o0, o1, Vt, Vt + 32, s0, s1, col, grp);  // O^T += V^T P^T
   }
@@ -727,7 +743,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
         dsum += g[0] * o[0] + g[1] * o[1] + g[2] * o[2] + g[3] * o[3];
       }
   }
-  dsum += __shfl_xor(dsum, 32, 64);
+  dsum = at_sum_halves(dsum);
   float* stats = p.stats + (static_cast<int64_t>(w.zh) * L + qc) * 4;
   const float m = stats[0], ll = stats[1];
   if (qv && grp == 0 && qb < nb) stats[2] = dsum;
@@ -836,12 +852,15 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int i = 4 * c4 + jj;
-          float x = s[i] * p.scale2;
+          // lanes past L and rows past L as in the f32 kernel
           if constexpr (MASK) {
             const int q = r0 + ql + jj;
+            float x = s[i] * p.scale2;
             if (q < L && p.mask[static_cast<int64_t>(q) * L + key] != 0) x = kAtMaskScore;
+            pw[i] = at_exp2((x - mq[jj]) - lq[jj]);
+          } else {
+            pw[i] = at_exp2(fmaf(s[i], p.scale2, -mq[jj]) - lq[jj]);
           }
-          pw[i] = kv ? at_exp2((x - mq[jj]) - lq[jj]) : 0.0f;
           s[i] = pw[i] * (dp[i] - dd[jj]);  // dS
         }
       }

@@ -490,6 +490,9 @@ def _at_bwd(**kw):
         (dict(d=48), _native.ERR_UNSUPPORTED, "head_dim"),
         (dict(len=-1), _native.ERR_INVALID_ARGUMENT, "negative"),
         (dict(strides=[2 * 9 * 32, 0, 9 * 32, 30] * 8), _native.ERR_INVALID_ARGUMENT, "multiple of 4"),
+        # row offsets within a (slice, head) are 32-bit: s_row < 2^24 and len * s_row < 2^31
+        (dict(strides=[0, 0, 0, 1 << 24] * 8), _native.ERR_UNSUPPORTED, "row stride"),
+        (dict(len=4096, strides=[0, 0, 0, 1 << 20] * 8), _native.ERR_UNSUPPORTED, "row stride"),
         (dict(q=0), _native.ERR_INVALID_ARGUMENT, "NULL"),
         (dict(k=(1 << 20) + 4), _native.ERR_INVALID_ARGUMENT, "aligned"),
     ],

@@ -82,6 +82,32 @@ def test_sdpa_against_oracle(shape, masked, bf16):
         assert_close(_np(t.grad), want, tg, f"grad_{name}")
 
 
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+@pytest.mark.parametrize("order", ["rising", "falling"])
+def test_sdpa_reference_score_moves(order, bf16):
+    """The forward's running reference score moves only when a key chunk's maximum exceeds it by
+    more than 8 (log2 units). Keys scaled up chunk by chunk (factors 1, 4, 7, 10, 13) move it at
+    every chunk, with the partial sums rescaled each time; scaled down, it never moves after the
+    first chunk and later weights are far below 1."""
+    b, h, length, d = 2, 4, 300, 32
+    _note(f"sdpa reference score {order} bf16={bf16}")
+    rng = np.random.default_rng(43)
+    q, k, v, g = (rng.standard_normal((b, h, length, d)).astype(np.float32) for _ in range(4))
+    factor = 1.0 + 3.0 * (np.arange(length) // 64)
+    k = k * (factor if order == "rising" else factor[::-1])[:, None].astype(np.float32)
+    if bf16:
+        q, k, v, g = (bf16_round(t) for t in (q, k, v, g))
+    dt = torch.bfloat16 if bf16 else None
+    tq, tk, tv = (_t(x, dt).requires_grad_(True) for x in (q, k, v))
+    out = scaled_dot_product_attention(tq, tk, tv)
+    out.backward(_t(g, dt))
+    torch.cuda.synchronize()
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    assert_close(_np(out), AT.sdpa(q, k, v, None), tf, "out")
+    for name, t, want in zip("qkv", (tq, tk, tv), AT.sdpa_vjp(q, k, v, g, None)):
+        assert_close(_np(t.grad), want, tg, f"grad_{name}")
+
+
 def test_reference_known_answers():
     """tests/test_attention.py:104-119 (at head_dim 32): equal scores give the mean of V, and the
     padding of the key blocks takes no weight."""

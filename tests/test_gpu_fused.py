@@ -136,6 +136,30 @@ def test_fused_kernel_variants(tune, variant):
     _check(out, grads, want_out, want_grads, False)
 
 
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+@pytest.mark.parametrize("points,ref_dim", [(2, 4), (2, 2), (4, 4)])
+def test_fused_in_kernel_and_row_paths_agree(tune, points, ref_dim, bf16):
+    """One whole level: the band kernel forms locations and weights itself and writes the offset,
+    logit and reference-point gradients (the in-kernel path); MSDA_FUSED_IN_KERNEL=0 forces the
+    prologue and epilogue row kernels around the plain band kernel. Both agree with the float64
+    oracle, and with each other to f32 rounding."""
+    shapes = ((24, 24),)
+    _note(f"fused in-kernel vs rows P={points} ref_dim={ref_dim} bf16={bf16}")
+    value, ref, off, logits, grad = make_fused_inputs(17, 3, 16, 16, 333, shapes, points, ref_dim,
+                                                      "bf16" if bf16 else "f32")
+    want_out, want_grads = _oracle64(value, shapes, ref, off, logits, grad, points)
+    runs = []
+    for flag in (1, 0):
+        tune({"MSDA_FUSED_IN_KERNEL": flag})
+        runs.append(_run_fused(value, shapes, ref, off, logits, grad, bf16))
+        _check(*runs[-1], want_out, want_grads, bf16)
+    (out1, g1), (out0, g0) = runs
+    assert np.array_equal(out1, out0), "the flag changes only the backward"
+    for name, a, b in zip(("grad_value", "grad_reference_points", "grad_sampling_offsets", "grad_attention_logits"),
+                          g1, g0):
+        assert_close(a, b, 1e-5, name)
+
+
 def test_fused_three_points_four_heads():
     """Four heads, three points (n_points not a power of two: the box form divides), one small
     level; the epilogue sums grad_reference_points over four head lanes."""
