@@ -17,7 +17,9 @@ graph replays (fwd_us, bwd_us, step_us) unless marked eager.
 
 Roofline: the dominant kernel's algorithmic HBM bytes (Workload.hbm_bytes) against 8 TB/s and its
 algorithmic LDS bytes (Workload.lds_bytes) against the LDS read peak measured in the same run by
-the library's probe (msda_probe_lds_read); `bound` is the resource whose time is larger. Configs
+the library's probe (msda_probe_lds_read); `bound` is the resource whose time is larger. For the
+backward, `roofline.lds_atomic` sets grad_value's f64 LDS additions (Workload.lds_atomic_adds)
+against the ds_add_f64 rate of a second probe (msda_probe_lds_atomic). Configs
 2 and 4 are also timed Infinity-Cache-cold ("cold" in per_config): the steps cycle through enough
 copies of the buffers that one pass over them exceeds the 256 MiB cache.
 
@@ -462,6 +464,36 @@ def lds_peak(dev, blocks=5120, reps=256, trials=5):
             "probe": "msda_probe_lds_read (ds_read_b128, 1 KB per wave instruction)"}
 
 
+def lds_atomic_peak(dev, blocks=5120, reps=64, trials=5):
+    """Device LDS f64 atomic-add rate (lane additions per second), measured with the library's
+    probe (msda_probe_lds_atomic: ds_add_f64, each wave instruction on 64 consecutive doubles) on
+    the current stream: best of `trials`; the probe's sums are checked."""
+    import torch
+
+    from rfdetr_jax_amd import _native
+
+    lib = _native.lib()
+    out = torch.empty(blocks * 256, dtype=torch.float64, device=dev)
+    ptr = ctypes.c_void_p(out.data_ptr())
+    ops = lib.msda_probe_lds_atomic_ops(blocks, reps)
+    h = _stream_handle()
+    _native.check(0 if lib.msda_probe_lds_atomic(ptr, blocks, reps, h) == 0 else _native.ERR_LAUNCH)
+    torch.cuda.synchronize()
+    if float(out.sum().item()) != float(ops):
+        raise RuntimeError("LDS atomic probe: wrong sum")
+    best = None
+    for _ in range(trials):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        lib.msda_probe_lds_atomic(ptr, blocks, reps, h)
+        end.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1000.0
+        best = us if best is None else min(best, us)
+    return {"gops": round(ops / best / 1e3, 1), "ops": ops, "us": round(best, 3), "blocks": blocks, "reps": reps,
+            "probe": "msda_probe_lds_atomic (ds_add_f64, 64 consecutive doubles per wave instruction)"}
+
+
 def measure_cold(w, dev, steps):
     """The step with its inputs and outputs not cache-resident: enough copies of the workload's
     buffers (at least three) that one pass over them exceeds the 256 MiB Infinity Cache; the steps
@@ -611,6 +643,13 @@ def main():
         lds = {"gbps": LDS_PEAK_NOMINAL_GBPS, "probe": "nominal (probe failed)"}
     lds_peak_gbps = lds["gbps"]
     log(f"LDS read peak {lds_peak_gbps:.0f} GB/s")
+    atom = None
+    if w.backward:
+        try:
+            atom = lds_atomic_peak(dev)
+            log(f"LDS f64 atomic-add peak {atom['gops']:.0f} G lane-adds/s")
+        except Exception as e:  # a measurement aid: the entry is left out
+            log(f"LDS atomic probe failed ({e})")
 
     kernels = {"fwd": (res["fwd_us_eager"], res["hbm_bytes"]["fwd"])}
     if w.backward:
@@ -651,6 +690,8 @@ def main():
                 entry.update({"bwd_us": round(r["bwd_us"], 3), "bwd_us_eager": round(r["bwd_us_eager"], 3),
                               "bwd_hbm_gbps": round(r["bwd_gbps"], 1),
                               "bwd_lds_gbps": round(lb["bwd"] / r["bwd_us"] / 1e3, 1)})
+                if atom is not None:
+                    entry["bwd_atomic_frac"] = round(cw.lds_atomic_adds() / atom["gops"] / 1e3 / r["bwd_us_eager"], 4)
             if cid in (2, 4):
                 log(f"workload {cw.name}: Infinity-Cache-cold steps")
                 entry["cold"] = measure_cold(cw, dev, max(60, args.steps // 2))
@@ -703,6 +744,12 @@ def main():
         "cpu_baseline": cpu,
         "per_config": per_config,
     }
+    if dom == "bwd" and atom is not None:
+        # grad_value's f64 LDS additions against the probe's rate: the backward's LDS-atomic bound
+        adds = w.lds_atomic_adds()
+        line["roofline"]["lds_atomic"] = {"adds": adds, "achieved_gops": round(adds / dom_us / 1e3, 1), "peak_gops": atom["gops"],
+                                          "peak_source": atom["probe"], "time_us": round(adds / atom["gops"] / 1e3, 3),
+                                          "frac": round(adds / atom["gops"] / 1e3 / dom_us, 4)}
     print(json.dumps(line), flush=True)
 
 

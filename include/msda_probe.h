@@ -24,6 +24,20 @@ int msda_probe_lds_read(unsigned* out, int blocks, int reps, void* stream);
 /* Bytes of LDS the probe reads for (blocks, reps): blocks * 256 threads * reps * 8 reads * 16 B. */
 int64_t msda_probe_lds_read_bytes(int blocks, int reps);
 
+/*
+ * LDS f64 atomic-add rate (the grad_value accumulation of msda_bwd adds with ds_add_f64):
+ * launches `blocks` workgroups of 256 threads on `stream`; every thread adds 1.0 with ds_add_f64
+ * 16 * reps times, each wave instruction to 64 consecutive doubles (every bank pair, each address
+ * once), and writes the sum of 16 of its workgroup's accumulators to `out` (blocks * 256
+ * doubles, device memory; they total 256 * 16 * reps per workgroup). The caller times the launch
+ * and divides msda_probe_lds_atomic_ops(blocks, reps) by the time. Returns 0, -1 on a bad
+ * argument, -3 on a launch failure.
+ */
+int msda_probe_lds_atomic(double* out, int blocks, int reps, void* stream);
+
+/* Lane additions the atomic probe performs for (blocks, reps): blocks * 256 * reps * 16. */
+int64_t msda_probe_lds_atomic_ops(int blocks, int reps);
+
 #ifdef __cplusplus
 }
 #endif

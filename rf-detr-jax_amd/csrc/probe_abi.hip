@@ -1,4 +1,5 @@
-// probe_abi.hip — LDS read-bandwidth probe of the device, for the benchmark's LDS roofline.
+// probe_abi.hip — LDS probes of the device (read bandwidth, f64 atomic-add rate), for the
+// benchmark's LDS rooflines.
 //
 // Every wave of every workgroup streams 16-byte LDS reads (ds_read_b128: the 64 lanes of a wave
 // read one contiguous 1 KB block per instruction; eight instructions in flight before one wait)
@@ -49,7 +50,40 @@ __global__ void __launch_bounds__(kProbeThreads) lds_read_probe_kernel(unsigned*
   out[blockIdx.x * kProbeThreads + threadIdx.x] = acc;
 }
 
+// LDS f64 atomic-add rate: every lane adds 1.0 with ds_add_f64 (no return) 16 times per repetition,
+// instruction u of a wave to the 64 consecutive doubles [64 u, 64 u + 64) of the wave's 8 KB
+// region (the lanes of an instruction cover every bank pair, each address once), then the thread
+// writes the sum of 16 of the doubles (the workgroup's total is 256 * 16 * reps).
+constexpr int kAtomicUnroll = 16;
+
+__global__ void __launch_bounds__(kProbeThreads) lds_atomic_probe_kernel(double* out, int reps) {
+  __shared__ __align__(16) double acc[kProbeThreads * kAtomicUnroll];  // 32 KB
+  for (int i = threadIdx.x; i < kProbeThreads * kAtomicUnroll; i += kProbeThreads) acc[i] = 0.0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  double* region = acc + wave * 64 * kAtomicUnroll + lane;
+  for (int r = 0; r < reps; ++r) {
+#pragma unroll
+    for (int u = 0; u < kAtomicUnroll; ++u) __hip_atomic_fetch_add(region + 64 * u, 1.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __syncthreads();
+  const double* mine = acc + threadIdx.x * kAtomicUnroll;
+  double sum = 0.0;
+  for (int i = 0; i < kAtomicUnroll; ++i) sum += mine[i];
+  out[blockIdx.x * kProbeThreads + threadIdx.x] = sum;
+}
+
 }  // namespace
+
+extern "C" int msda_probe_lds_atomic(double* out, int blocks, int reps, void* stream) {
+  if (out == nullptr || blocks < 1 || reps < 1) return -1;
+  hipLaunchKernelGGL(lds_atomic_probe_kernel, dim3(blocks), dim3(kProbeThreads), 0, static_cast<hipStream_t>(stream), out, reps);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int64_t msda_probe_lds_atomic_ops(int blocks, int reps) {
+  return static_cast<int64_t>(blocks) * kProbeThreads * reps * kAtomicUnroll;
+}
 
 extern "C" int msda_probe_lds_read(unsigned* out, int blocks, int reps, void* stream) {
   if (out == nullptr || blocks < 1 || reps < 1) return -1;

@@ -73,6 +73,11 @@ class Workload:
         bwd = corners * sv + corners * 4 + slices * sv + slices * 4 if self.backward else 0
         return {"fwd": fwd, "bwd": bwd, "total": fwd + bwd}
 
+    def lds_atomic_adds(self) -> int:
+        """Algorithmic LDS atomic additions of the backward: grad_value gets four corner rows of
+        head_dim channels per sample, each channel one f64 addition (ds_add_f64)."""
+        return self.samples * 4 * self.head_dim if self.backward else 0
+
     def scaled(self, batch: int | None = None, queries: int | None = None) -> "Workload":
         return Workload(self.cfg_id, self.name, batch or self.batch, self.heads, self.head_dim, queries or self.queries,
                         self.shapes, self.points, self.value_dtype, self.backward, self.uniform_locations)
