@@ -246,30 +246,57 @@ __device__ __forceinline__ void at_scale_scores(at_f16& s0, at_f16& s1, int k0, 
 
 // Online softmax over one chunk's two score blocks (raw dot products in s0, s1; keys
 // k0 + 32 h + 8 (i / 4) + 4 grp + i % 4 of register i, the lane's query qi): turns them into
-// exp2(x - m) with x = s log2(e) / sqrt(D) (blocked: finfo.min; past L: -inf) and adds them to the
-// running sum l. The reference score m moves only when the chunk's maximum exceeds it by more than
-// kAtLazy (then to that maximum, and the function returns the factor alpha = exp2(m_old - m_new)
-// that rescales l here and the caller's partial sums; otherwise alpha = 1 and nothing is
-// rescaled): weights stay within 2^kAtLazy, which f32 sums and the bf16 operands hold exactly as
-// well as weights within 1. The scores are scaled before their maximum is taken (a product is a
-// canonical float, so the maximum needs no quieting of its operands).
+// exp2(x - m) with x = s log2(e) / sqrt(D) (blocked: finfo.min; past L: -inf), against a running
+// reference score m that starts at 0 and moves only when the chunk's maximum exceeds it by more
+// than kAtLazy, or, while nothing has been summed (l = 0), lies more than kAtLow below it: weights
+// stay within 2^kAtLazy, which the f32 sums and bf16 operands hold as well as weights within 1, and
+// no weight that matters flushes to zero. When m moves, the function returns the factor alpha =
+// exp2(m_old - m_new) (0 while l = 0) that rescales l here and the caller's partial sums;
+// otherwise alpha = 1.
+// Without a mask, on a full chunk, each score costs one fma (x - m) before exp2, and the maximum
+// is taken on those (a computed float is canonical, so the maximum needs no quieting of its
+// operands).
 constexpr float kAtLazy = 8.0f;
+constexpr float kAtLow = 64.0f;
 
 template <bool MASK>
 __device__ __forceinline__ float at_softmax_chunk(at_f16& s0, at_f16& s1, int k0, int L, float scale2, const uint8_t* mask, int qi, int grp,
                                                   float& m, float& l) {
-  float bm = -INFINITY;
-  at_scale_scores<MASK>(s0, s1, k0, L, scale2, mask, qi, grp, bm);
-  bm = at_max_halves(bm);  // finite: every chunk holds a key below L
-  float alpha = 1.0f;
-  if (bm > m + kAtLazy) {  // also the first chunk (m = -inf); the same for both lanes of a query
-    alpha = at_exp2(m - bm);
-    m = bm;
+  float bm = -INFINITY, alpha = 1.0f;
+  if (!MASK && k0 + kAtChunk <= L) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s0[i] = fmaf(s0[i], scale2, -m);
+      s1[i] = fmaf(s1[i], scale2, -m);
+      bm = fmaxf(bm, fmaxf(s0[i], s1[i]));
+    }
+    bm = at_max_halves(bm);  // relative to m; the same in both lanes of a query
+    if (bm > kAtLazy || (l == 0.0f && bm < -kAtLow)) {
+      alpha = l == 0.0f ? 0.0f : at_exp2(-bm);
+      m += bm;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s0[i] -= bm;
+        s1[i] -= bm;
+      }
+    }
+  } else {
+    at_scale_scores<MASK>(s0, s1, k0, L, scale2, mask, qi, grp, bm);
+    bm = at_max_halves(bm);  // finite: every chunk holds a key below L
+    if (bm > m + kAtLazy || (l == 0.0f && bm < m - kAtLow)) {
+      alpha = l == 0.0f ? 0.0f : at_exp2(m - bm);
+      m = bm;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s0[i] -= m;
+      s1[i] -= m;
+    }
   }
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    s0[i] = at_exp2(s0[i] - m);
-    s1[i] = at_exp2(s1[i] - m);
+    s0[i] = at_exp2(s0[i]);
+    s1[i] = at_exp2(s1[i]);
   }
   float rs = 0.0f;
 #pragma unroll
@@ -308,7 +335,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : (MASK ? 1 
 #pragma unroll
     for (int c = 0; c < D / 8; ++c) qr[c] = at_ld4<VT>(qp, min(qi, L - 1) * p.st[kAtQ][3] + 8 * c + 4 * grp);
   }
-  float m = -INFINITY, l = 0.0f;
+  float m = 0.0f, l = 0.0f;  // reference score and sum (at_softmax_chunk)
   at_f16 o0[ND], o1[ND];
 #pragma unroll
   for (int nd = 0; nd < ND; ++nd) o0[nd] = o1[nd] = at_zero16();
@@ -665,7 +692,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
   const bool qv = qi < L;
   at_bf8 qr[D / 16];
   at_row_bf8<D>(qr, static_cast<const uint16_t*>(p.q) + w.sl.base(p, kAtQ), min(qi, L - 1) * p.st[kAtQ][3], grp);
-  float m = -INFINITY, l = 0.0f;
+  float m = 0.0f, l = 0.0f;  // reference score and sum (at_softmax_chunk)
   at_f16 o0[ND], o1[ND];
 #pragma unroll
   for (int nd = 0; nd < ND; ++nd) o0[nd] = o1[nd] = at_zero16();
