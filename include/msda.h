@@ -303,8 +303,8 @@ int msda_value_proj_bwd(const void* input, int dtype, const float* weight, const
  * layers.py:69, :93-94) or NULL. dtype: MSDA_DTYPE_F32 or MSDA_DTYPE_BF16 for every tensor;
  * arithmetic is f32 (v_mfma_f32_32x32x2_f32), softmax in f32.
  * stats: [batch * groups * heads * len][4] f32, 16-byte aligned, z-major (z = g * batch + b), then
- * head, then query: the forward writes entries 0 and 1 (a reference score m, within 8 below the
- * row maximum, and log2 of the softmax denominator taken relative to m, in units of
+ * head, then query: the forward writes entries 0 and 1 (a reference score m, between 8 below and
+ * 64 above the row maximum, and log2 of the softmax denominator taken relative to m, in units of
  * log2(e) q.k / sqrt(D)); the backward reads them and uses entry 2 for rowsum(grad_out * out).
  * Dropout on the attention weights (layers.py:537-544, active only with dropout > 0 in training)
  * is not part of this function. len is at most 65536, each row stride s_row below 2^24 elements
