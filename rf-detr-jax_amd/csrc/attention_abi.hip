@@ -16,10 +16,8 @@ using msda_host::fail;
 
 int lds_bytes(int d) { return (d == 32 ? msda::at_lds_floats<32>() : msda::at_lds_floats<64>()) * 4; }
 
-// bf16 kernels: row tiles [64][D + 8] and transposed tiles [D][72] of bf16, and per-row floats
-int lds_bf16(int d, int row_tiles, int t_tiles, bool rows_f32) {
-  return (row_tiles * msda::kAtChunk * (d + 8) + t_tiles * d * msda::kAtLdt) * 2 + (rows_f32 ? 3 * msda::kAtChunk * 4 : 0);
-}
+// bf16 kernels: two swizzled row tiles [64][D] of bf16, and (key side) three floats per row
+int lds_bf16(int d, bool rows_f32) { return 2 * msda::kAtChunk * d * 2 + (rows_f32 ? 3 * msda::kAtChunk * 4 : 0); }
 
 int at_validate(int dtype, int batch, int groups, int heads, int len, int head_dim, const int64_t* strides, int ntensors) {
   if (dtype != MSDA_DTYPE_F32 && dtype != MSDA_DTYPE_BF16) return fail(MSDA_ERR_UNSUPPORTED, "attention: unsupported dtype code %d", dtype);
@@ -113,7 +111,7 @@ int bwd_typed(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
 template <int D, bool MASK, int RB>
 int fwd_b_rb(const msda::AttnParams& p, hipStream_t st) {
   static std::atomic<int> granted[msda_host::kMaxDevices];
-  return at_launch(msda::attn_fwd_bf16_kernel<D, MASK, RB>, granted, p, lds_bf16(D, 1, 1, false), RB, st, "attention forward");
+  return at_launch(msda::attn_fwd_bf16_kernel<D, MASK, RB>, granted, p, lds_bf16(D, false), RB, st, "attention forward");
 }
 
 template <int D, bool MASK>
@@ -126,13 +124,13 @@ int bwd_b_rb(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
   int rc = MSDA_OK;
   {
     static std::atomic<int> granted[msda_host::kMaxDevices];
-    if ((rc = at_launch(msda::attn_bwd_q_bf16_kernel<D, MASK, RB>, granted, p, lds_bf16(D, 2, 1, false), RB, st,
+    if ((rc = at_launch(msda::attn_bwd_q_bf16_kernel<D, MASK, RB>, granted, p, lds_bf16(D, false), RB, st,
                         "attention backward (queries)")) != MSDA_OK)
       return rc;
   }
   if (want_kv) {
     static std::atomic<int> granted[msda_host::kMaxDevices];
-    rc = at_launch(msda::attn_bwd_kv_bf16_kernel<D, MASK, 4>, granted, p, lds_bf16(D, 2, 2, true), 4, st, "attention backward (keys, values)");
+    rc = at_launch(msda::attn_bwd_kv_bf16_kernel<D, MASK, 4>, granted, p, lds_bf16(D, true), 4, st, "attention backward (keys, values)");
   }
   return rc;
 }

@@ -566,9 +566,10 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bw
 }
 
 // ---- bf16 inputs: products on v_mfma_f32_32x32x16_bf16 -------------------------------------
-// Same work split, streaming and softmax as the f32 kernels. Operands stay bf16 in LDS: row tiles
-// [64][D + 8] (operands along the channels: one 16-byte read per MFMA) and transposed tiles
-// [D][64 + 8] (operands along the streamed rows: two 8-byte reads). v_mfma_f32_32x32x16_bf16: lane
+// Same work split, streaming and softmax as the f32 kernels. Operands stay bf16 in LDS, in one
+// swizzled row tile [64][D] per streamed tensor: operands along the channels are one 16-byte read
+// per MFMA, operands along the streamed rows two transposing reads (ds_read_b64_tr_b16) of the
+// same tile, so no transposed copy is staged. v_mfma_f32_32x32x16_bf16: lane
 // l supplies 8 elements of A row l % 32 and of B column l % 32 in reduction slots 8 (l / 32) + j,
 // and the product pairs slot j of both operands, so any reduction-index assignment shared by A and
 // B gives the sum; the result layout is that of the f32 32 x 32 products. Probabilities and dS
@@ -577,13 +578,6 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bw
 
 typedef __bf16 at_bf8 __attribute__((ext_vector_type(8)));
 typedef float at_f8 __attribute__((ext_vector_type(8)));
-
-// Row stride of a transposed bf16 tile: 136 bytes, so the 8-byte operand reads of 32 consecutive
-// rows fall on 32 distinct bank pairs (a 144-byte stride put rows c and c + 16 on the same pair).
-constexpr int kAtLdt = kAtChunk + 4;
-
-template <int D>
-constexpr int at_lds_bytes_bf16() { return (4 * kAtChunk * (D + 8) + 4 * D * kAtLdt) * 2 + 3 * kAtChunk * 4; }
 
 __device__ __forceinline__ at_bf8 at_bf8_of(uint2 lo, uint2 hi) { return __builtin_bit_cast(at_bf8, uint4{lo.x, lo.y, hi.x, hi.y}); }
 
@@ -603,6 +597,31 @@ __device__ __forceinline__ void at_row_bf8(at_bf8 (&r)[D / 16], const uint16_t* 
   }
 }
 
+// Swizzled row tiles [64][D] of bf16, without padding: 16-byte chunk c of row r sits at slot
+// c ^ at_sw(r), so the rows that 16 lanes read at one chunk index (row operands, one 16-byte read
+// per lane) and the four consecutive rows of a transposing read (below) fall on distinct banks.
+template <int D>
+__device__ __forceinline__ int at_sw(int r) {
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  return (r / (16 / CPR)) & (CPR - 1);
+}
+
+// element offset of channels ch .. ch + 3 of row r in a swizzled tile (ch a multiple of 4)
+template <int D>
+__device__ __forceinline__ int at_swo(int r, int ch) {
+  return r * D + 8 * ((ch >> 3) ^ at_sw<D>(r)) + (ch & 7);
+}
+
+typedef short at_s4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane 4a + b receives element b of the 8 bytes
+// that lanes a, 4 + a, 8 + a and 12 + a address (in that order): the 16 x 4 block of 16-bit
+// elements the group addresses, transposed.
+__device__ __forceinline__ uint2 at_read_tr(const uint16_t* p) {
+  const at_s4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) at_s4*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
 // A raw bf16 chunk (64 rows x D) in registers: 4-element vectors, rows clamped to L - 1.
 template <int D, int NT>
 struct AtChunkB {
@@ -615,50 +634,40 @@ struct AtChunkB {
       v[u] = *reinterpret_cast<const uint2*>(src + at_row_off(min(r0 + row, L - 1), rs) + 4 * c4);
     }
   }
-  __device__ void store_rows(uint16_t* dst, int r0, int L) const {  // [64][D + 8]
+  __device__ void store_sw(uint16_t* dst, int r0, int L) const {  // swizzled [64][D]
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
       const int idx = threadIdx.x + NT * u, row = idx / C4, c4 = idx - row * C4;
-      *reinterpret_cast<uint2*>(&dst[row * (D + 8) + 4 * c4]) = r0 + row < L ? v[u] : uint2{0u, 0u};
-    }
-  }
-  __device__ void store_t(uint16_t* dst, int r0, int L) const {  // [D][64 + 8]
-#pragma unroll
-    for (int u = 0; u < NV; ++u) {
-      const int idx = threadIdx.x + NT * u, row = idx / C4, c4 = idx - row * C4;
-      const uint2 w = r0 + row < L ? v[u] : uint2{0u, 0u};
-      dst[(4 * c4) * kAtLdt + row] = static_cast<uint16_t>(w.x);
-      dst[(4 * c4 + 1) * kAtLdt + row] = static_cast<uint16_t>(w.x >> 16);
-      dst[(4 * c4 + 2) * kAtLdt + row] = static_cast<uint16_t>(w.y);
-      dst[(4 * c4 + 3) * kAtLdt + row] = static_cast<uint16_t>(w.y >> 16);
+      *reinterpret_cast<uint2*>(&dst[at_swo<D>(row, 4 * c4)]) = r0 + row < L ? v[u] : uint2{0u, 0u};
     }
   }
 };
 
-// Result-layout scores of two 32-row blocks against register operands: s0 = X0 . xr, s1 = X1 . yr
-// (X rows from a row tile, the lane's row of X at col; two chains).
+// Result-layout scores of two 32-row blocks of swizzled row tiles against register operands (two
+// chains): s0 = X[rx .. rx + 31] . xr, s1 = Y[ry .. ry + 31] . yr (the lane's row at col).
 template <int D>
-__device__ __forceinline__ void at_scores_b(at_f16& s0, at_f16& s1, const uint16_t* X0, const uint16_t* X1, const at_bf8 (&xr)[D / 16],
-                                            const at_bf8 (&yr)[D / 16], int col, int grp) {
-  constexpr int LDR = D + 8;
+__device__ __forceinline__ void at_scores_sw(at_f16& s0, at_f16& s1, const uint16_t* X, int rx, const uint16_t* Y, int ry,
+                                             const at_bf8 (&xr)[D / 16], const at_bf8 (&yr)[D / 16], int col, int grp) {
   s0 = at_zero16();
   s1 = at_zero16();
 #pragma unroll
   for (int s = 0; s < D / 16; ++s) {
-    const at_bf8 a0 = __builtin_bit_cast(at_bf8, *reinterpret_cast<const uint4*>(&X0[col * LDR + 16 * s + 8 * grp]));
-    const at_bf8 a1 = __builtin_bit_cast(at_bf8, *reinterpret_cast<const uint4*>(&X1[col * LDR + 16 * s + 8 * grp]));
+    const at_bf8 a0 = __builtin_bit_cast(at_bf8, *reinterpret_cast<const uint4*>(&X[at_swo<D>(rx + col, 16 * s + 8 * grp)]));
+    const at_bf8 a1 = __builtin_bit_cast(at_bf8, *reinterpret_cast<const uint4*>(&Y[at_swo<D>(ry + col, 16 * s + 8 * grp)]));
     s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, xr[s], s0, 0, 0, 0);
     s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, yr[s], s1, 0, 0, 0);
   }
 }
 
-// acc0 += X0^T w0 and acc1 += X1^T w1 over one 32-row block (two chains): X from transposed tiles
-// (X0t, X1t at the block's first row), w in result-layout registers (register i is row
-// 8 (i / 4) + 4 (l / 32) + i % 4; slots 0..7 of MFMA s are registers 8 s .. 8 s + 7, rows
-// 16 s + 4 (l / 32) + 0..3 and 16 s + 8 + 4 (l / 32) + 0..3).
+// acc0 += X0^T w0 and acc1 += X1^T w1 (two chains) for the 32-row blocks at rows x0 of X0 and x1 of
+// X1, swizzled row tiles read by transposing reads, w in result-layout registers. Lane l's operand of MFMA (nd, s) holds
+// channel 32 nd + l % 32 at rows 16 s + 8 h + 4 (l / 32) + j (slot 4 h + j), the rows of result
+// register 8 s + 4 h + j of w: each of the two reads (h) has lane r of a 16-lane group g address
+// row 16 s + 8 h + 4 (l / 32) + r / 4, channels 32 nd + 16 (g % 2) + 4 (r % 4) .. + 3.
 template <int D>
-__device__ __forceinline__ void at_accum_b(at_f16 (&acc0)[D / 32], at_f16 (&acc1)[D / 32], const uint16_t* X0t, const uint16_t* X1t,
-                                           const at_f16& w0, const at_f16& w1, int col, int grp) {
+__device__ __forceinline__ void at_accum_tr(at_f16 (&acc0)[D / 32], at_f16 (&acc1)[D / 32], const uint16_t* X0, int x0, const uint16_t* X1,
+                                            int x1, const at_f16& w0, const at_f16& w1, int lane) {
+  const int g = lane >> 4, r = lane & 15, grp = lane >> 5;
   at_bf8 b0[2], b1[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
@@ -669,9 +678,9 @@ __device__ __forceinline__ void at_accum_b(at_f16 (&acc0)[D / 32], at_f16 (&acc1
   for (int nd = 0; nd < D / 32; ++nd)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int o = (32 * nd + col) * kAtLdt + 16 * s + 4 * grp;
-      const at_bf8 a0 = at_bf8_of(*reinterpret_cast<const uint2*>(&X0t[o]), *reinterpret_cast<const uint2*>(&X0t[o + 8]));
-      const at_bf8 a1 = at_bf8_of(*reinterpret_cast<const uint2*>(&X1t[o]), *reinterpret_cast<const uint2*>(&X1t[o + 8]));
+      const int c = 32 * nd + 16 * (g & 1) + 4 * (r & 3), ro = 16 * s + 4 * grp + (r >> 2);
+      const at_bf8 a0 = at_bf8_of(at_read_tr(X0 + at_swo<D>(x0 + ro, c)), at_read_tr(X0 + at_swo<D>(x0 + ro + 8, c)));
+      const at_bf8 a1 = at_bf8_of(at_read_tr(X1 + at_swo<D>(x1 + ro, c)), at_read_tr(X1 + at_swo<D>(x1 + ro + 8, c)));
       acc0[nd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0[s], acc0[nd], 0, 0, 0);
       acc1[nd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1[s], acc1[nd], 0, 0, 0);
     }
@@ -679,10 +688,10 @@ __device__ __forceinline__ void at_accum_b(at_f16 (&acc0)[D / 32], at_f16 (&acc1
 
 template <int D, bool MASK, int RB>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel(const AttnParams p) {
-  constexpr int NT = 64 * RB, LDR = D + 8, ND = D / 32;
+  constexpr int NT = 64 * RB, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
-  uint16_t* Kr = reinterpret_cast<uint16_t*>(at_lds);
-  uint16_t* Vt = Kr + kAtChunk * LDR;
+  uint16_t* Kr = reinterpret_cast<uint16_t*>(at_lds);  // swizzled [64][D] key and value rows
+  uint16_t* Vr = Kr + kAtChunk * D;
   const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
   const AttnWork w(p, (nb + RB - 1) / RB);
   const uint16_t* kp = static_cast<const uint16_t*>(p.k) + w.sl.base(p, kAtK);
@@ -701,8 +710,8 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
   vc.load(vp, p.st[kAtV][3], 0, L);
   for (int j = 0; j < nchunks; ++j) {
     __syncthreads();
-    kc.store_rows(Kr, j * kAtChunk, L);
-    vc.store_t(Vt, j * kAtChunk, L);
+    kc.store_sw(Kr, j * kAtChunk, L);
+    vc.store_sw(Vr, j * kAtChunk, L);
     __syncthreads();
     if (j + 1 < nchunks) {
       kc.load(kp, p.st[kAtK][3], (j + 1) * kAtChunk, L);
@@ -710,7 +719,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
     }
     if (qb >= nb) continue;
     at_f16 s0, s1;
-    at_scores_b<D>(s0, s1, Kr, Kr + 32 * LDR, qr, qr, col, grp);  // S^T for the chunk's two key blocks
+    at_scores_sw<D>(s0, s1, Kr, 0, Kr, 32, qr, qr, col, grp);  // S^T for the chunk's two key blocks
     const float alpha = at_softmax_chunk<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, qv ? qi : -1, grp, m, l);
     if (alpha != 1.0f) {
 #pragma unroll
@@ -719,7 +728,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
         o1[nd] *= alpha;
       }
     }
-    at_accum_b<D>(o0, o1, Vt, Vt + 32, s0, s1, col, grp);  // O^T += V^T P^T
+    at_accum_tr<D>(o0, o1, Vr, 0, Vr, 32, s0, s1, lane);  // O^T += V^T P^T
   }
   if (qv) {
     bf16_t* op = static_cast<bf16_t*>(p.out) + w.sl.base(p, kAtO);
@@ -739,11 +748,10 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
 
 template <int D, bool MASK, int RB>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_q_bf16_kernel(const AttnParams p) {
-  constexpr int NT = 64 * RB, LDR = D + 8, ND = D / 32;
+  constexpr int NT = 64 * RB, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
-  uint16_t* Kr = reinterpret_cast<uint16_t*>(at_lds);
-  uint16_t* Vr = Kr + kAtChunk * LDR;
-  uint16_t* Kt = Vr + kAtChunk * LDR;
+  uint16_t* Kr = reinterpret_cast<uint16_t*>(at_lds);  // swizzled [64][D] key and value rows
+  uint16_t* Vr = Kr + kAtChunk * D;
   const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
   const AttnWork w(p, (nb + RB - 1) / RB);
   const uint16_t* kp = static_cast<const uint16_t*>(p.k) + w.sl.base(p, kAtK);
@@ -783,9 +791,8 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
   vc.load(vp, p.st[kAtV][3], 0, L);
   for (int j = 0; j < nchunks; ++j) {
     __syncthreads();
-    kc.store_rows(Kr, j * kAtChunk, L);
-    kc.store_t(Kt, j * kAtChunk, L);
-    vc.store_rows(Vr, j * kAtChunk, L);
+    kc.store_sw(Kr, j * kAtChunk, L);
+    vc.store_sw(Vr, j * kAtChunk, L);
     __syncthreads();
     if (j + 1 < nchunks) {
       kc.load(kp, p.st[kAtK][3], (j + 1) * kAtChunk, L);
@@ -794,7 +801,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
     if (qb >= nb) continue;
     at_f16 s[2], dp[2];
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) at_scores_b<D>(s[h2], dp[h2], Kr + 32 * h2 * LDR, Vr + 32 * h2 * LDR, qr, gr, col, grp);
+    for (int h2 = 0; h2 < 2; ++h2) at_scores_sw<D>(s[h2], dp[h2], Kr, 32 * h2, Vr, 32 * h2, qr, gr, col, grp);
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
@@ -805,7 +812,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
         else if (MASK && qv && p.mask[static_cast<int64_t>(qi) * L + key] != 0) x = kAtMaskScore;
         s[h2][i] = at_exp2((x - m) - ll) * (dp[h2][i] - dsum);  // dS^T
       }
-    at_accum_b<D>(dq0, dq1, Kt, Kt + 32, s[0], s[1], col, grp);  // dQ^T += K^T dS^T
+    at_accum_tr<D>(dq0, dq1, Kr, 0, Kr, 32, s[0], s[1], lane);  // dQ^T += K^T dS^T
   }
   if (qv) {
     bf16_t* gqp = static_cast<bf16_t*>(p.gq) + w.sl.base(p, kAtGQ);
@@ -819,13 +826,11 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
 
 template <int D, bool MASK, int RB>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_kv_bf16_kernel(const AttnParams p) {
-  constexpr int NT = 64 * RB, LDR = D + 8, ND = D / 32;
+  constexpr int NT = 64 * RB, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
-  uint16_t* Qr = reinterpret_cast<uint16_t*>(at_lds);
-  uint16_t* Gr = Qr + kAtChunk * LDR;
-  uint16_t* Qt = Gr + kAtChunk * LDR;
-  uint16_t* Gt = Qt + D * kAtLdt;
-  float* Ms = reinterpret_cast<float*>(Gt + D * kAtLdt);  // [64][2]: m, log2 l (rows past L: +inf)
+  uint16_t* Qr = reinterpret_cast<uint16_t*>(at_lds);  // swizzled [64][D] query and output-gradient rows
+  uint16_t* Gr = Qr + kAtChunk * D;
+  float* Ms = reinterpret_cast<float*>(Gr + kAtChunk * D);  // [64][2]: m, log2 l (rows past L: +inf)
   float* Ds = Ms + 2 * kAtChunk;                          // [64]: rowsum(dO * O)
   const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
   const AttnWork w(p, (nb + RB - 1) / RB);
@@ -852,10 +857,8 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
   for (int j = 0; j < nchunks; ++j) {
     const int r0 = j * kAtChunk;
     __syncthreads();
-    qc.store_rows(Qr, r0, L);
-    qc.store_t(Qt, r0, L);
-    gc.store_rows(Gr, r0, L);
-    gc.store_t(Gt, r0, L);
+    qc.store_sw(Qr, r0, L);
+    gc.store_sw(Gr, r0, L);
     if (t < kAtChunk) {
       const bool in = r0 + t < L;
       Ms[2 * t] = in ? sq[0] : INFINITY;
@@ -868,7 +871,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {  // the chunk's two query blocks
       at_f16 s, dp;
-      at_scores_b<D>(s, dp, Qr + 32 * h2 * LDR, Gr + 32 * h2 * LDR, kr, vr, col, grp);  // S = Q K^T, dP = dO V^T
+      at_scores_sw<D>(s, dp, Qr, 32 * h2, Gr, 32 * h2, kr, vr, col, grp);  // S = Q K^T, dP = dO V^T
       at_f16 pw;
 #pragma unroll
       for (int c4 = 0; c4 < 4; ++c4) {
@@ -891,7 +894,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
           s[i] = pw[i] * (dp[i] - dd[jj]);  // dS
         }
       }
-      at_accum_b<D>(dv, dk, Gt + 32 * h2, Qt + 32 * h2, pw, s, col, grp);  // dV^T += dO^T P, dK^T += Q^T dS
+      at_accum_tr<D>(dv, dk, Gr, 32 * h2, Qr, 32 * h2, pw, s, lane);  // dV^T += dO^T P, dK^T += Q^T dS
     }
   }
   if (kv) {
