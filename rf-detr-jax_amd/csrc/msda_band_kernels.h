@@ -319,11 +319,15 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
   const int owned_elems = (r1 - r0) * W * D;
 
   // 1. staging (issued here, waited for before the barrier that precedes its use) and accumulator
+  //    zeroing. A band's staging goes to the upper half of the waves, so that the lower half's scan
+  //    loads (phase 2) do not queue behind the transfers (loads complete in issue order).
   if (tid == 0) cnt[0] = 0;
   if (!whole) __syncthreads();  // the counter, before any append
+  const int nwaves_all = nt >> 6;
+  const int stage_w0 = (!whole && nwaves_all >= 2) ? nwaves_all / 2 : 0;
   if (want_dots)
     stage_copy<VT, false>(vrows, static_cast<const VT*>(p.value) + n * slice + static_cast<int64_t>(L.start + r0 * W) * D,
-                          (rv1 - r0) * W * D, p.vec16 != 0);
+                          (rv1 - r0) * W * D, p.vec16 != 0, stage_w0, nwaves_all - stage_w0);
   if (want_dv)  // the band's cells and the guard cell on each side
     for (int i = tid; i < owned_elems + 2 * D; i += nt) accp[i - D] = 0.0;
 
@@ -597,8 +601,10 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
         __syncthreads();
       }
       // 2. scan: one query per thread, its P locations at level l four at a time; every point
-      //    whose clipped corner rows meet the band is listed as (query offset << 16 | point)
-      for (int qq = 0; qq < qn; qq += nt) {
+      //    whose clipped corner rows meet the band is listed as (query offset << 16 | point). The
+      //    first pass runs on the waves that do not stage (whole waves: the appends use ballots).
+      const int sth = (q0 == q_lo && stage_w0 > 0) ? stage_w0 * 64 : nt;
+      for (int qq = 0; qq < qn && tid < sth; qq += sth) {
         const int qo = qq + tid;
         const bool qv = qo < qn;
         const float2* lq = at(vw.loc, __umul24(static_cast<uint32_t>(q0 + (qv ? qo : 0)), vw.qstride));
@@ -644,7 +650,19 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
     using OT = std::remove_pointer_t<decltype(dst)>;
     if (p.vec16) {
       const int pairs = owned_elems >> 1;
-      for (int i = tid; i < pairs; i += nt) {
+      constexpr int U = 4;  // pairs per thread in flight: the LDS reads of a pass issue together
+      int i = tid;
+      for (; i + (U - 1) * nt < pairs; i += U * nt) {
+        float f[U][2];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          f[u][0] = static_cast<float>(accp[2 * (i + u * nt)]);
+          f[u][1] = static_cast<float>(accp[2 * (i + u * nt) + 1]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) store_vec<OT, 2>(dst + 2 * (i + u * nt), f[u]);
+      }
+      for (; i < pairs; i += nt) {
         float f[2] = {static_cast<float>(accp[2 * i]), static_cast<float>(accp[2 * i + 1])};
         store_vec<OT, 2>(dst + 2 * i, f);
       }

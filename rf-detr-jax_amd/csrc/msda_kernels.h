@@ -334,22 +334,26 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // block is in flight at once; the wave waits for its own transfers before returning (the caller's
 // barrier then publishes them). Otherwise each thread issues a batch of loads before any store.
 // kWait = false leaves the 16-byte path's transfers outstanding (the caller waits before its barrier).
+// wave0, nw: only waves [wave0, wave0 + nw) copy (default: all of the workgroup's waves).
 template <typename VT, bool kWait = true>
-__device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, int count, bool vec16) {
+__device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, int count, bool vec16, int wave0 = 0, int nw = 0) {
   constexpr int U = 8;
-  const int nt = blockDim.x;
+  if (nw <= 0) nw = static_cast<int>(blockDim.x >> 6);  // waves [wave0, wave0 + nw) copy; others return
+  const int wave = static_cast<int>(threadIdx.x >> 6) - wave0;
+  if (wave < 0 || wave >= nw) return;
+  const int nt = nw * 64, t = static_cast<int>(threadIdx.x) - wave0 * 64;
   if (vec16) {
     const int n16 = static_cast<int>((static_cast<int64_t>(count) * sizeof(VT)) / 16);
     const uint4* s = reinterpret_cast<const uint4*>(src);
     uint4* d = reinterpret_cast<uint4*>(dst);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = nt >> 6;
+    const int lane = threadIdx.x & 63;
     const int nblk = n16 >> 6;  // whole 1 KB blocks
-    for (int blk = wave; blk < nblk; blk += nwaves)
+    for (int blk = wave; blk < nblk; blk += nw)
       __builtin_amdgcn_global_load_lds(s + blk * 64 + lane, (MSDA_LDS void*)(d + blk * 64), 16, 0, 0);
-    for (int i = (nblk << 6) + static_cast<int>(threadIdx.x); i < n16; i += nt) d[i] = s[i];
+    for (int i = (nblk << 6) + t; i < n16; i += nt) d[i] = s[i];
     if constexpr (kWait) wait_vmem();
   } else {
-    int i = threadIdx.x;
+    int i = t;
     for (; i + (U - 1) * nt < count; i += U * nt) {
       VT r[U];
 #pragma unroll
