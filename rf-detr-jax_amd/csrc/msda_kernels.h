@@ -288,22 +288,6 @@ __device__ __forceinline__ void load_any_rot(const void* base, int64_t off, bool
   }
 }
 
-// load_any_rot with a 32-bit element offset from a byte base (byte offset formed in 32 bits)
-template <typename VT, int VEC>
-__device__ __forceinline__ void load_any_rot32(const char* base, uint32_t off, bool is_bf16, int rot, float (&o)[VEC]) {
-  constexpr int N = rot_chunks<VT, VEC>();
-  constexpr int E = VEC / N;
-#pragma unroll
-  for (int k = 0; k < N; ++k) {
-    const uint32_t e = off + static_cast<uint32_t>(((k + rot) & (N - 1)) * E);
-    float t[E];
-    if (is_bf16) load_vec<bf16_t, E>(reinterpret_cast<const bf16_t*>(base + e * 2u), t);
-    else load_vec<float, E>(reinterpret_cast<const float*>(base + e * 4u), t);
-#pragma unroll
-    for (int i = 0; i < E; ++i) o[k * E + i] = t[i];
-  }
-}
-
 template <typename VT, int VEC>
 __device__ __forceinline__ void store_any_rot(void* base, int64_t off, bool is_bf16, int rot, const float (&a)[VEC]) {
   constexpr int N = rot_chunks<VT, VEC>();
@@ -366,10 +350,6 @@ __device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, 
 }
 
 
-__device__ __forceinline__ float group_sum(float v, int lpq) {
-  for (int o = 1; o < lpq; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
 
 // ---------------------------------------------------------------------------------------------
 // per-sample kernels: shared work-item decomposition and staging

@@ -30,13 +30,8 @@ constexpr int kGemmBK = 64;   // reduction slice staged in LDS per step
 constexpr int kGemmLd = kGemmBK + 4;  // LDS row stride: 16-byte rows; the 16 rows an operand read covers span all 64 banks once
 constexpr int kGemmPer = kGemmBM * kGemmBK / 256;  // elements of each operand tile a thread stages per step
 
-__device__ __forceinline__ float vp_load(const void* base, int64_t i, bool bf16) {
-  if (bf16) return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(base)[i]) << 16);
-  return static_cast<const float*>(base)[i];
-}
-
-// The same with the dtype fixed at compile time (no branch between a load and its use, so the
-// loads of a staging step are all in flight together).
+// Element i of a value-dtype tensor as f32, the dtype fixed at compile time (no branch between a
+// load and its use, so the loads of a staging step are all in flight together).
 template <typename VT>
 __device__ __forceinline__ float vp_ld(const void* base, int64_t i) {
   if constexpr (sizeof(VT) == 2) return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(base)[i]) << 16);
