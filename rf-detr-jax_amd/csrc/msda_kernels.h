@@ -349,8 +349,6 @@ __device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, 
   }
 }
 
-
-
 // ---------------------------------------------------------------------------------------------
 // per-sample kernels: shared work-item decomposition and staging
 
