@@ -650,19 +650,7 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
     using OT = std::remove_pointer_t<decltype(dst)>;
     if (p.vec16) {
       const int pairs = owned_elems >> 1;
-      constexpr int U = 4;  // pairs per thread in flight: the LDS reads of a pass issue together
-      int i = tid;
-      for (; i + (U - 1) * nt < pairs; i += U * nt) {
-        float f[U][2];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          f[u][0] = static_cast<float>(accp[2 * (i + u * nt)]);
-          f[u][1] = static_cast<float>(accp[2 * (i + u * nt) + 1]);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) store_vec<OT, 2>(dst + 2 * (i + u * nt), f[u]);
-      }
-      for (; i < pairs; i += nt) {
+      for (int i = tid; i < pairs; i += nt) {
         float f[2] = {static_cast<float>(accp[2 * i]), static_cast<float>(accp[2 * i + 1])};
         store_vec<OT, 2>(dst + 2 * i, f);
       }
