@@ -230,11 +230,14 @@ struct SamplePlan {
 // Each level whose slice still fits one head's LDS budget is staged (packed in level order); the
 // rest are gathered through L2. Head groups: a workgroup serves `hg` heads of one batch entry, so
 // the lanes of one query touch contiguous runs of its [H, ...] rows; hg is the largest power of
-// two <= the cap (4) that divides n_heads and keeps the group's slices within the LDS. A workgroup
-// that fills a CU's LDS gets 1024 threads (measured on MI355X for a 24x24x16 f32 level: four heads
-// in one 1024-thread workgroup per CU match or beat two heads in two 512-thread workgroups, and
-// halve the location / weight rows fetched per query). Then one resident wave of workgroups:
-// fewer, longer workgroups amortise the value staging.
+// two <= the cap that divides n_heads and keeps the group's slices within the LDS. The cap is 4
+// for slices of 1024 queries or more and 1 below: with few queries per slice, one head per
+// workgroup spreads the staging over more CUs and lets more workgroups share one (measured on
+// MI355X, forward: config 0 3.7 against 5.3 us, config 1 5.6 against 6.0, config 3 10.1 against
+// 10.5, config 4 15.3 against 16.7), while at 3900 queries four heads per workgroup fetch the
+// location and weight rows and write the output rows as whole runs (14.2 against 17.0 us). A
+// workgroup that fills a CU's LDS gets 1024 threads. Then one resident wave of workgroups: fewer,
+// longer workgroups amortise the value staging.
 int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* prefix, int shift, msda::SampleParams* p,
                 SamplePlan* out) {
   auto knob = [&](const char* name, int dflt) {
@@ -256,7 +259,7 @@ int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* pref
   }
   const int64_t head_bytes = align16(static_cast<int64_t>(head_lds) * vbytes);
   int hg = 1;
-  const int hg_cap = std::max(1, knob("_HEADS", 4));
+  const int hg_cap = std::max(1, knob("_HEADS", s.queries >= 1024 ? 4 : 1));
   const int group_budget = std::min(budget, knob("_GROUP_LDS", dev.lds_bytes));
   while (hg * 2 <= hg_cap && s.heads % (hg * 2) == 0 && (hg * 2) * head_bytes <= group_budget) hg *= 2;
   // With every level staged a head's region is its whole value slice; regions stay 16-byte aligned.

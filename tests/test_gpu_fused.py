@@ -80,8 +80,9 @@ CASES = {
     "two_levels_p4": dict(shapes=((80, 80), (20, 20)), heads=16, dim=16, points=4, queries=150),
     # four levels x 4 points, 8 heads x 32 (the larger variants' decoder)
     "four_levels": dict(shapes=((40, 40), (20, 20), (10, 10), (5, 5)), heads=8, dim=32, points=4, queries=120),
-    # the forward's staged head group fills the LDS (bf16: 4 heads x 32 x 40 x 16 x 2 B = 160 KB)
-    "lds_full": dict(shapes=((32, 40),), heads=16, dim=16, points=2, queries=200),
+    # the forward's staged head group fills the LDS (bf16: 4 heads x 32 x 40 x 16 x 2 B = 160 KB;
+    # four heads per workgroup from 1024 queries)
+    "lds_full": dict(shapes=((32, 40),), heads=16, dim=16, points=2, queries=1024),
 }
 
 

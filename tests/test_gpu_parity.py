@@ -266,11 +266,13 @@ def test_forward_paired_lanes(tune, pair):
     {"MSDA_FWD_MAX_VEC": "16"},
     {**_BAND, "MSDA_BWD_MAX_VEC": "16"},
     {"MSDA_FWD_HEADS": "2"},
+    {"MSDA_FWD_HEADS": "4"},
 ], ids=lambda v: ",".join(f"{k}={x}" for k, x in v.items()))
 @pytest.mark.parametrize("shapes", [((24, 24),), ((24, 24), (12, 12))], ids=["one_level", "two_levels"])
 def test_kernel_variants(tune, variant, shapes):
     """Other launch variants (one query at a time and 16-channel lanes in the forward, one lane per
-    query in the backward, two-head forward workgroups) against the float64 oracle."""
+    query in the backward, two- and four-head forward workgroups, which 700 queries do not get by
+    default) against the float64 oracle."""
     for k, v in variant.items():
         tune({k: v})
     value, loc, attn, grad = make_inputs(5, 2, 8, 16, 700, shapes, 2)
@@ -348,9 +350,11 @@ def test_location_and_weight_gradients_are_deterministic():
     [("bf16", 16, 16, (32, 40)), ("f32", 8, 32, (16, 20)), ("f32", 16, 16, (32, 40))],
     ids=["bf16_h16_d16_32x40", "f32_h8_d32_16x20", "f32_h16_d16_32x40"],
 )
-def test_backward_where_the_forward_head_group_fills_the_lds(dtype, heads, dim, shape):
+def test_backward_where_the_forward_head_group_fills_the_lds(tune, dtype, heads, dim, shape):
     """Shapes whose forward stages a group of heads into the whole 160 KB LDS (bf16: 4 heads x 32 x
-    40 x 16 x 2 B = 163,840 B): the backward plans its own LDS use and must run them too."""
+    40 x 16 x 2 B = 163,840 B; the forward groups four heads by default from 1024 queries, forced
+    here at 400): the backward plans its own LDS use and must run them too."""
+    tune({"MSDA_FWD_HEADS": 4})
     bf16 = dtype == "bf16"
     shapes = (shape,)
     value, loc, attn, grad = make_inputs(91, 2, heads, dim, 400, shapes, 2)
