@@ -436,8 +436,10 @@ int plan_band(const Shape& s, int vbytes, int ch, const DevInfo& dev, BandPlan* 
     }
   }
   bp->qblock = std::max(1, (s.queries + bp->nqb - 1) / bp->nqb);
+  // Enough threads for one pass over the block's queries, in whole groups of four waves (one per
+  // SIMD; config 3: 768 rather than 640 threads, 38.2 against 39.1 us).
   int threads = env_int("MSDA_BWD_THREADS", 0);
-  if (threads <= 0) threads = std::min(1024 / per_cu, std::max(256, ((std::min(s.queries, bp->qblock) * lps + 63) / 64) * 64));
+  if (threads <= 0) threads = std::min(1024 / per_cu, std::max(256, ((std::min(s.queries, bp->qblock) * lps + 255) / 256) * 256));
   threads = std::max(64, std::min(msda::kBandMaxThreads, (threads / 64) * 64));
   if (lps > threads) return fail(MSDA_ERR_UNSUPPORTED, "head_dim %d too large", s.dim);
   bp->threads = threads;
