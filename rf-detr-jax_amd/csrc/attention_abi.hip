@@ -52,8 +52,11 @@ msda::AttnParams at_params(int dtype, int batch, int groups, int heads, int len,
   return p;
 }
 
-// Row blocks per workgroup: 4, unless that leaves more waves without a block than 2 does (at
-// 300 rows, 10 blocks: 4 per workgroup idles 2 of 12 waves, 2 per workgroup none).
+// Row blocks per workgroup of the query-side backward: 4, unless that leaves more waves without a
+// block than 2 does (at 300 rows, 10 blocks: 4 per workgroup idles 2 of 12 waves, 2 per workgroup
+// none). The forward always takes 4: fewer workgroups per (slice, head) stage the keys and values
+// (measured at 300 rows: bf16 53.4 against 58.9 us, f32 131.5 against 133.3, despite the idle
+// waves; 8 blocks: 81.6 us); the key side takes 4 as well (below).
 int at_row_blocks(int len) {
   const int nb = (len + 31) / 32;
   const int idle4 = (4 - nb % 4) % 4, idle2 = nb % 2;
@@ -83,7 +86,7 @@ int fwd_rb(const msda::AttnParams& p, hipStream_t st) {
 
 template <typename VT, int D, bool MASK>
 int fwd_typed(const msda::AttnParams& p, hipStream_t st) {
-  return at_row_blocks(p.len) == 2 ? fwd_rb<VT, D, MASK, 2>(p, st) : fwd_rb<VT, D, MASK, 4>(p, st);
+  return fwd_rb<VT, D, MASK, 4>(p, st);
 }
 
 template <typename VT, int D, bool MASK, int RB>
@@ -116,7 +119,7 @@ int fwd_b_rb(const msda::AttnParams& p, hipStream_t st) {
 
 template <int D, bool MASK>
 int fwd_b(const msda::AttnParams& p, hipStream_t st) {
-  return at_row_blocks(p.len) == 2 ? fwd_b_rb<D, MASK, 2>(p, st) : fwd_b_rb<D, MASK, 4>(p, st);
+  return fwd_b_rb<D, MASK, 4>(p, st);
 }
 
 template <int D, bool MASK, int RB>
