@@ -52,11 +52,12 @@ msda::AttnParams at_params(int dtype, int batch, int groups, int heads, int len,
   return p;
 }
 
-// Row blocks per workgroup of the query-side backward: 4, unless that leaves more waves without a
-// block than 2 does (at 300 rows, 10 blocks: 4 per workgroup idles 2 of 12 waves, 2 per workgroup
-// none). The forward always takes 4: fewer workgroups per (slice, head) stage the keys and values
-// (measured at 300 rows: bf16 53.4 against 58.9 us, f32 131.5 against 133.3, despite the idle
-// waves; 8 blocks: 81.6 us); the key side takes 4 as well (below).
+// Row blocks per workgroup of the f32 query-side backward: 4, unless that leaves more waves without
+// a block than 2 does (at 300 rows, 10 blocks: 4 per workgroup idles 2 of 12 waves, 2 per
+// workgroup none). The other kernels always take 4: fewer workgroups per (slice, head) stage the
+// streamed side, which outweighs the idle waves (measured at 300 rows: forward bf16 53.4 against
+// 58.9 us, f32 131.5 against 133.3, 8 blocks 81.6; bf16 grad_q step 188.5 against 194.0 us; f32
+// grad_q was slower with 4).
 int at_row_blocks(int len) {
   const int nb = (len + 31) / 32;
   const int idle4 = (4 - nb % 4) % 4, idle2 = nb % 2;
@@ -140,7 +141,7 @@ int bwd_b_rb(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
 
 template <int D, bool MASK>
 int bwd_b(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
-  return at_row_blocks(p.len) == 2 ? bwd_b_rb<D, MASK, 2>(p, want_kv, st) : bwd_b_rb<D, MASK, 4>(p, want_kv, st);
+  return bwd_b_rb<D, MASK, 4>(p, want_kv, st);
 }
 
 int fwd_dispatch(const msda::AttnParams& p, int d, bool bf16, hipStream_t st) {

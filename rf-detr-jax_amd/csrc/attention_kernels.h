@@ -200,6 +200,19 @@ __device__ __forceinline__ void at_accum2(at_f16 (&acc0)[D / 32], at_f16 (&acc1)
       }
 }
 
+// at_accum2 for one block (one chain): acc += X^T w, X rows at Xs.
+template <int D>
+__device__ __forceinline__ void at_accum1(at_f16 (&acc)[D / 32], const float* Xs, const at_f16& w, int col, int grp) {
+  constexpr int LD = D + 8;
+#pragma unroll
+  for (int nd = 0; nd < D / 32; ++nd)
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[nd] = __builtin_amdgcn_mfma_f32_32x32x2f32(Xs[(8 * c4 + 4 * grp + j) * LD + 32 * nd + col], w[4 * c4 + j], acc[nd], 0, 0, 0);
+}
+
 // Reductions over the two halves of a wave (lanes l and l ^ 32, which hold the same query) by
 // v_permlane32_swap: both lanes get the same bits.
 __device__ __forceinline__ float at_max_halves(float x) {
@@ -435,21 +448,21 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? ((MASK || RB == 2) ? 2 : 3)
       vc.load(vp, p.st[kAtV][3], (j + 1) * kAtChunk, L);
     }
     if (qb >= nb) continue;
-    at_f16 s[2], dp[2];
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2)  // the chunk's two key blocks: S^T and dP^T = V dO^T, two chains each
-      at_scores_pair<D>(s[h2], dp[h2], Ks + 32 * h2 * LD, Vs + 32 * h2 * LD, qr, gr, col, grp);
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2)
+    for (int h2 = 0; h2 < 2; ++h2) {  // the chunk's two key blocks in turn (half the score registers)
+      at_f16 s, dp;
+      at_scores_pair<D>(s, dp, Ks + 32 * h2 * LD, Vs + 32 * h2 * LD, qr, gr, col, grp);  // S^T, dP^T = V dO^T
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int key = j * kAtChunk + 32 * h2 + 8 * (i >> 2) + 4 * grp + (i & 3);
-        float x = s[h2][i] * p.scale2;
+        float x = s[i] * p.scale2;
         if (key >= L) x = -INFINITY;
         else if (MASK && qv && p.mask[static_cast<int64_t>(qi) * L + key] != 0) x = kAtMaskScore;
-        s[h2][i] = at_exp2((x - m) - ll) * (dp[h2][i] - dsum);  // dS^T
+        s[i] = at_exp2((x - m) - ll) * (dp[i] - dsum);  // dS^T
       }
-    at_accum2<D>(dq0, dq1, Ks, Ks + 32 * LD, s[0], s[1], col, grp);  // dQ^T += K^T dS^T, one chain per key block
+      if (h2 == 0) at_accum1<D>(dq0, Ks, s, col, grp);  // dQ^T += K^T dS^T
+      else at_accum1<D>(dq1, Ks + 32 * LD, s, col, grp);
+    }
   }
   if (qv) {
     VT* gqp = static_cast<VT*>(p.gq) + w.sl.base(p, kAtGQ);
@@ -686,6 +699,23 @@ __device__ __forceinline__ void at_accum_tr(at_f16 (&acc0)[D / 32], at_f16 (&acc
     }
 }
 
+// at_accum_tr for one block (one chain): acc += X^T w for the 32-row block at row x of X.
+template <int D>
+__device__ __forceinline__ void at_accum_tr1(at_f16 (&acc)[D / 32], const uint16_t* X, int x, const at_f16& w, int lane) {
+  const int g = lane >> 4, r = lane & 15, grp = lane >> 5;
+  at_bf8 b[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) b[s] = at_bf8_regs(w, 8 * s);
+#pragma unroll
+  for (int nd = 0; nd < D / 32; ++nd)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int c = 32 * nd + 16 * (g & 1) + 4 * (r & 3), ro = 16 * s + 4 * grp + (r >> 2);
+      const at_bf8 a = at_bf8_of(at_read_tr(X + at_swo<D>(x + ro, c)), at_read_tr(X + at_swo<D>(x + ro + 8, c)));
+      acc[nd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[s], acc[nd], 0, 0, 0);
+    }
+}
+
 template <int D, bool MASK, int RB>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel(const AttnParams p) {
   constexpr int NT = 64 * RB, ND = D / 32;
@@ -799,20 +829,21 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
       vc.load(vp, p.st[kAtV][3], (j + 1) * kAtChunk, L);
     }
     if (qb >= nb) continue;
-    at_f16 s[2], dp[2];
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) at_scores_sw<D>(s[h2], dp[h2], Kr, 32 * h2, Vr, 32 * h2, qr, gr, col, grp);
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2)
+    for (int h2 = 0; h2 < 2; ++h2) {  // the chunk's two key blocks in turn (half the score registers)
+      at_f16 s, dp;
+      at_scores_sw<D>(s, dp, Kr, 32 * h2, Vr, 32 * h2, qr, gr, col, grp);  // S^T and dP^T = V dO^T
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int key = j * kAtChunk + 32 * h2 + 8 * (i >> 2) + 4 * grp + (i & 3);
-        float x = s[h2][i] * p.scale2;
+        float x = s[i] * p.scale2;
         if (key >= L) x = -INFINITY;
         else if (MASK && qv && p.mask[static_cast<int64_t>(qi) * L + key] != 0) x = kAtMaskScore;
-        s[h2][i] = at_exp2((x - m) - ll) * (dp[h2][i] - dsum);  // dS^T
+        s[i] = at_exp2((x - m) - ll) * (dp[i] - dsum);  // dS^T
       }
-    at_accum_tr<D>(dq0, dq1, Kr, 0, Kr, 32, s[0], s[1], lane);  // dQ^T += K^T dS^T
+      if (h2 == 0) at_accum_tr1<D>(dq0, Kr, 0, s, lane);  // dQ^T += K^T dS^T
+      else at_accum_tr1<D>(dq1, Kr, 32, s, lane);
+    }
   }
   if (qv) {
     bf16_t* gqp = static_cast<bf16_t*>(p.gq) + w.sl.base(p, kAtGQ);
