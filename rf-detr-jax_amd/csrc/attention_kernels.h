@@ -532,12 +532,12 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bw
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int i = 4 * c4 + jj;
-        // A lane past L holds the clamped last key: finite values in its own result column only,
-        // which is not stored. Rows past L have m = +inf: weight 0.
+        // A lane past L holds the clamped last key (its mask entry too): finite values in its own
+        // result column only, which is not stored. Rows past L have m = +inf: weight 0.
         if constexpr (MASK) {
           const int q = r0 + ql + jj;
           float x = s[i] * p.scale2;
-          if (q < L && p.mask[static_cast<int64_t>(q) * L + key] != 0) x = kAtMaskScore;
+          if (q < L && p.mask[static_cast<int64_t>(q) * L + min(key, L - 1)] != 0) x = kAtMaskScore;
           pw[i] = at_exp2((x - mq[jj]) - lq[jj]);
         } else {
           pw[i] = at_exp2(fmaf(s[i], p.scale2, -mq[jj]) - lq[jj]);
@@ -917,7 +917,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
           if constexpr (MASK) {
             const int q = r0 + ql + jj;
             float x = s[i] * p.scale2;
-            if (q < L && p.mask[static_cast<int64_t>(q) * L + key] != 0) x = kAtMaskScore;
+            if (q < L && p.mask[static_cast<int64_t>(q) * L + min(key, L - 1)] != 0) x = kAtMaskScore;
             pw[i] = at_exp2((x - mq[jj]) - lq[jj]);
           } else {
             pw[i] = at_exp2(fmaf(s[i], p.scale2, -mq[jj]) - lq[jj]);
@@ -939,6 +939,208 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
         if (p.gk != nullptr) at_st1<bf16_t>(gkp, key * p.st[kAtGK][3] + d, dk[nd][i] * p.scale);
         if (p.gv != nullptr) at_st1<bf16_t>(gvp, key * p.st[kAtGV][3] + d, dv[nd][i]);
       }
+  }
+}
+
+
+// Fused backward (bf16, D = 32, L <= 32 kAtFusedBlocks, no mask: a masked kernel would not fit three
+// waves per SIMD without spilling): a workgroup is one (slice, head). Waves 0 .. nb - 1 own one key
+// block each and form S, dP, P and dS of each (query block, key block) pair once: they accumulate
+// the block's dK and dV (as attn_bwd_kv_bf16_kernel) and write dS into LDS tiles [32 keys][32
+// queries]. Waves nb and nb + 1 stage the query-side rows (Q, dO, and rowsum(dO * O) from O) one
+// chunk ahead and form dQ of the previous chunk's two query blocks, one block each, as one MFMA
+// chain over all key blocks, dQ^T = K^T dS^T, from a swizzled copy of K and the dS tiles by
+// transposing reads, so no partial sums cross waves. The row tiles and the dS tiles are double
+// buffered by chunk parity: one barrier per chunk.
+constexpr int kAtFusedBlocks = 10;  // key-block waves; with the two dQ waves, 768 threads (three waves per SIMD)
+
+// Dynamic LDS bytes of the fused kernel for nb key blocks: the swizzled key rows [32 nb][32] and
+// two sets of dS tiles [nb][2][32][32] (bf16). The query-side row tiles and per-row m, log2 l and
+// rowsum are static arrays, so the compiler knows that the dS stores leave them alone.
+constexpr int at_fused_lds_bytes(int nb) { return nb * (2048 + 2 * 4096); }
+
+__device__ __forceinline__ float at_bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float at_bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+// Stores a 32 x 32 result block v * scale (lane l: row r0 + l % 32, channels 8 c + 4 (l / 32) + e in
+// register 4 c + e) as bf16 rows of dst (row stride rs elements), rows past L skipped. Through the
+// wave's LDS scratch sc (32 rows of 40 elements) each lane then writes two 16-byte row pieces, four
+// lanes to a row, when dst and rs allow it; 2-byte stores of the result layout otherwise (a store
+// instruction of the result layout writes 2 elements into each of 32 rows).
+__device__ __forceinline__ void at_store_block(bf16_t* dst, int64_t rs, int r0, int L, const at_f16& v, float scale, uint16_t* sc,
+                                               int lane) {
+  const int col = lane & 31, grp = lane >> 5;
+  if ((reinterpret_cast<uintptr_t>(dst) & 15) != 0 || (rs & 7) != 0) {
+    if (r0 + col < L) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) at_st1<bf16_t>(dst, at_row_off(r0 + col, rs) + 8 * (i >> 2) + 4 * grp + (i & 3), v[i] * scale);
+    }
+    return;
+  }
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const uint4 u = __builtin_bit_cast(uint4, at_bf8_regs(v * scale, 8 * s2));
+    *reinterpret_cast<uint2*>(&sc[40 * col + 16 * s2 + 4 * grp]) = uint2{u.x, u.y};
+    *reinterpret_cast<uint2*>(&sc[40 * col + 16 * s2 + 8 + 4 * grp]) = uint2{u.z, u.w};
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int slot = lane + 64 * k, row = slot >> 2, ch = 8 * (slot & 3);
+    const uint4 x = *reinterpret_cast<const uint4*>(&sc[40 * row + ch]);
+    if (r0 + row < L) *reinterpret_cast<uint4*>(dst + at_row_off(r0 + row, rs) + ch) = x;
+  }
+}
+
+__global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_bf16_kernel(const AttnParams p) {
+  constexpr int D = 32;
+  __shared__ __align__(16) uint16_t Qr[2][kAtChunk * D];  // swizzled [64][D] query and output-gradient rows
+  __shared__ __align__(16) uint16_t Gr[2][kAtChunk * D];
+  __shared__ __align__(16) float Ms[2][2 * kAtChunk];  // [64][2]: m, log2 l (rows past L: +inf)
+  __shared__ __align__(16) float Ds[2][kAtChunk];      // [64]: rowsum(dO * O)
+  __shared__ __align__(16) uint16_t Sq[2][32 * 40];    // the dQ waves' output scratch
+  extern __shared__ __align__(16) float at_lds[];
+  const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
+  uint16_t* Kt = reinterpret_cast<uint16_t*>(at_lds);  // swizzled [32 nb][D] key rows (0 past L)
+  uint16_t* St = Kt + 32 * nb * D;                      // dS tiles: 1024 elements each, set, block, query block
+  const AttnSlice sl(p, static_cast<int>(blockIdx.x));
+  const uint16_t* kp = static_cast<const uint16_t*>(p.k) + sl.base(p, kAtK);
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, grp = lane >> 5, col = lane & 31;
+  if (wave < nb) {  // key block kb = wave (uniform per wave)
+    const int kb = wave, key = kb * 32 + col;
+    uint2 kc[4];  // the block's rows of the key copy: row 8 u + lane / 8, channels 4 (lane % 8) .. + 3
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = kb * 32 + 8 * u + (lane >> 3);
+      kc[u] = row < L ? *reinterpret_cast<const uint2*>(kp + at_row_off(row, p.st[kAtK][3]) + 4 * (lane & 7)) : uint2{0u, 0u};
+    }
+    at_bf8 kr[2], vr[2];
+    at_row_bf8<D>(kr, kp, min(key, L - 1) * p.st[kAtK][3], grp);
+    at_row_bf8<D>(vr, static_cast<const uint16_t*>(p.v) + sl.base(p, kAtV), min(key, L - 1) * p.st[kAtV][3], grp);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) *reinterpret_cast<uint2*>(&Kt[at_swo<D>(kb * 32 + 8 * u + (lane >> 3), 4 * (lane & 7))]) = kc[u];
+    at_f16 dk[1] = {at_zero16()}, dv[1] = {at_zero16()};
+    for (int j = 0; j <= nchunks; ++j) {
+      __syncthreads();  // chunk j staged; the dS tiles of chunk j - 2 read
+      if (j == nchunks) break;
+      const int b = j & 1;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {  // the chunk's two query blocks
+        at_f16 s, dp;
+        at_scores_sw<D>(s, dp, Qr[b], 32 * h2, Gr[b], 32 * h2, kr, vr, col, grp);  // S = Q K^T, dP = dO V^T
+        at_f16 pw;
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+          const int ql = 32 * h2 + 8 * c4 + 4 * grp;
+          const at_f4 ms0 = *reinterpret_cast<const at_f4*>(&Ms[b][2 * ql]), ms1 = *reinterpret_cast<const at_f4*>(&Ms[b][2 * ql + 4]);
+          const at_f4 dd = *reinterpret_cast<const at_f4*>(&Ds[b][ql]);
+          const float mq[4] = {ms0[0], ms0[2], ms1[0], ms1[2]}, lq[4] = {ms0[1], ms0[3], ms1[1], ms1[3]};
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int i = 4 * c4 + jj;
+            // A lane past L holds the clamped last key: its weights are finite, and its rows of the
+            // key copy are 0, so it adds nothing to dQ. Rows past L have m = +inf: weight 0.
+            pw[i] = at_exp2(fmaf(s[i], p.scale2, -mq[jj]) - lq[jj]);
+            s[i] = pw[i] * (dp[i] - dd[jj]);  // dS
+          }
+        }
+        at_accum_tr<D>(dv, dk, Gr[b], 32 * h2, Qr[b], 32 * h2, pw, s, lane);  // dV^T += dO^T P, dK^T += Q^T dS
+        // dS^T tile: row = key (this lane's col), columns = the block's queries
+        uint16_t* Th = St + ((b * nb + kb) * 2 + h2) * 1024;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const uint4 u = __builtin_bit_cast(uint4, at_bf8_regs(s, 8 * s2));
+          *reinterpret_cast<uint2*>(&Th[at_swo<D>(col, 16 * s2 + 4 * grp)]) = uint2{u.x, u.y};
+          *reinterpret_cast<uint2*>(&Th[at_swo<D>(col, 16 * s2 + 8 + 4 * grp)]) = uint2{u.z, u.w};
+        }
+      }
+    }
+    // the dS tile set that the last dQ pass does not read is this wave's output scratch now
+    uint16_t* sc = St + (((nchunks & 1) * nb + kb) * 2) * 1024;
+    if (p.gk != nullptr) at_store_block(static_cast<bf16_t*>(p.gk) + sl.base(p, kAtGK), p.st[kAtGK][3], kb * 32, L, dk[0], p.scale, sc, lane);
+    if (p.gv != nullptr) at_store_block(static_cast<bf16_t*>(p.gv) + sl.base(p, kAtGV), p.st[kAtGV][3], kb * 32, L, dv[0], 1.0f, sc, lane);
+    return;
+  }
+  // The two dQ waves. Staging: thread tq holds row tq / 2 of the chunk, channels 16 (tq % 2) .. + 15.
+  const int tq = t - 64 * nb, h2q = tq >> 6;  // h2q: the query block of each chunk this wave forms dQ for
+  const uint16_t* qp = static_cast<const uint16_t*>(p.q) + sl.base(p, kAtQ);
+  const uint16_t* gop = static_cast<const uint16_t*>(p.go) + sl.base(p, kAtGO);
+  const uint16_t* opp = static_cast<const uint16_t*>(p.o) + sl.base(p, kAtO);
+  float* stats = p.stats + static_cast<int64_t>(blockIdx.x) * L * 4;
+  const int srow = tq >> 1, shalf = tq & 1;
+  uint4 qv[2], gv[2], ov[2];
+  at_f4 sq = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto prefetch = [&](int r0) {
+    const int r = min(r0 + srow, L - 1);
+    auto ld16 = [](const uint16_t* e) {  // rows are 8-byte aligned
+      const uint2 lo = *reinterpret_cast<const uint2*>(e), hi = *reinterpret_cast<const uint2*>(e + 4);
+      return uint4{lo.x, lo.y, hi.x, hi.y};
+    };
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 16 * shalf + 8 * h;
+      qv[h] = ld16(qp + at_row_off(r, p.st[kAtQ][3]) + c);
+      gv[h] = ld16(gop + at_row_off(r, p.st[kAtGO][3]) + c);
+      ov[h] = ld16(opp + at_row_off(r, p.st[kAtO][3]) + c);
+    }
+    if (shalf == 0) sq = *reinterpret_cast<const at_f4*>(&stats[4 * r]);
+  };
+  auto stage = [&](int r0, int b) {
+    const bool in = r0 + srow < L;
+    float dd = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 16 * shalf + 8 * h;  // a 16-byte chunk of the swizzled row
+      *reinterpret_cast<uint4*>(&Qr[b][srow * D + 8 * ((c >> 3) ^ at_sw<D>(srow))]) = in ? qv[h] : uint4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<uint4*>(&Gr[b][srow * D + 8 * ((c >> 3) ^ at_sw<D>(srow))]) = in ? gv[h] : uint4{0u, 0u, 0u, 0u};
+      const uint32_t g4[4] = {gv[h].x, gv[h].y, gv[h].z, gv[h].w}, o4[4] = {ov[h].x, ov[h].y, ov[h].z, ov[h].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dd += at_bf16_lo(g4[e]) * at_bf16_lo(o4[e]) + at_bf16_hi(g4[e]) * at_bf16_hi(o4[e]);
+    }
+    // the row's other half: the neighbouring lane (DPP quad_perm [1, 0, 3, 2])
+    dd += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(dd), 0xB1, 0xF, 0xF, false));
+    if (shalf == 0) {
+      Ms[b][2 * srow] = in ? sq[0] : INFINITY;
+      Ms[b][2 * srow + 1] = in ? sq[1] : 0.0f;
+      Ds[b][srow] = in ? dd : 0.0f;
+      if (in) stats[4 * (r0 + srow) + 2] = dd;
+    }
+  };
+  prefetch(0);
+  stage(0, 0);
+  if (nchunks > 1) prefetch(kAtChunk);
+  bf16_t* gqp = static_cast<bf16_t*>(p.gq) + sl.base(p, kAtGQ);
+  const int g16 = lane >> 4, r = lane & 15;
+  const int tc = 16 * (g16 & 1) + 4 * (r & 3), tro = 4 * grp + (r >> 2);  // transposing-read lane offsets
+  for (int j = 0; j <= nchunks; ++j) {
+    __syncthreads();  // chunk j staged; the dS tiles of chunk j - 1 written
+    if (j + 1 < nchunks) {
+      stage((j + 1) * kAtChunk, (j + 1) & 1);
+      if (j + 2 < nchunks) prefetch((j + 2) * kAtChunk);
+    }
+    if (j == 0) continue;
+    const int jp = j - 1, bp = jp & 1;
+    // dQ^T = sum over key blocks of K^T dS^T: two chains (the two 16-key halves of each block),
+    // the next block's operands read while the current block's products run
+    at_f16 acc0 = at_zero16(), acc1 = at_zero16();
+    at_bf8 ka[2], sb[2];
+    auto operands = [&](int kb2) {
+      const uint16_t* Th = St + ((bp * nb + kb2) * 2 + h2q) * 1024;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int ro = 16 * s2 + tro;
+        ka[s2] = at_bf8_of(at_read_tr(Kt + at_swo<D>(32 * kb2 + ro, tc)), at_read_tr(Kt + at_swo<D>(32 * kb2 + ro + 8, tc)));
+        sb[s2] = at_bf8_of(at_read_tr(Th + at_swo<D>(ro, tc)), at_read_tr(Th + at_swo<D>(ro + 8, tc)));
+      }
+    };
+    operands(0);
+    for (int kb2 = 0; kb2 < nb; ++kb2) {
+      const at_bf8 a0 = ka[0], a1 = ka[1], b0 = sb[0], b1 = sb[1];
+      if (kb2 + 1 < nb) operands(kb2 + 1);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc1, 0, 0, 0);
+    }
+    // result column: the lane's query; rows: channels
+    at_store_block(gqp, p.st[kAtGQ][3], jp * kAtChunk + 32 * h2q, L, acc0 + acc1, p.scale, Sq[h2q], lane);
   }
 }
 

@@ -119,19 +119,25 @@ def test_reference_known_answers():
     assert_close(out, np.broadcast_to(want, out.shape), 1e-5, "mean")
 
 
-def test_grouped_rows_layout_against_split_groups():
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+def test_grouped_rows_layout_against_split_groups(bf16):
     """[B, G * P, C] rows with q and k read in place from a fused [B, Q, 2C] projection (row stride
     2C): the same as splitting the groups onto the batch, attending per head and merging back."""
     batch, groups, per, heads, d = 2, 13, 30, 8, 32
     c = heads * d
+    _note(f"grouped rows bf16={bf16}")
     rng = np.random.default_rng(42)
     qk = rng.standard_normal((batch, groups * per, 2 * c)).astype(np.float32)
     v = rng.standard_normal((batch, groups * per, c)).astype(np.float32)
     g = rng.standard_normal((batch, groups * per, c)).astype(np.float32)
-    tqk = _t(qk).requires_grad_(True)
-    tv = _t(v).requires_grad_(True)
+    if bf16:
+        qk, v, g = (bf16_round(x) for x in (qk, v, g))
+    dt = torch.bfloat16 if bf16 else None
+    tqk = _t(qk, dt).requires_grad_(True)
+    tv = _t(v, dt).requires_grad_(True)
     out = grouped_attention(tqk[..., :c], tqk[..., c:], tv, heads, groups)
-    out.backward(_t(g))
+    out.backward(_t(g, dt))
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
 
     def heads_of(x):  # [G B, P, C] -> [G B, H, P, D]
         return x.reshape(x.shape[0], per, heads, d).transpose(0, 2, 1, 3)
@@ -139,12 +145,12 @@ def test_grouped_rows_layout_against_split_groups():
     qs, ks, vs = (heads_of(AT.split_groups(x, per)) for x in (qk[..., :c], qk[..., c:], v))
     gs = heads_of(AT.split_groups(g, per))
     want = AT.merge_groups(AT.sdpa(qs, ks, vs).transpose(0, 2, 1, 3).reshape(groups * batch, per, c), batch)
-    assert_close(_np(out), want, 1e-5, "out")
+    assert_close(_np(out), want, tf, "out")
     dq, dk, dv = (AT.merge_groups(x.transpose(0, 2, 1, 3).reshape(groups * batch, per, c), batch) for x in AT.sdpa_vjp(qs, ks, vs, gs))
     gqk = _np(tqk.grad)
-    assert_close(gqk[..., :c], dq, 1e-4, "grad_q")
-    assert_close(gqk[..., c:], dk, 1e-4, "grad_k")
-    assert_close(_np(tv.grad), dv, 1e-4, "grad_v")
+    assert_close(gqk[..., :c], dq, tg, "grad_q")
+    assert_close(gqk[..., c:], dk, tg, "grad_k")
+    assert_close(_np(tv.grad), dv, tg, "grad_v")
 
 
 def _torch_reference(m, tgt, pos, groups, heads, grad):
@@ -217,3 +223,99 @@ def test_single_gradient_requests():
                 assert_close(_np(got[j]), want[j], 1e-4, f"gradient {j}")
             else:
                 assert got[j] is None
+
+
+FUSED_LENGTHS = [1, 17, 32, 33, 64, 65, 129, 200, 256, 257, 300, 319, 320, 321]
+
+
+@pytest.mark.parametrize("length", FUSED_LENGTHS)
+def test_fused_backward_against_two_kernel_path(length, tune):
+    """bf16 at head_dim 32 without a mask, up to 320 rows: one fused backward kernel (one
+    workgroup per (slice, head): a wave per key block, two waves that form dQ from the dS tiles)
+    against the oracle, and against the two-kernel path (MSDA_ATTN_FUSED=0) on the same forward;
+    both write rowsum(dO * O) into entry 2 of the statistics. 321 rows take the two kernels either
+    way."""
+    from rfdetr_jax_amd.attention import _Layout, attention_backward, attention_forward
+
+    b, h, d = 2, 3, 32
+    _note(f"fused backward L={length}")
+    rng = np.random.default_rng(45 + length)
+    q, k, v, g = (bf16_round(rng.standard_normal((b, h, length, d)).astype(np.float32)) for _ in range(4))
+    lay = _Layout(b, 1, h, length, d)
+    tq, tk, tv, tg = (_t(x, torch.bfloat16) for x in (q, k, v, g))
+    out, stats = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
+    fused = attention_backward(tq, tk, tv, out, stats, tg, lay, lay.strides_bhld)
+    torch.cuda.synchronize()
+    dsum_fused = _np(stats).reshape(b * h * length, 4)[:, 2].copy()
+    tune({"MSDA_ATTN_FUSED": 0})
+    split = attention_backward(tq, tk, tv, out, stats, tg, lay, lay.strides_bhld)
+    torch.cuda.synchronize()
+    dsum_split = _np(stats).reshape(b * h * length, 4)[:, 2]
+    want_dsum = (g.astype(np.float64) * _np(out).astype(np.float64)).sum(-1).reshape(-1)
+    assert_close(dsum_fused, want_dsum, 1e-5, "rowsum(dO * O), fused")
+    assert_close(dsum_split, want_dsum, 1e-5, "rowsum(dO * O), two kernels")
+    want = AT.sdpa_vjp(q, k, v, g)
+    for name, a, c, w in zip("qkv", fused, split, want):
+        assert_close(_np(a), w, 2e-2, f"grad_{name} fused")
+        assert_close(_np(c), w, 2e-2, f"grad_{name} two kernels")
+        assert_close(_np(a), _np(c).astype(np.float64), 1e-2, f"grad_{name} fused against two kernels")
+
+
+@pytest.mark.parametrize("needs", [(True, True, False), (True, False, True), (True, False, False), (False, True, True)],
+                         ids=["qk", "qv", "q", "kv"])
+def test_bf16_gradient_subsets(needs):
+    """bf16 at head_dim 32: grad_q with one of grad_k / grad_v (the fused kernel, skipping the
+    missing store), grad_q alone and grad_k with grad_v (the two-kernel path's halves)."""
+    from rfdetr_jax_amd.attention import _Layout, attention_backward, attention_forward
+
+    _note(f"bf16 gradient subset {needs}")
+    rng = np.random.default_rng(46)
+    q, k, v, g = (bf16_round(rng.standard_normal((2, 2, 150, 32)).astype(np.float32)) for _ in range(4))
+    lay = _Layout(2, 1, 2, 150, 32)
+    tq, tk, tv = (_t(x, torch.bfloat16) for x in (q, k, v))
+    out, stats = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
+    got = attention_backward(tq, tk, tv, out, stats, _t(g, torch.bfloat16), lay, lay.strides_bhld, None, needs)
+    torch.cuda.synchronize()
+    want = AT.sdpa_vjp(q, k, v, g)
+    for j in range(3):
+        if needs[j]:
+            assert_close(_np(got[j]), want[j], 2e-2, f"gradient {j}")
+        else:
+            assert got[j] is None
+
+
+def test_fused_backward_unaligned_gradients():
+    """The fused kernel's gradient stores: 16-byte row pieces through an LDS transpose when the
+    output rows allow it, element stores otherwise. Gradients here start 8 bytes into a buffer
+    and have a row stride of 36 elements (rows 8-byte aligned only)."""
+    import ctypes
+
+    from rfdetr_jax_amd import _native
+    from rfdetr_jax_amd.attention import _DTYPES, _Layout, _ptr, _stream, attention_forward
+
+    b, h, length, d, rs = 2, 3, 300, 32, 36
+    _note("fused backward, unaligned gradient rows")
+    rng = np.random.default_rng(47)
+    q, k, v, g = (bf16_round(rng.standard_normal((b, h, length, d)).astype(np.float32)) for _ in range(4))
+    lay = _Layout(b, 1, h, length, d)
+    tq, tk, tv, tg = (_t(x, torch.bfloat16) for x in (q, k, v, g))
+    out, stats = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
+    n = b * h * length * rs
+    bufs = [torch.zeros(n + 4, dtype=torch.bfloat16, device=_dev()) for _ in range(3)]
+    grads = [x[4:].view(b, h, length, rs)[..., :d] for x in bufs]
+    s = []
+    for t in (tq, tk, tv, out, tg):
+        s += lay.strides_bhld(t)
+    for t in grads:
+        s += [h * length * rs, 0, length * rs, rs]
+    strides = (ctypes.c_int64 * 32)(*s)
+    rc = _native.lib().msda_attention_bwd(_ptr(tq), _ptr(tk), _ptr(tv), _ptr(out), _ptr(stats), _ptr(tg), _DTYPES[torch.bfloat16],
+                                          _ptr(grads[0]), _ptr(grads[1]), _ptr(grads[2]), b, 1, h, length, d, strides, None,
+                                          _stream(_dev()))
+    _native.check(rc)
+    torch.cuda.synchronize()
+    for name, got, want in zip("qkv", grads, AT.sdpa_vjp(q, k, v, g)):
+        assert_close(_np(got), want, 2e-2, f"grad_{name}")
+    for x in bufs:  # nothing written outside the views
+        pad = _np(x[4:].view(b, h, length, rs)[..., d:])
+        assert not pad.any() and not _np(x[:4]).any()
