@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 
@@ -14,10 +15,16 @@ namespace {
 using msda_host::aligned_to;
 using msda_host::fail;
 
+// f32 kernels: two row tiles [64][D + 8] and three floats per row (more than the four waves' output
+// scratch, which reuses them after the last chunk)
 int lds_bytes(int d) { return (d == 32 ? msda::at_lds_floats<32>() : msda::at_lds_floats<64>()) * 4; }
+static_assert(msda::at_lds_floats<32>() * 4 >= 4 * msda::at_scratch_bytes<float>(), "f32 attention LDS holds the output scratch");
 
-// bf16 kernels: two swizzled row tiles [64][D] of bf16, and (key side) three floats per row
-int lds_bf16(int d, bool rows_f32) { return 2 * msda::kAtChunk * d * 2 + (rows_f32 ? 3 * msda::kAtChunk * 4 : 0); }
+// bf16 kernels: two swizzled row tiles [64][D] of bf16, and (key side) three floats per row; at
+// least the four waves' output scratch, which reuses them after the last chunk
+int lds_bf16(int d, bool rows_f32) {
+  return std::max(2 * msda::kAtChunk * d * 2 + (rows_f32 ? 3 * msda::kAtChunk * 4 : 0), 4 * msda::at_scratch_bytes<msda::bf16_t>());
+}
 
 int at_validate(int dtype, int batch, int groups, int heads, int len, int head_dim, const int64_t* strides, int ntensors) {
   if (dtype != MSDA_DTYPE_F32 && dtype != MSDA_DTYPE_BF16) return fail(MSDA_ERR_UNSUPPORTED, "attention: unsupported dtype code %d", dtype);

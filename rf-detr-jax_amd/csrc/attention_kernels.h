@@ -318,6 +318,65 @@ __device__ __forceinline__ float at_softmax_chunk(at_f16& s0, at_f16& s1, int k0
   return alpha;
 }
 
+typedef __bf16 at_bf8 __attribute__((ext_vector_type(8)));
+typedef float at_f8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ at_bf8 at_bf8_of(uint2 lo, uint2 hi) { return __builtin_bit_cast(at_bf8, uint4{lo.x, lo.y, hi.x, hi.y}); }
+
+// registers i0 .. i0 + 7 of a result block, rounded to bf16 (v_cvt_pk_bf16_f32, nearest even)
+__device__ __forceinline__ at_bf8 at_bf8_regs(const at_f16& v, int i0) {
+  const at_f8 f = {v[i0], v[i0 + 1], v[i0 + 2], v[i0 + 3], v[i0 + 4], v[i0 + 5], v[i0 + 6], v[i0 + 7]};
+  return __builtin_convertvector(f, at_bf8);
+}
+
+// Stores a 32 x 32 result block v * scale (lane l: row r0 + l % 32, channels 8 c + 4 (l / 32) + e in
+// register 4 c + e) as rows of dst (row stride rs elements), rows past L skipped, by the whole wave.
+// In the result layout one store instruction writes 1 or 2 elements into each of 32 rows; through
+// the wave's LDS scratch sc (at_scratch_bytes: 32 rows of 40 bf16 or 36 floats) each lane instead
+// writes 16-byte row pieces (whole rows per instruction) when dst and rs are 16-byte aligned, and
+// the result layout is stored element by element otherwise.
+template <typename VT>
+constexpr int at_scratch_bytes() { return sizeof(VT) == 2 ? 32 * 40 * 2 : 32 * 36 * 4; }  // per wave
+
+template <typename VT>
+__device__ __forceinline__ void at_store_block(VT* dst, int64_t rs, int r0, int L, const at_f16& v, float scale, void* sc, int lane) {
+  const int col = lane & 31, grp = lane >> 5;
+  constexpr int PER16 = 16 / sizeof(VT);  // elements per 16-byte piece
+  if ((reinterpret_cast<uintptr_t>(dst) & 15) != 0 || (rs % PER16) != 0) {
+    if (r0 + col < L) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) at_st1<VT>(dst, at_row_off(r0 + col, rs) + 8 * (i >> 2) + 4 * grp + (i & 3), v[i] * scale);
+    }
+    return;
+  }
+  if constexpr (sizeof(VT) == 2) {
+    uint16_t* t = static_cast<uint16_t*>(sc);  // [32][40]
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const uint4 u = __builtin_bit_cast(uint4, at_bf8_regs(v * scale, 8 * s2));
+      *reinterpret_cast<uint2*>(&t[40 * col + 16 * s2 + 4 * grp]) = uint2{u.x, u.y};
+      *reinterpret_cast<uint2*>(&t[40 * col + 16 * s2 + 8 + 4 * grp]) = uint2{u.z, u.w};
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int slot = lane + 64 * k, row = slot >> 2, ch = 8 * (slot & 3);
+      const uint4 x = *reinterpret_cast<const uint4*>(&t[40 * row + ch]);
+      if (r0 + row < L) *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(dst) + at_row_off(r0 + row, rs) + ch) = x;
+    }
+  } else {
+    float* t = static_cast<float*>(sc);  // [32][36]
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *reinterpret_cast<at_f4*>(&t[36 * col + 8 * c + 4 * grp]) = at_f4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]} * scale;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int slot = lane + 64 * k, row = slot >> 3, ch = 4 * (slot & 7);
+      const at_f4 x = *reinterpret_cast<const at_f4*>(&t[36 * row + ch]);
+      if (r0 + row < L) *reinterpret_cast<at_f4*>(reinterpret_cast<float*>(dst) + at_row_off(r0 + row, rs) + ch) = x;
+    }
+  }
+}
+
 // The workgroup's (slice, head) and row chunk: blockIdx.x = (z * H + h) * chunks + rc.
 struct AttnWork {
   int zh, rc;
@@ -377,15 +436,13 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : (MASK ? 1 
     }
     at_accum2<D>(o0, o1, Vs, Vs + 32 * LD, s0, s1, col, grp);  // O^T += V^T P^T, one chain per key block
   }
-  if (qv) {
+  __syncthreads();  // the chunk tiles hold the waves' output scratch from here
+  if (qb < nb) {
     VT* op = static_cast<VT*>(p.out) + w.sl.base(p, kAtO);
     const float inv = 1.0f / l;
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        at_st1<VT>(op, qi * p.st[kAtO][3] + 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3), (o0[nd][i] + o1[nd][i]) * inv);
-    if (grp == 0) {
+    for (int nd = 0; nd < ND; ++nd) at_store_block<VT>(op + 32 * nd, p.st[kAtO][3], qb * 32, L, o0[nd] + o1[nd], inv, at_lds + (threadIdx.x >> 6) * (at_scratch_bytes<VT>() / 4), lane);
+    if (qv && grp == 0) {
       float* stats = p.stats + (static_cast<int64_t>(w.zh) * L + qi) * 4;
       stats[0] = m;
       stats[1] = log2f(l);
@@ -464,13 +521,11 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? ((MASK || RB == 2) ? 2 : 3)
       else at_accum1<D>(dq1, Ks + 32 * LD, s, col, grp);
     }
   }
-  if (qv) {
+  __syncthreads();  // the chunk tiles hold the waves' output scratch from here
+  if (qb < nb) {
     VT* gqp = static_cast<VT*>(p.gq) + w.sl.base(p, kAtGQ);
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        at_st1<VT>(gqp, qi * p.st[kAtGQ][3] + 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3), (dq0[nd][i] + dq1[nd][i]) * p.scale);
+    for (int nd = 0; nd < ND; ++nd) at_store_block<VT>(gqp + 32 * nd, p.st[kAtGQ][3], qb * 32, L, dq0[nd] + dq1[nd], p.scale, at_lds + (threadIdx.x >> 6) * (at_scratch_bytes<VT>() / 4), lane);
   }
 }
 
@@ -564,17 +619,15 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bw
     block(r0, 0);
     block(r0, 1);
   }
-  if (kv) {
+  __syncthreads();  // the chunk tiles hold the waves' output scratch from here
+  if (kb < nb) {
     VT* gkp = static_cast<VT*>(p.gk) + w.sl.base(p, kAtGK);
     VT* gvp = static_cast<VT*>(p.gv) + w.sl.base(p, kAtGV);
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3);
-        if (p.gk != nullptr) at_st1<VT>(gkp, key * p.st[kAtGK][3] + d, dk[nd][i] * p.scale);
-        if (p.gv != nullptr) at_st1<VT>(gvp, key * p.st[kAtGV][3] + d, dv[nd][i]);
-      }
+    for (int nd = 0; nd < ND; ++nd) {
+      if (p.gk != nullptr) at_store_block<VT>(gkp + 32 * nd, p.st[kAtGK][3], kb * 32, L, dk[nd], p.scale, at_lds + (threadIdx.x >> 6) * (at_scratch_bytes<VT>() / 4), lane);
+      if (p.gv != nullptr) at_store_block<VT>(gvp + 32 * nd, p.st[kAtGV][3], kb * 32, L, dv[nd], 1.0f, at_lds + (threadIdx.x >> 6) * (at_scratch_bytes<VT>() / 4), lane);
+    }
   }
 }
 
@@ -588,17 +641,6 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bw
 // B gives the sum; the result layout is that of the f32 32 x 32 products. Probabilities and dS
 // are rounded to bf16 (v_cvt_pk_bf16_f32, nearest even) for the products they enter, as the
 // reference rounds the softmax weights to the input dtype (layers.py:96-98); sums are f32.
-
-typedef __bf16 at_bf8 __attribute__((ext_vector_type(8)));
-typedef float at_f8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ at_bf8 at_bf8_of(uint2 lo, uint2 hi) { return __builtin_bit_cast(at_bf8, uint4{lo.x, lo.y, hi.x, hi.y}); }
-
-// registers i0 .. i0 + 7 of a result block, rounded to bf16
-__device__ __forceinline__ at_bf8 at_bf8_regs(const at_f16& v, int i0) {
-  const at_f8 f = {v[i0], v[i0 + 1], v[i0 + 2], v[i0 + 3], v[i0 + 4], v[i0 + 5], v[i0 + 6], v[i0 + 7]};
-  return __builtin_convertvector(f, at_bf8);
-}
 
 // channels 16 s + 8 (l / 32) .. + 7 of one row, s < D / 16 (two 8-byte loads: rows are 8-byte aligned)
 template <int D>
@@ -760,15 +802,13 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
     }
     at_accum_tr<D>(o0, o1, Vr, 0, Vr, 32, s0, s1, lane);  // O^T += V^T P^T
   }
-  if (qv) {
+  __syncthreads();  // the chunk tiles hold the waves' output scratch from here
+  if (qb < nb) {
     bf16_t* op = static_cast<bf16_t*>(p.out) + w.sl.base(p, kAtO);
     const float inv = 1.0f / l;
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        at_st1<bf16_t>(op, qi * p.st[kAtO][3] + 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3), (o0[nd][i] + o1[nd][i]) * inv);
-    if (grp == 0) {
+    for (int nd = 0; nd < ND; ++nd) at_store_block<bf16_t>(op + 32 * nd, p.st[kAtO][3], qb * 32, L, o0[nd] + o1[nd], inv, at_lds + (threadIdx.x >> 6) * (at_scratch_bytes<bf16_t>() / 4), lane);
+    if (qv && grp == 0) {
       float* stats = p.stats + (static_cast<int64_t>(w.zh) * L + qi) * 4;
       stats[0] = m;
       stats[1] = log2f(l);
@@ -845,13 +885,11 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
       else at_accum_tr1<D>(dq1, Kr, 32, s, lane);
     }
   }
-  if (qv) {
+  __syncthreads();  // the chunk tiles hold the waves' output scratch from here
+  if (qb < nb) {
     bf16_t* gqp = static_cast<bf16_t*>(p.gq) + w.sl.base(p, kAtGQ);
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        at_st1<bf16_t>(gqp, qi * p.st[kAtGQ][3] + 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3), (dq0[nd][i] + dq1[nd][i]) * p.scale);
+    for (int nd = 0; nd < ND; ++nd) at_store_block<bf16_t>(gqp + 32 * nd, p.st[kAtGQ][3], qb * 32, L, dq0[nd] + dq1[nd], p.scale, at_lds + (threadIdx.x >> 6) * (at_scratch_bytes<bf16_t>() / 4), lane);
   }
 }
 
@@ -928,17 +966,15 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
       at_accum_tr<D>(dv, dk, Gr, 32 * h2, Qr, 32 * h2, pw, s, lane);  // dV^T += dO^T P, dK^T += Q^T dS
     }
   }
-  if (kv) {
+  __syncthreads();  // the chunk tiles hold the waves' output scratch from here
+  if (kb < nb) {
     bf16_t* gkp = static_cast<bf16_t*>(p.gk) + w.sl.base(p, kAtGK);
     bf16_t* gvp = static_cast<bf16_t*>(p.gv) + w.sl.base(p, kAtGV);
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = 32 * nd + 8 * (i >> 2) + 4 * grp + (i & 3);
-        if (p.gk != nullptr) at_st1<bf16_t>(gkp, key * p.st[kAtGK][3] + d, dk[nd][i] * p.scale);
-        if (p.gv != nullptr) at_st1<bf16_t>(gvp, key * p.st[kAtGV][3] + d, dv[nd][i]);
-      }
+    for (int nd = 0; nd < ND; ++nd) {
+      if (p.gk != nullptr) at_store_block<bf16_t>(gkp + 32 * nd, p.st[kAtGK][3], kb * 32, L, dk[nd], p.scale, at_lds + (threadIdx.x >> 6) * (at_scratch_bytes<bf16_t>() / 4), lane);
+      if (p.gv != nullptr) at_store_block<bf16_t>(gvp + 32 * nd, p.st[kAtGV][3], kb * 32, L, dv[nd], 1.0f, at_lds + (threadIdx.x >> 6) * (at_scratch_bytes<bf16_t>() / 4), lane);
+    }
   }
 }
 
@@ -961,35 +997,6 @@ constexpr int at_fused_lds_bytes(int nb) { return nb * (2048 + 2 * 4096); }
 
 __device__ __forceinline__ float at_bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float at_bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
-
-// Stores a 32 x 32 result block v * scale (lane l: row r0 + l % 32, channels 8 c + 4 (l / 32) + e in
-// register 4 c + e) as bf16 rows of dst (row stride rs elements), rows past L skipped. Through the
-// wave's LDS scratch sc (32 rows of 40 elements) each lane then writes two 16-byte row pieces, four
-// lanes to a row, when dst and rs allow it; 2-byte stores of the result layout otherwise (a store
-// instruction of the result layout writes 2 elements into each of 32 rows).
-__device__ __forceinline__ void at_store_block(bf16_t* dst, int64_t rs, int r0, int L, const at_f16& v, float scale, uint16_t* sc,
-                                               int lane) {
-  const int col = lane & 31, grp = lane >> 5;
-  if ((reinterpret_cast<uintptr_t>(dst) & 15) != 0 || (rs & 7) != 0) {
-    if (r0 + col < L) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) at_st1<bf16_t>(dst, at_row_off(r0 + col, rs) + 8 * (i >> 2) + 4 * grp + (i & 3), v[i] * scale);
-    }
-    return;
-  }
-#pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2) {
-    const uint4 u = __builtin_bit_cast(uint4, at_bf8_regs(v * scale, 8 * s2));
-    *reinterpret_cast<uint2*>(&sc[40 * col + 16 * s2 + 4 * grp]) = uint2{u.x, u.y};
-    *reinterpret_cast<uint2*>(&sc[40 * col + 16 * s2 + 8 + 4 * grp]) = uint2{u.z, u.w};
-  }
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int slot = lane + 64 * k, row = slot >> 2, ch = 8 * (slot & 3);
-    const uint4 x = *reinterpret_cast<const uint4*>(&sc[40 * row + ch]);
-    if (r0 + row < L) *reinterpret_cast<uint4*>(dst + at_row_off(r0 + row, rs) + ch) = x;
-  }
-}
 
 __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_bf16_kernel(const AttnParams p) {
   constexpr int D = 32;

@@ -284,38 +284,64 @@ def test_bf16_gradient_subsets(needs):
             assert got[j] is None
 
 
-def test_fused_backward_unaligned_gradients():
-    """The fused kernel's gradient stores: 16-byte row pieces through an LDS transpose when the
-    output rows allow it, element stores otherwise. Gradients here start 8 bytes into a buffer
-    and have a row stride of 36 elements (rows 8-byte aligned only)."""
+@pytest.mark.parametrize("path", ["bf16", "bf16-two-kernels", "f32"])
+def test_unaligned_output_rows(path, tune):
+    """Every kernel stores its results as 16-byte row pieces through an LDS transpose when the
+    output rows allow it, element by element otherwise. Here the forward output and the gradients
+    start 8 bytes (bf16) or 4 bytes (f32) into a buffer, with a row stride of 36 elements; the
+    elements between the rows stay untouched."""
     import ctypes
 
     from rfdetr_jax_amd import _native
     from rfdetr_jax_amd.attention import _DTYPES, _Layout, _ptr, _stream, attention_forward
 
+    bf16 = path != "f32"
+    if path == "bf16-two-kernels":
+        tune({"MSDA_ATTN_FUSED": 0})
     b, h, length, d, rs = 2, 3, 300, 32, 36
-    _note("fused backward, unaligned gradient rows")
+    off = 4 if bf16 else 1
+    dt = torch.bfloat16 if bf16 else torch.float32
+    _note(f"unaligned output rows {path}")
     rng = np.random.default_rng(47)
-    q, k, v, g = (bf16_round(rng.standard_normal((b, h, length, d)).astype(np.float32)) for _ in range(4))
+    q, k, v, g = (rng.standard_normal((b, h, length, d)).astype(np.float32) for _ in range(4))
+    if bf16:
+        q, k, v, g = (bf16_round(x) for x in (q, k, v, g))
     lay = _Layout(b, 1, h, length, d)
-    tq, tk, tv, tg = (_t(x, torch.bfloat16) for x in (q, k, v, g))
-    out, stats = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
+    tq, tk, tv, tg = (_t(x, dt) for x in (q, k, v, g))
     n = b * h * length * rs
-    bufs = [torch.zeros(n + 4, dtype=torch.bfloat16, device=_dev()) for _ in range(3)]
-    grads = [x[4:].view(b, h, length, rs)[..., :d] for x in bufs]
+    row_strides = [h * length * rs, 0, length * rs, rs]
+
+    def views(count):
+        bufs = [torch.zeros(n + off, dtype=dt, device=_dev()) for _ in range(count)]
+        return bufs, [x[off:].view(b, h, length, rs)[..., :d] for x in bufs]
+
+    def untouched(bufs):
+        for x in bufs:
+            assert not _np(x[off:].view(b, h, length, rs)[..., d:]).any() and not _np(x[:off]).any()
+
+    tf, tg_ = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    obufs, (out_u,) = views(1)
+    stats_u = torch.empty(b * h * length * 4, dtype=torch.float32, device=_dev())
+    s = lay.strides_bhld(tq) + lay.strides_bhld(tk) + lay.strides_bhld(tv) + row_strides
+    rc = _native.lib().msda_attention_fwd(_ptr(tq), _ptr(tk), _ptr(tv), _DTYPES[dt], _ptr(out_u), _ptr(stats_u), b, 1, h, length, d,
+                                          (ctypes.c_int64 * 16)(*s), None, _stream(_dev()))
+    _native.check(rc)
+    torch.cuda.synchronize()
+    assert_close(_np(out_u), AT.sdpa(q, k, v, None), tf, "out")
+    untouched(obufs)
+
+    out, stats = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
+    gbufs, grads = views(3)
     s = []
     for t in (tq, tk, tv, out, tg):
         s += lay.strides_bhld(t)
-    for t in grads:
-        s += [h * length * rs, 0, length * rs, rs]
-    strides = (ctypes.c_int64 * 32)(*s)
-    rc = _native.lib().msda_attention_bwd(_ptr(tq), _ptr(tk), _ptr(tv), _ptr(out), _ptr(stats), _ptr(tg), _DTYPES[torch.bfloat16],
-                                          _ptr(grads[0]), _ptr(grads[1]), _ptr(grads[2]), b, 1, h, length, d, strides, None,
-                                          _stream(_dev()))
+    for _ in grads:
+        s += row_strides
+    rc = _native.lib().msda_attention_bwd(_ptr(tq), _ptr(tk), _ptr(tv), _ptr(out), _ptr(stats), _ptr(tg), _DTYPES[dt],
+                                          _ptr(grads[0]), _ptr(grads[1]), _ptr(grads[2]), b, 1, h, length, d,
+                                          (ctypes.c_int64 * 32)(*s), None, _stream(_dev()))
     _native.check(rc)
     torch.cuda.synchronize()
     for name, got, want in zip("qkv", grads, AT.sdpa_vjp(q, k, v, g)):
-        assert_close(_np(got), want, 2e-2, f"grad_{name}")
-    for x in bufs:  # nothing written outside the views
-        pad = _np(x[4:].view(b, h, length, rs)[..., d:])
-        assert not pad.any() and not _np(x[:4]).any()
+        assert_close(_np(got), want, tg_, f"grad_{name}")
+    untouched(gbufs)
