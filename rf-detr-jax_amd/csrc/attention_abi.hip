@@ -151,24 +151,33 @@ int bwd_b(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
   return bwd_b_rb<D, MASK, 4>(p, want_kv, st);
 }
 
-// The fused bf16 backward: one workgroup per (slice, head), one wave per key block and two dQ waves.
-int bwd_fused(const msda::AttnParams& p, hipStream_t st) {
-  static std::atomic<int> granted[msda_host::kMaxDevices];
-  auto kernel = msda::attn_bwd_fused_bf16_kernel;
-  const int nb = (p.len + 31) / 32, waves = nb + 2, lds = msda::at_fused_lds_bytes(nb);
+// The fused backward: one workgroup per (slice, head), one wave per key block and two dQ waves.
+template <typename K>
+int bwd_fused_launch(K kernel, std::atomic<int> (&granted)[msda_host::kMaxDevices], const msda::AttnParams& p, int lds, hipStream_t st) {
   const int rc = msda_host::allow_lds(kernel, lds, granted);
   if (rc != MSDA_OK) return rc;
   const int64_t grid = static_cast<int64_t>(p.batch) * p.groups * p.heads;
   if (grid >= (int64_t{1} << 31)) return fail(MSDA_ERR_UNSUPPORTED, "attention: too many workgroups");
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * waves), lds, st, p);
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * ((p.len + 31) / 32 + 2)), lds, st, p);
   return msda_host::check_launch("attention backward (fused)");
 }
 
-// The fused kernel serves bf16 at head_dim 32 without a mask, with at most 32 kAtFusedBlocks rows,
-// when grad_q and grad_k or grad_v are wanted (MSDA_ATTN_FUSED=0 selects the two kernels): it
-// forms S and dP once per block pair instead of once in each kernel.
-bool use_fused(const msda::AttnParams& p, int d, bool bf16, bool want_kv) {
-  return bf16 && d == 32 && p.mask == nullptr && want_kv && p.gq != nullptr && p.len <= 32 * msda::kAtFusedBlocks && msda_host::knob("MSDA_ATTN_FUSED", 1) != 0;
+int bwd_fused(const msda::AttnParams& p, bool bf16, hipStream_t st) {
+  const int nb = (p.len + 31) / 32;
+  if (bf16) {
+    static std::atomic<int> granted[msda_host::kMaxDevices];
+    return bwd_fused_launch(msda::attn_bwd_fused_bf16_kernel, granted, p, msda::at_fused_lds_bytes(nb), st);
+  }
+  static std::atomic<int> granted[msda_host::kMaxDevices];
+  return bwd_fused_launch(msda::attn_bwd_fused_f32_kernel, granted, p, msda::at_fused_f32_lds_bytes(nb), st);
+}
+
+// The fused kernels serve head_dim 32 without a mask, with at most 32 kAtFusedBlocks rows, when
+// grad_q and grad_k or grad_v are wanted (MSDA_ATTN_FUSED=0 selects the two kernels): they form
+// S and dP once per block pair instead of once in each kernel.
+bool use_fused(const msda::AttnParams& p, int d, bool want_kv) {
+  return d == 32 && p.mask == nullptr && want_kv && p.gq != nullptr && p.len <= 32 * msda::kAtFusedBlocks &&
+         msda_host::knob("MSDA_ATTN_FUSED", 1) != 0;
 }
 
 int fwd_dispatch(const msda::AttnParams& p, int d, bool bf16, hipStream_t st) {
@@ -183,7 +192,7 @@ int fwd_dispatch(const msda::AttnParams& p, int d, bool bf16, hipStream_t st) {
 
 int bwd_dispatch(const msda::AttnParams& p, int d, bool bf16, bool want_kv, hipStream_t st) {
   const bool m = p.mask != nullptr;
-  if (use_fused(p, d, bf16, want_kv)) return bwd_fused(p, st);
+  if (use_fused(p, d, want_kv)) return bwd_fused(p, bf16, st);
   if (bf16) {
     if (d == 32) return m ? bwd_b<32, true>(p, want_kv, st) : bwd_b<32, false>(p, want_kv, st);
     return m ? bwd_b<64, true>(p, want_kv, st) : bwd_b<64, false>(p, want_kv, st);

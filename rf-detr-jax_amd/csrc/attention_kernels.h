@@ -1030,6 +1030,8 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
       __syncthreads();  // chunk j staged; the dS tiles of chunk j - 2 read
       if (j == nchunks) break;
       const int b = j & 1;
+      if (kb == 0 && j * kAtChunk + lane < L)  // rowsum(dO * O) into the statistics (their entry 2)
+        p.stats[(static_cast<int64_t>(blockIdx.x) * L + j * kAtChunk + lane) * 4 + 2] = Ds[b][lane];
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {  // the chunk's two query blocks
         at_f16 s, dp;
@@ -1075,7 +1077,7 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   float* stats = p.stats + static_cast<int64_t>(blockIdx.x) * L * 4;
   const int srow = tq >> 1, shalf = tq & 1;
   uint4 qv[2], gv[2], ov[2];
-  at_f4 sq = {0.0f, 0.0f, 0.0f, 0.0f};
+  float2 sq = {0.0f, 0.0f};  // m, log2 l (8 bytes: no register of a wider load left idle in flight)
   auto prefetch = [&](int r0) {
     const int r = min(r0 + srow, L - 1);
     auto ld16 = [](const uint16_t* e) {  // rows are 8-byte aligned
@@ -1089,7 +1091,7 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
       gv[h] = ld16(gop + at_row_off(r, p.st[kAtGO][3]) + c);
       ov[h] = ld16(opp + at_row_off(r, p.st[kAtO][3]) + c);
     }
-    if (shalf == 0) sq = *reinterpret_cast<const at_f4*>(&stats[4 * r]);
+    if (shalf == 0) sq = *reinterpret_cast<const float2*>(&stats[4 * r]);
   };
   auto stage = [&](int r0, int b) {
     const bool in = r0 + srow < L;
@@ -1106,10 +1108,9 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
     // the row's other half: the neighbouring lane (DPP quad_perm [1, 0, 3, 2])
     dd += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(dd), 0xB1, 0xF, 0xF, false));
     if (shalf == 0) {
-      Ms[b][2 * srow] = in ? sq[0] : INFINITY;
-      Ms[b][2 * srow + 1] = in ? sq[1] : 0.0f;
+      Ms[b][2 * srow] = in ? sq.x : INFINITY;
+      Ms[b][2 * srow + 1] = in ? sq.y : 0.0f;
       Ds[b][srow] = in ? dd : 0.0f;
-      if (in) stats[4 * (r0 + srow) + 2] = dd;
     }
   };
   prefetch(0);
@@ -1148,6 +1149,181 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
     }
     // result column: the lane's query; rows: channels
     at_store_block(gqp, p.st[kAtGQ][3], jp * kAtChunk + 32 * h2q, L, acc0 + acc1, p.scale, Sq[h2q], lane);
+  }
+}
+
+// Fused backward, f32 (D = 32, L <= 32 kAtFusedBlocks, no mask): the bf16 kernel's split, phase by
+// phase over 32-row query blocks, since f32 dS tiles of two 64-row chunks would not fit in LDS.
+// Key waves form S, dP, P and dS of their key block against the phase's query block, accumulate
+// dK and dV, and write dS into an f32 tile [32 keys][32 queries]. The two dQ waves stage the next
+// query block (Q, dO, rowsum(dO * O), 4 threads per row) and form dQ^T = K^T dS^T of the previous
+// block over half of the key blocks each (v_mfma_f32_32x32x2_f32, K from an LDS copy, two chains)
+// into LDS; one phase later key wave 0, which has time to spare, adds the halves and stores the
+// block's rows. Row tiles, dS tiles and the halves are double buffered by phase parity: one
+// barrier per phase.
+constexpr int at_fused_f32_lds_bytes(int nb) { return nb * (32 * 32 * 4 + 2 * 32 * 32 * 4); }  // K copy, two dS tile sets
+
+// element (r, c) of a swizzled f32 tile [32][32]: 16-byte chunk c / 4 of row r at slot (c / 4) ^ ((r / 2) % 8)
+__device__ __forceinline__ int at_f32sw(int r, int c) { return r * 32 + 4 * ((c >> 2) ^ ((r >> 1) & 7)) + (c & 3); }
+
+__global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_f32_kernel(const AttnParams p) {
+  constexpr int D = 32, LD = D + 8;
+  __shared__ __align__(16) float Qs[2][32 * LD];  // query rows of the phase's block, by parity
+  __shared__ __align__(16) float Gs[2][32 * LD];  // output-gradient rows
+  __shared__ __align__(16) float Ms[2][2 * 32];   // m, log2 l (rows past L: +inf)
+  __shared__ __align__(16) float Ds[2][32];       // rowsum(dO * O)
+  __shared__ __align__(16) float Xq[2][2][16 * 64];  // the dQ waves' halves of dQ^T (result layout), by parity
+  extern __shared__ __align__(16) float at_lds[];
+  const int L = p.len, nb = (L + 31) / 32;  // key blocks; also the query blocks (phases)
+  float* Kf = at_lds;                       // [32 nb][32] key rows (0 past L)
+  float* St = Kf + 32 * nb * D;             // dS tiles: 1024 floats each, parity, key block
+  const AttnSlice sl(p, static_cast<int>(blockIdx.x));
+  const float* kp = static_cast<const float*>(p.k) + sl.base(p, kAtK);
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, grp = lane >> 5, col = lane & 31;
+  if (wave < nb) {  // key block kb = wave (uniform per wave)
+    const int kb = wave, key = kb * 32 + col, kcl = min(key, L - 1);
+    at_f4 kc[4];  // the block's rows of the key copy: row 8 u + lane / 8, channels 4 (lane % 8) .. + 3
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = kb * 32 + 8 * u + (lane >> 3);
+      kc[u] = row < L ? *reinterpret_cast<const at_f4*>(kp + at_row_off(row, p.st[kAtK][3]) + 4 * (lane & 7)) : at_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    at_f4 kr[D / 8], vr[D / 8];
+    const float* vp = static_cast<const float*>(p.v) + sl.base(p, kAtV);
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) {
+      kr[c] = *reinterpret_cast<const at_f4*>(kp + at_row_off(kcl, p.st[kAtK][3]) + 8 * c + 4 * grp);
+      vr[c] = *reinterpret_cast<const at_f4*>(vp + at_row_off(kcl, p.st[kAtV][3]) + 8 * c + 4 * grp);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) *reinterpret_cast<at_f4*>(&Kf[(kb * 32 + 8 * u + (lane >> 3)) * D + 4 * (lane & 7)]) = kc[u];
+    at_f16 dk[1] = {at_zero16()}, dv[1] = {at_zero16()};
+    float* gqp = static_cast<float*>(p.gq) + sl.base(p, kAtGQ);
+    const bool gq16 = (reinterpret_cast<uintptr_t>(gqp) & 15) == 0 && (p.st[kAtGQ][3] & 3) == 0;
+    for (int j = 0; j <= nb + 1; ++j) {
+      __syncthreads();  // query block j staged; the dS tiles of block j - 2 read; the halves of block j - 2 written
+      if (kb == 0 && j >= 2) {
+        // dQ rows of block j - 2: slot u of this lane is query (lane + 64 u) / 8, channels
+        // 8 c + 4 h .. + 3 with c = ((lane + 64 u) % 8) / 2 and h = lane % 2 (8 lanes to a row)
+        const float* x0 = Xq[j & 1][0];
+        const float* x1 = Xq[j & 1][1];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int sl8 = lane + 64 * u, qr = sl8 >> 3, c = (sl8 & 7) >> 1, h = sl8 & 1;
+          const int x = 4 * (c * 64 + qr + 32 * h);
+          const at_f4 v = (*reinterpret_cast<const at_f4*>(&x0[x]) + *reinterpret_cast<const at_f4*>(&x1[x])) * p.scale;
+          const int q = (j - 2) * 32 + qr, d0 = 8 * c + 4 * h;
+          if (q < L) {
+            if (gq16) {
+              *reinterpret_cast<at_f4*>(gqp + at_row_off(q, p.st[kAtGQ][3]) + d0) = v;
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) gqp[at_row_off(q, p.st[kAtGQ][3]) + d0 + e] = v[e];
+            }
+          }
+        }
+      }
+      if (j >= nb) continue;
+      const int b = j & 1;
+      if (kb == 0 && lane < 32 && j * 32 + lane < L)  // rowsum(dO * O) into the statistics (their entry 2)
+        p.stats[(static_cast<int64_t>(blockIdx.x) * L + j * 32 + lane) * 4 + 2] = Ds[b][lane];
+      at_f16 s, dp;
+      at_scores_pair<D>(s, dp, Qs[b], Gs[b], kr, vr, col, grp);  // S = Q K^T, dP = dO V^T
+      at_f16 pw;
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {
+        const int ql = 8 * c4 + 4 * grp;
+        const at_f4 ms0 = *reinterpret_cast<const at_f4*>(&Ms[b][2 * ql]), ms1 = *reinterpret_cast<const at_f4*>(&Ms[b][2 * ql + 4]);
+        const at_f4 dd = *reinterpret_cast<const at_f4*>(&Ds[b][ql]);
+        const float mq[4] = {ms0[0], ms0[2], ms1[0], ms1[2]}, lq[4] = {ms0[1], ms0[3], ms1[1], ms1[3]};
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int i = 4 * c4 + jj;
+          // a lane past L holds the clamped last key: finite weights, and its rows of the key copy
+          // are 0, so it adds nothing to dQ; rows past L have m = +inf: weight 0
+          pw[i] = at_exp2(fmaf(s[i], p.scale2, -mq[jj]) - lq[jj]);
+          s[i] = pw[i] * (dp[i] - dd[jj]);  // dS
+        }
+      }
+      at_accum2<D>(dv, dk, Gs[b], Qs[b], pw, s, col, grp);  // dV^T += dO^T P, dK^T += Q^T dS
+      float* T = St + (b * nb + kb) * 1024;  // dS^T tile: row = key (this lane's col), columns = queries
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<at_f4*>(&T[at_f32sw(col, 8 * c + 4 * grp)]) = at_f4{s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]};
+    }
+    // the dQ waves read the last dS tiles before the last barrier: they hold the output scratch now
+    float* sc = St + kb * (at_scratch_bytes<float>() / 4);
+    if (p.gk != nullptr) at_store_block<float>(static_cast<float*>(p.gk) + sl.base(p, kAtGK), p.st[kAtGK][3], kb * 32, L, dk[0], p.scale, sc, lane);
+    if (p.gv != nullptr) at_store_block<float>(static_cast<float*>(p.gv) + sl.base(p, kAtGV), p.st[kAtGV][3], kb * 32, L, dv[0], 1.0f, sc, lane);
+    return;
+  }
+  // The two dQ waves. Staging: thread tq holds row tq / 4 of the block, channels 8 (tq % 4) .. + 7.
+  const int tq = t - 64 * nb, dqw = tq >> 6;
+  const float* qp = static_cast<const float*>(p.q) + sl.base(p, kAtQ);
+  const float* gop = static_cast<const float*>(p.go) + sl.base(p, kAtGO);
+  const float* opp = static_cast<const float*>(p.o) + sl.base(p, kAtO);
+  float* stats = p.stats + static_cast<int64_t>(blockIdx.x) * L * 4;
+  const int srow = tq >> 2, sq4 = tq & 3;
+  at_f4 qv[2], gv[2], ov[2];
+  float2 sq = {0.0f, 0.0f};  // m, log2 l (8 bytes: no register of a wider load left idle in flight)
+  auto prefetch = [&](int r0) {
+    const int r = min(r0 + srow, L - 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 8 * sq4 + 4 * h;
+      qv[h] = *reinterpret_cast<const at_f4*>(qp + at_row_off(r, p.st[kAtQ][3]) + c);
+      gv[h] = *reinterpret_cast<const at_f4*>(gop + at_row_off(r, p.st[kAtGO][3]) + c);
+      ov[h] = *reinterpret_cast<const at_f4*>(opp + at_row_off(r, p.st[kAtO][3]) + c);
+    }
+    if (sq4 == 0) sq = *reinterpret_cast<const float2*>(&stats[4 * r]);
+  };
+  auto stage = [&](int r0, int b) {
+    const bool in = r0 + srow < L;
+    const at_f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    float dd = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 8 * sq4 + 4 * h;
+      *reinterpret_cast<at_f4*>(&Qs[b][srow * LD + c]) = in ? qv[h] : z;
+      *reinterpret_cast<at_f4*>(&Gs[b][srow * LD + c]) = in ? gv[h] : z;
+      dd += gv[h][0] * ov[h][0] + gv[h][1] * ov[h][1] + gv[h][2] * ov[h][2] + gv[h][3] * ov[h][3];
+    }
+    // the row's four quarters: neighbouring lanes (DPP quad_perm [1, 0, 3, 2], then [2, 3, 0, 1])
+    dd += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(dd), 0xB1, 0xF, 0xF, false));
+    dd += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(dd), 0x4E, 0xF, 0xF, false));
+    if (sq4 == 0) {
+      Ms[b][2 * srow] = in ? sq.x : INFINITY;
+      Ms[b][2 * srow + 1] = in ? sq.y : 0.0f;
+      Ds[b][srow] = in ? dd : 0.0f;
+    }
+  };
+  prefetch(0);
+  stage(0, 0);
+  if (nb > 1) prefetch(32);
+  const int nh = (nb + 1) / 2, kb0 = dqw == 0 ? 0 : nh, kb1 = dqw == 0 ? nh : nb;  // this wave's key blocks
+  for (int j = 0; j <= nb + 1; ++j) {
+    __syncthreads();  // block j staged; the dS tiles of block j - 1 written; the halves of block j - 3 read
+    if (j + 1 < nb) {
+      stage((j + 1) * 32, (j + 1) & 1);
+      if (j + 2 < nb) prefetch((j + 2) * 32);
+    }
+    if (j == 0 || j > nb) continue;
+    const int bp = (j - 1) & 1;  // block j - 1: dQ^T over this wave's key blocks
+    at_f16 acc0 = at_zero16(), acc1 = at_zero16();
+    for (int kb2 = kb0; kb2 < kb1; ++kb2) {
+      const float* T = St + (bp * nb + kb2) * 1024;
+      const float* K = Kf + kb2 * 32 * D;
+#pragma unroll
+      for (int s2 = 0; s2 < 16; s2 += 2) {
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(K[(s2 + grp) * D + col], T[at_f32sw(s2 + grp, col)], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(K[(s2 + 16 + grp) * D + col], T[at_f32sw(s2 + 16 + grp, col)], acc1, 0, 0, 0);
+      }
+    }
+    float* x = Xq[(j + 1) & 1][dqw];  // block j - 1's parity
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *reinterpret_cast<at_f4*>(&x[4 * (c * 64 + lane)]) = at_f4{acc0[4 * c] + acc1[4 * c], acc0[4 * c + 1] + acc1[4 * c + 1],
+                                                                acc0[4 * c + 2] + acc1[4 * c + 2], acc0[4 * c + 3] + acc1[4 * c + 3]};
   }
 }
 

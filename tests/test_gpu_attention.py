@@ -228,21 +228,25 @@ def test_single_gradient_requests():
 FUSED_LENGTHS = [1, 17, 32, 33, 64, 65, 129, 200, 256, 257, 300, 319, 320, 321]
 
 
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
 @pytest.mark.parametrize("length", FUSED_LENGTHS)
-def test_fused_backward_against_two_kernel_path(length, tune):
-    """bf16 at head_dim 32 without a mask, up to 320 rows: one fused backward kernel (one
-    workgroup per (slice, head): a wave per key block, two waves that form dQ from the dS tiles)
-    against the oracle, and against the two-kernel path (MSDA_ATTN_FUSED=0) on the same forward;
-    both write rowsum(dO * O) into entry 2 of the statistics. 321 rows take the two kernels either
-    way."""
+def test_fused_backward_against_two_kernel_path(length, bf16, tune):
+    """Head_dim 32 without a mask, up to 320 rows: one fused backward kernel (one workgroup per
+    (slice, head): a wave per key block, two waves that form dQ from the dS tiles) against the
+    oracle, and against the two-kernel path (MSDA_ATTN_FUSED=0) on the same forward; both write
+    rowsum(dO * O) into entry 2 of the statistics. 321 rows take the two kernels either way."""
     from rfdetr_jax_amd.attention import _Layout, attention_backward, attention_forward
 
     b, h, d = 2, 3, 32
-    _note(f"fused backward L={length}")
+    _note(f"fused backward L={length} bf16={bf16}")
     rng = np.random.default_rng(45 + length)
-    q, k, v, g = (bf16_round(rng.standard_normal((b, h, length, d)).astype(np.float32)) for _ in range(4))
+    q, k, v, g = (rng.standard_normal((b, h, length, d)).astype(np.float32) for _ in range(4))
+    if bf16:
+        q, k, v, g = (bf16_round(x) for x in (q, k, v, g))
+    dt = torch.bfloat16 if bf16 else torch.float32
+    tol, cross = (2e-2, 1e-2) if bf16 else (1e-4, 1e-4)
     lay = _Layout(b, 1, h, length, d)
-    tq, tk, tv, tg = (_t(x, torch.bfloat16) for x in (q, k, v, g))
+    tq, tk, tv, tg = (_t(x, dt) for x in (q, k, v, g))
     out, stats = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
     fused = attention_backward(tq, tk, tv, out, stats, tg, lay, lay.strides_bhld)
     torch.cuda.synchronize()
@@ -256,30 +260,34 @@ def test_fused_backward_against_two_kernel_path(length, tune):
     assert_close(dsum_split, want_dsum, 1e-5, "rowsum(dO * O), two kernels")
     want = AT.sdpa_vjp(q, k, v, g)
     for name, a, c, w in zip("qkv", fused, split, want):
-        assert_close(_np(a), w, 2e-2, f"grad_{name} fused")
-        assert_close(_np(c), w, 2e-2, f"grad_{name} two kernels")
-        assert_close(_np(a), _np(c).astype(np.float64), 1e-2, f"grad_{name} fused against two kernels")
+        assert_close(_np(a), w, tol, f"grad_{name} fused")
+        assert_close(_np(c), w, tol, f"grad_{name} two kernels")
+        assert_close(_np(a), _np(c).astype(np.float64), cross, f"grad_{name} fused against two kernels")
 
 
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
 @pytest.mark.parametrize("needs", [(True, True, False), (True, False, True), (True, False, False), (False, True, True)],
                          ids=["qk", "qv", "q", "kv"])
-def test_bf16_gradient_subsets(needs):
-    """bf16 at head_dim 32: grad_q with one of grad_k / grad_v (the fused kernel, skipping the
-    missing store), grad_q alone and grad_k with grad_v (the two-kernel path's halves)."""
+def test_gradient_subsets_head_dim_32(needs, bf16):
+    """Head_dim 32: grad_q with one of grad_k / grad_v (the fused kernel, skipping the missing
+    store), grad_q alone and grad_k with grad_v (the two-kernel path's halves)."""
     from rfdetr_jax_amd.attention import _Layout, attention_backward, attention_forward
 
-    _note(f"bf16 gradient subset {needs}")
+    _note(f"gradient subset {needs} bf16={bf16}")
     rng = np.random.default_rng(46)
-    q, k, v, g = (bf16_round(rng.standard_normal((2, 2, 150, 32)).astype(np.float32)) for _ in range(4))
+    q, k, v, g = (rng.standard_normal((2, 2, 150, 32)).astype(np.float32) for _ in range(4))
+    if bf16:
+        q, k, v, g = (bf16_round(x) for x in (q, k, v, g))
+    dt = torch.bfloat16 if bf16 else torch.float32
     lay = _Layout(2, 1, 2, 150, 32)
-    tq, tk, tv = (_t(x, torch.bfloat16) for x in (q, k, v))
+    tq, tk, tv = (_t(x, dt) for x in (q, k, v))
     out, stats = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
-    got = attention_backward(tq, tk, tv, out, stats, _t(g, torch.bfloat16), lay, lay.strides_bhld, None, needs)
+    got = attention_backward(tq, tk, tv, out, stats, _t(g, dt), lay, lay.strides_bhld, None, needs)
     torch.cuda.synchronize()
     want = AT.sdpa_vjp(q, k, v, g)
     for j in range(3):
         if needs[j]:
-            assert_close(_np(got[j]), want[j], 2e-2, f"gradient {j}")
+            assert_close(_np(got[j]), want[j], 2e-2 if bf16 else 1e-4, f"gradient {j}")
         else:
             assert got[j] is None
 
