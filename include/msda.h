@@ -317,7 +317,9 @@ int msda_attention_fwd(const void* q, const void* k, const void* v, int dtype, v
 /*
  * Backward of msda_attention_fwd for the cotangent grad_out: grad_q, grad_k, grad_v (each may be
  * NULL to skip it; same layouts and dtype rules). out and stats are the forward's (stats entry 2
- * is overwritten).
+ * is overwritten). With head_dim 32, no mask, len <= 320 and grad_q plus grad_k or grad_v
+ * requested, one kernel forms all gradients (the tuning knob MSDA_ATTN_FUSED=0 selects the
+ * two-kernel path instead; the two agree within f32 summation order).
  * strides: [8 tensors: q, k, v, out, grad_out, grad_q, grad_k, grad_v][4].
  */
 int msda_attention_bwd(const void* q, const void* k, const void* v, const void* out, float* stats,
