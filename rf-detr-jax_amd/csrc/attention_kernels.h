@@ -984,10 +984,11 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
 // block each and form S, dP, P and dS of each (query block, key block) pair once: they accumulate
 // the block's dK and dV (as attn_bwd_kv_bf16_kernel) and write dS into LDS tiles [32 keys][32
 // queries]. Waves nb and nb + 1 stage the query-side rows (Q, dO, and rowsum(dO * O) from O) one
-// chunk ahead and form dQ of the previous chunk's two query blocks, one block each, as one MFMA
-// chain over all key blocks, dQ^T = K^T dS^T, from a swizzled copy of K and the dS tiles by
-// transposing reads, so no partial sums cross waves. The row tiles and the dS tiles are double
-// buffered by chunk parity: one barrier per chunk.
+// chunk ahead and form dQ of the previous chunk's two query blocks, one block each, over the first
+// half of the key blocks, dQ^T = K^T dS^T, from a swizzled copy of K and the dS tiles by
+// transposing reads; key waves 0 and 1, idle otherwise at that point, form the second half into
+// LDS, which the dQ waves add one chunk later before storing the block. The row tiles, dS tiles
+// and halves are double buffered by chunk parity: one barrier per chunk.
 constexpr int kAtFusedBlocks = 10;  // key-block waves; with the two dQ waves, 768 threads (three waves per SIMD)
 
 // Dynamic LDS bytes of the fused kernel for nb key blocks: the swizzled key rows [32 nb][32] and
@@ -1005,6 +1006,7 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   __shared__ __align__(16) float Ms[2][2 * kAtChunk];  // [64][2]: m, log2 l (rows past L: +inf)
   __shared__ __align__(16) float Ds[2][kAtChunk];      // [64]: rowsum(dO * O)
   __shared__ __align__(16) uint16_t Sq[2][32 * 40];    // the dQ waves' output scratch
+  __shared__ __align__(16) float Xq[2][2][16 * 64];      // key waves 0, 1: dQ^T of a block over the second half of the key blocks
   extern __shared__ __align__(16) float at_lds[];
   const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
   uint16_t* Kt = reinterpret_cast<uint16_t*>(at_lds);  // swizzled [32 nb][D] key rows (0 past L)
@@ -1026,9 +1028,32 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
 #pragma unroll
     for (int u = 0; u < 4; ++u) *reinterpret_cast<uint2*>(&Kt[at_swo<D>(kb * 32 + 8 * u + (lane >> 3), 4 * (lane & 7))]) = kc[u];
     at_f16 dk[1] = {at_zero16()}, dv[1] = {at_zero16()};
-    for (int j = 0; j <= nchunks; ++j) {
-      __syncthreads();  // chunk j staged; the dS tiles of chunk j - 2 read
-      if (j == nchunks) break;
+    const int nh = (nb + 1) / 2;  // key blocks [0, nh) for the dQ waves, [nh, nb) for key waves 0 and 1
+    for (int j = 0; j <= nchunks + 1; ++j) {
+      __syncthreads();  // chunk j staged; the dS tiles of chunk j - 2 read; the halves of chunk j - 3 added
+      if (kb < 2 && nb >= 2 && j >= 1 && j <= nchunks) {
+        // dQ^T of query block kb of chunk j - 1 over key blocks [nh, nb) into Xq (result layout)
+        const int bp = (j - 1) & 1, g16 = lane >> 4, r = lane & 15;
+        const int tc = 16 * (g16 & 1) + 4 * (r & 3), tro = 4 * grp + (r >> 2);
+        at_f16 acc0 = at_zero16(), acc1 = at_zero16();
+        for (int kb2 = nh; kb2 < nb; ++kb2) {
+          const uint16_t* Th = St + ((bp * nb + kb2) * 2 + kb) * 1024;
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            const int ro = 16 * s2 + tro;
+            const at_bf8 ka = at_bf8_of(at_read_tr(Kt + at_swo<D>(32 * kb2 + ro, tc)), at_read_tr(Kt + at_swo<D>(32 * kb2 + ro + 8, tc)));
+            const at_bf8 sb = at_bf8_of(at_read_tr(Th + at_swo<D>(ro, tc)), at_read_tr(Th + at_swo<D>(ro + 8, tc)));
+            if (s2 == 0) acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, sb, acc0, 0, 0, 0);
+            else acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, sb, acc1, 0, 0, 0);
+          }
+        }
+        float* x = Xq[bp][kb];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          *reinterpret_cast<at_f4*>(&x[4 * (c * 64 + lane)]) = at_f4{acc0[4 * c] + acc1[4 * c], acc0[4 * c + 1] + acc1[4 * c + 1],
+                                                                    acc0[4 * c + 2] + acc1[4 * c + 2], acc0[4 * c + 3] + acc1[4 * c + 3]};
+      }
+      if (j >= nchunks) continue;
       const int b = j & 1;
       if (kb == 0 && j * kAtChunk + lane < L)  // rowsum(dO * O) into the statistics (their entry 2)
         p.stats[(static_cast<int64_t>(blockIdx.x) * L + j * kAtChunk + lane) * 4 + 2] = Ds[b][lane];
@@ -1063,7 +1088,7 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
         }
       }
     }
-    // the dS tile set that the last dQ pass does not read is this wave's output scratch now
+    // the last dQ passes read the other dS tile set before the last barrier: this wave's output scratch now
     uint16_t* sc = St + (((nchunks & 1) * nb + kb) * 2) * 1024;
     if (p.gk != nullptr) at_store_block(static_cast<bf16_t*>(p.gk) + sl.base(p, kAtGK), p.st[kAtGK][3], kb * 32, L, dk[0], p.scale, sc, lane);
     if (p.gv != nullptr) at_store_block(static_cast<bf16_t*>(p.gv) + sl.base(p, kAtGV), p.st[kAtGV][3], kb * 32, L, dv[0], 1.0f, sc, lane);
@@ -1119,13 +1144,27 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   bf16_t* gqp = static_cast<bf16_t*>(p.gq) + sl.base(p, kAtGQ);
   const int g16 = lane >> 4, r = lane & 15;
   const int tc = 16 * (g16 & 1) + 4 * (r & 3), tro = 4 * grp + (r >> 2);  // transposing-read lane offsets
-  for (int j = 0; j <= nchunks; ++j) {
-    __syncthreads();  // chunk j staged; the dS tiles of chunk j - 1 written
+  const int nh = (nb + 1) / 2;
+  at_f16 held = at_zero16();  // dQ^T of this wave's query block of the previous chunk over key blocks [0, nh)
+  for (int j = 0; j <= nchunks + 1; ++j) {
+    __syncthreads();  // chunk j staged; the dS tiles of chunk j - 1 and the halves of chunk j - 2 written
+    if (j >= 2) {  // chunk j - 2: add key wave h2q's half and store
+      if (nb >= 2) {
+        const float* x = Xq[j & 1][h2q];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const at_f4 h4 = *reinterpret_cast<const at_f4*>(&x[4 * (c * 64 + lane)]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) held[4 * c + e] += h4[e];
+        }
+      }
+      at_store_block(gqp, p.st[kAtGQ][3], (j - 2) * kAtChunk + 32 * h2q, L, held, p.scale, Sq[h2q], lane);
+    }
     if (j + 1 < nchunks) {
       stage((j + 1) * kAtChunk, (j + 1) & 1);
       if (j + 2 < nchunks) prefetch((j + 2) * kAtChunk);
     }
-    if (j == 0) continue;
+    if (j == 0 || j > nchunks) continue;
     const int jp = j - 1, bp = jp & 1;
     // dQ^T = sum over key blocks of K^T dS^T: two chains (the two 16-key halves of each block),
     // the next block's operands read while the current block's products run
@@ -1141,14 +1180,13 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
       }
     };
     operands(0);
-    for (int kb2 = 0; kb2 < nb; ++kb2) {
+    for (int kb2 = 0; kb2 < nh; ++kb2) {
       const at_bf8 a0 = ka[0], a1 = ka[1], b0 = sb[0], b1 = sb[1];
-      if (kb2 + 1 < nb) operands(kb2 + 1);
+      if (kb2 + 1 < nh) operands(kb2 + 1);
       acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc0, 0, 0, 0);
       acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc1, 0, 0, 0);
     }
-    // result column: the lane's query; rows: channels
-    at_store_block(gqp, p.st[kAtGQ][3], jp * kAtChunk + 32 * h2q, L, acc0 + acc1, p.scale, Sq[h2q], lane);
+    held = acc0 + acc1;  // result column: the lane's query; rows: channels
   }
 }
 
