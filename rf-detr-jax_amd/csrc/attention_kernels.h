@@ -549,7 +549,6 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bw
   const float* stats = p.stats + static_cast<int64_t>(w.zh) * L * 4;
   const int t = threadIdx.x, lane = t & 63, grp = lane >> 5, col = lane & 31;
   const int kb = w.rc * RB + (t >> 6), key = kb * 32 + col;
-  const bool kv = key < L;
   at_f4 kr[D / 8], vr[D / 8];
   {
     const VT* kp = static_cast<const VT*>(p.k) + w.sl.base(p, kAtK);
@@ -908,7 +907,6 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
   const float* stats = p.stats + static_cast<int64_t>(w.zh) * L * 4;
   const int t = threadIdx.x, lane = t & 63, grp = lane >> 5, col = lane & 31;
   const int kb = w.rc * RB + (t >> 6), key = kb * 32 + col;
-  const bool kv = key < L;
   at_bf8 kr[D / 16], vr[D / 16];
   at_row_bf8<D>(kr, static_cast<const uint16_t*>(p.k) + w.sl.base(p, kAtK), min(key, L - 1) * p.st[kAtK][3], grp);
   at_row_bf8<D>(vr, static_cast<const uint16_t*>(p.v) + w.sl.base(p, kAtV), min(key, L - 1) * p.st[kAtV][3], grp);
