@@ -353,3 +353,45 @@ def test_unaligned_output_rows(path, tune):
     for name, got, want in zip("qkv", grads, AT.sdpa_vjp(q, k, v, g)):
         assert_close(_np(got), want, tg_, f"grad_{name}")
     untouched(gbufs)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+@pytest.mark.parametrize("seed", range(6))
+def test_fused_backward_random_shapes(seed, bf16):
+    """Seeded random shapes through the fused backward (head_dim 32, no mask): 1-3 images, 1-4
+    heads, 1-320 rows, rows padded to a random stride (a multiple of 4 elements, as the interface
+    requires), against the float64 oracle."""
+    import ctypes
+
+    from rfdetr_jax_amd import _native
+    from rfdetr_jax_amd.attention import _DTYPES, _Layout, _ptr, _stream, attention_forward
+
+    rng = np.random.default_rng(1000 + seed)
+    b, h, length, d = int(rng.integers(1, 4)), int(rng.integers(1, 5)), int(rng.integers(1, 321)), 32
+    rs = d + 4 * int(rng.integers(0, 4))
+    _note(f"fused random shape seed={seed} bf16={bf16}: b={b} h={h} L={length} row stride {rs}")
+    dt = torch.bfloat16 if bf16 else torch.float32
+    q, k, v, g = (rng.standard_normal((b, h, length, d)).astype(np.float32) for _ in range(4))
+    if bf16:
+        q, k, v, g = (bf16_round(x) for x in (q, k, v, g))
+
+    def padded(x):
+        buf = torch.zeros((b, h, length, rs), dtype=dt, device=_dev())
+        if x is not None:
+            buf[..., :d] = _t(x, dt)
+        return buf[..., :d]
+
+    tq, tk, tv, tg = (padded(x) for x in (q, k, v, g))
+    lay = _Layout(b, 1, h, length, d)
+    out, stats = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
+    grads = [padded(None) for _ in range(3)]
+    s = []
+    for t in (tq, tk, tv, out, tg, *grads):
+        s += lay.strides_bhld(t)
+    rc = _native.lib().msda_attention_bwd(_ptr(tq), _ptr(tk), _ptr(tv), _ptr(out), _ptr(stats), _ptr(tg), _DTYPES[dt],
+                                          _ptr(grads[0]), _ptr(grads[1]), _ptr(grads[2]), b, 1, h, length, d,
+                                          (ctypes.c_int64 * 32)(*s), None, _stream(_dev()))
+    _native.check(rc)
+    torch.cuda.synchronize()
+    for name, got, want in zip("qkv", grads, AT.sdpa_vjp(q, k, v, g)):
+        assert_close(_np(got), want, 2e-2 if bf16 else 1e-4, f"grad_{name}")
