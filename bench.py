@@ -386,7 +386,8 @@ def measure_attention(dev, steps, batch=8, groups=13, per=300, heads=8, head_dim
     on the [B, G * P, C] rows in place, beside torch's F.scaled_dot_product_attention on the same
     tensors split into groups and heads (the reference's _split_groups + head transposes) with its
     autograd backward. Algorithmic FLOPs: forward 4 L^2 D per (slice, head) (two products), backward
-    twice that (dV, dP, dQ, dK; the kernels' recomputation of the scores is not counted)."""
+    twice that (dV, dP, dQ, dK; the kernels' recomputation of the scores is not counted). Also the
+    step with the backward's two kernels (MSDA_ATTN_FUSED=0) in place of the fused one."""
     import numpy as np
     import torch
     import torch.nn.functional as F
@@ -427,10 +428,20 @@ def measure_attention(dev, steps, batch=8, groups=13, per=300, heads=8, head_dim
     flops_fwd = 4 * per * per * head_dim * batch * groups * heads
     fwd_us = time_graph(fwd, steps)[0]
     step_us = time_graph(ours, steps)[0]
+    # the same step with the backward's two kernels (each forming S, P and dP) instead of the fused one
+    from rfdetr_jax_amd import _native
+
+    lib = _native.lib()
+    _native.check(lib.msda_set_tuning(b"MSDA_ATTN_FUSED", b"0"))
+    try:
+        step_split_us = time_graph(ours, steps)[0]
+    finally:
+        lib.msda_set_tuning(b"MSDA_ATTN_FUSED", None)
     return {
         "shape": {"batch": batch, "groups": groups, "queries_per_group": per, "heads": heads, "head_dim": head_dim, "dtype": dtype},
         "fwd_us": round(fwd_us, 3),
         "step_us": round(step_us, 3),
+        "step_us_two_kernel_backward": round(step_split_us, 3),
         "fwd_tflops": round(flops_fwd / fwd_us / 1e6, 1),
         "step_tflops": round(3 * flops_fwd / step_us / 1e6, 1),
         "torch_step_us_eager": round(time_eager(torch_step, steps), 3),
