@@ -6,14 +6,17 @@ at the RF-DETR Nano group-DETR shape (config 2: batch 8, one 24x24 level, 16 hea
 queries, 2 points, f32). A "step" is one forward + one backward call over that batch, with
 inputs already resident in HBM.
 
-Timing: W warm-up steps, then K steps launched from Python as a training loop calls the op (each
-call validates, plans and enqueues its kernels; the host stays ahead of the GPU) between two events
-on the launch stream, synchronised on both sides: `value`. The same steps replayed from a HIP graph
-(20 steps per graph) are reported beside it as `graph_us_per_call`; on this ROCm image graph
-replays run slower (about 1 us more per kernel node). The dominant call's average duration (the
-roofline's `avg_launch_us`) is measured the same way, with events around K eager launches of that
-call alone, the launch pattern of the rocprofv3 kernel traces in profiles/. per_config times are
-graph replays (fwd_us, bwd_us, step_us) unless marked eager.
+Timing: W warm-up steps and then further steps until at least WARM_MS milliseconds of them have
+run (a fixed time-based warm-up, so that clocks and caches settle whatever W is), then K steps
+launched from Python as a training loop calls the op (each call validates, plans and enqueues its
+kernels; the host stays ahead of the GPU) between two events on the launch stream, synchronised on
+both sides: `value`. Eager launches are the headline because that is how a training step calls the
+op; the same steps replayed from a HIP graph (20 steps per graph) are reported beside it as
+`graph_us_per_call` (within about a microsecond of the eager figure at the headline shape, either
+side). The dominant call's average duration (the roofline's `avg_launch_us`) is measured the same
+way, with events around K eager launches of that call alone, the launch pattern of the rocprofv3
+kernel traces in profiles/. per_config times are graph replays (fwd_us, bwd_us, step_us) unless
+marked eager.
 
 Roofline: the dominant kernel's algorithmic HBM bytes (Workload.hbm_bytes) against 8 TB/s and its
 algorithmic LDS bytes (Workload.lds_bytes) against the LDS read peak measured in the same run by
@@ -49,6 +52,7 @@ METRIC = "deform-attn fwd+bwd μs/call + achieved HBM GB/s (% peak), Nano group-
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 LDS_PEAK_NOMINAL_GBPS = 256 * 128 * 2.4  # 256 CUs x 128 B/clk x 2.4 GHz, used only if the probe fails
 MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+WARM_MS = 150.0  # time-based warm-up before the first timed step of a workload
 
 
 def log(msg):
@@ -234,18 +238,30 @@ def time_eager(fn, reps):
     return start.elapsed_time(end) * 1000.0 / reps
 
 
-def measure(w, dev, steps, warmup):
-    calls = Calls(w, dev)
+def warm_up(step, warmup, min_ms=WARM_MS):
+    """`warmup` steps, then more until at least `min_ms` of wall time has passed (synchronised)."""
+    import torch
+
     h = _stream_handle()
     for _ in range(warmup):
-        calls.fwd(h)
-        if w.backward:
-            calls.bwd(h)
+        step(h)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < min_ms:
+        for _ in range(10):
+            step(h)
+        torch.cuda.synchronize()
+
+
+def measure(w, dev, steps, warmup):
+    calls = Calls(w, dev)
 
     def step(hs):
         calls.fwd(hs)
         if w.backward:
             calls.bwd(hs)
+
+    warm_up(step, warmup)
 
     res = {}
     res["step_us_graph"], res["graph_steps"] = time_graph(step, steps)
@@ -475,34 +491,37 @@ def lds_peak(dev, blocks=5120, reps=256, trials=5):
             "probe": "msda_probe_lds_read (ds_read_b128, 1 KB per wave instruction)"}
 
 
-def lds_atomic_peak(dev, blocks=5120, reps=64, trials=5):
-    """Device LDS f64 atomic-add rate (lane additions per second), measured with the library's
-    probe (msda_probe_lds_atomic: ds_add_f64, each wave instruction on 64 consecutive doubles) on
-    the current stream: best of `trials`; the probe's sums are checked."""
+def lds_atomic_peak(dev, blocks=5120, reps=64, trials=5, f32=False):
+    """Device LDS atomic-add rate (lane additions per second), measured with the library's probe
+    (msda_probe_lds_atomic: ds_add_f64, or with f32 msda_probe_lds_atomic_f32: ds_add_f32; each wave
+    instruction on 64 consecutive elements) on the current stream: best of `trials`; the probe's
+    sums are checked."""
     import torch
 
     from rfdetr_jax_amd import _native
 
     lib = _native.lib()
-    out = torch.empty(blocks * 256, dtype=torch.float64, device=dev)
+    probe = lib.msda_probe_lds_atomic_f32 if f32 else lib.msda_probe_lds_atomic
+    out = torch.empty(blocks * 256, dtype=torch.float32 if f32 else torch.float64, device=dev)
     ptr = ctypes.c_void_p(out.data_ptr())
     ops = lib.msda_probe_lds_atomic_ops(blocks, reps)
     h = _stream_handle()
-    _native.check(0 if lib.msda_probe_lds_atomic(ptr, blocks, reps, h) == 0 else _native.ERR_LAUNCH)
+    _native.check(0 if probe(ptr, blocks, reps, h) == 0 else _native.ERR_LAUNCH)
     torch.cuda.synchronize()
-    if float(out.sum().item()) != float(ops):
-        raise RuntimeError("LDS atomic probe: wrong sum")
+    if not bool(torch.all(out == 16.0 * reps).item()):
+        raise RuntimeError("LDS atomic probe: wrong sums")
     best = None
     for _ in range(trials):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        lib.msda_probe_lds_atomic(ptr, blocks, reps, h)
+        probe(ptr, blocks, reps, h)
         end.record()
         torch.cuda.synchronize()
         us = start.elapsed_time(end) * 1000.0
         best = us if best is None else min(best, us)
+    name = "msda_probe_lds_atomic_f32 (ds_add_f32" if f32 else "msda_probe_lds_atomic (ds_add_f64"
     return {"gops": round(ops / best / 1e3, 1), "ops": ops, "us": round(best, 3), "blocks": blocks, "reps": reps,
-            "probe": "msda_probe_lds_atomic (ds_add_f64, 64 consecutive doubles per wave instruction)"}
+            "probe": f"{name}, 64 consecutive elements per wave instruction)"}
 
 
 def measure_cold(w, dev, steps):
@@ -654,11 +673,13 @@ def main():
         lds = {"gbps": LDS_PEAK_NOMINAL_GBPS, "probe": "nominal (probe failed)"}
     lds_peak_gbps = lds["gbps"]
     log(f"LDS read peak {lds_peak_gbps:.0f} GB/s")
-    atom = None
+    atom = atom32 = None
     if w.backward:
         try:
             atom = lds_atomic_peak(dev)
             log(f"LDS f64 atomic-add peak {atom['gops']:.0f} G lane-adds/s")
+            atom32 = lds_atomic_peak(dev, blocks=1024, reps=4, f32=True)
+            log(f"LDS f32 atomic-add rate {atom32['gops']:.0f} G lane-adds/s")
         except Exception as e:  # a measurement aid: the entry is left out
             log(f"LDS atomic probe failed ({e})")
 
@@ -761,6 +782,10 @@ def main():
         line["roofline"]["lds_atomic"] = {"adds": adds, "achieved_gops": round(adds / dom_us / 1e3, 1), "peak_gops": atom["gops"],
                                           "peak_source": atom["probe"], "time_us": round(adds / atom["gops"] / 1e3, 3),
                                           "frac": round(adds / atom["gops"] / 1e3 / dom_us, 4)}
+        if atom32 is not None:  # why the accumulator is f64: the same adds at the f32 instruction's rate
+            line["roofline"]["lds_atomic"]["f32_gops"] = atom32["gops"]
+            line["roofline"]["lds_atomic"]["f32_source"] = atom32["probe"]
+            line["roofline"]["lds_atomic"]["f32_time_us"] = round(adds / atom32["gops"] / 1e3, 3)
     print(json.dumps(line), flush=True)
 
 

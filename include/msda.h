@@ -119,8 +119,9 @@ int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_qu
  *   grad_attention_weights  [batch, len_query, n_heads, n_levels*n_points]     f32
  * Replaces the JAX autodiff VJP of ops.py:64-134/289 and deform_pallas.py:157-175 (_sample_bwd).
  * Any of the three gradient pointers may be NULL to skip that gradient. grad_output has
- * grad_output_dtype (the forward's output dtype). grad_value is accumulated in LDS in f64 (every
- * product a * w * g of f32 values is exact); a workgroup owns a (slice, level band) and writes its
+ * grad_output_dtype (the forward's output dtype). grad_value is accumulated in LDS in f64 (a * w of
+ * two f32 values is exact in f64, its product with g is rounded to f64's 53 bits); a workgroup owns
+ * a (slice, level band) and writes its
  * rows once, rounded to value_dtype, or, when a level's queries are split over several
  * workgroups, writes f32 partial rows into the workspace that a second kernel adds in block order.
  * workspace must hold msda_bwd_workspace_size() bytes (16-byte aligned); it may be NULL when that

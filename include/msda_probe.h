@@ -38,6 +38,15 @@ int msda_probe_lds_atomic(double* out, int blocks, int reps, void* stream);
 /* Lane additions the atomic probe performs for (blocks, reps): blocks * 256 * reps * 16. */
 int64_t msda_probe_lds_atomic_ops(int blocks, int reps);
 
+/*
+ * LDS f32 atomic-add rate: as msda_probe_lds_atomic with 32-bit floats (ds_add_f32 through an LDS
+ * pointer; each wave instruction on 64 consecutive floats); writes blocks * 256 floats to `out`
+ * (they total 256 * 16 * reps per workgroup, exact in f32 while that is below 2^24). The lane
+ * additions are msda_probe_lds_atomic_ops(blocks, reps). Returns 0, -1 on a bad argument, -3 on a
+ * launch failure.
+ */
+int msda_probe_lds_atomic_f32(float* out, int blocks, int reps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -145,6 +145,42 @@ int lpq_shift_for(int dim, int vec) {
 // ------------------------------------------------------------------------------------------
 // per-device attributes (one-time, idempotent initialisation)
 
+// The scratch of msda_bwd_noalloc: a file-scope device array (each GPU the library runs on holds
+// its own copy until the process ends). Host code never uses the array's name as an address (on
+// the host it is only a stand-in for the symbol): its device address is looked up with
+// hipGetSymbolAddress once per device, with that device current, when the library first reads the
+// device's attributes (the first call of any entry point on it; a caller that captures
+// msda_bwd_noalloc into a graph has normally made a call before, outside the capture), and kept here.
+// 16 MiB: the nano group-DETR backward (batch 8, 16 heads, one 24x24 level, 3900 queries) needs
+// 9.4 MiB of partial sums; query blocks exist only while the grid is short of one resident wave of
+// workgroups, so most shapes need less or none. Shapes that need more are refused.
+constexpr int64_t kNoAllocScratchBytes = int64_t{16} << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+int resolve_scratch(int dev) {
+  if (g_scratch_ptr[dev].load(std::memory_order_acquire) != nullptr) return MSDA_OK;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || ptr == nullptr) {
+    (void)hipGetLastError();
+    return fail(MSDA_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+  }
+  g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+  return MSDA_OK;
+}
+
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MSDA_ERR_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MSDA_ERR_DEVICE, "device index %d out of range", dev);
+  const int rc = resolve_scratch(dev);  // normally done already by device_info
+  if (rc != MSDA_OK) return rc;
+  *out = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  return MSDA_OK;
+}
+
 struct DevInfo {
   int lds_bytes;
   int cus;
@@ -165,6 +201,8 @@ int device_info(DevInfo* info) {
     if (e != hipSuccess) return fail(MSDA_ERR_DEVICE, "hipDeviceGetAttribute(LDS): %s", hipGetErrorString(e));
     e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return fail(MSDA_ERR_DEVICE, "hipDeviceGetAttribute(CUs): %s", hipGetErrorString(e));
+    // msda_bwd_noalloc's scratch address (a failure is reported by that entry point)
+    if (resolve_scratch(dev) != MSDA_OK) g_last_error.clear();
     g_dev_lds[dev].store(lds, std::memory_order_relaxed);
     g_dev_cus[dev].store(cus, std::memory_order_relaxed);
   }
@@ -906,27 +944,34 @@ int64_t workspace_impl(int batch, int n_heads, int head_dim, int len_query, int 
   if (batch == 0 || len_query == 0) return 0;
   DevInfo dev;
   if ((rc = device_info(&dev)) != MSDA_OK) return rc;
-  if (ref_dim == 0) {
-    // the query blocks' partial sums; the plan depends on the value dtype, which the query does not
-    // name, so the larger of the two; and either kernel may run (the sorted gather needs aligned
-    // rows), so the larger of the two kernels' needs
-    int64_t need = 0;
-    for (int vbytes : {2, 4}) {
-      BandPlan bp;
-      if ((rc = plan_band(s, vbytes, 16, dev, &bp)) != MSDA_OK) return rc;
-      need = std::max(need, band_workspace(s, bp));
-      GatherPlan gp;
-      if (gather_eligible(s) && plan_gather(s, vbytes, dev, &gp) == MSDA_OK) need = std::max(need, gather_workspace(s, gp));
-    }
-    g_last_error.clear();
-    return need;
-  }
+  // The plan depends on the value dtype, which the query does not name: the larger need of the
+  // dtypes whose plan fits (a wide level can fit the LDS in bf16 but not in f32); an error only if
+  // neither fits. For the core op either backward kernel may run (the sorted gather needs aligned
+  // rows), so also the larger of the two kernels' needs.
   int64_t need = 0;
+  int planned = 0, err = MSDA_OK;
+  std::string msg;
   for (int vbytes : {2, 4}) {
     BandPlan bp;
-    if ((rc = plan_band(s, vbytes, 16, dev, &bp)) != MSDA_OK) return rc;
-    need = std::max(need, fused_layout(s, band_workspace(s, bp)).total);
+    if ((rc = plan_band(s, vbytes, 16, dev, &bp)) != MSDA_OK) {
+      err = rc;
+      msg = g_last_error;
+      continue;
+    }
+    ++planned;
+    if (ref_dim != 0) {
+      need = std::max(need, fused_layout(s, band_workspace(s, bp)).total);
+      continue;
+    }
+    need = std::max(need, band_workspace(s, bp));
+    GatherPlan gp;
+    if (gather_eligible(s) && plan_gather(s, vbytes, dev, &gp) == MSDA_OK) need = std::max(need, gather_workspace(s, gp));
   }
+  if (planned == 0) {
+    g_last_error = msg;
+    return err;
+  }
+  g_last_error.clear();
   return need;
 }
 
@@ -985,33 +1030,6 @@ int bwd_impl(const void* value, int value_dtype, const float* loc, const float* 
   g_last_error.clear();
   return bwd_band_impl(s, ch, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn,
                        workspace, workspace_bytes, dev, st);
-}
-
-// The scratch of msda_bwd_noalloc: a file-scope device array (each GPU the library runs on holds
-// its own copy until the process ends). Host code never uses the array's name as an address (on
-// the host it is only a stand-in for the symbol): its device address is looked up once per device
-// with hipGetSymbolAddress, with that device current, and kept here.
-// 16 MiB: the nano group-DETR backward (batch 8, 16 heads, one 24x24 level, 3900 queries) needs
-// 9.4 MiB of partial sums; query blocks exist only while the grid is short of one resident wave of
-// workgroups, so most shapes need less or none. Shapes that need more are refused.
-constexpr int64_t kNoAllocScratchBytes = int64_t{16} << 20;
-static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
-std::atomic<void*> g_scratch_ptr[kMaxDevices];
-
-int noalloc_scratch(void** out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(MSDA_ERR_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
-  if (dev < 0 || dev >= kMaxDevices) return fail(MSDA_ERR_DEVICE, "device index %d out of range", dev);
-  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
-  if (ptr == nullptr) {
-    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || ptr == nullptr)
-      return fail(MSDA_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
-  }
-  *out = ptr;
-  return MSDA_OK;
 }
 
 }  // namespace

@@ -24,17 +24,19 @@
 //     LDS counter, and a lane loads its next item's inputs before working on the current one. Per
 //     point, the band that holds its clipped floor row computes the corner dots from the staged rows
 //     and writes grad_attention_weights and grad_sampling_locations; every band its corner rows meet
-//     adds a*w_c*g for its corners into the accumulator with ds_add_f64 (exact products of f32
-//     values, summed in f64).
+//     adds a*w_c*g for its corners into the accumulator with ds_add_f64 (a*w_c is exact in f64;
+//     its product with g is rounded to f64, and the sum is kept in f64).
 //  4. Round the accumulator once to the value dtype and write the band's grad_value rows (or the
 //     block's f32 partial rows).
 //
-// Measured on MI355X (per CU, 64-lane instructions): ds_add_f64 ~9.3 cycles and ds_add_u64
-// ~7.2 when the 64 lanes hit 64 distinct 8-byte bank pairs, but ds_add_f32 ~189 cycles (also with
-// f32 denormals flushed) and ds_pk_add_f16 ~189. Lane i of a sample-lane layout therefore adds
-// channel (t + r_i) mod 16 in instruction t, r_i = i mod 16: the lanes of one instruction then
-// cover all 32 bank pairs of a 256-byte bank row twice (the same channel for every lane costs
-// 63.5 cycles, a rotation by 16-byte chunks only 32.8).
+// Measured on MI355X (per CU, 64-lane wave instructions, each written as the instruction): ds_add_f64
+// 9.1 cycles with the 64 lanes on 64 consecutive doubles and 9.4 on random 16-double cells with
+// rotated channels (17.1 on 8-double cells); ds_add_u64 7.0, ds_add_u32 5.0; but ds_add_f32,
+// ds_add_rtn_f32 and ds_pk_add_bf16 193 cycles whatever the addresses, consecutive ones included
+// (also with f32 denormals flushed). The accumulator is therefore f64 with 16-channel cells. Lane i
+// of a sample-lane layout adds channel (t + r_i) mod 16 in instruction t, r_i = i mod 16: the lanes
+// of one instruction then cover all 32 bank pairs of a 256-byte bank row twice (the same channel
+// for every lane costs 63.5 cycles, a rotation by 16-byte chunks only 32.8).
 #pragma once
 
 #include "msda_kernels.h"
@@ -172,8 +174,9 @@ __device__ __forceinline__ void band_dots(const VT* rows, const Bilinear& c, int
   d11 = row_dot<VT, CH>(rows + (c.o11 - rel), g);
 }
 
-// The sample's grad_value contributions of the corners in rows [r0, r1): (a * w_c) * g, the
-// product formed exactly (f32 factors, f64 product) and added in f64, one atomic per channel.
+// The sample's grad_value contributions of the corners in rows [r0, r1): (a * w_c) * g in f64
+// (a * w_c of two f32 values is exact, 48 significant bits; its product with g, up to 72, is
+// rounded to f64's 53) and added in f64, one atomic per channel.
 // `gr` holds the lane's channels rotated by `rr` places (gr[t] = channel (t + rr) mod CH), so
 // instruction t of the lanes of a wave adds distinct channel slots. KD: head_dim when known at
 // compile time (the accumulator cell size is then an immediate offset), else 0.

@@ -1,4 +1,4 @@
-// probe_abi.hip — LDS probes of the device (read bandwidth, f64 atomic-add rate), for the
+// probe_abi.hip — LDS probes of the device (read bandwidth, f64 and f32 atomic-add rates), for the
 // benchmark's LDS rooflines.
 //
 // Every wave of every workgroup streams 16-byte LDS reads (ds_read_b128: the 64 lanes of a wave
@@ -73,7 +73,35 @@ __global__ void __launch_bounds__(kProbeThreads) lds_atomic_probe_kernel(double*
   out[blockIdx.x * kProbeThreads + threadIdx.x] = sum;
 }
 
+// The same with 32-bit floats (ds_add_f32 through an explicit LDS pointer, the instruction the
+// compiler emits for atomicAdd on __shared__ floats): instruction u of a wave adds 1.0f to the 64
+// consecutive floats [64 u, 64 u + 64) of the wave's 4 KB region (every bank once). Measured on
+// MI355X this instruction is about 20 times slower than ds_add_f64 whatever the addresses, which is
+// why grad_value accumulates in f64.
+__global__ void __launch_bounds__(kProbeThreads) lds_atomic_f32_probe_kernel(float* out, int reps) {
+  __shared__ __align__(16) float acc[kProbeThreads * kAtomicUnroll];  // 16 KB
+  for (int i = threadIdx.x; i < kProbeThreads * kAtomicUnroll; i += kProbeThreads) acc[i] = 0.0f;
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __attribute__((address_space(3))) float* region = (__attribute__((address_space(3))) float*)(acc) + wave * 64 * kAtomicUnroll + lane;
+  for (int r = 0; r < reps; ++r) {
+#pragma unroll
+    for (int u = 0; u < kAtomicUnroll; ++u) __hip_atomic_fetch_add(region + 64 * u, 1.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __syncthreads();
+  const float* mine = acc + threadIdx.x * kAtomicUnroll;
+  float sum = 0.0f;
+  for (int i = 0; i < kAtomicUnroll; ++i) sum += mine[i];
+  out[blockIdx.x * kProbeThreads + threadIdx.x] = sum;
+}
+
 }  // namespace
+
+extern "C" int msda_probe_lds_atomic_f32(float* out, int blocks, int reps, void* stream) {
+  if (out == nullptr || blocks < 1 || reps < 1) return -1;
+  hipLaunchKernelGGL(lds_atomic_f32_probe_kernel, dim3(blocks), dim3(kProbeThreads), 0, static_cast<hipStream_t>(stream), out, reps);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
 
 extern "C" int msda_probe_lds_atomic(double* out, int blocks, int reps, void* stream) {
   if (out == nullptr || blocks < 1 || reps < 1) return -1;

@@ -50,6 +50,7 @@ SIGNATURES = {
     "msda_probe_lds_read": ([_P, _I, _I, _P], _I),
     "msda_probe_lds_read_bytes": ([_I, _I], _I64),
     "msda_probe_lds_atomic": ([_P, _I, _I, _P], _I),
+    "msda_probe_lds_atomic_f32": ([_P, _I, _I, _P], _I),
     "msda_probe_lds_atomic_ops": ([_I, _I], _I64),
 }
 

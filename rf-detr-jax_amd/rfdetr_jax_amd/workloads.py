@@ -65,12 +65,13 @@ class Workload:
     def lds_bytes(self) -> dict:
         """Algorithmic LDS bytes: the forward reads four corner rows per sample and stages each value
         slice once; the backward reads the corner rows, accumulates four grad_value rows per sample
-        (f32), stages the value slices and flushes the grad_value slices."""
+        into an f64 accumulator (8 bytes per channel addition: ds_add_f64), stages the value slices,
+        zeroes the accumulator and reads it back once at write-out (8 bytes per element each)."""
         sv = 2 if self.value_dtype == "bf16" else 4
         slices = self.batch * self.heads * self.len_value * self.head_dim
         corners = self.samples * 4 * self.head_dim
         fwd = corners * sv + slices * sv
-        bwd = corners * sv + corners * 4 + slices * sv + slices * 4 if self.backward else 0
+        bwd = corners * sv + corners * 8 + slices * sv + slices * 8 * 2 if self.backward else 0
         return {"fwd": fwd, "bwd": bwd, "total": fwd + bwd}
 
     def lds_atomic_adds(self) -> int:

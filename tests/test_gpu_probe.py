@@ -27,6 +27,18 @@ def test_lds_atomic_probe_sums():
     assert lib.msda_probe_lds_atomic(None, blocks, reps, None) == -1
 
 
+def test_lds_atomic_f32_probe_sums():
+    """The f32 probe's accumulators: one 1.0f per repetition each, so 16 * reps per thread (exact)."""
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    lib = _native.lib()
+    blocks, reps = 5, 3
+    out = torch.full((blocks * 256,), -1.0, dtype=torch.float32, device="cuda:0")
+    assert lib.msda_probe_lds_atomic_f32(ctypes.c_void_p(out.data_ptr()), blocks, reps, None) == 0
+    torch.cuda.synchronize()
+    assert torch.all(out == 16.0 * reps)
+    assert lib.msda_probe_lds_atomic_f32(None, blocks, reps, None) == -1
+
+
 def test_lds_read_probe_runs():
     """The read probe fills its output (one word per thread) and reports 8 KB per thread-repetition
     group as documented."""

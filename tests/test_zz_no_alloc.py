@@ -53,6 +53,44 @@ def _case(seed, batch, heads, queries, shapes, points):
     return [torch.from_numpy(np.ascontiguousarray(x)).to(d) for x in (value, loc, attn, grad)]
 
 
+def test_noalloc_first_call_captured_in_a_graph():
+    """The process's first msda_bwd_noalloc call (this test runs first in this file) is made under
+    graph capture: the scratch array's address was looked up when the library first used the
+    device (the reference call below), so the captured call only launches. Every replay, with
+    eager work and a synchronisation between replays, matches msda_bwd."""
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    shapes = ((24, 24),)
+    v, lc, a, g = _case(21, 2, 8, 3900, shapes, 2)
+    want = hip.ms_deform_attn_backward(v, shapes, lc, a, g)
+    torch.cuda.synchronize()
+    lib = _native.lib()
+    arr, starts = hip._shape_arrays(hip._as_shapes(shapes))
+    dims = (2, 8, 16, 3900, 1, 2, arr, starts, 576)
+    assert lib.msda_bwd_workspace_size(*dims) > 0, "the case must need partial sums"
+    gv, gl, ga = torch.empty_like(v), torch.empty_like(lc), torch.empty_like(a)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = lib.msda_bwd_noalloc(
+                hip._ptr(v), hip._VALUE_DTYPES[v.dtype], hip._ptr(lc), hip._ptr(a), hip._ptr(g),
+                hip._VALUE_DTYPES[g.dtype], hip._ptr(gv), hip._ptr(gl), hip._ptr(ga), *dims, hip._stream(v.device),
+            )
+    _native.check(rc)
+    other = torch.zeros(1 << 20, device=v.device)
+    for rep in range(3):
+        gv.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        _note(f"noalloc graph replay {rep}")
+        assert torch.equal(gl, want[1]), "grad_sampling_locations differs"
+        assert torch.equal(ga, want[2]), "grad_attention_weights differs"
+        assert_close(gv.cpu().numpy(), want[0].cpu().numpy(), 1e-5, "grad_value")
+        other.add_(1.0)
+        torch.cuda.synchronize()
+
+
 def test_noalloc_matches_workspace_entry_point_twice():
     assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
     cases = [(11, 2, 8, 3900, ((24, 24),), 2), (12, 1, 4, 1500, ((24, 24), (12, 12)), 2)]
