@@ -446,14 +446,21 @@ constexpr int query_group(int ns, int vec, bool fused = false) {
 // points and box offsets make the chunk half as long, within the same register budget.
 constexpr int pass_batch(bool fused) { return fused ? 2 : kPassBatch; }
 
+// own >= 0 (fwd_pair): only sample `own` of each query is loaded, into slot 0 (the lane computes
+// that sample's coordinates and receives the other's from its partner lane).
 template <int NS, int QU>
 __device__ __forceinline__ void load_group(SampleIn<NS> (&in)[QU], const float2* __restrict__ loc2, const float* __restrict__ attn,
-                                           int64_t row0, int64_t row_step, int q0, int q_step, int q_hi, int LP) {
+                                           int64_t row0, int64_t row_step, int q0, int q_step, int q_hi, int LP, int own = -1) {
 #pragma unroll
   for (int i = 0; i < QU; ++i) {
     if (q0 + i * q_step < q_hi) {
       const int64_t row = row0 + i * row_step;
-      load_in<NS>(in[i], loc2 + row * LP, attn + row * LP, 0, LP);
+      if (own >= 0) {
+        in[i].xy[0] = loc2[row * LP + own];
+        in[i].a[0] = attn[row * LP + own];
+      } else {
+        load_in<NS>(in[i], loc2 + row * LP, attn + row * LP, 0, LP);
+      }
     }
   }
 }
@@ -639,15 +646,17 @@ __device__ __forceinline__ void fwd_pass(float (&acc)[VEC], const SampleIn<N>& f
 }
 
 // One level, two points, two lanes per (query, head) (pair_share): lane j computes the corner
-// offsets and weights of sample j only and the two lanes exchange them, so each sample's
-// coordinates are computed once; each lane then adds its own sample first (the order of the two
-// f32 additions per channel is the only difference from fwd_pass).
+// offsets and weights of sample j only (in slot `slot` of f: 0 when the lane loaded its own sample
+// only, j when both are in registers, as after the fused prologue's softmax) and the two lanes
+// exchange them, so each sample's coordinates are computed once; each lane then adds its own
+// sample first (the order of the two f32 additions per channel is the only difference from
+// fwd_pass).
 template <typename VT, int VEC>
 __device__ __forceinline__ void fwd_pair(float (&acc)[VEC], const SampleIn<2>& f, const SampleParams& p, const VT* hlds,
-                                         int rot, int j) {
+                                         int rot, int slot) {
   const LevelDesc L = p.lv[0];
-  const float2 xy = j ? f.xy[1] : f.xy[0];
-  const float a = j ? f.a[1] : f.a[0];
+  const float2 xy = slot ? f.xy[1] : f.xy[0];
+  const float a = slot ? f.a[1] : f.a[0];
   const Bilinear c = bilinear(xy.x, xy.y, L, p.dim);
   // lane swap with the neighbour: DPP quad_perm [1, 0, 3, 2] (a register move, no LDS traffic)
   auto swap_i = [](int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); };
@@ -705,9 +714,11 @@ fwd_kernel(const SampleParams p) {
     }
   };
   // The first group's inputs are requested before the staging copy, so their latency overlaps it.
+  // fwd_pair lanes load their own sample only
+  const int own = (NS == 2 && kStaged && !kFused && p.pair_share) ? ln.j : -1;
   if constexpr (NS > 0)
     if (ln.active) {
-      load_group<NS, QU>(in, loc2, p.attn, row_first, row_step, q_first, ln.qpp, q_hi, LP);
+      load_group<NS, QU>(in, loc2, p.attn, row_first, row_step, q_first, ln.qpp, q_hi, LP, own);
       load_refs_group(q_first);
     }
   stage_group(p, lds, vg);
@@ -720,7 +731,7 @@ fwd_kernel(const SampleParams p) {
     for (int qg = q_first; qg < q_hi; qg += QU * ln.qpp) {
       const int64_t row0 = row_first + static_cast<int64_t>((qg - q_first) / ln.qpp) * row_step;
       if (qg != q_first) {
-        load_group<NS, QU>(in, loc2, p.attn, row0, row_step, qg, ln.qpp, q_hi, LP);
+        load_group<NS, QU>(in, loc2, p.attn, row0, row_step, qg, ln.qpp, q_hi, LP, own);
         load_refs_group(qg);
       }
       wait_vmem();
@@ -738,7 +749,7 @@ fwd_kernel(const SampleParams p) {
           for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
           if constexpr (NS == 2 && kStaged) {
             if (p.pair_share) {
-              fwd_pair<VT, VEC>(acc, in[i], p, hlds, rot, ln.j);
+              fwd_pair<VT, VEC>(acc, in[i], p, hlds, rot, kFused ? ln.j : 0);
               if (ln.lane_on) store_any_rot<VT, VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, rot, acc);
               continue;
             }
