@@ -915,7 +915,23 @@ int fused_bwd_impl(const Shape& s, int ch, const void* value, int value_dtype, c
     fp.fh[l] = static_cast<float>(s.h[l]);
   }
   const int64_t rows = fp.bq_total * s.heads;
-  hipLaunchKernelGGL(msda::fused_prologue_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256), 0, st, fp);
+  // Rows of at most 32 samples over at most 4 levels, a (b, q) group of heads x samples within 256
+  // threads and fewer than 2^31 samples: the kernels with one thread per sample.
+  const int lp = s.levels * s.points;
+  const int64_t nsamp = rows * lp;
+  const int nb = (s.levels <= 4 && lp <= 32 && s.heads * lp <= 256 && nsamp < (int64_t{1} << 31) &&
+                  env_int("MSDA_FUSED_PER_SAMPLE", 1) != 0)
+                     ? (lp <= 8 ? 8 : lp <= 16 ? 16 : 32)
+                     : 0;
+  const dim3 pgrid(static_cast<unsigned>((nsamp + 255) / 256));
+  if (nb == 8)
+    hipLaunchKernelGGL(msda::fused_prologue_samples_kernel<8>, pgrid, dim3(256), 0, st, fp);
+  else if (nb == 16)
+    hipLaunchKernelGGL(msda::fused_prologue_samples_kernel<16>, pgrid, dim3(256), 0, st, fp);
+  else if (nb == 32)
+    hipLaunchKernelGGL(msda::fused_prologue_samples_kernel<32>, pgrid, dim3(256), 0, st, fp);
+  else
+    hipLaunchKernelGGL(msda::fused_prologue_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256), 0, st, fp);
   if ((rc = msda_host::check_launch("msda fused backward (prologue)")) != MSDA_OK) return rc;
   float* dloc = grad_offsets != nullptr ? grad_offsets : (fz.dref != nullptr ? reinterpret_cast<float*>(ws + lay.dloc) : nullptr);
   rc = bwd_band_impl(s, ch, value, value_dtype, fp.loc, fp.attn, grad_output, grad_output_dtype, grad_value, dloc, grad_logits,
@@ -929,8 +945,20 @@ int fused_bwd_impl(const Shape& s, int ch, const void* value, int value_dtype, c
   int hp_shift = 0;
   while ((1 << hp_shift) < s.heads) ++hp_shift;
   const int64_t per_block = 256 >> hp_shift;
-  hipLaunchKernelGGL(msda::fused_epilogue_kernel, dim3(static_cast<unsigned>((fp.bq_total + per_block - 1) / per_block)), dim3(256),
-                     0, st, fp, hp_shift);
+  if (nb != 0) {
+    const int G = 256 / (s.heads * lp), hp = 1 << hp_shift;
+    const dim3 sgrid(static_cast<unsigned>((fp.bq_total + G - 1) / G));
+    const size_t lds = static_cast<size_t>(G) * (s.heads * lp + s.levels * hp) * sizeof(float4);
+    if (nb == 8)
+      hipLaunchKernelGGL(msda::fused_epilogue_samples_kernel<8>, sgrid, dim3(256), lds, st, fp, G, hp);
+    else if (nb == 16)
+      hipLaunchKernelGGL(msda::fused_epilogue_samples_kernel<16>, sgrid, dim3(256), lds, st, fp, G, hp);
+    else
+      hipLaunchKernelGGL(msda::fused_epilogue_samples_kernel<32>, sgrid, dim3(256), lds, st, fp, G, hp);
+  } else {
+    hipLaunchKernelGGL(msda::fused_epilogue_kernel, dim3(static_cast<unsigned>((fp.bq_total + per_block - 1) / per_block)),
+                       dim3(256), 0, st, fp, hp_shift);
+  }
   return msda_host::check_launch("msda fused backward (epilogue)");
 }
 

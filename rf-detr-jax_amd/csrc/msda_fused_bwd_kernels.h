@@ -112,6 +112,154 @@ __global__ void __launch_bounds__(256) fused_epilogue_kernel(const FusedRowParam
   }
 }
 
+// The same two steps with one thread per sample (b, q, h, k), for rows of at most NB samples over at
+// most four levels (every RF-DETR shape) and fewer than 2^31 samples. A row's lanes load its logits
+// (one broadcast address per row), each lane its own offset, location gradient and reference point:
+// loads and stores are contiguous runs, and there are LP times as many threads to hide latency as
+// the row kernels above have. The arithmetic and its order are those of the row kernels.
+__device__ __forceinline__ float level_pick(int l, const float (&a)[kMaxLevels]) {
+  return l == 0 ? a[0] : l == 1 ? a[1] : l == 2 ? a[2] : a[3];
+}
+
+template <int NB>
+__device__ __forceinline__ SoftmaxStats row_stats(const float (&x)[NB], int LP) {
+  SoftmaxStats st{-__builtin_inff(), 0.0f};
+#pragma unroll
+  for (int u = 0; u < NB; ++u)
+    if (u < LP) st.m = fmaxf(st.m, x[u]);
+#pragma unroll
+  for (int u = 0; u < NB; ++u)
+    if (u < LP) st.s += expf(x[u] - st.m);
+  return st;
+}
+
+template <int NB>
+__global__ void __launch_bounds__(256) fused_prologue_samples_kernel(const FusedRowParams p) {
+  const uint32_t LP = static_cast<uint32_t>(p.levels * p.points);
+  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;  // (b, q, h, k)
+  if (idx >= static_cast<uint32_t>(p.bq_total * p.heads) * LP) return;
+  const uint32_t row = idx / LP, k = idx - row * LP;
+  const int l = static_cast<int>(k) / p.points;
+  const uint32_t bq = row / static_cast<uint32_t>(p.heads);
+  const float* __restrict__ lg = p.logits + static_cast<size_t>(row) * LP;
+  float x[NB];
+#pragma unroll
+  for (int u = 0; u < NB; ++u)
+    if (u < static_cast<int>(LP)) x[u] = lg[u];
+  const float xk = lg[k];
+  const float2 o = reinterpret_cast<const float2*>(p.off)[idx];
+  const float4 r = fused_row_ref(p, bq, l);
+  const SoftmaxStats st = row_stats<NB>(x, LP);
+  float2 t;
+  reinterpret_cast<float2*>(p.loc)[idx] =
+      fused_location_at(o, r, t, level_pick(l, p.fw), level_pick(l, p.fh), p.ref_dim, p.inv_points, p.fpoints);
+  p.attn[idx] = softmax_weight(xk, st);
+}
+
+// 256 threads hold G whole (b, q) groups of heads x LP samples (G = 256 / (heads * LP) >= 1). The
+// softmax VJP is in place on grad_attention_logits: every thread's loads precede the barrier before
+// any store. The reference-point gradient goes through LDS: each sample's share, then per (group,
+// level, head) the shares of the level's points in order, then per (group, level) the heads by the
+// pairwise tree of the row kernel's xor shuffles over hp >= heads lanes (lane i + lane i + s at
+// stride s, the missing heads zero), so the sums are the row kernel's, bit for bit.
+// LDS: (G * heads * LP + G * levels * hp) float4.
+template <int NB>
+__global__ void __launch_bounds__(256) fused_epilogue_samples_kernel(const FusedRowParams p, int G, int hp) {
+  extern __shared__ float4 cbuf[];
+  const int LP = p.levels * p.points, H = p.heads, per_bq = H * LP;
+  const int t = threadIdx.x;
+  const int g = t / per_bq, rem = t - g * per_bq, h = rem / LP, k = rem - h * LP, l = k / p.points;
+  const uint32_t bq = blockIdx.x * static_cast<uint32_t>(G) + static_cast<uint32_t>(g);
+  const bool on = g < G && bq < static_cast<uint32_t>(p.bq_total);
+  const uint32_t row = bq * static_cast<uint32_t>(H) + static_cast<uint32_t>(h);
+  const uint32_t idx = row * static_cast<uint32_t>(LP) + static_cast<uint32_t>(k);
+  const bool want_dl = p.dlogits != nullptr, want_loc = p.dloc != nullptr;  // uniform
+  float x[NB], d[NB];
+  float xk = 0.0f, dk = 0.0f;
+  float2 gl = make_float2(0.0f, 0.0f), o = make_float2(0.0f, 0.0f);
+  float4 ref = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (on) {
+    if (want_dl) {
+      const float* __restrict__ lg = p.logits + static_cast<size_t>(row) * LP;
+      const float* __restrict__ dl = p.dlogits + static_cast<size_t>(row) * LP;
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        if (u < LP) {
+          x[u] = lg[u];
+          d[u] = dl[u];
+        }
+      }
+      xk = lg[k];
+      dk = dl[k];
+    }
+    if (want_loc) {
+      gl = reinterpret_cast<const float2*>(p.dloc)[idx];
+      o = reinterpret_cast<const float2*>(p.off)[idx];
+      ref = fused_row_ref(p, bq, l);
+    }
+  }
+  wait_vmem();
+  __syncthreads();  // the rows' dA are read before any of them is overwritten
+  if (on && want_dl) {
+    const SoftmaxStats st = row_stats<NB>(x, LP);
+    float S = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+      if (u < LP) S += softmax_weight(x[u], st) * d[u];
+    p.dlogits[idx] = softmax_weight(xk, st) * (dk - S);
+  }
+  if (!want_loc) return;  // uniform
+  float r4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (on) {
+    const float fw = level_pick(l, p.fw), fh = level_pick(l, p.fh);
+    float2 tt;
+    fused_location_at(o, ref, tt, fw, fh, p.ref_dim, p.inv_points, p.fpoints);
+    const float2 go = fused_offset_grad(gl, ref, tt, fw, fh, p.ref_dim, p.inv_points, p.fpoints, r4);
+    if (p.doff != nullptr) reinterpret_cast<float2*>(p.doff)[idx] = go;
+  }
+  if (p.dref == nullptr) return;  // uniform
+  if (g < G) cbuf[t] = make_float4(r4[0], r4[1], r4[2], r4[3]);  // [g][h][k] = t
+  __syncthreads();
+  const int L = p.levels, P = p.points;
+  float4* hs = cbuf + G * per_bq;  // [G][L][hp]
+  for (int i = t; i < G * L * hp; i += 256) {
+    const int g2 = i / (L * hp), r2 = i - g2 * (L * hp), l2 = r2 / hp, h2 = r2 - l2 * hp;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (h2 < H) {
+      const float4* c = cbuf + (g2 * H + h2) * LP + l2 * P;
+      for (int pt = 0; pt < P; ++pt) {
+        v.x += c[pt].x;
+        v.y += c[pt].y;
+        v.z += c[pt].z;
+        v.w += c[pt].w;
+      }
+    }
+    hs[i] = v;
+  }
+  __syncthreads();
+  for (int i = t; i < G * L; i += 256) {
+    const int g2 = i / L, l2 = i - g2 * L;
+    const uint32_t bq2 = blockIdx.x * static_cast<uint32_t>(G) + static_cast<uint32_t>(g2);
+    if (bq2 >= static_cast<uint32_t>(p.bq_total)) continue;
+    float4* v = hs + i * hp;
+    for (int sh = 1; sh < hp; sh <<= 1) {
+      for (int j = 0; j < hp; j += 2 * sh) {
+        v[j].x += v[j + sh].x;
+        v[j].y += v[j + sh].y;
+        v[j].z += v[j + sh].z;
+        v[j].w += v[j + sh].w;
+      }
+    }
+    float* dd = p.dref + (static_cast<size_t>(bq2) * L + l2) * p.ref_dim;
+    dd[0] = v[0].x;
+    dd[1] = v[0].y;
+    if (p.ref_dim == 4) {
+      dd[2] = v[0].z;
+      dd[3] = v[0].w;
+    }
+  }
+}
+
 // The reference-point gradient of the band kernel's fused epilogue when no part-sum kernel runs:
 // the per-head partials added in head order (ref_head_sum).
 __global__ void __launch_bounds__(256) ref_head_sum_kernel(const float* part, float* dref, int heads, int64_t n) {

@@ -592,9 +592,12 @@ __device__ __forceinline__ void fused_prologue_row(SampleIn<N>& f, FusedIn<N, tr
 }
 
 // The transpose of fused_location_at for one sample: the offset gradient, and the sample's share of
-// the reference-point gradient added into r (x, y, and w, h for boxes).
+// the reference-point gradient added into r (x, y, and w, h for boxes). Nothing is contracted: each
+// product is rounded before it is added, so a sum over points comes out the same whether it is kept
+// in r across the points or formed from the shares afterwards.
 __device__ __forceinline__ float2 fused_offset_grad(float2 gl, float4 ref, float2 t, float fw, float fh, int ref_dim,
                                                     float inv_points, float fpoints, float (&r)[4]) {
+#pragma clang fp contract(off)
   r[0] += gl.x;
   r[1] += gl.y;
   if (ref_dim == 2) return make_float2(gl.x / fw, gl.y / fh);

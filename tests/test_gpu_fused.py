@@ -161,6 +161,45 @@ def test_fused_in_kernel_and_row_paths_agree(tune, points, ref_dim, bf16):
         assert_close(a, b, 1e-5, name)
 
 
+ROW_CASES = {
+    # 9 samples per row (3 levels x 3 points): the 16-sample kernels; 6 heads: four (b, q) groups of
+    # 54 threads per workgroup, and 8 lanes in the head tree with two of them zero
+    "l3_p3_h6": dict(shapes=((12, 12), (6, 6), (3, 3)), heads=6, dim=16, points=3, queries=70),
+    # 32 samples per row (4 levels x 8 points), two (b, q) groups per workgroup
+    "l4_p8": dict(shapes=((16, 16), (8, 8), (4, 4), (2, 2)), heads=4, dim=16, points=8, queries=50),
+    # 16 heads x 16 samples: one (b, q) group fills the workgroup
+    "l4_p4_h16": dict(shapes=((16, 16), (8, 8), (4, 4), (2, 2)), heads=16, dim=16, points=4, queries=40),
+    # 16 heads x 32 samples (512 threads per group) and 5 levels: past the per-sample kernels'
+    # bounds, so the per-row kernels run either way
+    "l4_p8_h16": dict(shapes=((16, 16), (8, 8), (4, 4), (2, 2)), heads=16, dim=16, points=8, queries=30),
+    "l5_p2": dict(shapes=((16, 16), (8, 8), (4, 4), (2, 2), (1, 1)), heads=4, dim=16, points=2, queries=50),
+}
+
+
+@pytest.mark.parametrize("ref_dim", [2, 4])
+@pytest.mark.parametrize("case", sorted(ROW_CASES))
+def test_fused_row_kernels(tune, case, ref_dim):
+    """Several levels: the prologue and epilogue run as kernels of their own around the band
+    kernel. The kernels with one thread per sample (rows of at most 32 samples over at most 4
+    levels) and those with one thread per row (MSDA_FUSED_PER_SAMPLE=0) give bit-identical
+    reference-point, offset and logit gradients (grad_value within its run-to-run bound), matching
+    the float64 oracle; some logits are masked (-inf)."""
+    c = ROW_CASES[case]
+    _note(f"fused row kernels {case} ref_dim={ref_dim}")
+    value, ref, off, logits, grad = make_fused_inputs(15, 2, c["heads"], c["dim"], c["queries"], c["shapes"], c["points"],
+                                                      ref_dim)
+    logits[:, ::4, :, 1] = -np.inf
+    out, grads = _run_fused(value, c["shapes"], ref, off, logits, grad)
+    tune({"MSDA_FUSED_PER_SAMPLE": "0"})
+    out0, grads0 = _run_fused(value, c["shapes"], ref, off, logits, grad)
+    assert np.array_equal(out, out0)
+    assert_close(grads[0], grads0[0], 1e-5, "grad_value")
+    for name, g, g0 in zip(("grad_reference_points", "grad_sampling_offsets", "grad_attention_logits"), grads[1:], grads0[1:]):
+        assert np.array_equal(g, g0), name
+    want_out, want_grads = _oracle64(value, c["shapes"], ref, off, logits, grad, c["points"])
+    _check(out, grads, want_out, want_grads, False)
+
+
 def test_fused_three_points_four_heads():
     """Four heads, three points (n_points not a power of two: the box form divides), one small
     level; the epilogue sums grad_reference_points over four head lanes."""
