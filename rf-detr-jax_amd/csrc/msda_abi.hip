@@ -395,7 +395,8 @@ int launch_partial_sums(const Shape& s, int value_dtype, const float* part, int 
   const int64_t n = static_cast<int64_t>(s.batch) * s.heads * s.len_value * s.dim;
   const int64_t quads = n / 4;
   // a resident wave of workgroups, each thread four quads per pass
-  const int grid = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((quads + 1023) / 1024, static_cast<int64_t>(dev.cus) * 8)));
+  const int64_t per_wg = std::max(64, env_int("MSDA_PART_SUM_QUADS", 256));
+  const int grid = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((quads + per_wg - 1) / per_wg, static_cast<int64_t>(dev.cus) * 8)));
   const int vec = aligned(grad_value, value_dtype == MSDA_DTYPE_BF16 ? 8 : 16) ? 1 : 0;
   const int64_t stride = part_block_stride(s);
   const int64_t nref = static_cast<int64_t>(s.batch) * s.queries * ref_dim;
