@@ -119,6 +119,30 @@ def test_fused_full_size_against_c_oracle(ref_dim):
     assert math.isclose(float(np.sum(gv.astype(np.float64) * value)), inner, rel_tol=1e-4)
 
 
+@pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "f32"])
+@pytest.mark.parametrize("ref_dim", [2, 4])
+def test_fused_config3_size_against_c_oracle(ref_dim, bf16):
+    """The benchmark's config-3 shape (B=8, Q=300, 80x80 + 20x20 levels, 16 heads x 16, 4 points;
+    bf16 value as the workload has it, and f32) with the prologue fused: several levels, so the
+    prologue and epilogue kernels run around the banded backward. Against the f32 C oracle on the
+    same (bf16-rounded) values, plus <G, out> = <dV, V>."""
+    shapes = ((80, 80), (20, 20))
+    _note(f"fused config-3 size ref_dim={ref_dim} bf16={bf16}")
+    value, ref, off, logits, grad = make_fused_inputs(3, 8, 16, 16, 300, shapes, 4, ref_dim, "bf16" if bf16 else "f32")
+    out, (gv, gref, goff, glog) = _run_fused(value, shapes, ref, off, logits, grad, bf16)
+    loc, attn = PR.prologue(ref, off, logits, shapes, 4)
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    assert_close(out, cref.forward(value, shapes, loc, attn), tf, "out")
+    cv, cl, ca = cref.backward(value, shapes, loc, attn, grad)
+    w_off, w_log, w_ref = PR.prologue_vjp(ref, off, logits, shapes, 4, cl, ca)
+    assert_close(gv, cv, tg, "grad_value")
+    assert_close(goff, w_off, tg, "grad_sampling_offsets")
+    assert_close(glog, w_log, tg, "grad_attention_logits")
+    assert_close(gref, w_ref, tg, "grad_reference_points")
+    inner = float(np.sum(out.astype(np.float64) * grad))
+    assert math.isclose(float(np.sum(gv.astype(np.float64) * value)), inner, rel_tol=1e-2 if bf16 else 1e-4)
+
+
 @pytest.mark.parametrize("variant", [
     {"MSDA_FWD_GROUPED": "0"},          # per-query forward loop
     {"MSDA_FWD_PAIR": "0"},             # grouped forward without paired lanes
