@@ -553,6 +553,13 @@ int bwd_band_impl(const Shape& s, int ch, const void* value, int value_dtype, co
   p.lps_shift = bp.lps_shift;
   p.vec16 = rows_16b(s, vbytes, value, grad_value) ? 1 : 0;
   p.lds_acc = bp.layout.acc + s.dim * 8;  // after the leading guard cell
+  // Whole levels whose block gives the waves fewer than two chunks of queries each: one item per
+  // point (with one per query, waves get one chunk of queries or none, and the phase lasts a whole
+  // chunk's chain of points).
+  p.point_items = (fa == nullptr && static_cast<int64_t>(bp.qblock) * (1 << bp.lps_shift) < 2 * static_cast<int64_t>(bp.threads) &&
+                   env_int("MSDA_BWD_POINT_ITEMS", 1) != 0)
+                      ? 1
+                      : 0;
   p.lds_list = bp.layout.list;
   p.lds_cnt = bp.layout.cnt;
   int first = 0;

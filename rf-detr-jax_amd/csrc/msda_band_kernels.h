@@ -81,6 +81,9 @@ struct BandParams {
   float inv_points, fpoints;
   float* dref_part;
   int64_t bq_total;  // B * Q
+  // whole levels: one work item per point rather than per query (fewer queries than the
+  // workgroup's lanes can take two at a time; core op only)
+  int point_items;
 };
 
 // Item k of a slice: level l (the last whose first item <= k) and band k - band_first.
@@ -578,7 +581,17 @@ __global__ void __launch_bounds__(kBandMaxThreads) bwd_band_kernel(const BandPar
   // are multiples of P, so the base pointers decide
   const bool rows16 = (reinterpret_cast<uintptr_t>(vw.loc) & 15) == 0 &&
                       (reinterpret_cast<uintptr_t>(vw.attn) & (P == 4 ? 15 : 7)) == 0;
-  if (whole && rows16 && (P == 2 || (P == 4 && CH < 16))) {
+  if (!FZ && whole && p.point_items) {
+    // 2'. every sample of the block belongs to this workgroup, and its queries are few for the
+    //     lanes: one item per point (a query's points are consecutive items), so that every wave
+    //     has items and a lane's chain of items is short
+    if (tid == 0) cnt[1] = nwaves * qpw;
+    auto locate = [&](int e) {
+      const uint32_t qo = static_cast<uint32_t>(e) / static_cast<uint32_t>(P);
+      return make_uint2(static_cast<uint32_t>(q_lo) + qo, static_cast<uint32_t>(e) - qo * static_cast<uint32_t>(P));
+    };
+    pipelined(std::integral_constant<int, 1>{}, (q_hi - q_lo) * P, locate, true);
+  } else if (whole && rows16 && (P == 2 || (P == 4 && CH < 16))) {
     // 2'. every sample of the block belongs to this workgroup: one item per query
     if (tid == 0) cnt[1] = nwaves * qpw;
     auto locate = [&](int e) { return make_uint2(static_cast<uint32_t>(q_lo + e), 0u); };
