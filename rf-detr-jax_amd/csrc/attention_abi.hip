@@ -130,6 +130,28 @@ int fwd_b(const msda::AttnParams& p, hipStream_t st) {
   return fwd_b_rb<D, MASK, 4>(p, st);
 }
 
+// Every row of tensor t starts on a 16-byte boundary (base pointer and all four strides).
+bool rows16(const void* base, const msda::AttnParams& p, int t) {
+  return aligned_to(base, 16) && p.st[t][0] % 8 == 0 && p.st[t][1] % 8 == 0 && p.st[t][2] % 8 == 0 && p.st[t][3] % 8 == 0;
+}
+
+// The bf16 forward for head_dim 32 without a mask stages the whole key and value slice in LDS
+// (MSDA_ATTN_FWD_D32=0 selects the chunked kernel).
+bool use_fwd_d32(const msda::AttnParams& p, int d) {
+  return d == 32 && p.mask == nullptr && p.len <= msda::kAtFwdD32MaxLen && rows16(p.k, p, msda::kAtK) && rows16(p.v, p, msda::kAtV) &&
+         msda_host::knob("MSDA_ATTN_FWD_D32", 1) != 0;
+}
+
+// Four query blocks per workgroup (four workgroups of four waves fill a CU's LDS). Measured at
+// 300 rows (10 blocks): five per workgroup, which idles no wave and stages a third less, took 44.8
+// against 36 us at four waves per SIMD (three workgroups per CU), and 58.6 us at five (spills).
+int fwd_d32(const msda::AttnParams& p, hipStream_t st) {
+  static std::atomic<int> granted[msda_host::kMaxDevices];
+  // dynamic: the key and value rows of chunks 1 .. (chunk 0 has static arrays)
+  const int tiles = ((p.len + msda::kAtChunk - 1) / msda::kAtChunk - 1) * msda::kAtChunk * 32 * 2 * 2;
+  return at_launch(msda::attn_fwd_bf16_d32_kernel<4>, granted, p, tiles, 4, st, "attention forward");
+}
+
 template <int D, bool MASK, int RB>
 int bwd_b_rb(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
   int rc = MSDA_OK;
@@ -183,6 +205,7 @@ bool use_fused(const msda::AttnParams& p, int d, bool want_kv) {
 int fwd_dispatch(const msda::AttnParams& p, int d, bool bf16, hipStream_t st) {
   const bool m = p.mask != nullptr;
   if (bf16) {
+    if (use_fwd_d32(p, d)) return fwd_d32(p, st);
     if (d == 32) return m ? fwd_b<32, true>(p, st) : fwd_b<32, false>(p, st);
     return m ? fwd_b<64, true>(p, st) : fwd_b<64, false>(p, st);
   }

@@ -815,6 +815,191 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
   }
 }
 
+// ---- bf16, head_dim 32, no mask (the decoder's self-attention) --------------------------------
+// The softmax's vector work bounds the kernel above (v_exp_f32 occupies two issue slots of a
+// full-rate op, the rest one each; the matrix unit idles most of the time), so this forward moves
+// what it can off the vector unit:
+//  - the scores leave the MFMA already scaled and shifted: the query row is held as
+//    q' = q log2(e) / sqrt(D) split into bf16 hi + lo (|q' - hi - lo| <= 2^-16 |q'|: two products
+//    per operand instead of one f32 multiply), and the accumulator starts from -m (16 registers),
+//    so x - m costs no vector op;
+//  - the chunk maximum takes one v_max3_f32 per two scores;
+//  - row sums add the bf16-rounded weights that enter the product with V (v_dot2_f32_bf16 against
+//    (1, 1), one per two weights), each half-wave keeping its own sum until the end: the output is
+//    sum(bf16(P) v) / sum(bf16(P)), and the statistics hold that sum;
+//  - the whole key and value slice is staged in LDS once (global_load_lds_dwordx4 into swizzled
+//    [Lp][32] tiles, Lp = L rounded up to 64; rows past L are copies of row L - 1 whose scores are
+//    set to -inf), chunk 0 first: the later chunks land while chunk 0 is processed, and the key
+//    loop has one barrier and no staging code.
+// The host routes here only 16-byte aligned key and value rows with L <= kAtFwdD32MaxLen.
+constexpr int kAtFwdD32MaxLen = 512;
+
+__device__ __forceinline__ float at_max3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
+// sum of the eight bf16 weights of w, as v_dot2_f32_bf16 against (1, 1) added to acc
+__device__ __forceinline__ float at_sum_bf8(const at_bf8& w, float acc) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  const bf2 one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w, w, 0, 1), one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w, w, 2, 3), one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w, w, 4, 5), one, acc, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w, w, 6, 7), one, acc, false);
+}
+
+// Stores a 32 x 32 result block v * scale (lane l: row r0 + l % 32, channels 8 c + 4 (l / 32) + e in
+// register 4 c + e) as bf16 rows of dst (row stride rs elements, rows past L skipped) straight from
+// the result layout: four 8-byte pieces per lane when dst and rs allow, element by element
+// otherwise (the same rounding as at_store_block, without its LDS round trip and barrier).
+__device__ __forceinline__ void at_store_block_direct(bf16_t* dst, int64_t rs, int r0, int L, const at_f16& v, float scale, int lane) {
+  const int col = lane & 31, grp = lane >> 5;
+  if (r0 + col >= L) return;
+  if ((reinterpret_cast<uintptr_t>(dst) & 7) != 0 || (rs & 3) != 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) at_st1<bf16_t>(dst, at_row_off(r0 + col, rs) + 8 * (i >> 2) + 4 * grp + (i & 3), v[i] * scale);
+    return;
+  }
+  uint16_t* row = reinterpret_cast<uint16_t*>(dst) + at_row_off(r0 + col, rs) + 4 * grp;
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const uint4 u = __builtin_bit_cast(uint4, at_bf8_regs(v * scale, 8 * s2));
+    *reinterpret_cast<uint2*>(row + 16 * s2) = uint2{u.x, u.y};
+    *reinterpret_cast<uint2*>(row + 16 * s2 + 8) = uint2{u.z, u.w};
+  }
+}
+
+template <int RB>
+__global__ void __launch_bounds__(64 * RB, 4) attn_fwd_bf16_d32_kernel(const AttnParams p) {
+  constexpr int D = 32;
+  // Chunk 0's rows sit in their own static arrays: the compiler then knows that the transfers of
+  // the later chunks, still in flight while chunk 0 is processed, do not write what it reads.
+  __shared__ __align__(16) uint16_t K0[kAtChunk * D], V0[kAtChunk * D];
+  extern __shared__ __align__(16) float at_lds[];
+  const int L = p.len, nb = (L + 31) / 32, nch = (L + kAtChunk - 1) / kAtChunk, npc = nch * (kAtChunk / 16);
+  uint16_t* Kr = reinterpret_cast<uint16_t*>(at_lds);  // swizzled [Lp - 64][32] key rows of chunks 1 ..
+  uint16_t* Vr = Kr + (nch - 1) * kAtChunk * D;        // and value rows
+  // XCD-contiguous logical order: the workgroups of one (slice, head) share an L2
+  const int chunks = (nb + RB - 1) / RB, lid = xcd_logical(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int zh = lid / chunks, rc = lid - zh * chunks;
+  const AttnSlice sl(p, zh);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 5, col = lane & 31;
+  const uint16_t* kp = static_cast<const uint16_t*>(p.k) + sl.base(p, kAtK);
+  const uint16_t* vp = static_cast<const uint16_t*>(p.v) + sl.base(p, kAtV);
+  // 16-row piece pc (1 KB per tensor, one global_load_lds_dwordx4 per lane and tensor) into kd, vd:
+  // lane -> row 16 pc + lane / 4, LDS slot lane % 4, which holds the row's 16-byte chunk
+  // (lane % 4) ^ at_sw(row)
+  auto stage = [&](int pc, uint16_t* kd, uint16_t* vd) {
+    const int row = pc * 16 + (lane >> 2), c = (lane & 3) ^ at_sw<D>(row), r = min(row, L - 1);
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(kp + at_row_off(r, p.st[kAtK][3]) + 8 * c), (MSDA_LDS void*)(kd), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(vp + at_row_off(r, p.st[kAtV][3]) + 8 * c), (MSDA_LDS void*)(vd), 16, 0, 0);
+  };
+  for (int pc = wave; pc < kAtChunk / 16; pc += RB) stage(pc, K0 + pc * 16 * D, V0 + pc * 16 * D);
+  const int qb = rc * RB + wave, qi = qb * 32 + col;
+  const bool active = qb < nb;
+  at_bf8 qh[2], ql[2];  // q' = q log2(e) / sqrt(D) = hi + lo, channels 16 s + 8 grp .. + 7
+  {
+    at_bf8 qr[2];
+    at_row_bf8<D>(qr, static_cast<const uint16_t*>(p.q) + sl.base(p, kAtQ), at_row_off(min(qi, L - 1), p.st[kAtQ][3]), grp);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const at_f8 f = __builtin_convertvector(qr[s], at_f8) * p.scale2;
+      qh[s] = __builtin_convertvector(f, at_bf8);
+      ql[s] = __builtin_convertvector(f - __builtin_convertvector(qh[s], at_f8), at_bf8);
+    }
+  }
+  wait_vmem();  // this wave's chunk-0 transfers, before the barrier publishes them
+  __syncthreads();
+  for (int pc = kAtChunk / 16 + wave; pc < npc; pc += RB) stage(pc, Kr + (pc - 4) * 16 * D, Vr + (pc - 4) * 16 * D);
+  float m = 0.0f, ll = 0.0f;  // reference score (at_softmax_chunk); this half-wave's sum of weights
+  at_f16 negm = at_zero16(), o = at_zero16();
+  const int g = lane >> 4, r = lane & 15, c = 16 * (g & 1) + 4 * (r & 3);
+  // One chunk of 64 keys from swizzled tiles Kj, Vj (the swizzle repeats every 16 rows, so a
+  // chunk's offsets are those of a 64-row tile).
+  auto chunk = [&](const uint16_t* Kj, const uint16_t* Vj, int j) {
+    const int k0 = j * kAtChunk;
+    // S^T - m of the chunk's two key blocks: keys k0 + 32 h + 8 (i / 4) + 4 grp + i % 4 of register i
+    at_f16 s0, s1;
+    {
+      at_bf8 a0[2], a1[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        a0[s] = __builtin_bit_cast(at_bf8, *reinterpret_cast<const uint4*>(&Kj[at_swo<D>(col, 16 * s + 8 * grp)]));
+        a1[s] = __builtin_bit_cast(at_bf8, *reinterpret_cast<const uint4*>(&Kj[at_swo<D>(32 + col, 16 * s + 8 * grp)]));
+      }
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[0], qh[0], negm, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[0], qh[0], negm, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[1], qh[1], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[1], qh[1], s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[0], ql[0], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[0], ql[0], s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[1], ql[1], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[1], ql[1], s1, 0, 0, 0);
+    }
+    if (k0 + kAtChunk > L) {  // the last chunk: keys past L weigh 0
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = k0 + 8 * (i >> 2) + 4 * grp + (i & 3);
+        if (key >= L) s0[i] = -INFINITY;
+        if (key + 32 >= L) s1[i] = -INFINITY;
+      }
+    }
+    float bm0 = at_max3(s0[0], s0[1], s1[0]), bm1 = at_max3(s0[2], s0[3], s1[1]);
+#pragma unroll
+    for (int i = 2; i < 16; i += 2) {
+      bm0 = at_max3(bm0, s0[i], s1[i]);
+      bm1 = at_max3(bm1, s0[i + 1], s1[i + 1]);
+    }
+    const float bm = at_max_halves(fmaxf(bm0, bm1));  // relative to m; finite: the chunk holds a key below L
+    if (bm > kAtLazy || (j == 0 && bm < -kAtLow)) {     // move m (at_softmax_chunk; at j = 0 nothing is summed yet)
+      const float alpha = j == 0 ? 0.0f : at_exp2(-bm);
+      m += bm;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        negm[i] = -m;
+        s0[i] -= bm;
+        s1[i] -= bm;
+      }
+      o *= alpha;
+      ll *= alpha;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s0[i] = at_exp2(s0[i]);
+      s1[i] = at_exp2(s1[i]);
+    }
+    at_bf8 b0[2], b1[2];  // result registers 8 s .. 8 s + 7 of each block, rounded (the B operands of P V)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      b0[s] = at_bf8_regs(s0, 8 * s);
+      b1[s] = at_bf8_regs(s1, 8 * s);
+    }
+    ll = at_sum_bf8(b0[0], ll) + at_sum_bf8(b1[0], at_sum_bf8(b0[1], at_sum_bf8(b1[1], 0.0f)));
+    // O^T += V^T P^T (at_accum_tr, one accumulator)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int ro = 32 * h + 16 * s + 4 * grp + (r >> 2);
+        const at_bf8 a = at_bf8_of(at_read_tr(Vj + at_swo<D>(ro, c)), at_read_tr(Vj + at_swo<D>(ro + 8, c)));
+        o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, h == 0 ? b0[s] : b1[s], o, 0, 0, 0);
+      }
+  };
+  if (active) chunk(K0, V0, 0);
+  if (nch > 1) {
+    wait_vmem();  // this wave's transfers of the later chunks
+    __syncthreads();
+  }
+  for (int j = 1; active && j < nch; ++j) chunk(Kr + (j - 1) * kAtChunk * D, Vr + (j - 1) * kAtChunk * D, j);
+  if (active) {
+    const float l = at_sum_halves(ll);
+    at_store_block_direct(static_cast<bf16_t*>(p.out) + sl.base(p, kAtO), p.st[kAtO][3], qb * 32, L, o, 1.0f / l, lane);
+    if (qi < L && grp == 0) {
+      float* stats = p.stats + (static_cast<int64_t>(zh) * L + qi) * 4;
+      stats[0] = m;
+      stats[1] = log2f(l);
+    }
+  }
+}
+
 template <int D, bool MASK, int RB>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_q_bf16_kernel(const AttnParams p) {
   constexpr int NT = 64 * RB, ND = D / 32;

@@ -265,6 +265,71 @@ def test_fused_backward_against_two_kernel_path(length, bf16, tune):
         assert_close(_np(a), _np(c).astype(np.float64), cross, f"grad_{name} fused against two kernels")
 
 
+D32_LENGTHS = [1, 17, 63, 64, 65, 128, 129, 300, 320, 321, 480, 512, 513]
+
+
+@pytest.mark.parametrize("length", D32_LENGTHS)
+def test_bf16_forward_d32_against_chunked(length, tune):
+    """bf16, head_dim 32, no mask, 16-byte aligned key and value rows, up to 512 rows: the forward
+    that stages the whole key and value slice in LDS (scores leave the MFMA scaled and shifted,
+    row sums add the rounded weights) against the oracle and the chunked kernel
+    (MSDA_ATTN_FWD_D32=0). Its statistics give log2 sum_k 2^x (x = q.k log2(e) / sqrt(D)) as
+    m + log2 l, and drive the backward. 513 rows take the chunked kernel either way."""
+    from rfdetr_jax_amd.attention import _Layout, attention_backward, attention_forward
+
+    b, h, d = 2, 3, 32
+    _note(f"bf16 forward d32 L={length}")
+    rng = np.random.default_rng(47 + length)
+    q, k, v, g = (bf16_round(rng.standard_normal((b, h, length, d)).astype(np.float32)) for _ in range(4))
+    lay = _Layout(b, 1, h, length, d)
+    tq, tk, tv, tg = (_t(x, torch.bfloat16) for x in (q, k, v, g))
+    out, stats = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
+    grads = attention_backward(tq, tk, tv, out, stats, tg, lay, lay.strides_bhld)
+    torch.cuda.synchronize()
+    st = _np(stats).reshape(b, h, length, 4)
+    tune({"MSDA_ATTN_FWD_D32": 0})
+    out2, _ = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
+    torch.cuda.synchronize()
+    assert_close(_np(out), AT.sdpa(q, k, v, None), 2e-2, "out")
+    assert_close(_np(out), _np(out2).astype(np.float64), 1e-2, "out against the chunked kernel")
+    x = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), k.astype(np.float64)) * (np.log2(np.e) / np.sqrt(d))
+    xm = x.max(-1)
+    lse2 = xm + np.log2(np.exp2(x - xm[..., None]).sum(-1))
+    err = np.abs(st[..., 0] + st[..., 1] - lse2).max()
+    assert err <= 1e-2, f"m + log2 l against log2 sum 2^x: max error {err}"
+    for name, a, w in zip("qkv", grads, AT.sdpa_vjp(q, k, v, g)):
+        assert_close(_np(a), w, 2e-2, f"grad_{name}")
+
+
+@pytest.mark.parametrize("case", ["far_below", "unaligned_rows"])
+def test_bf16_forward_d32_edge_cases(case, tune):
+    """far_below: every score about -65 (log2 units), below the reference score's low limit, so it
+    moves at the first chunk; equal scores give the mean of V. unaligned_rows: key and value rows
+    with a stride of 36 elements (not 16-byte aligned) take the chunked kernel."""
+    from rfdetr_jax_amd.attention import _Layout, attention_forward
+
+    _note(f"bf16 forward d32 {case}")
+    b, h, length, d = 2, 2, 200, 32
+    rng = np.random.default_rng(48)
+    v = bf16_round(rng.standard_normal((b, h, length, d)).astype(np.float32))
+    if case == "far_below":
+        q = np.full((b, h, length, d), 8.0, np.float32)
+        k = -np.ones((b, h, length, d), np.float32)
+        lay = _Layout(b, 1, h, length, d)
+        out, _ = attention_forward(_t(q, torch.bfloat16), _t(k, torch.bfloat16), _t(v, torch.bfloat16), lay, lay.strides_bhld)
+        want = np.broadcast_to(v.astype(np.float64).mean(axis=2, keepdims=True), v.shape)
+        assert_close(_np(out), want, 2e-2, "mean of V")
+        return
+    q, k = (bf16_round(rng.standard_normal((b, h, length, d)).astype(np.float32)) for _ in range(2))
+    pad = np.zeros((b, h, length, 36), np.float32)
+    tq = _t(q, torch.bfloat16)
+    tk = _t(np.concatenate([k, pad[..., :4]], -1), torch.bfloat16)[..., :d]
+    tv = _t(np.concatenate([v, pad[..., :4]], -1), torch.bfloat16)[..., :d]
+    lay = _Layout(b, 1, h, length, d)
+    out, _ = attention_forward(tq, tk, tv, lay, lay.strides_bhld)
+    assert_close(_np(out), AT.sdpa(q, k, v, None), 2e-2, "out")
+
+
 @pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
 @pytest.mark.parametrize("needs", [(True, True, False), (True, False, True), (True, False, False), (False, True, True)],
                          ids=["qk", "qv", "q", "kv"])
