@@ -377,12 +377,14 @@ __device__ __forceinline__ void at_store_block(VT* dst, int64_t rs, int r0, int 
   }
 }
 
-// The workgroup's (slice, head) and row chunk: blockIdx.x = (z * H + h) * chunks + rc.
+// The workgroup's (slice, head) and row chunk: logical id (z * H + h) * chunks + rc, in
+// XCD-contiguous order (xcd_logical), so the workgroups of one (slice, head), and the heads of a
+// slice, which share the rows' cache lines, run on one XCD.
 struct AttnWork {
   int zh, rc;
   AttnSlice sl;
-  __device__ AttnWork(const AttnParams& p, int chunks) : zh(static_cast<int>(blockIdx.x) / chunks),
-      rc(static_cast<int>(blockIdx.x) - zh * chunks), sl(p, zh) {}
+  __device__ AttnWork(const AttnParams& p, int chunks) : AttnWork(p, chunks, xcd_logical(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x))) {}
+  __device__ AttnWork(const AttnParams& p, int chunks, int lid) : zh(lid / chunks), rc(lid - zh * chunks), sl(p, zh) {}
 };
 
 // Forward: out = softmax(q k^T / sqrt(D), blocked -> finfo.min) v. Each wave owns 32 queries; K and
@@ -1194,7 +1196,9 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
   uint16_t* Kt = reinterpret_cast<uint16_t*>(at_lds);  // swizzled [32 nb][D] key rows (0 past L)
   uint16_t* St = Kt + 32 * nb * D;                      // dS tiles: 1024 elements each, set, block, query block
-  const AttnSlice sl(p, static_cast<int>(blockIdx.x));
+  // XCD-contiguous logical order: the heads of a slice, which share the rows' cache lines, run on one XCD
+  const int zh = xcd_logical(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const AttnSlice sl(p, zh);
   const uint16_t* kp = static_cast<const uint16_t*>(p.k) + sl.base(p, kAtK);
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, grp = lane >> 5, col = lane & 31;
   if (wave < nb) {  // key block kb = wave (uniform per wave)
@@ -1239,7 +1243,7 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
       if (j >= nchunks) continue;
       const int b = j & 1;
       if (kb == 0 && j * kAtChunk + lane < L)  // rowsum(dO * O) into the statistics (their entry 2)
-        p.stats[(static_cast<int64_t>(blockIdx.x) * L + j * kAtChunk + lane) * 4 + 2] = Ds[b][lane];
+        p.stats[(static_cast<int64_t>(zh) * L + j * kAtChunk + lane) * 4 + 2] = Ds[b][lane];
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {  // the chunk's two query blocks
         at_f16 s, dp;
@@ -1282,7 +1286,7 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   const uint16_t* qp = static_cast<const uint16_t*>(p.q) + sl.base(p, kAtQ);
   const uint16_t* gop = static_cast<const uint16_t*>(p.go) + sl.base(p, kAtGO);
   const uint16_t* opp = static_cast<const uint16_t*>(p.o) + sl.base(p, kAtO);
-  float* stats = p.stats + static_cast<int64_t>(blockIdx.x) * L * 4;
+  float* stats = p.stats + static_cast<int64_t>(zh) * L * 4;
   const int srow = tq >> 1, shalf = tq & 1;
   uint4 qv[2], gv[2], ov[2];
   float2 sq = {0.0f, 0.0f};  // m, log2 l (8 bytes: no register of a wider load left idle in flight)
@@ -1398,7 +1402,8 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_f
   const int L = p.len, nb = (L + 31) / 32;  // key blocks; also the query blocks (phases)
   float* Kf = at_lds;                       // [32 nb][32] key rows (0 past L)
   float* St = Kf + 32 * nb * D;             // dS tiles: 1024 floats each, parity, key block
-  const AttnSlice sl(p, static_cast<int>(blockIdx.x));
+  const int zh = xcd_logical(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));  // as the bf16 kernel
+  const AttnSlice sl(p, zh);
   const float* kp = static_cast<const float*>(p.k) + sl.base(p, kAtK);
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, grp = lane >> 5, col = lane & 31;
   if (wave < nb) {  // key block kb = wave (uniform per wave)
@@ -1447,7 +1452,7 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_f
       if (j >= nb) continue;
       const int b = j & 1;
       if (kb == 0 && lane < 32 && j * 32 + lane < L)  // rowsum(dO * O) into the statistics (their entry 2)
-        p.stats[(static_cast<int64_t>(blockIdx.x) * L + j * 32 + lane) * 4 + 2] = Ds[b][lane];
+        p.stats[(static_cast<int64_t>(zh) * L + j * 32 + lane) * 4 + 2] = Ds[b][lane];
       at_f16 s, dp;
       at_scores_pair<D>(s, dp, Qs[b], Gs[b], kr, vr, col, grp);  // S = Q K^T, dP = dO V^T
       at_f16 pw;
@@ -1483,7 +1488,7 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_f
   const float* qp = static_cast<const float*>(p.q) + sl.base(p, kAtQ);
   const float* gop = static_cast<const float*>(p.go) + sl.base(p, kAtGO);
   const float* opp = static_cast<const float*>(p.o) + sl.base(p, kAtO);
-  float* stats = p.stats + static_cast<int64_t>(blockIdx.x) * L * 4;
+  float* stats = p.stats + static_cast<int64_t>(zh) * L * 4;
   const int srow = tq >> 2, sq4 = tq & 3;
   at_f4 qv[2], gv[2], ov[2];
   float2 sq = {0.0f, 0.0f};  // m, log2 l (8 bytes: no register of a wider load left idle in flight)
