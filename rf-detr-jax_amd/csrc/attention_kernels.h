@@ -1188,8 +1188,8 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   constexpr int D = 32;
   __shared__ __align__(16) uint16_t Qr[2][kAtChunk * D];  // swizzled [64][D] query and output-gradient rows
   __shared__ __align__(16) uint16_t Gr[2][kAtChunk * D];
-  __shared__ __align__(16) float Ms[2][2 * kAtChunk];  // [64][2]: m, log2 l (rows past L: +inf)
-  __shared__ __align__(16) float Ds[2][kAtChunk];      // [64]: rowsum(dO * O)
+  __shared__ __align__(16) float Ms[2][kAtChunk];  // [64]: -(m + log2 l) (rows past L: -inf)
+  __shared__ __align__(16) float Ds[2][kAtChunk];  // [64]: -rowsum(dO * O)
   __shared__ __align__(16) uint16_t Sq[2][32 * 40];    // the dQ waves' output scratch
   __shared__ __align__(16) float Xq[2][2][16 * 64];      // key waves 0, 1: dQ^T of a block over the second half of the key blocks
   extern __shared__ __align__(16) float at_lds[];
@@ -1209,8 +1209,17 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
       const int row = kb * 32 + 8 * u + (lane >> 3);
       kc[u] = row < L ? *reinterpret_cast<const uint2*>(kp + at_row_off(row, p.st[kAtK][3]) + 4 * (lane & 7)) : uint2{0u, 0u};
     }
-    at_bf8 kr[2], vr[2];
-    at_row_bf8<D>(kr, kp, min(key, L - 1) * p.st[kAtK][3], grp);
+    at_bf8 kh[2], kl[2], vr[2];  // k' = k log2(e) / sqrt(D) = hi + lo (as the forward's query rows)
+    {
+      at_bf8 kr[2];
+      at_row_bf8<D>(kr, kp, min(key, L - 1) * p.st[kAtK][3], grp);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const at_f8 f = __builtin_convertvector(kr[s], at_f8) * p.scale2;
+        kh[s] = __builtin_convertvector(f, at_bf8);
+        kl[s] = __builtin_convertvector(f - __builtin_convertvector(kh[s], at_f8), at_bf8);
+      }
+    }
     at_row_bf8<D>(vr, static_cast<const uint16_t*>(p.v) + sl.base(p, kAtV), min(key, L - 1) * p.st[kAtV][3], grp);
 #pragma unroll
     for (int u = 0; u < 4; ++u) *reinterpret_cast<uint2*>(&Kt[at_swo<D>(kb * 32 + 8 * u + (lane >> 3), 4 * (lane & 7))]) = kc[u];
@@ -1243,26 +1252,44 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
       if (j >= nchunks) continue;
       const int b = j & 1;
       if (kb == 0 && j * kAtChunk + lane < L)  // rowsum(dO * O) into the statistics (their entry 2)
-        p.stats[(static_cast<int64_t>(zh) * L + j * kAtChunk + lane) * 4 + 2] = Ds[b][lane];
+        p.stats[(static_cast<int64_t>(zh) * L + j * kAtChunk + lane) * 4 + 2] = -Ds[b][lane];
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {  // the chunk's two query blocks
+        // S - m - log2 l = Q k'^T - (m + log2 l) and dP - rowsum = dO V^T - rowsum: the
+        // accumulators start from the per-query shifts (register i: query 32 h2 + 8 (i / 4) +
+        // 4 grp + i % 4 of the chunk), so P = exp2 of the first and dS = P times the second.
         at_f16 s, dp;
-        at_scores_sw<D>(s, dp, Qr[b], 32 * h2, Gr[b], 32 * h2, kr, vr, col, grp);  // S = Q K^T, dP = dO V^T
-        at_f16 pw;
 #pragma unroll
         for (int c4 = 0; c4 < 4; ++c4) {
           const int ql = 32 * h2 + 8 * c4 + 4 * grp;
-          const at_f4 ms0 = *reinterpret_cast<const at_f4*>(&Ms[b][2 * ql]), ms1 = *reinterpret_cast<const at_f4*>(&Ms[b][2 * ql + 4]);
-          const at_f4 dd = *reinterpret_cast<const at_f4*>(&Ds[b][ql]);
-          const float mq[4] = {ms0[0], ms0[2], ms1[0], ms1[2]}, lq[4] = {ms0[1], ms0[3], ms1[1], ms1[3]};
+          const at_f4 ms = *reinterpret_cast<const at_f4*>(&Ms[b][ql]), dd = *reinterpret_cast<const at_f4*>(&Ds[b][ql]);
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int i = 4 * c4 + jj;
-            // A lane past L holds the clamped last key: its weights are finite, and its rows of the
-            // key copy are 0, so it adds nothing to dQ. Rows past L have m = +inf: weight 0.
-            pw[i] = at_exp2(fmaf(s[i], p.scale2, -mq[jj]) - lq[jj]);
-            s[i] = pw[i] * (dp[i] - dd[jj]);  // dS
+          for (int e = 0; e < 4; ++e) {
+            s[4 * c4 + e] = ms[e];
+            dp[4 * c4 + e] = dd[e];
           }
+        }
+        {
+          at_bf8 qa[2], ga[2];
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            qa[s2] = __builtin_bit_cast(at_bf8, *reinterpret_cast<const uint4*>(&Qr[b][at_swo<D>(32 * h2 + col, 16 * s2 + 8 * grp)]));
+            ga[s2] = __builtin_bit_cast(at_bf8, *reinterpret_cast<const uint4*>(&Gr[b][at_swo<D>(32 * h2 + col, 16 * s2 + 8 * grp)]));
+          }
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[0], kh[0], s, 0, 0, 0);
+          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ga[0], vr[0], dp, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[1], kh[1], s, 0, 0, 0);
+          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ga[1], vr[1], dp, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[0], kl[0], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[1], kl[1], s, 0, 0, 0);
+        }
+        at_f16 pw;
+        // A lane past L holds the clamped last key: its weights are finite, and its rows of the
+        // key copy are 0, so it adds nothing to dQ. Rows past L have a shift of -inf: weight 0.
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          pw[i] = at_exp2(s[i]);
+          s[i] = pw[i] * dp[i];  // dS
         }
         at_accum_tr<D>(dv, dk, Gr[b], 32 * h2, Qr[b], 32 * h2, pw, s, lane);  // dV^T += dO^T P, dK^T += Q^T dS
         // dS^T tile: row = key (this lane's col), columns = the block's queries
@@ -1320,9 +1347,8 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
     // the row's other half: the neighbouring lane (DPP quad_perm [1, 0, 3, 2])
     dd += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(dd), 0xB1, 0xF, 0xF, false));
     if (shalf == 0) {
-      Ms[b][2 * srow] = in ? sq.x : INFINITY;
-      Ms[b][2 * srow + 1] = in ? sq.y : 0.0f;
-      Ds[b][srow] = in ? dd : 0.0f;
+      Ms[b][srow] = in ? -(sq.x + sq.y) : -INFINITY;
+      Ds[b][srow] = in ? -dd : 0.0f;
     }
   };
   prefetch(0);
