@@ -1170,10 +1170,10 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
 // the block's dK and dV (as attn_bwd_kv_bf16_kernel) and write dS into LDS tiles [32 keys][32
 // queries]. Waves nb and nb + 1 stage the query-side rows (Q, dO, and rowsum(dO * O) from O) one
 // chunk ahead and form dQ of the previous chunk's two query blocks, one block each, over the first
-// half of the key blocks, dQ^T = K^T dS^T, from a swizzled copy of K and the dS tiles by
-// transposing reads; key waves 0 and 1, idle otherwise at that point, form the second half into
-// LDS, which the dQ waves add one chunk later before storing the block. The row tiles, dS tiles
-// and halves are double buffered by chunk parity: one barrier per chunk.
+// key blocks, dQ^T = K^T dS^T, from a swizzled copy of K and the dS tiles by transposing reads;
+// key waves 0 .. 3 form the rest in two parts into LDS, which the dQ waves add one chunk later
+// before storing the block. The row tiles, dS tiles and parts are double buffered by chunk parity:
+// one barrier per chunk.
 constexpr int kAtFusedBlocks = 10;  // key-block waves; with the two dQ waves, 768 threads (three waves per SIMD)
 
 // Dynamic LDS bytes of the fused kernel for nb key blocks: the swizzled key rows [32 nb][32] and
@@ -1191,7 +1191,7 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   __shared__ __align__(16) float Ms[2][kAtChunk];  // [64]: -(m + log2 l) (rows past L: -inf)
   __shared__ __align__(16) float Ds[2][kAtChunk];  // [64]: -rowsum(dO * O)
   __shared__ __align__(16) uint16_t Sq[2][32 * 40];    // the dQ waves' output scratch
-  __shared__ __align__(16) float Xq[2][2][16 * 64];      // key waves 0, 1: dQ^T of a block over the second half of the key blocks
+  __shared__ __align__(16) float Xq[2][2][2][16 * 64];   // by parity, part and query block: the helpers' partial dQ^T
   extern __shared__ __align__(16) float at_lds[];
   const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
   uint16_t* Kt = reinterpret_cast<uint16_t*>(at_lds);  // swizzled [32 nb][D] key rows (0 past L)
@@ -1201,6 +1201,12 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   const AttnSlice sl(p, zh);
   const uint16_t* kp = static_cast<const uint16_t*>(p.k) + sl.base(p, kAtK);
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, grp = lane >> 5, col = lane & 31;
+  // dQ^T of a query block sums over the key blocks: [0, n0) by the dQ wave of that block, [n0, n1)
+  // by key wave 0 or 1 (part 0) and [n1, nb) by key wave 2 or 3 (part 1), whose partial sums pass
+  // through LDS; the dQ waves also stage the rows, so they take the smallest share.
+  const int helpers = nb >= 4 ? 4 : (nb >= 2 ? 2 : 0);
+  const int n0 = helpers == 4 ? max(1, 3 * nb / 10) : helpers == 2 ? (nb + 1) / 2 : nb;
+  const int n1 = helpers == 4 ? n0 + (nb - n0 + 1) / 2 : nb;
   if (wave < nb) {  // key block kb = wave (uniform per wave)
     const int kb = wave, key = kb * 32 + col;
     uint2 kc[4];  // the block's rows of the key copy: row 8 u + lane / 8, channels 4 (lane % 8) .. + 3
@@ -1224,16 +1230,16 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
 #pragma unroll
     for (int u = 0; u < 4; ++u) *reinterpret_cast<uint2*>(&Kt[at_swo<D>(kb * 32 + 8 * u + (lane >> 3), 4 * (lane & 7))]) = kc[u];
     at_f16 dk[1] = {at_zero16()}, dv[1] = {at_zero16()};
-    const int nh = (nb + 1) / 2;  // key blocks [0, nh) for the dQ waves, [nh, nb) for key waves 0 and 1
     for (int j = 0; j <= nchunks + 1; ++j) {
       __syncthreads();  // chunk j staged; the dS tiles of chunk j - 2 read; the halves of chunk j - 3 added
-      if (kb < 2 && nb >= 2 && j >= 1 && j <= nchunks) {
-        // dQ^T of query block kb of chunk j - 1 over key blocks [nh, nb) into Xq (result layout)
+      if (kb < helpers && j >= 1 && j <= nchunks) {
+        // part kb / 2 of dQ^T of query block kb % 2 of chunk j - 1 into Xq (result layout)
+        const int part = kb >> 1, kbeg = part == 0 ? n0 : n1, kend = part == 0 ? n1 : nb;
         const int bp = (j - 1) & 1, g16 = lane >> 4, r = lane & 15;
         const int tc = 16 * (g16 & 1) + 4 * (r & 3), tro = 4 * grp + (r >> 2);
         at_f16 acc0 = at_zero16(), acc1 = at_zero16();
-        for (int kb2 = nh; kb2 < nb; ++kb2) {
-          const uint16_t* Th = St + ((bp * nb + kb2) * 2 + kb) * 1024;
+        for (int kb2 = kbeg; kb2 < kend; ++kb2) {
+          const uint16_t* Th = St + ((bp * nb + kb2) * 2 + (kb & 1)) * 1024;
 #pragma unroll
           for (int s2 = 0; s2 < 2; ++s2) {
             const int ro = 16 * s2 + tro;
@@ -1243,7 +1249,7 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
             else acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, sb, acc1, 0, 0, 0);
           }
         }
-        float* x = Xq[bp][kb];
+        float* x = Xq[bp][part][kb & 1];
 #pragma unroll
         for (int c = 0; c < 4; ++c)
           *reinterpret_cast<at_f4*>(&x[4 * (c * 64 + lane)]) = at_f4{acc0[4 * c] + acc1[4 * c], acc0[4 * c + 1] + acc1[4 * c + 1],
@@ -1357,13 +1363,12 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   bf16_t* gqp = static_cast<bf16_t*>(p.gq) + sl.base(p, kAtGQ);
   const int g16 = lane >> 4, r = lane & 15;
   const int tc = 16 * (g16 & 1) + 4 * (r & 3), tro = 4 * grp + (r >> 2);  // transposing-read lane offsets
-  const int nh = (nb + 1) / 2;
-  at_f16 held = at_zero16();  // dQ^T of this wave's query block of the previous chunk over key blocks [0, nh)
+  at_f16 held = at_zero16();  // dQ^T of this wave's query block of the previous chunk over key blocks [0, n0)
   for (int j = 0; j <= nchunks + 1; ++j) {
     __syncthreads();  // chunk j staged; the dS tiles of chunk j - 1 and the halves of chunk j - 2 written
     if (j >= 2) {  // chunk j - 2: add key wave h2q's half and store
-      if (nb >= 2) {
-        const float* x = Xq[j & 1][h2q];
+      for (int part = 0; 2 * part < helpers; ++part) {
+        const float* x = Xq[j & 1][part][h2q];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const at_f4 h4 = *reinterpret_cast<const at_f4*>(&x[4 * (c * 64 + lane)]);
@@ -1393,9 +1398,9 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
       }
     };
     operands(0);
-    for (int kb2 = 0; kb2 < nh; ++kb2) {
+    for (int kb2 = 0; kb2 < n0; ++kb2) {
       const at_bf8 a0 = ka[0], a1 = ka[1], b0 = sb[0], b1 = sb[1];
-      if (kb2 + 1 < nh) operands(kb2 + 1);
+      if (kb2 + 1 < n0) operands(kb2 + 1);
       acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc0, 0, 0, 0);
       acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc1, 0, 0, 0);
     }
