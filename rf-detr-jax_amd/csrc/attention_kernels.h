@@ -1203,9 +1203,10 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, grp = lane >> 5, col = lane & 31;
   // dQ^T of a query block sums over the key blocks: [0, n0) by the dQ wave of that block, [n0, n1)
   // by key wave 0 or 1 (part 0) and [n1, nb) by key wave 2 or 3 (part 1), whose partial sums pass
-  // through LDS; the dQ waves also stage the rows, so they take the smallest share.
+  // through LDS; the dQ waves also stage the rows, so they take the smallest share (2 of 10 key
+  // blocks measured faster than 3 or 4).
   const int helpers = nb >= 4 ? 4 : (nb >= 2 ? 2 : 0);
-  const int n0 = helpers == 4 ? max(1, 3 * nb / 10) : helpers == 2 ? (nb + 1) / 2 : nb;
+  const int n0 = helpers == 4 ? max(1, 2 * nb / 10) : helpers == 2 ? (nb + 1) / 2 : nb;
   const int n1 = helpers == 4 ? n0 + (nb - n0 + 1) / 2 : nb;
   if (wave < nb) {  // key block kb = wave (uniform per wave)
     const int kb = wave, key = kb * 32 + col;
