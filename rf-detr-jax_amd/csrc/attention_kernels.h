@@ -1190,7 +1190,6 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
   __shared__ __align__(16) uint16_t Gr[2][kAtChunk * D];
   __shared__ __align__(16) float Ms[2][kAtChunk];  // [64]: -(m + log2 l) (rows past L: -inf)
   __shared__ __align__(16) float Ds[2][kAtChunk];  // [64]: -rowsum(dO * O)
-  __shared__ __align__(16) uint16_t Sq[2][32 * 40];    // the dQ waves' output scratch
   __shared__ __align__(16) float Xq[2][2][2][16 * 64];   // by parity, part and query block: the helpers' partial dQ^T
   extern __shared__ __align__(16) float at_lds[];
   const int L = p.len, nb = (L + 31) / 32, nchunks = (L + kAtChunk - 1) / kAtChunk;
@@ -1377,7 +1376,9 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_b
           for (int e = 0; e < 4; ++e) held[4 * c + e] += h4[e];
         }
       }
-      at_store_block(gqp, p.st[kAtGQ][3], (j - 2) * kAtChunk + 32 * h2q, L, held, p.scale, Sq[h2q], lane);
+      // straight from the result layout: measured faster here than through LDS (the dK / dV stores
+      // at the end are not: through LDS they hold the workgroup's end less)
+      at_store_block_direct(gqp, p.st[kAtGQ][3], (j - 2) * kAtChunk + 32 * h2q, L, held, p.scale, lane);
     }
     if (j + 1 < nchunks) {
       stage((j + 1) * kAtChunk, (j + 1) & 1);
