@@ -60,6 +60,20 @@ enum msda_status {
   MSDA_ERR_DEVICE = -4            /* a HIP runtime query failed */
 };
 
+/*
+ * The reference's sampler names (ms_deform_attn_core_rows's `sampler`, ops.py:208-241), for
+ * msda_fwd_sampler / msda_bwd_sampler. MSDA_SAMPLER_HIP is this library's own: f32 interpolation
+ * throughout, what msda_fwd / msda_bwd compute.
+ */
+enum msda_sampler {
+  MSDA_SAMPLER_HIP = 0,
+  MSDA_SAMPLER_GATHER = 1,     /* ops.py:64-134 _sample_rows */
+  MSDA_SAMPLER_GATHER_F32 = 2, /* ops.py:137-144 _sample_rows_f32 */
+  MSDA_SAMPLER_MATMUL = 3,     /* ops.py:147-186 _sample_rows_matmul */
+  MSDA_SAMPLER_AUTO = 4,       /* per level: matmul when H * W <= 4096, else gather (ops.py:42, :277-279) */
+  MSDA_SAMPLER_PALLAS = 5      /* deform_pallas.py:193-228 sample_weighted */
+};
+
 /* Maximum number of feature levels per call. */
 #define MSDA_MAX_LEVELS 16
 
@@ -84,7 +98,8 @@ int msda_set_tuning(const char* name, const char* value);
 /*
  * Forward: output = sum_{l,p} A[b,q,h,l*P+p] * bilinear(value[b*H+h], level l, loc[b,q,h,l,p]).
  * Replaces ms_deform_attn_core_rows (src/rfdetr_jax/models/ops.py:208-292) and its "pallas"
- * branch (ops.py:243-263 -> deform_pallas.py:193-228 sample_weighted).
+ * branch (ops.py:243-263 -> deform_pallas.py:193-228 sample_weighted), interpolating in f32
+ * throughout; msda_fwd_sampler adds a named sampler's rounding points.
  * output_dtype is the dtype of result_type(value, attention_weights) in the reference (ops.py:260),
  * i.e. MSDA_DTYPE_F32 whenever the weights are f32; MSDA_DTYPE_BF16 is accepted for callers that
  * keep bf16 weights.
@@ -96,6 +111,32 @@ int msda_fwd(const void* value, int value_dtype,
              int n_levels, int n_points,
              const int32_t* spatial_shapes, const int32_t* level_start_index,
              int64_t len_value, void* stream);
+
+/*
+ * msda_fwd computing what the named reference sampler computes (`sampler`: enum msda_sampler),
+ * the `sampler` argument of ms_deform_attn_core_rows (ops.py:208-292). They differ in where a bf16
+ * value map is rounded and in how the Pallas kernel forms pixel coordinates; with an f32 value
+ * map gather, gather-f32, matmul and auto are the f32 interpolation of msda_fwd.
+ *   GATHER      bf16 value: the fractions, 1 - fraction, the four corner-weight products, each
+ *               value * weight product and the four-corner sum rounded to bf16 (ops.py:88-91,
+ *               :123, :134; the sum taken in f32).
+ *   GATHER_F32  bf16 value: f32 interpolation, the sample rounded to bf16 (ops.py:137-144).
+ *   MATMUL      bf16 value: the axis kernels 1 - f and f rounded to bf16, their products rounded
+ *               to bf16 (ops.py:170-184), the contraction with the values in f32 and rounded to
+ *               bf16 (ops.py:186).
+ *   AUTO        per level, MATMUL when H * W <= 4096, else GATHER (ops.py:42, :277-279).
+ *   PALLAS      pixel coordinates loc * size - 0.5 (deform_pallas.py:223-224) instead of
+ *               ((2 loc - 1 + 1) size - 1) / 2 (ops.py:83-84, :270); f32 interpolation.
+ * Each sample's weighted sum over levels and points is formed in f32 (ops.py:289). Returns
+ * MSDA_ERR_INVALID_ARGUMENT for an unknown sampler code; otherwise as msda_fwd.
+ */
+int msda_fwd_sampler(const void* value, int value_dtype,
+                     const float* sampling_locations, const float* attention_weights,
+                     void* output, int output_dtype, int sampler,
+                     int batch, int n_heads, int head_dim, int len_query,
+                     int n_levels, int n_points,
+                     const int32_t* spatial_shapes, const int32_t* level_start_index,
+                     int64_t len_value, void* stream);
 
 /*
  * Device workspace msda_bwd needs for this shape, in bytes, or a negative MSDA_ERR_* code: the f32
@@ -137,6 +178,25 @@ int msda_bwd(const void* value, int value_dtype,
              int n_levels, int n_points,
              const int32_t* spatial_shapes, const int32_t* level_start_index,
              int64_t len_value, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * msda_bwd for the gradient of msda_fwd_sampler: the VJP of the f32 interpolation at the pixel
+ * coordinates the named sampler forms (PALLAS: loc * size - 0.5, deform_pallas.py:157-175; the
+ * others those of ops.py:83-84), so the floor decisions are the forward's. The bf16 rounding points
+ * of GATHER, GATHER_F32 and MATMUL are forward-only: their VJP through the bf16 casts rounds the
+ * cotangents and scatter-adds them in bf16 in an order XLA chooses, which no fixed-order kernel
+ * reproduces; the gradients here are the f32 ones, within the bf16 tolerance of the reference's.
+ * Workspace as msda_bwd_workspace_size(); arguments and results otherwise as msda_bwd.
+ */
+int msda_bwd_sampler(const void* value, int value_dtype,
+                     const float* sampling_locations, const float* attention_weights,
+                     const void* grad_output, int grad_output_dtype,
+                     void* grad_value, float* grad_sampling_locations, float* grad_attention_weights,
+                     int sampler,
+                     int batch, int n_heads, int head_dim, int len_query,
+                     int n_levels, int n_points,
+                     const int32_t* spatial_shapes, const int32_t* level_start_index,
+                     int64_t len_value, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * msda_bwd without a workspace argument and without any device allocation, for callers that

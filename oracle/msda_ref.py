@@ -30,10 +30,17 @@ retyping of these formulas):
   finite differences of the float64 forward; linearity of the output in value and in weights
   (``<G, out> = <dV, V>`` and ``= <dA, A>``).
 * ``ms_deform_attn_core_rows_bf16_gather`` (the reference's bf16 rounding points of the ``gather``
-  sampler, ops.py:88-91 and :123-134, for documenting how far the kernels' f32 interpolation lies
-  from them): equal to the float64 forward where every fraction, weight and product is exact in
-  bf16 (quarter-pixel positions, small integer values); a planted mistake (the coordinate rounded to
-  bf16 instead of its fraction) changes the result.
+  sampler, ops.py:88-91 and :123-134): equal to the float64 forward where every fraction, weight
+  and product is exact in bf16 (quarter-pixel positions, small integer values); a planted mistake
+  (the coordinate rounded to bf16 instead of its fraction) changes the result.
+* ``ms_deform_attn_core_rows_sampler`` (each sampler name's forward: the bf16 rounding points of
+  ``gather`` ops.py:64-134, ``gather-f32`` :137-144 and ``matmul`` :147-186, ``auto``'s per-level
+  choice :277-279, the Pallas kernel's pixel coordinates deform_pallas.py:221-224): per-level
+  samples equal torch arithmetic in the reference's dtypes (bf16 operations round after every
+  step), every sampler equals the float64 forward where all roundings are exact, and the Pallas
+  coordinates equal torch f32 arithmetic and flip floor decisions against ops.py's near cell
+  boundaries. ``ms_deform_attn_core_rows_vjp_pallas``: finite differences of that forward and the
+  ``<G, out> = <dV, V> = <dA, A>`` identities.
 """
 
 from __future__ import annotations
@@ -45,6 +52,8 @@ __all__ = [
     "ms_deform_attn_core_rows",
     "ms_deform_attn_core_rows_vjp",
     "ms_deform_attn_core_rows_bf16_gather",
+    "ms_deform_attn_core_rows_sampler",
+    "ms_deform_attn_core_rows_vjp_pallas",
     "brute_force_forward",
     "bf16_round",
 ]
@@ -76,15 +85,25 @@ def _pixel_coords(loc: np.ndarray, size: int) -> np.ndarray:
     return ((grid + one) * ctype.type(size) - one) / ctype.type(2)
 
 
-def _corners(loc_x, loc_y, height, width):
+def _pallas_coords(loc: np.ndarray, size: int) -> np.ndarray:
+    """``loc * size - 0.5`` in float32, two roundings (deform_pallas.py:221-224)."""
+    loc = np.asarray(loc).astype(np.float32)
+    return loc * np.float32(size) - np.float32(0.5)
+
+
+def _corners(loc_x, loc_y, height, width, pallas=False):
     """Clipped corner indices, masked weights and masks for one level (ops.py:83-128).
 
     Returns ``idx[..., 4]`` (flat index inside the level, corner order (x0,y0),(x1,y0),(x0,y1),
     (x1,y1) as ops.py:110-118), ``w[..., 4]`` float64 masked weights, ``m[..., 4]`` float64 masks,
-    and the fractional parts ``fx, fy`` (float64) that the gradient needs.
+    and the fractional parts ``fx, fy`` (float64) that the gradient needs. ``pallas``: the pixel
+    coordinates of the Pallas sampler (deform_pallas.py:223-224), whose axis kernels
+    (:52-59) put 1 - frac and frac at floor and floor + 1 and match no position off the map, the
+    same weights and masks.
     """
-    ix = _pixel_coords(loc_x, width)
-    iy = _pixel_coords(loc_y, height)
+    coords = _pallas_coords if pallas else _pixel_coords
+    ix = coords(loc_x, width)
+    iy = coords(loc_y, height)
     ix0 = np.floor(ix)
     iy0 = np.floor(iy)
     # Rounded in the coordinate dtype, as ops.py:88-89 computes it (inexact for ix in (-1, 0)).
@@ -153,7 +172,7 @@ def ms_deform_attn_core_rows(value, spatial_shapes, sampling_locations, attentio
     return out.reshape(batch, len_query, n_heads * d)
 
 
-def ms_deform_attn_core_rows_vjp(value, spatial_shapes, sampling_locations, attention_weights, grad_output):
+def ms_deform_attn_core_rows_vjp(value, spatial_shapes, sampling_locations, attention_weights, grad_output, pallas=False):
     """Gradients of ops.py:208-292 for cotangent ``grad_output [B,Q,H*D]``.
 
     Returns ``(grad_value [B*H,S,D], grad_locations [B,Q,H,L,P,2], grad_weights [B,Q,H,L*P])``,
@@ -173,7 +192,7 @@ def ms_deform_attn_core_rows_vjp(value, spatial_shapes, sampling_locations, atte
         start = offsets[level]
         v_l = v64[:, :, start : offsets[level + 1], :]
         loc = sampling_locations[:, :, :, level]
-        idx, w, m, fx, fy = _corners(loc[..., 0], loc[..., 1], height, width)
+        idx, w, m, fx, fy = _corners(loc[..., 0], loc[..., 1], height, width, pallas=pallas)
         corners = _gather(v_l, idx)  # [B,Q,H,P,4,D]
         a = attn[:, :, :, level]  # [B,Q,H,P]
         sample = np.einsum("bqhpc,bqhpcd->bqhpd", w, corners)
@@ -234,6 +253,81 @@ def ms_deform_attn_core_rows_bf16_gather(value, spatial_shapes, sampling_locatio
         sample = bf16_round(prods.sum(axis=-2, dtype=np.float32))
         out += np.einsum("bqhp,bqhpd->bqhd", attn[:, :, :, level], sample.astype(np.float64))
     return out.reshape(batch, len_query, n_heads * d)
+
+
+#: _MATMUL_SAMPLER_MAX_LEVEL (ops.py:42): "auto" uses the matmul sampler up to this many positions.
+MATMUL_SAMPLER_MAX_LEVEL = 4096
+
+
+def _bf16_level_sample(v_l, loc, height, width, mode):
+    """One level's samples ``[B,Q,H,P,D]`` (float32 holding bf16 values) on a bf16 value map with
+    the rounding points of ``mode``: ``"gather"`` (ops.py:88-91, :123-134), ``"gather-f32"``
+    (ops.py:137-144: f32 interpolation, the sample rounded to bf16) or ``"matmul"`` (ops.py:170-186:
+    the axis kernels and their outer product rounded to bf16, the contraction in f32, its result
+    rounded to bf16). Products and sums in float32, one rounding each, corners in index order."""
+    one = np.float32(1)
+    ix = _pixel_coords(loc[..., 0], width).astype(np.float32)
+    iy = _pixel_coords(loc[..., 1], height).astype(np.float32)
+    fx = ix - np.floor(ix)
+    fy = iy - np.floor(iy)
+    idx, _, m, _, _ = _corners(loc[..., 0], loc[..., 1], height, width)
+    if mode == "gather":
+        wx1, wy1 = bf16_round(fx), bf16_round(fy)
+        wx0, wy0 = bf16_round(one - wx1), bf16_round(one - wy1)
+        weight = np.stack([bf16_round(wx0 * wy0), bf16_round(wx1 * wy0), bf16_round(wx0 * wy1), bf16_round(wx1 * wy1)], -1)
+    elif mode == "matmul":
+        kx0, kx1 = bf16_round(one - fx), bf16_round(fx)
+        ky0, ky1 = bf16_round(one - fy), bf16_round(fy)
+        weight = np.stack([bf16_round(ky0 * kx0), bf16_round(ky0 * kx1), bf16_round(ky1 * kx0), bf16_round(ky1 * kx1)], -1)
+    elif mode == "gather-f32":
+        wx0, wy0 = one - fx, one - fy
+        weight = np.stack([wx0 * wy0, fx * wy0, wx0 * fy, fx * fy], -1)
+    else:
+        raise ValueError(mode)
+    weight = weight * m.astype(np.float32)  # exact: the mask is 0 or 1
+    corners = _gather(v_l, idx)  # [B,Q,H,P,4,D] float32
+    prods = corners * weight[..., None]
+    if mode == "gather":
+        prods = bf16_round(prods)
+    total = ((prods[..., 0, :] + prods[..., 1, :]) + prods[..., 2, :]) + prods[..., 3, :]
+    return bf16_round(total)
+
+
+def ms_deform_attn_core_rows_sampler(value, spatial_shapes, sampling_locations, attention_weights, sampler, bf16_value):
+    """Forward of ops.py:208-292 with a named sampler (``"hip"``, ``"gather"``, ``"gather-f32"``,
+    ``"matmul"``, ``"auto"``, ``"pallas"``), float64 ``[B, Q, H*D]``: on a bf16 value map (``value``
+    holding bf16-representable float32 values, ``bf16_value`` true) each level's samples carry the
+    sampler's bf16 rounding points (_bf16_level_sample; "auto" picks matmul for levels of at most
+    MATMUL_SAMPLER_MAX_LEVEL positions, ops.py:277-279); "pallas" forms the pixel coordinates as
+    deform_pallas.py:223-224 does and interpolates in float64; "hip" and every sampler on an f32 map
+    is the float64 forward. The sum over levels and points (:289) in float64."""
+    if sampler == "hip":
+        return ms_deform_attn_core_rows(value, spatial_shapes, sampling_locations, attention_weights)
+    if sampler not in ("gather", "gather-f32", "matmul", "auto", "pallas"):
+        raise ValueError(f"unknown sampler {sampler!r}")
+    batch, len_query, n_heads, n_levels, n_points, d, offsets = _split(value, spatial_shapes, sampling_locations)
+    v64 = np.asarray(value, dtype=np.float64).reshape(batch, n_heads, -1, d)
+    attn = np.asarray(attention_weights, dtype=np.float64).reshape(batch, len_query, n_heads, n_levels, n_points)
+    out = np.zeros((batch, len_query, n_heads, d), np.float64)
+    for level, (height, width) in enumerate(spatial_shapes):
+        v_l = v64[:, :, offsets[level] : offsets[level + 1], :]
+        loc = sampling_locations[:, :, :, level]
+        mode = sampler
+        if mode == "auto":
+            mode = "matmul" if height * width <= MATMUL_SAMPLER_MAX_LEVEL else "gather"
+        if mode == "pallas" or not bf16_value:
+            idx, w, _, _, _ = _corners(loc[..., 0], loc[..., 1], height, width, pallas=mode == "pallas")
+            sample = np.einsum("bqhpc,bqhpcd->bqhpd", w, _gather(v_l, idx))
+        else:
+            sample = _bf16_level_sample(v_l.astype(np.float32), loc, height, width, mode).astype(np.float64)
+        out += np.einsum("bqhp,bqhpd->bqhd", attn[:, :, :, level], sample)
+    return out.reshape(batch, len_query, n_heads * d)
+
+
+def ms_deform_attn_core_rows_vjp_pallas(value, spatial_shapes, sampling_locations, attention_weights, grad_output):
+    """ms_deform_attn_core_rows_vjp at the Pallas sampler's pixel coordinates (deform_pallas.py:
+    97-120, 221-224): the same formulas, floor and fractions from loc * size - 0.5."""
+    return ms_deform_attn_core_rows_vjp(value, spatial_shapes, sampling_locations, attention_weights, grad_output, pallas=True)
 
 
 def brute_force_forward(value, spatial_shapes, sampling_locations, attention_weights):

@@ -258,6 +258,28 @@ msda::LevelDesc level_desc(const Shape& s, int l, int lds, int band_rows, int ba
   return d;
 }
 
+// The reference sampler a level reproduces (msda_fwd_sampler, msda_bwd_sampler): the forward's bf16
+// rounding points and the Pallas kernel's pixel coordinates (enum msda_sampler in msda.h).
+int check_sampler(int sampler) {
+  if (sampler < MSDA_SAMPLER_HIP || sampler > MSDA_SAMPLER_PALLAS) return fail(MSDA_ERR_INVALID_ARGUMENT, "unknown sampler code %d", sampler);
+  return MSDA_OK;
+}
+
+void apply_sampler(const Shape& s, int sampler, int value_dtype, msda::LevelDesc* lv) {
+  const bool bf16 = value_dtype == MSDA_DTYPE_BF16;
+  for (int l = 0; l < s.levels; ++l) {
+    int sm = sampler;
+    if (sm == MSDA_SAMPLER_AUTO)  // ops.py:277-279 with _MATMUL_SAMPLER_MAX_LEVEL = 4096 (ops.py:42)
+      sm = static_cast<int64_t>(s.h[l]) * s.w[l] <= 4096 ? MSDA_SAMPLER_MATMUL : MSDA_SAMPLER_GATHER;
+    lv[l].pallas_xy = sm == MSDA_SAMPLER_PALLAS ? 1 : 0;
+    lv[l].rmode = !bf16                             ? msda::kRoundNone
+                  : sm == MSDA_SAMPLER_GATHER       ? msda::kRoundGather
+                  : sm == MSDA_SAMPLER_GATHER_F32   ? msda::kRoundGatherF32
+                  : sm == MSDA_SAMPLER_MATMUL       ? msda::kRoundMatmul
+                                                    : msda::kRoundNone;
+  }
+}
+
 // ------------------------------------------------------------------------------------------
 // planning of the forward kernel
 
@@ -516,7 +538,8 @@ struct BandFusedArgs {
 
 int bwd_band_impl(const Shape& s, int ch, const void* value, int value_dtype, const float* loc, const float* attn,
                   const void* grad_output, int grad_output_dtype, void* grad_value, float* grad_loc, float* grad_attn, void* workspace,
-                  int64_t workspace_bytes, const DevInfo& dev, hipStream_t st, const BandFusedArgs* fa = nullptr) {
+                  int64_t workspace_bytes, const DevInfo& dev, hipStream_t st, const BandFusedArgs* fa = nullptr,
+                  int sampler = MSDA_SAMPLER_HIP) {
   const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   BandPlan bp;
   int rc = plan_band(s, vbytes, ch, dev, &bp);
@@ -567,6 +590,7 @@ int bwd_band_impl(const Shape& s, int ch, const void* value, int value_dtype, co
     p.lv[l] = level_desc(s, l, 0, bp.rows[l], first);
     first += bp.bands[l];
   }
+  apply_sampler(s, sampler, value_dtype, p.lv);
   const int grid = static_cast<int>(static_cast<int64_t>(s.batch) * s.heads * bp.nwork * p.nqb);
   if (fa != nullptr) {
     p.ref = fa->ref;
@@ -707,7 +731,7 @@ int64_t gather_workspace(const Shape& s, const GatherPlan& gp) {
 
 int bwd_gather_impl(const Shape& s, const void* value, int value_dtype, const float* loc, const float* attn, const void* grad_output,
                     int grad_output_dtype, void* grad_value, float* grad_loc, float* grad_attn, void* workspace,
-                    int64_t workspace_bytes, const DevInfo& dev, hipStream_t st) {
+                    int64_t workspace_bytes, const DevInfo& dev, hipStream_t st, int sampler = MSDA_SAMPLER_HIP) {
   const int vbytes = value_dtype == MSDA_DTYPE_BF16 ? 2 : 4;
   GatherPlan gp;
   int rc = plan_gather(s, vbytes, dev, &gp);
@@ -749,6 +773,7 @@ int bwd_gather_impl(const Shape& s, const void* value, int value_dtype, const fl
   p.lds_scan = gp.scan;
   p.lds_val = gp.val;
   for (int l = 0; l < s.levels; ++l) p.lv[l] = level_desc(s, l, 0, 1, 0);
+  apply_sampler(s, sampler, value_dtype, p.lv);
   const int grid = static_cast<int>(static_cast<int64_t>(s.batch) * s.heads * s.levels * gp.nqb);
   const bool gb = grad_output_dtype == MSDA_DTYPE_BF16;
   rc = value_dtype == MSDA_DTYPE_BF16 ? msda_host::dispatch_bwd_gather<msda::bf16_t>(s.dim, gb, p, grid, gp.threads, gp.lds, st)
@@ -804,13 +829,14 @@ void fill_fused(msda::SampleParams* p, const Fused* fz, int n_points) {
 
 int fwd_impl(const void* value, int value_dtype, const float* loc, const float* attn, void* output, int output_dtype, int batch,
              int n_heads, int head_dim, int len_query, int n_levels, int n_points, const int32_t* spatial_shapes,
-             const int32_t* level_start_index, int64_t len_value, void* stream, const Fused* fz) {
+             const int32_t* level_start_index, int64_t len_value, void* stream, const Fused* fz, int sampler = MSDA_SAMPLER_HIP) {
   g_last_error.clear();
   Shape s;
   int rc = validate(&s, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value);
   if (rc != MSDA_OK) return rc;
   if ((rc = check_dtype(value_dtype, "value")) != MSDA_OK) return rc;
   if ((rc = check_dtype(output_dtype, "output")) != MSDA_OK) return rc;
+  if ((rc = check_sampler(sampler)) != MSDA_OK) return rc;
   if (fz != nullptr && (rc = check_fused(*fz, batch == 0 ? 0 : len_query)) != MSDA_OK) return rc;
   if (batch == 0 || len_query == 0) return MSDA_OK;
   if (value == nullptr || loc == nullptr || attn == nullptr || output == nullptr)
@@ -845,9 +871,12 @@ int fwd_impl(const void* value, int value_dtype, const float* loc, const float* 
   fill_fused(&p, fz, n_points);
   SamplePlan plan;
   if ((rc = plan_sample(s, vbytes, dev, "MSDA_FWD", shift, &p, &plan)) != MSDA_OK) return rc;
+  apply_sampler(s, sampler, value_dtype, p.lv);
+  bool rounded = false;
+  for (int l = 0; l < n_levels; ++l) rounded = rounded || p.lv[l].rmode != msda::kRoundNone;
   // one level, two points, two lanes per (query, head), every level staged: the two lanes split the
-  // samples' coordinate work (fwd_pair)
-  p.pair_share = (n_levels == 1 && n_points == 2 && shift == 1 && p.all_staged && ns == 2 && env_int("MSDA_FWD_PAIR", 1)) ? 1 : 0;
+  // samples' coordinate work (fwd_pair; f32 interpolation only)
+  p.pair_share = (n_levels == 1 && n_points == 2 && shift == 1 && p.all_staged && ns == 2 && !rounded && env_int("MSDA_FWD_PAIR", 1)) ? 1 : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool fused = fz != nullptr;
   if (value_dtype == MSDA_DTYPE_BF16)
@@ -1014,11 +1043,12 @@ int64_t workspace_impl(int batch, int n_heads, int head_dim, int len_query, int 
 int bwd_impl(const void* value, int value_dtype, const float* loc, const float* attn, const void* grad_output, int grad_output_dtype,
              void* grad_value, float* grad_loc, float* grad_attn, int batch, int n_heads, int head_dim, int len_query, int n_levels,
              int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value, void* workspace,
-             int64_t workspace_bytes, void* stream, const Fused* fz) {
+             int64_t workspace_bytes, void* stream, const Fused* fz, int sampler = MSDA_SAMPLER_HIP) {
   g_last_error.clear();
   Shape s;
   int rc = validate(&s, batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value);
   if (rc != MSDA_OK) return rc;
+  if ((rc = check_sampler(sampler)) != MSDA_OK) return rc;
   if ((rc = check_dtype(value_dtype, "value")) != MSDA_OK) return rc;
   if ((rc = check_dtype(grad_output_dtype, "grad_output")) != MSDA_OK) return rc;
   const char* name = fz ? "msda_fused_bwd" : "msda_bwd";
@@ -1062,10 +1092,10 @@ int bwd_impl(const void* value, int value_dtype, const float* loc, const float* 
   if (len_query > 0 && gather_eligible(s) && gather_aligned(value, grad_value, grad_output, gbytes) &&
       plan_gather(s, vbytes, dev, &gp) == MSDA_OK)
     return bwd_gather_impl(s, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn,
-                           workspace, workspace_bytes, dev, st);
+                           workspace, workspace_bytes, dev, st, sampler);
   g_last_error.clear();
   return bwd_band_impl(s, ch, value, value_dtype, loc, attn, grad_output, grad_output_dtype, grad_value, grad_loc, grad_attn,
-                       workspace, workspace_bytes, dev, st);
+                       workspace, workspace_bytes, dev, st, nullptr, sampler);
 }
 
 }  // namespace
@@ -1098,6 +1128,14 @@ int msda_fwd(const void* value, int value_dtype, const float* sampling_locations
                   n_levels, n_points, spatial_shapes, level_start_index, len_value, stream, nullptr);
 }
 
+int msda_fwd_sampler(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
+                     void* output, int output_dtype, int sampler, int batch, int n_heads, int head_dim, int len_query, int n_levels,
+                     int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value,
+                     void* stream) {
+  return fwd_impl(value, value_dtype, sampling_locations, attention_weights, output, output_dtype, batch, n_heads, head_dim, len_query,
+                  n_levels, n_points, spatial_shapes, level_start_index, len_value, stream, nullptr, sampler);
+}
+
 int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_query, int n_levels, int n_points,
                                 const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value) {
   return workspace_impl(batch, n_heads, head_dim, len_query, n_levels, n_points, spatial_shapes, level_start_index, len_value, 0);
@@ -1111,6 +1149,16 @@ int msda_bwd(const void* value, int value_dtype, const float* sampling_locations
   return bwd_impl(value, value_dtype, sampling_locations, attention_weights, grad_output, grad_output_dtype, grad_value,
                   grad_sampling_locations, grad_attention_weights, batch, n_heads, head_dim, len_query, n_levels, n_points,
                   spatial_shapes, level_start_index, len_value, workspace, workspace_bytes, stream, nullptr);
+}
+
+int msda_bwd_sampler(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,
+                     const void* grad_output, int grad_output_dtype, void* grad_value, float* grad_sampling_locations,
+                     float* grad_attention_weights, int sampler, int batch, int n_heads, int head_dim, int len_query, int n_levels,
+                     int n_points, const int32_t* spatial_shapes, const int32_t* level_start_index, int64_t len_value,
+                     void* workspace, int64_t workspace_bytes, void* stream) {
+  return bwd_impl(value, value_dtype, sampling_locations, attention_weights, grad_output, grad_output_dtype, grad_value,
+                  grad_sampling_locations, grad_attention_weights, batch, n_heads, head_dim, len_query, n_levels, n_points,
+                  spatial_shapes, level_start_index, len_value, workspace, workspace_bytes, stream, nullptr, sampler);
 }
 
 int msda_bwd_noalloc(const void* value, int value_dtype, const float* sampling_locations, const float* attention_weights,

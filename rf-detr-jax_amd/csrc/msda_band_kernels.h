@@ -104,7 +104,7 @@ __device__ __forceinline__ BandItem band_item(const BandParams& p, int k) {
 // The clipped rows of a sample's two corner rows (ops.py:103-118 clip y0 and y0 + 1 into the
 // level); a non-finite coordinate clamps to -2, i.e. both rows clip to 0, where bilinear() puts it.
 __device__ __forceinline__ int2 clipped_rows(float ly, const LevelDesc& L) {
-  const float iy = pixel_coord(ly, L.fh);
+  const float iy = level_coord(ly, L.fh, L);
   const int y0 = static_cast<int>(fminf(fmaxf(floorf(iy), -2.0f), L.fh));
   return make_int2(min(max(y0, 0), L.h - 1), min(max(y0 + 1, 0), L.h - 1));
 }

@@ -39,7 +39,19 @@ struct LevelDesc {
   int lds;         // per-sample kernels: element offset of the staged level inside a head's LDS region, -1 = L2
   int band_rows;   // backward band kernel: image rows per band
   int band_first;  // backward band kernel: index of the level's first band among a slice's (level, band) items
+  // The reference sampler the level reproduces (msda_fwd_sampler / msda_bwd_sampler):
+  int rmode;      // forward rounding of a bf16 value map: kRoundNone, kRoundGather, kRoundGatherF32, kRoundMatmul
+  int pallas_xy;  // pixel coordinates as the Pallas sampler forms them, loc * size - 0.5
 };
+
+// Forward rounding points of the reference's samplers on a bf16 value map (ops.py:64-186):
+//   kRoundNone       f32 interpolation of the bf16 values, the weighted sum over points in f32;
+//   kRoundGather     "gather": fractions, 1 - fraction, the corner-weight products, each corner
+//                    product and the four-corner sum rounded to bf16 (ops.py:88-91, :123, :134);
+//   kRoundGatherF32  "gather-f32": f32 interpolation, the sample rounded to bf16 (ops.py:137-144);
+//   kRoundMatmul     "matmul": the axis kernels and their outer product rounded to bf16, the
+//                    contraction with the values in f32, its result rounded to bf16 (ops.py:163-186).
+enum RoundMode { kRoundNone = 0, kRoundGather = 1, kRoundGatherF32 = 2, kRoundMatmul = 3 };
 
 // Forward kernels.
 struct SampleParams {
@@ -96,6 +108,21 @@ __device__ __forceinline__ float pixel_coord(float loc, float size) {
   return ((grid + 1.0f) * size - 1.0f) * 0.5f;
 }
 
+// The pixel coordinate of a location along one axis of level L: ops.py's formula, or the Pallas
+// sampler's (LevelDesc::pallas_xy). Every kernel that decides a sample's cell goes through it, so
+// a band's scan and the sample's corners agree on the floor.
+// Written without a branch: ops.py's ((grid + 1) * size - 1) * 0.5 and the Pallas kernel's
+// (loc * size - 0.5) * 1 share the multiply by size and differ in its operand and in two constants,
+// so both cost the same six operations (a branch here stalled the backward's item loop).
+__device__ __forceinline__ float level_coord(float loc, float size, const LevelDesc& L) {
+#pragma clang fp contract(off)
+  const bool pallas = L.pallas_xy != 0;
+  const float grid1 = (2.0f * loc - 1.0f) + 1.0f;  // ops.py:270 then + 1 (2 * loc is exact)
+  const float x = pallas ? loc : grid1;
+  const float c = pallas ? 0.5f : 1.0f, half = pallas ? 1.0f : 0.5f;
+  return (x * size - c) * half;  // ops.py:83-84 (dividing by two is exact) / deform_pallas.py:223-224
+}
+
 struct Bilinear {
   int o00, o10, o01, o11;      // element offsets (clipped pixel index * dim) of the corners in the level
   float w00, w10, w01, w11;    // masked corner weights
@@ -110,8 +137,8 @@ struct Bilinear {
 __device__ __forceinline__ Bilinear bilinear(float lx, float ly, const LevelDesc& L, int dim) {
   Bilinear c;
   const int h = L.h, w = L.w;
-  const float ix = pixel_coord(lx, L.fw);
-  const float iy = pixel_coord(ly, L.fh);
+  const float ix = level_coord(lx, L.fw, L);
+  const float iy = level_coord(ly, L.fh, L);
   const float x0f = floorf(ix), y0f = floorf(iy);
   c.fx = ix - x0f;  // rounded in f32 like ops.py:88-89 (inexact only for ix in (-1, 0))
   c.fy = iy - y0f;
@@ -627,6 +654,54 @@ __device__ __forceinline__ void fwd_corners(float (&acc)[VEC], const VT* base, c
   for (int k = 0; k < VEC; ++k) acc[k] = fmaf(u1[k], a11, fmaf(u0[k], a01, acc[k]));
 }
 
+// The corners of one sample at a level with a reference sampler's bf16 rounding points (RoundMode),
+// added into acc as a * sample. Values are read in the lane's rotated chunk order; the rounding is
+// per channel, so the order does not matter. Products and sums are not contracted.
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+template <typename VT, int VEC, bool kLds>
+__device__ __forceinline__ void fwd_corners_rounded(float (&acc)[VEC], const VT* base, const Bilinear& c, float a, int rot, int mode) {
+#pragma clang fp contract(off)
+  float w00, w10, w01, w11;
+  if (mode == kRoundGather) {
+    const float wx1 = round_bf16(c.fx), wy1 = round_bf16(c.fy);
+    const float wx0 = round_bf16(1.0f - wx1), wy0 = round_bf16(1.0f - wy1);
+    w00 = round_bf16(wx0 * wy0) * c.m00;
+    w10 = round_bf16(wx1 * wy0) * c.m10;
+    w01 = round_bf16(wx0 * wy1) * c.m01;
+    w11 = round_bf16(wx1 * wy1) * c.m11;
+  } else if (mode == kRoundMatmul) {
+    const float kx0 = round_bf16(1.0f - c.fx), kx1 = round_bf16(c.fx);
+    const float ky0 = round_bf16(1.0f - c.fy), ky1 = round_bf16(c.fy);
+    w00 = round_bf16(ky0 * kx0) * c.m00;
+    w10 = round_bf16(ky0 * kx1) * c.m10;
+    w01 = round_bf16(ky1 * kx0) * c.m01;
+    w11 = round_bf16(ky1 * kx1) * c.m11;
+  } else {  // kRoundGatherF32: the f32 weights of ops.py:123-128
+    w00 = c.w00;
+    w10 = c.w10;
+    w01 = c.w01;
+    w11 = c.w11;
+  }
+  float u00[VEC], u10[VEC], u01[VEC], u11[VEC];
+  load_rot<VT, VEC, kLds>(base + c.o00, rot, u00);
+  load_rot<VT, VEC, kLds>(base + c.o10, rot, u10);
+  load_rot<VT, VEC, kLds>(base + c.o01, rot, u01);
+  load_rot<VT, VEC, kLds>(base + c.o11, rot, u11);
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    float p00 = u00[k] * w00, p10 = u10[k] * w10, p01 = u01[k] * w01, p11 = u11[k] * w11;
+    if (mode == kRoundGather) {
+      p00 = round_bf16(p00);
+      p10 = round_bf16(p10);
+      p01 = round_bf16(p01);
+      p11 = round_bf16(p11);
+    }
+    const float sample = round_bf16(((p00 + p10) + p01) + p11);
+    acc[k] = fmaf(a, sample, acc[k]);
+  }
+}
+
 // kStaged: every level is staged in LDS (no L2 gather path is compiled).
 template <typename VT, int VEC, int N, bool kStaged>
 __device__ __forceinline__ void fwd_pass(float (&acc)[VEC], const SampleIn<N>& f, int s0, int LP, int& l, int& pt,
@@ -638,8 +713,14 @@ __device__ __forceinline__ void fwd_pass(float (&acc)[VEC], const SampleIn<N>& f
       const LevelDesc L = p.lv[l];
       const Bilinear c = bilinear(f.xy[u].x, f.xy[u].y, L, D);
       // Separate LDS and global paths: a pointer that may be either compiles to flat loads.
-      if (kStaged || L.lds >= 0) fwd_corners<VT, VEC, true>(acc, hlds + L.lds, c, f.a[u], rot);
-      else fwd_corners<VT, VEC, false>(acc, vs + static_cast<int64_t>(L.start) * D, c, f.a[u], rot);
+      if (L.rmode != kRoundNone) {
+        if (kStaged || L.lds >= 0) fwd_corners_rounded<VT, VEC, true>(acc, hlds + L.lds, c, f.a[u], rot, L.rmode);
+        else fwd_corners_rounded<VT, VEC, false>(acc, vs + static_cast<int64_t>(L.start) * D, c, f.a[u], rot, L.rmode);
+      } else if (kStaged || L.lds >= 0) {
+        fwd_corners<VT, VEC, true>(acc, hlds + L.lds, c, f.a[u], rot);
+      } else {
+        fwd_corners<VT, VEC, false>(acc, vs + static_cast<int64_t>(L.start) * D, c, f.a[u], rot);
+      }
       if (++pt == p.points) {
         pt = 0;
         ++l;

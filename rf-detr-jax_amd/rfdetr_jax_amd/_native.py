@@ -33,8 +33,10 @@ SIGNATURES = {
     "msda_last_error": ([], ctypes.c_char_p),
     "msda_set_tuning": ([ctypes.c_char_p, ctypes.c_char_p], _I),
     "msda_fwd": ([_P, _I, _P, _P, _P, _I] + _DIMS + [_P], _I),
+    "msda_fwd_sampler": ([_P, _I, _P, _P, _P, _I, _I] + _DIMS + [_P], _I),
     "msda_bwd_workspace_size": (list(_DIMS), _I64),
     "msda_bwd": ([_P, _I, _P, _P, _P, _I, _P, _P, _P] + _DIMS + [_P, _I64, _P], _I),
+    "msda_bwd_sampler": ([_P, _I, _P, _P, _P, _I, _P, _P, _P, _I] + _DIMS + [_P, _I64, _P], _I),
     "msda_bwd_noalloc": ([_P, _I, _P, _P, _P, _I, _P, _P, _P] + _DIMS + [_P], _I),
     "msda_fused_fwd": ([_P, _I, _P, _I, _P, _P, _P, _I] + _DIMS + [_P], _I),
     "msda_fused_bwd_workspace_size": ([_I] * 7 + [_I32P, _I32P, _I64], _I64),

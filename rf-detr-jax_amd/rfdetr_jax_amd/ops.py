@@ -6,9 +6,12 @@ Mirrors ``rfdetr_jax.models.ops`` (src/rfdetr_jax/models/ops.py):
   ``spatial_shapes`` as Python ints, ``sampling_locations [B, Q, H, L, P, 2]``,
   ``attention_weights [B, Q, H, L*P]``, ``sampler``), same result ``[B, Q, H*D]`` with dtype
   ``result_type(value, attention_weights)`` (ops.py:260), same ``ValueError`` for an unknown
-  sampler (ops.py:235-238). Every sampler name the reference accepts selects the HIP kernels:
-  they compute the same function (the reference's tests hold them to 1e-5 of each other,
-  tests/test_ops.py:112-248), so configurations that name one keep working unchanged.
+  sampler (ops.py:235-238). Every sampler name the reference accepts selects the HIP kernels, with
+  that sampler's rounding points in the forward: on a bf16 value map ``"gather"``,
+  ``"gather-f32"``, ``"matmul"`` and ``"auto"`` round where ops.py:64-186 rounds, and ``"pallas"``
+  forms pixel coordinates as deform_pallas.py:223-224 does (include/msda.h, msda_fwd_sampler);
+  ``"hip"`` (the default) interpolates in f32 throughout. The backward is the f32 VJP at each
+  sampler's coordinates (msda_bwd_sampler).
 * :func:`ms_deform_attn_core` — ops.py:295-314, ``value [B, H, D, S]``.
 * :func:`ms_deform_attn` — the ``(value, spatial_shapes, level_start_index, sampling_locations,
   attention_weights)`` signature of the upstream Deformable-DETR op; ``level_start_index`` is
@@ -27,8 +30,10 @@ import torch
 
 from . import _native
 
-#: Sampler names accepted by ms_deform_attn_core_rows (the reference's five, ops.py:235, + "hip").
-SAMPLERS = ("hip", "gather", "gather-f32", "matmul", "auto", "pallas")
+#: Sampler names accepted by ms_deform_attn_core_rows (the reference's five, ops.py:235, + "hip"),
+#: with their codes in the C ABI (enum msda_sampler, include/msda.h).
+SAMPLER_CODES = {"hip": 0, "gather": 1, "gather-f32": 2, "matmul": 3, "auto": 4, "pallas": 5}
+SAMPLERS = tuple(SAMPLER_CODES)
 
 _VALUE_DTYPES = {torch.float32: _native.DTYPE_F32, torch.bfloat16: _native.DTYPE_BF16}
 
@@ -111,13 +116,23 @@ def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def _sampler_code(sampler: str) -> int:
+    if sampler not in SAMPLER_CODES:
+        raise ValueError(
+            f"unknown sampler {sampler!r}; expected 'gather', 'gather-f32', 'matmul', 'auto', 'pallas' or 'hip'"
+        )
+    return SAMPLER_CODES[sampler]
+
+
 def ms_deform_attn_forward(value, spatial_shapes, sampling_locations, attention_weights, level_start_index=None,
-                           out_dtype=None):
+                           out_dtype=None, sampler: str = "hip"):
     """One forward launch (no autograd): returns ``[B, Q, H*D]``.
 
     ``sampling_locations`` / ``attention_weights`` of another float dtype are converted to f32
-    first (the reference computes positions in at least f32, ops.py:80, :270).
+    first (the reference computes positions in at least f32, ops.py:80, :270). ``sampler`` picks the
+    rounding points of one of the reference's samplers (msda_fwd_sampler).
     """
+    code = _sampler_code(sampler)
     shapes = _as_shapes(spatial_shapes)
     _check_level_start_index(level_start_index, shapes)
     batch, len_query, n_heads, n_levels, n_points, head_dim = _check_inputs(
@@ -130,22 +145,26 @@ def ms_deform_attn_forward(value, spatial_shapes, sampling_locations, attention_
     out = torch.empty((batch, len_query, n_heads * head_dim), dtype=out_dtype, device=value.device)
     arr, starts = _shape_arrays(shapes)
     lib = _native.lib()
+    dims = (batch, n_heads, head_dim, len_query, n_levels, n_points, arr, starts, value.shape[1])
     with torch.cuda.device(value.device):
-        rc = lib.msda_fwd(
-            _ptr(value), _VALUE_DTYPES[value.dtype], _ptr(loc), _ptr(attn), _ptr(out), _VALUE_DTYPES[out_dtype],
-            batch, n_heads, head_dim, len_query, n_levels, n_points, arr, starts, value.shape[1], _stream(value.device),
-        )
+        head = (_ptr(value), _VALUE_DTYPES[value.dtype], _ptr(loc), _ptr(attn), _ptr(out), _VALUE_DTYPES[out_dtype])
+        if code == 0:
+            rc = lib.msda_fwd(*head, *dims, _stream(value.device))
+        else:
+            rc = lib.msda_fwd_sampler(*head, code, *dims, _stream(value.device))
     _native.check(rc)
     return out
 
 
 def ms_deform_attn_backward(value, spatial_shapes, sampling_locations, attention_weights, grad_output,
-                            level_start_index=None, needs=(True, True, True)):
+                            level_start_index=None, needs=(True, True, True), sampler: str = "hip"):
     """One backward launch: returns ``(grad_value, grad_sampling_locations, grad_attention_weights)``.
 
     ``grad_value`` has the value dtype (f32 accumulation, one rounding); the other two are f32.
-    Entries of ``needs`` that are false come back as ``None`` and are not computed.
+    Entries of ``needs`` that are false come back as ``None`` and are not computed. ``sampler``
+    picks the pixel coordinates of one of the reference's samplers (msda_bwd_sampler).
     """
+    code = _sampler_code(sampler)
     shapes = _as_shapes(spatial_shapes)
     _check_level_start_index(level_start_index, shapes)
     batch, len_query, n_heads, n_levels, n_points, head_dim = _check_inputs(
@@ -174,11 +193,12 @@ def ms_deform_attn_backward(value, spatial_shapes, sampling_locations, attention
         # the query blocks' partial grad_value sums (f32); torch's caching allocator serves it
         workspace = torch.empty((max(1, ws_bytes // 16), 4), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
-        rc = lib.msda_bwd(
-            _ptr(value), _VALUE_DTYPES[value.dtype], _ptr(loc), _ptr(attn), _ptr(grad_output),
-            _VALUE_DTYPES[grad_output.dtype], _ptr(grad_value), _ptr(grad_loc), _ptr(grad_attn),
-            *dims, _ptr(workspace), ws_bytes, _stream(dev),
-        )
+        head = (_ptr(value), _VALUE_DTYPES[value.dtype], _ptr(loc), _ptr(attn), _ptr(grad_output),
+                _VALUE_DTYPES[grad_output.dtype], _ptr(grad_value), _ptr(grad_loc), _ptr(grad_attn))
+        if code == 0:
+            rc = lib.msda_bwd(*head, *dims, _ptr(workspace), ws_bytes, _stream(dev))
+        else:
+            rc = lib.msda_bwd_sampler(*head, code, *dims, _ptr(workspace), ws_bytes, _stream(dev))
     _native.check(rc)
     return grad_value, grad_loc, grad_attn
 
@@ -187,10 +207,11 @@ class _MSDeformAttnFunction(torch.autograd.Function):
     """custom-VJP pair: forward = msda_fwd, backward = msda_bwd (deform_pallas.py:132-178 contract)."""
 
     @staticmethod
-    def forward(ctx, value, sampling_locations, attention_weights, shapes):
-        out = ms_deform_attn_forward(value, shapes, sampling_locations, attention_weights)
+    def forward(ctx, value, sampling_locations, attention_weights, shapes, sampler="hip"):
+        out = ms_deform_attn_forward(value, shapes, sampling_locations, attention_weights, sampler=sampler)
         ctx.save_for_backward(value, sampling_locations, attention_weights)
         ctx.shapes = shapes
+        ctx.sampler = sampler
         ctx.out_dtype = out.dtype
         return out
 
@@ -199,13 +220,13 @@ class _MSDeformAttnFunction(torch.autograd.Function):
         value, loc, attn = ctx.saved_tensors
         needs = ctx.needs_input_grad[:3]
         grad_output = grad_output.to(ctx.out_dtype)
-        gv, gl, ga = ms_deform_attn_backward(value, ctx.shapes, loc, attn, grad_output, needs=needs)
+        gv, gl, ga = ms_deform_attn_backward(value, ctx.shapes, loc, attn, grad_output, needs=needs, sampler=ctx.sampler)
         # Gradients come back in the input dtypes (deform_pallas.py:175).
         if gl is not None and gl.dtype != loc.dtype:
             gl = gl.to(loc.dtype)
         if ga is not None and ga.dtype != attn.dtype:
             ga = ga.to(attn.dtype)
-        return gv, gl, ga, None
+        return gv, gl, ga, None, None
 
 
 def ms_deform_attn_core_rows(value, spatial_shapes, sampling_locations, attention_weights, sampler: str = "hip"):
@@ -217,7 +238,8 @@ def ms_deform_attn_core_rows(value, spatial_shapes, sampling_locations, attentio
         sampling_locations: ``[B, Lq, n_heads, n_levels, n_points, 2]`` in ``[0, 1]`` (outside is
             zero-padded).
         attention_weights: ``[B, Lq, n_heads, n_levels * n_points]``.
-        sampler: one of :data:`SAMPLERS`; all select the HIP kernels.
+        sampler: one of :data:`SAMPLERS`; all select the HIP kernels, with the named sampler's
+            rounding points in the forward and its pixel coordinates in both directions.
 
     Returns:
         ``[B, Lq, n_heads * head_dim]`` with dtype ``result_type(value, attention_weights)``.
@@ -225,12 +247,9 @@ def ms_deform_attn_core_rows(value, spatial_shapes, sampling_locations, attentio
     Raises:
         ValueError: unknown ``sampler`` or inconsistent shapes.
     """
-    if sampler not in SAMPLERS:
-        raise ValueError(
-            f"unknown sampler {sampler!r}; expected 'gather', 'gather-f32', 'matmul', 'auto', 'pallas' or 'hip'"
-        )
+    _sampler_code(sampler)
     shapes = _as_shapes(spatial_shapes)
-    return _MSDeformAttnFunction.apply(value, sampling_locations, attention_weights, shapes)
+    return _MSDeformAttnFunction.apply(value, sampling_locations, attention_weights, shapes, sampler)
 
 
 def ms_deform_attn(value, spatial_shapes, level_start_index, sampling_locations, attention_weights):

@@ -63,36 +63,45 @@ def _starts(vals):
     return (ctypes.c_int32 * len(vals))(*vals)
 
 
-def _fwd(**kw):
+def _fwd(sampler=None, **kw):
+    """msda_fwd, or msda_fwd_sampler with the given sampler code."""
     args = dict(value=1 << 20, vdt=0, loc=1 << 20, attn=1 << 20, out=1 << 20, odt=0, batch=1, heads=2, dim=16,
                 queries=4, levels=1, points=2, shapes=_shapes([(4, 4)]), starts=_starts([0]), len_value=16)
     args.update(kw)
     lib = _native.lib()
-    rc = lib.msda_fwd(
-        ctypes.c_void_p(args["value"]), args["vdt"], ctypes.c_void_p(args["loc"]), ctypes.c_void_p(args["attn"]),
-        ctypes.c_void_p(args["out"]), args["odt"], args["batch"], args["heads"], args["dim"], args["queries"],
-        args["levels"], args["points"], args["shapes"], args["starts"], args["len_value"], None,
-    )
+    head = (ctypes.c_void_p(args["value"]), args["vdt"], ctypes.c_void_p(args["loc"]), ctypes.c_void_p(args["attn"]),
+            ctypes.c_void_p(args["out"]), args["odt"])
+    dims = (args["batch"], args["heads"], args["dim"], args["queries"], args["levels"], args["points"], args["shapes"],
+            args["starts"], args["len_value"], None)
+    rc = lib.msda_fwd(*head, *dims) if sampler is None else lib.msda_fwd_sampler(*head, sampler, *dims)
     return rc, lib.msda_last_error().decode()
 
 
-def _bwd(**kw):
+def _bwd(sampler=None, **kw):
+    """msda_bwd, or msda_bwd_sampler with the given sampler code."""
     args = dict(value=1 << 20, vdt=0, loc=1 << 20, attn=1 << 20, gout=1 << 20, gdt=0, dv=1 << 20, dl=1 << 20,
                 da=1 << 20, batch=1, heads=2, dim=16, queries=4, levels=1, points=2, shapes=_shapes([(4, 4)]),
                 starts=_starts([0]), len_value=16, ws=1 << 20, ws_bytes=1 << 20)
     args.update(kw)
     lib = _native.lib()
-    rc = lib.msda_bwd(
-        ctypes.c_void_p(args["value"]), args["vdt"], ctypes.c_void_p(args["loc"]), ctypes.c_void_p(args["attn"]),
-        ctypes.c_void_p(args["gout"]), args["gdt"], ctypes.c_void_p(args["dv"]), ctypes.c_void_p(args["dl"]),
-        ctypes.c_void_p(args["da"]), args["batch"], args["heads"], args["dim"], args["queries"], args["levels"],
-        args["points"], args["shapes"], args["starts"], args["len_value"], ctypes.c_void_p(args["ws"]),
-        args["ws_bytes"], None,
-    )
+    head = (ctypes.c_void_p(args["value"]), args["vdt"], ctypes.c_void_p(args["loc"]), ctypes.c_void_p(args["attn"]),
+            ctypes.c_void_p(args["gout"]), args["gdt"], ctypes.c_void_p(args["dv"]), ctypes.c_void_p(args["dl"]),
+            ctypes.c_void_p(args["da"]))
+    dims = (args["batch"], args["heads"], args["dim"], args["queries"], args["levels"], args["points"], args["shapes"],
+            args["starts"], args["len_value"], ctypes.c_void_p(args["ws"]), args["ws_bytes"], None)
+    rc = lib.msda_bwd(*head, *dims) if sampler is None else lib.msda_bwd_sampler(*head, sampler, *dims)
     return rc, lib.msda_last_error().decode()
 
 
-@pytest.mark.parametrize("call", [_fwd, _bwd])
+def _fwd_gather(**kw):
+    return _fwd(sampler=1, **kw)
+
+
+def _bwd_pallas(**kw):
+    return _bwd(sampler=5, **kw)
+
+
+@pytest.mark.parametrize("call", [_fwd, _bwd, _fwd_gather, _bwd_pallas])
 @pytest.mark.parametrize(
     "kw, code, message",
     [
@@ -113,6 +122,13 @@ def test_invalid_arguments_are_reported(call, kw, code, message):
     rc, msg = call(**kw)
     assert rc == code, msg
     assert message in msg
+
+
+@pytest.mark.parametrize("call", [_fwd, _bwd])
+@pytest.mark.parametrize("code", [-1, 6, 99])
+def test_unknown_sampler_code_is_rejected(call, code):
+    rc, msg = call(sampler=code)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "unknown sampler code" in msg
 
 
 def test_two_levels_level_start_index_checked():

@@ -284,3 +284,134 @@ def test_bf16_gather_emulation_planted_mistake_and_gap():
     f32_path = R.ms_deform_attn_core_rows(value, shapes, loc, attn)
     gap = np.abs(emu - f32_path).max() / max(1.0, np.abs(f32_path).max())
     assert 1e-4 < gap < 2e-2, gap
+
+
+# --------------------------------------------------------------------------------------------
+# the samplers' rounding points (ms_deform_attn_core_rows_sampler)
+
+
+def _torch_bf16_sampler_level(value_l, loc, height, width, mode):
+    """The reference's per-level samplers written with torch tensors of the dtypes the reference
+    uses (ops.py:64-186): every bf16 operation rounds by itself, as XLA's bf16 arithmetic does, so
+    where the oracle places its explicit bf16 roundings is checked against arithmetic that rounds
+    at every step. value_l [N, S, D] bf16-representable float32; loc [N, L, 2]. Returns [N, L, D]."""
+    import torch
+
+    bf = torch.bfloat16
+    v = torch.from_numpy(value_l).to(bf)
+    g = 2 * torch.from_numpy(loc).float() - 1
+    ix = ((g[..., 0] + 1) * width - 1) / 2
+    iy = ((g[..., 1] + 1) * height - 1) / 2
+    ix0, iy0 = torch.floor(ix), torch.floor(iy)
+    if mode == "matmul":
+        wx1, wy1 = (ix - ix0)[..., None], (iy - iy0)[..., None]
+        cols = torch.arange(width, dtype=torch.float32)
+        rows = torch.arange(height, dtype=torch.float32)
+        kx = torch.where(cols == ix0[..., None], 1 - wx1, 0.0) + torch.where(cols == ix0[..., None] + 1, wx1, 0.0)
+        ky = torch.where(rows == iy0[..., None], 1 - wy1, 0.0) + torch.where(rows == iy0[..., None] + 1, wy1, 0.0)
+        kernel = (ky.to(bf)[..., :, None] * kx.to(bf)[..., None, :]).reshape(*loc.shape[:2], height * width)
+        return torch.bmm(kernel.float(), v.float()).to(bf).float().numpy()  # f32 contraction, bf16 result
+    dt = bf if mode == "gather" else torch.float32
+    vv = v.to(dt)
+    wx1, wy1 = (ix - ix0).to(dt)[..., None], (iy - iy0).to(dt)[..., None]
+    wx0, wy0 = 1 - wx1, 1 - wy1
+    x0, y0 = ix0.long(), iy0.long()
+    x1, y1 = x0 + 1, y0 + 1
+    ins = [((xx >= 0) & (xx < width) & (yy >= 0) & (yy < height)) for xx, yy in ((x0, y0), (x1, y0), (x0, y1), (x1, y1))]
+    idx = [yy.clamp(0, height - 1) * width + xx.clamp(0, width - 1) for xx, yy in ((x0, y0), (x1, y0), (x0, y1), (x1, y1))]
+    weights = [wx0 * wy0, wx1 * wy0, wx0 * wy1, wx1 * wy1]
+    prods = []
+    for c in range(4):
+        corner = torch.gather(vv, 1, idx[c][..., None].expand(-1, -1, vv.shape[-1]))
+        prods.append(corner * (weights[c] * ins[c][..., None].to(dt)))
+    total = torch.stack(prods, 1).float().sum(1)  # the four-corner sum in f32
+    return total.to(bf).float().numpy()
+
+
+@pytest.mark.parametrize("mode", ["gather", "gather-f32", "matmul"])
+def test_bf16_sampler_rounding_points_match_rounding_arithmetic(mode):
+    """The oracle's explicit bf16 roundings of each sampler equal torch arithmetic in the dtypes the
+    reference computes in (bf16 ops round after every operation): a missing or extra rounding
+    point changes some of the 1920 samples."""
+    rng = np.random.default_rng(5)
+    shapes = ((13, 17),)
+    n, q, p, d = 4, 60, 2, 8
+    value = R.bf16_round(rng.standard_normal((n, 13 * 17, d)).astype(np.float32))
+    loc = rng.uniform(-0.1, 1.1, (n, q * p, 2)).astype(np.float32)
+    want = _torch_bf16_sampler_level(value, loc, 13, 17, mode)
+    got = R._bf16_level_sample(value.reshape(1, n, -1, d), loc.reshape(1, q, n, p, 2).transpose(0, 1, 2, 3, 4).reshape(1, n, q, p, 2).transpose(0, 2, 1, 3, 4), 13, 17, mode)
+    got = got.transpose(0, 2, 1, 3, 4).reshape(n, q * p, d)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_sampler_emulations_exact_where_bf16_is_exact():
+    """Every sampler's emulation equals the float64 forward when each rounding it applies is exact:
+    quarter-pixel positions on power-of-two levels (both pixel-coordinate formulas exact; fractions
+    and weight products multiples of 1/16), integer values in [-2, 2]."""
+    rng = np.random.default_rng(12)
+    shapes = ((8, 8), (4, 8))
+    b, q, h, d, p = 2, 9, 2, 4, 3
+    s = sum(hh * ww for hh, ww in shapes)
+    value = rng.integers(-2, 3, size=(b * h, s, d)).astype(np.float32)
+    loc = np.empty((b, q, h, len(shapes), p, 2), np.float32)
+    for lvl, (hh, ww) in enumerate(shapes):
+        loc[:, :, :, lvl, :, 0] = (rng.integers(-6, 4 * ww + 3, size=(b, q, h, p)) / 4.0 + 0.5) / ww
+        loc[:, :, :, lvl, :, 1] = (rng.integers(-6, 4 * hh + 3, size=(b, q, h, p)) / 4.0 + 0.5) / hh
+    attn = rng.random((b, q, h, len(shapes) * p)).astype(np.float32)
+    want = R.ms_deform_attn_core_rows(value, shapes, loc, attn)
+    for sampler in ("gather", "gather-f32", "matmul", "auto", "pallas"):
+        for bf in (True, False):
+            got = R.ms_deform_attn_core_rows_sampler(value, shapes, loc, attn, sampler, bf)
+            np.testing.assert_array_equal(got, want, err_msg=f"{sampler} bf16={bf}")
+
+
+def test_pallas_pixel_coordinates():
+    """The Pallas sampler's coordinates are loc * size - 0.5 in float32 (two roundings, torch f32
+    arithmetic as the checker); at an 80-wide level they differ from ops.py's
+    ((2 loc - 1 + 1) size - 1) / 2 for some positions, and where a floor decision differs the
+    sampler's output does."""
+    import torch
+
+    # positions within a few ulps of the cell boundaries (k + 1/2) / 80, where a floor can flip
+    edges = ((np.arange(-1, 81) + 0.5) / 80).astype(np.float32)
+    steps = np.arange(-8, 9)
+    loc = np.array([np.nextafter(e, np.float32(2 if k > 0 else -1)) if k else e for e in edges for k in steps], np.float32)
+    for _ in range(7):  # widen to +-8 ulps
+        loc = np.concatenate([loc, np.nextafter(loc, np.float32(2)), np.nextafter(loc, np.float32(-1))])
+    want = (torch.from_numpy(loc) * 80.0 - 0.5).numpy()
+    np.testing.assert_array_equal(R._pallas_coords(loc, 80), want)
+    gather_xy = R._pixel_coords(loc, 80).astype(np.float32)
+    differ = np.floor(want) != np.floor(gather_xy)
+    assert differ.any() and (want != gather_xy).mean() > 0.01
+    # one sample at a position whose floor differs: the two samplers read different cells
+    inner = differ & (np.floor(want) >= 1) & (np.floor(want) <= 77)
+    assert inner.any()
+    x = loc[np.argmax(inner)]
+    value = np.arange(80 * 2, dtype=np.float32).reshape(1, 160, 1)
+    sl = np.array([x, 0.25], np.float32).reshape(1, 1, 1, 1, 1, 2)
+    a = np.ones((1, 1, 1, 1), np.float32)
+    out_p = R.ms_deform_attn_core_rows_sampler(value, ((2, 80),), sl, a, "pallas", False)
+    out_g = R.ms_deform_attn_core_rows_sampler(value, ((2, 80),), sl, a, "gather", False)
+    assert out_p[0, 0, 0] != out_g[0, 0, 0]
+
+
+def test_pallas_vjp_is_the_vjp_at_pallas_coordinates():
+    """ms_deform_attn_core_rows_vjp_pallas against central finite differences of the Pallas
+    forward emulation (float64 interpolation) in the value and the weights, and the identity
+    <G, out> = <dV, V> = <dA, A>."""
+    shapes = ((5, 7), (3, 4))
+    value, loc, attn, grad = make_inputs(21, 1, 2, 3, 6, shapes, 2)
+    out = R.ms_deform_attn_core_rows_sampler(value, shapes, loc, attn, "pallas", False)
+    gv, gl, ga = R.ms_deform_attn_core_rows_vjp_pallas(value, shapes, loc, attn, grad)
+    g = grad.astype(np.float64)
+    assert np.isclose((g * out).sum(), (gv * value).sum(), rtol=1e-10)
+    assert np.isclose((g * out).sum(), (ga * attn).sum(), rtol=1e-10)
+    eps = 1e-3
+    for i in range(0, value.size, 7):
+        vp = value.astype(np.float64).copy().reshape(-1)
+        vm = vp.copy()
+        vp[i] += eps
+        vm[i] -= eps
+        fp = R.ms_deform_attn_core_rows_sampler(vp.reshape(value.shape), shapes, loc, attn, "pallas", False)
+        fm = R.ms_deform_attn_core_rows_sampler(vm.reshape(value.shape), shapes, loc, attn, "pallas", False)
+        assert np.isclose((g * (fp - fm)).sum() / (2 * eps), gv.reshape(-1)[i], atol=1e-6)
