@@ -368,7 +368,7 @@ int msda_value_proj_bwd(const void* input, int dtype, const float* weight, const
  * 64 above the row maximum, and log2 of the softmax denominator taken relative to m, in units of
  * log2(e) q.k / sqrt(D)); the backward reads them and uses entry 2 for rowsum(grad_out * out).
  * Dropout on the attention weights (layers.py:537-544, active only with dropout > 0 in training)
- * is not part of this function. len is at most 65536, each row stride s_row below 2^24 elements
+ * is msda_attention_fwd_dropout's. len is at most 65536, each row stride s_row below 2^24 elements
  * and len * s_row below 2^31 (row offsets within a (slice, head) are formed in 32 bits).
  */
 int msda_attention_fwd(const void* q, const void* k, const void* v, int dtype, void* out, float* stats,
@@ -387,6 +387,44 @@ int msda_attention_bwd(const void* q, const void* k, const void* v, const void* 
                        const void* grad_out, int dtype, void* grad_q, void* grad_k, void* grad_v,
                        int batch, int groups, int heads, int len, int head_dim,
                        const int64_t* strides, const uint8_t* mask, void* stream);
+
+/*
+ * msda_attention_fwd with dropout on the softmax weights, as MultiheadAttention applies it in
+ * training (layers.py:537-544: weights = nn.Dropout(rate)(softmax(scores)), then weights @ v):
+ *   out = (softmax(...) * keep / (1 - rate)) v.
+ * keep(z, h, q, k) is a function of (seed, z * heads + h, q, k) alone: each kernel that needs it
+ * regenerates it, so the backward of the same call (same seed and rate) drops the same weights and
+ * nothing is stored. A weight is kept with probability 1 - round(rate * 65536) / 65536. The
+ * reference draws its mask from JAX's threefry stream (flax nn.Dropout): the distribution is the
+ * same, the particular mask is not. rate in [0, 1) (MSDA_ERR_INVALID_ARGUMENT otherwise); rate 0
+ * computes what msda_attention_fwd computes. stats as msda_attention_fwd's (the softmax of every
+ * weight, before dropout). Dropout runs in the chunked kernels (neither the staged bf16 forward nor
+ * the fused backward).
+ * No counterpart in the reference's C interface (its dropout is a JAX op around the product); for
+ * callers that train with attention dropout.
+ */
+int msda_attention_fwd_dropout(const void* q, const void* k, const void* v, int dtype, void* out, float* stats,
+                               int batch, int groups, int heads, int len, int head_dim,
+                               const int64_t* strides, const uint8_t* mask, float rate, uint64_t seed, void* stream);
+
+/*
+ * Backward of msda_attention_fwd_dropout (same rate and seed as the forward call):
+ *   dV = (P * keep / (1 - rate))^T dO,  dP = (dO V^T) * keep / (1 - rate),
+ *   dS = P (dP - rowsum(dO * out)),     dQ = dS K / sqrt(D),  dK = dS^T Q / sqrt(D).
+ * Arguments otherwise as msda_attention_bwd (always the two-kernel path).
+ */
+int msda_attention_bwd_dropout(const void* q, const void* k, const void* v, const void* out, float* stats,
+                               const void* grad_out, int dtype, void* grad_q, void* grad_k, void* grad_v,
+                               int batch, int groups, int heads, int len, int head_dim,
+                               const int64_t* strides, const uint8_t* mask, float rate, uint64_t seed, void* stream);
+
+/*
+ * The keep decisions of msda_attention_fwd_dropout for (rate, seed): keep[z * heads + h][q][k] = 1
+ * where weight (q, k) is kept, else 0 ([batch * groups * heads][len][len] bytes, z = g * batch + b).
+ * For tests and for callers that need the mask itself; no counterpart in the reference.
+ */
+int msda_attention_dropout_keep(int batch, int groups, int heads, int len, float rate, uint64_t seed,
+                                uint8_t* keep, void* stream);
 
 #ifdef __cplusplus
 }

@@ -9,7 +9,14 @@ It restates, in NumPy (float64 from the given inputs):
   path): ``softmax(q k^T / sqrt(D))`` over the keys with ``where(mask, finfo(f32).min, scores)``
   for blocked positions (:93-96), then ``@ v``;
 * ``sdpa_vjp``: its transpose: ``dV = P^T dO``, ``dP = dO V^T``, ``dS = P (dP - rowsum(dO * O))``,
-  ``dQ = dS K / sqrt(D)``, ``dK = dS^T Q / sqrt(D)``;
+  zero at blocked positions (``jnp.where``'s VJP gives the replaced scores no gradient; this
+  matters only in a row whose every key is blocked, where P is uniform), ``dQ = dS K / sqrt(D)``,
+  ``dK = dS^T Q / sqrt(D)``;
+* both with ``keep`` and ``rate``: the dropout branch of ``MultiheadAttention.__call__``
+  (layers.py:537-544): ``weights = nn.Dropout(rate)(softmax(scores))``, flax's Dropout being
+  ``where(keep, weights / (1 - rate), 0)`` for a Bernoulli(1 - rate) ``keep``, then ``weights @ v``.
+  The mask is an input here (the reference draws it from JAX's PRNG); the VJP is written in the
+  textbook softmax form ``dS = P (dP_in - rowsum(P dP_in))`` with ``dP_in = (dO V^T) keep / (1 - rate)``;
 * ``split_groups`` / ``merge_groups``: ``_split_groups`` / ``_merge_groups``
   (src/rfdetr_jax/models/transformer.py:350-361): group ``g`` of image ``b`` is batch row
   ``g * B + b``;
@@ -19,7 +26,8 @@ It restates, in NumPy (float64 from the given inputs):
   (transformer.py:200-210): ``query = key = tgt + query_pos``, ``value = tgt``, groups folded onto
   the batch in training, the output merged back.
 
-Pinning (tests/test_attention_oracle.py): torch float64 ``F.scaled_dot_product_attention`` and
+Pinning (tests/test_attention_oracle.py): torch float64 ``F.scaled_dot_product_attention`` (with
+``dropout_p`` replaced by an explicit mask: torch float64 autograd of the composed ops) and
 ``nn.MultiheadAttention(batch_first=True)`` under autograd (outputs and every gradient); the
 reference's own checks (tests/test_attention.py: a masked key block against -inf masking; equal
 scores give the mean of V; tests/test_transformer.py:20-38: folding round-trips and group ``g`` of
@@ -48,19 +56,28 @@ def _probs(q, k, mask):
     return e / e.sum(-1, keepdims=True)
 
 
-def sdpa(q, k, v, mask=None):
-    """``[..., L, D]`` inputs (any leading axes) -> ``[..., L, D]`` float64. ``mask [L, L]``: True blocks."""
-    return _probs(q, k, mask) @ np.asarray(v, np.float64)
+def _dropped(p, keep, rate):
+    """flax ``nn.Dropout``: ``where(keep, p / (1 - rate), 0)``; ``keep`` None: ``p``."""
+    if keep is None:
+        return p
+    return np.where(np.asarray(keep, bool), p / (1.0 - rate), 0.0)
 
 
-def sdpa_vjp(q, k, v, grad, mask=None):
+def sdpa(q, k, v, mask=None, keep=None, rate=0.0):
+    """``[..., L, D]`` inputs (any leading axes) -> ``[..., L, D]`` float64. ``mask [L, L]``: True
+    blocks. ``keep [..., L, L]`` (True keeps a weight) with ``rate``: the dropout branch."""
+    return _dropped(_probs(q, k, mask), keep, rate) @ np.asarray(v, np.float64)
+
+
+def sdpa_vjp(q, k, v, grad, mask=None, keep=None, rate=0.0):
     """``(dq, dk, dv)`` of :func:`sdpa` for the cotangent ``grad``."""
     p = _probs(q, k, mask)
     q, k, v, g = (np.asarray(t, np.float64) for t in (q, k, v, grad))
-    out = p @ v
-    dv = np.swapaxes(p, -1, -2) @ g
-    dp = g @ np.swapaxes(v, -1, -2)
-    ds = p * (dp - (g * out).sum(-1, keepdims=True))
+    dv = np.swapaxes(_dropped(p, keep, rate), -1, -2) @ g
+    dp = _dropped(g @ np.swapaxes(v, -1, -2), keep, rate)  # the gradient of the softmax weights
+    ds = p * (dp - (p * dp).sum(-1, keepdims=True))
+    if mask is not None:  # where(mask, finfo.min, scores) passes no gradient to blocked scores
+        ds = np.where(np.asarray(mask, bool), 0.0, ds)
     scale = 1.0 / np.sqrt(q.shape[-1])
     return ds @ k * scale, np.swapaxes(ds, -1, -2) @ q * scale, dv
 

@@ -84,50 +84,51 @@ int at_launch(K kernel, std::atomic<int> (&granted)[msda_host::kMaxDevices], con
   return msda_host::check_launch(what);
 }
 
-// The mask is a template parameter: without one the kernels carry no per-score mask code (and
-// need fewer registers).
-template <typename VT, int D, bool MASK, int RB>
+// The mask and dropout are template parameters: without them the kernels carry no per-score mask
+// or hash code (and need fewer registers). Dropout runs in the MASK instantiations, whose mask
+// pointer may then be null.
+template <typename VT, int D, bool MASK, int RB, bool DROP = false>
 int fwd_rb(const msda::AttnParams& p, hipStream_t st) {
   static std::atomic<int> granted[msda_host::kMaxDevices];
-  return at_launch(msda::attn_fwd_kernel<VT, D, MASK, RB>, granted, p, lds_bytes(D), RB, st, "attention forward");
+  return at_launch(msda::attn_fwd_kernel<VT, D, MASK, RB, DROP>, granted, p, lds_bytes(D), RB, st, "attention forward");
 }
 
-template <typename VT, int D, bool MASK>
+template <typename VT, int D, bool MASK, bool DROP = false>
 int fwd_typed(const msda::AttnParams& p, hipStream_t st) {
-  return fwd_rb<VT, D, MASK, 4>(p, st);
+  return fwd_rb<VT, D, MASK, 4, DROP>(p, st);
 }
 
-template <typename VT, int D, bool MASK, int RB>
+template <typename VT, int D, bool MASK, int RB, bool DROP = false>
 int bwd_rb(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
   int rc = MSDA_OK;
   {  // grad_q, and rowsum(dO * O) into the statistics for the key side (alone when grad_q is NULL)
     static std::atomic<int> granted[msda_host::kMaxDevices];
-    if ((rc = at_launch(msda::attn_bwd_q_kernel<VT, D, MASK, RB>, granted, p, lds_bytes(D), RB, st, "attention backward (queries)")) !=
-        MSDA_OK)
+    if ((rc = at_launch(msda::attn_bwd_q_kernel<VT, D, MASK, RB, DROP>, granted, p, lds_bytes(D), RB, st,
+                        "attention backward (queries)")) != MSDA_OK)
       return rc;
   }
   if (want_kv) {  // 4 key blocks per workgroup: with 2, the staging registers of the Q and dO chunks cost an occupancy step
     static std::atomic<int> granted[msda_host::kMaxDevices];
-    rc = at_launch(msda::attn_bwd_kv_kernel<VT, D, MASK, 4>, granted, p, lds_bytes(D), 4, st, "attention backward (keys, values)");
+    rc = at_launch(msda::attn_bwd_kv_kernel<VT, D, MASK, 4, DROP>, granted, p, lds_bytes(D), 4, st, "attention backward (keys, values)");
   }
   return rc;
 }
 
-template <typename VT, int D, bool MASK>
+template <typename VT, int D, bool MASK, bool DROP = false>
 int bwd_typed(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
-  return at_row_blocks(p.len) == 2 ? bwd_rb<VT, D, MASK, 2>(p, want_kv, st) : bwd_rb<VT, D, MASK, 4>(p, want_kv, st);
+  return at_row_blocks(p.len) == 2 ? bwd_rb<VT, D, MASK, 2, DROP>(p, want_kv, st) : bwd_rb<VT, D, MASK, 4, DROP>(p, want_kv, st);
 }
 
 // bf16 inputs: the bf16-MFMA kernels
-template <int D, bool MASK, int RB>
+template <int D, bool MASK, int RB, bool DROP = false>
 int fwd_b_rb(const msda::AttnParams& p, hipStream_t st) {
   static std::atomic<int> granted[msda_host::kMaxDevices];
-  return at_launch(msda::attn_fwd_bf16_kernel<D, MASK, RB>, granted, p, lds_bf16(D, false), RB, st, "attention forward");
+  return at_launch(msda::attn_fwd_bf16_kernel<D, MASK, RB, DROP>, granted, p, lds_bf16(D, false), RB, st, "attention forward");
 }
 
-template <int D, bool MASK>
+template <int D, bool MASK, bool DROP = false>
 int fwd_b(const msda::AttnParams& p, hipStream_t st) {
-  return fwd_b_rb<D, MASK, 4>(p, st);
+  return fwd_b_rb<D, MASK, 4, DROP>(p, st);
 }
 
 // Every row of tensor t starts on a 16-byte boundary (base pointer and all four strides).
@@ -152,25 +153,26 @@ int fwd_d32(const msda::AttnParams& p, hipStream_t st) {
   return at_launch(msda::attn_fwd_bf16_d32_kernel<4>, granted, p, tiles, 4, st, "attention forward");
 }
 
-template <int D, bool MASK, int RB>
+template <int D, bool MASK, int RB, bool DROP = false>
 int bwd_b_rb(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
   int rc = MSDA_OK;
   {
     static std::atomic<int> granted[msda_host::kMaxDevices];
-    if ((rc = at_launch(msda::attn_bwd_q_bf16_kernel<D, MASK, RB>, granted, p, lds_bf16(D, false), RB, st,
+    if ((rc = at_launch(msda::attn_bwd_q_bf16_kernel<D, MASK, RB, DROP>, granted, p, lds_bf16(D, false), RB, st,
                         "attention backward (queries)")) != MSDA_OK)
       return rc;
   }
   if (want_kv) {
     static std::atomic<int> granted[msda_host::kMaxDevices];
-    rc = at_launch(msda::attn_bwd_kv_bf16_kernel<D, MASK, 4>, granted, p, lds_bf16(D, true), 4, st, "attention backward (keys, values)");
+    rc = at_launch(msda::attn_bwd_kv_bf16_kernel<D, MASK, 4, DROP>, granted, p, lds_bf16(D, true), 4, st,
+                   "attention backward (keys, values)");
   }
   return rc;
 }
 
-template <int D, bool MASK>
+template <int D, bool MASK, bool DROP = false>
 int bwd_b(const msda::AttnParams& p, bool want_kv, hipStream_t st) {
-  return bwd_b_rb<D, MASK, 4>(p, want_kv, st);
+  return bwd_b_rb<D, MASK, 4, DROP>(p, want_kv, st);
 }
 
 // The fused backward: one workgroup per (slice, head), one wave per key block and two dQ waves.
@@ -202,7 +204,13 @@ bool use_fused(const msda::AttnParams& p, int d, bool want_kv) {
          msda_host::knob("MSDA_ATTN_FUSED", 1) != 0;
 }
 
-int fwd_dispatch(const msda::AttnParams& p, int d, bool bf16, hipStream_t st) {
+// Dropout (rate > 0) runs in the chunked kernels' MASK + DROP instantiations, neither the fused
+// backward nor the staged bf16 forward.
+int fwd_dispatch(const msda::AttnParams& p, int d, bool bf16, bool drop, hipStream_t st) {
+  if (drop) {
+    if (bf16) return d == 32 ? fwd_b<32, true, true>(p, st) : fwd_b<64, true, true>(p, st);
+    return d == 32 ? fwd_typed<float, 32, true, true>(p, st) : fwd_typed<float, 64, true, true>(p, st);
+  }
   const bool m = p.mask != nullptr;
   if (bf16) {
     if (use_fwd_d32(p, d)) return fwd_d32(p, st);
@@ -213,7 +221,11 @@ int fwd_dispatch(const msda::AttnParams& p, int d, bool bf16, hipStream_t st) {
   return m ? fwd_typed<float, 64, true>(p, st) : fwd_typed<float, 64, false>(p, st);
 }
 
-int bwd_dispatch(const msda::AttnParams& p, int d, bool bf16, bool want_kv, hipStream_t st) {
+int bwd_dispatch(const msda::AttnParams& p, int d, bool bf16, bool want_kv, bool drop, hipStream_t st) {
+  if (drop) {
+    if (bf16) return d == 32 ? bwd_b<32, true, true>(p, want_kv, st) : bwd_b<64, true, true>(p, want_kv, st);
+    return d == 32 ? bwd_typed<float, 32, true, true>(p, want_kv, st) : bwd_typed<float, 64, true, true>(p, want_kv, st);
+  }
   const bool m = p.mask != nullptr;
   if (use_fused(p, d, want_kv)) return bwd_fused(p, bf16, st);
   if (bf16) {
@@ -224,23 +236,31 @@ int bwd_dispatch(const msda::AttnParams& p, int d, bool bf16, bool want_kv, hipS
   return m ? bwd_typed<float, 64, true>(p, want_kv, st) : bwd_typed<float, 64, false>(p, want_kv, st);
 }
 
-}  // namespace
+// Dropout arguments: rate in [0, 1) (0: none), the call's seed. Fills p's dropout fields.
+int at_dropout(msda::AttnParams* p, float rate, uint64_t seed, int len) {
+  if (!(rate >= 0.0f && rate < 1.0f)) return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: dropout rate %g outside [0, 1)", static_cast<double>(rate));
+  (void)len;  // the hash keys (q, k / 2) are distinct for the at most 65536 rows at_validate admits
+  p->drop_seed[0] = static_cast<uint32_t>(seed);
+  p->drop_seed[1] = static_cast<uint32_t>(seed >> 32);
+  p->drop_thr = static_cast<uint32_t>(std::min(65536.0, std::nearbyint(static_cast<double>(rate) * 65536.0)));
+  p->drop_scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(rate)));
+  return MSDA_OK;
+}
 
-extern "C" {
-
-int msda_attention_fwd(const void* q, const void* k, const void* v, int dtype, void* out, float* stats, int batch, int groups, int heads,
-                       int len, int head_dim, const int64_t* strides, const uint8_t* mask, void* stream) {
+int attention_fwd(const void* q, const void* k, const void* v, int dtype, void* out, float* stats, int batch, int groups, int heads,
+                  int len, int head_dim, const int64_t* strides, const uint8_t* mask, float rate, uint64_t seed, void* stream) {
   msda_host::clear_error();
   int rc = at_validate(dtype, batch, groups, heads, len, head_dim, strides, 4);
   if (rc != MSDA_OK) return rc;
+  static const int order[4] = {msda::kAtQ, msda::kAtK, msda::kAtV, msda::kAtO};
+  msda::AttnParams p = at_params(dtype, batch, groups, heads, len, head_dim, strides, 4, order);
+  if ((rc = at_dropout(&p, rate, seed, len)) != MSDA_OK) return rc;
   if (batch == 0 || groups == 0 || heads == 0 || len == 0) return MSDA_OK;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || stats == nullptr)
     return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_attention_fwd: NULL tensor pointer");
   const size_t a = dtype == MSDA_DTYPE_BF16 ? 8 : 16;
   if (!aligned_to(q, a) || !aligned_to(k, a) || !aligned_to(v, a) || !aligned_to(out, a / 4) || !aligned_to(stats, 16))
     return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: q, k, v must be aligned to 4 elements");
-  static const int order[4] = {msda::kAtQ, msda::kAtK, msda::kAtV, msda::kAtO};
-  msda::AttnParams p = at_params(dtype, batch, groups, heads, len, head_dim, strides, 4, order);
   p.q = q;
   p.k = k;
   p.v = v;
@@ -248,15 +268,18 @@ int msda_attention_fwd(const void* q, const void* k, const void* v, int dtype, v
   p.stats = stats;
   p.mask = mask;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return fwd_dispatch(p, head_dim, dtype == MSDA_DTYPE_BF16, st);
+  return fwd_dispatch(p, head_dim, dtype == MSDA_DTYPE_BF16, rate > 0.0f, st);
 }
 
-int msda_attention_bwd(const void* q, const void* k, const void* v, const void* out, float* stats, const void* grad_out, int dtype,
-                       void* grad_q, void* grad_k, void* grad_v, int batch, int groups, int heads, int len, int head_dim,
-                       const int64_t* strides, const uint8_t* mask, void* stream) {
+int attention_bwd(const void* q, const void* k, const void* v, const void* out, float* stats, const void* grad_out, int dtype,
+                  void* grad_q, void* grad_k, void* grad_v, int batch, int groups, int heads, int len, int head_dim,
+                  const int64_t* strides, const uint8_t* mask, float rate, uint64_t seed, void* stream) {
   msda_host::clear_error();
   int rc = at_validate(dtype, batch, groups, heads, len, head_dim, strides, 8);
   if (rc != MSDA_OK) return rc;
+  static const int order[8] = {msda::kAtQ, msda::kAtK, msda::kAtV, msda::kAtO, msda::kAtGO, msda::kAtGQ, msda::kAtGK, msda::kAtGV};
+  msda::AttnParams p = at_params(dtype, batch, groups, heads, len, head_dim, strides, 8, order);
+  if ((rc = at_dropout(&p, rate, seed, len)) != MSDA_OK) return rc;
   const bool want_q = grad_q != nullptr, want_kv = grad_k != nullptr || grad_v != nullptr;
   if (batch == 0 || groups == 0 || heads == 0 || len == 0 || (!want_q && !want_kv)) return MSDA_OK;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || stats == nullptr || grad_out == nullptr)
@@ -265,8 +288,6 @@ int msda_attention_bwd(const void* q, const void* k, const void* v, const void* 
   if (!aligned_to(q, a) || !aligned_to(k, a) || !aligned_to(v, a) || !aligned_to(out, a) || !aligned_to(grad_out, a) ||
       !aligned_to(grad_q, a / 4) || !aligned_to(grad_k, a / 4) || !aligned_to(grad_v, a / 4) || !aligned_to(stats, 16))
     return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: q, k, v, out, grad_out must be aligned to 4 elements");
-  static const int order[8] = {msda::kAtQ, msda::kAtK, msda::kAtV, msda::kAtO, msda::kAtGO, msda::kAtGQ, msda::kAtGK, msda::kAtGV};
-  msda::AttnParams p = at_params(dtype, batch, groups, heads, len, head_dim, strides, 8, order);
   p.q = q;
   p.k = k;
   p.v = v;
@@ -278,7 +299,56 @@ int msda_attention_bwd(const void* q, const void* k, const void* v, const void* 
   p.stats = stats;
   p.mask = mask;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return bwd_dispatch(p, head_dim, dtype == MSDA_DTYPE_BF16, want_kv, st);
+  return bwd_dispatch(p, head_dim, dtype == MSDA_DTYPE_BF16, want_kv, rate > 0.0f, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int msda_attention_fwd(const void* q, const void* k, const void* v, int dtype, void* out, float* stats, int batch, int groups, int heads,
+                       int len, int head_dim, const int64_t* strides, const uint8_t* mask, void* stream) {
+  return attention_fwd(q, k, v, dtype, out, stats, batch, groups, heads, len, head_dim, strides, mask, 0.0f, 0, stream);
+}
+
+int msda_attention_bwd(const void* q, const void* k, const void* v, const void* out, float* stats, const void* grad_out, int dtype,
+                       void* grad_q, void* grad_k, void* grad_v, int batch, int groups, int heads, int len, int head_dim,
+                       const int64_t* strides, const uint8_t* mask, void* stream) {
+  return attention_bwd(q, k, v, out, stats, grad_out, dtype, grad_q, grad_k, grad_v, batch, groups, heads, len, head_dim, strides, mask,
+                       0.0f, 0, stream);
+}
+
+int msda_attention_fwd_dropout(const void* q, const void* k, const void* v, int dtype, void* out, float* stats, int batch, int groups,
+                               int heads, int len, int head_dim, const int64_t* strides, const uint8_t* mask, float rate, uint64_t seed,
+                               void* stream) {
+  return attention_fwd(q, k, v, dtype, out, stats, batch, groups, heads, len, head_dim, strides, mask, rate, seed, stream);
+}
+
+int msda_attention_bwd_dropout(const void* q, const void* k, const void* v, const void* out, float* stats, const void* grad_out, int dtype,
+                               void* grad_q, void* grad_k, void* grad_v, int batch, int groups, int heads, int len, int head_dim,
+                               const int64_t* strides, const uint8_t* mask, float rate, uint64_t seed, void* stream) {
+  return attention_bwd(q, k, v, out, stats, grad_out, dtype, grad_q, grad_k, grad_v, batch, groups, heads, len, head_dim, strides, mask,
+                       rate, seed, stream);
+}
+
+int msda_attention_dropout_keep(int batch, int groups, int heads, int len, float rate, uint64_t seed, uint8_t* keep, void* stream) {
+  msda_host::clear_error();
+  if (batch < 0 || groups < 0 || heads < 0 || len < 0) return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: negative extent");
+  if (static_cast<int64_t>(batch) * groups * heads >= (int64_t{1} << 31) || len > 65536)
+    return fail(MSDA_ERR_UNSUPPORTED, "attention: too many slices or rows");
+  msda::AttnParams p{};
+  p.batch = batch;
+  p.groups = groups;
+  p.heads = heads;
+  p.len = len;
+  int rc = at_dropout(&p, rate, seed, len);
+  if (rc != MSDA_OK) return rc;
+  const int64_t pairs = static_cast<int64_t>(batch) * groups * heads * len * ((len + 1) / 2);
+  if (pairs == 0) return MSDA_OK;
+  if (keep == nullptr) return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_attention_dropout_keep: NULL keep");
+  const int grid = static_cast<int>(std::min<int64_t>((pairs + 255) / 256, 4096));
+  hipLaunchKernelGGL(msda::attn_drop_keep_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), p, keep, pairs);
+  return msda_host::check_launch("attention dropout keep mask");
 }
 
 }  // extern "C"

@@ -19,8 +19,9 @@
 // reference score m (moved, and the partial sums rescaled, only when a chunk's maximum exceeds it
 // by more than kAtLazy), and stores per query m and log2 of the denominator l relative to m for
 // the backward, which recomputes the probabilities as exp2((x - m) - log2 l).
-// Blocked positions take the score finfo(float32).min as in the reference (:93-96); keys past L
-// take -inf (weight 0).
+// Blocked positions take the score finfo(float32).min as in the reference (:93-96), and, as
+// jnp.where's VJP, pass no gradient to it: the backward sets dS = 0 there (which matters only in a
+// row whose every key is blocked, where the weights are uniform). Keys past L take -inf (weight 0).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -52,9 +53,55 @@ struct AttnParams {
   int batch, groups, heads, len;
   float scale;   // 1 / sqrt(D)
   float scale2;  // log2(e) / sqrt(D)
+  // Dropout on the softmax weights (the DROP kernels): weight (q, k) of (slice, head) zh is dropped
+  // when its 16-bit hash (at_drop_bits) is below drop_thr, and kept weights are scaled by drop_scale.
+  uint32_t drop_seed[2];  // the call's 64-bit seed, low and high word
+  uint32_t drop_thr;      // round(rate * 65536)
+  float drop_scale;       // 1 / (1 - rate)
 };
 
 constexpr float kAtMaskScore = -3.4028234663852886e38f;  // finfo(float32).min
+
+// ---- attention dropout (layers.py:537-544: flax nn.Dropout on the softmax weights) ------------
+// Every kernel that touches weight (q, k) regenerates its keep decision from (seed, zh, q, k), so
+// nothing is stored between the forward and the backward. The hash is pcg_hash (the PCG-RXS-M-XS
+// output permutation applied to one LCG step; Jarzynski and Olano, "Hash Functions for GPU
+// Rendering", JCGT 9(3), 2020). Keys 2 kh and 2 kh + 1 of query q share one 32-bit hash of
+// base(zh) ^ (q << 16 | kh): the even key takes its low half, the odd key its high half, and a
+// weight is kept when that half is at least drop_thr, i.e. with probability 1 - drop_thr / 65536
+// (rate rounded to a multiple of 2^-16). The input is distinct for every (q, kh) while q < 2^16;
+// the host bounds the length for dropout accordingly.
+__device__ __forceinline__ uint32_t at_pcg(uint32_t v) {
+  const uint32_t st = v * 747796405u + 2891336453u;
+  const uint32_t w = ((st >> ((st >> 28u) + 4u)) ^ st) * 277803737u;
+  return (w >> 22u) ^ w;
+}
+
+__device__ __forceinline__ uint32_t at_drop_base(const AttnParams& p, int zh) {
+  return at_pcg(p.drop_seed[0] ^ at_pcg(p.drop_seed[1] + static_cast<uint32_t>(zh)));
+}
+
+// the shared hash of keys 2 kh and 2 kh + 1 of query q
+__device__ __forceinline__ uint32_t at_drop_bits(uint32_t base, int q, int kh) {
+  return at_pcg(base ^ ((static_cast<uint32_t>(q) << 16) | static_cast<uint32_t>(kh)));
+}
+
+__device__ __forceinline__ bool at_drop_keep(uint32_t base, int q, int key, uint32_t thr) {
+  const uint32_t h = at_drop_bits(base, q, key >> 1);
+  return ((key & 1) ? (h >> 16) : (h & 0xffffu)) >= thr;
+}
+
+// Transposed score blocks (register i: key k0 + 8 (i / 4) + 4 grp + i % 4, k0 even; the lane's
+// query q): each value times `kept` if its weight is kept, else 0. Registers i and i + 1 (i even)
+// hold keys 2 kh and 2 kh + 1 and share one hash.
+__device__ __forceinline__ void at_drop_t(at_f16& s, uint32_t base, int q, int k0, int grp, uint32_t thr, float kept) {
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const uint32_t h = at_drop_bits(base, q, (k0 + 8 * (i >> 2) + 4 * grp + (i & 3)) >> 1);
+    s[i] = (h & 0xffffu) >= thr ? s[i] * kept : 0.0f;
+    s[i + 1] = (h >> 16) >= thr ? s[i + 1] * kept : 0.0f;
+  }
+}
 
 template <typename VT>
 __device__ __forceinline__ at_f4 at_ld4(const VT* p, int64_t i) {  // elements i .. i + 3 as f32
@@ -388,8 +435,10 @@ struct AttnWork {
 };
 
 // Forward: out = softmax(q k^T / sqrt(D), blocked -> finfo.min) v. Each wave owns 32 queries; K and
-// V stream through LDS; the running maximum rescales the partial sums.
-template <typename VT, int D, bool MASK, int RB>
+// V stream through LDS; the running maximum rescales the partial sums. DROP (host: with MASK, the
+// mask may then be null): the dropped weights are zeroed before the product with V, the sum l and
+// the statistics keep every weight, and the output is scaled by drop_scale / l.
+template <typename VT, int D, bool MASK, int RB, bool DROP = false>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : (MASK ? 1 : 2)) attn_fwd_kernel(const AttnParams p) {
   constexpr int NT = 64 * RB;
   constexpr int LD = D + 8, ND = D / 32;
@@ -403,6 +452,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : (MASK ? 1 
   const int lane = threadIdx.x & 63, grp = lane >> 5, col = lane & 31;
   const int qb = w.rc * RB + (threadIdx.x >> 6), qi = qb * 32 + col;
   const bool qv = qi < L;
+  const uint32_t dbase = DROP ? at_drop_base(p, w.zh) : 0u;
   at_f4 qr[D / 8];
   {
     const VT* qp = static_cast<const VT*>(p.q) + w.sl.base(p, kAtQ);
@@ -428,7 +478,8 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : (MASK ? 1 
     if (qb >= nb) continue;
     at_f16 s0, s1;
     at_scores2<D>(s0, s1, Ks, qr, col, grp);
-    const float alpha = at_softmax_chunk<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, qv ? qi : -1, grp, m, l);
+    const int mrow = qv && (!DROP || p.mask != nullptr) ? qi : -1;
+    const float alpha = at_softmax_chunk<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, mrow, grp, m, l);
     if (alpha != 1.0f) {
 #pragma unroll
       for (int nd = 0; nd < ND; ++nd) {
@@ -436,12 +487,16 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : (MASK ? 1 
         o1[nd] *= alpha;
       }
     }
+    if constexpr (DROP) {
+      at_drop_t(s0, dbase, qi, j * kAtChunk, grp, p.drop_thr, 1.0f);
+      at_drop_t(s1, dbase, qi, j * kAtChunk + 32, grp, p.drop_thr, 1.0f);
+    }
     at_accum2<D>(o0, o1, Vs, Vs + 32 * LD, s0, s1, col, grp);  // O^T += V^T P^T, one chain per key block
   }
   __syncthreads();  // the chunk tiles hold the waves' output scratch from here
   if (qb < nb) {
     VT* op = static_cast<VT*>(p.out) + w.sl.base(p, kAtO);
-    const float inv = 1.0f / l;
+    const float inv = (DROP ? p.drop_scale : 1.0f) / l;
 #pragma unroll
     for (int nd = 0; nd < ND; ++nd) at_store_block<VT>(op + 32 * nd, p.st[kAtO][3], qb * 32, L, o0[nd] + o1[nd], inv, at_lds + (threadIdx.x >> 6) * (at_scratch_bytes<VT>() / 4), lane);
     if (qv && grp == 0) {
@@ -456,7 +511,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : (MASK ? 1 
 // recomputed from the stored statistics. Each wave owns 32 queries; K and V stream through LDS.
 // Also stores rowsum(dO * O) of its queries in the statistics for the key-side kernel (with no
 // grad_q requested, that is all it does).
-template <typename VT, int D, bool MASK, int RB>
+template <typename VT, int D, bool MASK, int RB, bool DROP = false>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? ((MASK || RB == 2) ? 2 : 3) : 1) attn_bwd_q_kernel(const AttnParams p) {
   constexpr int NT = 64 * RB;
   constexpr int LD = D + 8, ND = D / 32;
@@ -471,6 +526,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? ((MASK || RB == 2) ? 2 : 3)
   const int qb = w.rc * RB + (threadIdx.x >> 6), qi = qb * 32 + col;
   const bool qv = qi < L;
   const int qc = min(qi, L - 1);
+  const uint32_t dbase = DROP ? at_drop_base(p, w.zh) : 0u;
   at_f4 qr[D / 8], gr[D / 8];
   float dsum = 0.0f;  // rowsum(dO * O) over this lane's half of the channels, then both halves
   {
@@ -511,13 +567,16 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? ((MASK || RB == 2) ? 2 : 3)
     for (int h2 = 0; h2 < 2; ++h2) {  // the chunk's two key blocks in turn (half the score registers)
       at_f16 s, dp;
       at_scores_pair<D>(s, dp, Ks + 32 * h2 * LD, Vs + 32 * h2 * LD, qr, gr, col, grp);  // S^T, dP^T = V dO^T
+      // DROP: dP of the dropped weights' inputs, dP_in = dP * drop_scale where kept, else 0
+      if constexpr (DROP) at_drop_t(dp, dbase, qi, j * kAtChunk + 32 * h2, grp, p.drop_thr, p.drop_scale);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int key = j * kAtChunk + 32 * h2 + 8 * (i >> 2) + 4 * grp + (i & 3);
         float x = s[i] * p.scale2;
+        bool blocked = false;  // where(mask, finfo.min, .) passes the score no gradient
         if (key >= L) x = -INFINITY;
-        else if (MASK && qv && p.mask[static_cast<int64_t>(qi) * L + key] != 0) x = kAtMaskScore;
-        s[i] = at_exp2((x - m) - ll) * (dp[i] - dsum);  // dS^T
+        else if (MASK && qv && (!DROP || p.mask != nullptr) && p.mask[static_cast<int64_t>(qi) * L + key] != 0) x = kAtMaskScore, blocked = true;
+        s[i] = blocked ? 0.0f : at_exp2((x - m) - ll) * (dp[i] - dsum);  // dS^T
       }
       if (h2 == 0) at_accum1<D>(dq0, Ks, s, col, grp);  // dQ^T += K^T dS^T
       else at_accum1<D>(dq1, Ks + 32 * LD, s, col, grp);
@@ -535,7 +594,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? ((MASK || RB == 2) ? 2 : 3)
 // in registers) and forms S and dP untransposed (queries x keys), so a lane owns one key; Q, dO and
 // the per-query statistics (with rowsum(dO * O), written by the query-side kernel) stream through
 // LDS.
-template <typename VT, int D, bool MASK, int RB>
+template <typename VT, int D, bool MASK, int RB, bool DROP = false>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bwd_kv_kernel(const AttnParams p) {
   constexpr int NT = 64 * RB;
   constexpr int LD = D + 8, ND = D / 32;
@@ -551,6 +610,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bw
   const float* stats = p.stats + static_cast<int64_t>(w.zh) * L * 4;
   const int t = threadIdx.x, lane = t & 63, grp = lane >> 5, col = lane & 31;
   const int kb = w.rc * RB + (t >> 6), key = kb * 32 + col;
+  const uint32_t dbase = DROP ? at_drop_base(p, w.zh) : 0u;
   at_f4 kr[D / 8], vr[D / 8];
   {
     const VT* kp = static_cast<const VT*>(p.k) + w.sl.base(p, kAtK);
@@ -590,15 +650,22 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 1 : 3) : 1) attn_bw
         const int i = 4 * c4 + jj;
         // A lane past L holds the clamped last key (its mask entry too): finite values in its own
         // result column only, which is not stored. Rows past L have m = +inf: weight 0.
+        bool blocked = false;  // where(mask, finfo.min, .) passes the score no gradient: dS = 0
         if constexpr (MASK) {
           const int q = r0 + ql + jj;
           float x = s[i] * p.scale2;
-          if (q < L && p.mask[static_cast<int64_t>(q) * L + min(key, L - 1)] != 0) x = kAtMaskScore;
+          if (q < L && (!DROP || p.mask != nullptr) && p.mask[static_cast<int64_t>(q) * L + min(key, L - 1)] != 0) x = kAtMaskScore, blocked = true;
           pw[i] = at_exp2((x - mq[jj]) - lq[jj]);
         } else {
           pw[i] = at_exp2(fmaf(s[i], p.scale2, -mq[jj]) - lq[jj]);
         }
-        s[i] = pw[i] * (dp[i] - dd[jj]);  // dS
+        if constexpr (DROP) {  // dS from dP * drop_scale where kept; dV from the dropped weights
+          const bool keep = at_drop_keep(dbase, r0 + ql + jj, key, p.drop_thr);
+          s[i] = blocked ? 0.0f : pw[i] * ((keep ? dp[i] * p.drop_scale : 0.0f) - dd[jj]);
+          pw[i] = keep ? pw[i] * p.drop_scale : 0.0f;
+        } else {
+          s[i] = blocked ? 0.0f : pw[i] * (dp[i] - dd[jj]);  // dS
+        }
       }
     }
     at_accum2<D>(dv, dk, Gs + 32 * h2 * LD, Qs + 32 * h2 * LD, pw, s, col, grp);
@@ -759,7 +826,7 @@ __device__ __forceinline__ void at_accum_tr1(at_f16 (&acc)[D / 32], const uint16
     }
 }
 
-template <int D, bool MASK, int RB>
+template <int D, bool MASK, int RB, bool DROP = false>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel(const AttnParams p) {
   constexpr int NT = 64 * RB, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
@@ -772,6 +839,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
   const int lane = threadIdx.x & 63, grp = lane >> 5, col = lane & 31;
   const int qb = w.rc * RB + (threadIdx.x >> 6), qi = qb * 32 + col;
   const bool qv = qi < L;
+  const uint32_t dbase = DROP ? at_drop_base(p, w.zh) : 0u;
   at_bf8 qr[D / 16];
   at_row_bf8<D>(qr, static_cast<const uint16_t*>(p.q) + w.sl.base(p, kAtQ), min(qi, L - 1) * p.st[kAtQ][3], grp);
   float m = 0.0f, l = 0.0f;  // reference score and sum (at_softmax_chunk)
@@ -793,7 +861,8 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
     if (qb >= nb) continue;
     at_f16 s0, s1;
     at_scores_sw<D>(s0, s1, Kr, 0, Kr, 32, qr, qr, col, grp);  // S^T for the chunk's two key blocks
-    const float alpha = at_softmax_chunk<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, qv ? qi : -1, grp, m, l);
+    const int mrow = qv && (!DROP || p.mask != nullptr) ? qi : -1;
+    const float alpha = at_softmax_chunk<MASK>(s0, s1, j * kAtChunk, L, p.scale2, p.mask, mrow, grp, m, l);
     if (alpha != 1.0f) {
 #pragma unroll
       for (int nd = 0; nd < ND; ++nd) {
@@ -801,12 +870,16 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? 3 : 2) attn_fwd_bf16_kernel
         o1[nd] *= alpha;
       }
     }
+    if constexpr (DROP) {
+      at_drop_t(s0, dbase, qi, j * kAtChunk, grp, p.drop_thr, 1.0f);
+      at_drop_t(s1, dbase, qi, j * kAtChunk + 32, grp, p.drop_thr, 1.0f);
+    }
     at_accum_tr<D>(o0, o1, Vr, 0, Vr, 32, s0, s1, lane);  // O^T += V^T P^T
   }
   __syncthreads();  // the chunk tiles hold the waves' output scratch from here
   if (qb < nb) {
     bf16_t* op = static_cast<bf16_t*>(p.out) + w.sl.base(p, kAtO);
-    const float inv = 1.0f / l;
+    const float inv = (DROP ? p.drop_scale : 1.0f) / l;
 #pragma unroll
     for (int nd = 0; nd < ND; ++nd) at_store_block<bf16_t>(op + 32 * nd, p.st[kAtO][3], qb * 32, L, o0[nd] + o1[nd], inv, at_lds + (threadIdx.x >> 6) * (at_scratch_bytes<bf16_t>() / 4), lane);
     if (qv && grp == 0) {
@@ -1002,7 +1075,7 @@ __global__ void __launch_bounds__(64 * RB, 4) attn_fwd_bf16_d32_kernel(const Att
   }
 }
 
-template <int D, bool MASK, int RB>
+template <int D, bool MASK, int RB, bool DROP = false>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_q_bf16_kernel(const AttnParams p) {
   constexpr int NT = 64 * RB, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
@@ -1016,6 +1089,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
   const int qb = w.rc * RB + (threadIdx.x >> 6), qi = qb * 32 + col;
   const bool qv = qi < L;
   const int qc = min(qi, L - 1);
+  const uint32_t dbase = DROP ? at_drop_base(p, w.zh) : 0u;
   at_bf8 qr[D / 16], gr[D / 16];
   float dsum = 0.0f;
   {
@@ -1059,13 +1133,15 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
     for (int h2 = 0; h2 < 2; ++h2) {  // the chunk's two key blocks in turn (half the score registers)
       at_f16 s, dp;
       at_scores_sw<D>(s, dp, Kr, 32 * h2, Vr, 32 * h2, qr, gr, col, grp);  // S^T and dP^T = V dO^T
+      if constexpr (DROP) at_drop_t(dp, dbase, qi, j * kAtChunk + 32 * h2, grp, p.drop_thr, p.drop_scale);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int key = j * kAtChunk + 32 * h2 + 8 * (i >> 2) + 4 * grp + (i & 3);
         float x = s[i] * p.scale2;
+        bool blocked = false;  // where(mask, finfo.min, .) passes the score no gradient
         if (key >= L) x = -INFINITY;
-        else if (MASK && qv && p.mask[static_cast<int64_t>(qi) * L + key] != 0) x = kAtMaskScore;
-        s[i] = at_exp2((x - m) - ll) * (dp[i] - dsum);  // dS^T
+        else if (MASK && qv && (!DROP || p.mask != nullptr) && p.mask[static_cast<int64_t>(qi) * L + key] != 0) x = kAtMaskScore, blocked = true;
+        s[i] = blocked ? 0.0f : at_exp2((x - m) - ll) * (dp[i] - dsum);  // dS^T
       }
       if (h2 == 0) at_accum_tr1<D>(dq0, Kr, 0, s, lane);  // dQ^T += K^T dS^T
       else at_accum_tr1<D>(dq1, Kr, 32, s, lane);
@@ -1079,7 +1155,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
   }
 }
 
-template <int D, bool MASK, int RB>
+template <int D, bool MASK, int RB, bool DROP = false>
 __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bwd_kv_bf16_kernel(const AttnParams p) {
   constexpr int NT = 64 * RB, ND = D / 32;
   extern __shared__ __align__(16) float at_lds[];
@@ -1094,6 +1170,7 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
   const float* stats = p.stats + static_cast<int64_t>(w.zh) * L * 4;
   const int t = threadIdx.x, lane = t & 63, grp = lane >> 5, col = lane & 31;
   const int kb = w.rc * RB + (t >> 6), key = kb * 32 + col;
+  const uint32_t dbase = DROP ? at_drop_base(p, w.zh) : 0u;
   at_bf8 kr[D / 16], vr[D / 16];
   at_row_bf8<D>(kr, static_cast<const uint16_t*>(p.k) + w.sl.base(p, kAtK), min(key, L - 1) * p.st[kAtK][3], grp);
   at_row_bf8<D>(vr, static_cast<const uint16_t*>(p.v) + w.sl.base(p, kAtV), min(key, L - 1) * p.st[kAtV][3], grp);
@@ -1137,15 +1214,22 @@ __global__ void __launch_bounds__(64 * RB, D == 32 ? (MASK ? 2 : 3) : 1) attn_bw
         for (int jj = 0; jj < 4; ++jj) {
           const int i = 4 * c4 + jj;
           // lanes past L and rows past L as in the f32 kernel
+          bool blocked = false;  // as in the f32 kernel
           if constexpr (MASK) {
             const int q = r0 + ql + jj;
             float x = s[i] * p.scale2;
-            if (q < L && p.mask[static_cast<int64_t>(q) * L + min(key, L - 1)] != 0) x = kAtMaskScore;
+            if (q < L && (!DROP || p.mask != nullptr) && p.mask[static_cast<int64_t>(q) * L + min(key, L - 1)] != 0) x = kAtMaskScore, blocked = true;
             pw[i] = at_exp2((x - mq[jj]) - lq[jj]);
           } else {
             pw[i] = at_exp2(fmaf(s[i], p.scale2, -mq[jj]) - lq[jj]);
           }
-          s[i] = pw[i] * (dp[i] - dd[jj]);  // dS
+          if constexpr (DROP) {  // as in the f32 kernel
+            const bool keep = at_drop_keep(dbase, r0 + ql + jj, key, p.drop_thr);
+            s[i] = blocked ? 0.0f : pw[i] * ((keep ? dp[i] * p.drop_scale : 0.0f) - dd[jj]);
+            pw[i] = keep ? pw[i] * p.drop_scale : 0.0f;
+          } else {
+            s[i] = blocked ? 0.0f : pw[i] * (dp[i] - dd[jj]);  // dS
+          }
         }
       }
       at_accum_tr<D>(dv, dk, Gr, 32 * h2, Qr, 32 * h2, pw, s, lane);  // dV^T += dO^T P, dK^T += Q^T dS
@@ -1583,6 +1667,21 @@ __global__ void __launch_bounds__(64 * (kAtFusedBlocks + 2), 3) attn_bwd_fused_f
     for (int c = 0; c < 4; ++c)
       *reinterpret_cast<at_f4*>(&x[4 * (c * 64 + lane)]) = at_f4{acc0[4 * c] + acc1[4 * c], acc0[4 * c + 1] + acc1[4 * c + 1],
                                                                 acc0[4 * c + 2] + acc1[4 * c + 2], acc0[4 * c + 3] + acc1[4 * c + 3]};
+  }
+}
+
+// keep[zh][q][k] = 1 where the DROP kernels keep weight (q, k) of (slice, head) zh, else 0: one
+// thread per key pair (2 kh, 2 kh + 1) of a row, grid-stride over the zh * L * ceil(L / 2) pairs.
+__global__ void __launch_bounds__(256) attn_drop_keep_kernel(const AttnParams p, uint8_t* __restrict__ keep, int64_t pairs) {
+  const int L = p.len, hp = (L + 1) / 2;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < pairs; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t row = i / hp;  // zh * L + q
+    const int kh = static_cast<int>(i - row * hp);
+    const int zh = static_cast<int>(row / L), q = static_cast<int>(row - static_cast<int64_t>(zh) * L);
+    const uint32_t h = at_drop_bits(at_drop_base(p, zh), q, kh);
+    uint8_t* dst = keep + row * L + 2 * kh;
+    dst[0] = (h & 0xffffu) >= p.drop_thr ? 1 : 0;
+    if (2 * kh + 1 < L) dst[1] = (h >> 16) >= p.drop_thr ? 1 : 0;
   }
 }
 

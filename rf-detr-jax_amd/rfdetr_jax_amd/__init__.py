@@ -9,7 +9,13 @@ decoder's grouped self-attention (``MultiheadAttention``, ``scaled_dot_product_a
 layers.py:54-99, :491-548).
 """
 
-from .attention import MultiheadAttention, decoder_self_attention, grouped_attention, scaled_dot_product_attention
+from .attention import (
+    MultiheadAttention,
+    decoder_self_attention,
+    dropout_keep_mask,
+    grouped_attention,
+    scaled_dot_product_attention,
+)
 from .grid_sample import bilinear_grid_sample, point_sample
 from .ops import (
     SAMPLERS,
@@ -30,6 +36,7 @@ __all__ = [
     "SAMPLERS",
     "bilinear_grid_sample",
     "decoder_self_attention",
+    "dropout_keep_mask",
     "grouped_attention",
     "ms_deform_attn",
     "ms_deform_attn_backward",

@@ -48,6 +48,10 @@ SIGNATURES = {
     "msda_value_proj_bwd": ([_P, _I, _P, _P, _P, _P, _P, _P] + [_I] * 5 + [_P, _I64, _P], _I),
     "msda_attention_fwd": ([_P, _P, _P, _I, _P, _P] + [_I] * 5 + [_P, _P, _P], _I),
     "msda_attention_bwd": ([_P, _P, _P, _P, _P, _P, _I, _P, _P, _P] + [_I] * 5 + [_P, _P, _P], _I),
+    "msda_attention_fwd_dropout": ([_P, _P, _P, _I, _P, _P] + [_I] * 5 + [_P, _P, ctypes.c_float, ctypes.c_uint64, _P], _I),
+    "msda_attention_bwd_dropout": ([_P, _P, _P, _P, _P, _P, _I, _P, _P, _P] + [_I] * 5
+                                   + [_P, _P, ctypes.c_float, ctypes.c_uint64, _P], _I),
+    "msda_attention_dropout_keep": ([_I] * 4 + [ctypes.c_float, ctypes.c_uint64, _P, _P], _I),
     # include/msda_probe.h
     "msda_probe_lds_read": ([_P, _I, _I, _P], _I),
     "msda_probe_lds_read_bytes": ([_I, _I], _I64),

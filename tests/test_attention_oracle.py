@@ -159,3 +159,100 @@ def test_planted_mistakes_are_caught(mistake, monkeypatch):
         else:
             tq, tk, tv = (torch.tensor(t, dtype=torch.float64) for t in (q, k, v))
             assert_close(AT.sdpa(q, k, v), F.scaled_dot_product_attention(tq, tk, tv).numpy(), 1e-9, "planted")
+
+
+def test_fully_blocked_row_gradients_match_torch_masked_fill():
+    """A row whose every key is blocked: the scores all become finfo(float32).min, the weights are
+    uniform (the output is the mean of V), and ``where`` (torch's masked_fill here, jnp.where in
+    layers.py:93-96) passes the blocked scores no gradient, so the row's dQ is 0 and it adds nothing
+    to dK; dV still receives the uniform weights. torch float64 autograd."""
+    q, k, v = _qkv(23, (2, 2, 9, 8))
+    mask = np.zeros((9, 9), bool)
+    mask[3] = True
+    mask[:, 7] = True
+    g = np.random.default_rng(6).standard_normal(q.shape)
+    tq, tk, tv = (torch.tensor(t, dtype=torch.float64, requires_grad=True) for t in (q, k, v))
+    scores = (tq @ tk.transpose(-1, -2) / np.sqrt(8)).masked_fill(torch.tensor(mask), float(np.finfo(np.float32).min))
+    out = torch.softmax(scores, -1) @ tv
+    out.backward(torch.tensor(g))
+    assert_close(AT.sdpa(q, k, v, mask), out.detach().numpy(), 1e-12, "out")
+    dq, dk, dv = AT.sdpa_vjp(q, k, v, g, mask)
+    assert not dq[:, :, 3].any()
+    for name, mine, want in zip("qkv", (dq, dk, dv), (tq.grad, tk.grad, tv.grad)):
+        assert_close(mine, want.numpy(), 1e-12, f"d{name}")
+
+
+def _torch_dropout_attention(q, k, v, mask, rate, seed):
+    """torch float64: softmax attention whose weights go through ``F.dropout`` (training), the
+    keep mask read back from which weights survived; returns (out, keep, autograd leaves)."""
+    tq, tk, tv = (torch.tensor(t, dtype=torch.float64, requires_grad=True) for t in (q, k, v))
+    scores = tq @ tk.transpose(-1, -2) / np.sqrt(q.shape[-1])
+    if mask is not None:
+        scores = scores.masked_fill(torch.tensor(mask), float(np.finfo(np.float32).min))
+    w = torch.softmax(scores, -1)
+    torch.manual_seed(seed)
+    wd = F.dropout(w, rate, training=True)
+    keep = (wd != 0).detach().numpy()
+    return wd @ tv, keep, (tq, tk, tv)
+
+
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("rate", [0.1, 0.5])
+def test_dropout_matches_torch_dropout_under_autograd(rate, masked):
+    """The dropout branch (layers.py:537-544) against torch's own ``F.dropout`` on the softmax
+    weights (which scales kept weights by 1 / (1 - rate), as flax's Dropout does), outputs and the
+    three gradients under float64 autograd, with the keep mask torch drew."""
+    q, k, v = _qkv(21, (2, 3, 10, 8))
+    mask = None
+    if masked:
+        mask = np.zeros((10, 10), bool)
+        mask[:, -2:] = True
+        mask[4] = True
+    out, keep, (tq, tk, tv) = _torch_dropout_attention(q, k, v, mask, rate, 5)
+    assert 0 < keep.sum() < keep.size
+    g = np.random.default_rng(3).standard_normal(q.shape)
+    out.backward(torch.tensor(g))
+    assert_close(AT.sdpa(q, k, v, mask, keep, rate), out.detach().numpy(), 1e-12, "out")
+    for name, mine, want in zip("qkv", AT.sdpa_vjp(q, k, v, g, mask, keep, rate), (tq.grad, tk.grad, tv.grad)):
+        assert_close(mine, want.numpy(), 1e-12, f"d{name}")
+
+
+def test_dropout_closed_forms():
+    """Every weight kept: the plain attention scaled by 1 / (1 - rate); rate 0 with any mask of ones:
+    the plain attention; every weight dropped: zeros, and zero gradients."""
+    q, k, v = _qkv(22, (1, 2, 7, 4))
+    g = np.random.default_rng(4).standard_normal(q.shape)
+    ones = np.ones((1, 2, 7, 7), bool)
+    assert_close(AT.sdpa(q, k, v, None, ones, 0.25), AT.sdpa(q, k, v) / 0.75, 1e-12, "all kept")
+    assert_close(AT.sdpa(q, k, v, None, ones, 0.0), AT.sdpa(q, k, v), 1e-12, "rate 0")
+    assert not AT.sdpa(q, k, v, None, ~ones, 0.25).any()
+    assert all(not t.any() for t in AT.sdpa_vjp(q, k, v, g, None, ~ones, 0.25))
+
+
+@pytest.mark.parametrize("mistake", ["scale_by_rate", "drop_before_softmax", "vjp_without_keep"])
+def test_dropout_planted_mistakes_are_caught(mistake, monkeypatch):
+    if mistake == "scale_by_rate":
+        monkeypatch.setattr(AT, "_dropped", lambda p, keep, rate: p if keep is None else np.where(keep, p / rate, 0.0))
+    elif mistake == "drop_before_softmax":
+        orig = AT._probs
+
+        def bad_probs(q_, k_, mask):
+            return orig(q_, k_, mask)
+
+        def bad_dropped(p, keep, rate):  # renormalise the kept weights, as dropping scores would
+            if keep is None:
+                return p
+            w = np.where(keep, p, 0.0)
+            return w / w.sum(-1, keepdims=True)
+        monkeypatch.setattr(AT, "_probs", bad_probs)
+        monkeypatch.setattr(AT, "_dropped", bad_dropped)
+    else:
+        orig = AT._dropped
+        calls = []
+
+        def once(p, keep, rate):  # the VJP's second use (dP) without the mask
+            calls.append(1)
+            return orig(p, keep, rate) if len(calls) % 2 == 1 else p
+        monkeypatch.setattr(AT, "_dropped", once)
+    with pytest.raises(AssertionError):
+        test_dropout_matches_torch_dropout_under_autograd(0.1, False)

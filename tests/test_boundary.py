@@ -539,6 +539,58 @@ def test_attention_module_mirror_errors():
         grouped_attention(torch.zeros(1, 10, 64), torch.zeros(1, 10, 64), torch.zeros(1, 10, 64), 2, groups=3)
     with pytest.raises(RuntimeError, match="no CPU path"):
         scaled_dot_product_attention(torch.zeros(1, 2, 3, 32), torch.zeros(1, 2, 3, 32), torch.zeros(1, 2, 3, 32))
+    with pytest.raises(ValueError, match="dropout rate"):
+        scaled_dot_product_attention(torch.zeros(1, 2, 3, 32), torch.zeros(1, 2, 3, 32), torch.zeros(1, 2, 3, 32), dropout=1.5)
+    # training with dropout goes to the same kernels (no CPU path either)
     m_drop = MultiheadAttention(64, 2, dropout=0.1).train()
-    with pytest.raises(NotImplementedError, match="dropout"):
+    with pytest.raises(RuntimeError, match="no CPU path"):
         m_drop(torch.zeros(1, 3, 64), torch.zeros(1, 3, 64), torch.zeros(1, 3, 64))
+
+
+def _at_drop(which, rate, seed=7, **kw):
+    """msda_attention_fwd_dropout / _bwd_dropout with _at_fwd's / _at_bwd's defaults."""
+    lib = _native.lib()
+    if which == "fwd":
+        args = dict(q=1 << 20, k=1 << 20, v=1 << 20, dt=0, o=1 << 20, st=1 << 20, batch=2, groups=1, heads=2, len=9, d=32,
+                    strides=[2 * 9 * 32, 0, 9 * 32, 32] * 4, m=0)
+        args.update(kw)
+        strides = (ctypes.c_int64 * len(args["strides"]))(*args["strides"])
+        rc = lib.msda_attention_fwd_dropout(ctypes.c_void_p(args["q"]), ctypes.c_void_p(args["k"]), ctypes.c_void_p(args["v"]),
+                                            args["dt"], ctypes.c_void_p(args["o"]), ctypes.c_void_p(args["st"]), args["batch"],
+                                            args["groups"], args["heads"], args["len"], args["d"], strides, ctypes.c_void_p(args["m"]),
+                                            rate, seed, None)
+    else:
+        args = dict(q=1 << 20, k=1 << 20, v=1 << 20, o=1 << 20, st=1 << 20, go=1 << 20, dt=0, gq=1 << 20, gk=1 << 20, gv=1 << 20,
+                    batch=2, groups=1, heads=2, len=9, d=32, strides=[2 * 9 * 32, 0, 9 * 32, 32] * 8, m=0)
+        args.update(kw)
+        strides = (ctypes.c_int64 * len(args["strides"]))(*args["strides"])
+        rc = lib.msda_attention_bwd_dropout(ctypes.c_void_p(args["q"]), ctypes.c_void_p(args["k"]), ctypes.c_void_p(args["v"]),
+                                            ctypes.c_void_p(args["o"]), ctypes.c_void_p(args["st"]), ctypes.c_void_p(args["go"]),
+                                            args["dt"], ctypes.c_void_p(args["gq"]), ctypes.c_void_p(args["gk"]),
+                                            ctypes.c_void_p(args["gv"]), args["batch"], args["groups"], args["heads"], args["len"],
+                                            args["d"], strides, ctypes.c_void_p(args["m"]), rate, seed, None)
+    return rc, lib.msda_last_error().decode()
+
+
+@pytest.mark.parametrize("which", ["fwd", "bwd"])
+@pytest.mark.parametrize("rate", [-0.1, 1.0, 2.0, float("nan")])
+def test_attention_dropout_rate_is_validated(which, rate):
+    """Dropout rates outside [0, 1) are refused before any HIP call (flax's rate 1, all weights
+    dropped, is the Python mirror's zeros)."""
+    rc, msg = _at_drop(which, rate)
+    assert rc == _native.ERR_INVALID_ARGUMENT and "dropout rate" in msg, msg
+
+
+@pytest.mark.parametrize("which", ["fwd", "bwd"])
+def test_attention_dropout_shares_the_plain_validation(which):
+    assert _at_drop(which, 0.1, d=48)[0] == _native.ERR_UNSUPPORTED
+    assert _at_drop(which, 0.1, q=0)[0] == _native.ERR_INVALID_ARGUMENT
+    assert _at_drop(which, 0.1, len=0)[0] == _native.OK  # empty: nothing to do
+
+
+def test_attention_dropout_keep_validation():
+    lib = _native.lib()
+    assert lib.msda_attention_dropout_keep(2, 1, 2, 9, 1.0, 1, None, None) == _native.ERR_INVALID_ARGUMENT
+    assert lib.msda_attention_dropout_keep(2, 1, 2, -1, 0.1, 1, None, None) == _native.ERR_INVALID_ARGUMENT
+    assert lib.msda_attention_dropout_keep(2, 1, 2, 9, 0.1, 1, None, None) == _native.ERR_INVALID_ARGUMENT  # NULL keep
+    assert lib.msda_attention_dropout_keep(2, 1, 2, 0, 0.1, 1, None, None) == _native.OK

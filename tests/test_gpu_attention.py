@@ -460,3 +460,133 @@ def test_fused_backward_random_shapes(seed, bf16):
     torch.cuda.synchronize()
     for name, got, want in zip("qkv", grads, AT.sdpa_vjp(q, k, v, g)):
         assert_close(_np(got), want, 2e-2 if bf16 else 1e-4, f"grad_{name}")
+
+
+# --------------------------------------------------------------------------------------------
+# attention dropout (layers.py:537-544): the keep decisions come from dropout_keep_mask, the same
+# hash the kernels evaluate; the expected values are the float64 oracle with that mask.
+
+DROP_SHAPES = {
+    "decoder": (3, 8, 300, 32),
+    "ragged64": (2, 2, 77, 64),
+    "one": (1, 1, 1, 32),
+}
+
+
+def _keep(batch, heads, length, rate, seed, groups=1):
+    from rfdetr_jax_amd.attention import dropout_keep_mask
+
+    return dropout_keep_mask(batch, heads, length, rate, seed, groups=groups, device=_dev())
+
+
+def test_dropout_keep_mask_statistics():
+    """Keep rate 1 - rate (overall, for even and odd keys, which share one hash, and across
+    neighbouring queries, within six standard deviations); the same (rate, seed) gives the same
+    mask, another seed or another slice an independent one (disagreement 2 r (1 - r))."""
+    b, h, length = 4, 8, 300
+    for rate in (0.1, 0.5, 0.9):
+        keep = _keep(b, h, length, rate, 1234).float()
+        n = keep.numel()
+        sd = (rate * (1 - rate) / n) ** 0.5
+        _note(f"dropout rate {rate}: kept {keep.mean().item():.5f}")
+        assert abs(keep.mean().item() - (1 - rate)) < 6 * sd
+        for part in (keep[..., 0::2], keep[..., 1::2]):
+            assert abs(part.mean().item() - (1 - rate)) < 6 * sd * 2 ** 0.5
+        both = (keep[..., 0:298:2] * keep[..., 1:299:2]).mean().item()  # the two halves of one hash
+        rows = (keep[:, :, 0::2, :] * keep[:, :, 1::2, :]).mean().item()
+        sd2 = ((1 - rate) ** 2 * (1 - (1 - rate) ** 2) / (n / 2)) ** 0.5
+        assert abs(both - (1 - rate) ** 2) < 6 * sd2 and abs(rows - (1 - rate) ** 2) < 6 * sd2
+    k1 = _keep(b, h, length, 0.1, 1234)
+    assert torch.equal(k1, _keep(b, h, length, 0.1, 1234))
+    other = (k1 != _keep(b, h, length, 0.1, 1235)).float().mean().item()
+    slices = (k1[0, 0] != k1[0, 1]).float().mean().item()
+    assert abs(other - 0.18) < 0.005 and abs(slices - 0.18) < 0.01
+    assert bool((_keep(1, 2, 40, 0.0, 5) == 1).all())
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+@pytest.mark.parametrize("masked", [False, True], ids=["nomask", "mask"])
+@pytest.mark.parametrize("shape", sorted(DROP_SHAPES))
+def test_dropout_against_oracle(shape, masked, bf16):
+    """Output and gradients with dropout (rate 0.1) against the float64 oracle given the kernels'
+    keep mask, with and without a key mask (a fully blocked row included)."""
+    b, h, length, d = DROP_SHAPES[shape]
+    rate, seed = 0.1, 1000 + length
+    _note(f"dropout {shape} masked={masked} bf16={bf16}")
+    rng = np.random.default_rng(43)
+    q, k, v, g = (rng.standard_normal((b, h, length, d)).astype(np.float32) for _ in range(4))
+    mask = None
+    if masked:
+        mask = rng.uniform(0, 1, (length, length)) < 0.2
+        mask[:, -3:] = True
+        mask[length // 2] = True
+    if bf16:
+        q, k, v, g = (bf16_round(t) for t in (q, k, v, g))
+    dt = torch.bfloat16 if bf16 else None
+    tq, tk, tv = (_t(x, dt).requires_grad_(True) for x in (q, k, v))
+    out = scaled_dot_product_attention(tq, tk, tv, None if mask is None else _t(mask), dropout=rate, seed=seed)
+    out.backward(_t(g, dt))
+    keep = _np(_keep(b, h, length, rate, seed)).astype(bool)
+    torch.cuda.synchronize()
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    assert_close(_np(out), AT.sdpa(q, k, v, mask, keep, rate), tf, "out")
+    for name, t, want in zip("qkv", (tq, tk, tv), AT.sdpa_vjp(q, k, v, g, mask, keep, rate)):
+        assert_close(_np(t.grad), want, tg, f"grad_{name}")
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+def test_grouped_dropout_rows_layout(bf16):
+    """Dropout on [B, G * P, C] rows with G groups: slice z = g * B + b of the keep mask belongs to
+    group g of image b (the order of _split_groups)."""
+    batch, groups, per, heads, d = 2, 3, 40, 4, 32
+    c = heads * d
+    rate, seed = 0.2, 9
+    rng = np.random.default_rng(44)
+    q, k, v, g = (rng.standard_normal((batch, groups * per, c)).astype(np.float32) for _ in range(4))
+    if bf16:
+        q, k, v, g = (bf16_round(x) for x in (q, k, v, g))
+    dt = torch.bfloat16 if bf16 else None
+    tq, tk, tv = (_t(x, dt).requires_grad_(True) for x in (q, k, v))
+    out = grouped_attention(tq, tk, tv, heads, groups, dropout=rate, seed=seed)
+    out.backward(_t(g, dt))
+    keep = _np(_keep(batch, heads, per, rate, seed, groups=groups)).astype(bool)  # [G B, H, P, P]
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+
+    def heads_of(x):  # [G B, P, C] -> [G B, H, P, D]
+        return x.reshape(x.shape[0], per, heads, d).transpose(0, 2, 1, 3)
+
+    def back(x):  # [G B, H, P, D] -> [B, G P, C]
+        return AT.merge_groups(x.transpose(0, 2, 1, 3).reshape(groups * batch, per, c), batch)
+
+    qs, ks, vs, gs = (heads_of(AT.split_groups(x, per)) for x in (q, k, v, g))
+    assert_close(_np(out), back(AT.sdpa(qs, ks, vs, None, keep, rate)), tf, "out")
+    for name, t, want in zip("qkv", (tq, tk, tv), AT.sdpa_vjp(qs, ks, vs, gs, None, keep, rate)):
+        assert_close(_np(t.grad), back(want), tg, f"grad_{name}")
+
+
+def test_dropout_module_training_and_eval():
+    """MultiheadAttention(dropout=0.1): in training a call draws its seed from torch's generator
+    (repeatable under torch.manual_seed, different otherwise) and its gradients are finite; in
+    eval the module is the plain attention; rate 0 is the plain path bit for bit; rate 1 gives
+    zeros (flax's Dropout at rate 1)."""
+    torch.manual_seed(0)
+    m = MultiheadAttention(64, 2, dropout=0.1).to(_dev())
+    x = torch.randn(2, 50, 64, device=_dev(), requires_grad=True)
+    m.train()
+    torch.manual_seed(5)
+    y1 = m(x, x, x)
+    torch.manual_seed(5)
+    y2 = m(x, x, x)
+    torch.manual_seed(6)
+    y3 = m(x, x, x)
+    assert torch.equal(y1, y2) and not torch.equal(y1, y3)
+    y1.square().sum().backward()
+    assert torch.isfinite(x.grad).all() and torch.isfinite(m.in_proj_weight.grad).all()
+    m.eval()
+    plain = MultiheadAttention(64, 2).to(_dev())
+    plain.load_state_dict(m.state_dict())
+    with torch.no_grad():
+        assert torch.equal(m(x, x, x), plain(x, x, x))
+    q, k, v = (torch.randn(1, 2, 33, 32, device=_dev()) for _ in range(3))
+    assert torch.equal(scaled_dot_product_attention(q, k, v, dropout=0.0, seed=3), scaled_dot_product_attention(q, k, v))
+    assert not scaled_dot_product_attention(q, k, v, dropout=1.0).any()
