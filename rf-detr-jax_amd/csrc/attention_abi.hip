@@ -236,10 +236,10 @@ int bwd_dispatch(const msda::AttnParams& p, int d, bool bf16, bool want_kv, bool
   return m ? bwd_typed<float, 64, true>(p, want_kv, st) : bwd_typed<float, 64, false>(p, want_kv, st);
 }
 
-// Dropout arguments: rate in [0, 1) (0: none), the call's seed. Fills p's dropout fields.
-int at_dropout(msda::AttnParams* p, float rate, uint64_t seed, int len) {
+// Dropout arguments: rate in [0, 1) (0: none), the call's seed. Fills p's dropout fields. The
+// hash inputs (q << 16 | k / 2) are distinct for the at most 65536 rows the callers admit.
+int at_dropout(msda::AttnParams* p, float rate, uint64_t seed) {
   if (!(rate >= 0.0f && rate < 1.0f)) return fail(MSDA_ERR_INVALID_ARGUMENT, "attention: dropout rate %g outside [0, 1)", static_cast<double>(rate));
-  (void)len;  // the hash keys (q, k / 2) are distinct for the at most 65536 rows at_validate admits
   p->drop_seed[0] = static_cast<uint32_t>(seed);
   p->drop_seed[1] = static_cast<uint32_t>(seed >> 32);
   p->drop_thr = static_cast<uint32_t>(std::min(65536.0, std::nearbyint(static_cast<double>(rate) * 65536.0)));
@@ -254,7 +254,7 @@ int attention_fwd(const void* q, const void* k, const void* v, int dtype, void* 
   if (rc != MSDA_OK) return rc;
   static const int order[4] = {msda::kAtQ, msda::kAtK, msda::kAtV, msda::kAtO};
   msda::AttnParams p = at_params(dtype, batch, groups, heads, len, head_dim, strides, 4, order);
-  if ((rc = at_dropout(&p, rate, seed, len)) != MSDA_OK) return rc;
+  if ((rc = at_dropout(&p, rate, seed)) != MSDA_OK) return rc;
   if (batch == 0 || groups == 0 || heads == 0 || len == 0) return MSDA_OK;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || stats == nullptr)
     return fail(MSDA_ERR_INVALID_ARGUMENT, "msda_attention_fwd: NULL tensor pointer");
@@ -279,7 +279,7 @@ int attention_bwd(const void* q, const void* k, const void* v, const void* out, 
   if (rc != MSDA_OK) return rc;
   static const int order[8] = {msda::kAtQ, msda::kAtK, msda::kAtV, msda::kAtO, msda::kAtGO, msda::kAtGQ, msda::kAtGK, msda::kAtGV};
   msda::AttnParams p = at_params(dtype, batch, groups, heads, len, head_dim, strides, 8, order);
-  if ((rc = at_dropout(&p, rate, seed, len)) != MSDA_OK) return rc;
+  if ((rc = at_dropout(&p, rate, seed)) != MSDA_OK) return rc;
   const bool want_q = grad_q != nullptr, want_kv = grad_k != nullptr || grad_v != nullptr;
   if (batch == 0 || groups == 0 || heads == 0 || len == 0 || (!want_q && !want_kv)) return MSDA_OK;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || stats == nullptr || grad_out == nullptr)
@@ -341,7 +341,7 @@ int msda_attention_dropout_keep(int batch, int groups, int heads, int len, float
   p.groups = groups;
   p.heads = heads;
   p.len = len;
-  int rc = at_dropout(&p, rate, seed, len);
+  int rc = at_dropout(&p, rate, seed);
   if (rc != MSDA_OK) return rc;
   const int64_t pairs = static_cast<int64_t>(batch) * groups * heads * len * ((len + 1) / 2);
   if (pairs == 0) return MSDA_OK;

@@ -79,7 +79,7 @@ __global__ void __launch_bounds__(256) fused_epilogue_kernel(const FusedRowParam
     float* dl = p.dlogits + row * LP;
     const SoftmaxStats st = softmax_stats(lg, LP);
     float S = 0.0f;
-    for (int k = 0; k < LP; ++k) S += softmax_weight(lg[k], st) * dl[k];
+    for (int k = 0; k < LP; ++k) S = fmaf(softmax_weight(lg[k], st), dl[k], S);  // one rounding per term, in every kernel
     for (int k = 0; k < LP; ++k) dl[k] = softmax_weight(lg[k], st) * (dl[k] - S);
   }
   if (p.dloc == nullptr) return;  // uniform: nothing below is requested
@@ -113,10 +113,13 @@ __global__ void __launch_bounds__(256) fused_epilogue_kernel(const FusedRowParam
 }
 
 // The same two steps with one thread per sample (b, q, h, k), for rows of at most NB samples over at
-// most four levels (every RF-DETR shape) and fewer than 2^31 samples. A row's lanes load its logits
-// (one broadcast address per row), each lane its own offset, location gradient and reference point:
-// loads and stores are contiguous runs, and there are LP times as many threads to hide latency as
-// the row kernels above have. The arithmetic and its order are those of the row kernels.
+// most four levels (every RF-DETR shape) and fewer than 2^31 samples. Each lane loads its own
+// offset, location gradient and reference point: loads and stores are contiguous runs, and there
+// are LP times as many threads to hide latency as the row kernels above have. When LP is a power of
+// two a row lies within one wave: each lane loads its own logit (and dA) and forms one exponential,
+// and the row's statistics and sums come from the other lanes by shuffles (row_stats_lanes);
+// otherwise every lane of a row loads the row's logits (one broadcast address per row) and forms
+// them all. The arithmetic and its order are those of the row kernels either way.
 __device__ __forceinline__ float level_pick(int l, const float (&a)[kMaxLevels]) {
   return l == 0 ? a[0] : l == 1 ? a[1] : l == 2 ? a[2] : a[3];
 }
@@ -133,11 +136,44 @@ __device__ __forceinline__ SoftmaxStats row_stats(const float (&x)[NB], int LP) 
   return st;
 }
 
+// The softmax statistics of a row held one logit per lane (xk), its LP lanes consecutive and
+// LP-aligned in the wave (LP a power of two dividing 64), for every lane of the row: the maximum by
+// a butterfly (exact in any order), the sum of the lanes' exp(x - m) (ek) gathered and added in
+// sample order from 0, as row_stats and softmax_stats add them, so the weights are theirs bit for
+// bit with one exponential per lane instead of LP. Every lane of the wave must take part.
+__device__ __forceinline__ SoftmaxStats row_stats_lanes(float xk, int LP, float& ek) {
+  SoftmaxStats st{xk, 0.0f};
+  for (int o = LP >> 1; o > 0; o >>= 1) st.m = fmaxf(st.m, __shfl_xor(st.m, o, LP));
+  ek = expf(xk - st.m);
+  for (int u = 0; u < LP; ++u) st.s += __shfl(ek, u, LP);
+  return st;
+}
+
+__device__ __forceinline__ bool rows_in_lanes(int LP) { return (LP & (LP - 1)) == 0 && LP <= 64; }
+
 template <int NB>
 __global__ void __launch_bounds__(256) fused_prologue_samples_kernel(const FusedRowParams p) {
   const uint32_t LP = static_cast<uint32_t>(p.levels * p.points);
-  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;  // (b, q, h, k)
-  if (idx >= static_cast<uint32_t>(p.bq_total * p.heads) * LP) return;
+  const uint32_t total = static_cast<uint32_t>(p.bq_total * p.heads) * LP;
+  uint32_t idx = blockIdx.x * 256u + threadIdx.x;  // (b, q, h, k)
+  if (rows_in_lanes(static_cast<int>(LP))) {  // uniform: one exponential per lane, the row's sums by shuffles
+    const bool on = idx < total;
+    if (!on) idx = 0;  // whole rows only, so the lanes past the end form rows of their own
+    const uint32_t row = idx / LP, k = idx - row * LP;
+    const int l = static_cast<int>(k) / p.points;
+    const float xk = p.logits[idx];
+    float ek;
+    const SoftmaxStats st = row_stats_lanes(xk, static_cast<int>(LP), ek);
+    if (!on) return;
+    const float2 o = reinterpret_cast<const float2*>(p.off)[idx];
+    const float4 r = fused_row_ref(p, row / static_cast<uint32_t>(p.heads), l);
+    float2 t;
+    reinterpret_cast<float2*>(p.loc)[idx] =
+        fused_location_at(o, r, t, level_pick(l, p.fw), level_pick(l, p.fh), p.ref_dim, p.inv_points, p.fpoints);
+    p.attn[idx] = ek / st.s;  // softmax_weight(xk, st)
+    return;
+  }
+  if (idx >= total) return;
   const uint32_t row = idx / LP, k = idx - row * LP;
   const int l = static_cast<int>(k) / p.points;
   const uint32_t bq = row / static_cast<uint32_t>(p.heads);
@@ -174,12 +210,16 @@ __global__ void __launch_bounds__(256) fused_epilogue_samples_kernel(const Fused
   const uint32_t row = bq * static_cast<uint32_t>(H) + static_cast<uint32_t>(h);
   const uint32_t idx = row * static_cast<uint32_t>(LP) + static_cast<uint32_t>(k);
   const bool want_dl = p.dlogits != nullptr, want_loc = p.dloc != nullptr;  // uniform
+  const bool lanes = rows_in_lanes(LP);  // uniform: each lane loads its own logit and dA only
   float x[NB], d[NB];
   float xk = 0.0f, dk = 0.0f;
   float2 gl = make_float2(0.0f, 0.0f), o = make_float2(0.0f, 0.0f);
   float4 ref = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (on) {
-    if (want_dl) {
+    if (want_dl && lanes) {
+      xk = p.logits[idx];
+      dk = p.dlogits[idx];
+    } else if (want_dl) {
       const float* __restrict__ lg = p.logits + static_cast<size_t>(row) * LP;
       const float* __restrict__ dl = p.dlogits + static_cast<size_t>(row) * LP;
 #pragma unroll
@@ -200,12 +240,19 @@ __global__ void __launch_bounds__(256) fused_epilogue_samples_kernel(const Fused
   }
   wait_vmem();
   __syncthreads();  // the rows' dA are read before any of them is overwritten
-  if (on && want_dl) {
+  if (want_dl && lanes) {  // every lane of the block takes part in the row shuffles
+    float ek;
+    const SoftmaxStats st = row_stats_lanes(xk, LP, ek);
+    const float wk = ek / st.s;  // softmax_weight(xk, st)
+    float S = 0.0f;
+    for (int u = 0; u < LP; ++u) S = fmaf(__shfl(wk, u, LP), __shfl(dk, u, LP), S);  // as the row kernel, in order
+    if (on) p.dlogits[idx] = wk * (dk - S);
+  } else if (on && want_dl) {
     const SoftmaxStats st = row_stats<NB>(x, LP);
     float S = 0.0f;
 #pragma unroll
     for (int u = 0; u < NB; ++u)
-      if (u < LP) S += softmax_weight(x[u], st) * d[u];
+      if (u < LP) S = fmaf(softmax_weight(x[u], st), d[u], S);
     p.dlogits[idx] = softmax_weight(xk, st) * (dk - S);
   }
   if (!want_loc) return;  // uniform

@@ -197,6 +197,10 @@ ROW_CASES = {
     # bounds, so the per-row kernels run either way
     "l4_p8_h16": dict(shapes=((16, 16), (8, 8), (4, 4), (2, 2)), heads=16, dim=16, points=8, queries=30),
     "l5_p2": dict(shapes=((16, 16), (8, 8), (4, 4), (2, 2), (1, 1)), heads=4, dim=16, points=2, queries=50),
+    # power-of-two rows, whose softmax the per-sample kernels take across the row's lanes: 8 samples
+    # (the config-3 shape's 2 levels x 4 points) and 2 samples (2 levels x 1 point)
+    "l2_p4": dict(shapes=((20, 20), (10, 10)), heads=8, dim=16, points=4, queries=90),
+    "l2_p1": dict(shapes=((20, 20), (10, 10)), heads=8, dim=16, points=1, queries=90),
 }
 
 
