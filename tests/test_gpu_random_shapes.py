@@ -1,0 +1,98 @@
+"""Seeded random shapes through msda_fwd / msda_bwd against the float64 oracle, on an MI355X.
+
+Each seed draws 1-4 levels of 1-40 rows and columns, 1-16 heads, head_dim 1-64, 1-8 points,
+1-400 queries, batch 1-3, f32 or bf16 values, and locations either clustered around reference
+points or uniform over [-0.1, 1.1]^2 (many corners outside the map). Both sizes are small enough
+for the float64 oracle (oracle/msda_ref.py) to finish in well under a second. The launch planner
+picks whatever plan the shape gets: whole levels or bands, query blocks and partial sums, lanes
+per query, head groups, staged or gathered levels. Tolerances are the contract's
+(``max|got - want| <= tol * max(1, max|want|)``): f32 forward 1e-5 and gradients 1e-4, bf16 2e-2.
+A second set of draws runs each of the reference's sampler names, whose forward on a bf16 map is
+held to 2e-6 of the oracle's restatement of that sampler (as in test_gpu_samplers).
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import msda_ref as R
+from rfdetr_jax_amd import ops as hip
+from rfdetr_jax_amd.workloads import make_inputs
+from tests._util import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _draw(seed):
+    rng = np.random.default_rng(7000 + seed)
+    levels = int(rng.integers(1, 5))
+    shapes = tuple((int(rng.integers(1, 41)), int(rng.integers(1, 41))) for _ in range(levels))
+    return dict(
+        shapes=shapes,
+        heads=int(rng.choice([1, 2, 3, 4, 5, 8, 16])),
+        dim=int(rng.choice([1, 2, 3, 4, 5, 8, 12, 16, 24, 32, 48, 64])),
+        points=int(rng.integers(1, 9)),
+        queries=int(rng.integers(1, 401)),
+        batch=int(rng.integers(1, 4)),
+        bf16=bool(rng.integers(0, 2)),
+        uniform=bool(rng.integers(0, 2)),
+    )
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shape_against_oracle(seed):
+    c = _draw(seed)
+    sys.stderr.write(f"[gpu] random shape seed={seed} {c}\n")
+    sys.stderr.flush()
+    value, loc, attn, grad = make_inputs(seed, c["batch"], c["heads"], c["dim"], c["queries"], c["shapes"], c["points"],
+                                         value_dtype="bf16" if c["bf16"] else "f32", uniform_locations=c["uniform"])
+    dev = torch.device("cuda:0")
+    v = torch.from_numpy(value).to(dev)
+    if c["bf16"]:
+        v = v.to(torch.bfloat16)
+    lc, a, g = (torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in (loc, attn, grad))
+    out = hip.ms_deform_attn_forward(v, c["shapes"], lc, a)
+    gv, gl, ga = hip.ms_deform_attn_backward(v, c["shapes"], lc, a, g)
+    torch.cuda.synchronize()
+    tf, tg = (2e-2, 2e-2) if c["bf16"] else (1e-5, 1e-4)
+    assert_close(out.float().cpu().numpy(), R.ms_deform_attn_core_rows(value, c["shapes"], loc, attn), tf, "out")
+    rv, rl, ra = R.ms_deform_attn_core_rows_vjp(value, c["shapes"], loc, attn, grad)
+    assert_close(gv.float().cpu().numpy(), rv, tg, "grad_value")
+    assert_close(gl.cpu().numpy(), rl, tg, "grad_loc")
+    assert_close(ga.cpu().numpy(), ra, tg, "grad_attn")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shape_named_sampler(seed):
+    """The same draws through each reference sampler name (autograd over ms_deform_attn_core_rows):
+    the forward against the oracle's restatement of that sampler's rounding points and pixel
+    coordinates, the gradients against the f32 VJP at its coordinates."""
+    c = _draw(100 + seed)
+    sampler = hip.SAMPLERS[seed % len(hip.SAMPLERS)]
+    sys.stderr.write(f"[gpu] random shape sampler={sampler} seed={seed} {c}\n")
+    sys.stderr.flush()
+    value, loc, attn, grad = make_inputs(100 + seed, c["batch"], c["heads"], c["dim"], c["queries"], c["shapes"], c["points"],
+                                         value_dtype="bf16" if c["bf16"] else "f32", uniform_locations=c["uniform"])
+    dev = torch.device("cuda:0")
+    v = torch.from_numpy(value).to(dev)
+    if c["bf16"]:
+        v = v.to(torch.bfloat16)
+    v.requires_grad_(True)
+    lc = torch.from_numpy(np.ascontiguousarray(loc)).to(dev).requires_grad_(True)
+    a = torch.from_numpy(np.ascontiguousarray(attn)).to(dev).requires_grad_(True)
+    g = torch.from_numpy(grad).to(dev)
+    out = hip.ms_deform_attn_core_rows(v, c["shapes"], lc, a, sampler)
+    (out * g).sum().backward()
+    torch.cuda.synchronize()
+    tf, tg = (2e-6, 2e-2) if c["bf16"] else (1e-5, 1e-4)
+    want = R.ms_deform_attn_core_rows_sampler(value, c["shapes"], loc, attn, sampler, c["bf16"])
+    assert_close(out.detach().cpu().numpy(), want, tf, f"{sampler} out")
+    vjp = R.ms_deform_attn_core_rows_vjp_pallas if sampler == "pallas" else R.ms_deform_attn_core_rows_vjp
+    rv, rl, ra = vjp(value, c["shapes"], loc, attn, grad)
+    assert_close(v.grad.float().cpu().numpy(), rv, tg, f"{sampler} grad_value")
+    assert_close(lc.grad.cpu().numpy(), rl, tg, f"{sampler} grad_loc")
+    assert_close(a.grad.cpu().numpy(), ra, tg, f"{sampler} grad_attn")
