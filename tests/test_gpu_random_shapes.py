@@ -96,3 +96,39 @@ def test_random_shape_named_sampler(seed):
     assert_close(v.grad.float().cpu().numpy(), rv, tg, f"{sampler} grad_value")
     assert_close(lc.grad.cpu().numpy(), rl, tg, f"{sampler} grad_loc")
     assert_close(a.grad.cpu().numpy(), ra, tg, f"{sampler} grad_attn")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_shape_fused_prologue(seed):
+    """The fused-prologue op (msda_fused_fwd / msda_fused_bwd) on random draws with point (2-dim) or
+    box (4-dim) reference points, against the prologue oracle composed with the core's float64
+    oracle: one level takes the band kernel's in-kernel prologue when it fits, several levels the
+    prologue and epilogue kernels (per sample for rows of up to 32 samples over up to 4 levels,
+    per row otherwise)."""
+    from oracle import prologue_ref as PR
+    from rfdetr_jax_amd.workloads import make_fused_inputs
+
+    c = _draw(200 + seed)
+    ref_dim = 2 if seed % 2 == 0 else 4
+    sys.stderr.write(f"[gpu] random shape fused seed={seed} ref_dim={ref_dim} {c}\n")
+    sys.stderr.flush()
+    value, ref, off, logits, grad = make_fused_inputs(200 + seed, c["batch"], c["heads"], c["dim"], c["queries"], c["shapes"],
+                                                      c["points"], ref_dim, "bf16" if c["bf16"] else "f32")
+    dev = torch.device("cuda:0")
+    v = torch.from_numpy(value).to(dev)
+    if c["bf16"]:
+        v = v.to(torch.bfloat16)
+    r, o, lg, g = (torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in (ref, off, logits, grad))
+    out = hip.ms_deform_attn_fused_forward(v, c["shapes"], r, o, lg)
+    gv, gref, goff, glog = hip.ms_deform_attn_fused_backward(v, c["shapes"], r, o, lg, g)
+    torch.cuda.synchronize()
+    loc, attn = PR.prologue(ref, off, logits, c["shapes"], c["points"])
+    want = R.ms_deform_attn_core_rows(value, c["shapes"], loc, attn)
+    rv, rl, ra = R.ms_deform_attn_core_rows_vjp(value, c["shapes"], loc, attn, grad)
+    roff, rlog, rref = PR.prologue_vjp(ref, off, logits, c["shapes"], c["points"], rl, ra)
+    tf, tg = (2e-2, 2e-2) if c["bf16"] else (1e-5, 1e-4)
+    assert_close(out.float().cpu().numpy(), want, tf, "out")
+    assert_close(gv.float().cpu().numpy(), rv, tg, "grad_value")
+    assert_close(gref.cpu().numpy(), rref, tg, "grad_reference_points")
+    assert_close(goff.cpu().numpy(), roff, tg, "grad_sampling_offsets")
+    assert_close(glog.cpu().numpy(), rlog, tg, "grad_attention_logits")
