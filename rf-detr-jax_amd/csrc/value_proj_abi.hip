@@ -33,6 +33,12 @@ int vp_validate(int dtype, int batch, int len_in, int in_features, int n_heads, 
   return MSDA_OK;
 }
 
+// ceil(2^32 / divisor) for the kernels' multiply-high divisions (vp_div); 0 marks a divisor of 1
+// (and an empty extent), whose magic 2^32 does not fit 32 bits.
+uint32_t vp_magic(int divisor) {
+  return divisor > 1 ? static_cast<uint32_t>(((uint64_t{1} << 32) + static_cast<uint64_t>(divisor) - 1) / static_cast<uint64_t>(divisor)) : 0u;
+}
+
 // grad_weight's product is split over m into slices of at least 256 rows (at most 64 slices); the
 // partial sums [splits][N][K + 1] are the workspace. A function of the shape only.
 int vp_splits(int64_t m) { return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(64, (m + 255) / 256))); }
@@ -118,8 +124,8 @@ int msda_value_proj_fwd(const void* input, int dtype, const float* weight, const
   p.n = n_heads * head_dim;
   p.heads = n_heads;
   p.dim = head_dim;
-  p.dim_magic = static_cast<uint32_t>(((uint64_t{1} << 32) + head_dim - 1) / head_dim);
-  p.seq_magic = static_cast<uint32_t>(((uint64_t{1} << 32) + len_in - 1) / len_in);
+  p.dim_magic = vp_magic(head_dim);
+  p.seq_magic = vp_magic(len_in);
   return launch_gemm_dt<msda::kGemmForward>(p, static_cast<int64_t>(batch) * len_in, p.n, 1, vec_path(p, eb, input, nullptr),
                                             static_cast<hipStream_t>(stream), "value projection forward");
 }
@@ -173,8 +179,8 @@ int msda_value_proj_bwd(const void* input, int dtype, const float* weight, const
   p.heads = n_heads;
   p.dim = head_dim;
   p.splits = vp_splits(m);
-  p.dim_magic = static_cast<uint32_t>(((uint64_t{1} << 32) + head_dim - 1) / head_dim);
-  p.seq_magic = len_in > 0 ? static_cast<uint32_t>(((uint64_t{1} << 32) + len_in - 1) / len_in) : 0u;
+  p.dim_magic = vp_magic(head_dim);
+  p.seq_magic = vp_magic(len_in);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (grad_input != nullptr && m > 0) {
     const bool vec = vec_path(p, eb, grad_value, nullptr);

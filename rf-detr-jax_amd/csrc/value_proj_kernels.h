@@ -64,12 +64,15 @@ struct ValueProjParams {
   int bf16;               // input / value dtype is bf16
   int batch, seq, k, n, heads, dim;  // M = batch * seq, N = heads * dim
   int splits;             // grad_w: slices of the m range
-  uint32_t dim_magic;     // ceil(2^32 / dim): n / dim = umulhi(n, dim_magic) for n * dim < 2^32
-  uint32_t seq_magic;     // ceil(2^32 / seq): m / seq = umulhi(m, seq_magic) for m * seq < 2^32
+  uint32_t dim_magic;     // ceil(2^32 / dim): n / dim = umulhi(n, dim_magic) for n * dim < 2^32; 0 for dim 1
+  uint32_t seq_magic;     // ceil(2^32 / seq): m / seq = umulhi(m, seq_magic) for m * seq < 2^32; 0 for seq 1
 };
 
+// x / divisor by its magic (vp_magic); a divisor of 1 has no 32-bit magic (2^32) and is marked 0.
+__device__ __forceinline__ uint32_t vp_div(uint32_t x, uint32_t magic) { return magic != 0u ? __umulhi(x, magic) : x; }
+
 __device__ __forceinline__ int vp_div_dim(const ValueProjParams& p, int n) {
-  return static_cast<int>(__umulhi(static_cast<uint32_t>(n), p.dim_magic));
+  return static_cast<int>(vp_div(static_cast<uint32_t>(n), p.dim_magic));
 }
 
 // The [B*H, S, D] layout as 32-bit element offsets (every tensor here has fewer than 2^32
@@ -78,7 +81,7 @@ __device__ __forceinline__ int vp_div_dim(const ValueProjParams& p, int n) {
 // n = (h, d). Padded rows are zeroed by the callers (in the epilogue or in LDS), so the loads
 // themselves carry no condition.
 __device__ __forceinline__ uint32_t vp_row_part(const ValueProjParams& p, int m) {
-  const uint32_t b = __umulhi(static_cast<uint32_t>(m), p.seq_magic), s = static_cast<uint32_t>(m) - b * static_cast<uint32_t>(p.seq);
+  const uint32_t b = vp_div(static_cast<uint32_t>(m), p.seq_magic), s = static_cast<uint32_t>(m) - b * static_cast<uint32_t>(p.seq);
   return (b * static_cast<uint32_t>(p.heads) * static_cast<uint32_t>(p.seq) + s) * static_cast<uint32_t>(p.dim);
 }
 

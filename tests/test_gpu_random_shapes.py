@@ -132,3 +132,81 @@ def test_random_shape_fused_prologue(seed):
     assert_close(gref.cpu().numpy(), rref, tg, "grad_reference_points")
     assert_close(goff.cpu().numpy(), roff, tg, "grad_sampling_offsets")
     assert_close(glog.cpu().numpy(), rlog, tg, "grad_attention_logits")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shape_value_projection(seed):
+    """The value projection (msda_value_proj_fwd / _bwd) on random [B, S, C] -> H x D shapes: C and
+    D multiples of 4 or not (the 16-byte MFMA tile kernel or the element-wise one), a padding mask
+    or none, f32 or bf16, against the float64 oracle (oracle/value_proj_ref.py)."""
+    from oracle import value_proj_ref as VP
+    from oracle.msda_ref import bf16_round
+    from rfdetr_jax_amd.value_proj import value_proj_backward, value_proj_forward
+
+    rng = np.random.default_rng(300 + seed)
+    b, s = int(rng.integers(1, 4)), int(rng.integers(1, 700))
+    k = int(rng.choice([4, 12, 30, 64, 100, 128, 256]))
+    h, d = int(rng.choice([1, 2, 3, 4, 8, 16])), int(rng.choice([1, 4, 5, 8, 16, 20, 32]))
+    bf16, masked = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+    sys.stderr.write(f"[gpu] random value projection seed={seed} b={b} s={s} k={k} h={h} d={d} bf16={bf16} masked={masked}\n")
+    sys.stderr.flush()
+    x = rng.standard_normal((b, s, k)).astype(np.float32)
+    w = (rng.standard_normal((h * d, k)) / np.sqrt(k)).astype(np.float32)
+    bias = rng.standard_normal(h * d).astype(np.float32)
+    mask = (rng.uniform(0, 1, (b, s)) < 0.2) if masked else None
+    g = rng.standard_normal((b * h, s, d)).astype(np.float32)
+    if bf16:
+        x, g = bf16_round(x), bf16_round(g)
+    dev = torch.device("cuda:0")
+    dt = torch.bfloat16 if bf16 else torch.float32
+
+    def t(a, dtype=torch.float32):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dtype)
+
+    tm = None if mask is None else torch.from_numpy(mask).to(dev)
+    out = value_proj_forward(t(x, dt), t(w), t(bias), h, tm)
+    gx, gw, gb = value_proj_backward(t(x, dt), t(w), h, t(g, dt), tm)
+    torch.cuda.synchronize()
+    wq = bf16_round(w) if bf16 else w  # the product sees weight.astype(x.dtype)
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    assert_close(out.float().cpu().numpy(), VP.value_proj_rows(x, wq, bias, h, mask), tf, "value")
+    rx, rw, rb = VP.value_proj_rows_vjp(x, wq, h, g, mask)
+    assert_close(gx.float().cpu().numpy(), rx, tg, "grad_input")
+    assert_close(gw.float().cpu().numpy(), rw, tg, "grad_weight")
+    assert_close(gb.float().cpu().numpy(), rb, tg, "grad_bias")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shape_grid_sample(seed):
+    """The border/zeros grid sampler (msda_grid_sample_fwd / _bwd) on random [N, C, H, W] maps (up
+    to 200 x 200, so some planes exceed the LDS budget and run in row bands) and grids reaching
+    outside [-1, 1], f32 or bf16, against oracle/grid_sample_ref.py."""
+    from oracle import grid_sample_ref as GS
+    from oracle.msda_ref import bf16_round
+    from rfdetr_jax_amd import grid_sample as gsm
+
+    rng = np.random.default_rng(400 + seed)
+    n, c = int(rng.integers(1, 5)), int(rng.choice([1, 2, 3, 4, 8, 16]))
+    hh, ww = int(rng.integers(1, 201)), int(rng.integers(1, 201))
+    gh, gw = int(rng.integers(1, 60)), int(rng.integers(1, 8))
+    mode = "border" if rng.integers(0, 2) else "zeros"
+    bf16 = bool(rng.integers(0, 2))
+    sys.stderr.write(f"[gpu] random grid sample seed={seed} n={n} c={c} {hh}x{ww} grid {gh}x{gw} {mode} bf16={bf16}\n")
+    sys.stderr.flush()
+    inputs = rng.standard_normal((n, c, hh, ww)).astype(np.float32)
+    grid = rng.uniform(-1.3, 1.3, (n, gh, gw, 2)).astype(np.float32)
+    grad = rng.standard_normal((n, c, gh, gw)).astype(np.float32)
+    if bf16:
+        inputs, grad = bf16_round(inputs), bf16_round(grad)
+    dev = torch.device("cuda:0")
+    dt = torch.bfloat16 if bf16 else torch.float32
+    ti = torch.from_numpy(inputs).to(dev).to(dt).requires_grad_(True)
+    tgr = torch.from_numpy(grid).to(dev).requires_grad_(True)
+    out = gsm.bilinear_grid_sample(ti, tgr, mode)
+    out.backward(torch.from_numpy(grad).to(dev).to(dt))
+    torch.cuda.synchronize()
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    assert_close(out.float().detach().cpu().numpy(), GS.bilinear_grid_sample(inputs, grid, mode), tf, "out")
+    gi, gg = GS.grid_sample_vjp(inputs, grid, grad, mode)
+    assert_close(ti.grad.float().cpu().numpy(), gi, tg, "grad_input")
+    assert_close(tgr.grad.cpu().numpy(), gg, tg, "grad_grid")

@@ -49,6 +49,10 @@ SHAPES = {
     "base": dict(b=1, s=1700, k=256, h=8, d=32),          # 8 heads x 32 (larger variants)
     "odd_steps": dict(b=1, s=130, k=160, h=4, d=12),      # odd reduction step counts; 64 % D != 0
     "elementwise": dict(b=2, s=45, k=30, h=2, d=5),       # K, D not multiples of 4: element-wise kernels
+    # divisors of 1 in the epilogue's (head, d) and (batch, position) splits, whose multiply-high
+    # magic 2^32 has no 32-bit form
+    "head_dim_1": dict(b=2, s=333, k=64, h=8, d=1),
+    "len_in_1": dict(b=5, s=1, k=32, h=4, d=8),
 }
 
 
