@@ -210,3 +210,63 @@ def test_random_shape_grid_sample(seed):
     gi, gg = GS.grid_sample_vjp(inputs, grid, grad, mode)
     assert_close(ti.grad.float().cpu().numpy(), gi, tg, "grad_input")
     assert_close(tgr.grad.cpu().numpy(), gg, tg, "grad_grid")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_shape_attention(seed):
+    """The decoder self-attention (msda_attention_fwd / _bwd and the dropout entry points) on random
+    draws: [B, H, L, D] heads or [B, G * P, C] rows with G groups, L 1-400, head_dim 32 or 64, a
+    key mask (with a fully blocked row) or none, dropout 0 or 0.15, f32 or bf16, against the
+    float64 oracle given the kernels' keep mask. Whichever kernels the shape gets run: the fused
+    or two-kernel backward, the staged or chunked bf16 forward."""
+    from oracle import attention_ref as AT
+    from oracle.msda_ref import bf16_round
+    from rfdetr_jax_amd.attention import dropout_keep_mask, grouped_attention, scaled_dot_product_attention
+
+    rng = np.random.default_rng(500 + seed)
+    b, g_, h = int(rng.integers(1, 4)), int(rng.integers(1, 4)), int(rng.choice([1, 2, 4, 8]))
+    length, d = int(rng.integers(1, 401)), int(rng.choice([32, 64]))
+    rows, masked, bf16 = bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+    rate = 0.15 if rng.integers(0, 2) else 0.0
+    if not rows:
+        g_ = 1
+    sys.stderr.write(f"[gpu] random attention seed={seed} b={b} g={g_} h={h} L={length} d={d} rows={rows} masked={masked} "
+                     f"bf16={bf16} dropout={rate}\n")
+    sys.stderr.flush()
+    z = g_ * b
+    q, k, v, gr = (rng.standard_normal((z, h, length, d)).astype(np.float32) for _ in range(4))
+    if bf16:
+        q, k, v, gr = (bf16_round(x) for x in (q, k, v, gr))
+    mask = None
+    if masked:
+        mask = rng.uniform(0, 1, (length, length)) < 0.2
+        mask[length // 2] = True
+    dev = torch.device("cuda:0")
+    dt = torch.bfloat16 if bf16 else torch.float32
+    seed_drop = 900 + seed
+
+    def rows_of(x):  # [G B, H, L, D] -> [B, G L, H D] (slice z = g B + b)
+        return x.reshape(g_, b, h, length, d).transpose(1, 0, 3, 2, 4).reshape(b, g_ * length, h * d)
+
+    def heads_of(x):  # the inverse
+        return x.reshape(b, g_, length, h, d).transpose(1, 0, 3, 2, 4).reshape(z, h, length, d)
+
+    tm = None if mask is None else torch.from_numpy(mask).to(dev)
+    if rows:
+        tq, tk, tv = (torch.from_numpy(np.ascontiguousarray(rows_of(x))).to(dev).to(dt).requires_grad_(True) for x in (q, k, v))
+        out = grouped_attention(tq, tk, tv, h, g_, tm, dropout=rate, seed=seed_drop)
+        out.backward(torch.from_numpy(np.ascontiguousarray(rows_of(gr))).to(dev).to(dt))
+        got = [heads_of(t.detach().float().cpu().numpy()) for t in (out, tq.grad, tk.grad, tv.grad)]
+    else:
+        tq, tk, tv = (torch.from_numpy(x).to(dev).to(dt).requires_grad_(True) for x in (q, k, v))
+        out = scaled_dot_product_attention(tq, tk, tv, tm, dropout=rate, seed=seed_drop)
+        out.backward(torch.from_numpy(gr).to(dev).to(dt))
+        got = [t.detach().float().cpu().numpy() for t in (out, tq.grad, tk.grad, tv.grad)]
+    keep = None
+    if rate > 0:
+        keep = dropout_keep_mask(b, h, length, rate, seed_drop, groups=g_, device=dev).cpu().numpy().astype(bool)
+    torch.cuda.synchronize()
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    assert_close(got[0], AT.sdpa(q, k, v, mask, keep, rate), tf, "out")
+    for name, mine, want in zip(("grad_q", "grad_k", "grad_v"), got[1:], AT.sdpa_vjp(q, k, v, gr, mask, keep, rate)):
+        assert_close(mine, want, tg, name)
