@@ -200,3 +200,41 @@ def test_vector_and_elementwise_kernels_agree(tune, bf16):
         torch.cuda.synchronize()
         for name, a, ref, tol in zip(("value", "grad_input", "grad_weight", "grad_bias"), got, want, (tf, tg, tg, tg)):
             assert_close(_np(a), ref, tol, f"{name} {mode}")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_msdeform_attn_module_random_shapes(seed):
+    """The whole module on random draws: 1-4 levels of 1-30 rows and columns, 1-8 heads, head_dim
+    4-32, 1-4 points, point or box reference points, a padding mask or none, against the module in
+    torch ops (float64, CPU), output and every parameter gradient."""
+    rng = np.random.default_rng(600 + seed)
+    n_levels = int(rng.integers(1, 5))
+    shapes = tuple((int(rng.integers(1, 31)), int(rng.integers(1, 31))) for _ in range(n_levels))
+    n_heads, n_points = int(rng.choice([1, 2, 4, 8])), int(rng.integers(1, 5))
+    d_model = n_heads * int(rng.choice([4, 8, 12, 16, 32]))
+    ref_dim, masked = (2, 4)[int(rng.integers(0, 2))], bool(rng.integers(0, 2))
+    b, lq = int(rng.integers(1, 3)), int(rng.integers(1, 80))
+    _note(f"module random seed={seed} shapes={shapes} heads={n_heads} points={n_points} d_model={d_model} ref_dim={ref_dim} "
+          f"masked={masked} b={b} lq={lq}")
+    torch.manual_seed(seed)
+    m = MSDeformAttn(d_model, n_levels, n_heads, n_points).to(_dev())
+    with torch.no_grad():
+        m.sampling_offsets.weight.copy_(_t((rng.standard_normal(m.sampling_offsets.weight.shape) * 0.05).astype(np.float32)))
+        m.attention_weights.weight.copy_(_t((rng.standard_normal(m.attention_weights.weight.shape) * 0.1).astype(np.float32)))
+        m.value_proj.bias.copy_(_t((rng.standard_normal(d_model) * 0.1).astype(np.float32)))
+    s = sum(h * w for h, w in shapes)
+    query = rng.standard_normal((b, lq, d_model)).astype(np.float32)
+    ref = rng.uniform(0.1, 0.9, (b, lq, 1, 2)).astype(np.float32)
+    if ref_dim == 4:
+        ref = np.concatenate([ref, rng.uniform(0.05, 0.4, (b, lq, 1, 2)).astype(np.float32)], -1)
+    ref = np.array(np.broadcast_to(ref, (b, lq, n_levels, ref_dim)))  # a writable copy
+    inp = rng.standard_normal((b, s, d_model)).astype(np.float32)
+    mask = (rng.uniform(0, 1, (b, s)) < 0.1) if masked else None
+    grad = rng.standard_normal((b, lq, d_model)).astype(np.float32)
+    out = m(_t(query), _t(ref), _t(inp), shapes, None if mask is None else _t(mask))
+    out.backward(_t(grad))
+    params = {k: _np(v) for k, v in m.named_parameters()}
+    want, want_grads = _torch_module_reference(params, query, ref, inp, shapes, mask, n_heads, n_levels, n_points, grad)
+    assert_close(_np(out), want, 1e-5, "module output")
+    for k, v in m.named_parameters():
+        assert_close(_np(v.grad), want_grads[k], 1e-4, f"grad {k}")
