@@ -270,3 +270,60 @@ def test_random_shape_attention(seed):
     assert_close(got[0], AT.sdpa(q, k, v, mask, keep, rate), tf, "out")
     for name, mine, want in zip(("grad_q", "grad_k", "grad_v"), got[1:], AT.sdpa_vjp(q, k, v, gr, mask, keep, rate)):
         assert_close(mine, want, tg, name)
+
+
+def _draw_wide(seed):
+    """Many levels and points: 5-16 levels of 1-16 rows and columns, 1-40 points (up to 640
+    samples per (query, head)), small heads and head_dim, so the oracle stays fast."""
+    rng = np.random.default_rng(8000 + seed)
+    levels = int(rng.integers(5, 17))
+    shapes = tuple((int(rng.integers(1, 17)), int(rng.integers(1, 17))) for _ in range(levels))
+    return dict(shapes=shapes, heads=int(rng.choice([1, 2, 3, 4])), dim=int(rng.choice([1, 2, 4, 8, 16])),
+                points=int(rng.integers(1, 41)), queries=int(rng.integers(1, 101)), batch=int(rng.integers(1, 3)),
+                bf16=bool(rng.integers(0, 2)), uniform=bool(rng.integers(0, 2)))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_wide_shape_against_oracle(seed):
+    """msda_fwd / msda_bwd, and the fused-prologue op (per-row prologue and epilogue kernels),
+    with many levels and points against the float64 oracles."""
+    from oracle import prologue_ref as PR
+    from rfdetr_jax_amd.workloads import make_fused_inputs
+
+    c = _draw_wide(seed)
+    sys.stderr.write(f"[gpu] random wide shape seed={seed} {c}\n")
+    sys.stderr.flush()
+    dev = torch.device("cuda:0")
+    tf, tg = (2e-2, 2e-2) if c["bf16"] else (1e-5, 1e-4)
+    value, loc, attn, grad = make_inputs(800 + seed, c["batch"], c["heads"], c["dim"], c["queries"], c["shapes"], c["points"],
+                                         value_dtype="bf16" if c["bf16"] else "f32", uniform_locations=c["uniform"])
+    v = torch.from_numpy(value).to(dev)
+    if c["bf16"]:
+        v = v.to(torch.bfloat16)
+    lc, a, g = (torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in (loc, attn, grad))
+    out = hip.ms_deform_attn_forward(v, c["shapes"], lc, a)
+    gv, gl, ga = hip.ms_deform_attn_backward(v, c["shapes"], lc, a, g)
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), R.ms_deform_attn_core_rows(value, c["shapes"], loc, attn), tf, "out")
+    rv, rl, ra = R.ms_deform_attn_core_rows_vjp(value, c["shapes"], loc, attn, grad)
+    assert_close(gv.float().cpu().numpy(), rv, tg, "grad_value")
+    assert_close(gl.cpu().numpy(), rl, tg, "grad_loc")
+    assert_close(ga.cpu().numpy(), ra, tg, "grad_attn")
+    ref_dim = 2 if seed % 2 == 0 else 4
+    value, ref, off, logits, grad = make_fused_inputs(900 + seed, c["batch"], c["heads"], c["dim"], c["queries"], c["shapes"],
+                                                      c["points"], ref_dim, "bf16" if c["bf16"] else "f32")
+    v = torch.from_numpy(value).to(dev)
+    if c["bf16"]:
+        v = v.to(torch.bfloat16)
+    r, o, lg, g = (torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in (ref, off, logits, grad))
+    out = hip.ms_deform_attn_fused_forward(v, c["shapes"], r, o, lg)
+    gv, gref, goff, glog = hip.ms_deform_attn_fused_backward(v, c["shapes"], r, o, lg, g)
+    torch.cuda.synchronize()
+    loc, attn = PR.prologue(ref, off, logits, c["shapes"], c["points"])
+    rv, rl, ra = R.ms_deform_attn_core_rows_vjp(value, c["shapes"], loc, attn, grad)
+    roff, rlog, rref = PR.prologue_vjp(ref, off, logits, c["shapes"], c["points"], rl, ra)
+    assert_close(out.float().cpu().numpy(), R.ms_deform_attn_core_rows(value, c["shapes"], loc, attn), tf, "fused out")
+    assert_close(gv.float().cpu().numpy(), rv, tg, "fused grad_value")
+    assert_close(gref.cpu().numpy(), rref, tg, "grad_reference_points")
+    assert_close(goff.cpu().numpy(), roff, tg, "grad_sampling_offsets")
+    assert_close(glog.cpu().numpy(), rlog, tg, "grad_attention_logits")
