@@ -168,7 +168,9 @@ int64_t msda_bwd_workspace_size(int batch, int n_heads, int head_dim, int len_qu
  * workspace must hold msda_bwd_workspace_size() bytes (16-byte aligned); it may be NULL when that
  * size is 0 or grad_value is NULL.
  * Limits (MSDA_ERR_UNSUPPORTED beyond them): levels of at most 32000 rows and columns,
- * len_query * n_heads * head_dim < 2^30 and len_query * n_heads * n_levels * n_points < 2^24.
+ * len_query * n_heads * head_dim < 2^30 and len_query * n_heads * n_levels * n_points < 2^24, and
+ * one image row of every level (its f64 accumulator, two staged value rows and a point list of at
+ * least one query) within the LDS: about 158 columns at head_dim 64 and 318 at head_dim 32 in f32.
  */
 int msda_bwd(const void* value, int value_dtype,
              const float* sampling_locations, const float* attention_weights,

@@ -470,6 +470,15 @@ int plan_band(const Shape& s, int vbytes, int ch, const DevInfo& dev, BandPlan* 
     if (s.points >= 65536) return fail(MSDA_ERR_UNSUPPORTED, "n_points %d: at most 65535 with banded levels", s.points);
     const int max_cap = std::max(64, std::min(8192, env_int("MSDA_BWD_LIST", 8192)));
     bp->qpass = std::max(1, std::min(s.queries, std::max(1, max_cap / s.points)));
+    // A level whose single image row would not fit beside a full list gets a shorter list (more
+    // scan passes per band) rather than a refusal; shapes that fit keep the full list.
+    for (;;) {
+      bool fits = true;
+      for (int l = 0; l < s.levels; ++l)
+        if (band_layout(1, s.w[l], s.dim, vbytes, bp->qpass * s.points, 0).total > dev.lds_bytes) fits = false;
+      if (fits || bp->qpass == 1) break;
+      bp->qpass = (bp->qpass + 1) / 2;
+    }
     bp->cap = bp->qpass * s.points;
     const int budget = dev.lds_bytes / per_cu - 512;
     int64_t nb_total = 0;
