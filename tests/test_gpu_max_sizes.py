@@ -15,7 +15,8 @@ the size:
 * a level too wide for one image row of the backward's f64 accumulator to fit in LDS is refused
   with MSDA_ERR_UNSUPPORTED, its forward still runs;
 * a level whose image row fits only beside a shorter point list (more scan passes per band)
-  against the float64 oracle.
+  against the float64 oracle;
+* the self-attention at 2048 and 4096 rows against the float64 oracle.
 """
 
 from __future__ import annotations
@@ -135,3 +136,35 @@ def test_wide_level_with_a_shorter_point_list_against_oracle():
     assert_close(gv.cpu().numpy(), rv, 1e-4, "grad_value")
     assert_close(gl.cpu().numpy(), rl, 1e-4, "grad_loc")
     assert_close(ga.cpu().numpy(), ra, 1e-4, "grad_attn")
+
+
+@pytest.mark.parametrize("length,head_dim,bf16,masked", [(2048, 64, False, True), (4096, 32, True, False), (4096, 64, False, False)])
+def test_long_attention_against_oracle(length, head_dim, bf16, masked):
+    """The chunked self-attention kernels far past the decoder's 300 rows (32 to 64 key chunks per
+    query block, the forward's reference score moving many times) against the float64 oracle."""
+    import numpy as np
+
+    from oracle import attention_ref as AT
+    from oracle.msda_ref import bf16_round
+    from rfdetr_jax_amd.attention import scaled_dot_product_attention
+    from tests._util import assert_close
+
+    _note(f"long attention L={length} D={head_dim} bf16={bf16} masked={masked}")
+    rng = np.random.default_rng(length + head_dim)
+    q, k, v, g = (rng.standard_normal((1, 2, length, head_dim)).astype(np.float32) for _ in range(4))
+    if bf16:
+        q, k, v, g = (bf16_round(x) for x in (q, k, v, g))
+    mask = None
+    if masked:
+        mask = rng.uniform(0, 1, (length, length)) < 0.3
+        mask[7] = True
+    dev = torch.device("cuda:0")
+    dt = torch.bfloat16 if bf16 else torch.float32
+    tq, tk, tv = (torch.from_numpy(x).to(dev).to(dt).requires_grad_(True) for x in (q, k, v))
+    out = scaled_dot_product_attention(tq, tk, tv, None if mask is None else torch.from_numpy(mask).to(dev))
+    out.backward(torch.from_numpy(g).to(dev).to(dt))
+    torch.cuda.synchronize()
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    assert_close(out.float().detach().cpu().numpy(), AT.sdpa(q, k, v, mask), tf, "out")
+    for name, t, want in zip("qkv", (tq, tk, tv), AT.sdpa_vjp(q, k, v, g, mask)):
+        assert_close(t.grad.float().cpu().numpy(), want, tg, f"grad_{name}")
