@@ -119,3 +119,29 @@ def test_noalloc_rejects_shapes_beyond_its_array(tune):
     rc = lib.msda_bwd_noalloc(null, 0, null, null, null, 0, null, null, null, *dims, null)
     assert rc == _native.ERR_UNSUPPORTED
     assert b"scratch" in lib.msda_last_error()
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_noalloc_random_shapes_with_query_blocks(seed):
+    """Random shapes whose levels fit the LDS whole and whose queries are split into blocks (so the
+    partial sums go to the library's array): 1-2 levels of 4-24 rows and columns, 1-8 heads,
+    head_dim 8-32, 1-4 points, 600-4000 queries, f32 or bf16, against msda_bwd with a workspace."""
+    rng = np.random.default_rng(1200 + seed)
+    levels = int(rng.integers(1, 3))
+    shapes = tuple((int(rng.integers(4, 25)), int(rng.integers(4, 25))) for _ in range(levels))
+    heads, dim = int(rng.choice([1, 2, 4, 8])), int(rng.choice([8, 16, 32]))
+    points, queries = int(rng.integers(1, 5)), int(rng.integers(600, 4001))
+    bf16 = bool(rng.integers(0, 2))
+    _note(f"noalloc random seed={seed} shapes={shapes} heads={heads} dim={dim} points={points} queries={queries} bf16={bf16}")
+    d = torch.device("cuda:0")
+    value, loc, attn, grad = make_inputs(1300 + seed, 1, heads, dim, queries, shapes, points,
+                                         value_dtype="bf16" if bf16 else "f32")
+    v, lc, a, g = (torch.from_numpy(np.ascontiguousarray(x)).to(d) for x in (value, loc, attn, grad))
+    if bf16:
+        v = v.to(torch.bfloat16)
+    want = hip.ms_deform_attn_backward(v, shapes, lc, a, g)
+    got = _noalloc_backward(v, shapes, lc, a, g)
+    torch.cuda.synchronize()
+    assert torch.equal(got[1], want[1]), "grad_sampling_locations differs"
+    assert torch.equal(got[2], want[2]), "grad_attention_weights differs"
+    assert_close(got[0].float().cpu().numpy(), want[0].float().cpu().numpy(), 2e-2 if bf16 else 1e-5, "grad_value")
