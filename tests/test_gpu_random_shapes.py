@@ -327,3 +327,40 @@ def test_random_wide_shape_against_oracle(seed):
     assert_close(gref.cpu().numpy(), rref, tg, "grad_reference_points")
     assert_close(goff.cpu().numpy(), roff, tg, "grad_sampling_offsets")
     assert_close(glog.cpu().numpy(), rlog, tg, "grad_attention_logits")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_shape_point_sample(seed):
+    """point_sample (unit-square points, bilinear or nearest with border padding) on random maps
+    and point layouts (flat [N, P, 2] or gridded [N, Hg, Wg, 2]), f32 or bf16, against the oracle
+    (oracle/grid_sample_ref.py point_sample and its VJP)."""
+    from oracle import grid_sample_ref as GS
+    from oracle.msda_ref import bf16_round
+    from rfdetr_jax_amd import grid_sample as gsm
+
+    rng = np.random.default_rng(1400 + seed)
+    n, c = int(rng.integers(1, 6)), int(rng.choice([1, 2, 3, 8]))
+    hh, ww = int(rng.integers(1, 120)), int(rng.integers(1, 120))
+    mode = "nearest" if rng.integers(0, 2) else "bilinear"
+    bf16 = bool(rng.integers(0, 2))
+    pts_shape = (n, int(rng.integers(1, 300)), 2) if rng.integers(0, 2) else (n, int(rng.integers(1, 20)), int(rng.integers(1, 20)), 2)
+    sys.stderr.write(f"[gpu] random point sample seed={seed} n={n} c={c} {hh}x{ww} points {pts_shape} {mode} bf16={bf16}\n")
+    sys.stderr.flush()
+    inputs = rng.standard_normal((n, c, hh, ww)).astype(np.float32)
+    pts = rng.uniform(-0.1, 1.1, pts_shape).astype(np.float32)
+    grad = rng.standard_normal((n, c) + pts_shape[1:-1]).astype(np.float32)
+    if bf16:
+        inputs, grad = bf16_round(inputs), bf16_round(grad)
+    dev = torch.device("cuda:0")
+    dt = torch.bfloat16 if bf16 else torch.float32
+    ti = torch.from_numpy(inputs).to(dev).to(dt).requires_grad_(True)
+    tp = torch.from_numpy(pts).to(dev).requires_grad_(True)
+    out = gsm.point_sample(ti, tp, mode)
+    out.backward(torch.from_numpy(grad).to(dev).to(dt))
+    torch.cuda.synchronize()
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    want = GS.point_sample(inputs, pts, mode)
+    gi, gp = GS.point_sample_vjp(inputs, pts, grad, mode)
+    assert_close(out.float().detach().cpu().numpy(), want, tf, "out")
+    assert_close(ti.grad.float().cpu().numpy(), gi, tg, "grad_input")
+    assert_close(tp.grad.cpu().numpy(), gp, tg, "grad_points")
