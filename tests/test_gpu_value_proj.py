@@ -238,3 +238,35 @@ def test_msdeform_attn_module_random_shapes(seed):
     assert_close(_np(out), want, 1e-5, "module output")
     for k, v in m.named_parameters():
         assert_close(_np(v.grad), want_grads[k], 1e-4, f"grad {k}")
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+def test_value_proj_misaligned_tensors(bf16):
+    """Input and grad_value views one element into their buffers (K and D multiples of 4, so only
+    the alignment keeps them off the 16-byte tile kernels): the element-wise kernels, against the
+    oracle."""
+    rng = np.random.default_rng(35)
+    b, s, k, h, d = 2, 70, 64, 4, 16
+    x = rng.standard_normal((b, s, k)).astype(np.float32)
+    w = (rng.standard_normal((h * d, k)) / 8).astype(np.float32)
+    bias = rng.standard_normal(h * d).astype(np.float32)
+    g = rng.standard_normal((b * h, s, d)).astype(np.float32)
+    if bf16:
+        x, g = bf16_round(x), bf16_round(g)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    xb = torch.zeros(x.size + 1, dtype=dt, device=_dev())
+    xb[1:] = _t(x.ravel(), dt)
+    gb_ = torch.zeros(g.size + 1, dtype=dt, device=_dev())
+    gb_[1:] = _t(g.ravel(), dt)
+    xv, gvv = xb[1:].view(b, s, k), gb_[1:].view(b * h, s, d)
+    assert xv.data_ptr() % 16 != 0 and gvv.data_ptr() % 16 != 0
+    out = value_proj_forward(xv, _t(w), _t(bias), h)
+    gx, gw, gb = value_proj_backward(xv, _t(w), h, gvv)
+    torch.cuda.synchronize()
+    wq = bf16_round(w) if bf16 else w
+    tf, tg = (2e-2, 2e-2) if bf16 else (1e-5, 1e-4)
+    assert_close(_np(out), VP.value_proj_rows(x, wq, bias, h), tf, "value")
+    rx, rw, rb = VP.value_proj_rows_vjp(x, wq, h, g)
+    assert_close(_np(gx), rx, tg, "grad_input")
+    assert_close(_np(gw), rw, tg, "grad_weight")
+    assert_close(_np(gb), rb, tg, "grad_bias")
