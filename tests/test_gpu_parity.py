@@ -462,3 +462,27 @@ def test_library_loaded_from_tree():
 
     maps = open(f"/proc/{os.getpid()}/maps").read()
     assert os.path.realpath(LIB_PATH) in maps or LIB_PATH in maps
+
+
+def test_far_out_locations_contribute_nothing():
+    """Locations whose pixel coordinates leave the int32 range (|loc| up to 1e10, also 2^31 / W
+    exactly and just past it): every corner is masked, so those samples add nothing to the output
+    or to grad_value, and their weight and location gradients are zero, as the float64 oracle has
+    it. The other samples of the same queries are unaffected."""
+    shapes = ((24, 24), (12, 12))
+    value, loc, attn, grad = make_inputs(44, 2, 4, 16, 200, shapes, 3)
+    far = np.array([1e10, -1e10, 3e9, -3e9, 2.0 ** 31 / 24, -(2.0 ** 31) / 24, 1e6, -1e6], np.float32)
+    rng = np.random.default_rng(45)
+    sel = rng.random(loc.shape[:-1]) < 0.3
+    loc = loc.copy()
+    loc[sel, 0] = rng.choice(far, int(sel.sum()))
+    loc[sel, 1] = rng.choice(far, int(sel.sum()))
+    _note("far-out locations")
+    out, (gv, gl, ga) = _run(value, shapes, loc, attn, grad)
+    assert_close(out, R.ms_deform_attn_core_rows(value, shapes, loc, attn), 1e-5, "out")
+    rv, rl, ra = R.ms_deform_attn_core_rows_vjp(value, shapes, loc, attn, grad)
+    assert_close(gv, rv, 1e-4, "grad_value")
+    assert_close(gl, rl, 1e-4, "grad_loc")
+    assert_close(ga, ra, 1e-4, "grad_attn")
+    ga5 = ga.reshape(loc.shape[:-1])
+    assert not ga5[sel].any() and not gl[sel].any()
