@@ -299,7 +299,7 @@ struct SamplePlan {
 // workgroup that fills a CU's LDS gets 1024 threads. Then one resident wave of workgroups: fewer,
 // longer workgroups amortise the value staging.
 int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* prefix, int shift, msda::SampleParams* p,
-                SamplePlan* out) {
+                SamplePlan* out, int hg_max = 1 << 30) {
   auto knob = [&](const char* name, int dflt) {
     std::string key = std::string(prefix) + name;
     return env_int(key.c_str(), dflt);
@@ -319,7 +319,7 @@ int plan_sample(const Shape& s, int vbytes, const DevInfo& dev, const char* pref
   }
   const int64_t head_bytes = align16(static_cast<int64_t>(head_lds) * vbytes);
   int hg = 1;
-  const int hg_cap = std::max(1, knob("_HEADS", s.queries >= 1024 ? 4 : 1));
+  const int hg_cap = std::min(hg_max, std::max(1, knob("_HEADS", s.queries >= 1024 ? 4 : 1)));
   const int group_budget = std::min(budget, knob("_GROUP_LDS", dev.lds_bytes));
   while (hg * 2 <= hg_cap && s.heads % (hg * 2) == 0 && (hg * 2) * head_bytes <= group_budget) hg *= 2;
   // With every level staged a head's region is its whole value slice; regions stay 16-byte aligned.
@@ -877,20 +877,58 @@ int fwd_impl(const void* value, int value_dtype, const float* loc, const float* 
   p.points = n_points;
   p.len_value = len_value;
   p.vec16 = rows_16b(s, vbytes, value, nullptr);
+  p.rheads = n_heads;
+  p.vstride = head_dim;
+  p.cs_shift = 0;
   fill_fused(&p, fz, n_points);
   SamplePlan plan;
   if ((rc = plan_sample(s, vbytes, dev, "MSDA_FWD", shift, &p, &plan)) != MSDA_OK) return rc;
+  // Opt-in (MSDA_FWD_SPLIT=1): a level too large for the LDS is staged by splitting each head's
+  // channels over 2 or 4 workgroups (one head each) when every level then fits, each part a whole
+  // number of 16-byte chunks per cell. Measured on MI355X at the two-level bf16 shape (80 x 80 and
+  // 20 x 20, 16 heads x 16, 300 queries, 4 points): 11.5 us against 10.5 us gathering the large
+  // level through L2, since staging reads every cell of the level where 2400 samples per slice
+  // touch fewer; so the default gathers.
+  int vec_used = vec, shift_used = shift;
+  if (!p.all_staged && aligned(value, 16) && env_int("MSDA_FWD_SPLIT", 0) != 0) {
+    for (int cs = 1; cs <= 2; ++cs) {
+      const int part = head_dim >> cs;
+      if (head_dim % (1 << cs) != 0 || (part * vbytes) % 16 != 0) break;
+      Shape s2 = s;
+      s2.heads = n_heads << cs;
+      s2.dim = part;
+      msda::SampleParams p2 = p;
+      p2.heads = s2.heads;
+      p2.dim = part;
+      p2.cs_shift = cs;
+      p2.vec16 = 1;
+      const int vec2 = pick_vec(part, env_int("MSDA_FWD_MAX_VEC", 8), {{value, vbytes}, {output, obytes}});
+      const int shift2 = lpq_shift_for(part, vec2);
+      SamplePlan plan2;
+      if (plan_sample(s2, vbytes, dev, "MSDA_FWD", shift2, &p2, &plan2, 1) != MSDA_OK) {
+        g_last_error.clear();
+        continue;
+      }
+      if (!p2.all_staged) continue;
+      s = s2;
+      p = p2;
+      plan = plan2;
+      vec_used = vec2;
+      shift_used = shift2;
+      break;
+    }
+  }
   apply_sampler(s, sampler, value_dtype, p.lv);
   bool rounded = false;
   for (int l = 0; l < n_levels; ++l) rounded = rounded || p.lv[l].rmode != msda::kRoundNone;
   // one level, two points, two lanes per (query, head), every level staged: the two lanes split the
   // samples' coordinate work (fwd_pair; f32 interpolation only)
-  p.pair_share = (n_levels == 1 && n_points == 2 && shift == 1 && p.all_staged && ns == 2 && !rounded && env_int("MSDA_FWD_PAIR", 1)) ? 1 : 0;
+  p.pair_share = (n_levels == 1 && n_points == 2 && shift_used == 1 && p.all_staged && ns == 2 && !rounded && env_int("MSDA_FWD_PAIR", 1)) ? 1 : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool fused = fz != nullptr;
   if (value_dtype == MSDA_DTYPE_BF16)
-    return msda_host::dispatch_fwd<msda::bf16_t>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st);
-  return msda_host::dispatch_fwd<float>(vec, ns, fused, p, plan.grid, plan.threads, plan.lds, st);
+    return msda_host::dispatch_fwd<msda::bf16_t>(vec_used, ns, fused, p, plan.grid, plan.threads, plan.lds, st);
+  return msda_host::dispatch_fwd<float>(vec_used, ns, fused, p, plan.grid, plan.threads, plan.lds, st);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -70,6 +70,12 @@ struct SampleParams {
   int head_lds;    // LDS elements of one head's staged levels
   int all_staged;  // every level is staged, so a head group's value rows are one contiguous copy
   int vec16;       // value staging may use 16-byte vectors
+  // Channel split (cs_shift > 0, forward only): 2^cs_shift workgroups share each head, one run of
+  // its channels each, so that a value slice too large for the LDS at head_dim channels is staged
+  // at head_dim / 2^cs_shift. `heads` and `dim` then count the split heads and their channels,
+  // while the tensors hold `rheads` heads of `vstride` channels (rheads == heads and vstride == dim
+  // without a split). The outputs of the parts are disjoint: no reduction.
+  int rheads, vstride, cs_shift;
   // MSDeformAttn prologue fused in (kFused kernels, ops.py:388-404): `loc` then holds the raw
   // sampling offsets and `attn` the attention logits.
   const float* ref;  // reference points [B, Q, L, ref_dim]
@@ -376,6 +382,28 @@ __device__ __forceinline__ void stage_copy(VT* dst, const VT* __restrict__ src, 
   }
 }
 
+// Staging of one part of a split head: `cells` cells of `dim` elements each, `stride` elements apart
+// in memory, packed in LDS. dim and stride are whole 16-byte chunks and src is 16-byte aligned, so
+// every chunk goes straight to LDS, 64 consecutive LDS chunks per wave instruction.
+template <typename VT>
+__device__ __forceinline__ void stage_cells(VT* dst, const VT* __restrict__ src, int cells, int dim, int stride) {
+  constexpr int E = 16 / static_cast<int>(sizeof(VT));  // elements per chunk
+  const int cpc = dim / E;                               // chunks per cell
+  const int n16 = cells * cpc;
+  const int t = static_cast<int>(threadIdx.x), nt = static_cast<int>(blockDim.x);
+  const int lane = t & 63, wave = t >> 6, nw = nt >> 6;
+  uint4* d = reinterpret_cast<uint4*>(dst);
+  auto chunk = [&](int i) {
+    const int cell = i / cpc;
+    return reinterpret_cast<const uint4*>(src + static_cast<int64_t>(cell) * stride) + (i - cell * cpc);
+  };
+  const int nblk = n16 >> 6;
+  for (int blk = wave; blk < nblk; blk += nw)
+    __builtin_amdgcn_global_load_lds(chunk(blk * 64 + lane), (MSDA_LDS void*)(d + blk * 64), 16, 0, 0);
+  for (int i = (nblk << 6) + t; i < n16; i += nt) d[i] = *chunk(i);
+  wait_vmem();
+}
+
 // ---------------------------------------------------------------------------------------------
 // per-sample kernels: shared work-item decomposition and staging
 
@@ -397,12 +425,13 @@ __device__ __forceinline__ SampleItem sample_item(const SampleParams& p) {
 }
 
 // The group's slices are consecutive rows of value [B*H, S, D]: when every level is staged they
-// are one contiguous copy.
+// are one contiguous copy (a split head, always alone in its group: one run of each cell).
 template <typename VT>
 __device__ __forceinline__ void stage_group(const SampleParams& p, VT* lds, const VT* __restrict__ vg) {
   const int64_t slice_elems = p.len_value * p.dim;
   if (p.all_staged) {
-    stage_copy(lds, vg, static_cast<int>(p.hg * slice_elems), p.vec16);
+    if (p.cs_shift > 0) stage_cells(lds, vg, static_cast<int>(p.len_value), p.dim, p.vstride);
+    else stage_copy(lds, vg, static_cast<int>(p.hg * slice_elems), p.vec16);
     return;
   }
   for (int hh = 0; hh < p.hg; ++hh)
@@ -776,8 +805,15 @@ fwd_kernel(const SampleParams p) {
   const int rot = ln.rot;
   const int D = p.dim;
   const int64_t slice_elems = p.len_value * D;
-  const VT* __restrict__ vg = static_cast<const VT*>(p.value) + (static_cast<int64_t>(it.b) * p.heads + it.h0) * slice_elems;
+  // split heads: head h is run h & csm of the channels of head h >> cs_shift in memory
+  const int csm = (1 << p.cs_shift) - 1;
+  const VT* __restrict__ vg = static_cast<const VT*>(p.value) +
+                              (static_cast<int64_t>(it.b) * p.rheads + (it.h0 >> p.cs_shift)) * (p.len_value * p.vstride) +
+                              (it.h0 & csm) * D;
   const int h = it.h0 + ln.hl;
+  const int rh = h >> p.cs_shift, sub = h & csm;
+  // (b, q, rh) rows of the locations and weights; output row (row << cs_shift) + sub of [B, Q, H, D]
+  auto out_off = [&](int64_t row) { return ((row << p.cs_shift) + sub) * D + ln.c0; };
   const int LP = p.levels * p.points;
   const int q_lo = it.qb * p.qblock;
   const int q_hi = min(p.queries, q_lo + p.qblock);
@@ -785,8 +821,8 @@ fwd_kernel(const SampleParams p) {
   constexpr int QU = query_group(NS, VEC, kFused);
   constexpr int NI = NS == 0 ? 1 : NS;
   const int q_first = q_lo + ln.qs;
-  const int64_t row_first = (static_cast<int64_t>(it.b) * p.queries + q_first) * p.heads + h;  // (b, q, h)
-  const int64_t row_step = static_cast<int64_t>(ln.qpp) * p.heads;
+  const int64_t row_first = (static_cast<int64_t>(it.b) * p.queries + q_first) * p.rheads + rh;  // (b, q, h)
+  const int64_t row_step = static_cast<int64_t>(ln.qpp) * p.rheads;
   const int64_t bq0 = static_cast<int64_t>(it.b) * p.queries;  // query row b * Q of the reference points
   SampleIn<NI> in[QU];
   FusedIn<NI, kFused> fin[QU];
@@ -834,19 +870,19 @@ fwd_kernel(const SampleParams p) {
           if constexpr (NS == 2 && kStaged) {
             if (p.pair_share) {
               fwd_pair<VT, VEC>(acc, in[i], p, hlds, rot, kFused ? ln.j : 0);
-              if (ln.lane_on) store_any_rot<VT, VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, rot, acc);
+              if (ln.lane_on) store_any_rot<VT, VEC>(p.out, out_off(row), p.out_bf16 != 0, rot, acc);
               continue;
             }
           }
           int l = 0, pt = 0;  // level and point of the next sample (level-major order, ops.py:285)
           fwd_pass<VT, VEC, NS, kStaged>(acc, in[i], 0, LP, l, pt, p, hlds, vs, rot);
-          if (ln.lane_on) store_any_rot<VT, VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, rot, acc);
+          if (ln.lane_on) store_any_rot<VT, VEC>(p.out, out_off(row), p.out_bf16 != 0, rot, acc);
         }
       }
     }
   } else {
     for (int q = q_first; q < q_hi; q += ln.qpp) {
-      const int64_t row = (static_cast<int64_t>(it.b) * p.queries + q) * p.heads + h;
+      const int64_t row = (static_cast<int64_t>(it.b) * p.queries + q) * p.rheads + rh;
       float acc[VEC];
 #pragma unroll
       for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
@@ -864,7 +900,7 @@ fwd_kernel(const SampleParams p) {
         }
         fwd_pass<VT, VEC, PB, kStaged>(acc, f, s0, LP, l, pt, p, hlds, vs, rot);
       }
-      if (ln.lane_on) store_any_rot<VT, VEC>(p.out, row * D + ln.c0, p.out_bf16 != 0, rot, acc);
+      if (ln.lane_on) store_any_rot<VT, VEC>(p.out, out_off(row), p.out_bf16 != 0, rot, acc);
     }
   }
 }
