@@ -883,14 +883,20 @@ int fwd_impl(const void* value, int value_dtype, const float* loc, const float* 
   fill_fused(&p, fz, n_points);
   SamplePlan plan;
   if ((rc = plan_sample(s, vbytes, dev, "MSDA_FWD", shift, &p, &plan)) != MSDA_OK) return rc;
-  // Opt-in (MSDA_FWD_SPLIT=1): a level too large for the LDS is staged by splitting each head's
-  // channels over 2 or 4 workgroups (one head each) when every level then fits, each part a whole
-  // number of 16-byte chunks per cell. Measured on MI355X at the two-level bf16 shape (80 x 80 and
-  // 20 x 20, 16 heads x 16, 300 queries, 4 points): 11.5 us against 10.5 us gathering the large
-  // level through L2, since staging reads every cell of the level where 2400 samples per slice
-  // touch fewer; so the default gathers.
+  // A level too large for the LDS can be staged by splitting each head's channels over 2 or 4
+  // workgroups (one head each) when every level then fits, each part a whole number of 16-byte
+  // chunks per cell. Staging reads every cell of the level, gathering only what the samples touch,
+  // so the split pays with many queries per slice. Measured on MI355X (forward through a HIP graph,
+  // gathered against split): f32 at 3900 queries 78.1 -> 70.1 us (64 x 64 and 32 x 32 levels,
+  // 16 heads x 16), 40.7 -> 39.0 (40 x 40 and 20 x 20, 8 x 32), 12.9 -> 11.6 (48 x 48, 8 x 32),
+  // at 1200 queries 40.8 -> 30.2 and 21.4 -> 21.2, at 300 queries 14.9 -> 14.7 and 8.8 -> 10.5;
+  // bf16 slower at every count (80 x 80 and 20 x 20, 16 x 16: 300 queries 10.5 -> 11.5, 3900
+  // queries 63.9 -> 72.9, eager). So: f32 value maps with at least 1024 queries, unless the knob
+  // MSDA_FWD_SPLIT says otherwise (0 never, 1 whenever it fits).
   int vec_used = vec, shift_used = shift;
-  if (!p.all_staged && aligned(value, 16) && env_int("MSDA_FWD_SPLIT", 0) != 0) {
+  const int split_knob = env_int("MSDA_FWD_SPLIT", -1);
+  const bool split = split_knob > 0 || (split_knob < 0 && vbytes == 4 && len_query >= 1024);
+  if (!p.all_staged && aligned(value, 16) && split) {
     for (int cs = 1; cs <= 2; ++cs) {
       const int part = head_dim >> cs;
       if (head_dim % (1 << cs) != 0 || (part * vbytes) % 16 != 0) break;

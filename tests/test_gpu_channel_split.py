@@ -1,9 +1,9 @@
 """The forward's channel split on an MI355X: value levels too large for the LDS at head_dim channels,
 staged at a half or a quarter of each head's channels per workgroup.
 
-The split is opt-in (tuning knob MSDA_FWD_SPLIT=1; it measured slower than gathering the large
-level through L2 at the two-level bf16 shape). Each case runs the forward twice, with the split and
-without it (the default). Both compute every output channel with
+The library splits f32 value maps with at least 1024 queries by default; the tuning knob
+MSDA_FWD_SPLIT forces the split (1) or the L2 gather of the large level (0). Each case runs the
+forward twice, with the split and without it. Both compute every output channel with
 the same operations in the same order, so the outputs must be bit-identical; the split output is
 also checked against the float64 oracle. The cases cover one and two chunks of 16 bytes per staged
 cell, a split by two and by four, f32 and bf16 value maps, a level that fills the LDS, query counts
@@ -36,6 +36,7 @@ CASES = {
     "f32_d32_quarter_two_chunks": ("f32", 32, ((64, 64),), 2, 200, 1, 4),
     "f32_d8_half_fills_lds": ("f32", 8, ((100, 100),), 2, 300, 1, 2),
     "bf16_d16_many_queries": ("bf16", 16, ((80, 80),), 2, 3900, 1, 8),
+    "f32_d16_split_by_default": ("f32", 16, ((64, 64), (32, 32)), 4, 1200, 1, 4),
 }
 
 
@@ -48,7 +49,8 @@ def _both(fn):
     """fn() with the channel split, then without it."""
     with _native.tuning({"MSDA_FWD_SPLIT": 1}):
         split = fn()
-    plain = fn()
+    with _native.tuning({"MSDA_FWD_SPLIT": 0}):
+        plain = fn()
     torch.cuda.synchronize()
     return split, plain
 
